@@ -1,0 +1,356 @@
+"""Benchmark of the quantized-matvec hot path on one MI355X.
+
+Headline workload: a qwen35-27B-shaped decode-step weight sweep, batch 1 — 64
+layers (48 gated-delta SSM + 16 gated-attention) with a UD-Q3_K_XL-like quant mix and the Q6_K LM head with
+on-device argmax, 13.44 GiB of synthetic seeded raw GGUF blocks resident in HBM. One step = one sweep:
+every weight matrix of the step read once by its qmv (activations quantized once per distinct input).
+`value` = algorithmic bytes of the step / step time (GB/s); `ms_per_step` = ms per sweep.
+
+Also reported: per-quant-type matvec throughput at 5120x17408 (configs[0..2] shapes, rotating over weight
+copies larger than the 256 MB MALL), the roofline of the dominant kernel (HIP events on its stream), and
+the reference CPU path timed on a bounded sample on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ntok 1] [--no-graph] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, AMD-published
+METRIC = "achieved HBM GB/s (% of MI355X peak) per quant type; ms per 27B decode-step sweep"
+
+# Per-layer matrices (name, type, rows, cols, input group); shapes from qwen_tensors.py:98-118 via the
+# survey's config 4. Full attention at layers 3, 7, ..., 63 (test_phase29_qwen_ops.py:207-209).
+Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, IQ4_XS, IQ3_S, IQ2_XXS = 11, 12, 13, 14, 8, 23, 21, 16
+SSM_LAYER = [
+    ("ssm.qkv", Q5_K, 10240, 5120, "in"),
+    ("ssm.gate", Q5_K, 6144, 5120, "in"),
+    ("ssm.beta", Q8_0, 48, 5120, "in"),
+    ("ssm.alpha", Q8_0, 48, 5120, "in"),
+    ("ssm.out", Q6_K, 5120, 6144, "out"),
+]
+ATTN_LAYER = [
+    ("attn.q", Q5_K, 12288, 5120, "in"),
+    ("attn.k", Q6_K, 1024, 5120, "in"),
+    ("attn.v", Q6_K, 1024, 5120, "in"),
+    ("attn.out", Q6_K, 5120, 6144, "out"),
+]
+FFN = [
+    ("ffn.gate", Q3_K, 17408, 5120, "ffn_in"),
+    ("ffn.up", Q3_K, 17408, 5120, "ffn_in"),
+    ("ffn.down", Q4_K, 5120, 17408, "down"),
+]
+LM_HEAD = ("output", Q6_K, 248320, 5120, "head")
+N_LAYERS = 64
+
+
+def sweep_plan():
+    """[(name, type, rows, cols, input-key)] of one decode step in execution order."""
+    plan = []
+    for layer in range(N_LAYERS):
+        mix = ATTN_LAYER if layer % 4 == 3 else SSM_LAYER
+        for name, ty, rows, cols, grp in mix + FFN:
+            plan.append((f"blk.{layer}.{name}", ty, rows, cols, f"{layer}.{grp}"))
+    plan.append(LM_HEAD[:4] + ("head",))
+    return plan
+
+
+TYPE_NAMES = {Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_0: "Q8_0", IQ4_XS: "IQ4_XS",
+              IQ3_S: "IQ3_S", IQ2_XXS: "IQ2_XXS"}
+PER_TYPE = [Q4_K, Q3_K, IQ4_XS, IQ3_S, IQ2_XXS, Q6_K]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def alg_bytes(ty, rows, cols, ntok):
+    from vinf_3080ti_amd import row_bytes
+
+    return rows * row_bytes(ty, cols) + 4 * ntok * (rows + cols)
+
+
+class Hip:
+    """Thin layer over the C ABI with torch-owned device memory."""
+
+    def __init__(self, torch):
+        from vinf_3080ti_amd import _lib
+
+        self.torch = torch
+        self.lib = _lib.load()
+        _lib.check(self.lib.vq_init(), "vq_init")
+        self.stream = torch.cuda.current_stream()
+
+    def s(self):
+        return self.torch.cuda.current_stream().cuda_stream
+
+    def quantize(self, x, ntok, cols, xq, xd, xs):
+        st = self.lib.vq_quantize_x(x.data_ptr(), ntok, cols, xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), self.s())
+        assert st == 0, st
+
+    def qmv_q(self, ty, w, rows, cols, xq, xd, xs, ntok, y):
+        st = self.lib.vq_qmv_q(ty, w.data_ptr(), rows, cols, xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), ntok,
+                               y.data_ptr(), self.s())
+        assert st == 0, st
+
+    def argmax(self, y, n, ntok, out):
+        st = self.lib.vq_argmax_rows(y.data_ptr(), n, ntok, out.data_ptr(), self.s())
+        assert st == 0, st
+
+
+def make_weights(torch, ty, rows, cols, seed, copies=1):
+    from vinf_3080ti_amd.synth import torch_baseline_rows
+
+    return [torch_baseline_rows(ty, rows, cols, seed + 7919 * c, "cuda") for c in range(copies)]
+
+
+def time_kernel_loop(torch, fn, n_iter):
+    """Average duration (ms) of fn() launches bracketed by HIP events on the current stream."""
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(n_iter):
+        fn(i)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / n_iter
+
+
+def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=640 << 20):
+    """Per-launch µs and GB/s of the matvec kernel alone (activations pre-quantized), rotating weights."""
+    from vinf_3080ti_amd import row_bytes
+
+    nbytes = rows * row_bytes(ty, cols)
+    copies = max(2, -(-min_rotation_bytes // nbytes))
+    ws = make_weights(torch, ty, rows, cols, 1234 + ty, copies)
+    x = torch.randn(ntok, cols, device="cuda")
+    ng = cols // 32
+    xq = torch.empty(ntok, cols, dtype=torch.int8, device="cuda")
+    xd = torch.empty(ntok, ng, device="cuda")
+    xs = torch.empty(ntok, ng, device="cuda")
+    y = torch.empty(ntok, rows, device="cuda")
+    hip.quantize(x, ntok, cols, xq, xd, xs)
+    for i in range(copies):  # warm-up
+        hip.qmv_q(ty, ws[i], rows, cols, xq, xd, xs, ntok, y)
+    ms = time_kernel_loop(torch, lambda i: hip.qmv_q(ty, ws[i % copies], rows, cols, xq, xd, xs, ntok, y), iters)
+    b = alg_bytes(ty, rows, cols, ntok)
+    del ws
+    torch.cuda.empty_cache()
+    return {"us": ms * 1e3, "GBps": b / (ms * 1e-3) / 1e9, "bytes": b, "frac": b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "copies": copies}
+
+
+class Sweep:
+    """All weights of one 27B decode step resident in HBM, plus the per-step launch sequence."""
+
+    def __init__(self, torch, hip, ntok):
+        self.torch, self.hip, self.ntok = torch, hip, ntok
+        self.plan = sweep_plan()
+        self.w = [make_weights(torch, ty, rows, cols, 1 + i)[0] for i, (_, ty, rows, cols, _) in enumerate(self.plan)]
+        self.bytes = sum(alg_bytes(ty, r, c, ntok) for _, ty, r, c, _ in self.plan)
+        self.weight_bytes = sum(w.numel() - 256 for w in self.w)
+        maxc = max(p[3] for p in self.plan)
+        maxr = max(p[2] for p in self.plan)
+        self.x = torch.randn(ntok, maxc, device="cuda")
+        self.xq = torch.empty(ntok * maxc, dtype=torch.int8, device="cuda")
+        self.xd = torch.empty(ntok * maxc // 32, device="cuda")
+        self.xs = torch.empty(ntok * maxc // 32, device="cuda")
+        self.y = torch.empty(ntok * maxr, device="cuda")
+        self.ids = torch.empty(ntok, dtype=torch.int32, device="cuda")
+
+    def step(self):
+        """One decode-step sweep: every matrix read once; matrices sharing an input (ssm qkv/gate/beta/alpha,
+        attention q/k/v, ffn gate/up) reuse one int8 quantization of it."""
+        hip, ntok = self.hip, self.ntok
+        prev = None
+        for (name, ty, rows, cols, key), w in zip(self.plan, self.w):
+            if key != prev:
+                hip.quantize(self.x, ntok, cols, self.xq, self.xd, self.xs)
+                prev = key
+            hip.qmv_q(ty, w, rows, cols, self.xq, self.xd, self.xs, ntok, self.y)
+            if name == "output":
+                hip.argmax(self.y, rows, ntok, self.ids)
+
+
+def cpu_baseline(budget_s=12.0):
+    """The reference's own CPU path (oracle/_ref, compiled from qwen_cpu.c) on a bounded sample of the sweep:
+    each distinct matrix shape timed once at batch 1 (LM head on 1/16 of its rows, scaled), then combined
+    with the per-step counts into an estimated ms per sweep and GB/s."""
+    import glob
+    import importlib.util
+
+    import numpy as np
+
+    from vinf_3080ti_amd import synth, tables
+
+    paths = glob.glob(str(ROOT / "oracle" / "_ref" / "_cpu_qwen*.so"))
+    threads = max(1, min(16, (os.cpu_count() or 2) // 2))
+    if paths:
+        spec = importlib.util.spec_from_file_location("_cpu_qwen", paths[0])
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        rt = mod.CpuRuntime(tables.table("iq3s_grid"), threads)
+        kind = "reference"
+
+        def run(ty, w, rows, cols, x):
+            rt.add_tensor(f"w{id(w)}", w, ty, cols, rows)
+            rt.alloc("x", cols)
+            rt.alloc("y", rows)
+            rt.write("x", x.tobytes())
+            t0 = time.perf_counter()
+            n = 0
+            while True:
+                rt.qmv(f"w{id(w)}", "x", "y", 1)
+                n += 1
+                if time.perf_counter() - t0 > budget_s / 13:
+                    break
+            return (time.perf_counter() - t0) / n
+    else:
+        from oracle import oracle
+
+        kind = "port"
+
+        def run(ty, w, rows, cols, x):
+            t0 = time.perf_counter()
+            n = 0
+            while True:
+                oracle.qmv(ty, w, rows, cols, x, 1, threads=threads)
+                n += 1
+                if time.perf_counter() - t0 > budget_s / 13:
+                    break
+            return (time.perf_counter() - t0) / n
+
+    rng = np.random.default_rng(5)
+    total_s, total_b = 0.0, 0
+    counts = {}
+    for name, ty, rows, cols, _ in sweep_plan():
+        key = (name.split(".", 2)[-1], ty, rows, cols)
+        counts[key] = counts.get(key, 0) + 1
+    for (name, ty, rows, cols), count in counts.items():
+        r = rows if rows < 100000 else rows // 16
+        w = synth.baseline_rows(ty, r, cols, rng)
+        x = rng.standard_normal(cols).astype(np.float32)
+        t = run(ty, w, r, cols, x) * (rows / r)
+        total_s += t * count
+        total_b += alg_bytes(ty, rows, cols, 1) * count
+    return {"value": total_b / total_s / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
+            "ms_per_step": total_s * 1e3,
+            "sample": "27B sweep, batch 1: each distinct matrix shape timed once (LM head on 1/16 of its rows), "
+                      "weighted by its per-step count"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--ntok", type=int, default=1)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-per-type", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (weights shard by rows; see "
+              "DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    hip = Hip(torch)
+
+    # Roofline of the dominant kernel (FFN gate/up: Q3_K 17408x5120, 128 launches per step).
+    log("roofline: Q3_K 17408x5120 matvec")
+    dom = bench_matvec(torch, hip, Q3_K, 17408, 5120, args.ntok, iters=100)
+    per_type = {}
+    if not args.no_per_type:
+        for ty in PER_TYPE:
+            log(f"per-type: {TYPE_NAMES[ty]} 5120x17408")
+            r = bench_matvec(torch, hip, ty, 5120, 17408, args.ntok)
+            per_type[TYPE_NAMES[ty]] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+        r = bench_matvec(torch, hip, Q4_K, 4096, 4096, args.ntok)
+        per_type["Q4_K@4096x4096"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+
+    log("sweep: allocating 13.4 GiB of weights")
+    sw = Sweep(torch, hip, args.ntok)
+    for _ in range(args.warmup):
+        sw.step()
+    torch.cuda.synchronize()
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                sw.step()
+        torch.cuda.synchronize()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+    log(f"sweep: timing {args.steps} steps ({'graph' if graph else 'eager'})")
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        graph.replay() if graph else sw.step()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(stop) / args.steps
+    value = sw.bytes / (ms * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline: reference CPU path on a bounded sample")
+        cpu = cpu_baseline()
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"qwen35-27B decode-step weight sweep (UD-Q3_K_XL-like mix, Q6_K LM head + argmax), batch {args.ntok}",
+            "ntok": args.ntok,
+            "bytes_per_step": sw.bytes,
+            "weight_bytes_per_step": sw.weight_bytes,
+            "launch": "hipGraph" if graph else "eager",
+            "frac_of_hbm_peak": round(value / HBM_PEAK_GBPS, 4),
+            "wall_s": round(wall, 3),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"qmv_stream_kernel<Q3_K,{args.ntok}> 17408x5120",
+            "achieved": round(dom["GBps"], 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(dom["frac"], 4),
+            "avg_us": round(dom["us"], 3),
+            "traffic": None,
+        },
+        "cpu_baseline": None if cpu is None else {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()},
+        "per_type": per_type,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,106 @@
+/* vq.h -- C ABI of the MI355X quantized-weight matvec library (libvq_hip.so).
+ *
+ * Plain pointers and sizes only. Every device pointer is a HIP device allocation on the current device;
+ * `stream` is a hipStream_t (NULL = the null stream). All launches are asynchronous on `stream`.
+ * Every entry point returns an int status: 0 on success, a negative VQ_ERR_* code for an invalid
+ * argument (checked on the host before anything is launched), or a positive hipError_t value.
+ *
+ * Layouts (the reference's, see /root/reference/engine/csrc/megakernel/qwen_runtime.cu:616,626 and
+ * csrc/cpu/qwen_cpu.c:603,635):
+ *   w    raw GGUF blocks, row-major: row r occupies bytes [r*row_bytes, (r+1)*row_bytes) with
+ *        row_bytes = cols/block_size*type_size, and at least VQ_TAIL_PAD (16) readable bytes follow the
+ *        last row (the reference pads uploads the same way, qwen_runtime.cu:1366-1367)
+ *   x    fp32 activations [ntok][cols]
+ *   y    fp32 outputs     [ntok][rows]
+ *   xq   int8 [ntok][cols], xd/xs fp32 [ntok][cols/32]: per 32-group scale d and d*sum(q)
+ */
+#ifndef VQ_H_
+#define VQ_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes (positive values are hipError_t). */
+#define VQ_OK 0
+#define VQ_ERR_TYPE (-1)      /* unsupported GGUF type id                                   */
+#define VQ_ERR_SHAPE (-2)     /* rows/cols/ntok invalid, cols not a multiple of 32 / block  */
+#define VQ_ERR_WORKSPACE (-3) /* workspace NULL or smaller than the matching *_bytes query  */
+#define VQ_ERR_ARG (-4)       /* NULL pointer or other invalid argument                     */
+#define VQ_ERR_NOT_INIT (-5)  /* vq_init() has not run on this device                        */
+
+/* GGUF type ids accepted by every entry point (qwen_quant.cuh:17-33, parser.py:33-63). */
+#define VQ_TYPE_F32 0
+#define VQ_TYPE_F16 1
+#define VQ_TYPE_Q8_0 8
+#define VQ_TYPE_Q2_K 10
+#define VQ_TYPE_Q3_K 11
+#define VQ_TYPE_Q4_K 12
+#define VQ_TYPE_Q5_K 13
+#define VQ_TYPE_Q6_K 14
+#define VQ_TYPE_IQ2_XXS 16
+#define VQ_TYPE_IQ2_XS 17
+#define VQ_TYPE_IQ3_XXS 18
+#define VQ_TYPE_IQ4_NL 20
+#define VQ_TYPE_IQ3_S 21
+#define VQ_TYPE_IQ2_S 22
+#define VQ_TYPE_IQ4_XS 23
+
+/* Replaces: type_traits() (qwen_quant.cuh:40-58) / GGUF_TYPE_TRAITS (parser.py:65-94). */
+int vq_type_traits(int type, int *block_size, int *type_size);
+
+/* Bytes of one weight row, or -1 for an unsupported type / cols not a multiple of the block size.
+ * Replaces: row_bytes computation in Runtime_upload (qwen_runtime.cu:1352). */
+long long vq_row_bytes(int type, int cols);
+
+/* Human-readable text for a status code (for RuntimeError messages, qwen_runtime.cu:1100-1103). */
+const char *vq_status_string(int status);
+
+/* Prepare the library on the current device. Replaces: Runtime_init (qwen_runtime.cu:1272-1297). */
+int vq_init(void);
+
+/* Replace the IQ3_S codebook (512 entries x 4 magnitudes, 2048 bytes, host memory) on the current device.
+ * Replaces: the iq3s_grid argument of Runtime(iq3s_grid) (qwen_runtime.cu:1272-1286, cuda/qwen_runtime.py:41-44). */
+int vq_set_iq3s_grid(const uint8_t *grid);
+
+/* Workspace bytes vq_qmv needs for the int8 activations of `ntok` tokens of `cols` columns. */
+size_t vq_qmv_workspace_bytes(int cols, int ntok);
+
+/* Quantize activations to int8 per 32-group: d = amax/127, q = rint(x/d), xs = d*sum(q).
+ * Replaces: the activation quantizer of Cpu_qmv (qwen_cpu.c:607-627). */
+int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, float *xs, void *stream);
+
+/* y[t][r] = W[r] . x[t] for t < ntok (any ntok >= 1; weights are read once per 8 tokens).
+ * Quantized types quantize x into `workspace` first (vq_qmv_workspace_bytes); F32/F16 weights use x
+ * directly and need no workspace. Replaces: Runtime_qmv (qwen_runtime.cu:1860-1912) on its matvec branch,
+ * whose numerics contract is Cpu_qmv (qwen_cpu.c:581-641). */
+int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, float *y, void *workspace,
+           size_t workspace_bytes, void *stream);
+
+/* Same as vq_qmv with activations already quantized by vq_quantize_x (quantized types only), so several
+ * matrices that share one input (gate/up, q/k/v) quantize it once. Replaces: dot_row_q's caller loop
+ * (qwen_cpu.c:628-637). */
+int vq_qmv_q(int type, const uint8_t *w, int rows, int cols, const int8_t *xq, const float *xd, const float *xs,
+             int ntok, float *y, void *stream);
+
+/* Test hook: part[((t*rows + r)*(cols/32) + g)*2 + h] = exact int32 sum over the 16 elements of half h
+ * of group g of (weight code * xq). Replaces: the integer stage of dot_row_q (qwen_cpu.c:125-342). */
+int vq_int_partials(int type, const uint8_t *w, int rows, int cols, const int8_t *xq, int ntok, int32_t *part,
+                    void *stream);
+
+/* Test hook: out[r*cols + c] = fp32 value of W[r][c]. Replaces: deq8 (qwen_quant.cuh:151-279) and
+ * dequantize_tensor (dequant.py:17-57). */
+int vq_dequant_rows(int type, const uint8_t *w, int rows, int cols, float *out, void *stream);
+
+/* out[t] = argmax_i x[t*n + i] (ties -> lowest index; NaN never wins; an all -inf/NaN row gives INT32_MAX).
+ * Replaces: argmax_kernel + Runtime_argmax / Runtime_argmax_rows (qwen_runtime.cu:850-876, 2167-2197). */
+int vq_argmax_rows(const float *x, int n, int ntok, int32_t *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VQ_H_ */

@@ -1,0 +1,127 @@
+"""ctypes binding of oracle/libvq_oracle.so (test infrastructure only; see vq_oracle.c's header).
+
+Functions mirror the reference CPU path (/root/reference/engine/csrc/cpu/qwen_cpu.c):
+  qmv            Cpu_qmv (:581-641) with dot_row_q/dot_row_f (:125-360), bit-identical fp32 outputs
+  quantize_x     activation quantizer (:607-627)
+  dequant_rows   dequant.py:121-500 / qwen_quant.cuh deq8 (:151-279)
+  int_partials   exact int32 sum of code*xq per (token, row, group, 16-half)
+  decode_codes   integer codes + per-16 scales/mins with dequant == scale*code - min
+  argmax_rows    argmax_kernel (qwen_runtime.cu:850-876), ties to the lowest index
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libvq_oracle.so"
+
+_TABLE_IDS = {"iq2xxs_grid": 0, "iq2xs_grid": 1, "iq2s_grid": 2, "iq3xxs_grid": 3, "iq3s_grid": 4, "ksigns_iq2xs": 5}
+
+_lib = None
+
+
+def build() -> None:
+    import subprocess
+
+    subprocess.check_call(["make", "-s", "-C", str(HERE), "all"])
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        P, I = ctypes.c_void_p, ctypes.c_int
+        L.vqo_traits.argtypes = [I, ctypes.POINTER(I), ctypes.POINTER(I)]
+        L.vqo_table.argtypes = [I, P]
+        L.vqo_dequant_rows.argtypes = [I, P, I, I, P]
+        L.vqo_decode_codes.argtypes = [I, P, I, I, P, P, P]
+        L.vqo_quantize_x.argtypes = [P, I, I, P, P, P]
+        L.vqo_int_partials.argtypes = [I, P, I, I, P, I, P]
+        L.vqo_qmv.argtypes = [I, P, I, I, P, I, P, I]
+        L.vqo_argmax_rows.argtypes = [P, I, I, P]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def _u8(raw) -> np.ndarray:
+    return np.ascontiguousarray(np.frombuffer(raw, dtype=np.uint8) if isinstance(raw, (bytes, bytearray, memoryview)) else raw, dtype=np.uint8)
+
+
+def traits(type_id: int) -> tuple[int, int]:
+    bs, ts = ctypes.c_int(), ctypes.c_int()
+    if not lib().vqo_traits(type_id, ctypes.byref(bs), ctypes.byref(ts)):
+        raise ValueError(f"unsupported type {type_id}")
+    return bs.value, ts.value
+
+
+def table(name: str) -> bytes:
+    n = lib().vqo_table(_TABLE_IDS[name], None)
+    buf = np.empty(n, np.uint8)
+    lib().vqo_table(_TABLE_IDS[name], _p(buf))
+    return buf.tobytes()
+
+
+def dequant_rows(type_id: int, raw, rows: int, cols: int) -> np.ndarray:
+    w = _u8(raw)
+    out = np.empty((rows, cols), np.float32)
+    if lib().vqo_dequant_rows(type_id, _p(w), rows, cols, _p(out)):
+        raise ValueError("dequant_rows: bad type/shape")
+    return out
+
+
+def decode_codes(type_id: int, raw, rows: int, cols: int):
+    w = _u8(raw)
+    codes = np.empty((rows, cols), np.int8)
+    scales = np.empty((rows, cols // 16), np.float32)
+    mins = np.empty((rows, cols // 16), np.float32)
+    if lib().vqo_decode_codes(type_id, _p(w), rows, cols, _p(codes), _p(scales), _p(mins)):
+        raise ValueError("decode_codes: bad type/shape")
+    return codes, scales, mins
+
+
+def quantize_x(x: np.ndarray, ntok: int, cols: int):
+    x = np.ascontiguousarray(x, np.float32).reshape(ntok, cols)
+    xq = np.empty((ntok, cols), np.int8)
+    xd = np.empty((ntok, cols // 32), np.float32)
+    xs = np.empty((ntok, cols // 32), np.float32)
+    if lib().vqo_quantize_x(_p(x), ntok, cols, _p(xq), _p(xd), _p(xs)):
+        raise ValueError("quantize_x: bad shape")
+    return xq, xd, xs
+
+
+def int_partials(type_id: int, raw, rows: int, cols: int, xq: np.ndarray, ntok: int) -> np.ndarray:
+    w = _u8(raw)
+    xq = np.ascontiguousarray(xq, np.int8)
+    out = np.empty((ntok, rows, cols // 32, 2), np.int32)
+    if lib().vqo_int_partials(type_id, _p(w), rows, cols, _p(xq), ntok, _p(out)):
+        raise ValueError("int_partials: bad type/shape")
+    return out
+
+
+def qmv(type_id: int, raw, rows: int, cols: int, x: np.ndarray, ntok: int, threads: int | None = None) -> np.ndarray:
+    w = _u8(raw)
+    x = np.ascontiguousarray(x, np.float32).reshape(ntok, cols)
+    y = np.empty((ntok, rows), np.float32)
+    if threads is None:
+        threads = os.cpu_count() or 1
+    if lib().vqo_qmv(type_id, _p(w), rows, cols, _p(x), ntok, _p(y), threads):
+        raise ValueError("qmv: bad type/shape")
+    return y
+
+
+def argmax_rows(x: np.ndarray, n: int, ntok: int) -> list[int]:
+    x = np.ascontiguousarray(x, np.float32).reshape(ntok, n)
+    out = np.empty(ntok, np.int32)
+    lib().vqo_argmax_rows(_p(x), n, ntok, _p(out))
+    return [int(v) for v in out]

@@ -1,0 +1,91 @@
+"""The C-ABI library loads, exports every symbol include/vq.h declares, and rejects bad arguments on the
+host before anything reaches the GPU; the Python runtime's validation mirrors the reference's. CPU only."""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+from vinf_3080ti_amd import _lib, gguf_types, runtime
+from vinf_3080ti_amd import GGUFTensorType as T
+from vinf_3080ti_amd.build import LIB
+
+HEADER = ROOT / "include" / "vq.h"
+
+
+def declared_symbols() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(vq_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB.exists():
+        pytest.fail(f"{LIB} is not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(str(LIB))
+    for name in declared_symbols():
+        assert hasattr(raw, name), name
+
+
+def test_traits_match_python_table(lib):
+    for ty, (bs, ts) in gguf_types.TYPE_TRAITS.items():
+        b, t = ctypes.c_int(), ctypes.c_int()
+        assert lib.vq_type_traits(int(ty), ctypes.byref(b), ctypes.byref(t)) == 0
+        assert (b.value, t.value) == (bs, ts)
+        assert lib.vq_row_bytes(int(ty), 5120 if bs <= 256 and 5120 % bs == 0 else bs) == (5120 // bs * ts if 5120 % bs == 0 else ts)
+    assert lib.vq_type_traits(2, None, None) == _lib.VQ_ERR_TYPE  # Q4_0 has no matvec here
+    assert lib.vq_row_bytes(int(T.Q4_K), 100) == -1
+
+
+def test_host_side_argument_checks(lib):
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails its host-side checks
+    assert lib.vq_qmv(2, fake, 4, 256, fake, 1, fake, fake, 1 << 20, None) == _lib.VQ_ERR_TYPE
+    assert lib.vq_qmv(int(T.Q4_K), fake, 4, 100, fake, 1, fake, fake, 1 << 20, None) == _lib.VQ_ERR_SHAPE
+    assert lib.vq_qmv(int(T.Q4_K), fake, 0, 256, fake, 1, fake, fake, 1 << 20, None) == _lib.VQ_ERR_SHAPE
+    assert lib.vq_qmv(int(T.Q4_K), fake, 4, 256, fake, 0, fake, fake, 1 << 20, None) == _lib.VQ_ERR_SHAPE
+    assert lib.vq_qmv(int(T.Q4_K), None, 4, 256, fake, 1, fake, fake, 1 << 20, None) == _lib.VQ_ERR_ARG
+    assert lib.vq_qmv(int(T.Q4_K), fake, 4, 256, fake, 1, fake, fake, 16, None) == _lib.VQ_ERR_WORKSPACE
+    assert lib.vq_qmv_q(int(T.F32), fake, 4, 256, fake, fake, fake, 1, fake, None) == _lib.VQ_ERR_TYPE
+    assert lib.vq_quantize_x(fake, 1, 48, fake, fake, fake, None) == _lib.VQ_ERR_SHAPE
+    assert lib.vq_argmax_rows(fake, 0, 1, fake, None) == _lib.VQ_ERR_SHAPE
+    assert lib.vq_set_iq3s_grid(None) == _lib.VQ_ERR_ARG
+    assert lib.vq_qmv_workspace_bytes(5120, 8) >= 5120 * 8 + 2 * 4 * 160 * 8
+    assert b"workspace" in lib.vq_status_string(_lib.VQ_ERR_WORKSPACE)
+
+
+def test_python_error_mapping(lib):
+    with pytest.raises(ValueError):
+        _lib.check(_lib.VQ_ERR_SHAPE, "qmv")
+    with pytest.raises(RuntimeError, match="qmv failed"):
+        _lib.check(_lib.VQ_ERR_WORKSPACE, "qmv")
+
+
+def test_upload_validation_mirrors_reference():
+    # test_phase30_cuda_qmatvec.py:127-134: Q4_0 is rejected, a wrong byte length is rejected.
+    with pytest.raises(ValueError):
+        runtime._check_upload_args("w", 34, int(T.Q4_0) if hasattr(T, "Q4_0") else 2, 32, 1)
+    with pytest.raises(ValueError):
+        runtime._check_upload_args("w", 33, int(T.Q8_0), 32, 1)
+    with pytest.raises(ValueError):
+        runtime._check_upload_args("w", 144, int(T.Q4_K), 128, 1)  # cols not a multiple of 256
+    assert runtime._check_upload_args("w", 2 * 144, int(T.Q4_K), 256, 2) == (144, 288)
+    with pytest.raises(ValueError):
+        runtime._check_qmv_args("w", 256, 0)
+    with pytest.raises(ValueError):
+        runtime._check_qmv_args("w", 48, 1)
+
+
+def test_product_does_not_import_oracle():
+    for path in (ROOT / "vinf_3080ti_amd").rglob("*.py"):
+        text = path.read_text()
+        assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", text, re.M), path

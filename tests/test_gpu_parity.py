@@ -1,0 +1,174 @@
+"""GPU parity of the HIP path against the oracle and the reference's golden vectors, through the C ABI.
+
+Bars: quantizer, dequantization and integer partials bit-exact; fp32 outputs within rel-L2 <= 1e-5 of
+the reference CPU path (the oracle is bit-identical to it, see test_oracle.py).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from vinf_3080ti_amd import GGUFTensorType as T
+from vinf_3080ti_amd import QUANT_TYPES, synth
+
+pytestmark = pytest.mark.gpu
+ALL_TYPES = list(QUANT_TYPES) + [T.F32, T.F16]
+REL_L2_TOL = 1e-5  # north-star fp32 tolerance vs the reference CPU path
+
+
+@pytest.fixture(scope="module")
+def env():
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from vinf_3080ti_amd import _lib
+
+    lib = _lib.load()
+    assert lib.vq_init() == 0
+    return torch, lib
+
+
+def dev(torch, a: np.ndarray):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def wdev(torch, w: np.ndarray):
+    """Weights with the 16-byte tail pad the kernels may read."""
+    buf = np.zeros(w.size + 256, np.uint8)
+    buf[: w.size] = w
+    return dev(torch, buf)
+
+
+def P(t) -> int:
+    return t.data_ptr()
+
+
+def gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok):
+    wd, xd = wdev(torch, w), dev(torch, x.astype(np.float32).reshape(ntok, cols))
+    y = torch.empty(ntok, rows, dtype=torch.float32, device="cuda")
+    nws = lib.vq_qmv_workspace_bytes(cols, ntok)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
+    st = lib.vq_qmv(int(ty), P(wd), rows, cols, P(xd), ntok, P(y), P(ws), nws, None)
+    assert st == 0, lib.vq_status_string(st)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("ntok,cols", [(1, 256), (3, 1024), (8, 5120), (2, 17408)])
+def test_quantize_x_bit_exact(env, oracle_mod, ntok, cols):
+    torch, lib = env
+    rng = np.random.default_rng(cols + ntok)
+    x = (rng.standard_normal((ntok, cols)) * rng.choice([1e-3, 1.0, 30.0], size=(ntok, cols))).astype(np.float32)
+    x[0, :32] = 0.0  # a zero group
+    x[-1, 64:96] = np.float32(0.5) * np.arange(-16, 16, dtype=np.float32)  # exact halves after scaling
+    xd_ = dev(torch, x)
+    ng = cols // 32
+    xq = torch.empty(ntok, cols, dtype=torch.int8, device="cuda")
+    d = torch.empty(ntok, ng, dtype=torch.float32, device="cuda")
+    s = torch.empty(ntok, ng, dtype=torch.float32, device="cuda")
+    assert lib.vq_quantize_x(P(xd_), ntok, cols, P(xq), P(d), P(s), None) == 0
+    torch.cuda.synchronize()
+    q_ref, d_ref, s_ref = oracle_mod.quantize_x(x, ntok, cols)
+    assert np.array_equal(xq.cpu().numpy(), q_ref)
+    assert np.array_equal(d.cpu().numpy().view(np.uint32), d_ref.view(np.uint32))
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("ty", ALL_TYPES, ids=lambda t: t.name)
+def test_dequant_bit_exact(env, oracle_mod, ty):
+    torch, lib = env
+    rows, cols = 7, 1024
+    w = synth.baseline_rows(ty, rows, cols, 11 + int(ty))
+    out = torch.empty(rows, cols, dtype=torch.float32, device="cuda")
+    wd = wdev(torch, w)
+    assert lib.vq_dequant_rows(int(ty), P(wd), rows, cols, P(out), None) == 0
+    torch.cuda.synchronize()
+    ref = oracle_mod.dequant_rows(int(ty), w, rows, cols)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("ty", QUANT_TYPES, ids=lambda t: t.name)
+def test_int_partials_bit_exact(env, oracle_mod, ty):
+    torch, lib = env
+    rows, cols, ntok = 9, 1024, 3
+    rng = np.random.default_rng(40 + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    xq, _, _ = oracle_mod.quantize_x(x, ntok, cols)
+    part = torch.empty(ntok, rows, cols // 32, 2, dtype=torch.int32, device="cuda")
+    wd, xqd = wdev(torch, w), dev(torch, xq)
+    assert lib.vq_int_partials(int(ty), P(wd), rows, cols, P(xqd), ntok, P(part), None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(part.cpu().numpy(), oracle_mod.int_partials(int(ty), w, rows, cols, xq, ntok))
+
+
+@pytest.mark.parametrize("ty", ALL_TYPES, ids=lambda t: t.name)
+def test_qmv_matches_reference_golden(env, golden, ty):
+    torch, lib = env
+    w, x, y = golden[f"w_{ty.name}"], golden[f"x_{ty.name}"], golden[f"y_{ty.name}"]
+    got = gpu_qmv(torch, lib, ty, w, y.shape[1], x.shape[1], x, x.shape[0])
+    assert rel_l2(got, y) <= REL_L2_TOL
+
+
+@pytest.mark.parametrize("ty", ALL_TYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("ntok", [1, 2, 5, 8, 11])
+def test_qmv_matches_oracle(env, oracle_mod, ty, ntok):
+    torch, lib = env
+    rows, cols = 37, 2048 if ty not in (T.F32, T.F16) else 1024
+    rng = np.random.default_rng(1000 * ntok + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    got = gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok)
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok)
+    for t in range(ntok):
+        assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, ntok, t)
+
+
+@pytest.mark.parametrize(
+    "ty,rows,cols",
+    [(T.Q4_K, 5120, 17408), (T.Q3_K, 5120, 17408), (T.Q6_K, 5120, 17408), (T.IQ4_XS, 5120, 17408),
+     (T.IQ3_S, 5120, 17408), (T.IQ2_XXS, 5120, 17408), (T.Q3_K, 17408, 5120), (T.Q5_K, 10240, 5120),
+     (T.Q8_0, 48, 5120), (T.Q4_K, 4096, 4096)],
+    ids=lambda v: v.name if isinstance(v, T) else str(v))
+def test_qmv_baseline_shapes(env, oracle_mod, ty, rows, cols):
+    torch, lib = env
+    rng = np.random.default_rng(rows + cols + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    for ntok in (1, 8):
+        x = rng.standard_normal((ntok, cols)).astype(np.float32)
+        got = gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok)
+        ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok, threads=16)
+        assert rel_l2(got, ref) <= REL_L2_TOL, (ty.name, ntok)
+
+
+def test_argmax_rows_semantics(env, oracle_mod):
+    torch, lib = env
+    rng = np.random.default_rng(3)
+    n, ntok = 248320, 4
+    x = rng.standard_normal((ntok, n)).astype(np.float32)
+    x[1, 1000] = x[1, 5] = 50.0  # tie -> lowest index
+    x[2, :] = np.nan
+    x[2, 777] = 1.0  # NaN never wins
+    x[3, :] = -np.inf  # no value beats -inf -> INT32_MAX like the reference kernel
+    out = torch.empty(ntok, dtype=torch.int32, device="cuda")
+    xd_ = dev(torch, x)
+    assert lib.vq_argmax_rows(P(xd_), n, ntok, P(out), None) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().tolist()
+    assert got == oracle_mod.argmax_rows(x, n, ntok)
+    assert got[1] == 5 and got[2] == 777 and got[3] == 2**31 - 1
+
+
+def test_zero_and_extreme_activations(env, oracle_mod):
+    torch, lib = env
+    rows, cols = 16, 1024
+    w = synth.baseline_rows(T.Q4_K, rows, cols, 9)
+    x = np.zeros((2, cols), np.float32)
+    x[1, ::7] = 3.0e4
+    got = gpu_qmv(torch, lib, T.Q4_K, w, rows, cols, x, 2)
+    ref = oracle_mod.qmv(int(T.Q4_K), w, rows, cols, x, 2)
+    assert np.array_equal(got[0], ref[0]) and np.all(got[0] == 0)
+    assert rel_l2(got[1], ref[1]) <= REL_L2_TOL

@@ -1,0 +1,126 @@
+"""The Python runtime on the GPU: reference-style API behaviour (engine/tests/test_phase30_cuda_qmatvec.py,
+test_phase31e_cpu_layers.py) with the HIP library underneath."""
+from __future__ import annotations
+
+import random
+
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from vinf_3080ti_amd import GGUFTensorType as T
+from vinf_3080ti_amd import HIP_MATVEC_TYPES, QUANT_TYPES, synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def rt():
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from vinf_3080ti_amd.runtime import HipWeightRuntime
+
+    return HipWeightRuntime()
+
+
+def test_every_type_matches_cpu_dequant_within_int8_bound(rt, oracle_mod):
+    """test_phase31e_cpu_layers.py:29-60: int8-activation matvec vs float64 dequant matvec, bound
+    1.05 * sum_g sum|w| * amax_g(x) / 254 + 1e-4 (1 + |ref|) per output."""
+    rng = random.Random(3101)
+    rows, cols = 12, 512
+    for ty in sorted(HIP_MATVEC_TYPES):
+        raw = synth.synthetic_rows(ty, rows, cols, np.random.default_rng(rng.getrandbits(32)))
+        xs = np.array([[rng.uniform(-1, 1) for _ in range(cols)] for _ in range(3)], np.float32)
+        rt.upload_raw("w", raw.tobytes(), ty, cols, rows)
+        rt.alloc("w.x", cols * 3)
+        rt.alloc("w.y", rows * 3)
+        rt.write_floats("w.x", xs.reshape(-1).tolist())
+        rt.qmv("w", "w.x", "w.y", 3)
+        got = np.array(rt.read_floats("w.y"), np.float64).reshape(3, rows)
+        wf = oracle_mod.dequant_rows(int(ty), raw, rows, cols).astype(np.float64)
+        for t in range(3):
+            ref = wf @ xs[t].astype(np.float64)
+            if ty in (T.F32, T.F16):
+                bound = np.zeros(rows)
+            else:
+                amax = np.abs(xs[t].reshape(-1, 32)).max(1)
+                bound = (np.abs(wf).reshape(rows, -1, 32).sum(2) * amax / 254.0).sum(1)
+            assert np.all(np.abs(got[t] - ref) <= 1.05 * bound + 1e-4 * (1 + np.abs(ref))), ty.name
+        rt.free("w")
+    assert rt.device_bytes() == 0
+
+
+def test_matvec_sync_entry(rt, oracle_mod):
+    rows, cols = 5, 512
+    raw = synth.synthetic_rows(T.Q6_K, rows, cols, 30)
+    x = np.random.default_rng(30).uniform(-1, 1, cols).astype(np.float32)
+    rt.upload_raw("m", raw.tobytes(), T.Q6_K, cols, rows)
+    got = np.array(rt.matvec("m", x.tolist()), np.float32)
+    assert rel_l2(got, oracle_mod.qmv(int(T.Q6_K), raw, rows, cols, x, 1)[0]) <= 1e-5
+    rt.free("m")
+
+
+def test_invalid_uploads_and_names_fail_cleanly(rt):
+    """test_phase30_cuda_qmatvec.py:127-134 and the error contract of qwen_runtime.cu:1199-1223."""
+    with pytest.raises(ValueError):
+        rt.upload_raw("w", b"\x00" * 34, 2, 32, 1)  # Q4_0: no matvec
+    with pytest.raises(ValueError):
+        rt.upload_raw("w", b"\x00" * 33, T.Q8_0, 32, 1)
+    with pytest.raises(KeyError):
+        rt.matvec("missing", [0.0] * 32)
+    rt.upload_raw("q", bytes(34), T.Q8_0, 32, 1)
+    rt.alloc("x", 32)
+    rt.alloc("y", 1)
+    rt.alloc("h", 64, 2)
+    with pytest.raises(KeyError):
+        rt.qmv("q", "nope", "y")
+    with pytest.raises(ValueError):
+        rt.qmv("q", "x", "y", 2)  # x too small for 2 tokens
+    with pytest.raises(ValueError):
+        rt.qmv("q", "x", "y", 0)
+    with pytest.raises(TypeError):
+        rt.qmv("q", "h", "y")
+    with pytest.raises(ValueError):
+        rt.argmax_rows("x", 4, 0)
+    with pytest.raises(ValueError):
+        rt.alloc("z", 0)
+    rt.free("q")
+    with pytest.raises(KeyError):
+        rt.free("q")
+
+
+def test_buffers_roundtrip_and_argmax(rt):
+    rt.alloc("b", 10)
+    assert rt.read_floats("b") == [0.0] * 10
+    rt.write_floats("b", [1.0, 9.0, 3.0, 9.0], 2)
+    assert rt.read_floats("b", 4, 2) == [1.0, 9.0, 3.0, 9.0]
+    assert rt.argmax("b", 10) == 3
+    assert rt.argmax_rows("b", 5, 2) == [3, 0]
+    rt.zero("b")
+    assert rt.read_floats("b") == [0.0] * 10
+
+
+def test_tensor_info_and_reupload(rt):
+    raw = synth.synthetic_rows(T.Q4_K, 3, 512, 1)
+    rt.upload_raw("t", raw.tobytes(), T.Q4_K, 512, 3)
+    addr, ty, rows, cols, rb, nbytes, resident = rt.tensor_info("t")
+    assert (ty, rows, cols, rb, nbytes, resident) == (int(T.Q4_K), 3, 512, 288, 864, True)
+    assert addr % 256 == 0
+    rt.upload_raw("t", raw[:288].tobytes(), T.Q4_K, 512, 1)  # re-upload replaces
+    assert rt.tensor_info("t")[2] == 1 and rt.device_bytes() == 288
+    rt.free("t")
+
+
+def test_ntok_above_eight_chunks_like_reference(rt, oracle_mod):
+    rows, cols, ntok = 33, 1024, 19
+    raw = synth.baseline_rows(T.IQ3_S, rows, cols, 4)
+    x = np.random.default_rng(4).standard_normal((ntok, cols)).astype(np.float32)
+    rt.upload_raw("c", raw.tobytes(), T.IQ3_S, cols, rows)
+    rt.alloc("cx", cols * ntok)
+    rt.alloc("cy", rows * ntok)
+    rt.write_floats("cx", x.reshape(-1).tolist())
+    rt.qmv("c", "cx", "cy", ntok)
+    got = np.array(rt.read_floats("cy"), np.float32).reshape(ntok, rows)
+    assert rel_l2(got, oracle_mod.qmv(int(T.IQ3_S), raw, rows, cols, x, ntok)) <= 1e-5
+    rt.free("c")

@@ -1,0 +1,234 @@
+"""Pins of the CPU oracle (oracle/vq_oracle.c) against the reference: KATs from the reference's own tests,
+golden vectors written from the reference's compiled CPU path, codebook digests, and exact integer
+brute force. CPU only."""
+from __future__ import annotations
+
+import glob
+import hashlib
+import importlib.util
+import struct
+
+import numpy as np
+import pytest
+
+from conftest import REFERENCE, ROOT
+from vinf_3080ti_amd import GGUFTensorType as T
+from vinf_3080ti_amd import QUANT_TYPES, synth, tables
+
+ALL_TYPES = list(QUANT_TYPES) + [T.F32, T.F16]
+
+
+def dq(oracle, ty, block: bytes, cols: int) -> list[float]:
+    return [float(v) for v in oracle.dequant_rows(int(ty), block, 1, cols)[0]]
+
+
+def qs_pair() -> bytes:
+    return bytes(lo | (hi << 4) for lo, hi in zip(range(16), reversed(range(16))))
+
+
+# ---- known-answer tests of the reference (engine/tests/test_gguf_dequant.py) -------------------------
+
+def test_kat_q8_0(oracle_mod):  # test_gguf_dequant.py:38-44
+    v = dq(oracle_mod, T.Q8_0, struct.pack("<e32b", 0.5, *range(-16, 16)), 32)
+    assert v[0] == -8.0 and v[-1] == 7.5
+
+
+def test_kat_q4_k(oracle_mod):  # :54-74
+    block = struct.pack("<ee", 0.5, 0.25) + bytes([1, 2, 3, 4, 0, 1, 2, 3, 5, 6, 7, 8]) + qs_pair() * 8
+    v = dq(oracle_mod, T.Q4_K, block, 256)
+    assert v[:4] == [0.0, 0.5, 1.0, 1.5] and v[16:20] == [0.0, 0.5, 1.0, 1.5]
+    assert v[32:34] == [14.75, 13.75]
+    assert (v[64], v[96], v[128], v[160], v[192], v[224]) == (-0.5, 29.25, 0.0, 45.0, 0.0, 60.0)
+
+
+def test_kat_q3_k(oracle_mod):  # :76-97
+    hmask = bytearray([0xFF] * 32)
+    hmask[3] &= ~(1 << 5) & 0xFF
+    qs = bytearray([0xFF] * 64)
+    qs[32] = 0
+    scales = bytes(k | (k + 8) << 4 for k in range(8)) + bytes([0xE4] * 4)
+    v = dq(oracle_mod, T.Q3_K, bytes(hmask) + bytes(qs) + scales + struct.pack("<e", 0.5), 256)
+    expect = {0: -48.0, 3: -48.0, 35: -45.0, 80: -16.5, 128: 0.0, 129: 12.0, 160: 0.0, 163: -5.0, 255: 46.5}
+    assert {k: v[k] for k in expect} == expect
+
+
+def test_kat_iq3_s_grid():  # :99-106
+    g = tables.table("iq3s_grid")
+    assert len(g) == 2048
+    assert tuple(g[0:4]) == (1, 1, 1, 1) and tuple(g[12:16]) == (11, 1, 1, 1) and tuple(g[20:24]) == (1, 3, 1, 1)
+
+
+def test_kat_q2_k(oracle_mod):  # :108-125, expected values in ggml's loop order
+    scales = bytes((k % 16) | (((7 * k) % 16) << 4) for k in range(16))
+    qs = bytes((i * 37 + 11) % 256 for i in range(64))
+    v = dq(oracle_mod, T.Q2_K, scales + qs + struct.pack("<ee", 0.5, 0.25), 256)
+    expected, idx = [], 0
+    for n in range(2):
+        q = qs[32 * n : 32 * n + 32]
+        for j in range(4):
+            for s in range(2):
+                sc = scales[idx]
+                idx += 1
+                expected += [0.5 * (sc & 0xF) * ((q[16 * s + l] >> (2 * j)) & 3) - 0.25 * (sc >> 4) for l in range(16)]
+    assert v == [float(np.float32(e)) for e in expected]
+
+
+def test_kat_q5_k(oracle_mod):  # :127-142
+    block = struct.pack("<ee", 0.5, 0.25) + bytes([1, 2, 3, 4, 0, 1, 2, 3, 5, 6, 7, 8]) + bytes([0b01010101] * 32) + qs_pair() * 8
+    v = dq(oracle_mod, T.Q5_K, block, 256)
+    assert v[:4] == [8.0, 8.5, 9.0, 9.5] and v[32:36] == [14.75, 13.75, 12.75, 11.75]
+    assert (v[64], v[96], v[128], v[160], v[192], v[224]) == (23.5, 29.25, 40.0, 45.0, 56.0, 60.0)
+
+
+def test_kat_q6_k(oracle_mod):  # :144-159
+    block = bytes([0x10] * 128) + bytes([0b11100100] * 64) + struct.pack("<16b", *range(1, 17)) + struct.pack("<e", 0.5)
+    v = dq(oracle_mod, T.Q6_K, block, 256)
+    assert [v[i] for i in range(0, 128, 16)] == [-16.0, -32.0, -24.0, -32.0, 2.5, 3.0, 59.5, 68.0]
+
+
+def test_kat_iq4_nl(oracle_mod):  # :161-167
+    v = dq(oracle_mod, T.IQ4_NL, struct.pack("<e", 0.5) + qs_pair(), 32)
+    assert v[:4] == [-63.5, -52.0, -41.5, -32.5] and v[16:20] == [56.5, 44.5, 34.5, 26.5]
+
+
+def test_kat_iq4_xs(oracle_mod):  # :169-178
+    v = dq(oracle_mod, T.IQ4_XS, struct.pack("<eH", 0.5, 0xAAAA) + bytes([0x11] * 4) + qs_pair() * 8, 256)
+    assert v[:4] == [-63.5, -52.0, -41.5, -32.5] and v[32:36] == [-63.5, -52.0, -41.5, -32.5]
+
+
+def test_kat_iq3_s(oracle_mod):  # :180-193
+    block = struct.pack("<e", 0.5) + bytes(64) + bytes(8) + bytes([1] + [0] * 31) + bytes(4)
+    v = dq(oracle_mod, T.IQ3_S, block, 256)
+    assert v[0] == -0.5 and v[1:4] == [0.5, 0.5, 0.5] and v[32] == 0.5
+
+
+def test_kat_iq2_iq3xxs_closed_form(oracle_mod):
+    """No reference KAT covers these four types; pin one hand-built block each from the ggml layout."""
+    g2 = tables.table("iq2xxs_grid")
+    # IQ2_XXS, d = 1: group 0 picks entries 1,2,3,4 with sign patterns ksigns[1], 0, 0, 0 and scale nibble 15.
+    aux0 = 1 | (2 << 8) | (3 << 16) | (4 << 24)
+    aux1 = 1 | (15 << 28)
+    block = struct.pack("<e", 1.0) + struct.pack("<II", aux0, aux1) + bytes(56)
+    v = dq(oracle_mod, T.IQ2_XXS, block, 256)
+    db = (0.5 + 15) * 0.25
+    ks1 = tables.table("ksigns_iq2xs")[1]  # 0x81: elements 0 and 7 negative
+    assert ks1 == 0x81
+    first = [db * g2[8 + j] * (-1 if (ks1 >> j) & 1 else 1) for j in range(8)]
+    assert v[:8] == first and v[8:16] == [db * g2[16 + j] for j in range(8)]
+    assert v[32:40] == [0.5 * 0.25 * 8.0] * 8  # group 1: entry 0 (all 8), scale nibble 0
+    # IQ3_XXS, d = 2: group 0 entries (5, 6), sign index 0, scale nibble 3 -> db = 2*(3.5)*0.5
+    g3 = tables.table("iq3xxs_grid")
+    block = struct.pack("<e", 2.0) + bytes([5, 6]) + bytes(62) + struct.pack("<I", 3 << 28) + bytes(28)
+    v = dq(oracle_mod, T.IQ3_XXS, block, 256)
+    assert v[:8] == [3.5 * g3[20 + j] for j in range(4)] + [3.5 * g3[24 + j] for j in range(4)]
+
+
+# ---- codebooks -------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["iq2xxs_grid", "iq2xs_grid", "iq2s_grid", "iq3xxs_grid", "iq3s_grid", "ksigns_iq2xs"])
+def test_codebooks_match_reference_digest(golden, oracle_mod, name):
+    assert hashlib.sha256(tables.table(name)).digest() == golden[f"sha256_{name}"].tobytes()
+    assert oracle_mod.table(name) == tables.table(name)
+
+
+@pytest.mark.skipif(not REFERENCE.exists(), reason="reference checkout not mounted")
+def test_codebooks_match_reference_text():
+    import sys
+
+    sys.path.insert(0, str(ROOT / "vinf_3080ti_amd" / "csrc"))
+    from gen_iq_grids import reference_tables
+
+    for name, data in reference_tables(REFERENCE.parent).items():
+        assert tables.table(name) == data, name
+
+
+# ---- golden vectors from the reference's compiled CPU path ---------------------------------------------
+
+@pytest.mark.parametrize("ty", ALL_TYPES, ids=lambda t: t.name)
+def test_qmv_bit_identical_to_reference_golden(golden, oracle_mod, ty):
+    w, x, y = golden[f"w_{ty.name}"], golden[f"x_{ty.name}"], golden[f"y_{ty.name}"]
+    got = oracle_mod.qmv(int(ty), w, y.shape[1], x.shape[1], x, x.shape[0], threads=2)
+    assert np.array_equal(got.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("ty", QUANT_TYPES, ids=lambda t: t.name)
+def test_dequant_matches_reference_one_hot_probe(golden, oracle_mod, ty):
+    """probe[c][r] is the reference's qmv of one-hot x = e_c: W[r][c] up to ~3 ulp of activation rounding."""
+    w, probe = golden[f"pw_{ty.name}"], golden[f"probe_{ty.name}"].astype(np.float64)
+    rows, cols = probe.shape[1], probe.shape[0]
+    v = oracle_mod.dequant_rows(int(ty), w, rows, cols).astype(np.float64).T
+    _, scales, mins = oracle_mod.decode_codes(int(ty), w, rows, cols)
+    mag = np.abs(v) + np.repeat(np.abs(mins).astype(np.float64), 16, axis=1).T
+    assert np.all(np.abs(probe - v) <= 2.0**-20 * mag + 1e-30)
+    # the probe separates neighbouring codes: the smallest nonzero scale step is far above the tolerance
+    assert np.all(2.0**-20 * mag < np.repeat(np.abs(scales).astype(np.float64), 16, axis=1).T + (scales == 0).repeat(16, 1).T)
+
+
+def test_quantizer_matches_reference_q8_0(golden, oracle_mod):
+    """The reference's quantize_q8_0 (qwen_cpu.c:953-985) applies the same amax/127, lrintf rule."""
+    for n in range(4):
+        x = golden[f"q8x_{n}"]
+        blocks = golden[f"q8_{n}"].reshape(-1, 34)
+        xq, xd, _ = oracle_mod.quantize_x(x, 1, x.size)
+        assert np.array_equal(xq.reshape(-1, 32).view(np.uint8), blocks[:, 2:])
+        assert np.array_equal(xd.reshape(-1).astype("<f2").view(np.uint8).reshape(-1, 2), blocks[:, :2])
+
+
+@pytest.mark.skipif(not glob.glob(str(ROOT / "oracle" / "_ref" / "_cpu_qwen*.so")), reason="oracle/_ref not built")
+@pytest.mark.parametrize("ty", ALL_TYPES, ids=lambda t: t.name)
+def test_qmv_bit_identical_to_reference_live(oracle_mod, ty):
+    spec = importlib.util.spec_from_file_location("_cpu_qwen", glob.glob(str(ROOT / "oracle" / "_ref" / "_cpu_qwen*.so"))[0])
+    ref = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(ref)
+    rt = ref.CpuRuntime(tables.table("iq3s_grid"), 2)
+    rng = np.random.default_rng(int(ty) + 7)
+    for rows, cols, ntok in [(9, 1024, 8), (3, 256, 13), (5, 2048, 1)]:
+        w = synth.baseline_rows(ty, rows, cols, rng)
+        x = rng.standard_normal((ntok, cols)).astype(np.float32)
+        rt.add_tensor(f"w{rows}", w.tobytes(), int(ty), cols, rows)
+        rt.alloc("x", cols * ntok)
+        rt.alloc("y", rows * ntok)
+        rt.write("x", x.tobytes())
+        rt.qmv(f"w{rows}", "x", "y", ntok)
+        yr = np.frombuffer(rt.read("y"), np.float32).reshape(ntok, rows)
+        assert np.array_equal(yr.view(np.uint32), oracle_mod.qmv(int(ty), w, rows, cols, x, ntok).view(np.uint32))
+
+
+# ---- exact integer structure ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("ty", QUANT_TYPES, ids=lambda t: t.name)
+def test_codes_scales_reproduce_dequant_and_partials(oracle_mod, ty):
+    rows, cols, ntok = 6, 512, 3
+    rng = np.random.default_rng(100 + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    codes, scales, mins = oracle_mod.decode_codes(int(ty), w, rows, cols)
+    deq = oracle_mod.dequant_rows(int(ty), w, rows, cols)
+    s = np.repeat(scales.astype(np.float64), 16, axis=1)
+    m = np.repeat(mins.astype(np.float64), 16, axis=1)
+    assert np.array_equal((s * codes - m).astype(np.float32), deq)  # exact product, one rounding
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    xq, _, _ = oracle_mod.quantize_x(x, ntok, cols)
+    part = oracle_mod.int_partials(int(ty), w, rows, cols, xq, ntok)
+    brute = np.einsum("rgk,tgk->trg", codes.reshape(rows, -1, 16).astype(np.int64), xq.reshape(ntok, -1, 16).astype(np.int64))
+    assert np.array_equal(part.reshape(ntok, rows, -1), brute)
+
+
+def test_quantizer_closed_form(oracle_mod):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((2, 256)).astype(np.float32) * 3
+    x[1, 32:64] = 0.0
+    xq, xd, xs = oracle_mod.quantize_x(x, 2, 256)
+    g = x.reshape(2, 8, 32)
+    amax = np.abs(g).max(-1)
+    assert np.array_equal(xd, (amax / np.float32(127)).astype(np.float32))
+    assert np.all(np.abs(xq.astype(int)) <= 127)
+    assert np.all(np.abs(xq.reshape(2, 8, 32)).max(-1)[amax > 0] == 127)
+    assert np.all(xq[1, 32:64] == 0) and xd[1, 1] == 0 and xs[1, 1] == 0
+    err = np.abs(xq.reshape(2, 8, 32) * xd[..., None].astype(np.float64) - g)
+    assert np.all(err <= 0.5 * xd[..., None] * (1 + 1e-6) + 1e-12)
+    assert np.array_equal(xs, (xd * xq.reshape(2, 8, 32).astype(np.int64).sum(-1).astype(np.float32)).astype(np.float32))
+
+
+def test_argmax_semantics(oracle_mod):
+    x = np.array([[1, 5, 5, 2], [np.nan, 3, np.nan, 3], [-np.inf] * 4], np.float32)
+    assert oracle_mod.argmax_rows(x, 4, 3) == [1, 1, 2**31 - 1]

@@ -1,0 +1,69 @@
+"""ctypes binding of libvq_hip.so (the C ABI declared in include/vq.h).
+
+Loading fails loudly: there is no CPU fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+from .build import LIB
+
+P, I, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+
+# name -> (restype, argtypes); every symbol include/vq.h declares.
+SIGNATURES: dict[str, tuple[object, list]] = {
+    "vq_type_traits": (I, [I, ctypes.POINTER(I), ctypes.POINTER(I)]),
+    "vq_row_bytes": (ctypes.c_longlong, [I, I]),
+    "vq_status_string": (ctypes.c_char_p, [I]),
+    "vq_init": (I, []),
+    "vq_set_iq3s_grid": (I, [P]),
+    "vq_qmv_workspace_bytes": (SZ, [I, I]),
+    "vq_quantize_x": (I, [P, I, I, P, P, P, P]),
+    "vq_qmv": (I, [I, P, I, I, P, I, P, P, SZ, P]),
+    "vq_qmv_q": (I, [I, P, I, I, P, P, P, I, P, P]),
+    "vq_int_partials": (I, [I, P, I, I, P, I, P, P]),
+    "vq_dequant_rows": (I, [I, P, I, I, P, P]),
+    "vq_argmax_rows": (I, [P, I, I, P, P]),
+}
+
+VQ_OK, VQ_ERR_TYPE, VQ_ERR_SHAPE, VQ_ERR_WORKSPACE, VQ_ERR_ARG, VQ_ERR_NOT_INIT = 0, -1, -2, -3, -4, -5
+
+_lib: ctypes.CDLL | None = None
+
+
+class LibraryUnavailableError(RuntimeError):
+    """libvq_hip.so is not built or cannot be loaded."""
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path or LIB)
+    if not p.exists():
+        raise LibraryUnavailableError(f"{p} is not built; run `python -m vinf_3080ti_amd.build`")
+    try:
+        lib = ctypes.CDLL(str(p))
+    except OSError as exc:
+        raise LibraryUnavailableError(f"cannot load {p}: {exc}") from exc
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def status_text(status: int) -> str:
+    return load().vq_status_string(status).decode()
+
+
+def check(status: int, context: str) -> None:
+    """Raise the reference's exception types for a non-zero status (qwen_runtime.cu:1100-1103)."""
+    if status == VQ_OK:
+        return
+    if status in (VQ_ERR_TYPE, VQ_ERR_SHAPE, VQ_ERR_ARG):
+        raise ValueError(f"{context}: {status_text(status)}")
+    raise RuntimeError(f"{context} failed: {status_text(status)}")

@@ -1,0 +1,340 @@
+"""Name-keyed device runtime of the quantized-matvec path (drop-in for vinf's CUDA runtime on this path).
+
+`Runtime` mirrors the method surface of the reference's `_cuda_qwen_runtime.Runtime` that the qwen35
+forward pass uses around its matvecs (/root/reference/engine/csrc/megakernel/qwen_runtime.cu:2602-2677):
+upload/free/has/tensor_info/device_bytes/mem_info, alloc/zero/write/read/copy/buffer_ptr/buffer_elem,
+qmv/matvec, argmax/argmax_rows, set_gemm_min_rows, synchronize. `HipWeightRuntime` mirrors the Python
+wrapper `CudaWeightRuntime` (src/vinf/cuda/qwen_runtime.py:47-116), so
+`QwenGpuExecutor(..., runtime=HipWeightRuntime())` reaches these kernels for every qmv.
+
+Device memory is held in torch tensors (plumbing only); every computation is a call into libvq_hip.so
+on torch's current HIP stream. Errors follow the reference: KeyError for unknown names, ValueError for
+bad shapes/sizes/types, TypeError for an fp16 buffer where fp32 is needed, RuntimeError("<ctx> failed:
+<device error>") for device errors.
+"""
+from __future__ import annotations
+
+import struct
+from array import array
+from dataclasses import dataclass
+from typing import Sequence
+
+import torch
+
+from . import _lib
+from .gguf_types import HIP_MATVEC_TYPES, GGUFTensorType, traits
+
+MAX_TOKENS = 8  # tokens per matvec launch (kMaxTokens, qwen_runtime.cu:572)
+MAX_ARGMAX_ROWS = 256  # kMaxArgmaxRows (qwen_runtime.cu:573)
+_PAD = 256  # every weight allocation carries >= 16 readable bytes past its end (qwen_runtime.cu:1366-1367)
+
+
+@dataclass
+class _Tensor:
+    data: torch.Tensor  # uint8, nbytes + padding
+    type: int
+    rows: int
+    cols: int
+    row_bytes: int
+    nbytes: int
+
+
+@dataclass
+class _Buffer:
+    data: torch.Tensor  # float32 or float16
+    elem: int
+
+
+def _check_upload_args(name: str, nbytes_given: int, type_id: int, cols: int, rows: int) -> tuple[int, int]:
+    """Validation of Runtime_upload (qwen_runtime.cu:1338-1357). Returns (row_bytes, nbytes)."""
+    try:
+        bs, ts = traits(type_id)
+    except ValueError:
+        raise ValueError(f"unsupported GGUF tensor type id {type_id} for HIP matvec") from None
+    if cols <= 0 or rows <= 0 or cols % bs != 0:
+        raise ValueError(f"{name}: cols={cols} must be a positive multiple of the block size")
+    row_bytes = cols // bs * ts
+    nbytes = row_bytes * rows
+    if nbytes_given != nbytes:
+        raise ValueError(f"{name}: got {nbytes_given} bytes, expected {nbytes}")
+    return row_bytes, nbytes
+
+
+def _check_qmv_args(name: str, cols: int, ntok: int) -> None:
+    """Validation of Runtime_qmv (qwen_runtime.cu:1865-1868)."""
+    if ntok < 1:
+        raise ValueError("ntok must be positive")
+    if cols % 32 != 0:
+        raise ValueError(f"{name}: matvec cols must be a multiple of 32")
+
+
+class Runtime:
+    """Persistent device store of raw GGUF tensors and fp32 buffers, keyed by name."""
+
+    def __init__(self, iq3s_grid: bytes | None = None, device: int | None = None) -> None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("Runtime needs a ROCm GPU: torch.cuda.is_available() is False")
+        self._lib = _lib.load()
+        self.device = torch.device("cuda", torch.cuda.current_device() if device is None else device)
+        with torch.cuda.device(self.device):
+            _lib.check(self._lib.vq_init(), "vq_init")
+            if iq3s_grid is not None:
+                grid = bytes(iq3s_grid)
+                if len(grid) != 512 * 4:
+                    raise ValueError("iq3s_grid must be 2048 bytes (512 entries x 4 values)")
+                _lib.check(self._lib.vq_set_iq3s_grid(grid), "vq_set_iq3s_grid")
+        self.tensors: dict[str, _Tensor] = {}
+        self.buffers: dict[str, _Buffer] = {}
+        self._ws = torch.empty(0, dtype=torch.uint8, device=self.device)
+        self._argmax_out = torch.empty(MAX_ARGMAX_ROWS, dtype=torch.int32, device=self.device)
+        self.gemm_min_rows = 0
+
+    # ---- helpers ----------------------------------------------------------------------------------
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _tensor(self, name: str) -> _Tensor:
+        t = self.tensors.get(name)
+        if t is None:
+            raise KeyError(f"weight tensor {name} is not loaded")
+        return t
+
+    def _any_buffer(self, name: str) -> _Buffer:
+        b = self.buffers.get(name)
+        if b is None:
+            raise KeyError(f"device buffer {name} is not allocated")
+        return b
+
+    def _f32_buffer(self, name: str, min_n: int) -> torch.Tensor:
+        """find_buffer (qwen_runtime.cu:1206-1223)."""
+        b = self._any_buffer(name)
+        if b.elem != 4:
+            raise TypeError(f"device buffer {name} is fp16 (KV cache), not fp32")
+        if b.data.numel() < min_n:
+            raise ValueError(f"device buffer {name} has {b.data.numel()} floats, need {min_n}")
+        return b.data
+
+    def _workspace(self, nbytes: int) -> torch.Tensor:
+        if self._ws.numel() < nbytes:
+            self._ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    # ---- weights ----------------------------------------------------------------------------------
+    def upload(self, name: str, data, type_id: int, cols: int, rows: int, resident: bool = True, group: int = -1) -> None:
+        """Copy raw GGUF blocks to the device (Runtime_upload, qwen_runtime.cu:1338-1409).
+
+        Every tensor is resident in HBM: `resident=False` (pinned-host streaming on the 12 GB card) is
+        accepted and ignored. Weight groups (CUDA VMM regions) do not exist here: group >= 0 is rejected.
+        """
+        view = memoryview(data).cast("B")
+        row_bytes, nbytes = _check_upload_args(name, view.nbytes, int(type_id), int(cols), int(rows))
+        if group >= 0:
+            raise ValueError(f"unknown weight group {group}")
+        self.tensors.pop(name, None)
+        host = torch.frombuffer(bytearray(view), dtype=torch.uint8)
+        padded = (nbytes + 16 + _PAD - 1) // _PAD * _PAD
+        dev = torch.zeros(padded, dtype=torch.uint8, device=self.device)
+        dev[:nbytes].copy_(host)
+        self.tensors[name] = _Tensor(dev, int(type_id), int(rows), int(cols), row_bytes, nbytes)
+
+    def upload_device(self, name: str, data: torch.Tensor, type_id: int, cols: int, rows: int) -> None:
+        """Register device-resident raw blocks (uint8 tensor of >= nbytes + 16 bytes) without a host copy."""
+        if data.device != self.device or data.dtype != torch.uint8 or not data.is_contiguous():
+            raise ValueError(f"{name}: expected a contiguous uint8 tensor on {self.device}")
+        try:
+            bs, ts = traits(type_id)
+        except ValueError:
+            raise ValueError(f"unsupported GGUF tensor type id {type_id} for HIP matvec") from None
+        if cols <= 0 or rows <= 0 or cols % bs != 0:
+            raise ValueError(f"{name}: cols={cols} must be a positive multiple of the block size")
+        row_bytes = cols // bs * ts
+        nbytes = row_bytes * rows
+        if data.numel() < nbytes + 16:
+            raise ValueError(f"{name}: device tensor needs {nbytes + 16} bytes (16 bytes of tail padding)")
+        self.tensors[name] = _Tensor(data, int(type_id), int(rows), int(cols), row_bytes, nbytes)
+
+    def free(self, name: str) -> None:
+        if name not in self.tensors:
+            raise KeyError(name)
+        del self.tensors[name]
+
+    def has(self, name: str) -> bool:
+        return name in self.tensors
+
+    def device_bytes(self) -> int:
+        return sum(t.nbytes for t in self.tensors.values())
+
+    def tensor_info(self, name: str) -> tuple[int, int, int, int, int, int, bool]:
+        """(device_address, gguf_type, rows, cols, row_bytes, nbytes, resident) (qwen_runtime.cu:1460-1473)."""
+        t = self._tensor(name)
+        return (t.data.data_ptr(), t.type, t.rows, t.cols, t.row_bytes, t.nbytes, True)
+
+    def mem_info(self) -> tuple[int, int]:
+        return torch.cuda.mem_get_info(self.device)
+
+    # ---- buffers ----------------------------------------------------------------------------------
+    def alloc(self, name: str, n: int, elem: int = 4, virtual: bool = False) -> None:
+        """Zeroed device buffer of n elements (Runtime_alloc, qwen_runtime.cu:1616-1650)."""
+        if n <= 0:
+            raise ValueError(f"buffer {name} size must be positive")
+        if elem not in (4, 2):
+            raise ValueError("element size must be 4 (fp32) or 2 (fp16)")
+        dtype = torch.float32 if elem == 4 else torch.float16
+        self.buffers[name] = _Buffer(torch.zeros(int(n), dtype=dtype, device=self.device), elem)
+
+    def zero(self, name: str) -> None:
+        self._any_buffer(name).data.zero_()
+
+    def write(self, name: str, data, offset: int = 0) -> None:
+        b = self._any_buffer(name)
+        view = memoryview(data).cast("B")
+        if offset < 0 or view.nbytes % b.elem or offset + view.nbytes // b.elem > b.data.numel():
+            raise ValueError(f"write to {name}: bad offset/size for {b.elem}-byte elements")
+        host = torch.frombuffer(bytearray(view), dtype=b.data.dtype)
+        b.data[offset : offset + host.numel()].copy_(host)
+
+    def read(self, name: str, n: int = -1, offset: int = 0) -> bytes:
+        b = self._any_buffer(name)
+        avail = b.data.numel()
+        if offset < 0 or offset > avail:
+            raise ValueError("bad read offset")
+        count = avail - offset if n < 0 else n
+        if offset + count > avail:
+            raise ValueError(f"read of {count} elements exceeds buffer {name}")
+        return b.data[offset : offset + count].cpu().numpy().tobytes()
+
+    def copy(self, dst: str, dst_offset: int, src: str, src_offset: int, n: int) -> None:
+        d = self._f32_buffer(dst, dst_offset + n)
+        s = self._f32_buffer(src, src_offset + n)
+        d[dst_offset : dst_offset + n].copy_(s[src_offset : src_offset + n].clone())
+
+    def buffer_ptr(self, name: str) -> tuple[int, int]:
+        b = self._f32_buffer(name, 0)
+        return (b.data_ptr(), b.numel())
+
+    def buffer_elem(self, name: str) -> int:
+        return self._any_buffer(name).elem
+
+    def buffer_tensor(self, name: str) -> torch.Tensor:
+        """The torch tensor behind a buffer (for zero-copy interop)."""
+        return self._any_buffer(name).data
+
+    # ---- the hot path -------------------------------------------------------------------------------
+    def qmv(self, weight: str, x: str, y: str, ntok: int = 1) -> None:
+        """y[t] = W x[t] for t < ntok, asynchronous on the current stream (Runtime_qmv, qwen_runtime.cu:1860-1912)."""
+        if ntok < 1:
+            raise ValueError("ntok must be positive")
+        t = self._tensor(weight)
+        _check_qmv_args(weight, t.cols, ntok)
+        xb = self._f32_buffer(x, t.cols * ntok)
+        yb = self._f32_buffer(y, t.rows * ntok)
+        self._qmv_ptrs(t, xb.data_ptr(), yb.data_ptr(), ntok)
+
+    def _qmv_ptrs(self, t: _Tensor, x_ptr: int, y_ptr: int, ntok: int) -> None:
+        ws_bytes = self._lib.vq_qmv_workspace_bytes(t.cols, ntok)
+        ws = self._workspace(ws_bytes)
+        st = self._lib.vq_qmv(t.type, t.data.data_ptr(), t.rows, t.cols, x_ptr, ntok, y_ptr, ws.data_ptr(),
+                              ws.numel(), self._stream())
+        _lib.check(st, "qmv launch")
+
+    def qmv_tensor(self, weight: str, x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
+        """Tensor form: x [ntok, cols] fp32 on the device -> y [ntok, rows] fp32."""
+        t = self._tensor(weight)
+        if x.dim() == 1:
+            x = x.unsqueeze(0)
+        ntok = x.shape[0]
+        _check_qmv_args(weight, t.cols, ntok)
+        if x.shape[1] != t.cols or x.dtype != torch.float32 or x.device != self.device:
+            raise ValueError(f"{weight}: x must be float32 [ntok, {t.cols}] on {self.device}")
+        x = x.contiguous()
+        if y is None:
+            y = torch.empty(ntok, t.rows, dtype=torch.float32, device=self.device)
+        self._qmv_ptrs(t, x.data_ptr(), y.data_ptr(), ntok)
+        return y
+
+    def matvec(self, name: str, x: bytes) -> bytes:
+        """Synchronous debug matvec: fp32 bytes in, fp32 bytes out (Runtime_matvec, qwen_runtime.cu:2280-2315)."""
+        t = self.tensors.get(name)
+        if t is None:
+            raise KeyError(f"{name} is not resident on the GPU")
+        view = memoryview(x).cast("B")
+        if view.nbytes != t.cols * 4:
+            raise ValueError(f"{name}: x has {view.nbytes} bytes, expected {t.cols} float32")
+        xd = torch.frombuffer(bytearray(view), dtype=torch.float32).to(self.device)
+        y = self.qmv_tensor(name, xd)
+        torch.cuda.synchronize(self.device)
+        return y.cpu().numpy().tobytes()
+
+    def argmax(self, name: str, n: int) -> int:
+        """Index of the largest of the first n floats; ties -> lowest index (Runtime_argmax, :2167-2179)."""
+        xb = self._f32_buffer(name, n)
+        _lib.check(self._lib.vq_argmax_rows(xb.data_ptr(), n, 1, self._argmax_out.data_ptr(), self._stream()), "argmax")
+        return int(self._argmax_out[0].item())
+
+    def argmax_rows(self, name: str, n: int, ntok: int) -> list[int]:
+        """Row-wise argmax of ntok rows of n floats (Runtime_argmax_rows, :2181-2197)."""
+        if ntok < 1 or ntok > MAX_ARGMAX_ROWS:
+            raise ValueError(f"ntok must be in [1, {MAX_ARGMAX_ROWS}]")
+        xb = self._f32_buffer(name, n * ntok)
+        _lib.check(self._lib.vq_argmax_rows(xb.data_ptr(), n, ntok, self._argmax_out.data_ptr(), self._stream()),
+                   "argmax_rows")
+        return [int(v) for v in self._argmax_out[:ntok].tolist()]
+
+    def set_gemm_min_rows(self, n: int) -> None:
+        """Prompt passes with ntok >= n take the prefill GEMM (0 = never) (qwen_runtime.cu:2324-2330)."""
+        if n < 0:
+            raise ValueError("gemm_min_rows must be >= 0")
+        self.gemm_min_rows = int(n)
+
+    def synchronize(self) -> None:
+        torch.cuda.synchronize(self.device)
+
+
+def iq3s_grid_bytes() -> bytes:
+    """The 2048-byte IQ3_S codebook the reference passes to Runtime() (cuda/qwen_runtime.py:41-44)."""
+    from .tables import table
+
+    return table("iq3s_grid")
+
+
+class HipWeightRuntime:
+    """Drop-in for CudaWeightRuntime (src/vinf/cuda/qwen_runtime.py:47-116) on the matvec path."""
+
+    def __init__(self, device: int | None = None) -> None:
+        self._rt = Runtime(iq3s_grid_bytes(), device)
+
+    def mem_info(self) -> tuple[int, int]:
+        return self._rt.mem_info()
+
+    def device_bytes(self) -> int:
+        return self._rt.device_bytes()
+
+    def has(self, name: str) -> bool:
+        return self._rt.has(name)
+
+    def free(self, name: str) -> None:
+        self._rt.free(name)
+
+    def upload_raw(self, name: str, data, tensor_type: GGUFTensorType, cols: int, rows: int, *, resident: bool = True) -> None:
+        if int(tensor_type) not in HIP_MATVEC_TYPES:
+            raise ValueError(f"{name}: no HIP matvec for type {int(tensor_type)}")
+        self._rt.upload(name, data, int(tensor_type), cols, rows, resident)
+
+    def matvec(self, name: str, values: Sequence[float]) -> list[float]:
+        out = array("f")
+        out.frombytes(self._rt.matvec(name, array("f", values).tobytes()))
+        return out.tolist()
+
+    def read_floats(self, name: str, n: int = -1, offset: int = 0) -> list[float]:
+        data = self._rt.read(name, n, offset)
+        if self._rt.buffer_elem(name) == 2:
+            return list(struct.unpack(f"<{len(data) // 2}e", data))
+        out = array("f")
+        out.frombytes(data)
+        return out.tolist()
+
+    def write_floats(self, name: str, values, offset: int = 0) -> None:
+        self._rt.write(name, array("f", values).tobytes(), offset)
+
+    def __getattr__(self, name: str):
+        return getattr(self._rt, name)
