@@ -92,13 +92,15 @@ class Hip:
     def s(self):
         return self.torch.cuda.current_stream().cuda_stream
 
-    def quantize(self, x, ntok, cols, xq, xd, xs):
-        st = self.lib.vq_quantize_x(x.data_ptr(), ntok, cols, xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), self.s())
+    def xpack(self, cols, ntok):
+        return self.torch.empty(self.lib.vq_xpack_bytes(cols, ntok), dtype=self.torch.uint8, device="cuda")
+
+    def pack(self, x, ntok, cols, xp):
+        st = self.lib.vq_pack_x(x.data_ptr(), ntok, cols, xp.data_ptr(), self.s())
         assert st == 0, st
 
-    def qmv_q(self, ty, w, rows, cols, xq, xd, xs, ntok, y):
-        st = self.lib.vq_qmv_q(ty, w.data_ptr(), rows, cols, xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), ntok,
-                               y.data_ptr(), self.s())
+    def qmv_packed(self, ty, w, rows, cols, xp, ntok, y):
+        st = self.lib.vq_qmv_packed(ty, w.data_ptr(), rows, cols, xp.data_ptr(), ntok, y.data_ptr(), self.s())
         assert st == 0, st
 
     def argmax(self, y, n, ntok, out):
@@ -132,15 +134,12 @@ def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=
     copies = max(2, -(-min_rotation_bytes // nbytes))
     ws = make_weights(torch, ty, rows, cols, 1234 + ty, copies)
     x = torch.randn(ntok, cols, device="cuda")
-    ng = cols // 32
-    xq = torch.empty(ntok, cols, dtype=torch.int8, device="cuda")
-    xd = torch.empty(ntok, ng, device="cuda")
-    xs = torch.empty(ntok, ng, device="cuda")
+    xp = hip.xpack(cols, ntok)
     y = torch.empty(ntok, rows, device="cuda")
-    hip.quantize(x, ntok, cols, xq, xd, xs)
+    hip.pack(x, ntok, cols, xp)
     for i in range(copies):  # warm-up
-        hip.qmv_q(ty, ws[i], rows, cols, xq, xd, xs, ntok, y)
-    ms = time_kernel_loop(torch, lambda i: hip.qmv_q(ty, ws[i % copies], rows, cols, xq, xd, xs, ntok, y), iters)
+        hip.qmv_packed(ty, ws[i], rows, cols, xp, ntok, y)
+    ms = time_kernel_loop(torch, lambda i: hip.qmv_packed(ty, ws[i % copies], rows, cols, xp, ntok, y), iters)
     b = alg_bytes(ty, rows, cols, ntok)
     del ws
     torch.cuda.empty_cache()
@@ -160,9 +159,7 @@ class Sweep:
         maxc = max(p[3] for p in self.plan)
         maxr = max(p[2] for p in self.plan)
         self.x = torch.randn(ntok, maxc, device="cuda")
-        self.xq = torch.empty(ntok * maxc, dtype=torch.int8, device="cuda")
-        self.xd = torch.empty(ntok * maxc // 32, device="cuda")
-        self.xs = torch.empty(ntok * maxc // 32, device="cuda")
+        self.xp = hip.xpack(maxc, ntok)
         self.y = torch.empty(ntok * maxr, device="cuda")
         self.ids = torch.empty(ntok, dtype=torch.int32, device="cuda")
 
@@ -173,9 +170,9 @@ class Sweep:
         prev = None
         for (name, ty, rows, cols, key), w in zip(self.plan, self.w):
             if key != prev:
-                hip.quantize(self.x, ntok, cols, self.xq, self.xd, self.xs)
+                hip.pack(self.x, ntok, cols, self.xp)
                 prev = key
-            hip.qmv_q(ty, w, rows, cols, self.xq, self.xd, self.xs, ntok, self.y)
+            hip.qmv_packed(ty, w, rows, cols, self.xp, ntok, self.y)
             if name == "output":
                 hip.argmax(self.y, rows, ntok, self.ids)
 

@@ -13,6 +13,10 @@
  *   x    fp32 activations [ntok][cols]
  *   y    fp32 outputs     [ntok][rows]
  *   xq   int8 [ntok][cols], xd/xs fp32 [ntok][cols/32]: per 32-group scale d and d*sum(q)
+ *   xpack  packed quantized activations, one record per token, vq_xpack_bytes(cols,1) bytes apart
+ *        (16-byte multiple): xq[cols] int8 | xd[cols/32] fp32 | xh[cols/32] u32, where xh holds the
+ *        sums of q over elements 0..15 (low 16 bits, signed) and 16..31 (high 16 bits, signed) of each
+ *        group. The matvec copies a record verbatim into LDS.
  */
 #ifndef VQ_H_
 #define VQ_H_
@@ -66,12 +70,19 @@ int vq_init(void);
  * Replaces: the iq3s_grid argument of Runtime(iq3s_grid) (qwen_runtime.cu:1272-1286, cuda/qwen_runtime.py:41-44). */
 int vq_set_iq3s_grid(const uint8_t *grid);
 
-/* Workspace bytes vq_qmv needs for the int8 activations of `ntok` tokens of `cols` columns. */
+/* Bytes of the packed activations (xpack) of `ntok` tokens of `cols` columns; 0 if cols % 32 != 0. */
+size_t vq_xpack_bytes(int cols, int ntok);
+
+/* Workspace bytes vq_qmv needs (the packed activations of `ntok` tokens). */
 size_t vq_qmv_workspace_bytes(int cols, int ntok);
 
-/* Quantize activations to int8 per 32-group: d = amax/127, q = rint(x/d), xs = d*sum(q).
- * Replaces: the activation quantizer of Cpu_qmv (qwen_cpu.c:607-627). */
+/* Quantize activations to int8 per 32-group: d = amax/127, id = 1/d, q = rint(x*id), xs = d*sum(q).
+ * xs may be NULL. Replaces: the activation quantizer of Cpu_qmv (qwen_cpu.c:607-627). */
 int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, float *xs, void *stream);
+
+/* The same quantizer writing the packed layout `xpack` (vq_xpack_bytes(cols, ntok) bytes) that
+ * vq_qmv_packed and vq_int_partials read. Replaces: the same quantizer (qwen_cpu.c:607-627). */
+int vq_pack_x(const float *x, int ntok, int cols, void *xpack, void *stream);
 
 /* y[t][r] = W[r] . x[t] for t < ntok (any ntok >= 1; weights are read once per 8 tokens).
  * Quantized types quantize x into `workspace` first (vq_qmv_workspace_bytes); F32/F16 weights use x
@@ -80,15 +91,16 @@ int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, flo
 int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, float *y, void *workspace,
            size_t workspace_bytes, void *stream);
 
-/* Same as vq_qmv with activations already quantized by vq_quantize_x (quantized types only), so several
+/* Same as vq_qmv with activations already packed by vq_pack_x (quantized types only), so several
  * matrices that share one input (gate/up, q/k/v) quantize it once. Replaces: dot_row_q's caller loop
  * (qwen_cpu.c:628-637). */
-int vq_qmv_q(int type, const uint8_t *w, int rows, int cols, const int8_t *xq, const float *xd, const float *xs,
-             int ntok, float *y, void *stream);
+int vq_qmv_packed(int type, const uint8_t *w, int rows, int cols, const void *xpack, int ntok, float *y,
+                  void *stream);
 
 /* Test hook: part[((t*rows + r)*(cols/32) + g)*2 + h] = exact int32 sum over the 16 elements of half h
- * of group g of (weight code * xq). Replaces: the integer stage of dot_row_q (qwen_cpu.c:125-342). */
-int vq_int_partials(int type, const uint8_t *w, int rows, int cols, const int8_t *xq, int ntok, int32_t *part,
+ * of group g of (weight code * xq), computed by the matvec's own decoders from packed activations.
+ * Replaces: the integer stage of dot_row_q (qwen_cpu.c:125-342). */
+int vq_int_partials(int type, const uint8_t *w, int rows, int cols, const void *xpack, int ntok, int32_t *part,
                     void *stream);
 
 /* Test hook: out[r*cols + c] = fp32 value of W[r][c]. Replaces: deq8 (qwen_quant.cuh:151-279) and

@@ -55,11 +55,18 @@ def test_host_side_argument_checks(lib):
     assert lib.vq_qmv(int(T.Q4_K), fake, 4, 256, fake, 0, fake, fake, 1 << 20, None) == _lib.VQ_ERR_SHAPE
     assert lib.vq_qmv(int(T.Q4_K), None, 4, 256, fake, 1, fake, fake, 1 << 20, None) == _lib.VQ_ERR_ARG
     assert lib.vq_qmv(int(T.Q4_K), fake, 4, 256, fake, 1, fake, fake, 16, None) == _lib.VQ_ERR_WORKSPACE
-    assert lib.vq_qmv_q(int(T.F32), fake, 4, 256, fake, fake, fake, 1, fake, None) == _lib.VQ_ERR_TYPE
-    assert lib.vq_quantize_x(fake, 1, 48, fake, fake, fake, None) == _lib.VQ_ERR_SHAPE
+    assert lib.vq_qmv_packed(int(T.F32), fake, 4, 256, fake, 1, fake, None) == _lib.VQ_ERR_TYPE
+    assert lib.vq_qmv_packed(int(T.Q4_K), fake, 4, 256, None, 1, fake, None) == _lib.VQ_ERR_ARG
+    assert lib.vq_quantize_x(fake, 1, 48, fake, fake, None, None) == _lib.VQ_ERR_SHAPE
+    assert lib.vq_pack_x(fake, 1, 48, fake, None) == _lib.VQ_ERR_SHAPE
+    assert lib.vq_int_partials(int(T.F16), fake, 4, 256, fake, 1, fake, None) == _lib.VQ_ERR_TYPE
     assert lib.vq_argmax_rows(fake, 0, 1, fake, None) == _lib.VQ_ERR_SHAPE
     assert lib.vq_set_iq3s_grid(None) == _lib.VQ_ERR_ARG
-    assert lib.vq_qmv_workspace_bytes(5120, 8) >= 5120 * 8 + 2 * 4 * 160 * 8
+    # packed record: cols int8 codes + cols/32 fp32 scales + cols/32 u32 half sums, 16-byte aligned per token
+    assert lib.vq_xpack_bytes(5120, 1) == 5120 + 160 * 8
+    assert lib.vq_xpack_bytes(96, 1) == 128 and lib.vq_xpack_bytes(96, 3) == 384
+    assert lib.vq_xpack_bytes(48, 1) == 0
+    assert lib.vq_qmv_workspace_bytes(5120, 8) >= lib.vq_xpack_bytes(5120, 8)
     assert b"workspace" in lib.vq_status_string(_lib.VQ_ERR_WORKSPACE)
 
 

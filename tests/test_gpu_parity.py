@@ -46,6 +46,18 @@ def P(t) -> int:
     return t.data_ptr()
 
 
+def pack_ref(q: np.ndarray, d: np.ndarray, stride: int) -> np.ndarray:
+    """Expected packed activation records: q int8 | d fp32 | (sum q[0:16], sum q[16:32]) as int16 pairs, zero pad."""
+    ntok, cols = q.shape
+    ng = cols // 32
+    out = np.zeros((ntok, stride), np.uint8)
+    out[:, :cols] = q.view(np.uint8)
+    out[:, cols : cols + 4 * ng] = np.ascontiguousarray(d, dtype=np.float32).view(np.uint8)
+    h = q.reshape(ntok, ng, 2, 16).astype(np.int64).sum(-1).astype(np.int16)  # [t][g][half]: low, high
+    out[:, cols + 4 * ng : cols + 8 * ng] = np.ascontiguousarray(h).view(np.uint8).reshape(ntok, 4 * ng)
+    return out.reshape(-1)
+
+
 def gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok):
     wd, xd = wdev(torch, w), dev(torch, x.astype(np.float32).reshape(ntok, cols))
     y = torch.empty(ntok, rows, dtype=torch.float32, device="cuda")
@@ -70,11 +82,15 @@ def test_quantize_x_bit_exact(env, oracle_mod, ntok, cols):
     d = torch.empty(ntok, ng, dtype=torch.float32, device="cuda")
     s = torch.empty(ntok, ng, dtype=torch.float32, device="cuda")
     assert lib.vq_quantize_x(P(xd_), ntok, cols, P(xq), P(d), P(s), None) == 0
+    stride = lib.vq_xpack_bytes(cols, 1)
+    xp = torch.full((lib.vq_xpack_bytes(cols, ntok),), 0xAB, dtype=torch.uint8, device="cuda")
+    assert lib.vq_pack_x(P(xd_), ntok, cols, P(xp), None) == 0
     torch.cuda.synchronize()
     q_ref, d_ref, s_ref = oracle_mod.quantize_x(x, ntok, cols)
     assert np.array_equal(xq.cpu().numpy(), q_ref)
     assert np.array_equal(d.cpu().numpy().view(np.uint32), d_ref.view(np.uint32))
     assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(xp.cpu().numpy(), pack_ref(q_ref, d_ref, stride))
 
 
 @pytest.mark.parametrize("ty", ALL_TYPES, ids=lambda t: t.name)
@@ -97,10 +113,10 @@ def test_int_partials_bit_exact(env, oracle_mod, ty):
     rng = np.random.default_rng(40 + int(ty))
     w = synth.baseline_rows(ty, rows, cols, rng)
     x = rng.standard_normal((ntok, cols)).astype(np.float32)
-    xq, _, _ = oracle_mod.quantize_x(x, ntok, cols)
+    xq, xd, _ = oracle_mod.quantize_x(x, ntok, cols)
     part = torch.empty(ntok, rows, cols // 32, 2, dtype=torch.int32, device="cuda")
-    wd, xqd = wdev(torch, w), dev(torch, xq)
-    assert lib.vq_int_partials(int(ty), P(wd), rows, cols, P(xqd), ntok, P(part), None) == 0
+    wd, xpd = wdev(torch, w), dev(torch, pack_ref(xq, xd, lib.vq_xpack_bytes(cols, 1)))
+    assert lib.vq_int_partials(int(ty), P(wd), rows, cols, P(xpd), ntok, P(part), None) == 0
     torch.cuda.synchronize()
     assert np.array_equal(part.cpu().numpy(), oracle_mod.int_partials(int(ty), w, rows, cols, xq, ntok))
 

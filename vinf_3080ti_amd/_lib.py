@@ -5,6 +5,7 @@ Loading fails loudly: there is no CPU fallback for any entry point.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 from .build import LIB
@@ -18,10 +19,12 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_status_string": (ctypes.c_char_p, [I]),
     "vq_init": (I, []),
     "vq_set_iq3s_grid": (I, [P]),
+    "vq_xpack_bytes": (SZ, [I, I]),
     "vq_qmv_workspace_bytes": (SZ, [I, I]),
     "vq_quantize_x": (I, [P, I, I, P, P, P, P]),
+    "vq_pack_x": (I, [P, I, I, P, P]),
+    "vq_qmv_packed": (I, [I, P, I, I, P, I, P, P]),
     "vq_qmv": (I, [I, P, I, I, P, I, P, P, SZ, P]),
-    "vq_qmv_q": (I, [I, P, I, I, P, P, P, I, P, P]),
     "vq_int_partials": (I, [I, P, I, I, P, I, P, P]),
     "vq_dequant_rows": (I, [I, P, I, I, P, P]),
     "vq_argmax_rows": (I, [P, I, I, P, P]),
@@ -37,10 +40,11 @@ class LibraryUnavailableError(RuntimeError):
 
 
 def load(path: Path | None = None) -> ctypes.CDLL:
+    """Load the library (VQ_LIB_PATH overrides the in-tree build, e.g. for tuning variants)."""
     global _lib
     if _lib is not None and path is None:
         return _lib
-    p = Path(path or LIB)
+    p = Path(path or os.environ.get("VQ_LIB_PATH") or LIB)
     if not p.exists():
         raise LibraryUnavailableError(f"{p} is not built; run `python -m vinf_3080ti_amd.build`")
     try:

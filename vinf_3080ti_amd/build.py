@@ -1,46 +1,73 @@
-"""Build the HIP library libvq_hip.so in-tree for gfx950 (hipcc, no JIT cache)."""
+"""Build the HIP library libvq_hip.so in-tree for gfx950 (hipcc, no JIT cache).
+
+Each translation unit (the C ABI in vq_api.hip and one unit per quantized GGUF type) is compiled to an
+object in csrc/_build/ in parallel, then linked into vinf_3080ti_amd/libvq_hip.so.
+"""
 from __future__ import annotations
 
+import concurrent.futures as cf
 import os
 import subprocess
+import sys
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
+BUILD = CSRC / "_build"
 LIB = PKG / "libvq_hip.so"
-SOURCES = [CSRC / "vq_kernels.hip"]
-HEADERS = [CSRC / "vq_common.h", CSRC / "vq_decode.h", CSRC / "vq_iq_grids.h", PKG.parent / "include" / "vq.h"]
+INCLUDE = PKG.parent / "include"
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
     "-std=c++20",
     "-fPIC",
-    "-shared",
     # Packed fp32 VALU ops stay off: hand-written code and hipcc's own packing both avoid them.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
 
+def sources() -> list[Path]:
+    return [CSRC / "vq_api.hip"] + sorted(CSRC.glob("vq_t_*.hip"))
+
+
+def headers() -> list[Path]:
+    return sorted(CSRC.glob("*.h")) + [INCLUDE / "vq.h"]
+
+
 def hipcc() -> str:
-    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
-    return str(Path(rocm) / "bin" / "hipcc")
+    return str(Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "bin" / "hipcc")
 
 
-def build(force: bool = True, verbose: bool = False) -> Path:
-    """Compile every source into LIB. force=False skips the compile when LIB is newer than its inputs."""
-    if not force and LIB.exists():
-        newest = max(p.stat().st_mtime for p in SOURCES + HEADERS)
-        if LIB.stat().st_mtime >= newest:
-            return LIB
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, *map(str, SOURCES), "-o", str(tmp)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
-    os.replace(tmp, LIB)
+def _compile(src: Path, force: bool) -> Path:
+    obj = BUILD / (src.stem + ".o")
+    newest = max(p.stat().st_mtime for p in headers() + [src])
+    if force or not obj.exists() or obj.stat().st_mtime < newest:
+        tmp = obj.with_suffix(".o.tmp")
+        res = subprocess.run([hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(tmp)], stdout=subprocess.PIPE,
+                             stderr=subprocess.STDOUT, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}")
+        os.replace(tmp, obj)
+    return obj
+
+
+def build(force: bool = True, jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every translation unit and link LIB. force=False reuses objects newer than their inputs."""
+    BUILD.mkdir(exist_ok=True)
+    srcs = sources()
+    jobs = jobs or min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, force), srcs))
+    if force or not LIB.exists() or LIB.stat().st_mtime < max(o.stat().st_mtime for o in objs):
+        tmp = LIB.with_suffix(".so.tmp")
+        cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        os.replace(tmp, LIB)
     return LIB
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(force="--force" in sys.argv, verbose=True))

@@ -1,0 +1,370 @@
+// vq_api.hip -- MI355X (gfx950, wave64) quantized-weight matvec: the C ABI (include/vq.h) and the
+// type-independent kernels.
+//
+// Kernels here (hand-written for CDNA4):
+//   quantize_x_kernel    fp32 activations -> int8 per 32-group + (xd, xs, 16-element sums) [qwen_cpu.c:607-627]
+//   qmv_float_kernel     y = W x for F32/F16 weights with fp32 activations                [qwen_cpu.c:345-360]
+//   dequant_float_kernel test hook for F32/F16 weights
+//   argmax_rows_kernel   row argmax, ties to the lowest index                            [qwen_runtime.cu:850-876]
+// The quantized kernels (one translation unit per GGUF type) are in vq_qmv_impl.h / vq_t_<type>.hip.
+//
+// Data layout in HBM: weights are the GGUF tensor bytes as uploaded (row-major, row_bytes =
+// cols/block_size*type_size, rows back to back, >= VQ_TAIL_PAD readable bytes after the last row).
+// Activations x[t*cols + c] fp32, outputs y[t*rows + r] fp32 (the reference's token-major layout).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "vq_common.h"
+#include "vq_qmv.h"
+#include "../../include/vq.h"
+
+namespace {
+
+__device__ __forceinline__ float half_to_float(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h & 0xFFFFu)));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// ---- activation quantizer ------------------------------------------------------------------------------
+// One thread per (token, 32-group). Same IEEE operations as the reference CPU quantizer
+// (qwen_cpu.c:607-627): amax = max|v|, d = amax/127 (correctly rounded division), id = 1/d,
+// q = rint(v*id) (round half to even, as lrintf), xs = d*sum(q).
+// Outputs go to (xq, xd, xs, xh) with per-token strides, so one kernel writes either the separate arrays of
+// vq_quantize_x or the packed activation record of vq_pack_x (layout: vq_xpack_h_offset / vq_xpack_stride in vq_common.h).
+struct XOut {
+    int8_t *xq;
+    float *xd, *xs;
+    uint32_t *xh;  // (sum of half 0) | (sum of half 1) << 16
+    long q_stride, d_stride;  // per-token strides in elements (xs and xh use d_stride)
+};
+
+__global__ __launch_bounds__(256) void quantize_x_kernel(const float *__restrict__ x, int ntok, int cols, XOut o) {
+    const int ng = cols >> 5;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= ntok * ng) return;
+    const int t = i / ng, g = i - t * ng;
+    const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols + 32 * g);
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float4 f = src[k];
+        v[4 * k] = f.x;
+        v[4 * k + 1] = f.y;
+        v[4 * k + 2] = f.z;
+        v[4 * k + 3] = f.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(v[k]));
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    int half_sum[2] = {0, 0};
+    uint32_t packed[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        uint32_t p = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int q = static_cast<int>(__builtin_rintf(v[4 * k + b] * id));
+            half_sum[k >> 2] += q;
+            p |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * b);
+        }
+        packed[k] = p;
+    }
+    const int sum = half_sum[0] + half_sum[1];
+    uint4 *dst = reinterpret_cast<uint4 *>(o.xq + t * o.q_stride + 32 * g);
+    dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    o.xd[t * o.d_stride + g] = d;
+    if (o.xs) o.xs[t * o.d_stride + g] = d * static_cast<float>(sum);
+    if (o.xh)
+        o.xh[t * o.d_stride + g] = (static_cast<uint32_t>(half_sum[0]) & 0xFFFFu) | (static_cast<uint32_t>(half_sum[1]) << 16);
+}
+
+// ---- float weights (F32/F16): one wave per row, fp32 activations, no quantization (qwen_cpu.c:345-360) ---
+template <int T, int NT>
+__global__ __launch_bounds__(256) void qmv_float_kernel(const uint8_t *__restrict__ w, int rows, int cols, long row_bytes,
+                                                        const float *__restrict__ x, float *__restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint8_t *rp = w + static_cast<size_t>(row) * row_bytes;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    for (int c = 4 * lane; c < cols; c += 256) {
+        float wv[4];
+        if constexpr (T == VQ_F32) {
+            const float4 f = *reinterpret_cast<const float4 *>(rp + 4 * static_cast<size_t>(c));
+            wv[0] = f.x;
+            wv[1] = f.y;
+            wv[2] = f.z;
+            wv[3] = f.w;
+        } else {
+            const uint2 h = *reinterpret_cast<const uint2 *>(rp + 2 * static_cast<size_t>(c));
+            wv[0] = half_to_float(h.x);
+            wv[1] = half_to_float(h.x >> 16);
+            wv[2] = half_to_float(h.y);
+            wv[3] = half_to_float(h.y >> 16);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float4 f = *reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols + c);
+            acc[t] = fmaf(wv[0], f.x, fmaf(wv[1], f.y, fmaf(wv[2], f.z, fmaf(wv[3], f.w, acc[t]))));
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float v = wave_sum(acc[t]);
+        if (lane == 0) y[static_cast<size_t>(t) * rows + row] = v;
+    }
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void dequant_float_kernel(const uint8_t *__restrict__ w, int rows, int cols,
+                                                            long row_bytes, float *__restrict__ out) {
+    const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<long>(rows) * cols) return;
+    const long r = i / cols, c = i - r * cols;
+    const uint8_t *p = w + r * row_bytes;
+    out[i] = T == VQ_F32 ? reinterpret_cast<const float *>(p)[c] : half_to_float(reinterpret_cast<const uint16_t *>(p)[c]);
+}
+
+// ---- argmax ------------------------------------------------------------------------------------------------
+// One workgroup per row; strict '>' inside each thread's strided scan and lowest index on equal values
+// in the tree, so the lowest index of the maximum wins and NaN never does.
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restrict__ x, int n, int32_t *__restrict__ out) {
+    __shared__ float s_v[1024];
+    __shared__ int32_t s_i[1024];
+    const float *row = x + static_cast<size_t>(blockIdx.x) * n;
+    float bv = -__builtin_inff();
+    int32_t bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = row[i];
+        if (v > bv) {
+            bv = v;
+            bi = i;
+        }
+    }
+    s_v[threadIdx.x] = bv;
+    s_i[threadIdx.x] = bi;
+    __syncthreads();
+    for (int stride = blockDim.x / 2; stride > 0; stride >>= 1) {
+        if (threadIdx.x < stride) {
+            const float ov = s_v[threadIdx.x + stride];
+            const int32_t oi = s_i[threadIdx.x + stride];
+            if (ov > s_v[threadIdx.x] || (ov == s_v[threadIdx.x] && oi < s_i[threadIdx.x])) {
+                s_v[threadIdx.x] = ov;
+                s_i[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = s_i[0];
+}
+
+// ---- host-side dispatch --------------------------------------------------------------------------------
+
+int hip_status(hipError_t e) { return e == hipSuccess ? VQ_OK : static_cast<int>(e); }
+
+int check_matrix(int type, int rows, int cols) {
+    int bs, ts;
+    if (!vq_traits(type, &bs, &ts)) return VQ_ERR_TYPE;
+    if (rows < 1 || cols < 32 || cols % 32 != 0 || cols % bs != 0) return VQ_ERR_SHAPE;
+    return VQ_OK;
+}
+
+long row_bytes_of(int type, int cols) {
+    int bs, ts;
+    vq_traits(type, &bs, &ts);
+    return static_cast<long>(cols / bs) * ts;
+}
+
+// Calls f(std::integral_constant<int, T>) for a quantized type id.
+template <typename F>
+int dispatch_quant(int type, F &&f) {
+    switch (type) {
+        case VQ_Q8_0: return f(std::integral_constant<int, VQ_Q8_0>{});
+        case VQ_Q2_K: return f(std::integral_constant<int, VQ_Q2_K>{});
+        case VQ_Q3_K: return f(std::integral_constant<int, VQ_Q3_K>{});
+        case VQ_Q4_K: return f(std::integral_constant<int, VQ_Q4_K>{});
+        case VQ_Q5_K: return f(std::integral_constant<int, VQ_Q5_K>{});
+        case VQ_Q6_K: return f(std::integral_constant<int, VQ_Q6_K>{});
+        case VQ_IQ4_NL: return f(std::integral_constant<int, VQ_IQ4_NL>{});
+        case VQ_IQ4_XS: return f(std::integral_constant<int, VQ_IQ4_XS>{});
+        case VQ_IQ3_S: return f(std::integral_constant<int, VQ_IQ3_S>{});
+        case VQ_IQ2_XXS: return f(std::integral_constant<int, VQ_IQ2_XXS>{});
+        case VQ_IQ2_XS: return f(std::integral_constant<int, VQ_IQ2_XS>{});
+        case VQ_IQ2_S: return f(std::integral_constant<int, VQ_IQ2_S>{});
+        case VQ_IQ3_XXS: return f(std::integral_constant<int, VQ_IQ3_XXS>{});
+        default: return VQ_ERR_TYPE;
+    }
+}
+
+template <int T>
+int launch_float(const uint8_t *w, int rows, int cols, const float *x, int ntok, float *y, hipStream_t s) {
+    const long rb = row_bytes_of(T, cols);
+    const dim3 grid((rows + 3) / 4), block(256);
+    for (int c = 0; c < ntok; c += 8) {
+        const int m = ntok - c < 8 ? ntok - c : 8;
+        const float *xo = x + static_cast<size_t>(c) * cols;
+        float *yo = y + static_cast<size_t>(c) * rows;
+        switch (m) {
+#define VQ_CASE(N) \
+    case N: qmv_float_kernel<T, N><<<grid, block, 0, s>>>(w, rows, cols, rb, xo, yo); break;
+            VQ_CASE(1) VQ_CASE(2) VQ_CASE(3) VQ_CASE(4) VQ_CASE(5) VQ_CASE(6) VQ_CASE(7) VQ_CASE(8)
+#undef VQ_CASE
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_status(e);
+    }
+    return VQ_OK;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
+
+}  // namespace
+
+// ---- C ABI -------------------------------------------------------------------------------------------------
+
+extern "C" {
+
+int vq_type_traits(int type, int *block_size, int *type_size) {
+    return vq_traits(type, block_size, type_size) ? VQ_OK : VQ_ERR_TYPE;
+}
+
+long long vq_row_bytes(int type, int cols) {
+    int bs, ts;
+    if (!vq_traits(type, &bs, &ts) || cols <= 0 || cols % bs) return -1;
+    return static_cast<long long>(cols / bs) * ts;
+}
+
+const char *vq_status_string(int status) {
+    switch (status) {
+        case VQ_OK: return "success";
+        case VQ_ERR_TYPE: return "unsupported GGUF tensor type";
+        case VQ_ERR_SHAPE: return "invalid shape";
+        case VQ_ERR_WORKSPACE: return "workspace too small";
+        case VQ_ERR_ARG: return "invalid argument";
+        case VQ_ERR_NOT_INIT: return "library not initialised on this device";
+        default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown error";
+    }
+}
+
+int vq_init(void) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    return hip_status(e);
+}
+
+int vq_set_iq3s_grid(const uint8_t *grid) {
+    if (grid == nullptr) return VQ_ERR_ARG;
+    return vq::set_iq3s_grid(grid);
+}
+
+size_t vq_xpack_bytes(int cols, int ntok) {
+    if (cols <= 0 || ntok <= 0 || cols % 32) return 0;
+    return static_cast<size_t>(vq_xpack_stride(cols)) * ntok;
+}
+
+size_t vq_qmv_workspace_bytes(int cols, int ntok) { return vq_xpack_bytes(cols, ntok); }
+
+int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, float *xs, void *stream) {
+    if (!x || !xq || !xd) return VQ_ERR_ARG;
+    if (ntok < 1 || cols < 32 || cols % 32) return VQ_ERR_SHAPE;
+    const int n = ntok * (cols / 32);
+    const XOut o{xq, xd, xs, nullptr, cols, cols / 32};
+    quantize_x_kernel<<<(n + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(x, ntok, cols, o);
+    return hip_status(hipGetLastError());
+}
+
+int vq_pack_x(const float *x, int ntok, int cols, void *xpack, void *stream) {
+    if (!x || !xpack) return VQ_ERR_ARG;
+    if (ntok < 1 || cols < 32 || cols % 32) return VQ_ERR_SHAPE;
+    const int n = ntok * (cols / 32);
+    const long stride = vq_xpack_stride(cols);
+    char *base = static_cast<char *>(xpack);
+    const XOut o{reinterpret_cast<int8_t *>(base), reinterpret_cast<float *>(base + cols), nullptr,
+                 reinterpret_cast<uint32_t *>(base + vq_xpack_h_offset(cols)), stride, stride / 4};
+    quantize_x_kernel<<<(n + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(x, ntok, cols, o);
+    return hip_status(hipGetLastError());
+}
+
+int vq_qmv_packed(int type, const uint8_t *w, int rows, int cols, const void *xpack, int ntok, float *y, void *stream) {
+    int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;  // float weights take fp32 activations (vq_qmv)
+    if (!w || !xpack || !y) return VQ_ERR_ARG;
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    const long rb = row_bytes_of(type, cols);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t *xp = static_cast<const uint8_t *>(xpack);
+    return dispatch_quant(type, [&](auto tc) {
+        return vq::launch_quant<decltype(tc)::value>(w, rows, cols, rb, xp, ntok, y, s);
+    });
+}
+
+int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, float *y, void *workspace,
+           size_t workspace_bytes, void *stream) {
+    int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (!w || !x || !y) return VQ_ERR_ARG;
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (type == VQ_F32) return launch_float<VQ_F32>(w, rows, cols, x, ntok, y, s);
+    if (type == VQ_F16) return launch_float<VQ_F16>(w, rows, cols, x, ntok, y, s);
+    if (!workspace || workspace_bytes < vq_qmv_workspace_bytes(cols, ntok)) return VQ_ERR_WORKSPACE;
+    st = vq_pack_x(x, ntok, cols, workspace, stream);
+    if (st) return st;
+    return vq_qmv_packed(type, w, rows, cols, workspace, ntok, y, stream);
+}
+
+int vq_int_partials(int type, const uint8_t *w, int rows, int cols, const void *xpack, int ntok, int32_t *part,
+                    void *stream) {
+    int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;
+    if (!w || !xpack || !part) return VQ_ERR_ARG;
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    const long rb = row_bytes_of(type, cols);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t *xp = static_cast<const uint8_t *>(xpack);
+    return dispatch_quant(type, [&](auto tc) {
+        return vq::launch_partials<decltype(tc)::value>(w, rows, cols, rb, xp, ntok, part, s);
+    });
+}
+int vq_dequant_rows(int type, const uint8_t *w, int rows, int cols, float *out, void *stream) {
+    int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (!w || !out) return VQ_ERR_ARG;
+    const long rb = row_bytes_of(type, cols);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (type == VQ_F32 || type == VQ_F16) {
+        const long n = static_cast<long>(rows) * cols;
+        if (type == VQ_F32)
+            dequant_float_kernel<VQ_F32><<<(n + 255) / 256, 256, 0, s>>>(w, rows, cols, rb, out);
+        else
+            dequant_float_kernel<VQ_F16><<<(n + 255) / 256, 256, 0, s>>>(w, rows, cols, rb, out);
+        return hip_status(hipGetLastError());
+    }
+    return dispatch_quant(type, [&](auto tc) { return vq::launch_dequant<decltype(tc)::value>(w, rows, cols, rb, out, s); });
+}
+
+int vq_argmax_rows(const float *x, int n, int ntok, int32_t *out, void *stream) {
+    if (!x || !out) return VQ_ERR_ARG;
+    if (n < 1 || ntok < 1) return VQ_ERR_SHAPE;
+    argmax_rows_kernel<<<ntok, 1024, 0, static_cast<hipStream_t>(stream)>>>(x, n, out);
+    return hip_status(hipGetLastError());
+}
+
+}  // extern "C"

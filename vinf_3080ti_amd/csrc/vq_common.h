@@ -91,6 +91,12 @@ VQ_UNIT(VQ_IQ2_S, 82, 8)
 VQ_UNIT(VQ_IQ3_XXS, 98, 8)
 #undef VQ_UNIT
 
+// Packed activation record of one token (written by vq_pack_x, read by the quantized matvec, which copies it
+// verbatim into LDS): xq[cols] int8 | xd[cols/32] fp32 | xh[cols/32] u32 (16-element sums of q: half 0 in
+// the low 16 bits, half 1 in the high 16 bits, both signed). Tokens are vq_xpack_stride(cols) bytes apart.
+VQ_HD constexpr int vq_xpack_h_offset(int cols) { return cols + (cols / 32) * 4; }
+VQ_HD constexpr int vq_xpack_stride(int cols) { return (cols + (cols / 32) * 8 + 15) / 16 * 16; }
+
 // Weight buffers handed to the kernels carry at least this many readable bytes past the last block: the
 // streaming loads round the end of a row range up to 16 bytes.
 #define VQ_TAIL_PAD 16

@@ -1,0 +1,21 @@
+// vq_qmv.h -- host-side declarations of the per-type quantized kernels (defined in vq_qmv_impl.h and
+// instantiated once per GGUF type in vq_t_<type>.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vq {
+
+template <int T>
+int launch_quant(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int ntok, float *y,
+                 hipStream_t s);
+template <int T>
+int launch_partials(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int ntok,
+                    int32_t *part, hipStream_t s);
+template <int T>
+int launch_dequant(const uint8_t *w, int rows, int cols, long row_bytes, float *out, hipStream_t s);
+
+// Replace the IQ3_S codebook used by the IQ3_S kernels (defined in the IQ3_S translation unit).
+int set_iq3s_grid(const uint8_t *grid);
+
+}  // namespace vq
