@@ -11,170 +11,391 @@ namespace vq {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Tuning knobs (compile-time; the defaults are the measured best on MI355X).
-#ifndef VQ_KW_MAX
-#define VQ_KW_MAX 8  // longest straight-line window of units per lane
-#endif
-#ifndef VQ_RING_BYTES
-#define VQ_RING_BYTES 128  // bytes of raw slice data per lane kept in flight
-#endif
-#ifndef VQ_PIN
-#define VQ_PIN 2  // 0: free scheduling, 1: memory clobber per slot, 2: plus a scheduling barrier
-#endif
-#ifndef VQ_USE_XL
-#define VQ_USE_XL 1  // stage activations in LDS when they fit
-#endif
-#ifndef VQ_MAX_NT
-#define VQ_MAX_NT 8  // tokens per launch compiled (tuning builds may restrict this)
-#endif
-#ifndef VQ_MAX_WAVES
-#define VQ_MAX_WAVES 16  // waves per workgroup
+// Streaming geometry (compile-time; overridable for tuning builds).
+#ifndef VQ_X_LDS_MAX
+#define VQ_X_LDS_MAX (64 * 1024)  // bytes of activation records one launch keeps in LDS
 #endif
 
-// Slices kept in flight per lane (ring depth): enough outstanding loads to cover HBM latency within the
-// VGPR budget.
+// ---- global -> LDS DMA ---------------------------------------------------------------------------------
+// The weight stream reaches LDS through global_load_lds_dwordx4 (each lane moves 16 bytes; a wave writes
+// 1 KB contiguously at M0), so bytes in flight cost no VGPRs. The DMA is issued from inline asm: the
+// compiler then neither counts it nor inserts its own vmcnt(0) before every LDS read, and the kernel waits
+// on vmcnt itself (loads retire in order, so "at most N outstanding" means "all but the last N landed").
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void *)p));
+}
+// 64 lanes x 16 bytes: lane i copies base[voff_i .. +16) to LDS lds + 16 i. base and lds are wave-uniform.
+__device__ __forceinline__ void dma16(const void *base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, %0" ::"s"(base), "v"(voff), "s"(lds) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Sum over the 64 lanes with DPP moves (no LDS round trips): pairs, quads, half rows, rows, then rows 1/3
+// take row 0/2 (row_bcast:15) and rows 2/3 take lane 31 (row_bcast:31); lane 63 ends with the total.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f<0xB1>(v);        // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);        // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);       // row_half_mirror
+    v += dpp_f<0x140>(v);       // row_mirror
+    v += dpp_f<0x142, 0xA>(v);  // row_bcast:15
+    v += dpp_f<0x143, 0xC>(v);  // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Per-type stage shape: LPU lanes decode one unit (each takes SPB/LPU of its slices), so a stage is the
+// 64/LPU consecutive units of the wave's stream; each wave streams through a ring of RP 1 KB pieces. Tuning
+// builds override with VQ_LPU / VQ_RING_KB.
 template <int T>
-constexpr int kUnroll = VQ_RING_BYTES / static_cast<int>(sizeof(typename Sl<T>::W)) < 2
-                            ? 2
-                            : (VQ_RING_BYTES / static_cast<int>(sizeof(typename Sl<T>::W)) > 8
-                                   ? 8
-                                   : VQ_RING_BYTES / static_cast<int>(sizeof(typename Sl<T>::W)));
+struct StageShape {
+#ifdef VQ_LPU
+    static constexpr int LPU = VQ_LPU < Sl<T>::SPB ? VQ_LPU : Sl<T>::SPB;
+#else
+    // Two lanes per super-block for the K-quants with cheap decoders; one for the table-driven IQ types and
+    // Q6_K, whose per-slice decode dominates (measured on MI355X).
+    static constexpr int LPU = (T == VQ_Q2_K || T == VQ_Q3_K || T == VQ_Q4_K || T == VQ_Q5_K) ? 2 : 1;
+#endif
+#ifdef VQ_WAVES
+    static constexpr int NW = VQ_WAVES;
+#else
+    static constexpr int NW = Sl<T>::UG == 1 ? 8 : 4;  // waves per workgroup
+#endif
+#ifdef VQ_RING_KB
+    static constexpr int RP = VQ_RING_KB;  // ring size in 1 KB pieces (power of two)
+#else
+    static constexpr int RP = 8;
+#endif
+#ifdef VQ_SLICE_BLOCKED
+    static constexpr bool BLOCKED = VQ_SLICE_BLOCKED;  // lane j takes slices j*SPB/LPU.. (else j, j+LPU, ..)
+#else
+    static constexpr bool BLOCKED = false;
+#endif
+};
 
-constexpr int kXLdsMax = 48 * 1024;  // NT * vq_xpack_stride(cols) <= this -> activations live in LDS
-constexpr int kXStagePieces = 4;     // 16-byte pieces of the activation records each thread stages per pass
+// LDS image of the activation records: per token, the int8 codes in blocks of 256 followed by XPAD bytes
+// of padding (so that the codes lanes of neighbouring units read fall in different LDS banks), then the
+// group scales xd and the half sums xh as in the packed record. Built by the DMA: LDS chunk i (16 bytes)
+// is fetched from the packed record chunk that belongs there.
+#ifndef VQ_XPAD
+#define VQ_XPAD 32
+#endif
+struct XImage {
+    int ng, nblk, xq_bytes, bytes;  // bytes: one token's image (16-byte multiple)
+    __host__ __device__ explicit XImage(int cols)
+        : ng(cols / 32), nblk((cols / 32 + 7) / 8), xq_bytes(((cols / 32 + 7) / 8) * (256 + VQ_XPAD)),
+          bytes((((cols / 32 + 7) / 8) * (256 + VQ_XPAD) + (cols / 32) * 8 + 15) / 16 * 16) {}
+    __device__ int code_off(int G, int h) const { return (G >> 3) * (256 + VQ_XPAD) + (G & 7) * 32 + 16 * h; }
+    // Byte of the packed record (vq_xpack_h_offset layout) that LDS image byte o (16-byte aligned) holds,
+    // or -1 for padding.
+    __device__ int src_of(int o, int cols) const {
+        if (o < xq_bytes) {
+            const int blk = o / (256 + VQ_XPAD), w = o - blk * (256 + VQ_XPAD);
+            return w < 256 && blk * 256 + w < cols ? blk * 256 + w : -1;
+        }
+        return cols + (o - xq_bytes);
+    }
+};
+
+template <int T>
+struct Stream {
+    using S = Sl<T>;
+    static constexpr int LPU = StageShape<T>::LPU;
+    static constexpr int SPL = S::SPB / LPU;  // slices per lane
+    static constexpr int SU = 64 / LPU;       // units per stage
+    static constexpr bool BLOCKED = StageShape<T>::BLOCKED;
+    // Most 1 KB pieces one stage's bytes touch (its units plus the aligned dword the decoders may read past
+    // the last unit), the ring size (at least two pieces more) and the pieces kept requested beyond the
+    // current stage.
+    static constexpr int PMAX = (SU * S::UB + 4 + 1023) / 1024 + 1;
+    static constexpr int RP = StageShape<T>::RP >= PMAX + 2 ? StageShape<T>::RP : 2 * StageShape<T>::RP;
+    static constexpr int NW = StageShape<T>::NW;
+    static constexpr int LA = RP - PMAX;
+    static constexpr int WAVE_LDS = (RP + 1) * 1024;  // ring + mirror of its first piece
+    static_assert(S::SPB % LPU == 0 && (RP & (RP - 1)) == 0 && LA >= 1 && LA < 64, "ring geometry");
+};
+
+template <int T>
+constexpr int grid_table_bytes() {
+    return TabSpec<T>::n8 * 8 + TabSpec<T>::n4 * 4;
+}
+template <int T>
+__device__ __forceinline__ const uint8_t *grid_table_src() {
+    if constexpr (T == VQ_IQ2_XXS) return reinterpret_cast<const uint8_t *>(g_iq2xxs.v);
+    if constexpr (T == VQ_IQ2_XS) return reinterpret_cast<const uint8_t *>(g_iq2xs.v);
+    if constexpr (T == VQ_IQ2_S) return reinterpret_cast<const uint8_t *>(g_iq2s.v);
+    if constexpr (T == VQ_IQ3_XXS) return reinterpret_cast<const uint8_t *>(g_iq3xxs.v);
+    if constexpr (T == VQ_IQ3_S) return reinterpret_cast<const uint8_t *>(g_iq3s.v);
+    return nullptr;
+}
 
 // Quantized matvec: y[t][r] = W[r] . x[t] for t < NT.
 //
-// A workgroup of W waves is split into lane groups of L lanes, one weight row per group. Lane i of a group
-// keeps one slice position ss = i % SPB (L is a multiple of SPB) and handles the units u0, u0 + du, ... of
-// the row (u0 = i / SPB, du = L / SPB), so consecutive lanes read consecutive bytes and every load
-// instruction is coalesced. A window of KW units per lane is straight-line code: slot k + U is loaded
-// right after slot k is decoded, so U slices stay in flight, and with no branches inside the window the
-// waitcnt pass issues partial vmcnt waits (a loop back-edge or an early exit would make it drain every
-// load, or let LLVM sink each load next to its use). Slots past the row end load a clamped unit and are
-// dropped with a select. Rows longer than KW units per lane take several windows.
+// Wave g of the grid owns rows [g*rpw, (g+1)*rpw) -- a contiguous byte range, since rows are back to back
+// and each row is a whole number of units (32-element groups for Q8_0/IQ4_NL, 256-element super-blocks
+// otherwise). It streams that range through a private LDS ring of RP 1 KB pieces, keeping LA pieces past
+// the stage being decoded requested (a stage is SU = 64/LPU units). In a stage, the LPU lanes of unit i decode its slices with
+// the type's slice decoders (weights, activation records and IQ tables all read from LDS), so the block
+// header is decoded once per 256/LPU elements. A stage may hold the end of one row, whole rows and the
+// start of another: a segmented scan over the lanes (segments = rows) sums each row's part, segment ends
+// of finished rows write y, and the part of a row that continues into the next stage is carried.
 //
-// XL: all NT tokens' packed activation records (vq_pack_x) are copied to LDS first, so the per-slice
-// activation reads are LDS reads: they neither add L1 traffic nor join the in-order vmcnt queue of the weight
-// loads. The staging loads are issued before the first weight loads (vmcnt retires in order: waiting for
-// activations issued after the weights would wait for the weights too), then the weight prologue, then
-// the activations are written to LDS behind a partial wait.
-//
-// The group's L partial sums are reduced with cross-lane shuffles; lane 0 of the group writes y.
-template <int T, int NT, bool XL, int KW>
-__global__ __launch_bounds__(1024) void qmv_slice_kernel(const uint8_t *__restrict__ w, int rows, int cols,
-                                                         long row_bytes, const uint8_t *__restrict__ xpack,
-                                                         float *__restrict__ y, int L) {
+// LDS: [grid table | activation image of the NT tokens | ring + mirror piece per wave]. At start-up each
+// wave requests its share of the table and of the activation image, then its first pieces, and waits until
+// only the lookahead pieces are outstanding: the activations and the first stage are in, the weight
+// stream is already moving.
+template <int T, int NT, bool FEW>
+__global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const uint8_t *__restrict__ w, int rows, int cols,
+                                                                   const uint8_t *__restrict__ xpack,
+                                                                   float *__restrict__ y, int rpw) {
     using S = Sl<T>;
-    constexpr int NP = S::NP;
-    constexpr int U = kUnroll<T> < KW ? kUnroll<T> : KW;
-    extern __shared__ __attribute__((aligned(16))) uint8_t s_x[];
-    __shared__ uint2 s8[TabSpec<T>::n8 > 0 ? TabSpec<T>::n8 : 1];
-    __shared__ uint32_t s4[TabSpec<T>::n4 > 0 ? TabSpec<T>::n4 : 1];
+    using G = Stream<T>;
+    constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, RP = G::RP, LA = G::LA;
+    constexpr int TB = grid_table_bytes<T>();
+    extern __shared__ __attribute__((aligned(1024))) uint8_t s_dyn[];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_grid[TB > 0 ? TB : 16];
     __shared__ uint4 sks[TabSpec<T>::ks ? 128 : 1];
     __shared__ uint4 ssm[TabSpec<T>::sm ? 256 : 1];
 
-    const int ng = cols >> 5;
-    const int xb = vq_xpack_stride(cols);
-    const int xh_off = vq_xpack_h_offset(cols);
     const int lane = threadIdx.x & 63;
-    const int li = lane & (L - 1);
-    const int row = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * (64 / L) + lane / L;
-    const int nu = ng / S::UG;
-    const int ss = li & (S::SPB - 1);
-    const int du = L / S::SPB;
-    const int u0 = li / S::SPB;
-    const uint8_t *wp = w + static_cast<size_t>(min(row, rows - 1)) * row_bytes;
-    auto unit_ptr = [&](int u) { return wp + static_cast<size_t>(min(u, nu - 1)) * S::UB; };
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    constexpr int NW = G::NW;
+    const int nu = (cols >> 5) / S::UG;
+    const int xb = vq_xpack_stride(cols);
+    const XImage xi(cols);
+    const int xreg = (NT * xi.bytes + 1023) & ~1023;
+    uint8_t *ring = s_dyn + xreg + wv * G::WAVE_LDS;
+    const uint32_t ring_a = lds_addr(ring);
 
-    // Activation staging loads first (first pass of kXStagePieces 16-byte pieces per thread), then the first
-    // window's weight prologue, so HBM traffic starts at once and the staging wait does not cover the weights.
-    const int npieces = XL ? NT * xb / 16 : 0;
-    u32x4 xs_reg[kXStagePieces];
-    if constexpr (XL) {
-#pragma unroll
-        for (int k = 0; k < kXStagePieces; ++k)
-            xs_reg[k] = reinterpret_cast<const u32x4 *>(xpack)[min(static_cast<int>(threadIdx.x) + k * static_cast<int>(blockDim.x), npieces - 1)];
-    }
-    asm volatile("" ::: "memory");
-    typename S::W wr[KW];
-#pragma unroll
-    for (int k = 0; k < U; ++k) S::load(unit_ptr(u0 + k * du), ss, wr[k]);
-    asm volatile("" ::: "memory");
-
-    const Tabs tb = stage_tabs<T>(s8, s4, sks, ssm);
-    if constexpr (XL) {
-#pragma unroll
-        for (int k = 0; k < kXStagePieces; ++k) {
-            const int i = threadIdx.x + k * blockDim.x;
-            if (i < npieces) reinterpret_cast<u32x4 *>(s_x)[i] = xs_reg[k];
+    // Rows of this wave and its stages.
+    const long r0 = static_cast<long>(blockIdx.x * NW + wv) * rpw;
+    const long r1 = r0 + rpw < rows ? r0 + rpw : rows;
+    const long U0 = r0 * nu, U1 = r1 * nu;
+    const int nst = r0 < rows ? static_cast<int>((U1 - U0 + SU - 1) / SU) : 0;
+    // The wave's byte stream starts at the 16-byte boundary b0 below its first unit; piece k holds stream
+    // bytes [1024k, 1024k + 1024) in ring slot k % RP, and piece k = 0 (mod RP) also in the mirror slot RP, so a
+    // unit that starts in the last slot reads on contiguously. Pieces past the stream's end re-read its last
+    // chunk, which keeps the number of loads issued per piece constant.
+    const long b0 = (U0 * UB) & ~15L;
+    // Last chunk to load: the one holding the dword past the stream's last unit, but never one that ends
+    // beyond the matrix's 16 readable pad bytes (the decoders discard bytes past a block).
+    const long mend = static_cast<long>(rows) * nu * UB;
+    const long lastc = ((U1 * UB + 4) < mend ? (U1 * UB + 4) : mend) & ~15L;
+    const uint32_t last = static_cast<uint32_t>(U1 > U0 ? lastc - b0 : 0);
+    const uint8_t *wb = w + b0;
+    int issued = 0;
+    auto issue_to = [&](int target) {
+        for (; issued < target; ++issued) {
+            const uint32_t off = static_cast<uint32_t>(issued) * 1024 + lane * 16;
+            const uint32_t src = off < last ? off : last;
+            const uint32_t slot = issued & (RP - 1);
+            dma16(wb, src, ring_a + slot * 1024);
+            if (slot == 0) dma16(wb, src, ring_a + RP * 1024);
         }
-        for (int i = threadIdx.x + kXStagePieces * blockDim.x; i < npieces; i += blockDim.x)
-            reinterpret_cast<u32x4 *>(s_x)[i] = reinterpret_cast<const u32x4 *>(xpack)[i];
+    };
+    // Pieces stage s needs: all below its end piece.
+    auto end_piece = [&](int s) {
+        const long ua = U0 + static_cast<long>(s) * SU;
+        const long ub = ua + SU < U1 ? ua + SU : U1;
+        return static_cast<int>((ub * UB + 4 - b0 + 1023) >> 10);
+    };
+
+    // Start-up: table and activation pieces (striped over the waves), then the first D-1 stages.
+    if constexpr (TB > 0) {
+        const uint8_t *src = grid_table_src<T>();
+        for (int p = wv; p < TB / 1024; p += NW) dma16(src + p * 1024, lane * 16, lds_addr(s_grid) + p * 1024);
     }
-    if constexpr (XL || TabSpec<T>::n8 > 0 || TabSpec<T>::n4 > 0) __syncthreads();
-    const uint8_t *xsrc = XL ? s_x : xpack;  // activation records: LDS copy or the global packed buffer
+    for (int p = wv; p < xreg / 1024; p += NW) {
+        const int o = p * 1024 + lane * 16;  // LDS image byte of this lane's chunk
+        const int t = o / xi.bytes;
+        const int src = t < NT ? xi.src_of(o - t * xi.bytes, cols) : -1;
+        dma16(xpack, static_cast<uint32_t>(src >= 0 ? t * xb + src : 0), lds_addr(s_dyn) + p * 1024);
+    }
+    if (nst > 0) issue_to(end_piece(0) + LA);
+    Tabs tb{};
+    if constexpr (TabSpec<T>::n8 > 0) tb.grid8 = reinterpret_cast<const uint2 *>(s_grid);
+    if constexpr (TabSpec<T>::n4 > 0) tb.grid4 = reinterpret_cast<const uint32_t *>(s_grid);
+    if constexpr (TabSpec<T>::ks) {
+        for (int i = threadIdx.x; i < 128; i += blockDim.x) sks[i] = sign_entry(ksigns(i));
+        tb.ks128 = sks;
+    }
+    if constexpr (TabSpec<T>::sm) {
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) ssm[i] = sign_entry(i);
+        tb.sm256 = ssm;
+    }
+    if (nst > 0)
+        wait_vm<LA>();
+    else
+        wait_vm<0>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (nst == 0) return;
 
-    int pg[NP], ph[NP];
+    const int ul = lane / LPU;  // unit of this lane within a stage
+    const int lj = lane % LPU;  // which of the unit's lanes
+    const float inv_nu = 1.0f / static_cast<float>(nu);
+    long row_a = r0;       // row of the stage's first unit (wave-uniform)
+    int col_a = 0;         // its unit index within that row
+    long carry_row = -1;   // row whose earlier part is in carry[] (segmented-scan path)
+    float carry[NT];
+    float acc[3][NT];      // rows row_a, row_a+1, row_a+2 (FEW path: a stage touches at most three rows)
 #pragma unroll
-    for (int p = 0; p < NP; ++p) S::part(ss, p, pg[p], ph[p]);
-    float acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    for (int t = 0; t < NT; ++t) carry[t] = acc[0][t] = acc[1][t] = acc[2][t] = 0.0f;
 
-    for (int wb = 0; wb < nu; wb += KW * du) {
-        if (wb > 0) {
+    for (int s = 0; s < nst; ++s) {
+        issue_to(end_piece(s) + LA);
+        wait_vm<LA>();  // every piece below end_piece(s) has landed
+        const long ua = U0 + static_cast<long>(s) * SU;
+        const int nval = static_cast<int>((U1 - ua < SU ? U1 - ua : SU));  // units in this stage
+        const bool valid = ul < nval;
+        const uint8_t *up = ring + (((ua + (valid ? ul : 0)) * UB - b0) & (RP * 1024 - 1));
+        // Row and column unit of this lane's unit: c = col_a + ul = q*nu + cu with q small.
+        const int c = col_a + ul;
+        int q = static_cast<int>(static_cast<float>(c) * inv_nu);
+        q = (q + 1) * nu <= c ? q + 1 : q;
+        q = q * nu > c ? q - 1 : q;
+        const int cu = c - q * nu;
+        const int G0 = cu * S::UG;
+
+        float v[NT];
 #pragma unroll
-            for (int k = 0; k < U; ++k) S::load(unit_ptr(wb + u0 + k * du), ss, wr[k]);
+        for (int t = 0; t < NT; ++t) v[t] = 0.0f;
+#ifdef VQ_NODECODE
+        v[0] = static_cast<float>(*reinterpret_cast<const uint32_t *>(up + 4 * lj) & 0xFF) * static_cast<float>(G0);
+#else
+        // The unit's group scales and half sums of every token (two 16-byte LDS reads each).
+        float xdu[NT][S::UG];
+        int32_t xhu[NT][S::UG];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint8_t *xt = s_dyn + t * xi.bytes + xi.xq_bytes;
+#pragma unroll
+            for (int g = 0; g < S::UG; ++g) {
+                xdu[t][g] = reinterpret_cast<const float *>(xt)[G0 + g];
+                if constexpr (kNeedsX<T>) xhu[t][g] = reinterpret_cast<const int32_t *>(xt + 4 * xi.ng)[G0 + g];
+            }
         }
 #pragma unroll
-        for (int k = 0; k < KW; ++k) {
-            if (k + U < KW) S::load(unit_ptr(wb + u0 + (k + U) * du), ss, wr[k + U]);
-#if VQ_PIN >= 1
-            // Pin the load issue point: without a memory clobber LLVM sinks each load next to its use.
-            asm volatile("" ::: "memory");
-#endif
-#if VQ_PIN >= 2
-            // Keep the slot's decode here too, so register pressure stays at U slots.
-            __builtin_amdgcn_sched_barrier(0);
-#endif
-            const int u = wb + u0 + k * du;
-            const bool valid = u < nu;
-            uint32_t c[NP][4];
-            S::codes(wr[k], ss, tb, c);
+        for (int k = 0; k < G::SPL; ++k) {
+            const int ss = G::BLOCKED ? lj * G::SPL + k : lj + LPU * k;
+            typename S::W wr;
+            S::load(up, ss, wr);
+            uint32_t cd[NP][4];
+            S::codes(wr, ss, tb, cd);
             float sc[NP], mn[NP];
-            S::scales(wr[k], ss, sc, mn);
-            const int G0 = min(u, nu - 1) * S::UG;
+            S::scales(wr, ss, sc, mn);
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
+            for (int p = 0; p < NP; ++p) {
+                int pg, ph;
+                S::part(ss, p, pg, ph);
+                const int Gi = G0 + pg;
 #pragma unroll
-                for (int p = 0; p < NP; ++p) {
-                    const int G = G0 + pg[p];
-                    const uint8_t *xt = xsrc + t * xb;
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(xt + 32 * G + 16 * ph[p]);
-                    const float xdv = reinterpret_cast<const float *>(xt + cols)[G];
+                for (int t = 0; t < NT; ++t) {
+                    const uint8_t *xt = s_dyn + t * xi.bytes;
+                    const u32x4 xv4 = *reinterpret_cast<const u32x4 *>(xt + xi.code_off(Gi, ph));
+                    const float xdv = xdu[t][pg];
                     const int X = kNeedsX<T> ? static_cast<int>(static_cast<int16_t>(
-                                                   reinterpret_cast<const uint32_t *>(xt + xh_off)[G] >> (16 * ph[p])))
+                                                   static_cast<uint32_t>(xhu[t][pg]) >> (16 * ph)))
                                              : 0;
-                    const uint32_t xv[4] = {v.x, v.y, v.z, v.w};
-                    const int Sv = dot16(c[p], xv) - S::OFF * X;
-                    float f = static_cast<float>(Sv) * sc[p];
-                    if constexpr (kHasMin<T>) f = fmaf(-static_cast<float>(X), mn[p], f);
-                    const float nacc = fmaf(f, xdv, acc[t]);
-                    acc[t] = valid ? nacc : acc[t];
+                    const uint32_t xv[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
+                    const int Sv = dot16(cd[p], xv) - S::OFF * X;
+                    float g = static_cast<float>(Sv) * sc[p];
+                    if constexpr (kHasMin<T>) g = fmaf(-static_cast<float>(X), mn[p], g);
+                    v[t] = fmaf(g, xdv, v[t]);
                 }
+            }
         }
-    }
+
+#endif
+        if constexpr (FEW) {
+            // Rows have at least SU/2 units, so this lane's unit is in row row_a + q with q <= 2. Rows that end
+            // in this stage are summed over the wave and written; the others shift down.
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        float v = acc[t];
-        for (int off = L >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-        acc[t] = v;
-    }
-    if (li == 0 && row < rows) {
+            for (int t = 0; t < NT; ++t) {
+                acc[0][t] += q == 0 ? v[t] : 0.0f;
+                acc[1][t] += q == 1 ? v[t] : 0.0f;
+                acc[2][t] += q == 2 ? v[t] : 0.0f;
+            }
+            const int done = (col_a + nval) / nu;  // rows completed by this stage (0..2)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) y[static_cast<size_t>(t) * rows + row] = acc[t];
+            for (int k = 0; k < 2; ++k) {
+                if (k < done) {
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const float tot = wave_sum(acc[k][t]);
+                        if (lane == 0) y[static_cast<size_t>(t) * rows + row_a + k] = tot;
+                    }
+                }
+            }
+            if (done == 1) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    acc[0][t] = acc[1][t];
+                    acc[1][t] = acc[2][t];
+                    acc[2][t] = 0.0f;
+                }
+            } else if (done == 2) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    acc[0][t] = acc[2][t];
+                    acc[1][t] = acc[2][t] = 0.0f;
+                }
+            }
+            row_a += done;
+            col_a += nval - done * nu;
+        } else {
+        // Segmented inclusive scan over lanes; segments are rows (row ids are non-decreasing in lane order).
+        const int rr = valid ? static_cast<int>(row_a + q) : 0x7FFFFFFF;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int rp = __shfl_up(rr, d, 64);
+            const bool m = lane >= d && rp == rr;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float vp = __shfl_up(v[t], d, 64);
+                v[t] += m ? vp : 0.0f;
+            }
+        }
+        const int rn = __shfl_down(rr, 1, 64);
+        const bool seg_end = valid && (lane == 63 || rn != rr);
+        if (rr == carry_row) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) v[t] += carry[t];
+        }
+        const long ub = ua + nval;
+        if (seg_end && (static_cast<long>(rr) + 1) * nu <= ub) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) y[static_cast<size_t>(t) * rows + rr] = v[t];
+        }
+        // The stage's last row continues into the next stage unless it ends here.
+        const int lv = nval * LPU - 1;
+        const long last_row = __builtin_amdgcn_readlane(rr, lv);
+        if ((last_row + 1) * nu > ub) {
+            carry_row = last_row;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) carry[t] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[t]), lv));
+        } else {
+            carry_row = -1;
+        }
+        // Advance the stage origin by SU units.
+        col_a += SU;
+        if (col_a >= nu) {
+            const int adv = col_a / nu;
+            row_a += adv;
+            col_a -= adv * nu;
+        }
+        }
+        asm volatile("" ::: "memory");  // this stage's LDS reads stay ahead of the next DMA into its slot
     }
+    wait_vm<0>();  // no DMA may still be writing this wave's ring when it exits
 }
 
 // ---- test hooks (same decoders as the matvec) -----------------------------------------------------------
@@ -245,70 +466,83 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict_
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : static_cast<int>(e); }
 
-// Lanes per row: the widest group that still gives every lane >= 3 slices of the row.
-inline int lanes_per_row(int nsl) {
-    int L = 64;
-    while (L > 8 && nsl < 3 * L) L >>= 1;
-    return L;
-}
-
-// Waves per workgroup: as many as fit 1024 threads while the grid still spreads over all 256 CUs.
-inline int waves_per_wg(long lane_groups, int L) {
-    const long waves = (lane_groups * L + 63) / 64;
-    int W = VQ_MAX_WAVES;
-    while (W > 4 && waves / W < 512) W >>= 1;
-    return W;
-}
-
-template <int T, int N, bool XL>
-int launch_window(int KW, dim3 grid, dim3 block, size_t lds, hipStream_t s, const uint8_t *w, int rows, int cols,
-                  long rb, const uint8_t *xp, float *yo, int L) {
-    if constexpr (N <= 2) {
-        switch (KW) {
-            case 4: qmv_slice_kernel<T, N, XL, 4><<<grid, block, lds, s>>>(w, rows, cols, rb, xp, yo, L); break;
-            case 8: qmv_slice_kernel<T, N, XL, 8><<<grid, block, lds, s>>>(w, rows, cols, rb, xp, yo, L); break;
-            case 12: qmv_slice_kernel<T, N, XL, 12><<<grid, block, lds, s>>>(w, rows, cols, rb, xp, yo, L); break;
-            default: qmv_slice_kernel<T, N, XL, 16><<<grid, block, lds, s>>>(w, rows, cols, rb, xp, yo, L); break;
-        }
-    } else {
-        (void)KW;
-        qmv_slice_kernel<T, N, XL, 8><<<grid, block, lds, s>>>(w, rows, cols, rb, xp, yo, L);
+// Largest dynamic LDS a launch of `kernel` may use: the device's per-workgroup limit minus the kernel's
+// static LDS, raised once per kernel (launches above 64 KB need the attribute). 0 if the query fails.
+inline int raise_dynamic_lds(const void *kernel) {
+    int dev = 0, limit = 0;
+    hipFuncAttributes a{};
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&limit, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+        hipFuncGetAttributes(&a, kernel) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
     }
+    const int dyn = limit - static_cast<int>(a.sharedSizeBytes);
+    if (dyn <= 0 || hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, dyn) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return dyn;
+}
+
+inline size_t static_lds_bytes(const void *kernel) {
+    hipFuncAttributes a{};
+    if (hipFuncGetAttributes(&a, kernel) != hipSuccess) {
+        (void)hipGetLastError();
+        return 16 * 1024;
+    }
+    return a.sharedSizeBytes;
+}
+
+template <int T, int N>
+int launch_stream(const uint8_t *w, int rows, int cols, const uint8_t *xp, float *yo, hipStream_t s) {
+    using G = Stream<T>;
+    const bool few = 2 * ((cols / 32) / Sl<T>::UG) >= G::SU;
+    static const int max_dyn_f = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true>));
+    static const int max_dyn_s = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false>));
+    const int max_dyn = few ? max_dyn_f : max_dyn_s;
+    const int xreg = (N * XImage(cols).bytes + 1023) & ~1023;
+    const size_t lds = static_cast<size_t>(xreg) + static_cast<size_t>(G::NW) * G::WAVE_LDS;
+    if (lds > static_cast<size_t>(max_dyn)) return static_cast<int>(hipErrorInvalidConfiguration);
+    static const size_t lds_static = static_lds_bytes(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true>));
+    const size_t lds_wg = lds + lds_static;
+    // Waves the chip holds at this LDS footprint (160 KB per CU, at most 32 waves per CU), then rows per wave
+    // so the grid fills them.
+    long wg_per_cu = static_cast<long>((160 * 1024) / lds_wg);
+    if (wg_per_cu > 32 / G::NW) wg_per_cu = 32 / G::NW;
+    if (wg_per_cu < 1) wg_per_cu = 1;
+    const long target = 256 * wg_per_cu * G::NW;
+    const int rpw = static_cast<int>((rows + target - 1) / target);
+    const long waves = (rows + rpw - 1) / rpw;
+    const dim3 grid(static_cast<unsigned>((waves + G::NW - 1) / G::NW)), block(64 * G::NW);
+    if (few)
+        qmv_stream_kernel<T, N, true><<<grid, block, lds, s>>>(w, rows, cols, xp, yo, rpw);
+    else
+        qmv_stream_kernel<T, N, false><<<grid, block, lds, s>>>(w, rows, cols, xp, yo, rpw);
     return hip_status(hipGetLastError());
 }
 
 template <int T>
 int launch_quant(const uint8_t *w, int rows, int cols, long rb, const uint8_t *xpack, int ntok, float *y,
                  hipStream_t s) {
-    using S = Sl<T>;
-    const int ng = cols / 32;
-    const int nu = ng / S::UG;
-    const int L = lanes_per_row(nu * S::SPB);
-    const int du = L / S::SPB;
-    const int per_lane = (nu + du - 1) / du;
-    int KW = per_lane <= 4 ? 4 : per_lane <= 8 ? 8 : per_lane <= 12 ? 12 : 16;
-    if (KW > VQ_KW_MAX) KW = VQ_KW_MAX;
-    const int W = waves_per_wg(rows, L);
-    const int rows_per_wg = W * (64 / L);
-    const dim3 grid((rows + rows_per_wg - 1) / rows_per_wg), block(64 * W);
-    for (int c = 0; c < ntok; c += 8) {
-        const int m = ntok - c < 8 ? ntok - c : 8;
-        const uint8_t *xp = xpack + static_cast<size_t>(c) * vq_xpack_stride(cols);
+    (void)rb;
+    const int xb = vq_xpack_stride(cols);
+    int chunk = VQ_X_LDS_MAX / XImage(cols).bytes;
+    chunk = chunk > 8 ? 8 : chunk < 1 ? 1 : chunk;
+    for (int c = 0; c < ntok; c += chunk) {
+        const int m = ntok - c < chunk ? ntok - c : chunk;
+        const uint8_t *xp = xpack + static_cast<size_t>(c) * xb;
         float *yo = y + static_cast<size_t>(c) * rows;
-        const size_t lds = static_cast<size_t>(m) * vq_xpack_stride(cols);
-        const bool xl = VQ_USE_XL && lds <= kXLdsMax;
         int st = 0;
         switch (m) {
-#define VQ_CASE(N)                                                                                         \
-    case N:                                                                                                \
-        if constexpr (N <= VQ_MAX_NT)                                                                      \
-            st = xl ? launch_window<T, N, true>(KW, grid, block, lds, s, w, rows, cols, rb, xp, yo, L) \
-                    : launch_window<T, N, false>(KW, grid, block, 0, s, w, rows, cols, rb, xp, yo, L); \
-        else                                                                                               \
-            st = hipErrorInvalidValue;                                                                     \
-        break;
-            VQ_CASE(1) VQ_CASE(2) VQ_CASE(3) VQ_CASE(4) VQ_CASE(5) VQ_CASE(6) VQ_CASE(7) VQ_CASE(8)
-#undef VQ_CASE
+            case 1: st = launch_stream<T, 1>(w, rows, cols, xp, yo, s); break;
+            case 2: st = launch_stream<T, 2>(w, rows, cols, xp, yo, s); break;
+            case 3: st = launch_stream<T, 3>(w, rows, cols, xp, yo, s); break;
+            case 4: st = launch_stream<T, 4>(w, rows, cols, xp, yo, s); break;
+            case 5: st = launch_stream<T, 5>(w, rows, cols, xp, yo, s); break;
+            case 6: st = launch_stream<T, 6>(w, rows, cols, xp, yo, s); break;
+            case 7: st = launch_stream<T, 7>(w, rows, cols, xp, yo, s); break;
+            default: st = launch_stream<T, 8>(w, rows, cols, xp, yo, s); break;
         }
         if (st) return st;
     }
