@@ -3,7 +3,8 @@
 Headline workload: a qwen35-27B-shaped decode-step weight sweep, batch 1 — 64
 layers (48 gated-delta SSM + 16 gated-attention) with a UD-Q3_K_XL-like quant mix and the Q6_K LM head with
 on-device argmax, 13.44 GiB of synthetic seeded raw GGUF blocks resident in HBM. One step = one sweep:
-every weight matrix of the step read once by its qmv (activations quantized once per distinct input).
+every weight matrix of the step read once: per distinct input one vq_pack_x, one vq_qmv_group launch per
+run of same-type matrices sharing it (<= 4), and the fused vq_lmhead_argmax for the LM head.
 `value` = algorithmic bytes of the step / step time (GB/s); `ms_per_step` = ms per sweep.
 
 Also reported: per-quant-type matvec throughput at 5120x17408 (configs[0..2] shapes, rotating over weight
@@ -99,8 +100,26 @@ class Hip:
         st = self.lib.vq_pack_x(x.data_ptr(), ntok, cols, xp.data_ptr(), self.s())
         assert st == 0, st
 
+    def qmv(self, ty, w, rows, cols, x, ntok, y):
+        st = self.lib.vq_qmv(ty, w.data_ptr(), rows, cols, x.data_ptr(), ntok, y.data_ptr(), None, 0, self.s())
+        assert st == 0, st
+
     def qmv_packed(self, ty, w, rows, cols, xp, ntok, y):
         st = self.lib.vq_qmv_packed(ty, w.data_ptr(), rows, cols, xp.data_ptr(), ntok, y.data_ptr(), self.s())
+        assert st == 0, st
+
+    def group(self, ty, ws, rows, ys, cols, xp, ntok):
+        import ctypes
+
+        n = len(ws)
+        st = self.lib.vq_qmv_group(ty, n, (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws]),
+                                   (ctypes.c_int * n)(*rows), (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]),
+                                   cols, xp.data_ptr(), ntok, self.s())
+        assert st == 0, st
+
+    def lmhead(self, ty, w, rows, cols, x, ntok, out, ws):
+        st = self.lib.vq_lmhead_argmax(ty, w.data_ptr(), rows, cols, x.data_ptr(), ntok, out.data_ptr(), None,
+                                       ws.data_ptr(), ws.numel(), self.s())
         assert st == 0, st
 
     def argmax(self, y, n, ntok, out):
@@ -126,21 +145,27 @@ def time_kernel_loop(torch, fn, n_iter):
     return start.elapsed_time(stop) / n_iter
 
 
-def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=640 << 20):
-    """Per-launch µs and GB/s of the matvec kernel alone (activations pre-quantized), rotating weights."""
+def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=640 << 20, group=1):
+    """Per-launch µs and GB/s of the matvec kernel alone: `group` matrices of rows x cols (one vq_qmv_group
+    launch) on activations packed beforehand, rotating over weight copies larger than the MALL."""
     from vinf_3080ti_amd import row_bytes
 
-    nbytes = rows * row_bytes(ty, cols)
+    nbytes = rows * row_bytes(ty, cols) * group
     copies = max(2, -(-min_rotation_bytes // nbytes))
-    ws = make_weights(torch, ty, rows, cols, 1234 + ty, copies)
+    ws = make_weights(torch, ty, rows, cols, 1234 + ty, copies * group)
     x = torch.randn(ntok, cols, device="cuda")
     xp = hip.xpack(cols, ntok)
-    y = torch.empty(ntok, rows, device="cuda")
     hip.pack(x, ntok, cols, xp)
+    ys = [torch.empty(ntok, rows, device="cuda") for _ in range(group)]
+
+    def launch(i):
+        c = i % copies
+        hip.group(ty, ws[c * group:(c + 1) * group], [rows] * group, ys, cols, xp, ntok)
+
     for i in range(copies):  # warm-up
-        hip.qmv_packed(ty, ws[i], rows, cols, xp, ntok, y)
-    ms = time_kernel_loop(torch, lambda i: hip.qmv_packed(ty, ws[i % copies], rows, cols, xp, ntok, y), iters)
-    b = alg_bytes(ty, rows, cols, ntok)
+        launch(i)
+    ms = time_kernel_loop(torch, launch, iters)
+    b = alg_bytes(ty, rows, cols, ntok) * group
     del ws
     torch.cuda.empty_cache()
     return {"us": ms * 1e3, "GBps": b / (ms * 1e-3) / 1e9, "bytes": b, "frac": b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
@@ -157,24 +182,52 @@ class Sweep:
         self.bytes = sum(alg_bytes(ty, r, c, ntok) for _, ty, r, c, _ in self.plan)
         self.weight_bytes = sum(w.numel() - 256 for w in self.w)
         maxc = max(p[3] for p in self.plan)
-        maxr = max(p[2] for p in self.plan)
         self.x = torch.randn(ntok, maxc, device="cuda")
         self.xp = hip.xpack(maxc, ntok)
-        self.y = torch.empty(ntok * maxr, device="cuda")
+        self.ys = {}  # one output per matrix shape of a group position (outputs are not consumed)
         self.ids = torch.empty(ntok, dtype=torch.int32, device="cuda")
+        # Launch sequence: per distinct input one pack, then one grouped matvec per run of consecutive
+        # same-type matrices (<= 4) reading it; the LM head is the fused matvec + argmax.
+        self.ops = []
+        i = 0
+        while i < len(self.plan):
+            name, ty, rows, cols, key = self.plan[i]
+            if name == "output":
+                nws = hip.lib.vq_lmhead_argmax_workspace_bytes(ty, rows, cols, ntok)
+                self.head_ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+                self.ops.append(("head", i))
+                i += 1
+                continue
+            self.ops.append(("pack", cols))
+            j = i
+            while j < len(self.plan) and self.plan[j][4] == key:
+                k = j
+                while (k < len(self.plan) and k - j < 4 and self.plan[k][4] == key and self.plan[k][1] == ty
+                       and self.plan[k][3] == cols):
+                    k += 1
+                self.ops.append(("group", list(range(j, k))))
+                j = k
+                if j < len(self.plan):
+                    ty, cols = self.plan[j][1], self.plan[j][3]
+            i = j
+        for _, _, rows, _, _ in self.plan:
+            self.ys.setdefault(rows, torch.empty(ntok, rows, device="cuda"))
+        self.launches = sum(1 if op[0] != "head" else 2 for op in self.ops)
 
     def step(self):
-        """One decode-step sweep: every matrix read once; matrices sharing an input (ssm qkv/gate/beta/alpha,
-        attention q/k/v, ffn gate/up) reuse one int8 quantization of it."""
+        """One decode-step sweep: every matrix read once."""
         hip, ntok = self.hip, self.ntok
-        prev = None
-        for (name, ty, rows, cols, key), w in zip(self.plan, self.w):
-            if key != prev:
-                hip.pack(self.x, ntok, cols, self.xp)
-                prev = key
-            hip.qmv_packed(ty, w, rows, cols, self.xp, ntok, self.y)
-            if name == "output":
-                hip.argmax(self.y, rows, ntok, self.ids)
+        for op in self.ops:
+            if op[0] == "pack":
+                hip.pack(self.x, ntok, op[1], self.xp)
+            elif op[0] == "group":
+                idx = op[1]
+                _, ty, _, cols, _ = self.plan[idx[0]]
+                rows = [self.plan[i][2] for i in idx]
+                hip.group(ty, [self.w[i] for i in idx], rows, [self.ys[r] for r in rows], cols, self.xp, ntok)
+            else:
+                _, ty, rows, cols, _ = self.plan[op[1]]
+                hip.lmhead(ty, self.w[op[1]], rows, cols, self.x, ntok, self.ids, self.head_ws)
 
 
 def cpu_baseline(budget_s=12.0):
@@ -264,9 +317,9 @@ def main() -> None:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     hip = Hip(torch)
 
-    # Roofline of the dominant kernel (FFN gate/up: Q3_K 17408x5120, 128 launches per step).
-    log("roofline: Q3_K 17408x5120 matvec")
-    dom = bench_matvec(torch, hip, Q3_K, 17408, 5120, args.ntok, iters=100)
+    # Roofline of the dominant kernel: the FFN gate+up launch (2 x Q3_K 17408x5120, 64 launches per step).
+    log("roofline: grouped Q3_K 2 x 17408x5120 matvec")
+    dom = bench_matvec(torch, hip, Q3_K, 17408, 5120, args.ntok, iters=100, group=2)
     per_type = {}
     if not args.no_per_type:
         for ty in PER_TYPE:
@@ -330,12 +383,13 @@ def main() -> None:
             "bytes_per_step": sw.bytes,
             "weight_bytes_per_step": sw.weight_bytes,
             "launch": "hipGraph" if graph else "eager",
+            "launches_per_step": sw.launches,
             "frac_of_hbm_peak": round(value / HBM_PEAK_GBPS, 4),
             "wall_s": round(wall, 3),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"qmv_stream_kernel<Q3_K,{args.ntok}> 17408x5120",
+            "kernel": f"qmv_stream_kernel<Q3_K,{args.ntok}> gate+up group 2x17408x5120",
             "achieved": round(dom["GBps"], 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

@@ -2,6 +2,8 @@
  *
  * Plain pointers and sizes only. Every device pointer is a HIP device allocation on the current device;
  * `stream` is a hipStream_t (NULL = the null stream). All launches are asynchronous on `stream`.
+ * Weights, fp32 activations and packed activations passed to the matvec entry points must be 16-byte
+ * aligned (VQ_ERR_ARG otherwise): weights are streamed with 16-byte global-to-LDS loads.
  * Every entry point returns an int status: 0 on success, a negative VQ_ERR_* code for an invalid
  * argument (checked on the host before anything is launched), or a positive hipError_t value.
  *
@@ -73,7 +75,8 @@ int vq_set_iq3s_grid(const uint8_t *grid);
 /* Bytes of the packed activations (xpack) of `ntok` tokens of `cols` columns; 0 if cols % 32 != 0. */
 size_t vq_xpack_bytes(int cols, int ntok);
 
-/* Workspace bytes vq_qmv needs (the packed activations of `ntok` tokens). */
+/* Workspace bytes vq_qmv needs: 0 for cols <= 8192 (the activations are quantized inside the matvec),
+ * else vq_xpack_bytes(cols, ntok) (they are packed into the workspace by vq_pack_x first). */
 size_t vq_qmv_workspace_bytes(int cols, int ntok);
 
 /* Quantize activations to int8 per 32-group: d = amax/127, id = 1/d, q = rint(x*id), xs = d*sum(q).
@@ -84,9 +87,10 @@ int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, flo
  * vq_qmv_packed and vq_int_partials read. Replaces: the same quantizer (qwen_cpu.c:607-627). */
 int vq_pack_x(const float *x, int ntok, int cols, void *xpack, void *stream);
 
-/* y[t][r] = W[r] . x[t] for t < ntok (any ntok >= 1; weights are read once per 8 tokens).
- * Quantized types quantize x into `workspace` first (vq_qmv_workspace_bytes); F32/F16 weights use x
- * directly and need no workspace. Replaces: Runtime_qmv (qwen_runtime.cu:1860-1912) on its matvec branch,
+/* y[t][r] = W[r] . x[t] for t < ntok (any ntok >= 1; weights are read once per launch of up to 8 tokens).
+ * Quantized types quantize x per 32-group with the vq_pack_x quantizer: inside the matvec, or into
+ * `workspace` (>= vq_qmv_workspace_bytes, else VQ_ERR_WORKSPACE) when that is non-zero; F32/F16 weights use
+ * x directly. Replaces: Runtime_qmv (qwen_runtime.cu:1860-1912) on its matvec branch,
  * whose numerics contract is Cpu_qmv (qwen_cpu.c:581-641). */
 int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, float *y, void *workspace,
            size_t workspace_bytes, void *stream);
@@ -96,6 +100,25 @@ int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int n
  * (qwen_cpu.c:628-637). */
 int vq_qmv_packed(int type, const uint8_t *w, int rows, int cols, const void *xpack, int ntok, float *y,
                   void *stream);
+
+/* Grouped matvec: y[k][t][r] = W_k[r] . x[t] for k < n <= VQ_MAX_GROUP matrices of one quantized type and
+ * width sharing packed activations (a layer's gate/up or q/k/v): one launch streams all of them. w, rows, y
+ * are host arrays of n entries. No counterpart in the reference's per-matrix qmv (qwen_runtime.cu:1860);
+ * its effect equals n vq_qmv_packed calls. */
+#define VQ_MAX_GROUP 4
+int vq_qmv_group(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                 const void *xpack, int ntok, void *stream);
+
+/* Workspace bytes vq_lmhead_argmax needs for this matrix and ntok (0 for invalid arguments). */
+size_t vq_lmhead_argmax_workspace_bytes(int type, int rows, int cols, int ntok);
+
+/* Fused LM head: out_idx[t] = argmax_r (W[r] . x[t]) for t < ntok (ties -> lowest row; NaN and -inf never
+ * win; INT32_MAX when no row qualifies), without re-reading the logits: each wave keeps the best of its
+ * rows and a one-block kernel reduces the per-wave bests. logits may be NULL; if not, y[t][r] is written
+ * too. Replaces: the QMV_FLAG_ARGMAX path + op_argmax (qwen_megakernel.cu:552-606,800-829) and
+ * Runtime_qmv + Runtime_argmax_rows (qwen_runtime.cu:1860-1912,2181-2197). */
+int vq_lmhead_argmax(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, int32_t *out_idx,
+                     float *logits, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Test hook: part[((t*rows + r)*(cols/32) + g)*2 + h] = exact int32 sum over the 16 elements of half h
  * of group g of (weight code * xq), computed by the matvec's own decoders from packed activations.

@@ -54,7 +54,9 @@ def test_host_side_argument_checks(lib):
     assert lib.vq_qmv(int(T.Q4_K), fake, 0, 256, fake, 1, fake, fake, 1 << 20, None) == _lib.VQ_ERR_SHAPE
     assert lib.vq_qmv(int(T.Q4_K), fake, 4, 256, fake, 0, fake, fake, 1 << 20, None) == _lib.VQ_ERR_SHAPE
     assert lib.vq_qmv(int(T.Q4_K), None, 4, 256, fake, 1, fake, fake, 1 << 20, None) == _lib.VQ_ERR_ARG
-    assert lib.vq_qmv(int(T.Q4_K), fake, 4, 256, fake, 1, fake, fake, 16, None) == _lib.VQ_ERR_WORKSPACE
+    assert lib.vq_qmv(int(T.Q4_K), ctypes.c_void_p(0x1008), 4, 256, fake, 1, fake, None, 0, None) == _lib.VQ_ERR_ARG
+    assert lib.vq_qmv(int(T.Q4_K), fake, 4, 256, ctypes.c_void_p(0x1004), 1, fake, None, 0, None) == _lib.VQ_ERR_ARG
+    assert lib.vq_qmv_packed(int(T.Q4_K), fake, 4, 256, ctypes.c_void_p(0x1001), 1, fake, None) == _lib.VQ_ERR_ARG
     assert lib.vq_qmv_packed(int(T.F32), fake, 4, 256, fake, 1, fake, None) == _lib.VQ_ERR_TYPE
     assert lib.vq_qmv_packed(int(T.Q4_K), fake, 4, 256, None, 1, fake, None) == _lib.VQ_ERR_ARG
     assert lib.vq_quantize_x(fake, 1, 48, fake, fake, None, None) == _lib.VQ_ERR_SHAPE
@@ -66,7 +68,20 @@ def test_host_side_argument_checks(lib):
     assert lib.vq_xpack_bytes(5120, 1) == 5120 + 160 * 8
     assert lib.vq_xpack_bytes(96, 1) == 128 and lib.vq_xpack_bytes(96, 3) == 384
     assert lib.vq_xpack_bytes(48, 1) == 0
-    assert lib.vq_qmv_workspace_bytes(5120, 8) >= lib.vq_xpack_bytes(5120, 8)
+    assert lib.vq_qmv_workspace_bytes(5120, 8) == 0  # narrow inputs are quantized inside the matvec
+    assert lib.vq_qmv_workspace_bytes(17408, 2) == lib.vq_xpack_bytes(17408, 2)
+    assert lib.vq_qmv(int(T.Q4_K), fake, 4, 17408, fake, 1, fake, None, 0, None) == _lib.VQ_ERR_WORKSPACE
+    arr = (ctypes.c_void_p * 5)(*([fake] * 5))
+    rws = (ctypes.c_int * 5)(*([4] * 5))
+    assert lib.vq_qmv_group(int(T.Q4_K), 0, arr, rws, arr, 256, fake, 1, None) == _lib.VQ_ERR_ARG
+    assert lib.vq_qmv_group(int(T.Q4_K), 5, arr, rws, arr, 256, fake, 1, None) == _lib.VQ_ERR_ARG
+    assert lib.vq_qmv_group(int(T.F32), 2, arr, rws, arr, 256, fake, 1, None) == _lib.VQ_ERR_TYPE
+    assert lib.vq_qmv_group(int(T.Q4_K), 2, arr, rws, arr, 100, fake, 1, None) == _lib.VQ_ERR_SHAPE
+    assert lib.vq_lmhead_argmax_workspace_bytes(int(T.F16), 4, 256, 1) == 0
+    nws = lib.vq_lmhead_argmax_workspace_bytes(int(T.Q6_K), 248320, 5120, 1)
+    assert nws >= 8 * 256  # one key per wave per token
+    assert lib.vq_lmhead_argmax(int(T.Q6_K), fake, 248320, 5120, fake, 1, fake, None, fake, nws - 1,
+                                None) == _lib.VQ_ERR_WORKSPACE
     assert b"workspace" in lib.vq_status_string(_lib.VQ_ERR_WORKSPACE)
 
 

@@ -188,3 +188,84 @@ def test_zero_and_extreme_activations(env, oracle_mod):
     ref = oracle_mod.qmv(int(T.Q4_K), w, rows, cols, x, 2)
     assert np.array_equal(got[0], ref[0]) and np.all(got[0] == 0)
     assert rel_l2(got[1], ref[1]) <= REL_L2_TOL
+
+
+def _pack(torch, lib, x: np.ndarray, ntok: int, cols: int):
+    xd_ = dev(torch, x.astype(np.float32).reshape(ntok, cols))
+    xp = torch.empty(lib.vq_xpack_bytes(cols, ntok), dtype=torch.uint8, device="cuda")
+    assert lib.vq_pack_x(P(xd_), ntok, cols, P(xp), None) == 0
+    return xp
+
+
+@pytest.mark.parametrize("ty,rows_list,cols", [(T.Q3_K, [37, 64], 2048), (T.Q8_0, [48, 48, 5], 5120),
+                                               (T.Q5_K, [300, 77, 9, 128], 5120), (T.IQ2_XXS, [130, 3], 1024)],
+                         ids=lambda v: v.name if isinstance(v, T) else str(v))
+@pytest.mark.parametrize("ntok", [1, 3, 9])
+def test_qmv_group_matches_oracle(env, oracle_mod, ty, rows_list, cols, ntok):
+    """One grouped launch over matrices sharing packed activations == each matrix on its own."""
+    torch, lib = env
+    rng = np.random.default_rng(sum(rows_list) + ntok)
+    ws = [synth.baseline_rows(ty, r, cols, rng) for r in rows_list]
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    xp = _pack(torch, lib, x, ntok, cols)
+    wd = [wdev(torch, w) for w in ws]
+    ys = [torch.full((ntok, r), np.nan, dtype=torch.float32, device="cuda") for r in rows_list]
+    n = len(rows_list)
+    wa = (ctypes.c_void_p * n)(*[P(t) for t in wd])
+    ra = (ctypes.c_int * n)(*rows_list)
+    ya = (ctypes.c_void_p * n)(*[P(t) for t in ys])
+    assert lib.vq_qmv_group(int(ty), n, wa, ra, ya, cols, P(xp), ntok, None) == 0
+    torch.cuda.synchronize()
+    for w, r, y in zip(ws, rows_list, ys):
+        ref = oracle_mod.qmv(int(ty), w, r, cols, x, ntok)
+        got = y.cpu().numpy()
+        for t in range(ntok):
+            assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, r, t)
+
+
+def _lmhead(torch, lib, ty, wd, rows, cols, x, ntok, with_logits=True):
+    xd_ = dev(torch, x.astype(np.float32).reshape(ntok, cols))
+    nws = lib.vq_lmhead_argmax_workspace_bytes(int(ty), rows, cols, ntok)
+    assert nws > 0
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+    out = torch.full((ntok,), -7, dtype=torch.int32, device="cuda")
+    logits = torch.empty(ntok, rows, dtype=torch.float32, device="cuda") if with_logits else None
+    st = lib.vq_lmhead_argmax(int(ty), P(wd), rows, cols, P(xd_), ntok, P(out), P(logits) if with_logits else None,
+                              P(ws), nws, None)
+    assert st == 0, lib.vq_status_string(st)
+    torch.cuda.synchronize()
+    return out.cpu().tolist(), (logits.cpu().numpy() if with_logits else None)
+
+
+@pytest.mark.parametrize("ty,rows,cols", [(T.Q6_K, 4099, 1024), (T.Q8_0, 2000, 512), (T.Q4_K, 777, 9216)],
+                         ids=lambda v: v.name if isinstance(v, T) else str(v))
+@pytest.mark.parametrize("ntok", [1, 3, 9])
+def test_lmhead_argmax_fused(env, oracle_mod, ty, rows, cols, ntok):
+    """Fused LM-head argmax: the index of the largest logit (exactly that of the logits it also writes),
+    ties to the lowest row, NaN rows never win; agrees with the reference CPU logits."""
+    torch, lib = env
+    rng = np.random.default_rng(rows + ntok)
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok)
+    rb = len(w) // rows
+    # Tie: copy token 0's best row over a lower row; NaN: a row whose fp16 scale is NaN.
+    best0 = int(np.argmax(ref[0]))
+    low = best0 // 2
+    w = w.copy()
+    w[low * rb:(low + 1) * rb] = w[best0 * rb:(best0 + 1) * rb]
+    nan_row = (best0 + 1) % rows if (best0 + 1) % rows != low else (best0 + 2) % rows
+    d_off = {T.Q6_K: 208, T.Q8_0: 0, T.Q4_K: 0}[ty]
+    w[nan_row * rb + d_off: nan_row * rb + d_off + 2] = np.frombuffer(np.float16(np.nan).tobytes(), np.uint8)
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok)
+    wd = wdev(torch, w)
+    idx, logits = _lmhead(torch, lib, ty, wd, rows, cols, x, ntok)
+    idx2, _ = _lmhead(torch, lib, ty, wd, rows, cols, x, ntok, with_logits=False)
+    assert idx == idx2
+    assert idx == oracle_mod.argmax_rows(logits, rows, ntok)  # exactly the argmax of its own logits
+    assert idx[0] == low  # the tie goes to the lower row
+    for t in range(ntok):
+        assert np.isnan(logits[t, nan_row]) and idx[t] != nan_row
+        finite = np.where(np.isnan(ref[t]), -np.inf, ref[t])
+        assert finite[idx[t]] >= finite.max() - 1e-4 * np.abs(finite).max(), t
+        assert rel_l2(np.nan_to_num(logits[t]), np.nan_to_num(ref[t])) <= REL_L2_TOL

@@ -18,6 +18,7 @@
 
 #include "vq_common.h"
 #include "vq_qmv.h"
+#include "vq_quant.h"
 #include "../../include/vq.h"
 
 namespace {
@@ -33,9 +34,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // ---- activation quantizer ------------------------------------------------------------------------------
-// One thread per (token, 32-group). Same IEEE operations as the reference CPU quantizer
-// (qwen_cpu.c:607-627): amax = max|v|, d = amax/127 (correctly rounded division), id = 1/d,
-// q = rint(v*id) (round half to even, as lrintf), xs = d*sum(q).
+// One thread per (token, 32-group), quantize_group (vq_quant.h) per group; xs = d*sum(q).
 // Outputs go to (xq, xd, xs, xh) with per-token strides, so one kernel writes either the separate arrays of
 // vq_quantize_x or the packed activation record of vq_pack_x (layout: vq_xpack_h_offset / vq_xpack_stride in vq_common.h).
 struct XOut {
@@ -50,42 +49,13 @@ __global__ __launch_bounds__(256) void quantize_x_kernel(const float *__restrict
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= ntok * ng) return;
     const int t = i / ng, g = i - t * ng;
-    const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols + 32 * g);
-    float v[32];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float4 f = src[k];
-        v[4 * k] = f.x;
-        v[4 * k + 1] = f.y;
-        v[4 * k + 2] = f.z;
-        v[4 * k + 3] = f.w;
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(v[k]));
-    const float d = amax / 127.0f;
-    const float id = d > 0.0f ? 1.0f / d : 0.0f;
-    int half_sum[2] = {0, 0};
-    uint32_t packed[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        uint32_t p = 0;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const int q = static_cast<int>(__builtin_rintf(v[4 * k + b] * id));
-            half_sum[k >> 2] += q;
-            p |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * b);
-        }
-        packed[k] = p;
-    }
-    const int sum = half_sum[0] + half_sum[1];
+    const vq::QGroup qg = vq::quantize_group(x + static_cast<size_t>(t) * cols + 32 * g);
     uint4 *dst = reinterpret_cast<uint4 *>(o.xq + t * o.q_stride + 32 * g);
-    dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-    o.xd[t * o.d_stride + g] = d;
-    if (o.xs) o.xs[t * o.d_stride + g] = d * static_cast<float>(sum);
-    if (o.xh)
-        o.xh[t * o.d_stride + g] = (static_cast<uint32_t>(half_sum[0]) & 0xFFFFu) | (static_cast<uint32_t>(half_sum[1]) << 16);
+    dst[0] = make_uint4(qg.q[0], qg.q[1], qg.q[2], qg.q[3]);
+    dst[1] = make_uint4(qg.q[4], qg.q[5], qg.q[6], qg.q[7]);
+    o.xd[t * o.d_stride + g] = qg.d;
+    if (o.xs) o.xs[t * o.d_stride + g] = qg.d * static_cast<float>(qg.hs0 + qg.hs1);
+    if (o.xh) o.xh[t * o.d_stride + g] = qg.half_sums();
 }
 
 // ---- float weights (F32/F16): one wave per row, fp32 activations, no quantization (qwen_cpu.c:345-360) ---
@@ -228,6 +198,8 @@ int launch_float(const uint8_t *w, int rows, int cols, const float *x, int ntok,
     return VQ_OK;
 }
 
+bool misaligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
+
 size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
 }  // namespace
@@ -277,7 +249,13 @@ size_t vq_xpack_bytes(int cols, int ntok) {
     return static_cast<size_t>(vq_xpack_stride(cols)) * ntok;
 }
 
-size_t vq_qmv_workspace_bytes(int cols, int ntok) { return vq_xpack_bytes(cols, ntok); }
+// Activations of up to this many columns are quantized inside the matvec (each workgroup quantizes its own
+// copy: cheaper than a separate quantizer launch for narrow inputs); wider ones are packed first.
+constexpr int kFusedQuantMaxCols = 8192;
+
+size_t vq_qmv_workspace_bytes(int cols, int ntok) {
+    return cols > kFusedQuantMaxCols ? vq_xpack_bytes(cols, ntok) : 0;
+}
 
 int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, float *xs, void *stream) {
     if (!x || !xq || !xd) return VQ_ERR_ARG;
@@ -304,13 +282,12 @@ int vq_qmv_packed(int type, const uint8_t *w, int rows, int cols, const void *xp
     int st = check_matrix(type, rows, cols);
     if (st) return st;
     if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;  // float weights take fp32 activations (vq_qmv)
-    if (!w || !xpack || !y) return VQ_ERR_ARG;
+    if (!w || !xpack || !y || misaligned16(w) || misaligned16(xpack)) return VQ_ERR_ARG;
     if (ntok < 1) return VQ_ERR_SHAPE;
     const long rb = row_bytes_of(type, cols);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const uint8_t *xp = static_cast<const uint8_t *>(xpack);
     return dispatch_quant(type, [&](auto tc) {
-        return vq::launch_quant<decltype(tc)::value>(w, rows, cols, rb, xp, ntok, y, s);
+        return vq::launch_quant<decltype(tc)::value>(w, rows, cols, rb, xpack, false, ntok, y, s);
     });
 }
 
@@ -318,15 +295,72 @@ int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int n
            size_t workspace_bytes, void *stream) {
     int st = check_matrix(type, rows, cols);
     if (st) return st;
-    if (!w || !x || !y) return VQ_ERR_ARG;
+    if (!w || !x || !y || misaligned16(w) || misaligned16(x)) return VQ_ERR_ARG;
     if (ntok < 1) return VQ_ERR_SHAPE;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (type == VQ_F32) return launch_float<VQ_F32>(w, rows, cols, x, ntok, y, s);
     if (type == VQ_F16) return launch_float<VQ_F16>(w, rows, cols, x, ntok, y, s);
-    if (!workspace || workspace_bytes < vq_qmv_workspace_bytes(cols, ntok)) return VQ_ERR_WORKSPACE;
-    st = vq_pack_x(x, ntok, cols, workspace, stream);
+    const long rb = row_bytes_of(type, cols);
+    const size_t need = vq_qmv_workspace_bytes(cols, ntok);
+    if (need > 0) {
+        if (!workspace || workspace_bytes < need || misaligned16(workspace)) return VQ_ERR_WORKSPACE;
+        st = vq_pack_x(x, ntok, cols, workspace, stream);
+        if (st) return st;
+        return vq_qmv_packed(type, w, rows, cols, workspace, ntok, y, stream);
+    }
+    return dispatch_quant(type, [&](auto tc) {
+        return vq::launch_quant<decltype(tc)::value>(w, rows, cols, rb, x, true, ntok, y, s);
+    });
+}
+
+int vq_qmv_group(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                 const void *xpack, int ntok, void *stream) {
+    if (n < 1 || n > VQ_MAX_GROUP || !w || !rows || !y) return VQ_ERR_ARG;
+    if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;
+    for (int k = 0; k < n; ++k) {
+        const int st = check_matrix(type, rows[k], cols);
+        if (st) return st;
+        if (!w[k] || !y[k] || misaligned16(w[k])) return VQ_ERR_ARG;
+    }
+    if (!xpack || misaligned16(xpack)) return VQ_ERR_ARG;
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return dispatch_quant(type, [&](auto tc) {
+        return vq::launch_quant_jobs<decltype(tc)::value>(n, w, rows, y, cols, xpack, false, ntok, nullptr, nullptr, s);
+    });
+}
+
+size_t vq_lmhead_argmax_workspace_bytes(int type, int rows, int cols, int ntok) {
+    if (check_matrix(type, rows, cols) || type == VQ_F32 || type == VQ_F16 || ntok < 1) return 0;
+    const long kw = dispatch_quant(type, [&](auto tc) {
+        return static_cast<int>(vq::argmax_waves<decltype(tc)::value>(rows, cols, ntok));
+    });
+    return align256(static_cast<size_t>(ntok) * kw * 8) + vq_qmv_workspace_bytes(cols, ntok);
+}
+
+int vq_lmhead_argmax(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, int32_t *out_idx,
+                     float *logits, void *workspace, size_t workspace_bytes, void *stream) {
+    int st = check_matrix(type, rows, cols);
     if (st) return st;
-    return vq_qmv_packed(type, w, rows, cols, workspace, ntok, y, stream);
+    if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;
+    if (!w || !x || !out_idx || misaligned16(w) || misaligned16(x)) return VQ_ERR_ARG;
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    const size_t need = vq_lmhead_argmax_workspace_bytes(type, rows, cols, ntok);
+    if (!workspace || workspace_bytes < need || misaligned16(workspace)) return VQ_ERR_WORKSPACE;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto *keys = static_cast<unsigned long long *>(workspace);
+    const size_t pack_bytes = vq_qmv_workspace_bytes(cols, ntok);
+    const void *xin = x;
+    if (pack_bytes > 0) {
+        void *xp = static_cast<uint8_t *>(workspace) + (need - pack_bytes);
+        st = vq_pack_x(x, ntok, cols, xp, stream);
+        if (st) return st;
+        xin = xp;
+    }
+    return dispatch_quant(type, [&](auto tc) {
+        return vq::launch_quant_jobs<decltype(tc)::value>(1, &w, &rows, &logits, cols, xin, pack_bytes == 0, ntok,
+                                                          keys, out_idx, s);
+    });
 }
 
 int vq_int_partials(int type, const uint8_t *w, int rows, int cols, const void *xpack, int ntok, int32_t *part,

@@ -7,8 +7,15 @@
 namespace vq {
 
 template <int T>
-int launch_quant(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int ntok, float *y,
+int launch_quant(const uint8_t *w, int rows, int cols, long row_bytes, const void *x, bool x_f32, int ntok, float *y,
                  hipStream_t s);
+// y_j = W_j x for n <= 4 matrices of type T sharing cols and x; optional fused argmax (n == 1): `amax` holds
+// [ntok][argmax_waves] keys, amax_out[t] receives the index.
+template <int T>
+int launch_quant_jobs(int n, const uint8_t *const *w, const int *rows, float *const *y, int cols, const void *x,
+                      bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s);
+template <int T>
+long argmax_waves(int rows, int cols, int ntok);
 template <int T>
 int launch_partials(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int ntok,
                     int32_t *part, hipStream_t s);

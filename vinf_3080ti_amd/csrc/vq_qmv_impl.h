@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "vq_qmv.h"
+#include "vq_quant.h"
 #include "vq_tables.h"
 
 namespace vq {
@@ -136,6 +137,30 @@ __device__ __forceinline__ const uint8_t *grid_table_src() {
     return nullptr;
 }
 
+// One launch covers up to kMaxJobs matrices of the same type and width that share the activations (a
+// layer's gate/up, q/k/v, ...). Job j owns the grid's waves [wave0, wave0 + ceil(rows/rpw)).
+constexpr int kMaxJobs = 4;
+struct QJob {
+    const uint8_t *w;
+    float *y;  // [NT][rows], or null (argmax only)
+    int rows, rpw, wave0;
+};
+struct QJobs {
+    QJob j[kMaxJobs];
+    int n;
+    int waves;               // total waves of the grid that own rows
+    unsigned long long *amax;  // null, or [NT][waves] per-wave argmax keys (see argmax_key)
+};
+
+// Argmax key of a value at row r: larger key = larger value, then lower row. NaN and -inf never win (the
+// reference kernel starts from -inf and takes strictly greater values); 0 = no candidate.
+__device__ __forceinline__ unsigned long long argmax_key(float v, long r) {
+    const uint32_t u = __float_as_uint(v);
+    if (v != v || v == -__builtin_huge_valf()) return 0ull;
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<unsigned long long>(o) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(r));
+}
+
 // Quantized matvec: y[t][r] = W[r] . x[t] for t < NT.
 //
 // Wave g of the grid owns rows [g*rpw, (g+1)*rpw) -- a contiguous byte range, since rows are back to back
@@ -151,10 +176,9 @@ __device__ __forceinline__ const uint8_t *grid_table_src() {
 // wave requests its share of the table and of the activation image, then its first pieces, and waits until
 // only the lookahead pieces are outstanding: the activations and the first stage are in, the weight
 // stream is already moving.
-template <int T, int NT, bool FEW>
-__global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const uint8_t *__restrict__ w, int rows, int cols,
-                                                                   const uint8_t *__restrict__ xpack,
-                                                                   float *__restrict__ y, int rpw) {
+template <int T, int NT, bool FEW, bool XF32>
+__global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJobs jobs, int cols,
+                                                                   const void *__restrict__ xin) {
     using S = Sl<T>;
     using G = Stream<T>;
     constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, RP = G::RP, LA = G::LA;
@@ -174,8 +198,15 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const ui
     uint8_t *ring = s_dyn + xreg + wv * G::WAVE_LDS;
     const uint32_t ring_a = lds_addr(ring);
 
-    // Rows of this wave and its stages.
-    const long r0 = static_cast<long>(blockIdx.x * NW + wv) * rpw;
+    // This wave's job, rows and stages.
+    const int gw = blockIdx.x * NW + wv;
+    int jb = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxJobs; ++k) jb = (k < jobs.n && gw >= jobs.j[k].wave0) ? k : jb;
+    const uint8_t *const w = jobs.j[jb].w;
+    float *const y = jobs.j[jb].y;
+    const int rows = jobs.j[jb].rows, rpw = jobs.j[jb].rpw;
+    const long r0 = gw < jobs.waves ? static_cast<long>(gw - jobs.j[jb].wave0) * rpw : rows;
     const long r1 = r0 + rpw < rows ? r0 + rpw : rows;
     const long U0 = r0 * nu, U1 = r1 * nu;
     const int nst = r0 < rows ? static_cast<int>((U1 - U0 + SU - 1) / SU) : 0;
@@ -212,13 +243,29 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const ui
         const uint8_t *src = grid_table_src<T>();
         for (int p = wv; p < TB / 1024; p += NW) dma16(src + p * 1024, lane * 16, lds_addr(s_grid) + p * 1024);
     }
-    for (int p = wv; p < xreg / 1024; p += NW) {
-        const int o = p * 1024 + lane * 16;  // LDS image byte of this lane's chunk
-        const int t = o / xi.bytes;
-        const int src = t < NT ? xi.src_of(o - t * xi.bytes, cols) : -1;
-        dma16(xpack, static_cast<uint32_t>(src >= 0 ? t * xb + src : 0), lds_addr(s_dyn) + p * 1024);
+    if constexpr (!XF32) {
+        for (int p = wv; p < xreg / 1024; p += NW) {
+            const int o = p * 1024 + lane * 16;  // LDS image byte of this lane's chunk
+            const int t = o / xi.bytes;
+            const int src = t < NT ? xi.src_of(o - t * xi.bytes, cols) : -1;
+            dma16(xin, static_cast<uint32_t>(src >= 0 ? t * xb + src : 0), lds_addr(s_dyn) + p * 1024);
+        }
     }
     if (nst > 0) issue_to(end_piece(0) + LA);
+    if constexpr (XF32) {
+        // fp32 activations: quantize each 32-group here, straight into the LDS image (the weight stream is
+        // already requested, so this overlaps its first round trip).
+        const float *x = static_cast<const float *>(xin);
+        for (int i = threadIdx.x; i < NT * xi.ng; i += blockDim.x) {
+            const int t = i / xi.ng, g = i - t * xi.ng;
+            const QGroup qg = quantize_group(x + static_cast<size_t>(t) * cols + 32 * g);
+            uint8_t *img = s_dyn + t * xi.bytes;
+            *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 0)) = u32x4{qg.q[0], qg.q[1], qg.q[2], qg.q[3]};
+            *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 1)) = u32x4{qg.q[4], qg.q[5], qg.q[6], qg.q[7]};
+            reinterpret_cast<float *>(img + xi.xq_bytes)[g] = qg.d;
+            reinterpret_cast<uint32_t *>(img + xi.xq_bytes + 4 * xi.ng)[g] = qg.half_sums();
+        }
+    }
     Tabs tb{};
     if constexpr (TabSpec<T>::n8 > 0) tb.grid8 = reinterpret_cast<const uint2 *>(s_grid);
     if constexpr (TabSpec<T>::n4 > 0) tb.grid4 = reinterpret_cast<const uint32_t *>(s_grid);
@@ -247,8 +294,12 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const ui
     long carry_row = -1;   // row whose earlier part is in carry[] (segmented-scan path)
     float carry[NT];
     float acc[3][NT];      // rows row_a, row_a+1, row_a+2 (FEW path: a stage touches at most three rows)
+    unsigned long long best[NT];  // argmax key of this wave's finished rows (wave-uniform)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) carry[t] = acc[0][t] = acc[1][t] = acc[2][t] = 0.0f;
+    for (int t = 0; t < NT; ++t) {
+        carry[t] = acc[0][t] = acc[1][t] = acc[2][t] = 0.0f;
+        best[t] = 0ull;
+    }
 
     for (int s = 0; s < nst; ++s) {
         issue_to(end_piece(s) + LA);
@@ -331,7 +382,9 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const ui
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         const float tot = wave_sum(acc[k][t]);
-                        if (lane == 0) y[static_cast<size_t>(t) * rows + row_a + k] = tot;
+                        if (y != nullptr && lane == 0) y[static_cast<size_t>(t) * rows + row_a + k] = tot;
+                        const unsigned long long key = argmax_key(tot, row_a + k);
+                        best[t] = key > best[t] ? key : best[t];
                     }
                 }
             }
@@ -371,9 +424,22 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const ui
             for (int t = 0; t < NT; ++t) v[t] += carry[t];
         }
         const long ub = ua + nval;
-        if (seg_end && (static_cast<long>(rr) + 1) * nu <= ub) {
+        const bool row_done = seg_end && (static_cast<long>(rr) + 1) * nu <= ub;
+        if (row_done && y != nullptr) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) y[static_cast<size_t>(t) * rows + rr] = v[t];
+        }
+        if (jobs.amax != nullptr) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                unsigned long long key = row_done ? argmax_key(v[t], rr) : 0ull;
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) {
+                    const unsigned long long o = __shfl_xor(key, off, 64);
+                    key = o > key ? o : key;
+                }
+                best[t] = key > best[t] ? key : best[t];
+            }
         }
         // The stage's last row continues into the next stage unless it ends here.
         const int lv = nval * LPU - 1;
@@ -395,7 +461,34 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const ui
         }
         asm volatile("" ::: "memory");  // this stage's LDS reads stay ahead of the next DMA into its slot
     }
+    if (jobs.amax != nullptr && lane == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) jobs.amax[static_cast<size_t>(t) * jobs.waves + gw] = best[t];
+    }
     wait_vm<0>();  // no DMA may still be writing this wave's ring when it exits
+}
+
+// Final argmax over the per-wave keys: one workgroup per token; INT32_MAX when no value qualifies.
+static __global__ __launch_bounds__(256) void argmax_keys_kernel(const unsigned long long *__restrict__ keys, int n,
+                                                          int32_t *__restrict__ out) {
+    __shared__ unsigned long long red[4];
+    unsigned long long k = 0ull;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const unsigned long long v = keys[static_cast<size_t>(blockIdx.x) * n + i];
+        k = v > k ? v : k;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_xor(k, off, 64);
+        k = o > k ? o : k;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < static_cast<int>(blockDim.x >> 6); ++i) k = red[i] > k ? red[i] : k;
+        k = red[0] > k ? red[0] : k;
+        out[blockIdx.x] = k == 0ull ? 0x7FFFFFFF : static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(k));
+    }
 }
 
 // ---- test hooks (same decoders as the matvec) -----------------------------------------------------------
@@ -494,59 +587,135 @@ inline size_t static_lds_bytes(const void *kernel) {
     return a.sharedSizeBytes;
 }
 
+// Launch geometry of one grouped matvec: rows per wave so that the waves the chip holds at this LDS
+// footprint (160 KB per CU, at most 32 waves per CU) cover all rows of all jobs once.
+struct Geometry {
+    size_t lds;  // dynamic LDS bytes
+    int rpw;
+    bool few;
+};
 template <int T, int N>
-int launch_stream(const uint8_t *w, int rows, int cols, const uint8_t *xp, float *yo, hipStream_t s) {
+Geometry geometry(long total_rows, int cols) {
     using G = Stream<T>;
-    const bool few = 2 * ((cols / 32) / Sl<T>::UG) >= G::SU;
-    static const int max_dyn_f = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true>));
-    static const int max_dyn_s = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false>));
-    const int max_dyn = few ? max_dyn_f : max_dyn_s;
+    static const size_t lds_static =
+        static_lds_bytes(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, false>));
+    Geometry g;
     const int xreg = (N * XImage(cols).bytes + 1023) & ~1023;
-    const size_t lds = static_cast<size_t>(xreg) + static_cast<size_t>(G::NW) * G::WAVE_LDS;
-    if (lds > static_cast<size_t>(max_dyn)) return static_cast<int>(hipErrorInvalidConfiguration);
-    static const size_t lds_static = static_lds_bytes(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true>));
-    const size_t lds_wg = lds + lds_static;
-    // Waves the chip holds at this LDS footprint (160 KB per CU, at most 32 waves per CU), then rows per wave
-    // so the grid fills them.
-    long wg_per_cu = static_cast<long>((160 * 1024) / lds_wg);
+    g.lds = static_cast<size_t>(xreg) + static_cast<size_t>(G::NW) * G::WAVE_LDS;
+    long wg_per_cu = static_cast<long>((160 * 1024) / (g.lds + lds_static));
     if (wg_per_cu > 32 / G::NW) wg_per_cu = 32 / G::NW;
     if (wg_per_cu < 1) wg_per_cu = 1;
     const long target = 256 * wg_per_cu * G::NW;
-    const int rpw = static_cast<int>((rows + target - 1) / target);
-    const long waves = (rows + rpw - 1) / rpw;
-    const dim3 grid(static_cast<unsigned>((waves + G::NW - 1) / G::NW)), block(64 * G::NW);
-    if (few)
-        qmv_stream_kernel<T, N, true><<<grid, block, lds, s>>>(w, rows, cols, xp, yo, rpw);
+    g.rpw = static_cast<int>((total_rows + target - 1) / target);
+    g.few = 2 * ((cols / 32) / Sl<T>::UG) >= G::SU;
+    return g;
+}
+
+// Rows per wave for a launch of n jobs (total rows) with N tokens.
+template <int T>
+int rows_per_wave(long total_rows, int cols, int n_tok) {
+    switch (n_tok) {
+        case 1: return geometry<T, 1>(total_rows, cols).rpw;
+        case 2: return geometry<T, 2>(total_rows, cols).rpw;
+        case 3: return geometry<T, 3>(total_rows, cols).rpw;
+        case 4: return geometry<T, 4>(total_rows, cols).rpw;
+        case 5: return geometry<T, 5>(total_rows, cols).rpw;
+        case 6: return geometry<T, 6>(total_rows, cols).rpw;
+        case 7: return geometry<T, 7>(total_rows, cols).rpw;
+        default: return geometry<T, 8>(total_rows, cols).rpw;
+    }
+}
+
+// Fills rpw / wave0 / waves of `jobs` (w, y, rows, n set by the caller); returns the wave count.
+inline long plan_jobs(QJobs &jobs, int rpw) {
+    long waves = 0;
+    for (int k = 0; k < jobs.n; ++k) {
+        jobs.j[k].rpw = rpw;
+        jobs.j[k].wave0 = static_cast<int>(waves);
+        waves += (jobs.j[k].rows + rpw - 1) / rpw;
+    }
+    jobs.waves = static_cast<int>(waves);
+    return waves;
+}
+
+template <int T, int N, bool XF32>
+int launch_stream(const QJobs &jobs, int cols, const void *xp, hipStream_t s) {
+    using G = Stream<T>;
+    static const int max_dyn_f = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, XF32>));
+    static const int max_dyn_s = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false, XF32>));
+    const Geometry g = geometry<T, N>(1, cols);
+    if (g.lds > static_cast<size_t>(g.few ? max_dyn_f : max_dyn_s)) return static_cast<int>(hipErrorInvalidConfiguration);
+    const dim3 grid(static_cast<unsigned>((jobs.waves + G::NW - 1) / G::NW)), block(64 * G::NW);
+    if (g.few)
+        qmv_stream_kernel<T, N, true, XF32><<<grid, block, g.lds, s>>>(jobs, cols, xp);
     else
-        qmv_stream_kernel<T, N, false><<<grid, block, lds, s>>>(w, rows, cols, xp, yo, rpw);
+        qmv_stream_kernel<T, N, false, XF32><<<grid, block, g.lds, s>>>(jobs, cols, xp);
     return hip_status(hipGetLastError());
 }
 
+// Tokens per launch: as many (<= 8) as the activation image budget holds.
+inline int token_chunk(int cols) {
+    const int chunk = VQ_X_LDS_MAX / XImage(cols).bytes;
+    return chunk > 8 ? 8 : chunk < 1 ? 1 : chunk;
+}
+
+// Waves of a single-job launch (the argmax key count per token).
 template <int T>
-int launch_quant(const uint8_t *w, int rows, int cols, long rb, const uint8_t *xpack, int ntok, float *y,
-                 hipStream_t s) {
-    (void)rb;
-    const int xb = vq_xpack_stride(cols);
-    int chunk = VQ_X_LDS_MAX / XImage(cols).bytes;
-    chunk = chunk > 8 ? 8 : chunk < 1 ? 1 : chunk;
+long argmax_waves(int rows, int cols, int ntok) {
+    const int m = ntok < token_chunk(cols) ? ntok : token_chunk(cols);
+    const int rpw = rows_per_wave<T>(rows, cols, m);
+    return (rows + rpw - 1) / rpw;
+}
+
+// y_j = W_j x for the n jobs (same type and cols), x fp32 (quantized in-kernel) or packed. With `amax`
+// ([ntok][argmax_waves] keys, single job), also amax_out[t] = argmax_r y[t][r].
+template <int T>
+int launch_quant_jobs(int n, const uint8_t *const *w, const int *rows, float *const *y, int cols, const void *x,
+                      bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s) {
+    if (n < 1 || n > kMaxJobs || (amax && n != 1)) return static_cast<int>(hipErrorInvalidValue);
+    const size_t tok_bytes = x_f32 ? static_cast<size_t>(cols) * 4 : static_cast<size_t>(vq_xpack_stride(cols));
+    const int chunk = token_chunk(cols);
+    long total = 0;
+    for (int k = 0; k < n; ++k) total += rows[k];
+    const int rpw = rows_per_wave<T>(total, cols, ntok < chunk ? ntok : chunk);
+    long kw = 0;
     for (int c = 0; c < ntok; c += chunk) {
         const int m = ntok - c < chunk ? ntok - c : chunk;
-        const uint8_t *xp = xpack + static_cast<size_t>(c) * xb;
-        float *yo = y + static_cast<size_t>(c) * rows;
-        int st = 0;
-        switch (m) {
-            case 1: st = launch_stream<T, 1>(w, rows, cols, xp, yo, s); break;
-            case 2: st = launch_stream<T, 2>(w, rows, cols, xp, yo, s); break;
-            case 3: st = launch_stream<T, 3>(w, rows, cols, xp, yo, s); break;
-            case 4: st = launch_stream<T, 4>(w, rows, cols, xp, yo, s); break;
-            case 5: st = launch_stream<T, 5>(w, rows, cols, xp, yo, s); break;
-            case 6: st = launch_stream<T, 6>(w, rows, cols, xp, yo, s); break;
-            case 7: st = launch_stream<T, 7>(w, rows, cols, xp, yo, s); break;
-            default: st = launch_stream<T, 8>(w, rows, cols, xp, yo, s); break;
+        QJobs jobs{};
+        jobs.n = n;
+        for (int k = 0; k < n; ++k) {
+            jobs.j[k].w = w[k];
+            jobs.j[k].y = y[k] ? y[k] + static_cast<size_t>(c) * rows[k] : nullptr;
+            jobs.j[k].rows = rows[k];
         }
+        kw = plan_jobs(jobs, rpw);
+        jobs.amax = amax ? amax + static_cast<size_t>(c) * kw : nullptr;
+        const void *xp = static_cast<const uint8_t *>(x) + static_cast<size_t>(c) * tok_bytes;
+        int st = 0;
+#define VQ_CASE(N)                                                                  \
+    case N:                                                                         \
+        st = x_f32 ? launch_stream<T, N, true>(jobs, cols, xp, s)                   \
+                   : launch_stream<T, N, false>(jobs, cols, xp, s);                 \
+        break;
+        switch (m) {
+            VQ_CASE(1) VQ_CASE(2) VQ_CASE(3) VQ_CASE(4) VQ_CASE(5) VQ_CASE(6) VQ_CASE(7)
+            default: VQ_CASE(8)
+        }
+#undef VQ_CASE
         if (st) return st;
     }
+    if (amax) {
+        argmax_keys_kernel<<<ntok, 256, 0, s>>>(amax, static_cast<int>(kw), amax_out);
+        return hip_status(hipGetLastError());
+    }
     return 0;
+}
+
+template <int T>
+int launch_quant(const uint8_t *w, int rows, int cols, long rb, const void *x, bool x_f32, int ntok, float *y,
+                 hipStream_t s) {
+    (void)rb;
+    return launch_quant_jobs<T>(1, &w, &rows, &y, cols, x, x_f32, ntok, nullptr, nullptr, s);
 }
 
 template <int T>
@@ -570,7 +739,10 @@ int launch_dequant(const uint8_t *w, int rows, int cols, long rb, float *out, hi
 
 // Explicit instantiation of one type's entry points (used by the per-type translation units).
 #define VQ_INSTANTIATE(T)                                                                                       \
-    template int vq::launch_quant<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t); \
+    template int vq::launch_quant<T>(const uint8_t *, int, int, long, const void *, bool, int, float *, hipStream_t); \
+    template int vq::launch_quant_jobs<T>(int, const uint8_t *const *, const int *, float *const *, int, const void *, \
+                                          bool, int, unsigned long long *, int32_t *, hipStream_t);                 \
+    template long vq::argmax_waves<T>(int, int, int);                                                                \
     template int vq::launch_partials<T>(const uint8_t *, int, int, long, const uint8_t *, int, int32_t *,          \
                                         hipStream_t);                                                            \
     template int vq::launch_dequant<T>(const uint8_t *, int, int, long, float *, hipStream_t);

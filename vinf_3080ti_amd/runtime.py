@@ -85,7 +85,6 @@ class Runtime:
                 _lib.check(self._lib.vq_set_iq3s_grid(grid), "vq_set_iq3s_grid")
         self.tensors: dict[str, _Tensor] = {}
         self.buffers: dict[str, _Buffer] = {}
-        self._ws = torch.empty(0, dtype=torch.uint8, device=self.device)
         self._argmax_out = torch.empty(MAX_ARGMAX_ROWS, dtype=torch.int32, device=self.device)
         self.gemm_min_rows = 0
 
@@ -113,11 +112,6 @@ class Runtime:
         if b.data.numel() < min_n:
             raise ValueError(f"device buffer {name} has {b.data.numel()} floats, need {min_n}")
         return b.data
-
-    def _workspace(self, nbytes: int) -> torch.Tensor:
-        if self._ws.numel() < nbytes:
-            self._ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
-        return self._ws
 
     # ---- weights ----------------------------------------------------------------------------------
     def upload(self, name: str, data, type_id: int, cols: int, rows: int, resident: bool = True, group: int = -1) -> None:
@@ -151,6 +145,8 @@ class Runtime:
         nbytes = row_bytes * rows
         if data.numel() < nbytes + 16:
             raise ValueError(f"{name}: device tensor needs {nbytes + 16} bytes (16 bytes of tail padding)")
+        if data.data_ptr() % 16:
+            raise ValueError(f"{name}: device tensor must be 16-byte aligned")
         self.tensors[name] = _Tensor(data, int(type_id), int(rows), int(cols), row_bytes, nbytes)
 
     def free(self, name: str) -> None:
@@ -231,10 +227,7 @@ class Runtime:
         self._qmv_ptrs(t, xb.data_ptr(), yb.data_ptr(), ntok)
 
     def _qmv_ptrs(self, t: _Tensor, x_ptr: int, y_ptr: int, ntok: int) -> None:
-        ws_bytes = self._lib.vq_qmv_workspace_bytes(t.cols, ntok)
-        ws = self._workspace(ws_bytes)
-        st = self._lib.vq_qmv(t.type, t.data.data_ptr(), t.rows, t.cols, x_ptr, ntok, y_ptr, ws.data_ptr(),
-                              ws.numel(), self._stream())
+        st = self._lib.vq_qmv(t.type, t.data.data_ptr(), t.rows, t.cols, x_ptr, ntok, y_ptr, None, 0, self._stream())
         _lib.check(st, "qmv launch")
 
     def qmv_tensor(self, weight: str, x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
@@ -247,6 +240,8 @@ class Runtime:
         if x.shape[1] != t.cols or x.dtype != torch.float32 or x.device != self.device:
             raise ValueError(f"{weight}: x must be float32 [ntok, {t.cols}] on {self.device}")
         x = x.contiguous()
+        if x.data_ptr() % 16:  # the kernels read activations with 16-byte loads
+            x = x.clone()
         if y is None:
             y = torch.empty(ntok, t.rows, dtype=torch.float32, device=self.device)
         self._qmv_ptrs(t, x.data_ptr(), y.data_ptr(), ntok)
