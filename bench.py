@@ -3,8 +3,9 @@
 Headline workload: a qwen35-27B-shaped decode-step weight sweep, batch 1 — 64
 layers (48 gated-delta SSM + 16 gated-attention) with a UD-Q3_K_XL-like quant mix and the Q6_K LM head with
 on-device argmax, 13.44 GiB of synthetic seeded raw GGUF blocks resident in HBM. One step = one sweep:
-every weight matrix of the step read once: per distinct input one vq_pack_x, one vq_qmv_group launch per
-run of same-type matrices sharing it (<= 4), and the fused vq_lmhead_argmax for the LM head.
+every weight matrix of the step read once: one grouped launch per run of same-type matrices sharing an
+input (<= 4; vq_qmv_group_f32 quantizing in-kernel, or vq_pack_x + vq_qmv_group for the 17408-wide FFN
+down input), and the fused vq_lmhead_argmax for the LM head.
 `value` = algorithmic bytes of the step / step time (GB/s); `ms_per_step` = ms per sweep.
 
 Also reported: per-quant-type matvec throughput at 5120x17408 (configs[0..2] shapes, rotating over weight
@@ -66,7 +67,20 @@ def sweep_plan():
 
 TYPE_NAMES = {Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_0: "Q8_0", IQ4_XS: "IQ4_XS",
               IQ3_S: "IQ3_S", IQ2_XXS: "IQ2_XXS"}
+FUSED_QUANT_MAX_COLS = 8192  # narrower inputs are quantized inside the matvec (vq_qmv_group_f32)
 PER_TYPE = [Q4_K, Q3_K, IQ4_XS, IQ3_S, IQ2_XXS, Q6_K]
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary (FETCH_SIZE +
+    WRITE_SIZE, each scaled by the same counter's reading for a plain device copy), or None."""
+    f = ROOT / "profiles" / "qmv_q3k_gateup_2x17408x5120_pmc.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1].strip())
+    return None
 
 
 def log(*a):
@@ -115,6 +129,15 @@ class Hip:
         st = self.lib.vq_qmv_group(ty, n, (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws]),
                                    (ctypes.c_int * n)(*rows), (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]),
                                    cols, xp.data_ptr(), ntok, self.s())
+        assert st == 0, st
+
+    def group_f32(self, ty, ws, rows, ys, cols, x, ntok):
+        import ctypes
+
+        n = len(ws)
+        st = self.lib.vq_qmv_group_f32(ty, n, (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws]),
+                                       (ctypes.c_int * n)(*rows), (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]),
+                                       cols, x.data_ptr(), ntok, self.s())
         assert st == 0, st
 
     def lmhead(self, ty, w, rows, cols, x, ntok, out, ws):
@@ -198,14 +221,16 @@ class Sweep:
                 self.ops.append(("head", i))
                 i += 1
                 continue
-            self.ops.append(("pack", cols))
+            packed = cols > FUSED_QUANT_MAX_COLS
+            if packed:
+                self.ops.append(("pack", cols))
             j = i
             while j < len(self.plan) and self.plan[j][4] == key:
                 k = j
                 while (k < len(self.plan) and k - j < 4 and self.plan[k][4] == key and self.plan[k][1] == ty
                        and self.plan[k][3] == cols):
                     k += 1
-                self.ops.append(("group", list(range(j, k))))
+                self.ops.append(("group", list(range(j, k)), packed))
                 j = k
                 if j < len(self.plan):
                     ty, cols = self.plan[j][1], self.plan[j][3]
@@ -224,7 +249,11 @@ class Sweep:
                 idx = op[1]
                 _, ty, _, cols, _ = self.plan[idx[0]]
                 rows = [self.plan[i][2] for i in idx]
-                hip.group(ty, [self.w[i] for i in idx], rows, [self.ys[r] for r in rows], cols, self.xp, ntok)
+                ys = [self.ys[r] for r in rows]
+                if op[2]:
+                    hip.group(ty, [self.w[i] for i in idx], rows, ys, cols, self.xp, ntok)
+                else:
+                    hip.group_f32(ty, [self.w[i] for i in idx], rows, ys, cols, self.x, ntok)
             else:
                 _, ty, rows, cols, _ = self.plan[op[1]]
                 hip.lmhead(ty, self.w[op[1]], rows, cols, self.x, ntok, self.ids, self.head_ws)
@@ -306,6 +335,8 @@ def main() -> None:
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-per-type", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the dominant launch (plus a 256 MiB device copy that calibrates PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (weights shard by rows; see "
@@ -320,6 +351,25 @@ def main() -> None:
     # Roofline of the dominant kernel: the FFN gate+up launch (2 x Q3_K 17408x5120, 64 launches per step).
     log("roofline: grouped Q3_K 2 x 17408x5120 matvec")
     dom = bench_matvec(torch, hip, Q3_K, 17408, 5120, args.ntok, iters=100, group=2)
+    traffic = profiled_traffic()
+    roofline = {
+        "bound": "hbm",
+        "kernel": f"qmv_stream_kernel<Q3_K,{args.ntok}> gate+up group 2x17408x5120",
+        "achieved": round(dom["GBps"], 2),
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(dom["frac"], 4),
+        "avg_us": round(dom["us"], 3),
+        "traffic": traffic,
+    }
+    if args.roofline_only:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)  # PMC calibration: 256 MiB read + 256 MiB written per copy
+        torch.cuda.synchronize()
+        print(json.dumps({"roofline": roofline, "bytes_per_launch": dom["bytes"]}), flush=True)
+        return
     per_type = {}
     if not args.no_per_type:
         for ty in PER_TYPE:
@@ -387,16 +437,7 @@ def main() -> None:
             "frac_of_hbm_peak": round(value / HBM_PEAK_GBPS, 4),
             "wall_s": round(wall, 3),
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": f"qmv_stream_kernel<Q3_K,{args.ntok}> gate+up group 2x17408x5120",
-            "achieved": round(dom["GBps"], 2),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(dom["frac"], 4),
-            "avg_us": round(dom["us"], 3),
-            "traffic": None,
-        },
+        "roofline": roofline,
         "cpu_baseline": None if cpu is None else {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()},
         "per_type": per_type,
     }

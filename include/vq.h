@@ -109,6 +109,11 @@ int vq_qmv_packed(int type, const uint8_t *w, int rows, int cols, const void *xp
 int vq_qmv_group(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
                  const void *xpack, int ntok, void *stream);
 
+/* vq_qmv_group on fp32 activations, quantized inside the matvec by every workgroup (no separate quantizer
+ * launch; best for narrow inputs, cols <= 8192). Same numerics as vq_pack_x + vq_qmv_group. */
+int vq_qmv_group_f32(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                     const float *x, int ntok, void *stream);
+
 /* Workspace bytes vq_lmhead_argmax needs for this matrix and ntok (0 for invalid arguments). */
 size_t vq_lmhead_argmax_workspace_bytes(int type, int rows, int cols, int ntok);
 

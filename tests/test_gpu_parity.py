@@ -147,7 +147,7 @@ def test_qmv_matches_oracle(env, oracle_mod, ty, ntok):
     "ty,rows,cols",
     [(T.Q4_K, 5120, 17408), (T.Q3_K, 5120, 17408), (T.Q6_K, 5120, 17408), (T.IQ4_XS, 5120, 17408),
      (T.IQ3_S, 5120, 17408), (T.IQ2_XXS, 5120, 17408), (T.Q3_K, 17408, 5120), (T.Q5_K, 10240, 5120),
-     (T.Q8_0, 48, 5120), (T.Q4_K, 4096, 4096)],
+     (T.Q8_0, 48, 5120), (T.Q4_K, 4096, 4096), (T.Q6_K, 5120, 6144), (T.Q6_K, 1024, 5120)],
     ids=lambda v: v.name if isinstance(v, T) else str(v))
 def test_qmv_baseline_shapes(env, oracle_mod, ty, rows, cols):
     torch, lib = env
@@ -201,20 +201,23 @@ def _pack(torch, lib, x: np.ndarray, ntok: int, cols: int):
                                                (T.Q5_K, [300, 77, 9, 128], 5120), (T.IQ2_XXS, [130, 3], 1024)],
                          ids=lambda v: v.name if isinstance(v, T) else str(v))
 @pytest.mark.parametrize("ntok", [1, 3, 9])
-def test_qmv_group_matches_oracle(env, oracle_mod, ty, rows_list, cols, ntok):
-    """One grouped launch over matrices sharing packed activations == each matrix on its own."""
+@pytest.mark.parametrize("f32", [False, True], ids=["packed", "f32"])
+def test_qmv_group_matches_oracle(env, oracle_mod, ty, rows_list, cols, ntok, f32):
+    """One grouped launch over matrices sharing the activations (packed, or fp32 quantized in-kernel) ==
+    each matrix on its own."""
     torch, lib = env
     rng = np.random.default_rng(sum(rows_list) + ntok)
     ws = [synth.baseline_rows(ty, r, cols, rng) for r in rows_list]
     x = rng.standard_normal((ntok, cols)).astype(np.float32)
-    xp = _pack(torch, lib, x, ntok, cols)
+    xp = dev(torch, x) if f32 else _pack(torch, lib, x, ntok, cols)
     wd = [wdev(torch, w) for w in ws]
     ys = [torch.full((ntok, r), np.nan, dtype=torch.float32, device="cuda") for r in rows_list]
     n = len(rows_list)
     wa = (ctypes.c_void_p * n)(*[P(t) for t in wd])
     ra = (ctypes.c_int * n)(*rows_list)
     ya = (ctypes.c_void_p * n)(*[P(t) for t in ys])
-    assert lib.vq_qmv_group(int(ty), n, wa, ra, ya, cols, P(xp), ntok, None) == 0
+    fn = lib.vq_qmv_group_f32 if f32 else lib.vq_qmv_group
+    assert fn(int(ty), n, wa, ra, ya, cols, P(xp), ntok, None) == 0
     torch.cuda.synchronize()
     for w, r, y in zip(ws, rows_list, ys):
         ref = oracle_mod.qmv(int(ty), w, r, cols, x, ntok)

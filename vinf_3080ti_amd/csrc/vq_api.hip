@@ -313,8 +313,8 @@ int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int n
     });
 }
 
-int vq_qmv_group(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
-                 const void *xpack, int ntok, void *stream) {
+static int qmv_group_any(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                         const void *x, bool x_f32, int ntok, void *stream) {
     if (n < 1 || n > VQ_MAX_GROUP || !w || !rows || !y) return VQ_ERR_ARG;
     if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;
     for (int k = 0; k < n; ++k) {
@@ -322,12 +322,22 @@ int vq_qmv_group(int type, int n, const uint8_t *const *w, const int *rows, floa
         if (st) return st;
         if (!w[k] || !y[k] || misaligned16(w[k])) return VQ_ERR_ARG;
     }
-    if (!xpack || misaligned16(xpack)) return VQ_ERR_ARG;
+    if (!x || misaligned16(x)) return VQ_ERR_ARG;
     if (ntok < 1) return VQ_ERR_SHAPE;
     hipStream_t s = static_cast<hipStream_t>(stream);
     return dispatch_quant(type, [&](auto tc) {
-        return vq::launch_quant_jobs<decltype(tc)::value>(n, w, rows, y, cols, xpack, false, ntok, nullptr, nullptr, s);
+        return vq::launch_quant_jobs<decltype(tc)::value>(n, w, rows, y, cols, x, x_f32, ntok, nullptr, nullptr, s);
     });
+}
+
+int vq_qmv_group(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                 const void *xpack, int ntok, void *stream) {
+    return qmv_group_any(type, n, w, rows, y, cols, xpack, false, ntok, stream);
+}
+
+int vq_qmv_group_f32(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                     const float *x, int ntok, void *stream) {
+    return qmv_group_any(type, n, w, rows, y, cols, x, true, ntok, stream);
 }
 
 size_t vq_lmhead_argmax_workspace_bytes(int type, int rows, int cols, int ntok) {

@@ -140,6 +140,9 @@ __device__ __forceinline__ const uint8_t *grid_table_src() {
 // One launch covers up to kMaxJobs matrices of the same type and width that share the activations (a
 // layer's gate/up, q/k/v, ...). Job j owns the grid's waves [wave0, wave0 + ceil(rows/rpw)).
 constexpr int kMaxJobs = 4;
+// Row accumulators per lane on the fast path: a stage of SU units touches at most kRowSlots rows when
+// rows have at least SU/(kRowSlots-1) units.
+constexpr int kRowSlots = 5;
 struct QJob {
     const uint8_t *w;
     float *y;  // [NT][rows], or null (argmax only)
@@ -293,11 +296,14 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
     int col_a = 0;         // its unit index within that row
     long carry_row = -1;   // row whose earlier part is in carry[] (segmented-scan path)
     float carry[NT];
-    float acc[3][NT];      // rows row_a, row_a+1, row_a+2 (FEW path: a stage touches at most three rows)
+    constexpr int NS = kRowSlots;
+    float acc[NS][NT];     // rows row_a .. row_a+NS-1 (FEW path: a stage touches at most NS rows)
     unsigned long long best[NT];  // argmax key of this wave's finished rows (wave-uniform)
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        carry[t] = acc[0][t] = acc[1][t] = acc[2][t] = 0.0f;
+        carry[t] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NS; ++k) acc[k][t] = 0.0f;
         best[t] = 0ull;
     }
 
@@ -367,17 +373,15 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
 
 #endif
         if constexpr (FEW) {
-            // Rows have at least SU/2 units, so this lane's unit is in row row_a + q with q <= 2. Rows that end
-            // in this stage are summed over the wave and written; the others shift down.
+            // Rows have at least SU/(NS-1) units, so this lane's unit is in row row_a + q with q < NS. Rows that
+            // end in this stage are summed over the wave and written; the others shift down.
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                acc[0][t] += q == 0 ? v[t] : 0.0f;
-                acc[1][t] += q == 1 ? v[t] : 0.0f;
-                acc[2][t] += q == 2 ? v[t] : 0.0f;
-            }
-            const int done = (col_a + nval) / nu;  // rows completed by this stage (0..2)
+            for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
+                for (int k = 0; k < NS; ++k) acc[k][t] += q == k ? v[t] : 0.0f;
+            const int done = (col_a + nval) / nu;  // rows completed by this stage (0..NS-1)
+#pragma unroll
+            for (int k = 0; k < NS - 1; ++k) {
                 if (k < done) {
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
@@ -388,19 +392,17 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
                     }
                 }
             }
-            if (done == 1) {
+            if (done > 0) {
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    acc[0][t] = acc[1][t];
-                    acc[1][t] = acc[2][t];
-                    acc[2][t] = 0.0f;
-                }
-            } else if (done == 2) {
+                for (int k = 0; k < NS; ++k)
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    acc[0][t] = acc[2][t];
-                    acc[1][t] = acc[2][t] = 0.0f;
-                }
+                    for (int t = 0; t < NT; ++t) {
+                        float nv = 0.0f;
+#pragma unroll
+                        for (int d = 1; d < NS; ++d)
+                            if (k + d < NS) nv = done == d ? acc[k + d][t] : nv;
+                        acc[k][t] = nv;
+                    }
             }
             row_a += done;
             col_a += nval - done * nu;
@@ -607,7 +609,7 @@ Geometry geometry(long total_rows, int cols) {
     if (wg_per_cu < 1) wg_per_cu = 1;
     const long target = 256 * wg_per_cu * G::NW;
     g.rpw = static_cast<int>((total_rows + target - 1) / target);
-    g.few = 2 * ((cols / 32) / Sl<T>::UG) >= G::SU;
+    g.few = (kRowSlots - 1) * ((cols / 32) / Sl<T>::UG) >= G::SU;
     return g;
 }
 
