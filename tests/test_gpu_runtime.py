@@ -124,3 +124,48 @@ def test_ntok_above_eight_chunks_like_reference(rt, oracle_mod):
     got = np.array(rt.read_floats("cy"), np.float32).reshape(ntok, rows)
     assert rel_l2(got, oracle_mod.qmv(int(T.IQ3_S), raw, rows, cols, x, ntok)) <= 1e-5
     rt.free("c")
+
+
+def test_wide_inputs_pack_through_the_runtime_workspace(rt, oracle_mod):
+    """cols > 8192 (FFN down) takes the pack + packed-matvec path with the runtime's own workspace."""
+    rows, cols, ntok = 40, 17408, 3
+    raw = synth.baseline_rows(T.Q4_K, rows, cols, 8)
+    x = np.random.default_rng(8).standard_normal((ntok, cols)).astype(np.float32)
+    rt.upload_raw("wide", raw.tobytes(), T.Q4_K, cols, rows)
+    rt.alloc("wx", cols * ntok)
+    rt.alloc("wy", rows * ntok)
+    rt.write_floats("wx", x.reshape(-1).tolist())
+    rt.qmv("wide", "wx", "wy", ntok)
+    got = np.array(rt.read_floats("wy"), np.float32).reshape(ntok, rows)
+    assert rel_l2(got, oracle_mod.qmv(int(T.Q4_K), raw, rows, cols, x, ntok)) <= 1e-5
+    rt.free("wide")
+
+
+@pytest.mark.parametrize("cols", [5120, 9216])
+def test_qmv_group_and_lmhead_argmax(rt, oracle_mod, cols):
+    ntok = 2
+    rng = np.random.default_rng(cols)
+    a = synth.baseline_rows(T.Q5_K, 96, cols, rng)
+    b = synth.baseline_rows(T.Q5_K, 40, cols, rng)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    rt.upload_raw("ga", a.tobytes(), T.Q5_K, cols, 96)
+    rt.upload_raw("gb", b.tobytes(), T.Q5_K, cols, 40)
+    rt.alloc("gx", cols * ntok)
+    rt.alloc("gya", 96 * ntok)
+    rt.alloc("gyb", 40 * ntok)
+    rt.write_floats("gx", x.reshape(-1).tolist())
+    rt.qmv_group(["ga", "gb"], "gx", ["gya", "gyb"], ntok)
+    ya = np.array(rt.read_floats("gya"), np.float32).reshape(ntok, 96)
+    yb = np.array(rt.read_floats("gyb"), np.float32).reshape(ntok, 40)
+    ra = oracle_mod.qmv(int(T.Q5_K), a, 96, cols, x, ntok)
+    rb = oracle_mod.qmv(int(T.Q5_K), b, 40, cols, x, ntok)
+    assert rel_l2(ya, ra) <= 1e-5 and rel_l2(yb, rb) <= 1e-5
+    ids = rt.lmhead_argmax("ga", "gx", ntok, logits="gya")
+    assert ids == rt.argmax_rows("gya", 96, ntok)
+    assert ids == rt.lmhead_argmax("ga", "gx", ntok)
+    with pytest.raises(ValueError):
+        rt.qmv_group(["ga", "t_missing_type"], "gx", ["gya"], ntok)
+    with pytest.raises(KeyError):
+        rt.qmv_group(["ga", "nope"], "gx", ["gya", "gyb"], ntok)
+    for n in ("ga", "gb"):
+        rt.free(n)

@@ -14,6 +14,8 @@ bad shapes/sizes/types, TypeError for an fp16 buffer where fp32 is needed, Runti
 """
 from __future__ import annotations
 
+import ctypes
+
 import struct
 from array import array
 from dataclasses import dataclass
@@ -86,11 +88,18 @@ class Runtime:
         self.tensors: dict[str, _Tensor] = {}
         self.buffers: dict[str, _Buffer] = {}
         self._argmax_out = torch.empty(MAX_ARGMAX_ROWS, dtype=torch.int32, device=self.device)
+        self._ws = torch.empty(0, dtype=torch.uint8, device=self.device)
         self.gemm_min_rows = 0
 
     # ---- helpers ----------------------------------------------------------------------------------
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _workspace(self, nbytes: int) -> torch.Tensor:
+        """Device scratch for packed activations / argmax keys, grown on demand and reused (stream-ordered)."""
+        if self._ws.numel() < nbytes:
+            self._ws = torch.empty(max(nbytes, 2 * self._ws.numel()), dtype=torch.uint8, device=self.device)
+        return self._ws
 
     def _tensor(self, name: str) -> _Tensor:
         t = self.tensors.get(name)
@@ -227,8 +236,62 @@ class Runtime:
         self._qmv_ptrs(t, xb.data_ptr(), yb.data_ptr(), ntok)
 
     def _qmv_ptrs(self, t: _Tensor, x_ptr: int, y_ptr: int, ntok: int) -> None:
-        st = self._lib.vq_qmv(t.type, t.data.data_ptr(), t.rows, t.cols, x_ptr, ntok, y_ptr, None, 0, self._stream())
+        if t.type in (0, 1):
+            ws = None
+            nws = 0
+        else:
+            nws = self._lib.vq_qmv_workspace_bytes(t.cols, ntok)
+            ws = self._workspace(nws).data_ptr() if nws else None
+        st = self._lib.vq_qmv(t.type, t.data.data_ptr(), t.rows, t.cols, x_ptr, ntok, y_ptr, ws, nws, self._stream())
         _lib.check(st, "qmv launch")
+
+    def qmv_group(self, weights: Sequence[str], x: str, ys: Sequence[str], ntok: int = 1) -> None:
+        """ys[k][t] = W_k x[t] for up to 4 weights of one quantized type and width that read the same input,
+        in one launch (a layer's gate/up or q/k/v). Same results as one qmv per weight; no counterpart in
+        the reference's per-op runtime, whose callers issue one qmv each (qwen_gpu.py:865-867)."""
+        if not 1 <= len(weights) <= 4 or len(weights) != len(ys):
+            raise ValueError("qmv_group takes 1 to 4 weights and as many outputs")
+        if ntok < 1:
+            raise ValueError("ntok must be positive")
+        ts = [self._tensor(w) for w in weights]
+        t0 = ts[0]
+        if any(t.type != t0.type or t.cols != t0.cols for t in ts) or t0.type in (0, 1):
+            raise ValueError("qmv_group weights must share one quantized type and cols")
+        _check_qmv_args(weights[0], t0.cols, ntok)
+        xb = self._f32_buffer(x, t0.cols * ntok)
+        yb = [self._f32_buffer(y, t.rows * ntok) for y, t in zip(ys, ts)]
+        n = len(ts)
+        wa = (ctypes.c_void_p * n)(*[t.data.data_ptr() for t in ts])
+        ra = (ctypes.c_int * n)(*[t.rows for t in ts])
+        ya = (ctypes.c_void_p * n)(*[b.data_ptr() for b in yb])
+        nws = self._lib.vq_qmv_workspace_bytes(t0.cols, ntok)
+        if nws == 0:
+            st = self._lib.vq_qmv_group_f32(t0.type, n, wa, ra, ya, t0.cols, xb.data_ptr(), ntok, self._stream())
+        else:
+            xp = self._workspace(nws)
+            _lib.check(self._lib.vq_pack_x(xb.data_ptr(), ntok, t0.cols, xp.data_ptr(), self._stream()), "pack_x")
+            st = self._lib.vq_qmv_group(t0.type, n, wa, ra, ya, t0.cols, xp.data_ptr(), ntok, self._stream())
+        _lib.check(st, "qmv_group launch")
+
+    def lmhead_argmax(self, weight: str, x: str, ntok: int = 1, logits: str | None = None) -> list[int]:
+        """argmax_r (W x[t])[r] for t < ntok, fused with the matvec (ties -> lowest row, NaN never wins);
+        the logits are written to `logits` only if given. Equals qmv + argmax_rows (qwen_runtime.cu:1860-1912,
+        2181-2197) without re-reading the logits, like the megakernel's fused argmax
+        (qwen_megakernel.cu:552-606,800-829)."""
+        if not 1 <= ntok <= MAX_ARGMAX_ROWS:
+            raise ValueError(f"ntok must be in [1, {MAX_ARGMAX_ROWS}]")
+        t = self._tensor(weight)
+        if t.type in (0, 1):
+            raise ValueError(f"{weight}: lmhead_argmax needs a quantized weight")
+        _check_qmv_args(weight, t.cols, ntok)
+        xb = self._f32_buffer(x, t.cols * ntok)
+        lp = self._f32_buffer(logits, t.rows * ntok).data_ptr() if logits is not None else None
+        nws = self._lib.vq_lmhead_argmax_workspace_bytes(t.type, t.rows, t.cols, ntok)
+        ws = self._workspace(nws)
+        st = self._lib.vq_lmhead_argmax(t.type, t.data.data_ptr(), t.rows, t.cols, xb.data_ptr(), ntok,
+                                        self._argmax_out.data_ptr(), lp, ws.data_ptr(), nws, self._stream())
+        _lib.check(st, "lmhead_argmax")
+        return [int(v) for v in self._argmax_out[:ntok].tolist()]
 
     def qmv_tensor(self, weight: str, x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
         """Tensor form: x [ntok, cols] fp32 on the device -> y [ntok, rows] fp32."""
