@@ -195,6 +195,37 @@ def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=
             "copies": copies}
 
 
+MFMA_INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, AMD-published (no sparsity)
+
+
+def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 << 20):
+    """Prefill contraction: M tokens x (rows x cols) weights on int8 MFMA, with the
+    activations packed beforehand; µs per launch, int8 TOPS (2*M*rows*cols ops) and utilisation of the MFMA
+    peak."""
+    from vinf_3080ti_amd import row_bytes
+
+    nbytes = rows * row_bytes(ty, cols)
+    copies = max(2, -(-min_rotation_bytes // nbytes))
+    ws = make_weights(torch, ty, rows, cols, 4321 + ty, copies)
+    x = torch.randn(M, cols, device="cuda")
+    xp = hip.xpack(cols, M)
+    hip.pack(x, M, cols, xp)
+    y = torch.empty(M, rows, device="cuda")
+
+    def launch(i):
+        st = hip.lib.vq_qgemm(ty, ws[i % copies].data_ptr(), rows, cols, xp.data_ptr(), M, y.data_ptr(), hip.s())
+        assert st == 0, st
+
+    for i in range(copies):
+        launch(i)
+    ms = time_kernel_loop(torch, launch, iters)
+    del ws
+    torch.cuda.empty_cache()
+    tops = 2.0 * M * rows * cols / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 3), "int8_tops": round(tops, 2), "mfma_util": round(tops / MFMA_INT8_PEAK_TOPS, 4),
+            "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 class Sweep:
     """All weights of one 27B decode step resident in HBM, plus the per-step launch sequence."""
 
@@ -379,6 +410,12 @@ def main() -> None:
         r = bench_matvec(torch, hip, Q4_K, 4096, 4096, args.ntok)
         per_type["Q4_K@4096x4096"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
 
+    prefill = {}
+    if not args.no_per_type:
+        for rows, cols in ((17408, 5120), (5120, 17408)):
+            log(f"prefill: 512 tokens x Q4_K {rows}x{cols}")
+            prefill[f"Q4_K_{rows}x{cols}_M512"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512)
+
     log("sweep: allocating 13.4 GiB of weights")
     sw = Sweep(torch, hip, args.ntok)
     for _ in range(args.warmup):
@@ -440,6 +477,7 @@ def main() -> None:
         "roofline": roofline,
         "cpu_baseline": None if cpu is None else {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()},
         "per_type": per_type,
+        "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
 

@@ -114,6 +114,13 @@ int vq_qmv_group(int type, int n, const uint8_t *const *w, const int *rows, floa
 int vq_qmv_group_f32(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
                      const float *x, int ntok, void *stream);
 
+/* Prefill contraction: y[t][r] = W[r] . x[t] for t < M (any M >= 1; meant for M >= 64) on int8 MFMA
+ * (v_mfma_i32_16x16x32_i8), activations packed by vq_pack_x. Same quantized numerics as the matvec (rel-L2
+ * <= 1e-5 against the reference CPU path), weights read once per 128 tokens. Replaces: the prefill branch of
+ * Runtime_qmv for ntok >= gemm_min_rows, vinf_qgemm_kernel (qwen_runtime.cu:1886-1902,663-739), which rounds
+ * x to fp16 instead of using the CPU path's int8 activations. */
+int vq_qgemm(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *stream);
+
 /* Workspace bytes vq_lmhead_argmax needs for this matrix and ntok (0 for invalid arguments). */
 size_t vq_lmhead_argmax_workspace_bytes(int type, int rows, int cols, int ntok);
 

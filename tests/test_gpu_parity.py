@@ -272,3 +272,43 @@ def test_lmhead_argmax_fused(env, oracle_mod, ty, rows, cols, ntok):
         finite = np.where(np.isnan(ref[t]), -np.inf, ref[t])
         assert finite[idx[t]] >= finite.max() - 1e-4 * np.abs(finite).max(), t
         assert rel_l2(np.nan_to_num(logits[t]), np.nan_to_num(ref[t])) <= REL_L2_TOL
+
+
+@pytest.mark.parametrize("ty", QUANT_TYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("rows,cols,M", [(130, 1024, 17), (64, 512, 200)])
+def test_qgemm_matches_oracle(env, oracle_mod, ty, rows, cols, M):
+    """The MFMA prefill contraction on the same int8 activations: within the fp32 bar of the CPU path,
+    for ragged row and token tiles."""
+    torch, lib = env
+    rng = np.random.default_rng(rows * M + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((M, cols)).astype(np.float32)
+    xp = _pack(torch, lib, x, M, cols)
+    y = torch.full((M, rows), np.nan, dtype=torch.float32, device="cuda")
+    wd = wdev(torch, w)
+    st = lib.vq_qgemm(int(ty), P(wd), rows, cols, P(xp), M, P(y), None)
+    assert st == 0, lib.vq_status_string(st)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x, M, threads=16)
+    assert np.isfinite(got).all()
+    for t in range(M):
+        assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, t)
+
+
+@pytest.mark.parametrize("ty,rows,cols", [(T.Q4_K, 17408, 5120), (T.Q4_K, 5120, 17408), (T.Q3_K, 1000, 5120)],
+                         ids=lambda v: v.name if isinstance(v, T) else str(v))
+def test_qgemm_prefill_shapes(env, oracle_mod, ty, rows, cols):
+    torch, lib = env
+    M = 512 if rows * cols <= 17408 * 5120 else 64
+    rng = np.random.default_rng(rows + cols)
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((M, cols)).astype(np.float32)
+    xp = _pack(torch, lib, x, M, cols)
+    y = torch.empty(M, rows, dtype=torch.float32, device="cuda")
+    assert lib.vq_qgemm(int(ty), P(wdev(torch, w)), rows, cols, P(xp), M, P(y), None) == 0
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    sel = np.r_[0:3, M - 2:M]  # the oracle runs a few tokens; the kernel's tiles are uniform
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x[sel], len(sel), threads=16)
+    assert rel_l2(got[sel], ref) <= REL_L2_TOL

@@ -340,6 +340,20 @@ int vq_qmv_group_f32(int type, int n, const uint8_t *const *w, const int *rows, 
     return qmv_group_any(type, n, w, rows, y, cols, x, true, ntok, stream);
 }
 
+int vq_qgemm(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *stream) {
+    int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;
+    if (!w || !xpack || !y || misaligned16(w) || misaligned16(xpack)) return VQ_ERR_ARG;
+    if (M < 1) return VQ_ERR_SHAPE;
+    const long rb = row_bytes_of(type, cols);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t *xp = static_cast<const uint8_t *>(xpack);
+    return dispatch_quant(type, [&](auto tc) {
+        return vq::launch_gemm<decltype(tc)::value>(w, rows, cols, rb, xp, M, y, s);
+    });
+}
+
 size_t vq_lmhead_argmax_workspace_bytes(int type, int rows, int cols, int ntok) {
     if (check_matrix(type, rows, cols) || type == VQ_F32 || type == VQ_F16 || ntok < 1) return 0;
     const long kw = dispatch_quant(type, [&](auto tc) {

@@ -16,6 +16,10 @@ int launch_quant_jobs(int n, const uint8_t *const *w, const int *rows, float *co
                       bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s);
 template <int T>
 long argmax_waves(int rows, int cols, int ntok);
+// Prefill contraction on int8 MFMA: y[t][r] = W[r] . x[t] for t < M, activations packed (vq_pack_x).
+template <int T>
+int launch_gemm(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int M, float *y,
+                hipStream_t s);
 template <int T>
 int launch_partials(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int ntok,
                     int32_t *part, hipStream_t s);

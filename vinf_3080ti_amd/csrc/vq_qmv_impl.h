@@ -745,6 +745,7 @@ int launch_dequant(const uint8_t *w, int rows, int cols, long rb, float *out, hi
     template int vq::launch_quant_jobs<T>(int, const uint8_t *const *, const int *, float *const *, int, const void *, \
                                           bool, int, unsigned long long *, int32_t *, hipStream_t);                 \
     template long vq::argmax_waves<T>(int, int, int);                                                                \
+    template int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \
     template int vq::launch_partials<T>(const uint8_t *, int, int, long, const uint8_t *, int, int32_t *,          \
                                         hipStream_t);                                                            \
     template int vq::launch_dequant<T>(const uint8_t *, int, int, long, float *, hipStream_t);

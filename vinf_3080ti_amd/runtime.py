@@ -236,6 +236,15 @@ class Runtime:
         self._qmv_ptrs(t, xb.data_ptr(), yb.data_ptr(), ntok)
 
     def _qmv_ptrs(self, t: _Tensor, x_ptr: int, y_ptr: int, ntok: int) -> None:
+        if t.type not in (0, 1) and self.gemm_min_rows > 0 and ntok >= self.gemm_min_rows:
+            # Prompt pass: the MFMA contraction (the prefill branch of Runtime_qmv, qwen_runtime.cu:1886-1902).
+            nws = self._lib.vq_xpack_bytes(t.cols, ntok)
+            xp = self._workspace(nws)
+            _lib.check(self._lib.vq_pack_x(x_ptr, ntok, t.cols, xp.data_ptr(), self._stream()), "pack_x")
+            st = self._lib.vq_qgemm(t.type, t.data.data_ptr(), t.rows, t.cols, xp.data_ptr(), ntok, y_ptr,
+                                    self._stream())
+            _lib.check(st, "qgemm launch")
+            return
         if t.type in (0, 1):
             ws = None
             nws = 0
@@ -339,7 +348,7 @@ class Runtime:
         return [int(v) for v in self._argmax_out[:ntok].tolist()]
 
     def set_gemm_min_rows(self, n: int) -> None:
-        """Prompt passes with ntok >= n take the prefill GEMM (0 = never) (qwen_runtime.cu:2324-2330)."""
+        """qmv calls with ntok >= n take the MFMA prefill contraction (0 = never) (qwen_runtime.cu:2324-2330)."""
         if n < 0:
             raise ValueError("gemm_min_rows must be >= 0")
         self.gemm_min_rows = int(n)
