@@ -226,13 +226,57 @@ def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 <
             "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
 
 
+def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20):
+    """the qwen35 SwiGLU MLP block's three matvecs (gate/up Q3_K 17408x5120, down
+    Q6_K 5120x17408) at batch ntok, weights rotating beyond the MALL. Small batches (>= 6 tokens) take the
+    int8-MFMA path through vq_qmv with its workspace; smaller ones one pack + grouped gate/up + down launch."""
+    from vinf_3080ti_amd import row_bytes
+
+    H, F = 5120, 17408
+    per_set = 2 * F * row_bytes(Q3_K, H) + H * row_bytes(Q6_K, F)
+    copies = max(2, -(-min_rotation_bytes // per_set))
+    sets = [(make_weights(torch, Q3_K, F, H, 11 + 3 * c)[0], make_weights(torch, Q3_K, F, H, 12 + 3 * c)[0],
+             make_weights(torch, Q6_K, H, F, 13 + 3 * c)[0]) for c in range(copies)]
+    x = torch.randn(ntok, H, device="cuda")
+    h = torch.randn(ntok, F, device="cuda")
+    g, u, d = (torch.empty(ntok, F, device="cuda"), torch.empty(ntok, F, device="cuda"),
+               torch.empty(ntok, H, device="cuda"))
+    lib = hip.lib
+    mfma = ntok >= 6
+    nws = max(lib.vq_qmv_workspace_bytes_for(Q3_K, F, H, ntok), lib.vq_qmv_workspace_bytes_for(Q6_K, H, F, ntok))
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
+    xp, hp = hip.xpack(H, ntok), hip.xpack(F, ntok)
+
+    def launch(i):
+        wg, wu, wd = sets[i % copies]
+        if mfma:
+            for w, rows, cols, xi, yo in ((wg, F, H, x, g), (wu, F, H, x, u), (wd, H, F, h, d)):
+                st = lib.vq_qmv(Q3_K if w is not wd else Q6_K, w.data_ptr(), rows, cols, xi.data_ptr(), ntok,
+                                yo.data_ptr(), ws.data_ptr(), nws, hip.s())
+                assert st == 0, st
+        else:
+            hip.pack(x, ntok, H, xp)
+            hip.group(Q3_K, [wg, wu], [F, F], [g, u], H, xp, ntok)
+            hip.pack(h, ntok, F, hp)
+            hip.group(Q6_K, [wd], [H], [d], F, hp, ntok)
+
+    for i in range(copies):
+        launch(i)
+    ms = time_kernel_loop(torch, launch, iters)
+    b = 2 * alg_bytes(Q3_K, F, H, ntok) + alg_bytes(Q6_K, H, F, ntok)
+    del sets
+    torch.cuda.empty_cache()
+    return {"us": round(ms * 1e3, 2), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
+            "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "path": "mfma" if mfma else "stream"}
+
+
 class Sweep:
     """All weights of one 27B decode step resident in HBM, plus the per-step launch sequence."""
 
-    def __init__(self, torch, hip, ntok):
+    def __init__(self, torch, hip, ntok, weights=None):
         self.torch, self.hip, self.ntok = torch, hip, ntok
         self.plan = sweep_plan()
-        self.w = [make_weights(torch, ty, rows, cols, 1 + i)[0] for i, (_, ty, rows, cols, _) in enumerate(self.plan)]
+        self.w = weights or [make_weights(torch, ty, rows, cols, 1 + i)[0] for i, (_, ty, rows, cols, _) in enumerate(self.plan)]
         self.bytes = sum(alg_bytes(ty, r, c, ntok) for _, ty, r, c, _ in self.plan)
         self.weight_bytes = sum(w.numel() - 256 for w in self.w)
         maxc = max(p[3] for p in self.plan)
@@ -288,6 +332,33 @@ class Sweep:
             else:
                 _, ty, rows, cols, _ = self.plan[op[1]]
                 hip.lmhead(ty, self.w[op[1]], rows, cols, self.x, ntok, self.ids, self.head_ws)
+
+
+def time_sweep(torch, sw, steps, warmup, use_graph=True):
+    """ms per step of a Sweep (hipGraph-captured unless use_graph is False)."""
+    for _ in range(warmup):
+        sw.step()
+    torch.cuda.synchronize()
+    graph = None
+    if use_graph:
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                sw.step()
+        torch.cuda.synchronize()
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        graph.replay() if graph else sw.step()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps, graph is not None
 
 
 def cpu_baseline(budget_s=12.0):
@@ -410,8 +481,11 @@ def main() -> None:
         r = bench_matvec(torch, hip, Q4_K, 4096, 4096, args.ntok)
         per_type["Q4_K@4096x4096"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
 
-    prefill = {}
+    prefill, mlp = {}, {}
     if not args.no_per_type:
+        for n in (1, 4, 8):
+            log(f"SwiGLU MLP block, batch {n}")
+            mlp[f"batch{n}"] = bench_mlp(torch, hip, n)
         for rows, cols in ((17408, 5120), (5120, 17408)):
             log(f"prefill: 512 tokens x Q4_K {rows}x{cols}")
             prefill[f"Q4_K_{rows}x{cols}_M512"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512)
@@ -446,6 +520,15 @@ def main() -> None:
     ms = start.elapsed_time(stop) / args.steps
     value = sw.bytes / (ms * 1e-3) / 1e9
 
+    sweep4 = None
+    if not args.no_per_type and args.ntok == 1:
+        log("sweep at batch 4 (same resident weights)")
+        sw4 = Sweep(torch, hip, 4, weights=sw.w)
+        ms4, _ = time_sweep(torch, sw4, max(5, args.steps // 3), args.warmup, use_graph=not args.no_graph)
+        sweep4 = {"ms_per_step": round(ms4, 4), "GBps": round(sw4.bytes / (ms4 * 1e-3) / 1e9, 2),
+                  "frac": round(sw4.bytes / (ms4 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        del sw4
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline: reference CPU path on a bounded sample")
@@ -478,6 +561,8 @@ def main() -> None:
         "cpu_baseline": None if cpu is None else {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()},
         "per_type": per_type,
         "prefill": prefill,
+        "mlp_block": mlp,
+        "sweep_batch4": sweep4,
     }
     print(json.dumps(out), flush=True)
 

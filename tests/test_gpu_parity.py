@@ -58,10 +58,13 @@ def pack_ref(q: np.ndarray, d: np.ndarray, stride: int) -> np.ndarray:
     return out.reshape(-1)
 
 
-def gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok):
+def gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok, fast=False):
+    """vq_qmv with the minimal workspace (streaming matvec), or with vq_qmv_workspace_bytes_for (fast: the
+    MFMA small-batch path for 2..16 tokens)."""
     wd, xd = wdev(torch, w), dev(torch, x.astype(np.float32).reshape(ntok, cols))
     y = torch.empty(ntok, rows, dtype=torch.float32, device="cuda")
-    nws = lib.vq_qmv_workspace_bytes(cols, ntok)
+    nws = (lib.vq_qmv_workspace_bytes_for(int(ty), rows, cols, ntok) if fast
+           else lib.vq_qmv_workspace_bytes(cols, ntok))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
     st = lib.vq_qmv(int(ty), P(wd), rows, cols, P(xd), ntok, P(y), P(ws), nws, None)
     assert st == 0, lib.vq_status_string(st)
@@ -312,3 +315,33 @@ def test_qgemm_prefill_shapes(env, oracle_mod, ty, rows, cols):
     sel = np.r_[0:3, M - 2:M]  # the oracle runs a few tokens; the kernel's tiles are uniform
     ref = oracle_mod.qmv(int(ty), w, rows, cols, x[sel], len(sel), threads=16)
     assert rel_l2(got[sel], ref) <= REL_L2_TOL
+
+
+@pytest.mark.parametrize("ty", ALL_TYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("ntok", [6, 8, 11, 16])
+def test_qmv_mfma_small_batch_matches_oracle(env, oracle_mod, ty, ntok):
+    """The int8-MFMA small-batch matvec (6..16 tokens) on ragged 16-row blocks."""
+    torch, lib = env
+    rows, cols = 37, 2048 if ty not in (T.F32, T.F16) else 1024
+    rng = np.random.default_rng(7000 + 100 * ntok + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    got = gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok, fast=True)
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok)
+    for t in range(ntok):
+        assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, ntok, t)
+
+
+@pytest.mark.parametrize("ty,rows,cols", [(T.Q3_K, 17408, 5120), (T.Q4_K, 5120, 17408), (T.Q6_K, 5120, 6144),
+                                          (T.IQ2_XXS, 5120, 17408), (T.Q8_0, 48, 5120), (T.Q5_K, 1000, 5120)],
+                         ids=lambda v: v.name if isinstance(v, T) else str(v))
+def test_qmv_mfma_baseline_shapes(env, oracle_mod, ty, rows, cols):
+    """Split-K (several K ranges summed by the second kernel) at the sweep's shapes, batch 8 and 16."""
+    torch, lib = env
+    rng = np.random.default_rng(rows * 7 + cols + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    for ntok in (8, 16):
+        x = rng.standard_normal((ntok, cols)).astype(np.float32)
+        got = gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok, fast=True)
+        ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok, threads=16)
+        assert rel_l2(got, ref) <= REL_L2_TOL, (ty.name, ntok)

@@ -19,6 +19,7 @@
 #include "vq_common.h"
 #include "vq_qmv.h"
 #include "vq_quant.h"
+#include "vq_mfma_impl.h"
 #include "../../include/vq.h"
 
 namespace {
@@ -257,6 +258,18 @@ size_t vq_qmv_workspace_bytes(int cols, int ntok) {
     return cols > kFusedQuantMaxCols ? vq_xpack_bytes(cols, ntok) : 0;
 }
 
+// Small batches (6..16 tokens) take the MFMA matvec when the workspace holds the packed activations and the
+// split-K partial sums: from about 6 tokens on it beats the streaming kernel, whose per-token work is VALU
+// (measured on MI355X at 17408x5120 and 5120x17408).
+constexpr int kMfmaMinTok = 6;
+bool mfma_batch(int type, int ntok) { return type != VQ_F32 && type != VQ_F16 && ntok >= kMfmaMinTok && ntok <= 16; }
+
+size_t vq_qmv_workspace_bytes_for(int type, int rows, int cols, int ntok) {
+    if (check_matrix(type, rows, cols) || ntok < 1) return 0;
+    if (mfma_batch(type, ntok)) return align256(vq_xpack_bytes(cols, ntok)) + vq::mfma_part_bytes(rows, cols, ntok);
+    return (type == VQ_F32 || type == VQ_F16) ? 0 : vq_qmv_workspace_bytes(cols, ntok);
+}
+
 int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, float *xs, void *stream) {
     if (!x || !xq || !xd) return VQ_ERR_ARG;
     if (ntok < 1 || cols < 32 || cols % 32) return VQ_ERR_SHAPE;
@@ -301,6 +314,17 @@ int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int n
     if (type == VQ_F32) return launch_float<VQ_F32>(w, rows, cols, x, ntok, y, s);
     if (type == VQ_F16) return launch_float<VQ_F16>(w, rows, cols, x, ntok, y, s);
     const long rb = row_bytes_of(type, cols);
+    if (mfma_batch(type, ntok) && workspace && !misaligned16(workspace) &&
+        workspace_bytes >= vq_qmv_workspace_bytes_for(type, rows, cols, ntok)) {
+        const size_t xpb = align256(vq_xpack_bytes(cols, ntok));
+        st = vq_pack_x(x, ntok, cols, workspace, stream);
+        if (st) return st;
+        const uint8_t *xp = static_cast<const uint8_t *>(workspace);
+        float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + xpb);
+        return dispatch_quant(type, [&](auto tc) {
+            return vq::launch_mfma<decltype(tc)::value>(w, rows, cols, rb, xp, ntok, y, part, s);
+        });
+    }
     const size_t need = vq_qmv_workspace_bytes(cols, ntok);
     if (need > 0) {
         if (!workspace || workspace_bytes < need || misaligned16(workspace)) return VQ_ERR_WORKSPACE;

@@ -10,8 +10,9 @@
 // vinf_qgemm_kernel, qwen_runtime.cu:663-739, rounds x to fp16 instead, which the CPU contract does not
 // allow). Only the summation order differs from the matvec.
 //
-// Work split: a workgroup of 8 waves computes a 128-row x 128-token tile; wave w owns rows 32*(w % 4) ..
-// +32 (two 16-row MFMA blocks) and tokens 64*(w / 4) .. +64 (four 16-token blocks). The K loop walks 256
+// Work split: a workgroup of 4 waves computes a 64-row x 64-token tile; wave w owns rows 32*(w % 2) ..
+// +32 (two 16-row MFMA blocks) and tokens 32*(w / 2) .. +32 (two 16-token blocks). Workgroups that share
+// weight rows are adjacent in the grid (token tile = blockIdx.x), so the re-reads of a row block hit L2. The K loop walks 256
 // elements at a time: the raw weight slices and activation chunks of step k+1 are loaded into registers
 // while step k's MFMAs run, then decoded into LDS (signed int8 codes [row][k], float scales per row and
 // 16-element part; activation codes [token][k], group scales and half sums).
@@ -24,7 +25,7 @@
 
 namespace vq {
 
-constexpr int kGemmBM = 128, kGemmBN = 128, kGemmWaves = 8, kGemmKS = 256;
+constexpr int kGemmBM = 64, kGemmBN = 64, kGemmWaves = 4, kGemmKS = 256;
 constexpr int kGemmRowPad = kGemmKS + 8;  // LDS row stride of the code tiles (bytes)
 
 // Parts of one 32-group share one scale (and min): one K=32 MFMA per group. Otherwise the two 16-halves are
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(const uint8_t *_
     __shared__ uint4 ssm[TabSpec<T>::sm ? 256 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int r0 = blockIdx.x * kGemmBM, t0 = blockIdx.y * kGemmBN;
+    const int r0 = blockIdx.y * kGemmBM, t0 = blockIdx.x * kGemmBN;
     const int ng = cols >> 5, nu = ng / UG;
     const int xb = vq_xpack_stride(cols), xh_off = vq_xpack_h_offset(cols);
     const int nsteps = (cols + kGemmKS - 1) / kGemmKS;
@@ -139,15 +140,16 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(const uint8_t *_
         }
     };
 
-    float acc[2][4][4];
+    constexpr int TB = kGemmBN / 32;  // 16-token blocks per wave
+    float acc[2][TB][4];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < TB; ++b)
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[a][b][j] = 0.0f;
 
-    const int rw = 32 * (wv & 3), tw = 64 * (wv >> 2);  // this wave's row / token offsets in the tile
+    const int rw = 32 * (wv & 1), tw = 16 * TB * (wv >> 1);  // this wave's row / token offsets in the tile
     const int lr = lane & 15, lk = lane >> 4;          // MFMA operand row/col and K chunk of this lane
 
     if (TabSpec<T>::n8 > 0 || TabSpec<T>::n4 > 0) __syncthreads();
@@ -158,12 +160,12 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(const uint8_t *_
         if (k + 1 < nsteps) load_step(k + 1);  // in flight during this step's MFMAs
 #pragma unroll
         for (int gg = 0; gg < NG; ++gg) {
-            long a[2], b[4];
+            long a[2], b[TB];
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb)
                 a[rb] = *reinterpret_cast<const long *>(s_codes + (rw + 16 * rb + lr) * kGemmRowPad + 32 * gg + 8 * lk);
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb)
+            for (int tb = 0; tb < TB; ++tb)
                 b[tb] = *reinterpret_cast<const long *>(s_xq + (tw + 16 * tb + lr) * kGemmRowPad + 32 * gg + 8 * lk);
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(const uint8_t *_
                         mnr[h][j] = s_mn[rw + 16 * rb + 4 * lk + j][gg * 2 + h];
                     }
 #pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
+                for (int tb = 0; tb < TB; ++tb) {
                     const int tl = tw + 16 * tb + lr;
                     const float xd = s_xd[tl][gg];
                     if constexpr (kScalePer32<T>) {
@@ -214,7 +216,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(const uint8_t *_
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
+        for (int tb = 0; tb < TB; ++tb) {
             const int t = t0 + tw + 16 * tb + lr;
             if (t >= M) continue;
 #pragma unroll
@@ -227,7 +229,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(const uint8_t *_
 
 template <int T>
 int launch_gemm(const uint8_t *w, int rows, int cols, long rb, const uint8_t *xpack, int M, float *y, hipStream_t s) {
-    const dim3 grid((rows + kGemmBM - 1) / kGemmBM, (M + kGemmBN - 1) / kGemmBN), block(64 * kGemmWaves);
+    const dim3 grid((M + kGemmBN - 1) / kGemmBN, (rows + kGemmBM - 1) / kGemmBM), block(64 * kGemmWaves);
     qgemm_kernel<T><<<grid, block, 0, s>>>(w, rows, cols, rb, xpack, M, y);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : static_cast<int>(e);

@@ -20,6 +20,11 @@ long argmax_waves(int rows, int cols, int ntok);
 template <int T>
 int launch_gemm(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int M, float *y,
                 hipStream_t s);
+// Small-batch (2..16 tokens) matvec on int8 MFMA; `part` holds mfma_part_bytes(rows, cols, ntok) bytes (unused
+// when that is 0).
+template <int T>
+int launch_mfma(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int ntok, float *y,
+                float *part, hipStream_t s);
 template <int T>
 int launch_partials(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int ntok,
                     int32_t *part, hipStream_t s);

@@ -10,8 +10,6 @@
 
 namespace vq {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
 // Streaming geometry (compile-time; overridable for tuning builds).
 #ifndef VQ_X_LDS_MAX
 #define VQ_X_LDS_MAX (64 * 1024)  // bytes of activation records one launch keeps in LDS
@@ -746,6 +744,8 @@ int launch_dequant(const uint8_t *w, int rows, int cols, long rb, float *out, hi
                                           bool, int, unsigned long long *, int32_t *, hipStream_t);                 \
     template long vq::argmax_waves<T>(int, int, int);                                                                \
     template int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \
+    template int vq::launch_mfma<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, float *,       \
+                                    hipStream_t);                                                                \
     template int vq::launch_partials<T>(const uint8_t *, int, int, long, const uint8_t *, int, int32_t *,          \
                                         hipStream_t);                                                            \
     template int vq::launch_dequant<T>(const uint8_t *, int, int, long, float *, hipStream_t);

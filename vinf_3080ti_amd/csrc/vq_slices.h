@@ -24,6 +24,8 @@
 
 namespace vq {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 // Codebooks in global memory (device tables of the library).
 struct Grids {
     const uint2 *iq2xxs;     // 256 entries of 8 magnitudes

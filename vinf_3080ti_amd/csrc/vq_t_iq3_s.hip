@@ -1,6 +1,6 @@
 // vq_t_iq3_s.hip -- IQ3_S instantiation of the quantized matvec kernels (vq_qmv_impl.h).
 #include "vq_qmv_impl.h"
-#include "vq_gemm_impl.h"
+#include "vq_mfma_impl.h"
 
 VQ_INSTANTIATE(VQ_IQ3_S)
 

@@ -249,7 +249,7 @@ class Runtime:
             ws = None
             nws = 0
         else:
-            nws = self._lib.vq_qmv_workspace_bytes(t.cols, ntok)
+            nws = self._lib.vq_qmv_workspace_bytes_for(t.type, t.rows, t.cols, ntok)
             ws = self._workspace(nws).data_ptr() if nws else None
         st = self._lib.vq_qmv(t.type, t.data.data_ptr(), t.rows, t.cols, x_ptr, ntok, y_ptr, ws, nws, self._stream())
         _lib.check(st, "qmv launch")
