@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <unordered_map>
+
 #include "vq_qmv.h"
 #include "vq_quant.h"
 #include "vq_tables.h"
@@ -50,32 +53,31 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Finished row sums one wave keeps in LDS until its end: rows per wave * tokens <= kYSlots.
+constexpr int kYSlots = 256;
+
 // Per-type stage shape: LPU lanes decode one unit (each takes SPB/LPU of its slices), so a stage is the
-// 64/LPU consecutive units of the wave's stream; each wave streams through a ring of RP 1 KB pieces. Tuning
-// builds override with VQ_LPU / VQ_RING_KB.
+// SU = 64/LPU consecutive units of the wave's stream. LPU is chosen so that a stage spans about 2-7 KB: the
+// wave holds two stages of raw bytes in VGPRs (one landing, one in flight), so the stage size sets both the
+// bytes a wave keeps in flight and its VGPR cost. Tuning builds override with VQ_LPU / VQ_WAVES.
 template <int T>
 struct StageShape {
+    static constexpr int LPU_DEFAULT =
+        (T == VQ_Q8_0 || T == VQ_IQ4_NL || T == VQ_IQ2_XXS || T == VQ_IQ2_XS || T == VQ_IQ2_S) ? 1 : 2;
 #ifdef VQ_LPU
     static constexpr int LPU = VQ_LPU < Sl<T>::SPB ? VQ_LPU : Sl<T>::SPB;
 #else
-    // Two lanes per super-block for the K-quants with cheap decoders; one for the table-driven IQ types and
-    // Q6_K, whose per-slice decode dominates (measured on MI355X).
-    static constexpr int LPU = (T == VQ_Q2_K || T == VQ_Q3_K || T == VQ_Q4_K || T == VQ_Q5_K) ? 2 : 1;
+    static constexpr int LPU = LPU_DEFAULT;
 #endif
 #ifdef VQ_WAVES
     static constexpr int NW = VQ_WAVES;
 #else
-    static constexpr int NW = Sl<T>::UG == 1 ? 8 : 4;  // waves per workgroup
+    static constexpr int NW = 4;  // waves per workgroup
 #endif
-#ifdef VQ_RING_KB
-    static constexpr int RP = VQ_RING_KB;  // ring size in 1 KB pieces (power of two)
+#ifdef VQ_NBUF
+    static constexpr int NB = VQ_NBUF;
 #else
-    static constexpr int RP = 8;
-#endif
-#ifdef VQ_SLICE_BLOCKED
-    static constexpr bool BLOCKED = VQ_SLICE_BLOCKED;  // lane j takes slices j*SPB/LPU.. (else j, j+LPU, ..)
-#else
-    static constexpr bool BLOCKED = false;
+    static constexpr int NB = 1;
 #endif
 };
 
@@ -109,16 +111,18 @@ struct Stream {
     static constexpr int LPU = StageShape<T>::LPU;
     static constexpr int SPL = S::SPB / LPU;  // slices per lane
     static constexpr int SU = 64 / LPU;       // units per stage
-    static constexpr bool BLOCKED = StageShape<T>::BLOCKED;
-    // Most 1 KB pieces one stage's bytes touch (its units plus the aligned dword the decoders may read past
-    // the last unit), the ring size (at least two pieces more) and the pieces kept requested beyond the
-    // current stage.
-    static constexpr int PMAX = (SU * S::UB + 4 + 1023) / 1024 + 1;
-    static constexpr int RP = StageShape<T>::RP >= PMAX + 2 ? StageShape<T>::RP : 2 * StageShape<T>::RP;
+    static constexpr bool BLOCKED = false;    // lane j of a unit takes slices j, j+LPU, ...
+    // 16-byte chunks one stage's bytes can touch (its units plus the dword the decoders may read past the
+    // last unit, from an arbitrary 16-byte phase) and the dwordx4 loads per lane that cover them.
+    static constexpr int CMAX = (SU * S::UB + 4 + 15) / 16 + 1;
+    static constexpr int NL = (CMAX + 63) / 64;
     static constexpr int NW = StageShape<T>::NW;
-    static constexpr int LA = RP - PMAX;
-    static constexpr int WAVE_LDS = (RP + 1) * 1024;  // ring + mirror of its first piece
-    static_assert(S::SPB % LPU == 0 && (RP & (RP - 1)) == 0 && LA >= 1 && LA < 64, "ring geometry");
+    static constexpr int NB = StageShape<T>::NB;  // stages in flight while one is decoded (1 or 2)
+    // Per wave: the stage buffer, then the finished row sums ([NT][rpw] fp32, rpw * NT <= kYSlots). Row sums
+    // are written to y once, at the end: a vector store in the stage loop would leave stores and loads
+    // pending on the one vmcnt counter, and the compiler then waits for all loads, both buffers included.
+    static constexpr int WAVE_LDS = NL * 1024 + 4 * kYSlots;
+    static_assert(S::SPB % LPU == 0 && NL >= 1 && NL <= 16, "stage geometry");
 };
 
 template <int T>
@@ -166,23 +170,23 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, long r) {
 //
 // Wave g of the grid owns rows [g*rpw, (g+1)*rpw) -- a contiguous byte range, since rows are back to back
 // and each row is a whole number of units (32-element groups for Q8_0/IQ4_NL, 256-element super-blocks
-// otherwise). It streams that range through a private LDS ring of RP 1 KB pieces, keeping LA pieces past
-// the stage being decoded requested (a stage is SU = 64/LPU units). In a stage, the LPU lanes of unit i decode its slices with
-// the type's slice decoders (weights, activation records and IQ tables all read from LDS), so the block
-// header is decoded once per 256/LPU elements. A stage may hold the end of one row, whole rows and the
-// start of another: a segmented scan over the lanes (segments = rows) sums each row's part, segment ends
-// of finished rows write y, and the part of a row that continues into the next stage is carried.
+// otherwise). It walks that range in stages of SU = 64/LPU units. A stage's bytes (16-byte chunks
+// [c0, c1)) arrive in VGPRs by NL coalesced nontemporal dwordx4 loads per lane, two stages ahead: while
+// stage s is decoded, the loads of stages s+1 and s+2 are in flight. The landed chunks of stage s are
+// written to the wave's LDS stage buffer (lane order = byte order), and the LPU lanes of each unit decode
+// its slices with the type's slice decoders (weights, activation records and IQ tables all read from LDS),
+// so the block header is decoded once per 256/LPU elements. Rows that end in the stage are summed over the
+// wave and written.
 //
-// LDS: [grid table | activation image of the NT tokens | ring + mirror piece per wave]. At start-up each
-// wave requests its share of the table and of the activation image, then its first pieces, and waits until
-// only the lookahead pieces are outstanding: the activations and the first stage are in, the weight
-// stream is already moving.
+// LDS: [grid table | activation image of the NT tokens | one stage buffer per wave]. At start-up the waves
+// request their share of the table and of the activation image (DMA), then their first two stages, and
+// meet at one barrier once the activations are in.
 template <int T, int NT, bool FEW, bool XF32>
 __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJobs jobs, int cols,
                                                                    const void *__restrict__ xin) {
     using S = Sl<T>;
     using G = Stream<T>;
-    constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, RP = G::RP, LA = G::LA;
+    constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, NL = G::NL;
     constexpr int TB = grid_table_bytes<T>();
     extern __shared__ __attribute__((aligned(1024))) uint8_t s_dyn[];
     __shared__ __attribute__((aligned(1024))) uint8_t s_grid[TB > 0 ? TB : 16];
@@ -196,8 +200,8 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
     const int xb = vq_xpack_stride(cols);
     const XImage xi(cols);
     const int xreg = (NT * xi.bytes + 1023) & ~1023;
-    uint8_t *ring = s_dyn + xreg + wv * G::WAVE_LDS;
-    const uint32_t ring_a = lds_addr(ring);
+    uint8_t *const sbuf = s_dyn + xreg + wv * G::WAVE_LDS;
+    float *const ybuf = reinterpret_cast<float *>(sbuf + NL * 1024);
 
     // This wave's job, rows and stages.
     const int gw = blockIdx.x * NW + wv;
@@ -211,35 +215,30 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
     const long r1 = r0 + rpw < rows ? r0 + rpw : rows;
     const long U0 = r0 * nu, U1 = r1 * nu;
     const int nst = r0 < rows ? static_cast<int>((U1 - U0 + SU - 1) / SU) : 0;
-    // The wave's byte stream starts at the 16-byte boundary b0 below its first unit; piece k holds stream
-    // bytes [1024k, 1024k + 1024) in ring slot k % RP, and piece k = 0 (mod RP) also in the mirror slot RP, so a
-    // unit that starts in the last slot reads on contiguously. Pieces past the stream's end re-read its last
-    // chunk, which keeps the number of loads issued per piece constant.
-    const long b0 = (U0 * UB) & ~15L;
-    // Last chunk to load: the one holding the dword past the stream's last unit, but never one that ends
-    // beyond the matrix's 16 readable pad bytes (the decoders discard bytes past a block).
+    // Chunks of stage s: [c0, c1) with c0 the chunk of its first byte and c1 past the chunk holding the dword
+    // after its last unit -- but never past the chunk holding the matrix's last byte (the weight buffer has
+    // 16 readable pad bytes; decoders discard bytes past a block). Lanes past c1 re-read chunk c1 - 1 (the
+    // same addresses as a lane that does load it: no extra traffic), so every stage issues exactly NL loads.
     const long mend = static_cast<long>(rows) * nu * UB;
-    const long lastc = ((U1 * UB + 4) < mend ? (U1 * UB + 4) : mend) & ~15L;
-    const uint32_t last = static_cast<uint32_t>(U1 > U0 ? lastc - b0 : 0);
-    const uint8_t *wb = w + b0;
-    int issued = 0;
-    auto issue_to = [&](int target) {
-        for (; issued < target; ++issued) {
-            const uint32_t off = static_cast<uint32_t>(issued) * 1024 + lane * 16;
-            const uint32_t src = off < last ? off : last;
-            const uint32_t slot = issued & (RP - 1);
-            dma16(wb, src, ring_a + slot * 1024);
-            if (slot == 0) dma16(wb, src, ring_a + RP * 1024);
-        }
-    };
-    // Pieces stage s needs: all below its end piece.
-    auto end_piece = [&](int s) {
+    const u32x4 *const w16 = reinterpret_cast<const u32x4 *>(w);
+    auto chunk0 = [&](int s) { return ((U0 + static_cast<long>(s) * SU) * UB) >> 4; };
+    auto load_stage = [&](int s, u32x4 (&R)[NL]) {
         const long ua = U0 + static_cast<long>(s) * SU;
         const long ub = ua + SU < U1 ? ua + SU : U1;
-        return static_cast<int>((ub * UB + 4 - b0 + 1023) >> 10);
+        const long e = ub * UB + 4 < mend ? ub * UB + 4 : mend;
+        const long c0 = (ua * UB) >> 4, cl = ((e + 15) >> 4) - 1;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const long c = c0 + lane + 64 * i;
+            R[i] = __builtin_nontemporal_load(w16 + (c < cl ? c : cl));
+        }
+    };
+    auto store_stage = [&](const u32x4 (&R)[NL]) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) reinterpret_cast<u32x4 *>(sbuf)[lane + 64 * i] = R[i];
     };
 
-    // Start-up: table and activation pieces (striped over the waves), then the first D-1 stages.
+    // Start-up: table and activation pieces (striped over the waves), then the first two stages.
     if constexpr (TB > 0) {
         const uint8_t *src = grid_table_src<T>();
         for (int p = wv; p < TB / 1024; p += NW) dma16(src + p * 1024, lane * 16, lds_addr(s_grid) + p * 1024);
@@ -252,7 +251,13 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
             dma16(xin, static_cast<uint32_t>(src >= 0 ? t * xb + src : 0), lds_addr(s_dyn) + p * 1024);
         }
     }
-    if (nst > 0) issue_to(end_piece(0) + LA);
+    // Every wave issues exactly NL loads per buffer fill, whatever its stage count (stages past the last
+    // re-read the last one, from L2): the compiler's vmcnt bookkeeping then sees the same number of loads
+    // in flight on every path and waits for one buffer only.
+    const int slast = nst > 0 ? nst - 1 : 0;
+    u32x4 RA[NL], RB[G::NB == 2 ? NL : 1];
+    load_stage(0, RA);
+    if constexpr (G::NB == 2) load_stage(1 < slast ? 1 : slast, RB);
     if constexpr (XF32) {
         // fp32 activations: quantize each 32-group here, straight into the LDS image (the weight stream is
         // already requested, so this overlaps its first round trip).
@@ -278,10 +283,9 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
         for (int i = threadIdx.x; i < 256; i += blockDim.x) ssm[i] = sign_entry(i);
         tb.sm256 = ssm;
     }
-    if (nst > 0)
-        wait_vm<LA>();
-    else
-        wait_vm<0>();
+    // The DMAs were issued before this wave's stage loads, and loads retire in order: once at most the
+    // stage loads are outstanding, the table and activation pieces have landed.
+    if constexpr (TB > 0 || !XF32) wait_vm<G::NB * NL>();
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -305,13 +309,12 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
         best[t] = 0ull;
     }
 
-    for (int s = 0; s < nst; ++s) {
-        issue_to(end_piece(s) + LA);
-        wait_vm<LA>();  // every piece below end_piece(s) has landed
+    // Decode stage s from the stage buffer (its chunk c0 at sbuf) and fold it into the row sums.
+    auto run_stage = [&](int s) {
         const long ua = U0 + static_cast<long>(s) * SU;
         const int nval = static_cast<int>((U1 - ua < SU ? U1 - ua : SU));  // units in this stage
         const bool valid = ul < nval;
-        const uint8_t *up = ring + (((ua + (valid ? ul : 0)) * UB - b0) & (RP * 1024 - 1));
+        const uint8_t *up = sbuf + ((ua + (valid ? ul : 0)) * UB - (chunk0(s) << 4));
         // Row and column unit of this lane's unit: c = col_a + ul = q*nu + cu with q small.
         const int c = col_a + ul;
         int q = static_cast<int>(static_cast<float>(c) * inv_nu);
@@ -368,7 +371,6 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
                 }
             }
         }
-
 #endif
         if constexpr (FEW) {
             // Rows have at least SU/(NS-1) units, so this lane's unit is in row row_a + q with q < NS. Rows that
@@ -384,7 +386,7 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         const float tot = wave_sum(acc[k][t]);
-                        if (y != nullptr && lane == 0) y[static_cast<size_t>(t) * rows + row_a + k] = tot;
+                        if (lane == 0) ybuf[t * rpw + static_cast<int>(row_a + k - r0)] = tot;
                         const unsigned long long key = argmax_key(tot, row_a + k);
                         best[t] = key > best[t] ? key : best[t];
                     }
@@ -405,67 +407,99 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
             row_a += done;
             col_a += nval - done * nu;
         } else {
-        // Segmented inclusive scan over lanes; segments are rows (row ids are non-decreasing in lane order).
-        const int rr = valid ? static_cast<int>(row_a + q) : 0x7FFFFFFF;
+            // Segmented inclusive scan over lanes; segments are rows (row ids are non-decreasing in lane order).
+            const int rr = valid ? static_cast<int>(row_a + q) : 0x7FFFFFFF;
 #pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int rp = __shfl_up(rr, d, 64);
-            const bool m = lane >= d && rp == rr;
+            for (int d = 1; d < 64; d <<= 1) {
+                const int rp = __shfl_up(rr, d, 64);
+                const bool m = lane >= d && rp == rr;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const float vp = __shfl_up(v[t], d, 64);
-                v[t] += m ? vp : 0.0f;
-            }
-        }
-        const int rn = __shfl_down(rr, 1, 64);
-        const bool seg_end = valid && (lane == 63 || rn != rr);
-        if (rr == carry_row) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) v[t] += carry[t];
-        }
-        const long ub = ua + nval;
-        const bool row_done = seg_end && (static_cast<long>(rr) + 1) * nu <= ub;
-        if (row_done && y != nullptr) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) y[static_cast<size_t>(t) * rows + rr] = v[t];
-        }
-        if (jobs.amax != nullptr) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                unsigned long long key = row_done ? argmax_key(v[t], rr) : 0ull;
-#pragma unroll
-                for (int off = 32; off > 0; off >>= 1) {
-                    const unsigned long long o = __shfl_xor(key, off, 64);
-                    key = o > key ? o : key;
+                for (int t = 0; t < NT; ++t) {
+                    const float vp = __shfl_up(v[t], d, 64);
+                    v[t] += m ? vp : 0.0f;
                 }
-                best[t] = key > best[t] ? key : best[t];
+            }
+            const int rn = __shfl_down(rr, 1, 64);
+            const bool seg_end = valid && (lane == 63 || rn != rr);
+            if (rr == carry_row) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) v[t] += carry[t];
+            }
+            const long ub = ua + nval;
+            const bool row_done = seg_end && (static_cast<long>(rr) + 1) * nu <= ub;
+            if (row_done) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) ybuf[t * rpw + static_cast<int>(rr - r0)] = v[t];
+            }
+            if (jobs.amax != nullptr) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    unsigned long long key = row_done ? argmax_key(v[t], rr) : 0ull;
+#pragma unroll
+                    for (int off = 32; off > 0; off >>= 1) {
+                        const unsigned long long o = __shfl_xor(key, off, 64);
+                        key = o > key ? o : key;
+                    }
+                    best[t] = key > best[t] ? key : best[t];
+                }
+            }
+            // The stage's last row continues into the next stage unless it ends here.
+            const int lv = nval * LPU - 1;
+            const long last_row = __builtin_amdgcn_readlane(rr, lv);
+            if ((last_row + 1) * nu > ub) {
+                carry_row = last_row;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) carry[t] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[t]), lv));
+            } else {
+                carry_row = -1;
+            }
+            // Advance the stage origin by SU units.
+            col_a += SU;
+            if (col_a >= nu) {
+                const int adv = col_a / nu;
+                row_a += adv;
+                col_a -= adv * nu;
             }
         }
-        // The stage's last row continues into the next stage unless it ends here.
-        const int lv = nval * LPU - 1;
-        const long last_row = __builtin_amdgcn_readlane(rr, lv);
-        if ((last_row + 1) * nu > ub) {
-            carry_row = last_row;
+    };
+
+    // Two stages in flight: RA holds even stages, RB odd ones. Writing a buffer to LDS waits (compiler-
+    // inserted vmcnt) for its own loads only; the stage buffer is rewritten after the previous stage's LDS
+    // reads were issued, and a wave's LDS operations complete in order.
+    // (No exit from the middle of the pair: a path from there back through the latch would look, to the
+    // compiler, like RA's loads being the last ones issued.)
+    int s = 0;
+    if constexpr (G::NB == 1) {
+        // One stage in flight: stage s+1 loads while stage s is decoded.
+        for (; s + 1 < nst; ++s) {
+            store_stage(RA);
+            load_stage(s + 1, RA);
+            run_stage(s);
+        }
+    } else {
+    for (; s + 1 < nst; s += 2) {
+        store_stage(RA);
+        load_stage(s + 2 < slast ? s + 2 : slast, RA);
+        run_stage(s);
+        store_stage(RB);
+        load_stage(s + 3 < slast ? s + 3 : slast, RB);
+        run_stage(s + 1);
+    }
+    }
+    if (s < nst) {
+        store_stage(RA);
+        run_stage(s);
+    }
+    if (y != nullptr) {
+        const int nr = static_cast<int>(r1 - r0);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) carry[t] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[t]), lv));
-        } else {
-            carry_row = -1;
-        }
-        // Advance the stage origin by SU units.
-        col_a += SU;
-        if (col_a >= nu) {
-            const int adv = col_a / nu;
-            row_a += adv;
-            col_a -= adv * nu;
-        }
-        }
-        asm volatile("" ::: "memory");  // this stage's LDS reads stay ahead of the next DMA into its slot
+        for (int t = 0; t < NT; ++t)
+            for (int i = lane; i < nr; i += 64) y[static_cast<size_t>(t) * rows + r0 + i] = ybuf[t * rpw + i];
     }
     if (jobs.amax != nullptr && lane == 0) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) jobs.amax[static_cast<size_t>(t) * jobs.waves + gw] = best[t];
     }
-    wait_vm<0>();  // no DMA may still be writing this wave's ring when it exits
 }
 
 // Final argmax over the per-wave keys: one workgroup per token; INT32_MAX when no value qualifies.
@@ -594,20 +628,47 @@ struct Geometry {
     int rpw;
     bool few;
 };
+// Resident workgroups per CU of a qmv_stream_kernel instantiation at `lds` dynamic LDS bytes (VGPR, LDS and
+// wave limits, as the runtime computes them); 1 if the query fails.
+inline int resident_wgs(const void *kernel, int threads, size_t lds) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, lds) != hipSuccess || n < 1) {
+        (void)hipGetLastError();
+        return 1;
+    }
+    return n;
+}
 template <int T, int N>
 Geometry geometry(long total_rows, int cols) {
     using G = Stream<T>;
-    static const size_t lds_static =
-        static_lds_bytes(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, false>));
     Geometry g;
     const int xreg = (N * XImage(cols).bytes + 1023) & ~1023;
     g.lds = static_cast<size_t>(xreg) + static_cast<size_t>(G::NW) * G::WAVE_LDS;
-    long wg_per_cu = static_cast<long>((160 * 1024) / (g.lds + lds_static));
-    if (wg_per_cu > 32 / G::NW) wg_per_cu = 32 / G::NW;
-    if (wg_per_cu < 1) wg_per_cu = 1;
+    g.few = (kRowSlots - 1) * ((cols / 32) / Sl<T>::UG) >= G::SU;
+    // Both activation forms of the chosen row path: the grid must not depend on the form. Cached per
+    // (few, LDS bytes): the occupancy queries cost host time on every launch otherwise.
+    static std::mutex mu;
+    static std::unordered_map<long, int> cache;
+    const long key = static_cast<long>(g.lds) * 2 + (g.few ? 1 : 0);
+    long wg_per_cu;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        auto it = cache.find(key);
+        if (it == cache.end()) {
+            const void *ka = g.few ? reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, false>)
+                                   : reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false, false>);
+            const void *kb = g.few ? reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, true>)
+                                   : reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false, true>);
+            (void)raise_dynamic_lds(ka);
+            (void)raise_dynamic_lds(kb);
+            const int ra = resident_wgs(ka, 64 * G::NW, g.lds), rb = resident_wgs(kb, 64 * G::NW, g.lds);
+            it = cache.emplace(key, ra < rb ? ra : rb).first;
+        }
+        wg_per_cu = it->second;
+    }
     const long target = 256 * wg_per_cu * G::NW;
     g.rpw = static_cast<int>((total_rows + target - 1) / target);
-    g.few = (kRowSlots - 1) * ((cols / 32) / Sl<T>::UG) >= G::SU;
+    if (g.rpw > kYSlots / N) g.rpw = kYSlots / N;  // more than one round of waves for very tall launches
     return g;
 }
 
