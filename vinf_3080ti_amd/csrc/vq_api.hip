@@ -35,9 +35,13 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // ---- activation quantizer ------------------------------------------------------------------------------
-// One thread per (token, 32-group), quantize_group (vq_quant.h) per group; xs = d*sum(q).
+// Eight lanes per (token, 32-group): each lane loads one float4 of the group (coalesced), the group's amax
+// is reduced over the eight lanes, and each lane quantizes its four values with the same IEEE operations as
+// quantize_group (vq_quant.h): amax = max|v| (exact in any order), d = amax/127, id = 1/d (0 if d == 0),
+// q = rint(v*id). The integer sums of the two 16-element halves (lanes 0-3 and 4-7) are exact in any order.
 // Outputs go to (xq, xd, xs, xh) with per-token strides, so one kernel writes either the separate arrays of
-// vq_quantize_x or the packed activation record of vq_pack_x (layout: vq_xpack_h_offset / vq_xpack_stride in vq_common.h).
+// vq_quantize_x or the packed activation record of vq_pack_x (layout: vq_xpack_h_offset / vq_xpack_stride in
+// vq_common.h).
 struct XOut {
     int8_t *xq;
     float *xd, *xs;
@@ -47,16 +51,37 @@ struct XOut {
 
 __global__ __launch_bounds__(256) void quantize_x_kernel(const float *__restrict__ x, int ntok, int cols, XOut o) {
     const int ng = cols >> 5;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= ntok * ng) return;
-    const int t = i / ng, g = i - t * ng;
-    const vq::QGroup qg = vq::quantize_group(x + static_cast<size_t>(t) * cols + 32 * g);
-    uint4 *dst = reinterpret_cast<uint4 *>(o.xq + t * o.q_stride + 32 * g);
-    dst[0] = make_uint4(qg.q[0], qg.q[1], qg.q[2], qg.q[3]);
-    dst[1] = make_uint4(qg.q[4], qg.q[5], qg.q[6], qg.q[7]);
-    o.xd[t * o.d_stride + g] = qg.d;
-    if (o.xs) o.xs[t * o.d_stride + g] = qg.d * static_cast<float>(qg.hs0 + qg.hs1);
-    if (o.xh) o.xh[t * o.d_stride + g] = qg.half_sums();
+    const long grp = (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x) >> 3;
+    const int sub = threadIdx.x & 7;
+    const bool ok = grp < static_cast<long>(ntok) * ng;
+    const long gi = ok ? grp : 0;  // every lane takes part in the shuffles
+    const int t = static_cast<int>(gi / ng), g = static_cast<int>(gi - static_cast<long>(t) * ng);
+    const float4 f = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols + 32 * g)[sub];
+    float amax = 0.0f;
+    amax = fmaxf(amax, fabsf(f.x));
+    amax = fmaxf(amax, fabsf(f.y));
+    amax = fmaxf(amax, fabsf(f.z));
+    amax = fmaxf(amax, fabsf(f.w));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    const int q0 = static_cast<int>(__builtin_rintf(f.x * id)), q1 = static_cast<int>(__builtin_rintf(f.y * id));
+    const int q2 = static_cast<int>(__builtin_rintf(f.z * id)), q3 = static_cast<int>(__builtin_rintf(f.w * id));
+    const uint32_t packed = (static_cast<uint32_t>(q0) & 0xFFu) | ((static_cast<uint32_t>(q1) & 0xFFu) << 8) |
+                            ((static_cast<uint32_t>(q2) & 0xFFu) << 16) | (static_cast<uint32_t>(q3) << 24);
+    int hs = q0 + q1 + q2 + q3;
+    hs += __shfl_xor(hs, 1, 64);
+    hs += __shfl_xor(hs, 2, 64);           // lanes 0-3: half 0, lanes 4-7: half 1
+    const int hs1 = __shfl_xor(hs, 4, 64);  // lane 0: the other half
+    if (!ok) return;
+    reinterpret_cast<uint32_t *>(o.xq + t * o.q_stride + 32 * g)[sub] = packed;
+    if (sub == 0) {
+        o.xd[t * o.d_stride + g] = d;
+        if (o.xs) o.xs[t * o.d_stride + g] = d * static_cast<float>(hs + hs1);
+        if (o.xh) o.xh[t * o.d_stride + g] = (static_cast<uint32_t>(hs) & 0xFFFFu) | (static_cast<uint32_t>(hs1) << 16);
+    }
 }
 
 // ---- float weights (F32/F16): one wave per row, fp32 activations, no quantization (qwen_cpu.c:345-360) ---
@@ -273,7 +298,7 @@ size_t vq_qmv_workspace_bytes_for(int type, int rows, int cols, int ntok) {
 int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, float *xs, void *stream) {
     if (!x || !xq || !xd) return VQ_ERR_ARG;
     if (ntok < 1 || cols < 32 || cols % 32) return VQ_ERR_SHAPE;
-    const int n = ntok * (cols / 32);
+    const long n = 8L * ntok * (cols / 32);  // eight lanes per group
     const XOut o{xq, xd, xs, nullptr, cols, cols / 32};
     quantize_x_kernel<<<(n + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(x, ntok, cols, o);
     return hip_status(hipGetLastError());
@@ -282,7 +307,7 @@ int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, flo
 int vq_pack_x(const float *x, int ntok, int cols, void *xpack, void *stream) {
     if (!x || !xpack) return VQ_ERR_ARG;
     if (ntok < 1 || cols < 32 || cols % 32) return VQ_ERR_SHAPE;
-    const int n = ntok * (cols / 32);
+    const long n = 8L * ntok * (cols / 32);  // eight lanes per group
     const long stride = vq_xpack_stride(cols);
     char *base = static_cast<char *>(xpack);
     const XOut o{reinterpret_cast<int8_t *>(base), reinterpret_cast<float *>(base + cols), nullptr,

@@ -63,7 +63,7 @@ constexpr int kYSlots = 256;
 template <int T>
 struct StageShape {
     static constexpr int LPU_DEFAULT =
-        (T == VQ_Q8_0 || T == VQ_IQ4_NL || T == VQ_IQ2_XXS || T == VQ_IQ2_XS || T == VQ_IQ2_S) ? 1 : 2;
+        (T == VQ_Q8_0 || T == VQ_IQ4_NL || T == VQ_IQ2_XXS || T == VQ_IQ2_XS || T == VQ_IQ2_S || T == VQ_Q3_K) ? 1 : 2;
 #ifdef VQ_LPU
     static constexpr int LPU = VQ_LPU < Sl<T>::SPB ? VQ_LPU : Sl<T>::SPB;
 #else
@@ -243,7 +243,11 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
         const uint8_t *src = grid_table_src<T>();
         for (int p = wv; p < TB / 1024; p += NW) dma16(src + p * 1024, lane * 16, lds_addr(s_grid) + p * 1024);
     }
+#ifndef VQ_NOXIMG
     if constexpr (!XF32) {
+#else
+    if constexpr (false) {
+#endif
         for (int p = wv; p < xreg / 1024; p += NW) {
             const int o = p * 1024 + lane * 16;  // LDS image byte of this lane's chunk
             const int t = o / xi.bytes;
@@ -287,7 +291,9 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
     // stage loads are outstanding, the table and activation pieces have landed.
     if constexpr (TB > 0 || !XF32) wait_vm<G::NB * NL>();
     wait_lgkm0();
+#ifndef VQ_NOBAR
     __builtin_amdgcn_s_barrier();
+#endif
     asm volatile("" ::: "memory");
     if (nst == 0) return;
 
@@ -666,6 +672,9 @@ Geometry geometry(long total_rows, int cols) {
         }
         wg_per_cu = it->second;
     }
+#ifdef VQ_WGCAP
+    if (wg_per_cu > VQ_WGCAP) wg_per_cu = VQ_WGCAP;
+#endif
     const long target = 256 * wg_per_cu * G::NW;
     g.rpw = static_cast<int>((total_rows + target - 1) / target);
     if (g.rpw > kYSlots / N) g.rpw = kYSlots / N;  // more than one round of waves for very tall launches
