@@ -227,10 +227,13 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
         const long ub = ua + SU < U1 ? ua + SU : U1;
         const long e = ub * UB + 4 < mend ? ub * UB + 4 : mend;
         const long c0 = (ua * UB) >> 4, cl = ((e + 15) >> 4) - 1;
+        // Wave-uniform base and limit; per-lane 32-bit chunk offsets.
+        const u32x4 *const base = w16 + c0;
+        const int lim = __builtin_amdgcn_readfirstlane(static_cast<int>(cl - c0));
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-            const long c = c0 + lane + 64 * i;
-            R[i] = __builtin_nontemporal_load(w16 + (c < cl ? c : cl));
+            const unsigned c = static_cast<unsigned>(lane + 64 * i);
+            R[i] = __builtin_nontemporal_load(base + (c < static_cast<unsigned>(lim) ? c : static_cast<unsigned>(lim)));
         }
     };
     auto store_stage = [&](const u32x4 (&R)[NL]) {
@@ -347,6 +350,60 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
                 if constexpr (kNeedsX<T>) xhu[t][g] = reinterpret_cast<const int32_t *>(xt + 4 * xi.ng)[G0 + g];
             }
         }
+        if constexpr (kIntScales<T>()) {
+            // Integer scales: per (token, group) the exact int32 sum of S * scale (and X * min), then one
+            // conversion and fp32 multiply-add per group with the activation scale; the unit's fp32 multipliers
+            // (d, dmin) are applied once.
+            int gs[NT][S::UG], gm[NT][S::UG];
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int g = 0; g < S::UG; ++g) gs[t][g] = gm[t][g] = 0;
+            float dmul = 0.0f, dmn = 0.0f;
+#pragma unroll
+            for (int k = 0; k < G::SPL; ++k) {
+                const int ss = lj + LPU * k;
+                typename S::W wr;
+                S::load(up, ss, wr);
+                uint32_t cd[NP][4];
+                S::codes(wr, ss, tb, cd);
+                int isc[NP], imn[NP];
+                S::iscales(wr, ss, isc);
+                if constexpr (kHasMin<T>) S::imins(wr, ss, imn);
+                if (k == 0) {
+                    dmul = S::dmul(wr);
+                    if constexpr (kHasMin<T>) dmn = S::dmin(wr);
+                }
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    int pg, ph;
+                    S::part(ss, p, pg, ph);
+                    const int Gi = G0 + pg;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const uint8_t *xt = s_dyn + t * xi.bytes;
+                        const u32x4 xv4 = *reinterpret_cast<const u32x4 *>(xt + xi.code_off(Gi, ph));
+                        const int X = kNeedsX<T> ? static_cast<int>(static_cast<int16_t>(
+                                                       static_cast<uint32_t>(xhu[t][pg]) >> (16 * ph)))
+                                                 : 0;
+                        const int Sv = dot4(cd[p][3], xv4.w, dot4(cd[p][2], xv4.z, dot4(cd[p][1], xv4.y,
+                                            dot4(cd[p][0], xv4.x, -S::OFF * X))));
+                        gs[t][pg] += __mul24(Sv, isc[p]);
+                        if constexpr (kHasMin<T>) gm[t][pg] += __mul24(X, imn[p]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float a = 0.0f, m = 0.0f;
+#pragma unroll
+                for (int g = 0; g < S::UG; ++g) {
+                    a = fmaf(static_cast<float>(gs[t][g]), xdu[t][g], a);
+                    if constexpr (kHasMin<T>) m = fmaf(static_cast<float>(gm[t][g]), xdu[t][g], m);
+                }
+                v[t] = kHasMin<T> ? fmaf(a, dmul, -m * dmn) : a * dmul;
+            }
+        } else {
 #pragma unroll
         for (int k = 0; k < G::SPL; ++k) {
             const int ss = G::BLOCKED ? lj * G::SPL + k : lj + LPU * k;
@@ -376,6 +433,7 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
                     v[t] = fmaf(g, xdv, v[t]);
                 }
             }
+        }
         }
 #endif
         if constexpr (FEW) {

@@ -280,9 +280,14 @@ struct Sl<VQ_Q3_K> {
         const int j0 = 4 * (s >> 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t qs = w.qs.word(i), hm = w.hm.word(i) >> j0;
+            const uint32_t qs = w.qs.word(i), hm = w.hm.word(i);
 #pragma unroll
-            for (int p = 0; p < 4; ++p) c[p][i] = ((qs >> (2 * p)) & 0x03030303u) | (((hm >> p) & 0x01010101u) << 2);
+            for (int p = 0; p < 4; ++p) {
+                // hmask bit j0+p of each byte moved straight to bit 2 (one shift, one mask)
+                const int sh = j0 + p - 2;
+                const uint32_t hb = (sh >= 0 ? hm >> sh : hm << -sh) & 0x04040404u;
+                c[p][i] = ((qs >> (2 * p)) & 0x03030303u) | hb;
+            }
         }
     }
     static __device__ __forceinline__ void scales(const W &w, int s, float *sc, float *mn) {
@@ -304,6 +309,20 @@ struct Sl<VQ_Q3_K> {
         sc[2] = d * (ubyte1(v) - 32.0f);
         sc[3] = d * (ubyte3(v) - 32.0f);
         mn[0] = mn[1] = mn[2] = mn[3] = 0.0f;
+    }
+    // Integer form of the same scales: part p weighs d * isc[p].
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.sw.word(3)); }
+    static __device__ __forceinline__ void iscales(const W &w, int s, int (&isc)[NP]) {
+        const uint32_t sw0 = w.sw.word(0), sw1 = w.sw.word(1), sw2 = w.sw.word(2);
+        const int hh = s & 1, q2 = s >> 1;
+        const uint32_t lo4 = ((sw0 >> (8 * hh + 4 * q2)) & 0x000F000Fu) | (((sw1 >> (8 * hh + 4 * q2)) & 0x000F000Fu) << 8);
+        const uint32_t hb = sw2 >> (8 * hh + 4 * q2);
+        const uint32_t v = lo4 | ((hb & 0x00030003u) << 4) | ((((hb >> 2) & 0x00030003u) << 4) << 8);
+        isc[0] = static_cast<int>(v & 0xFFu) - 32;
+        isc[1] = static_cast<int>((v >> 16) & 0xFFu) - 32;
+        isc[2] = static_cast<int>((v >> 8) & 0xFFu) - 32;
+        isc[3] = static_cast<int>(v >> 24) - 32;
     }
 };
 
@@ -638,5 +657,13 @@ constexpr bool kHasMin = T == VQ_Q2_K || T == VQ_Q4_K || T == VQ_Q5_K;
 // Types whose integer partial needs X (offset codes).
 template <int T>
 constexpr bool kNeedsX = kHasMin<T> || T == VQ_Q3_K || T == VQ_Q6_K;
+// Slice decoders that also give their scales as integers (Sl<T>::iscales, with one fp32 multiplier per unit
+// Sl<T>::dmul, and for types with mins Sl<T>::imins / Sl<T>::dmin): the matvec then sums S * scale per group
+// in int32 and converts once per group.
+template <int T>
+constexpr bool kIntScales() {
+    if constexpr (requires { Sl<T>::kInt; }) return Sl<T>::kInt;
+    return false;
+}
 
 }  // namespace vq
