@@ -79,7 +79,7 @@ def test_host_side_argument_checks(lib):
     assert lib.vq_qmv_group(int(T.Q4_K), 2, arr, rws, arr, 100, fake, 1, None) == _lib.VQ_ERR_SHAPE
     assert lib.vq_lmhead_argmax_workspace_bytes(int(T.F16), 4, 256, 1) == 0
     nws = lib.vq_lmhead_argmax_workspace_bytes(int(T.Q6_K), 248320, 5120, 1)
-    assert nws >= 8 * 256  # one key per wave per token
+    assert nws >= 8 * 256  # one key per workgroup (one or more per CU) per token
     assert lib.vq_lmhead_argmax(int(T.Q6_K), fake, 248320, 5120, fake, 1, fake, None, fake, nws - 1,
                                 None) == _lib.VQ_ERR_WORKSPACE
     assert b"workspace" in lib.vq_status_string(_lib.VQ_ERR_WORKSPACE)

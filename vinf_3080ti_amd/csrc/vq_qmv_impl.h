@@ -11,6 +11,9 @@
 #include "vq_quant.h"
 #include "vq_tables.h"
 
+#ifdef VQ_TIMING
+extern "C" void *vq_debug_timing_buffer();
+#endif
 namespace vq {
 
 // Streaming geometry (compile-time; overridable for tuning builds).
@@ -53,13 +56,9 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// Finished row sums one wave keeps in LDS until its end: rows per wave * tokens <= kYSlots.
-constexpr int kYSlots = 256;
-
 // Per-type stage shape: LPU lanes decode one unit (each takes SPB/LPU of its slices), so a stage is the
-// SU = 64/LPU consecutive units of the wave's stream. LPU is chosen so that a stage spans about 2-7 KB: the
-// wave holds two stages of raw bytes in VGPRs (one landing, one in flight), so the stage size sets both the
-// bytes a wave keeps in flight and its VGPR cost. Tuning builds override with VQ_LPU / VQ_WAVES.
+// SU = 64/LPU consecutive units of a workgroup's byte range, about 2-7 KB: a wave holds one stage of raw
+// bytes in VGPRs while it decodes the previous one. Tuning builds override with VQ_LPU.
 template <int T>
 struct StageShape {
     static constexpr int LPU_DEFAULT =
@@ -69,22 +68,12 @@ struct StageShape {
 #else
     static constexpr int LPU = LPU_DEFAULT;
 #endif
-#ifdef VQ_WAVES
-    static constexpr int NW = VQ_WAVES;
-#else
-    static constexpr int NW = 4;  // waves per workgroup
-#endif
-#ifdef VQ_NBUF
-    static constexpr int NB = VQ_NBUF;
-#else
-    static constexpr int NB = 1;
-#endif
 };
 
 // LDS image of the activation records: per token, the int8 codes in blocks of 256 followed by XPAD bytes
 // of padding (so that the codes lanes of neighbouring units read fall in different LDS banks), then the
-// group scales xd and the half sums xh as in the packed record. Built by the DMA: LDS chunk i (16 bytes)
-// is fetched from the packed record chunk that belongs there.
+// group scales xd and the half sums xh as in the packed record. Built by DMA from a packed record, or by
+// quantizing fp32 activations in the kernel.
 #ifndef VQ_XPAD
 #define VQ_XPAD 32
 #endif
@@ -105,25 +94,31 @@ struct XImage {
     }
 };
 
+// Waves per workgroup: one 16-wave workgroup per CU for one token (the activation image is small), 8 waves
+// otherwise (the image of several tokens takes the LDS that more stage buffers would need).
+template <int NT>
+constexpr int wg_waves() {
+    return NT == 1 ? 16 : 8;
+}
+
 template <int T>
 struct Stream {
     using S = Sl<T>;
     static constexpr int LPU = StageShape<T>::LPU;
     static constexpr int SPL = S::SPB / LPU;  // slices per lane
     static constexpr int SU = 64 / LPU;       // units per stage
-    static constexpr bool BLOCKED = false;    // lane j of a unit takes slices j, j+LPU, ...
     // 16-byte chunks one stage's bytes can touch (its units plus the dword the decoders may read past the
     // last unit, from an arbitrary 16-byte phase) and the dwordx4 loads per lane that cover them.
     static constexpr int CMAX = (SU * S::UB + 4 + 15) / 16 + 1;
     static constexpr int NL = (CMAX + 63) / 64;
-    static constexpr int NW = StageShape<T>::NW;
-    static constexpr int NB = StageShape<T>::NB;  // stages in flight while one is decoded (1 or 2)
-    // Per wave: the stage buffer, then the finished row sums ([NT][rpw] fp32, rpw * NT <= kYSlots). Row sums
-    // are written to y once, at the end: a vector store in the stage loop would leave stores and loads
-    // pending on the one vmcnt counter, and the compiler then waits for all loads, both buffers included.
-    static constexpr int WAVE_LDS = NL * 1024 + 4 * kYSlots;
+    static constexpr int STAGE_LDS = NL * 1024;  // one wave's stage buffer
     static_assert(S::SPB % LPU == 0 && NL >= 1 && NL <= 16, "stage geometry");
 };
+
+// Partial row sums of one workgroup: [stage][row of the stage][token] fp32, at most this many floats.
+constexpr int kSlotFloats = 4096;
+// Rows a stage of SU consecutive units can touch when rows have nu units.
+__host__ __device__ constexpr int rows_per_stage(int su, int nu) { return (su - 1) / nu + 2; }
 
 template <int T>
 constexpr int grid_table_bytes() {
@@ -140,21 +135,23 @@ __device__ __forceinline__ const uint8_t *grid_table_src() {
 }
 
 // One launch covers up to kMaxJobs matrices of the same type and width that share the activations (a
-// layer's gate/up, q/k/v, ...). Job j owns the grid's waves [wave0, wave0 + ceil(rows/rpw)).
+// layer's gate/up, q/k/v, ...). Each job's rows are cut into ranges of `rwg` rows, one per workgroup; job j
+// owns the workgroups [b0, b0 + ceil(rows / rwg)).
 constexpr int kMaxJobs = 4;
-// Row accumulators per lane on the fast path: a stage of SU units touches at most kRowSlots rows when
-// rows have at least SU/(kRowSlots-1) units.
-constexpr int kRowSlots = 5;
 struct QJob {
     const uint8_t *w;
     float *y;  // [NT][rows], or null (argmax only)
-    int rows, rpw, wave0;
+    int rows, b0;
 };
 struct QJobs {
     QJob j[kMaxJobs];
     int n;
-    int waves;               // total waves of the grid that own rows
-    unsigned long long *amax;  // null, or [NT][waves] per-wave argmax keys (see argmax_key)
+    int rwg;      // rows per workgroup
+    int blocks;   // workgroups of the launch
+    unsigned long long *amax;  // null, or [NT][blocks] per-workgroup argmax keys (see argmax_key)
+#ifdef VQ_TIMING
+    unsigned long long *tm;  // diagnostic builds: per-wave {start, after prologue, loop end, exit, hw id}
+#endif
 };
 
 // Argmax key of a value at row r: larger key = larger value, then lower row. NaN and -inf never win (the
@@ -168,72 +165,82 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, long r) {
 
 // Quantized matvec: y[t][r] = W[r] . x[t] for t < NT.
 //
-// Wave g of the grid owns rows [g*rpw, (g+1)*rpw) -- a contiguous byte range, since rows are back to back
-// and each row is a whole number of units (32-element groups for Q8_0/IQ4_NL, 256-element super-blocks
-// otherwise). It walks that range in stages of SU = 64/LPU units. A stage's bytes (16-byte chunks
-// [c0, c1)) arrive in VGPRs by NL coalesced nontemporal dwordx4 loads per lane, two stages ahead: while
-// stage s is decoded, the loads of stages s+1 and s+2 are in flight. The landed chunks of stage s are
-// written to the wave's LDS stage buffer (lane order = byte order), and the LPU lanes of each unit decode
-// its slices with the type's slice decoders (weights, activation records and IQ tables all read from LDS),
-// so the block header is decoded once per 256/LPU elements. Rows that end in the stage are summed over the
-// wave and written.
+// Workgroup b owns a contiguous range of rows of one job -- a contiguous byte range, since rows are back to
+// back and each is a whole number of units (32-element groups for Q8_0/IQ4_NL, 256-element super-blocks
+// otherwise) -- cut into stages of SU = 64/LPU units. Its waves take stages from an LDS counter: wave w starts
+// with stage w, and each further stage is handed out when a wave asks, so waves that the memory system
+// serves faster take more stages and the workgroup's waves finish together (with static shares they finished
+// up to 3 us apart within a CU, measured on MI355X). A stage's bytes (16-byte chunks [c0, c1)) arrive in VGPRs
+// by NL coalesced nontemporal dwordx4 loads per lane, one stage ahead: a wave requests its next stage before
+// it decodes the current one. The landed stage goes to the wave's LDS stage buffer (lane order = byte order)
+// and the LPU lanes of each unit decode its slices with the type's slice decoders (weights, activations and
+// IQ tables all read from LDS), so the block header is decoded once per 256/LPU elements. A segmented scan
+// over the lanes gives each row's part in the stage, kept in an LDS slot per (stage, row); after a barrier the
+// workgroup adds each row's parts in stage order and writes y. Which wave decodes a stage does not change any
+// sum: results are deterministic.
 //
-// LDS: [grid table | activation image of the NT tokens | one stage buffer per wave]. At start-up the waves
-// request their share of the table and of the activation image (DMA), then their first two stages, and
-// meet at one barrier once the activations are in.
-template <int T, int NT, bool FEW, bool XF32>
-__global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJobs jobs, int cols,
-                                                                   const void *__restrict__ xin) {
+// LDS: [grid table | activation image of the NT tokens | stage buffer per wave | row-part slots]. At start-up
+// the waves load the table and the activations (DMA of the packed record, or quantization of fp32 values),
+// then request their first stage, and meet at one barrier.
+template <int T, int NT, bool XF32>
+__global__ __launch_bounds__(64 * wg_waves<NT>()) void qmv_stream_kernel(const QJobs jobs, int cols,
+                                                                    const void *__restrict__ xin) {
     using S = Sl<T>;
     using G = Stream<T>;
-    constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, NL = G::NL;
+    constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, NL = G::NL, NW = wg_waves<NT>();
     constexpr int TB = grid_table_bytes<T>();
     extern __shared__ __attribute__((aligned(1024))) uint8_t s_dyn[];
     __shared__ __attribute__((aligned(1024))) uint8_t s_grid[TB > 0 ? TB : 16];
     __shared__ uint4 sks[TabSpec<T>::ks ? 128 : 1];
     __shared__ uint4 ssm[TabSpec<T>::sm ? 256 : 1];
+    __shared__ int s_next;                        // next stage to hand out
+    __shared__ unsigned long long s_best[NT][NW];  // argmax reduction
 
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    constexpr int NW = G::NW;
+#ifdef VQ_TIMING
+    const unsigned long long tm0 = __builtin_amdgcn_s_memrealtime();
+    unsigned long long tm1 = 0, tm2 = 0;
+#endif
     const int nu = (cols >> 5) / S::UG;
     const int xb = vq_xpack_stride(cols);
     const XImage xi(cols);
     const int xreg = (NT * xi.bytes + 1023) & ~1023;
-    uint8_t *const sbuf = s_dyn + xreg + wv * G::WAVE_LDS;
-    float *const ybuf = reinterpret_cast<float *>(sbuf + NL * 1024);
+    uint8_t *const sbuf = s_dyn + xreg + wv * G::STAGE_LDS;
+    float *const slots = reinterpret_cast<float *>(s_dyn + xreg + NW * G::STAGE_LDS);
+    const int rs = rows_per_stage(SU, nu);
 
-    // This wave's job, rows and stages.
-    const int gw = blockIdx.x * NW + wv;
+    // This workgroup's job, rows and stages (all 32-bit unit indices: a matrix has < 2^31 units).
+    const int b = blockIdx.x;
     int jb = 0;
 #pragma unroll
-    for (int k = 1; k < kMaxJobs; ++k) jb = (k < jobs.n && gw >= jobs.j[k].wave0) ? k : jb;
+    for (int k = 1; k < kMaxJobs; ++k) jb = (k < jobs.n && b >= jobs.j[k].b0) ? k : jb;
     const uint8_t *const w = jobs.j[jb].w;
     float *const y = jobs.j[jb].y;
-    const int rows = jobs.j[jb].rows, rpw = jobs.j[jb].rpw;
-    const long r0 = gw < jobs.waves ? static_cast<long>(gw - jobs.j[jb].wave0) * rpw : rows;
-    const long r1 = r0 + rpw < rows ? r0 + rpw : rows;
-    const long U0 = r0 * nu, U1 = r1 * nu;
-    const int nst = r0 < rows ? static_cast<int>((U1 - U0 + SU - 1) / SU) : 0;
-    // Chunks of stage s: [c0, c1) with c0 the chunk of its first byte and c1 past the chunk holding the dword
-    // after its last unit -- but never past the chunk holding the matrix's last byte (the weight buffer has
-    // 16 readable pad bytes; decoders discard bytes past a block). Lanes past c1 re-read chunk c1 - 1 (the
-    // same addresses as a lane that does load it: no extra traffic), so every stage issues exactly NL loads.
+    const int rows = jobs.j[jb].rows;
+    const int R0 = (b - jobs.j[jb].b0) * jobs.rwg;
+    const int R1 = R0 + jobs.rwg < rows ? R0 + jobs.rwg : rows;
+    const int U0 = R0 * nu, U1 = R1 * nu;
+    const int nst = R0 < rows ? (U1 - U0 + SU - 1) / SU : 0;
+    // Stage s: 16-byte chunks [c0, c1) with c0 the one holding its first byte and c1 past the one holding the
+    // dword after its last unit -- but never past the one holding the matrix's last byte (the weight buffer
+    // has 16 readable pad bytes; decoders discard bytes past a block). Lanes past c1 re-read c1 - 1
+    // (addresses a lane that does load it also reads: no extra traffic), so every stage issues exactly NL
+    // loads.
     const long mend = static_cast<long>(rows) * nu * UB;
-    const u32x4 *const w16 = reinterpret_cast<const u32x4 *>(w);
-    auto chunk0 = [&](int s) { return ((U0 + static_cast<long>(s) * SU) * UB) >> 4; };
     auto load_stage = [&](int s, u32x4 (&R)[NL]) {
         const long ua = U0 + static_cast<long>(s) * SU;
         const long ub = ua + SU < U1 ? ua + SU : U1;
         const long e = ub * UB + 4 < mend ? ub * UB + 4 : mend;
         const long c0 = (ua * UB) >> 4, cl = ((e + 15) >> 4) - 1;
         // Wave-uniform base and limit; per-lane 32-bit chunk offsets.
-        const u32x4 *const base = w16 + c0;
-        const int lim = __builtin_amdgcn_readfirstlane(static_cast<int>(cl - c0));
+        const u32x4 *const base = reinterpret_cast<const u32x4 *>(w) + c0;
+        const long d = cl - c0;
+        const unsigned lim = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(d > 0 ? d : 0)));
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
             const unsigned c = static_cast<unsigned>(lane + 64 * i);
-            R[i] = __builtin_nontemporal_load(base + (c < static_cast<unsigned>(lim) ? c : static_cast<unsigned>(lim)));
+            R[i] = __builtin_nontemporal_load(base + (c < lim ? c : lim));
         }
     };
     auto store_stage = [&](const u32x4 (&R)[NL]) {
@@ -241,16 +248,34 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
         for (int i = 0; i < NL; ++i) reinterpret_cast<u32x4 *>(sbuf)[lane + 64 * i] = R[i];
     };
 
-    // Start-up: table and activation pieces (striped over the waves), then the first two stages.
+    // Start-up: table pieces and activations first, alone (waiting for them then waits behind no weight
+    // traffic), then the first stage.
     if constexpr (TB > 0) {
         const uint8_t *src = grid_table_src<T>();
         for (int p = wv; p < TB / 1024; p += NW) dma16(src + p * 1024, lane * 16, lds_addr(s_grid) + p * 1024);
     }
-#ifndef VQ_NOXIMG
-    if constexpr (!XF32) {
-#else
-    if constexpr (false) {
-#endif
+    if constexpr (XF32) {
+        const float *xf = static_cast<const float *>(xin);
+        for (int i = threadIdx.x; i < NT * xi.ng; i += blockDim.x) {
+            const int t = i / xi.ng, g = i - t * xi.ng;
+            const float4 *src = reinterpret_cast<const float4 *>(xf + static_cast<size_t>(t) * cols + 32 * g);
+            float v[32];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float4 f = src[k];
+                v[4 * k] = f.x;
+                v[4 * k + 1] = f.y;
+                v[4 * k + 2] = f.z;
+                v[4 * k + 3] = f.w;
+            }
+            const QGroup qg = quantize_group(v);
+            uint8_t *img = s_dyn + t * xi.bytes;
+            *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 0)) = u32x4{qg.q[0], qg.q[1], qg.q[2], qg.q[3]};
+            *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 1)) = u32x4{qg.q[4], qg.q[5], qg.q[6], qg.q[7]};
+            reinterpret_cast<float *>(img + xi.xq_bytes)[g] = qg.d;
+            reinterpret_cast<uint32_t *>(img + xi.xq_bytes + 4 * xi.ng)[g] = qg.half_sums();
+        }
+    } else {
         for (int p = wv; p < xreg / 1024; p += NW) {
             const int o = p * 1024 + lane * 16;  // LDS image byte of this lane's chunk
             const int t = o / xi.bytes;
@@ -258,27 +283,12 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
             dma16(xin, static_cast<uint32_t>(src >= 0 ? t * xb + src : 0), lds_addr(s_dyn) + p * 1024);
         }
     }
-    // Every wave issues exactly NL loads per buffer fill, whatever its stage count (stages past the last
-    // re-read the last one, from L2): the compiler's vmcnt bookkeeping then sees the same number of loads
-    // in flight on every path and waits for one buffer only.
-    const int slast = nst > 0 ? nst - 1 : 0;
-    u32x4 RA[NL], RB[G::NB == 2 ? NL : 1];
-    load_stage(0, RA);
-    if constexpr (G::NB == 2) load_stage(1 < slast ? 1 : slast, RB);
-    if constexpr (XF32) {
-        // fp32 activations: quantize each 32-group here, straight into the LDS image (the weight stream is
-        // already requested, so this overlaps its first round trip).
-        const float *x = static_cast<const float *>(xin);
-        for (int i = threadIdx.x; i < NT * xi.ng; i += blockDim.x) {
-            const int t = i / xi.ng, g = i - t * xi.ng;
-            const QGroup qg = quantize_group(x + static_cast<size_t>(t) * cols + 32 * g);
-            uint8_t *img = s_dyn + t * xi.bytes;
-            *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 0)) = u32x4{qg.q[0], qg.q[1], qg.q[2], qg.q[3]};
-            *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 1)) = u32x4{qg.q[4], qg.q[5], qg.q[6], qg.q[7]};
-            reinterpret_cast<float *>(img + xi.xq_bytes)[g] = qg.d;
-            reinterpret_cast<uint32_t *>(img + xi.xq_bytes + 4 * xi.ng)[g] = qg.half_sums();
-        }
-    }
+    wait_vm<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    int s = wv < nst ? wv : -1;
+    u32x4 RA[NL];
+    load_stage(s >= 0 ? s : 0, RA);
+    if (threadIdx.x == 0) s_next = NW;
     Tabs tb{};
     if constexpr (TabSpec<T>::n8 > 0) tb.grid8 = reinterpret_cast<const uint2 *>(s_grid);
     if constexpr (TabSpec<T>::n4 > 0) tb.grid4 = reinterpret_cast<const uint32_t *>(s_grid);
@@ -290,42 +300,27 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
         for (int i = threadIdx.x; i < 256; i += blockDim.x) ssm[i] = sign_entry(i);
         tb.sm256 = ssm;
     }
-    // The DMAs were issued before this wave's stage loads, and loads retire in order: once at most the
-    // stage loads are outstanding, the table and activation pieces have landed.
-    if constexpr (TB > 0 || !XF32) wait_vm<G::NB * NL>();
     wait_lgkm0();
-#ifndef VQ_NOBAR
     __builtin_amdgcn_s_barrier();
-#endif
     asm volatile("" ::: "memory");
-    if (nst == 0) return;
+#ifdef VQ_TIMING
+    tm1 = __builtin_amdgcn_s_memrealtime();
+#endif
 
     const int ul = lane / LPU;  // unit of this lane within a stage
     const int lj = lane % LPU;  // which of the unit's lanes
     const float inv_nu = 1.0f / static_cast<float>(nu);
-    long row_a = r0;       // row of the stage's first unit (wave-uniform)
-    int col_a = 0;         // its unit index within that row
-    long carry_row = -1;   // row whose earlier part is in carry[] (segmented-scan path)
-    float carry[NT];
-    constexpr int NS = kRowSlots;
-    float acc[NS][NT];     // rows row_a .. row_a+NS-1 (FEW path: a stage touches at most NS rows)
-    unsigned long long best[NT];  // argmax key of this wave's finished rows (wave-uniform)
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        carry[t] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < NS; ++k) acc[k][t] = 0.0f;
-        best[t] = 0ull;
-    }
 
-    // Decode stage s from the stage buffer (its chunk c0 at sbuf) and fold it into the row sums.
+    // Decode stage s from the stage buffer; each row's part goes to its slot.
     auto run_stage = [&](int s) {
-        const long ua = U0 + static_cast<long>(s) * SU;
-        const int nval = static_cast<int>((U1 - ua < SU ? U1 - ua : SU));  // units in this stage
+        const int ua = U0 + s * SU;
+        const int nval = U1 - ua < SU ? U1 - ua : SU;  // units in this stage
+        const int rf = ua / nu;                          // row of the stage's first unit
+        const int col = ua - rf * nu;                    // its unit index within that row
         const bool valid = ul < nval;
-        const uint8_t *up = sbuf + ((ua + (valid ? ul : 0)) * UB - (chunk0(s) << 4));
-        // Row and column unit of this lane's unit: c = col_a + ul = q*nu + cu with q small.
-        const int c = col_a + ul;
+        const uint8_t *up = sbuf + ((static_cast<long>(ua) + (valid ? ul : 0)) * UB - ((static_cast<long>(ua) * UB >> 4) << 4));
+        // Row and column unit of this lane's unit: c = col + ul = q*nu + cu with q small.
+        const int c = col + ul;
         int q = static_cast<int>(static_cast<float>(c) * inv_nu);
         q = (q + 1) * nu <= c ? q + 1 : q;
         q = q * nu > c ? q - 1 : q;
@@ -338,7 +333,7 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
 #ifdef VQ_NODECODE
         v[0] = static_cast<float>(*reinterpret_cast<const uint32_t *>(up + 4 * lj) & 0xFF) * static_cast<float>(G0);
 #else
-        // The unit's group scales and half sums of every token (two 16-byte LDS reads each).
+        // The unit's group scales and half sums of every token.
         float xdu[NT][S::UG];
         int32_t xhu[NT][S::UG];
 #pragma unroll
@@ -405,168 +400,136 @@ __global__ __launch_bounds__(64 * Stream<T>::NW) void qmv_stream_kernel(const QJ
             }
         } else {
 #pragma unroll
-        for (int k = 0; k < G::SPL; ++k) {
-            const int ss = G::BLOCKED ? lj * G::SPL + k : lj + LPU * k;
-            typename S::W wr;
-            S::load(up, ss, wr);
-            uint32_t cd[NP][4];
-            S::codes(wr, ss, tb, cd);
-            float sc[NP], mn[NP];
-            S::scales(wr, ss, sc, mn);
+            for (int k = 0; k < G::SPL; ++k) {
+                const int ss = lj + LPU * k;
+                typename S::W wr;
+                S::load(up, ss, wr);
+                uint32_t cd[NP][4];
+                S::codes(wr, ss, tb, cd);
+                float sc[NP], mn[NP];
+                S::scales(wr, ss, sc, mn);
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                int pg, ph;
-                S::part(ss, p, pg, ph);
-                const int Gi = G0 + pg;
+                for (int p = 0; p < NP; ++p) {
+                    int pg, ph;
+                    S::part(ss, p, pg, ph);
+                    const int Gi = G0 + pg;
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const uint8_t *xt = s_dyn + t * xi.bytes;
-                    const u32x4 xv4 = *reinterpret_cast<const u32x4 *>(xt + xi.code_off(Gi, ph));
-                    const float xdv = xdu[t][pg];
-                    const int X = kNeedsX<T> ? static_cast<int>(static_cast<int16_t>(
-                                                   static_cast<uint32_t>(xhu[t][pg]) >> (16 * ph)))
-                                             : 0;
-                    const uint32_t xv[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
-                    const int Sv = dot16(cd[p], xv) - S::OFF * X;
-                    float g = static_cast<float>(Sv) * sc[p];
-                    if constexpr (kHasMin<T>) g = fmaf(-static_cast<float>(X), mn[p], g);
-                    v[t] = fmaf(g, xdv, v[t]);
+                    for (int t = 0; t < NT; ++t) {
+                        const uint8_t *xt = s_dyn + t * xi.bytes;
+                        const u32x4 xv4 = *reinterpret_cast<const u32x4 *>(xt + xi.code_off(Gi, ph));
+                        const float xdv = xdu[t][pg];
+                        const int X = kNeedsX<T> ? static_cast<int>(static_cast<int16_t>(
+                                                       static_cast<uint32_t>(xhu[t][pg]) >> (16 * ph)))
+                                                 : 0;
+                        const uint32_t xv[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
+                        const int Sv = dot16(cd[p], xv) - S::OFF * X;
+                        float g = static_cast<float>(Sv) * sc[p];
+                        if constexpr (kHasMin<T>) g = fmaf(-static_cast<float>(X), mn[p], g);
+                        v[t] = fmaf(g, xdv, v[t]);
+                    }
                 }
             }
-        }
         }
 #endif
-        if constexpr (FEW) {
-            // Rows have at least SU/(NS-1) units, so this lane's unit is in row row_a + q with q < NS. Rows that
-            // end in this stage are summed over the wave and written; the others shift down.
+        // Segmented inclusive scan over the lanes; segments are the stage's rows (q is non-decreasing in lane
+        // order). The last lane of each segment holds that row's part of the stage.
+        const int key = valid ? q : 0x7FFFFFFF;
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
+        for (int d = 1; d < 64; d <<= 1) {
+            const int kp = __shfl_up(key, d, 64);
+            const bool m = lane >= d && kp == key;
 #pragma unroll
-                for (int k = 0; k < NS; ++k) acc[k][t] += q == k ? v[t] : 0.0f;
-            const int done = (col_a + nval) / nu;  // rows completed by this stage (0..NS-1)
-#pragma unroll
-            for (int k = 0; k < NS - 1; ++k) {
-                if (k < done) {
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) {
-                        const float tot = wave_sum(acc[k][t]);
-                        if (lane == 0) ybuf[t * rpw + static_cast<int>(row_a + k - r0)] = tot;
-                        const unsigned long long key = argmax_key(tot, row_a + k);
-                        best[t] = key > best[t] ? key : best[t];
-                    }
-                }
+            for (int t = 0; t < NT; ++t) {
+                const float vp = __shfl_up(v[t], d, 64);
+                v[t] += m ? vp : 0.0f;
             }
-            if (done > 0) {
+        }
+        const int kn = __shfl_down(key, 1, 64);
+        if (valid && (lane == 63 || kn != key)) {
 #pragma unroll
-                for (int k = 0; k < NS; ++k)
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) {
-                        float nv = 0.0f;
-#pragma unroll
-                        for (int d = 1; d < NS; ++d)
-                            if (k + d < NS) nv = done == d ? acc[k + d][t] : nv;
-                        acc[k][t] = nv;
-                    }
-            }
-            row_a += done;
-            col_a += nval - done * nu;
-        } else {
-            // Segmented inclusive scan over lanes; segments are rows (row ids are non-decreasing in lane order).
-            const int rr = valid ? static_cast<int>(row_a + q) : 0x7FFFFFFF;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const int rp = __shfl_up(rr, d, 64);
-                const bool m = lane >= d && rp == rr;
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const float vp = __shfl_up(v[t], d, 64);
-                    v[t] += m ? vp : 0.0f;
-                }
-            }
-            const int rn = __shfl_down(rr, 1, 64);
-            const bool seg_end = valid && (lane == 63 || rn != rr);
-            if (rr == carry_row) {
-#pragma unroll
-                for (int t = 0; t < NT; ++t) v[t] += carry[t];
-            }
-            const long ub = ua + nval;
-            const bool row_done = seg_end && (static_cast<long>(rr) + 1) * nu <= ub;
-            if (row_done) {
-#pragma unroll
-                for (int t = 0; t < NT; ++t) ybuf[t * rpw + static_cast<int>(rr - r0)] = v[t];
-            }
-            if (jobs.amax != nullptr) {
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    unsigned long long key = row_done ? argmax_key(v[t], rr) : 0ull;
-#pragma unroll
-                    for (int off = 32; off > 0; off >>= 1) {
-                        const unsigned long long o = __shfl_xor(key, off, 64);
-                        key = o > key ? o : key;
-                    }
-                    best[t] = key > best[t] ? key : best[t];
-                }
-            }
-            // The stage's last row continues into the next stage unless it ends here.
-            const int lv = nval * LPU - 1;
-            const long last_row = __builtin_amdgcn_readlane(rr, lv);
-            if ((last_row + 1) * nu > ub) {
-                carry_row = last_row;
-#pragma unroll
-                for (int t = 0; t < NT; ++t) carry[t] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[t]), lv));
-            } else {
-                carry_row = -1;
-            }
-            // Advance the stage origin by SU units.
-            col_a += SU;
-            if (col_a >= nu) {
-                const int adv = col_a / nu;
-                row_a += adv;
-                col_a -= adv * nu;
-            }
+            for (int t = 0; t < NT; ++t) slots[(s * rs + q) * NT + t] = v[t];
         }
     };
 
-    // Two stages in flight: RA holds even stages, RB odd ones. Writing a buffer to LDS waits (compiler-
-    // inserted vmcnt) for its own loads only; the stage buffer is rewritten after the previous stage's LDS
-    // reads were issued, and a wave's LDS operations complete in order.
-    // (No exit from the middle of the pair: a path from there back through the latch would look, to the
-    // compiler, like RA's loads being the last ones issued.)
-    int s = 0;
-    if constexpr (G::NB == 1) {
-        // One stage in flight: stage s+1 loads while stage s is decoded.
-        for (; s + 1 < nst; ++s) {
-            store_stage(RA);
-            load_stage(s + 1, RA);
-            run_stage(s);
+    // One stage in flight: the next stage's loads are issued before the current one is decoded. Writing RA to
+    // LDS waits (compiler-inserted vmcnt) for its loads; the stage buffer is rewritten after the previous
+    // stage's LDS reads were issued, and a wave's LDS operations complete in order. The next stage number is
+    // asked for one stage ahead, so its LDS round trip hides behind a decode.
+    // One lane takes the ticket (a wave-wide atomic would take one per lane); readfirstlane shares it.
+    auto take = [&]() { return lane == 0 ? atomicAdd(&s_next, 1) : 0; };
+    int ask = s >= 0 ? take() : nst;  // the stage after s (valid in lane 0)
+    while (s >= 0) {
+        store_stage(RA);
+        const int sn = __builtin_amdgcn_readfirstlane(ask);
+        if (sn < nst) {
+            load_stage(sn, RA);
+            ask = take();
         }
-    } else {
-    for (; s + 1 < nst; s += 2) {
-        store_stage(RA);
-        load_stage(s + 2 < slast ? s + 2 : slast, RA);
         run_stage(s);
-        store_stage(RB);
-        load_stage(s + 3 < slast ? s + 3 : slast, RB);
-        run_stage(s + 1);
+        s = sn < nst ? sn : -1;
     }
-    }
-    if (s < nst) {
-        store_stage(RA);
-        run_stage(s);
-    }
-    if (y != nullptr) {
-        const int nr = static_cast<int>(r1 - r0);
+#ifdef VQ_TIMING
+    tm2 = __builtin_amdgcn_s_memrealtime();
+#endif
+    __syncthreads();
+
+    // Each row's parts in stage order: the row's units are [r*nu - U0, (r+1)*nu - U0) of the range.
+    unsigned long long best[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-            for (int i = lane; i < nr; i += 64) y[static_cast<size_t>(t) * rows + r0 + i] = ybuf[t * rpw + i];
-    }
-    if (jobs.amax != nullptr && lane == 0) {
+    for (int t = 0; t < NT; ++t) best[t] = 0ull;
+    for (int r = R0 + static_cast<int>(threadIdx.x); r < R1; r += blockDim.x) {
+        const int ua = r * nu - U0, ue = ua + nu - 1;
+        const int s0 = ua / SU, s1 = ue / SU;
+        float tot[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) jobs.amax[static_cast<size_t>(t) * jobs.waves + gw] = best[t];
+        for (int t = 0; t < NT; ++t) tot[t] = 0.0f;
+        for (int st = s0; st <= s1; ++st) {
+            const int qs = r - (U0 + st * SU) / nu;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) tot[t] += slots[(st * rs + qs) * NT + t];
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (y != nullptr) y[static_cast<size_t>(t) * rows + r] = tot[t];
+            const unsigned long long key = argmax_key(tot[t], r);
+            best[t] = key > best[t] ? key : best[t];
+        }
     }
+    if (jobs.amax != nullptr) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            unsigned long long k = best[t];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const unsigned long long o = __shfl_xor(k, off, 64);
+                k = o > k ? o : k;
+            }
+            if (lane == 0) s_best[t][wv] = k;
+        }
+        __syncthreads();
+        if (threadIdx.x < NT) {
+            unsigned long long k = 0ull;
+            for (int i = 0; i < NW; ++i) k = s_best[threadIdx.x][i] > k ? s_best[threadIdx.x][i] : k;
+            jobs.amax[static_cast<size_t>(threadIdx.x) * jobs.blocks + b] = k;
+        }
+    }
+#ifdef VQ_TIMING
+    if (jobs.tm != nullptr && lane == 0) {
+        const long gw = static_cast<long>(b) * NW + wv;
+        if (gw < 65536) {
+            unsigned hw, xcc;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+            unsigned long long *o = jobs.tm + 6 * static_cast<size_t>(gw);
+            o[0] = tm0; o[1] = tm1; o[2] = tm2; o[3] = __builtin_amdgcn_s_memrealtime();
+            o[4] = (static_cast<unsigned long long>(xcc) << 32) | hw;
+            o[5] = 0;
+        }
+    }
+#endif
 }
 
-// Final argmax over the per-wave keys: one workgroup per token; INT32_MAX when no value qualifies.
+// Final argmax over the per-workgroup keys: one workgroup per token; INT32_MAX when no value qualifies.
 static __global__ __launch_bounds__(256) void argmax_keys_kernel(const unsigned long long *__restrict__ keys, int n,
                                                           int32_t *__restrict__ out) {
     __shared__ unsigned long long red[4];
@@ -685,12 +648,10 @@ inline size_t static_lds_bytes(const void *kernel) {
     return a.sharedSizeBytes;
 }
 
-// Launch geometry of one grouped matvec: rows per wave so that the waves the chip holds at this LDS
-// footprint (160 KB per CU, at most 32 waves per CU) cover all rows of all jobs once.
+// Launch geometry: LDS bytes, resident workgroups on the chip, rows per workgroup.
 struct Geometry {
     size_t lds;  // dynamic LDS bytes
-    int rpw;
-    bool few;
+    int wgres;   // workgroups resident at once on the whole chip (0 if the LDS does not fit)
 };
 // Resident workgroups per CU of a qmv_stream_kernel instantiation at `lds` dynamic LDS bytes (VGPR, LDS and
 // wave limits, as the runtime computes them); 1 if the query fails.
@@ -703,82 +664,89 @@ inline int resident_wgs(const void *kernel, int threads, size_t lds) {
     return n;
 }
 template <int T, int N>
-Geometry geometry(long total_rows, int cols) {
+Geometry geometry(int cols, int slot_floats) {
     using G = Stream<T>;
+    constexpr int NW = wg_waves<N>();
     Geometry g;
     const int xreg = (N * XImage(cols).bytes + 1023) & ~1023;
-    g.lds = static_cast<size_t>(xreg) + static_cast<size_t>(G::NW) * G::WAVE_LDS;
-    g.few = (kRowSlots - 1) * ((cols / 32) / Sl<T>::UG) >= G::SU;
-    // Both activation forms of the chosen row path: the grid must not depend on the form. Cached per
-    // (few, LDS bytes): the occupancy queries cost host time on every launch otherwise.
+    g.lds = static_cast<size_t>(xreg) + static_cast<size_t>(NW) * G::STAGE_LDS + 4 * static_cast<size_t>(slot_floats);
+    // Both activation forms: the grid must not depend on the form. Cached per LDS size: the occupancy
+    // queries cost host time on every launch otherwise.
     static std::mutex mu;
     static std::unordered_map<long, int> cache;
-    const long key = static_cast<long>(g.lds) * 2 + (g.few ? 1 : 0);
-    long wg_per_cu;
-    {
-        std::lock_guard<std::mutex> lock(mu);
-        auto it = cache.find(key);
-        if (it == cache.end()) {
-            const void *ka = g.few ? reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, false>)
-                                   : reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false, false>);
-            const void *kb = g.few ? reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, true>)
-                                   : reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false, true>);
-            (void)raise_dynamic_lds(ka);
-            (void)raise_dynamic_lds(kb);
-            const int ra = resident_wgs(ka, 64 * G::NW, g.lds), rb = resident_wgs(kb, 64 * G::NW, g.lds);
-            it = cache.emplace(key, ra < rb ? ra : rb).first;
-        }
-        wg_per_cu = it->second;
+    // (Without a device the queries fail: then 160 KB and one workgroup per CU, so that workspace sizes can
+    // still be computed.)
+    static const int max_a = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false>));
+    static const int max_b = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true>));
+    const int lim = max_a > 0 && max_b > 0 ? (max_a < max_b ? max_a : max_b) : 160 * 1024;
+    if (g.lds > static_cast<size_t>(lim)) {
+        g.wgres = 0;
+        return g;
     }
-#ifdef VQ_WGCAP
-    if (wg_per_cu > VQ_WGCAP) wg_per_cu = VQ_WGCAP;
-#endif
-    const long target = 256 * wg_per_cu * G::NW;
-    g.rpw = static_cast<int>((total_rows + target - 1) / target);
-    if (g.rpw > kYSlots / N) g.rpw = kYSlots / N;  // more than one round of waves for very tall launches
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(static_cast<long>(g.lds));
+    if (it == cache.end()) {
+        const int ra = resident_wgs(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false>), 64 * NW, g.lds);
+        const int rb = resident_wgs(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true>), 64 * NW, g.lds);
+        it = cache.emplace(static_cast<long>(g.lds), ra < rb ? ra : rb).first;
+    }
+    g.wgres = 256 * it->second;
     return g;
 }
 
-// Rows per wave for a launch of n jobs (total rows) with N tokens.
-template <int T>
-int rows_per_wave(long total_rows, int cols, int n_tok) {
-    switch (n_tok) {
-        case 1: return geometry<T, 1>(total_rows, cols).rpw;
-        case 2: return geometry<T, 2>(total_rows, cols).rpw;
-        case 3: return geometry<T, 3>(total_rows, cols).rpw;
-        case 4: return geometry<T, 4>(total_rows, cols).rpw;
-        case 5: return geometry<T, 5>(total_rows, cols).rpw;
-        case 6: return geometry<T, 6>(total_rows, cols).rpw;
-        case 7: return geometry<T, 7>(total_rows, cols).rpw;
-        default: return geometry<T, 8>(total_rows, cols).rpw;
-    }
-}
-
-// Fills rpw / wave0 / waves of `jobs` (w, y, rows, n set by the caller); returns the wave count.
-inline long plan_jobs(QJobs &jobs, int rpw) {
-    long waves = 0;
-    for (int k = 0; k < jobs.n; ++k) {
-        jobs.j[k].rpw = rpw;
-        jobs.j[k].wave0 = static_cast<int>(waves);
-        waves += (jobs.j[k].rows + rpw - 1) / rpw;
-    }
-    jobs.waves = static_cast<int>(waves);
-    return waves;
-}
-
-template <int T, int N, bool XF32>
-int launch_stream(const QJobs &jobs, int cols, const void *xp, hipStream_t s) {
+// Dynamic LDS of a launch with N tokens and rwg rows per workgroup.
+template <int T, int N>
+size_t launch_lds(int cols, int rwg) {
     using G = Stream<T>;
-    static const int max_dyn_f = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, XF32>));
-    static const int max_dyn_s = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false, XF32>));
-    const Geometry g = geometry<T, N>(1, cols);
-    if (g.lds > static_cast<size_t>(g.few ? max_dyn_f : max_dyn_s)) return static_cast<int>(hipErrorInvalidConfiguration);
-    const dim3 grid(static_cast<unsigned>((jobs.waves + G::NW - 1) / G::NW)), block(64 * G::NW);
-    if (g.few)
-        qmv_stream_kernel<T, N, true, XF32><<<grid, block, g.lds, s>>>(jobs, cols, xp);
-    else
-        qmv_stream_kernel<T, N, false, XF32><<<grid, block, g.lds, s>>>(jobs, cols, xp);
-    return hip_status(hipGetLastError());
+    const int nu = (cols / 32) / Sl<T>::UG;
+    const long nst = (static_cast<long>(rwg) * nu + G::SU - 1) / G::SU;
+    const int xreg = (N * XImage(cols).bytes + 1023) & ~1023;
+    return static_cast<size_t>(xreg) + static_cast<size_t>(wg_waves<N>()) * G::STAGE_LDS +
+           4 * static_cast<size_t>(nst * rows_per_stage(G::SU, nu) * N);
+}
+
+// Work split of one launch.
+struct Plan {
+    int rwg, blocks, slot_floats;
+    size_t lds;
+};
+template <int T, int N>
+Plan plan_n(const int *rows, int n, int cols) {
+    using G = Stream<T>;
+    const int nu = (cols / 32) / Sl<T>::UG;
+    const int rs = rows_per_stage(G::SU, nu);
+    long total = 0;
+    for (int k = 0; k < n; ++k) total += rows[k];
+    Plan p{};
+    // Rows per workgroup: one round of workgroups over all rows, but no more stages than the slots hold.
+    const Geometry g0 = geometry<T, N>(cols, kSlotFloats);
+    if (g0.wgres == 0) return p;  // blocks = 0: does not fit
+    long rwg = (total + g0.wgres - 1) / g0.wgres;
+    const long max_st = kSlotFloats / (rs * N);
+    const long max_rows = (max_st * G::SU) / nu;  // whole rows whose stages fit (a row range starts on a row)
+    if (rwg > max_rows) rwg = max_rows;
+    if (rwg < 1) rwg = 1;
+    p.rwg = static_cast<int>(rwg);
+    long blocks = 0;
+    for (int k = 0; k < n; ++k) blocks += (rows[k] + p.rwg - 1) / p.rwg;
+    p.blocks = static_cast<int>(blocks);
+    const long nst = (rwg * nu + G::SU - 1) / G::SU;
+    p.slot_floats = static_cast<int>(nst * rs * N);
+    p.lds = geometry<T, N>(cols, p.slot_floats).lds;
+    return p;
+}
+template <int T>
+Plan plan_launch(const int *rows, int n, int cols, int n_tok) {
+    switch (n_tok) {
+        case 1: return plan_n<T, 1>(rows, n, cols);
+        case 2: return plan_n<T, 2>(rows, n, cols);
+        case 3: return plan_n<T, 3>(rows, n, cols);
+        case 4: return plan_n<T, 4>(rows, n, cols);
+        case 5: return plan_n<T, 5>(rows, n, cols);
+        case 6: return plan_n<T, 6>(rows, n, cols);
+        case 7: return plan_n<T, 7>(rows, n, cols);
+        default: return plan_n<T, 8>(rows, n, cols);
+    }
 }
 
 // Tokens per launch: as many (<= 8) as the activation image budget holds.
@@ -787,12 +755,11 @@ inline int token_chunk(int cols) {
     return chunk > 8 ? 8 : chunk < 1 ? 1 : chunk;
 }
 
-// Waves of a single-job launch (the argmax key count per token).
+// Workgroups of a single-job launch (the argmax key count per token).
 template <int T>
 long argmax_waves(int rows, int cols, int ntok) {
     const int m = ntok < token_chunk(cols) ? ntok : token_chunk(cols);
-    const int rpw = rows_per_wave<T>(rows, cols, m);
-    return (rows + rpw - 1) / rpw;
+    return plan_launch<T>(&rows, 1, cols, m).blocks;
 }
 
 // y_j = W_j x for the n jobs (same type and cols), x fp32 (quantized in-kernel) or packed. With `amax`
@@ -803,37 +770,50 @@ int launch_quant_jobs(int n, const uint8_t *const *w, const int *rows, float *co
     if (n < 1 || n > kMaxJobs || (amax && n != 1)) return static_cast<int>(hipErrorInvalidValue);
     const size_t tok_bytes = x_f32 ? static_cast<size_t>(cols) * 4 : static_cast<size_t>(vq_xpack_stride(cols));
     const int chunk = token_chunk(cols);
-    long total = 0;
-    for (int k = 0; k < n; ++k) total += rows[k];
-    const int rpw = rows_per_wave<T>(total, cols, ntok < chunk ? ntok : chunk);
-    long kw = 0;
+    // One split for every token chunk (the first is the widest), so the argmax key layout is the same.
+    const Plan pl = plan_launch<T>(rows, n, cols, ntok < chunk ? ntok : chunk);
+    if (pl.blocks <= 0) return static_cast<int>(hipErrorInvalidConfiguration);
     for (int c = 0; c < ntok; c += chunk) {
         const int m = ntok - c < chunk ? ntok - c : chunk;
         QJobs jobs{};
         jobs.n = n;
+        int b0 = 0;
         for (int k = 0; k < n; ++k) {
             jobs.j[k].w = w[k];
             jobs.j[k].y = y[k] ? y[k] + static_cast<size_t>(c) * rows[k] : nullptr;
             jobs.j[k].rows = rows[k];
+            jobs.j[k].b0 = b0;
+            b0 += (rows[k] + pl.rwg - 1) / pl.rwg;
         }
-        kw = plan_jobs(jobs, rpw);
-        jobs.amax = amax ? amax + static_cast<size_t>(c) * kw : nullptr;
+        jobs.rwg = pl.rwg;
+        jobs.blocks = pl.blocks;
+#ifdef VQ_TIMING
+        jobs.tm = static_cast<unsigned long long *>(vq_debug_timing_buffer());
+#endif
+        jobs.amax = amax ? amax + static_cast<size_t>(c) * pl.blocks : nullptr;
         const void *xp = static_cast<const uint8_t *>(x) + static_cast<size_t>(c) * tok_bytes;
-        int st = 0;
-#define VQ_CASE(N)                                                                  \
-    case N:                                                                         \
-        st = x_f32 ? launch_stream<T, N, true>(jobs, cols, xp, s)                   \
-                   : launch_stream<T, N, false>(jobs, cols, xp, s);                 \
-        break;
+        const dim3 grid(static_cast<unsigned>(pl.blocks));
+        // A narrower last chunk keeps the plan's rows per workgroup; its own token count sets the LDS (the
+        // waves per workgroup may differ).
+#define VQ_CASE(N)                                                                                            \
+    case N: {                                                                                                 \
+        const size_t lds = launch_lds<T, N>(cols, pl.rwg);                                                    \
+        if (x_f32)                                                                                            \
+            qmv_stream_kernel<T, N, true><<<grid, dim3(64 * wg_waves<N>()), lds, s>>>(jobs, cols, xp);       \
+        else                                                                                                  \
+            qmv_stream_kernel<T, N, false><<<grid, dim3(64 * wg_waves<N>()), lds, s>>>(jobs, cols, xp);      \
+        break;                                                                                                \
+    }
         switch (m) {
             VQ_CASE(1) VQ_CASE(2) VQ_CASE(3) VQ_CASE(4) VQ_CASE(5) VQ_CASE(6) VQ_CASE(7)
             default: VQ_CASE(8)
         }
 #undef VQ_CASE
+        const int st = hip_status(hipGetLastError());
         if (st) return st;
     }
     if (amax) {
-        argmax_keys_kernel<<<ntok, 256, 0, s>>>(amax, static_cast<int>(kw), amax_out);
+        argmax_keys_kernel<<<ntok, 256, 0, s>>>(amax, pl.blocks, amax_out);
         return hip_status(hipGetLastError());
     }
     return 0;

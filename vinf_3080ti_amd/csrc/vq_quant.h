@@ -19,17 +19,8 @@ struct QGroup {
     }
 };
 
-// src: 32 consecutive fp32 values, 16-byte aligned.
-__device__ __forceinline__ QGroup quantize_group(const float *__restrict__ src) {
-    float v[32];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float4 f = reinterpret_cast<const float4 *>(src)[k];
-        v[4 * k] = f.x;
-        v[4 * k + 1] = f.y;
-        v[4 * k + 2] = f.z;
-        v[4 * k + 3] = f.w;
-    }
+// v: 32 consecutive fp32 values (registers, or memory 16-byte aligned).
+__device__ __forceinline__ QGroup quantize_group(const float *__restrict__ v) {
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(v[k]));
