@@ -4,8 +4,8 @@ Headline workload: a qwen35-27B-shaped decode-step we
 layers (48 gated-delta SSM + 16 gated-attention) with a UD-Q3_K_XL-like quant mix and the Q6_K LM head with
 on-device argmax, 13.44 GiB of synthetic seeded raw GGUF blocks resident in HBM. One step = one sweep:
 every weight matrix of the step read once: one grouped launch per run of same-type matrices sharing an
-input (<= 4; vq_qmv_group_f32 quantizing in-kernel, or vq_pack_x + vq_qmv_group for the 17408-wide FFN
-down input), and the fused vq_lmhead_argmax for the LM head.
+input (<= 4; vq_qmv_group_f32, which quantizes the fp32 activations in-kernel), and the fused
+vq_lmhead_argmax for the LM head.
 `value` = algorithmic bytes of the step / step time (GB/s); `ms_per_step` = ms per sweep.
 
 Also reported: per-quant-type matvec throughput at 5120x17408 (configs[0..2] shapes, rotating over weight
@@ -67,7 +67,7 @@ def sweep_plan():
 
 TYPE_NAMES = {Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_0: "Q8_0", IQ4_XS: "IQ4_XS",
               IQ3_S: "IQ3_S", IQ2_XXS: "IQ2_XXS"}
-FUSED_QUANT_MAX_COLS = 8192  # narrower inputs are quantized inside the matvec (vq_qmv_group_f32)
+FUSED_QUANT_MAX_COLS = 24576  # narrower inputs are quantized inside the matvec (vq_qmv_group_f32)
 PER_TYPE = [Q4_K, Q3_K, IQ4_XS, IQ3_S, IQ2_XXS, Q6_K]
 
 

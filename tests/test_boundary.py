@@ -69,8 +69,9 @@ def test_host_side_argument_checks(lib):
     assert lib.vq_xpack_bytes(96, 1) == 128 and lib.vq_xpack_bytes(96, 3) == 384
     assert lib.vq_xpack_bytes(48, 1) == 0
     assert lib.vq_qmv_workspace_bytes(5120, 8) == 0  # narrow inputs are quantized inside the matvec
-    assert lib.vq_qmv_workspace_bytes(17408, 2) == lib.vq_xpack_bytes(17408, 2)
-    assert lib.vq_qmv(int(T.Q4_K), fake, 4, 17408, fake, 1, fake, None, 0, None) == _lib.VQ_ERR_WORKSPACE
+    assert lib.vq_qmv_workspace_bytes(17408, 2) == 0  # the FFN down input too
+    assert lib.vq_qmv_workspace_bytes(32768, 2) == lib.vq_xpack_bytes(32768, 2)
+    assert lib.vq_qmv(int(T.Q4_K), fake, 4, 32768, fake, 1, fake, None, 0, None) == _lib.VQ_ERR_WORKSPACE
     arr = (ctypes.c_void_p * 5)(*([fake] * 5))
     rws = (ctypes.c_int * 5)(*([4] * 5))
     assert lib.vq_qmv_group(int(T.Q4_K), 0, arr, rws, arr, 256, fake, 1, None) == _lib.VQ_ERR_ARG

@@ -163,6 +163,22 @@ def test_qmv_baseline_shapes(env, oracle_mod, ty, rows, cols):
         assert rel_l2(got, ref) <= REL_L2_TOL, (ty.name, ntok)
 
 
+@pytest.mark.parametrize("cols", [24576, 49152])
+@pytest.mark.parametrize("ty", [T.Q6_K, T.Q3_K, T.IQ2_S, T.Q8_0], ids=lambda v: v.name)
+def test_qmv_wide_inputs(env, oracle_mod, ty, cols):
+    """The widest in-kernel-quantized input (24576) and a packed one (49152): activation images that push
+    the workgroup to fewer waves (its LDS then holds fewer stage buffers)."""
+    torch, lib = env
+    rng = np.random.default_rng(cols + int(ty))
+    rows = 37
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    for ntok in (1, 3):
+        x = rng.standard_normal((ntok, cols)).astype(np.float32)
+        got = gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok)
+        ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok)
+        assert rel_l2(got, ref) <= REL_L2_TOL, (ty.name, cols, ntok)
+
+
 def test_argmax_rows_semantics(env, oracle_mod):
     torch, lib = env
     rng = np.random.default_rng(3)

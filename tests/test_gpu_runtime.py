@@ -127,8 +127,8 @@ def test_ntok_above_eight_chunks_like_reference(rt, oracle_mod):
 
 
 def test_wide_inputs_pack_through_the_runtime_workspace(rt, oracle_mod):
-    """cols > 8192 (FFN down) takes the pack + packed-matvec path with the runtime's own workspace."""
-    rows, cols, ntok = 40, 17408, 3
+    """cols > 24576 takes the pack + packed-matvec path with the runtime's own workspace."""
+    rows, cols, ntok = 40, 32768, 3
     raw = synth.baseline_rows(T.Q4_K, rows, cols, 8)
     x = np.random.default_rng(8).standard_normal((ntok, cols)).astype(np.float32)
     rt.upload_raw("wide", raw.tobytes(), T.Q4_K, cols, rows)

@@ -286,8 +286,9 @@ size_t vq_xpack_bytes(int cols, int ntok) {
 }
 
 // Activations of up to this many columns are quantized inside the matvec (each workgroup quantizes its own
-// copy: cheaper than a separate quantizer launch for narrow inputs); wider ones are packed first.
-constexpr int kFusedQuantMaxCols = 8192;
+// copy: with one workgroup per CU this beats a separate quantizer launch even for the 17408-wide FFN down
+// input, measured on MI355X); wider ones are packed first.
+constexpr int kFusedQuantMaxCols = 24576;
 
 size_t vq_qmv_workspace_bytes(int cols, int ntok) {
     return cols > kFusedQuantMaxCols ? vq_xpack_bytes(cols, ntok) : 0;

@@ -94,12 +94,13 @@ struct XImage {
     }
 };
 
-// Waves per workgroup: one 16-wave workgroup per CU for one token (the activation image is small), 8 waves
-// otherwise (the image of several tokens takes the LDS that more stage buffers would need).
+// Waves per workgroup: preferably one 16-wave workgroup per CU for one token, 8 waves for several (their
+// activation image takes the LDS that more stage buffers would need); 4 when the image is too wide for that.
 template <int NT>
 constexpr int wg_waves() {
     return NT == 1 ? 16 : 8;
 }
+constexpr int kFallbackWaves = 4;
 
 template <int T>
 struct Stream {
@@ -182,12 +183,11 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, long r) {
 // LDS: [grid table | activation image of the NT tokens | stage buffer per wave | row-part slots]. At start-up
 // the waves load the table and the activations (DMA of the packed record, or quantization of fp32 values),
 // then request their first stage, and meet at one barrier.
-template <int T, int NT, bool XF32>
-__global__ __launch_bounds__(64 * wg_waves<NT>()) void qmv_stream_kernel(const QJobs jobs, int cols,
-                                                                    const void *__restrict__ xin) {
+template <int T, int NT, bool XF32, int NW>
+__global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(const QJobs jobs, int cols, const void *__restrict__ xin) {
     using S = Sl<T>;
     using G = Stream<T>;
-    constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, NL = G::NL, NW = wg_waves<NT>();
+    constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, NL = G::NL;
     constexpr int TB = grid_table_bytes<T>();
     extern __shared__ __attribute__((aligned(1024))) uint8_t s_dyn[];
     __shared__ __attribute__((aligned(1024))) uint8_t s_grid[TB > 0 ? TB : 16];
@@ -648,7 +648,7 @@ inline size_t static_lds_bytes(const void *kernel) {
     return a.sharedSizeBytes;
 }
 
-// Launch geometry: LDS bytes, resident workgroups on the chip, rows per workgroup.
+// Launch geometry: LDS bytes and resident workgroups on the chip.
 struct Geometry {
     size_t lds;  // dynamic LDS bytes
     int wgres;   // workgroups resident at once on the whole chip (0 if the LDS does not fit)
@@ -663,21 +663,23 @@ inline int resident_wgs(const void *kernel, int threads, size_t lds) {
     }
     return n;
 }
-template <int T, int N>
-Geometry geometry(int cols, int slot_floats) {
-    using G = Stream<T>;
-    constexpr int NW = wg_waves<N>();
-    Geometry g;
+// Dynamic LDS of a launch with N tokens, NW waves per workgroup and `slot_floats` row-part slots.
+template <int T, int N, int NW>
+size_t stream_lds(int cols, long slot_floats) {
     const int xreg = (N * XImage(cols).bytes + 1023) & ~1023;
-    g.lds = static_cast<size_t>(xreg) + static_cast<size_t>(NW) * G::STAGE_LDS + 4 * static_cast<size_t>(slot_floats);
+    return static_cast<size_t>(xreg) + static_cast<size_t>(NW) * Stream<T>::STAGE_LDS + 4 * static_cast<size_t>(slot_floats);
+}
+template <int T, int N, int NW>
+Geometry geometry(int cols, long slot_floats) {
+    Geometry g;
+    g.lds = stream_lds<T, N, NW>(cols, slot_floats);
     // Both activation forms: the grid must not depend on the form. Cached per LDS size: the occupancy
-    // queries cost host time on every launch otherwise.
+    // queries cost host time on every launch otherwise. (Without a device the queries fail: then 160 KB and
+    // one workgroup per CU, so that workspace sizes can still be computed.)
     static std::mutex mu;
     static std::unordered_map<long, int> cache;
-    // (Without a device the queries fail: then 160 KB and one workgroup per CU, so that workspace sizes can
-    // still be computed.)
-    static const int max_a = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false>));
-    static const int max_b = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true>));
+    static const int max_a = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false, NW>));
+    static const int max_b = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, NW>));
     const int lim = max_a > 0 && max_b > 0 ? (max_a < max_b ? max_a : max_b) : 160 * 1024;
     if (g.lds > static_cast<size_t>(lim)) {
         g.wgres = 0;
@@ -686,32 +688,20 @@ Geometry geometry(int cols, int slot_floats) {
     std::lock_guard<std::mutex> lock(mu);
     auto it = cache.find(static_cast<long>(g.lds));
     if (it == cache.end()) {
-        const int ra = resident_wgs(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false>), 64 * NW, g.lds);
-        const int rb = resident_wgs(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true>), 64 * NW, g.lds);
+        const int ra = resident_wgs(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false, NW>), 64 * NW, g.lds);
+        const int rb = resident_wgs(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, NW>), 64 * NW, g.lds);
         it = cache.emplace(static_cast<long>(g.lds), ra < rb ? ra : rb).first;
     }
     g.wgres = 256 * it->second;
     return g;
 }
 
-// Dynamic LDS of a launch with N tokens and rwg rows per workgroup.
-template <int T, int N>
-size_t launch_lds(int cols, int rwg) {
-    using G = Stream<T>;
-    const int nu = (cols / 32) / Sl<T>::UG;
-    const long nst = (static_cast<long>(rwg) * nu + G::SU - 1) / G::SU;
-    const int xreg = (N * XImage(cols).bytes + 1023) & ~1023;
-    return static_cast<size_t>(xreg) + static_cast<size_t>(wg_waves<N>()) * G::STAGE_LDS +
-           4 * static_cast<size_t>(nst * rows_per_stage(G::SU, nu) * N);
-}
-
-// Work split of one launch.
+// Work split of one launch: rows per workgroup and workgroups (0 if no geometry fits).
 struct Plan {
-    int rwg, blocks, slot_floats;
-    size_t lds;
+    int rwg, blocks;
 };
-template <int T, int N>
-Plan plan_n(const int *rows, int n, int cols) {
+template <int T, int N, int NW>
+Plan plan_nw(const int *rows, int n, int cols) {
     using G = Stream<T>;
     const int nu = (cols / 32) / Sl<T>::UG;
     const int rs = rows_per_stage(G::SU, nu);
@@ -719,8 +709,8 @@ Plan plan_n(const int *rows, int n, int cols) {
     for (int k = 0; k < n; ++k) total += rows[k];
     Plan p{};
     // Rows per workgroup: one round of workgroups over all rows, but no more stages than the slots hold.
-    const Geometry g0 = geometry<T, N>(cols, kSlotFloats);
-    if (g0.wgres == 0) return p;  // blocks = 0: does not fit
+    const Geometry g0 = geometry<T, N, NW>(cols, kSlotFloats);
+    if (g0.wgres == 0) return p;
     long rwg = (total + g0.wgres - 1) / g0.wgres;
     const long max_st = kSlotFloats / (rs * N);
     const long max_rows = (max_st * G::SU) / nu;  // whole rows whose stages fit (a row range starts on a row)
@@ -730,10 +720,12 @@ Plan plan_n(const int *rows, int n, int cols) {
     long blocks = 0;
     for (int k = 0; k < n; ++k) blocks += (rows[k] + p.rwg - 1) / p.rwg;
     p.blocks = static_cast<int>(blocks);
-    const long nst = (rwg * nu + G::SU - 1) / G::SU;
-    p.slot_floats = static_cast<int>(nst * rs * N);
-    p.lds = geometry<T, N>(cols, p.slot_floats).lds;
     return p;
+}
+template <int T, int N>
+Plan plan_n(const int *rows, int n, int cols) {
+    const Plan p = plan_nw<T, N, wg_waves<N>()>(rows, n, cols);
+    return p.blocks > 0 ? p : plan_nw<T, N, kFallbackWaves>(rows, n, cols);
 }
 template <int T>
 Plan plan_launch(const int *rows, int n, int cols, int n_tok) {
@@ -747,6 +739,34 @@ Plan plan_launch(const int *rows, int n, int cols, int n_tok) {
         case 7: return plan_n<T, 7>(rows, n, cols);
         default: return plan_n<T, 8>(rows, n, cols);
     }
+}
+
+// One launch of N tokens with rows-per-workgroup rwg: the preferred waves per workgroup if the LDS holds
+// them, else kFallbackWaves (rwg comes from the launch's plan, so every token chunk splits the rows alike).
+template <int T, int N>
+int launch_stream(const QJobs &jobs, int cols, const void *xp, bool x_f32, hipStream_t s) {
+    using G = Stream<T>;
+    const int nu = (cols / 32) / Sl<T>::UG;
+    const long nst = (static_cast<long>(jobs.rwg) * nu + G::SU - 1) / G::SU;
+    const long slots = nst * rows_per_stage(G::SU, nu) * N;
+    constexpr int NWP = wg_waves<N>(), NWF = kFallbackWaves;
+    const dim3 grid(static_cast<unsigned>(jobs.blocks));
+    if (geometry<T, N, NWP>(cols, slots).wgres > 0) {
+        const size_t lds = stream_lds<T, N, NWP>(cols, slots);
+        if (x_f32)
+            qmv_stream_kernel<T, N, true, NWP><<<grid, dim3(64 * NWP), lds, s>>>(jobs, cols, xp);
+        else
+            qmv_stream_kernel<T, N, false, NWP><<<grid, dim3(64 * NWP), lds, s>>>(jobs, cols, xp);
+    } else if (geometry<T, N, NWF>(cols, slots).wgres > 0) {
+        const size_t lds = stream_lds<T, N, NWF>(cols, slots);
+        if (x_f32)
+            qmv_stream_kernel<T, N, true, NWF><<<grid, dim3(64 * NWF), lds, s>>>(jobs, cols, xp);
+        else
+            qmv_stream_kernel<T, N, false, NWF><<<grid, dim3(64 * NWF), lds, s>>>(jobs, cols, xp);
+    } else {
+        return static_cast<int>(hipErrorInvalidConfiguration);
+    }
+    return hip_status(hipGetLastError());
 }
 
 // Tokens per launch: as many (<= 8) as the activation image budget holds.
@@ -792,24 +812,17 @@ int launch_quant_jobs(int n, const uint8_t *const *w, const int *rows, float *co
 #endif
         jobs.amax = amax ? amax + static_cast<size_t>(c) * pl.blocks : nullptr;
         const void *xp = static_cast<const uint8_t *>(x) + static_cast<size_t>(c) * tok_bytes;
-        const dim3 grid(static_cast<unsigned>(pl.blocks));
-        // A narrower last chunk keeps the plan's rows per workgroup; its own token count sets the LDS (the
-        // waves per workgroup may differ).
-#define VQ_CASE(N)                                                                                            \
-    case N: {                                                                                                 \
-        const size_t lds = launch_lds<T, N>(cols, pl.rwg);                                                    \
-        if (x_f32)                                                                                            \
-            qmv_stream_kernel<T, N, true><<<grid, dim3(64 * wg_waves<N>()), lds, s>>>(jobs, cols, xp);       \
-        else                                                                                                  \
-            qmv_stream_kernel<T, N, false><<<grid, dim3(64 * wg_waves<N>()), lds, s>>>(jobs, cols, xp);      \
-        break;                                                                                                \
-    }
+        int st = 0;
         switch (m) {
-            VQ_CASE(1) VQ_CASE(2) VQ_CASE(3) VQ_CASE(4) VQ_CASE(5) VQ_CASE(6) VQ_CASE(7)
-            default: VQ_CASE(8)
+            case 1: st = launch_stream<T, 1>(jobs, cols, xp, x_f32, s); break;
+            case 2: st = launch_stream<T, 2>(jobs, cols, xp, x_f32, s); break;
+            case 3: st = launch_stream<T, 3>(jobs, cols, xp, x_f32, s); break;
+            case 4: st = launch_stream<T, 4>(jobs, cols, xp, x_f32, s); break;
+            case 5: st = launch_stream<T, 5>(jobs, cols, xp, x_f32, s); break;
+            case 6: st = launch_stream<T, 6>(jobs, cols, xp, x_f32, s); break;
+            case 7: st = launch_stream<T, 7>(jobs, cols, xp, x_f32, s); break;
+            default: st = launch_stream<T, 8>(jobs, cols, xp, x_f32, s); break;
         }
-#undef VQ_CASE
-        const int st = hip_status(hipGetLastError());
         if (st) return st;
     }
     if (amax) {
