@@ -140,6 +140,16 @@ class Hip:
                                        cols, x.data_ptr(), ntok, self.s())
         assert st == 0, st
 
+    def mixed_f32(self, tys, ws, rows, ys, cols, x, ntok):
+        import ctypes
+
+        n = len(ws)
+        st = self.lib.vq_qmv_group_mixed_f32(n, (ctypes.c_int * n)(*tys),
+                                             (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws]),
+                                             (ctypes.c_int * n)(*rows), (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]),
+                                             cols, x.data_ptr(), ntok, self.s())
+        assert st == 0, st
+
     def lmhead(self, ty, w, rows, cols, x, ntok, out, ws):
         st = self.lib.vq_lmhead_argmax(ty, w.data_ptr(), rows, cols, x.data_ptr(), ntok, out.data_ptr(), None,
                                        ws.data_ptr(), ws.numel(), self.s())
@@ -301,6 +311,13 @@ class Sweep:
                 self.ops.append(("pack", cols))
             j = i
             while j < len(self.plan) and self.plan[j][4] == key:
+                run = [k for k in range(j, min(j + 4, len(self.plan))) if self.plan[k][4] == key]
+                tys = {self.plan[k][1] for k in run}
+                if len(tys) > 1 and not packed and len(tys - {Q8_0}) == 1:
+                    # A main type and Q8_0 small tensors reading one input: one mixed launch.
+                    self.ops.append(("mixed", run))
+                    j = run[-1] + 1
+                    continue
                 k = j
                 while (k < len(self.plan) and k - j < 4 and self.plan[k][4] == key and self.plan[k][1] == ty
                        and self.plan[k][3] == cols):
@@ -320,6 +337,11 @@ class Sweep:
         for op in self.ops:
             if op[0] == "pack":
                 hip.pack(self.x, ntok, op[1], self.xp)
+            elif op[0] == "mixed":
+                idx = op[1]
+                cols = self.plan[idx[0]][3]
+                hip.mixed_f32([self.plan[i][1] for i in idx], [self.w[i] for i in idx], [self.plan[i][2] for i in idx],
+                              [self.ys[self.plan[i][2]] for i in idx], cols, self.x, ntok)
             elif op[0] == "group":
                 idx = op[1]
                 _, ty, _, cols, _ = self.plan[idx[0]]

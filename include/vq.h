@@ -115,9 +115,17 @@ int vq_qmv_group(int type, int n, const uint8_t *const *w, const int *rows, floa
                  const void *xpack, int ntok, void *stream);
 
 /* vq_qmv_group on fp32 activations, quantized inside the matvec by every workgroup (no separate quantizer
- * launch; best for narrow inputs, cols <= 8192). Same numerics as vq_pack_x + vq_qmv_group. */
+ * launch; best up to cols = 24576, which covers a qwen35 FFN down input). Same numerics as vq_pack_x +
+ * vq_qmv_group. */
 int vq_qmv_group_f32(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
                      const float *x, int ntok, void *stream);
+
+/* vq_qmv_group_f32 over matrices of up to two quantized types (types[k] per matrix): a main type and Q8_0,
+ * the type GGUF mixes give a layer's small tensors (e.g. the gated-delta beta/alpha projections next to its
+ * Q5_K qkv/gate). One launch per token chunk of at most 4; other type mixes run as one launch per type. No
+ * counterpart in the reference's per-matrix qmv (qwen_runtime.cu:1860); its effect equals n vq_qmv calls. */
+int vq_qmv_group_mixed_f32(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y,
+                           int cols, const float *x, int ntok, void *stream);
 
 /* Prefill contraction: y[t][r] = W[r] . x[t] for t < M (any M >= 1; meant for M >= 64) on int8 MFMA
  * (v_mfma_i32_16x16x32_i8), activations packed by vq_pack_x. Same quantized numerics as the matvec (rel-L2

@@ -209,6 +209,35 @@ def test_zero_and_extreme_activations(env, oracle_mod):
     assert rel_l2(got[1], ref[1]) <= REL_L2_TOL
 
 
+@pytest.mark.parametrize("mix", [[T.Q5_K, T.Q5_K, T.Q8_0, T.Q8_0], [T.Q8_0, T.Q6_K], [T.Q4_K, T.Q8_0, T.Q4_K],
+                                 [T.IQ4_XS, T.Q8_0], [T.Q5_K, T.Q6_K, T.Q8_0]],
+                         ids=lambda m: "+".join(t.name for t in m))
+@pytest.mark.parametrize("ntok", [1, 3, 6])
+def test_qmv_group_mixed_matches_oracle(env, oracle_mod, mix, ntok):
+    """A grouped launch over a main type and Q8_0 (a gated-delta layer's qkv/gate + beta/alpha) == each matrix
+    on its own; more than 4 tokens run as several launches, and a mix of two non-Q8_0 types as one launch per
+    type."""
+    torch, lib = env
+    cols = 5120
+    rng = np.random.default_rng(ntok + len(mix))
+    rows_list = [[640, 384, 48, 48][k % 4] for k in range(len(mix))]
+    ws = [synth.baseline_rows(ty, r, cols, rng) for ty, r in zip(mix, rows_list)]
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    xd_ = dev(torch, x)
+    wd = [wdev(torch, w) for w in ws]
+    ys = [torch.full((ntok, r), np.nan, dtype=torch.float32, device="cuda") for r in rows_list]
+    n = len(mix)
+    ta = (ctypes.c_int * n)(*[int(t) for t in mix])
+    wa = (ctypes.c_void_p * n)(*[P(t) for t in wd])
+    ra = (ctypes.c_int * n)(*rows_list)
+    ya = (ctypes.c_void_p * n)(*[P(t) for t in ys])
+    assert lib.vq_qmv_group_mixed_f32(n, ta, wa, ra, ya, cols, P(xd_), ntok, None) == 0
+    torch.cuda.synchronize()
+    for ty, w, r, yt in zip(mix, ws, rows_list, ys):
+        ref = oracle_mod.qmv(int(ty), w, r, cols, x, ntok)
+        assert rel_l2(yt.cpu().numpy(), ref) <= REL_L2_TOL, (ty.name, r)
+
+
 def _pack(torch, lib, x: np.ndarray, ntok: int, cols: int):
     xd_ = dev(torch, x.astype(np.float32).reshape(ntok, cols))
     xp = torch.empty(lib.vq_xpack_bytes(cols, ntok), dtype=torch.uint8, device="cuda")

@@ -167,7 +167,16 @@ def test_qmv_group_and_lmhead_argmax(rt, oracle_mod, cols):
         rt.qmv_group(["ga", "t_missing_type"], "gx", ["gya"], ntok)
     with pytest.raises(KeyError):
         rt.qmv_group(["ga", "nope"], "gx", ["gya", "gyb"], ntok)
-    for n in ("ga", "gb"):
+    # A main type plus Q8_0 small tensors in one group (a gated-delta layer's qkv + beta).
+    q8 = synth.baseline_rows(T.Q8_0, 48, cols, rng)
+    rt.upload_raw("gq8", q8.tobytes(), T.Q8_0, cols, 48)
+    rt.alloc("gyq", 48 * ntok)
+    rt.qmv_group(["ga", "gq8"], "gx", ["gya", "gyq"], ntok)
+    ya = np.array(rt.read_floats("gya"), np.float32).reshape(ntok, 96)
+    yq = np.array(rt.read_floats("gyq"), np.float32).reshape(ntok, 48)
+    assert rel_l2(ya, ra) <= 1e-5
+    assert rel_l2(yq, oracle_mod.qmv(int(T.Q8_0), q8, 48, cols, x, ntok)) <= 1e-5
+    for n in ("ga", "gb", "gq8"):
         rt.free(n)
 
 

@@ -29,6 +29,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_int_partials": (I, [I, P, I, I, P, I, P, P]),
     "vq_qmv_group": (I, [I, I, P, P, P, I, P, I, P]),
     "vq_qmv_group_f32": (I, [I, I, P, P, P, I, P, I, P]),
+    "vq_qmv_group_mixed_f32": (I, [I, P, P, P, P, I, P, I, P]),
     "vq_qgemm": (I, [I, P, I, I, P, I, P, P]),
     "vq_lmhead_argmax_workspace_bytes": (SZ, [I, I, I, I]),
     "vq_lmhead_argmax": (I, [I, P, I, I, P, I, P, P, P, SZ, P]),

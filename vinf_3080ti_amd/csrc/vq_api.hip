@@ -400,6 +400,52 @@ int vq_qmv_group_f32(int type, int n, const uint8_t *const *w, const int *rows, 
     return qmv_group_any(type, n, w, rows, y, cols, x, true, ntok, stream);
 }
 
+int vq_qmv_group_mixed_f32(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y,
+                           int cols, const float *x, int ntok, void *stream) {
+    if (n < 1 || n > VQ_MAX_GROUP || !types || !w || !rows || !y) return VQ_ERR_ARG;
+    int main_type = -1;
+    bool mixed = false;
+    for (int k = 0; k < n; ++k) {
+        if (types[k] == VQ_F32 || types[k] == VQ_F16) return VQ_ERR_TYPE;
+        const int st = check_matrix(types[k], rows[k], cols);
+        if (st) return st;
+        if (!w[k] || !y[k] || misaligned16(w[k])) return VQ_ERR_ARG;
+        if (types[k] != VQ_Q8_0) {
+            if (main_type >= 0 && types[k] != main_type) mixed = true;  // two non-Q8_0 types
+            main_type = types[k];
+        }
+    }
+    if (!x || misaligned16(x)) return VQ_ERR_ARG;
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    if (main_type < 0) main_type = VQ_Q8_0;
+    if (mixed) {
+        // Other mixes: one grouped launch per type, in order of first appearance.
+        bool done[VQ_MAX_GROUP] = {};
+        for (int k = 0; k < n; ++k) {
+            if (done[k]) continue;
+            const uint8_t *wk[VQ_MAX_GROUP];
+            int rk[VQ_MAX_GROUP];
+            float *yk[VQ_MAX_GROUP];
+            int m = 0;
+            for (int j = k; j < n; ++j)
+                if (!done[j] && types[j] == types[k]) {
+                    wk[m] = w[j];
+                    rk[m] = rows[j];
+                    yk[m] = y[j];
+                    ++m;
+                    done[j] = true;
+                }
+            const int st = vq_qmv_group_f32(types[k], m, wk, rk, yk, cols, x, ntok, stream);
+            if (st) return st;
+        }
+        return VQ_OK;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return dispatch_quant(main_type, [&](auto tc) {
+        return vq::launch_mixed_q8<decltype(tc)::value>(n, types, w, rows, y, cols, x, ntok, s);
+    });
+}
+
 int vq_qgemm(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *stream) {
     int st = check_matrix(type, rows, cols);
     if (st) return st;

@@ -16,6 +16,11 @@ int launch_quant_jobs(int n, const uint8_t *const *w, const int *rows, float *co
                       bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s);
 template <int T>
 long argmax_waves(int rows, int cols, int ntok);
+// y_j = W_j x for n <= 4 matrices sharing cols and fp32 x, of type T or Q8_0 (types[j]), in one launch.
+constexpr int kMixedMaxTokens = 4;  // tokens per launch of a mixed-type group (more go in several launches)
+template <int T>
+int launch_mixed_q8(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                    const float *x, int ntok, hipStream_t s);
 // Prefill contraction on int8 MFMA: y[t][r] = W[r] . x[t] for t < M, activations packed (vq_pack_x).
 template <int T>
 int launch_gemm(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int M, float *y,

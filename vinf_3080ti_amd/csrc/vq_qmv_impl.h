@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
 
 #include "vq_qmv.h"
@@ -143,11 +144,12 @@ struct QJob {
     const uint8_t *w;
     float *y;  // [NT][rows], or null (argmax only)
     int rows, b0;
+    int rwg;    // rows per workgroup
+    int type;   // GGUF type (a launch may mix its main type with one other, see qmv_stream_kernel)
 };
 struct QJobs {
     QJob j[kMaxJobs];
     int n;
-    int rwg;      // rows per workgroup
     int blocks;   // workgroups of the launch
     unsigned long long *amax;  // null, or [NT][blocks] per-workgroup argmax keys (see argmax_key)
 #ifdef VQ_TIMING
@@ -184,7 +186,7 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, long r) {
 // the waves load the table and the activations (DMA of the packed record, or quantization of fp32 values),
 // then request their first stage, and meet at one barrier.
 template <int T, int NT, bool XF32, int NW>
-__global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(const QJobs jobs, int cols, const void *__restrict__ xin) {
+__device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const int cols, const void *__restrict__ xin) {
     using S = Sl<T>;
     using G = Stream<T>;
     constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, NL = G::NL;
@@ -210,16 +212,13 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(const QJobs jobs, i
     float *const slots = reinterpret_cast<float *>(s_dyn + xreg + NW * G::STAGE_LDS);
     const int rs = rows_per_stage(SU, nu);
 
-    // This workgroup's job, rows and stages (all 32-bit unit indices: a matrix has < 2^31 units).
+    // This workgroup's rows and stages (all 32-bit unit indices: a matrix has < 2^31 units).
     const int b = blockIdx.x;
-    int jb = 0;
-#pragma unroll
-    for (int k = 1; k < kMaxJobs; ++k) jb = (k < jobs.n && b >= jobs.j[k].b0) ? k : jb;
     const uint8_t *const w = jobs.j[jb].w;
     float *const y = jobs.j[jb].y;
-    const int rows = jobs.j[jb].rows;
-    const int R0 = (b - jobs.j[jb].b0) * jobs.rwg;
-    const int R1 = R0 + jobs.rwg < rows ? R0 + jobs.rwg : rows;
+    const int rows = jobs.j[jb].rows, rwg = jobs.j[jb].rwg;
+    const int R0 = (b - jobs.j[jb].b0) * rwg;
+    const int R1 = R0 + rwg < rows ? R0 + rwg : rows;
     const int U0 = R0 * nu, U1 = R1 * nu;
     const int nst = R0 < rows ? (U1 - U0 + SU - 1) / SU : 0;
     // Stage s: 16-byte chunks [c0, c1) with c0 the one holding its first byte and c1 past the one holding the
@@ -529,6 +528,24 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(const QJobs jobs, i
 #endif
 }
 
+// The kernel: workgroup b runs the body of its job's type. T2 == T for one-type launches; otherwise jobs of
+// type T2 (a layer's small tensors, e.g. Q8_0, next to its main matrices) share the launch and its
+// activations, and the workgroup size and LDS are the larger of the two types'.
+template <int T, int T2, int NT, bool XF32, int NW>
+__global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(const QJobs jobs, int cols, const void *__restrict__ xin) {
+    const int b = blockIdx.x;
+    int jb = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxJobs; ++k) jb = (k < jobs.n && b >= jobs.j[k].b0) ? k : jb;
+    if constexpr (T2 != T) {
+        if (jobs.j[jb].type == T2) {
+            stream_wg<T2, NT, XF32, NW>(jobs, jb, cols, xin);
+            return;
+        }
+    }
+    stream_wg<T, NT, XF32, NW>(jobs, jb, cols, xin);
+}
+
 // Final argmax over the per-workgroup keys: one workgroup per token; INT32_MAX when no value qualifies.
 static __global__ __launch_bounds__(256) void argmax_keys_kernel(const unsigned long long *__restrict__ keys, int n,
                                                           int32_t *__restrict__ out) {
@@ -649,12 +666,8 @@ inline size_t static_lds_bytes(const void *kernel) {
 }
 
 // Launch geometry: LDS bytes and resident workgroups on the chip.
-struct Geometry {
-    size_t lds;  // dynamic LDS bytes
-    int wgres;   // workgroups resident at once on the whole chip (0 if the LDS does not fit)
-};
-// Resident workgroups per CU of a qmv_stream_kernel instantiation at `lds` dynamic LDS bytes (VGPR, LDS and
-// wave limits, as the runtime computes them); 1 if the query fails.
+// Resident workgroups per CU of a kernel at `lds` dynamic LDS bytes (VGPR, LDS and wave limits, as the
+// runtime computes them); 1 if the query fails.
 inline int resident_wgs(const void *kernel, int threads, size_t lds) {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, lds) != hipSuccess || n < 1) {
@@ -663,108 +676,145 @@ inline int resident_wgs(const void *kernel, int threads, size_t lds) {
     }
     return n;
 }
-// Dynamic LDS of a launch with N tokens, NW waves per workgroup and `slot_floats` row-part slots.
-template <int T, int N, int NW>
-size_t stream_lds(int cols, long slot_floats) {
-    const int xreg = (N * XImage(cols).bytes + 1023) & ~1023;
-    return static_cast<size_t>(xreg) + static_cast<size_t>(NW) * Stream<T>::STAGE_LDS + 4 * static_cast<size_t>(slot_floats);
+// Row-part slots (floats) of a workgroup of type TT with rwg rows and N tokens, and the most rows they allow.
+template <int TT, int N>
+long slot_floats(int cols, long rwg) {
+    using G = Stream<TT>;
+    const int nu = (cols / 32) / Sl<TT>::UG;
+    return (rwg * nu + G::SU - 1) / G::SU * rows_per_stage(G::SU, nu) * N;
 }
-template <int T, int N, int NW>
-Geometry geometry(int cols, long slot_floats) {
-    Geometry g;
-    g.lds = stream_lds<T, N, NW>(cols, slot_floats);
-    // Both activation forms: the grid must not depend on the form. Cached per LDS size: the occupancy
-    // queries cost host time on every launch otherwise. (Without a device the queries fail: then 160 KB and
-    // one workgroup per CU, so that workspace sizes can still be computed.)
+template <int TT, int N>
+long max_rwg(int cols) {
+    using G = Stream<TT>;
+    const int nu = (cols / 32) / Sl<TT>::UG;
+    const long max_st = kSlotFloats / (rows_per_stage(G::SU, nu) * N);
+    const long r = (max_st * G::SU) / nu;  // whole rows whose stages fit (a row range starts on a row)
+    return r > 0 ? r : 1;
+}
+// Dynamic LDS of a workgroup of type TT with N tokens, NW waves and `slots` row-part slots.
+template <int TT, int N, int NW>
+size_t stream_lds(int cols, long slots) {
+    const int xreg = (N * XImage(cols).bytes + 1023) & ~1023;
+    return static_cast<size_t>(xreg) + static_cast<size_t>(NW) * Stream<TT>::STAGE_LDS + 4 * static_cast<size_t>(slots);
+}
+// Resident workgroups on the chip of qmv_stream_kernel<T, T2, N, *, NW> at `lds` bytes, 0 if the LDS does not
+// fit. Both activation forms: the grid must not depend on the form. Cached per LDS size: the occupancy
+// queries cost host time on every launch otherwise. (Without a device the queries fail: then 160 KB and one
+// workgroup per CU, so that workspace sizes can still be computed.)
+template <int T, int T2, int N, int NW>
+int resident_chip(size_t lds) {
     static std::mutex mu;
     static std::unordered_map<long, int> cache;
-    static const int max_a = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false, NW>));
-    static const int max_b = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, NW>));
+    static const int max_a = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, T2, N, false, NW>));
+    static const int max_b = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_stream_kernel<T, T2, N, true, NW>));
     const int lim = max_a > 0 && max_b > 0 ? (max_a < max_b ? max_a : max_b) : 160 * 1024;
-    if (g.lds > static_cast<size_t>(lim)) {
-        g.wgres = 0;
-        return g;
-    }
+    if (lds > static_cast<size_t>(lim)) return 0;
     std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(static_cast<long>(g.lds));
+    auto it = cache.find(static_cast<long>(lds));
     if (it == cache.end()) {
-        const int ra = resident_wgs(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, false, NW>), 64 * NW, g.lds);
-        const int rb = resident_wgs(reinterpret_cast<const void *>(&qmv_stream_kernel<T, N, true, NW>), 64 * NW, g.lds);
-        it = cache.emplace(static_cast<long>(g.lds), ra < rb ? ra : rb).first;
+        const int ra = resident_wgs(reinterpret_cast<const void *>(&qmv_stream_kernel<T, T2, N, false, NW>), 64 * NW, lds);
+        const int rb = resident_wgs(reinterpret_cast<const void *>(&qmv_stream_kernel<T, T2, N, true, NW>), 64 * NW, lds);
+        it = cache.emplace(static_cast<long>(lds), ra < rb ? ra : rb).first;
     }
-    g.wgres = 256 * it->second;
-    return g;
+    return 256 * it->second;
 }
 
-// Work split of one launch: rows per workgroup and workgroups (0 if no geometry fits).
+// Work split of one launch: rows per workgroup of each job, workgroups, waves per workgroup (0 blocks if no
+// geometry fits). types[k] is T or T2.
 struct Plan {
-    int rwg, blocks;
+    int rwg[kMaxJobs], b0[kMaxJobs];
+    int blocks, nw;
 };
-template <int T, int N, int NW>
-Plan plan_nw(const int *rows, int n, int cols) {
-    using G = Stream<T>;
-    const int nu = (cols / 32) / Sl<T>::UG;
-    const int rs = rows_per_stage(G::SU, nu);
-    long total = 0;
-    for (int k = 0; k < n; ++k) total += rows[k];
+template <int T, int T2, int N, int NW>
+size_t plan_lds(const int *types, int n, int cols, const int *rwg) {
+    size_t lds = 0;
+    for (int k = 0; k < n; ++k) {
+        const size_t l = types[k] == T2 && T2 != T ? stream_lds<T2, N, NW>(cols, slot_floats<T2, N>(cols, rwg[k]))
+                                                   : stream_lds<T, N, NW>(cols, slot_floats<T, N>(cols, rwg[k]));
+        lds = l > lds ? l : lds;
+    }
+    return lds;
+}
+template <int T, int T2, int N, int NW>
+Plan plan_nw(const int *types, const int *rows, int n, int cols) {
     Plan p{};
-    // Rows per workgroup: one round of workgroups over all rows, but no more stages than the slots hold.
-    const Geometry g0 = geometry<T, N, NW>(cols, kSlotFloats);
-    if (g0.wgres == 0) return p;
-    long rwg = (total + g0.wgres - 1) / g0.wgres;
-    const long max_st = kSlotFloats / (rs * N);
-    const long max_rows = (max_st * G::SU) / nu;  // whole rows whose stages fit (a row range starts on a row)
-    if (rwg > max_rows) rwg = max_rows;
-    if (rwg < 1) rwg = 1;
-    p.rwg = static_cast<int>(rwg);
-    long blocks = 0;
-    for (int k = 0; k < n; ++k) blocks += (rows[k] + p.rwg - 1) / p.rwg;
-    p.blocks = static_cast<int>(blocks);
+    int cap[kMaxJobs];
+    for (int k = 0; k < n; ++k)
+        cap[k] = static_cast<int>(types[k] == T2 && T2 != T ? max_rwg<T2, N>(cols) : max_rwg<T, N>(cols));
+    // One round of workgroups, shared out in proportion to each job's bytes (at least one each).
+    const int wres = resident_chip<T, T2, N, NW>(plan_lds<T, T2, N, NW>(types, n, cols, cap));
+    if (wres == 0) return p;
+    double bytes[kMaxJobs], total = 0.0;
+    for (int k = 0; k < n; ++k) {
+        int bs = 0, ts = 0;
+        vq_traits(types[k], &bs, &ts);
+        bytes[k] = static_cast<double>(rows[k]) * (cols / bs) * ts;
+        total += bytes[k];
+    }
+    int blocks = 0;
+    for (int k = 0; k < n; ++k) {
+        long nb = static_cast<long>(wres * bytes[k] / total);
+        if (nb < 1) nb = 1;
+        long rwg = (rows[k] + nb - 1) / nb;
+        if (rwg > cap[k]) rwg = cap[k];
+        if (rwg < 1) rwg = 1;
+        p.rwg[k] = static_cast<int>(rwg);
+        p.b0[k] = blocks;
+        blocks += static_cast<int>((rows[k] + rwg - 1) / rwg);
+    }
+    p.blocks = blocks;
+    p.nw = NW;
     return p;
 }
-template <int T, int N>
-Plan plan_n(const int *rows, int n, int cols) {
-    const Plan p = plan_nw<T, N, wg_waves<N>()>(rows, n, cols);
-    return p.blocks > 0 ? p : plan_nw<T, N, kFallbackWaves>(rows, n, cols);
+template <int T, int T2, int N>
+Plan plan_n(const int *types, const int *rows, int n, int cols) {
+    const Plan p = plan_nw<T, T2, N, wg_waves<N>()>(types, rows, n, cols);
+    return p.blocks > 0 ? p : plan_nw<T, T2, N, kFallbackWaves>(types, rows, n, cols);
 }
-template <int T>
-Plan plan_launch(const int *rows, int n, int cols, int n_tok) {
-    switch (n_tok) {
-        case 1: return plan_n<T, 1>(rows, n, cols);
-        case 2: return plan_n<T, 2>(rows, n, cols);
-        case 3: return plan_n<T, 3>(rows, n, cols);
-        case 4: return plan_n<T, 4>(rows, n, cols);
-        case 5: return plan_n<T, 5>(rows, n, cols);
-        case 6: return plan_n<T, 6>(rows, n, cols);
-        case 7: return plan_n<T, 7>(rows, n, cols);
-        default: return plan_n<T, 8>(rows, n, cols);
-    }
+// Most tokens per launch: 8, or kMixedMaxTokens for mixed-type launches (fewer kernel instantiations).
+template <int T, int T2>
+constexpr int max_tokens() {
+    return T2 == T ? 8 : kMixedMaxTokens;
+}
+// f(std::integral_constant<int, N>) for N = n_tok clamped to [1, NMAX].
+template <int NMAX, typename F>
+auto with_tokens(int n_tok, F &&f) {
+    if (n_tok <= 1 || NMAX == 1) return f(std::integral_constant<int, 1>{});
+    if constexpr (NMAX >= 2) if (n_tok == 2 || NMAX == 2) return f(std::integral_constant<int, 2>{});
+    if constexpr (NMAX >= 3) if (n_tok == 3 || NMAX == 3) return f(std::integral_constant<int, 3>{});
+    if constexpr (NMAX >= 4) if (n_tok == 4 || NMAX == 4) return f(std::integral_constant<int, 4>{});
+    if constexpr (NMAX >= 5) if (n_tok == 5 || NMAX == 5) return f(std::integral_constant<int, 5>{});
+    if constexpr (NMAX >= 6) if (n_tok == 6 || NMAX == 6) return f(std::integral_constant<int, 6>{});
+    if constexpr (NMAX >= 7) if (n_tok == 7 || NMAX == 7) return f(std::integral_constant<int, 7>{});
+    return f(std::integral_constant<int, (NMAX >= 8 ? 8 : NMAX)>{});
+}
+template <int T, int T2>
+Plan plan_launch(const int *types, const int *rows, int n, int cols, int n_tok) {
+    return with_tokens<max_tokens<T, T2>()>(n_tok, [&](auto nt) { return plan_n<T, T2, decltype(nt)::value>(types, rows, n, cols); });
 }
 
-// One launch of N tokens with rows-per-workgroup rwg: the preferred waves per workgroup if the LDS holds
-// them, else kFallbackWaves (rwg comes from the launch's plan, so every token chunk splits the rows alike).
-template <int T, int N>
-int launch_stream(const QJobs &jobs, int cols, const void *xp, bool x_f32, hipStream_t s) {
-    using G = Stream<T>;
-    const int nu = (cols / 32) / Sl<T>::UG;
-    const long nst = (static_cast<long>(jobs.rwg) * nu + G::SU - 1) / G::SU;
-    const long slots = nst * rows_per_stage(G::SU, nu) * N;
+// One launch of N tokens with the plan's rows per workgroup: the preferred waves per workgroup if the LDS
+// holds them, else kFallbackWaves (the rows per workgroup come from the launch's plan, so every token chunk
+// splits the rows alike).
+template <int T, int T2, int N>
+int launch_stream(const QJobs &jobs, const int *types, int cols, const void *xp, bool x_f32, hipStream_t s) {
+    int rwg[kMaxJobs];
+    for (int k = 0; k < jobs.n; ++k) rwg[k] = jobs.j[k].rwg;
     constexpr int NWP = wg_waves<N>(), NWF = kFallbackWaves;
     const dim3 grid(static_cast<unsigned>(jobs.blocks));
-    if (geometry<T, N, NWP>(cols, slots).wgres > 0) {
-        const size_t lds = stream_lds<T, N, NWP>(cols, slots);
+    const size_t ldsp = plan_lds<T, T2, N, NWP>(types, jobs.n, cols, rwg);
+    if (resident_chip<T, T2, N, NWP>(ldsp) > 0) {
         if (x_f32)
-            qmv_stream_kernel<T, N, true, NWP><<<grid, dim3(64 * NWP), lds, s>>>(jobs, cols, xp);
+            qmv_stream_kernel<T, T2, N, true, NWP><<<grid, dim3(64 * NWP), ldsp, s>>>(jobs, cols, xp);
         else
-            qmv_stream_kernel<T, N, false, NWP><<<grid, dim3(64 * NWP), lds, s>>>(jobs, cols, xp);
-    } else if (geometry<T, N, NWF>(cols, slots).wgres > 0) {
-        const size_t lds = stream_lds<T, N, NWF>(cols, slots);
-        if (x_f32)
-            qmv_stream_kernel<T, N, true, NWF><<<grid, dim3(64 * NWF), lds, s>>>(jobs, cols, xp);
-        else
-            qmv_stream_kernel<T, N, false, NWF><<<grid, dim3(64 * NWF), lds, s>>>(jobs, cols, xp);
+            qmv_stream_kernel<T, T2, N, false, NWP><<<grid, dim3(64 * NWP), ldsp, s>>>(jobs, cols, xp);
     } else {
-        return static_cast<int>(hipErrorInvalidConfiguration);
+        const size_t ldsf = plan_lds<T, T2, N, NWF>(types, jobs.n, cols, rwg);
+        if (resident_chip<T, T2, N, NWF>(ldsf) == 0) return static_cast<int>(hipErrorInvalidConfiguration);
+        if (x_f32)
+            qmv_stream_kernel<T, T2, N, true, NWF><<<grid, dim3(64 * NWF), ldsf, s>>>(jobs, cols, xp);
+        else
+            qmv_stream_kernel<T, T2, N, false, NWF><<<grid, dim3(64 * NWF), ldsf, s>>>(jobs, cols, xp);
     }
     return hip_status(hipGetLastError());
 }
@@ -779,50 +829,42 @@ inline int token_chunk(int cols) {
 template <int T>
 long argmax_waves(int rows, int cols, int ntok) {
     const int m = ntok < token_chunk(cols) ? ntok : token_chunk(cols);
-    return plan_launch<T>(&rows, 1, cols, m).blocks;
+    const int ty = T;
+    return plan_launch<T, T>(&ty, &rows, 1, cols, m).blocks;
 }
 
-// y_j = W_j x for the n jobs (same type and cols), x fp32 (quantized in-kernel) or packed. With `amax`
+// y_j = W_j x for the n jobs (types T or T2, same cols), x fp32 (quantized in-kernel) or packed. With `amax`
 // ([ntok][argmax_waves] keys, single job), also amax_out[t] = argmax_r y[t][r].
-template <int T>
-int launch_quant_jobs(int n, const uint8_t *const *w, const int *rows, float *const *y, int cols, const void *x,
-                      bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s) {
+template <int T, int T2>
+int launch_jobs(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                const void *x, bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s) {
     if (n < 1 || n > kMaxJobs || (amax && n != 1)) return static_cast<int>(hipErrorInvalidValue);
     const size_t tok_bytes = x_f32 ? static_cast<size_t>(cols) * 4 : static_cast<size_t>(vq_xpack_stride(cols));
-    const int chunk = token_chunk(cols);
+    const int chunk = token_chunk(cols) < max_tokens<T, T2>() ? token_chunk(cols) : max_tokens<T, T2>();
     // One split for every token chunk (the first is the widest), so the argmax key layout is the same.
-    const Plan pl = plan_launch<T>(rows, n, cols, ntok < chunk ? ntok : chunk);
+    const Plan pl = plan_launch<T, T2>(types, rows, n, cols, ntok < chunk ? ntok : chunk);
     if (pl.blocks <= 0) return static_cast<int>(hipErrorInvalidConfiguration);
     for (int c = 0; c < ntok; c += chunk) {
         const int m = ntok - c < chunk ? ntok - c : chunk;
         QJobs jobs{};
         jobs.n = n;
-        int b0 = 0;
         for (int k = 0; k < n; ++k) {
             jobs.j[k].w = w[k];
             jobs.j[k].y = y[k] ? y[k] + static_cast<size_t>(c) * rows[k] : nullptr;
             jobs.j[k].rows = rows[k];
-            jobs.j[k].b0 = b0;
-            b0 += (rows[k] + pl.rwg - 1) / pl.rwg;
+            jobs.j[k].b0 = pl.b0[k];
+            jobs.j[k].rwg = pl.rwg[k];
+            jobs.j[k].type = types[k];
         }
-        jobs.rwg = pl.rwg;
         jobs.blocks = pl.blocks;
 #ifdef VQ_TIMING
         jobs.tm = static_cast<unsigned long long *>(vq_debug_timing_buffer());
 #endif
         jobs.amax = amax ? amax + static_cast<size_t>(c) * pl.blocks : nullptr;
         const void *xp = static_cast<const uint8_t *>(x) + static_cast<size_t>(c) * tok_bytes;
-        int st = 0;
-        switch (m) {
-            case 1: st = launch_stream<T, 1>(jobs, cols, xp, x_f32, s); break;
-            case 2: st = launch_stream<T, 2>(jobs, cols, xp, x_f32, s); break;
-            case 3: st = launch_stream<T, 3>(jobs, cols, xp, x_f32, s); break;
-            case 4: st = launch_stream<T, 4>(jobs, cols, xp, x_f32, s); break;
-            case 5: st = launch_stream<T, 5>(jobs, cols, xp, x_f32, s); break;
-            case 6: st = launch_stream<T, 6>(jobs, cols, xp, x_f32, s); break;
-            case 7: st = launch_stream<T, 7>(jobs, cols, xp, x_f32, s); break;
-            default: st = launch_stream<T, 8>(jobs, cols, xp, x_f32, s); break;
-        }
+        const int st = with_tokens<max_tokens<T, T2>()>(m, [&](auto nt) {
+            return launch_stream<T, T2, decltype(nt)::value>(jobs, types, cols, xp, x_f32, s);
+        });
         if (st) return st;
     }
     if (amax) {
@@ -830,6 +872,24 @@ int launch_quant_jobs(int n, const uint8_t *const *w, const int *rows, float *co
         return hip_status(hipGetLastError());
     }
     return 0;
+}
+
+template <int T>
+int launch_quant_jobs(int n, const uint8_t *const *w, const int *rows, float *const *y, int cols, const void *x,
+                      bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s) {
+    int types[kMaxJobs];
+    for (int k = 0; k < kMaxJobs; ++k) types[k] = T;
+    return launch_jobs<T, T>(n, types, w, rows, y, cols, x, x_f32, ntok, amax, amax_out, s);
+}
+
+// Jobs of type T and Q8_0 in one launch (fp32 activations; token chunks of at most kMixedMaxTokens).
+template <int T>
+int launch_mixed_q8(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                    const float *x, int ntok, hipStream_t s) {
+    if constexpr (T == VQ_Q8_0)
+        return launch_jobs<T, T>(n, types, w, rows, y, cols, x, true, ntok, nullptr, nullptr, s);
+    else
+        return launch_jobs<T, VQ_Q8_0>(n, types, w, rows, y, cols, x, true, ntok, nullptr, nullptr, s);
 }
 
 template <int T>
@@ -864,6 +924,8 @@ int launch_dequant(const uint8_t *w, int rows, int cols, long rb, float *out, hi
     template int vq::launch_quant_jobs<T>(int, const uint8_t *const *, const int *, float *const *, int, const void *, \
                                           bool, int, unsigned long long *, int32_t *, hipStream_t);                 \
     template long vq::argmax_waves<T>(int, int, int);                                                                \
+    template int vq::launch_mixed_q8<T>(int, const int *, const uint8_t *const *, const int *, float *const *, int, \
+                                        const float *, int, hipStream_t);                                          \
     template int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \
     template int vq::launch_mfma<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, float *,       \
                                     hipStream_t);                                                                \

@@ -255,17 +255,18 @@ class Runtime:
         _lib.check(st, "qmv launch")
 
     def qmv_group(self, weights: Sequence[str], x: str, ys: Sequence[str], ntok: int = 1) -> None:
-        """ys[k][t] = W_k x[t] for up to 4 weights of one quantized type and width that read the same input,
-        in one launch (a layer's gate/up or q/k/v). Same results as one qmv per weight; no counterpart in
-        the reference's per-op runtime, whose callers issue one qmv each (qwen_gpu.py:865-867)."""
+        """ys[k][t] = W_k x[t] for up to 4 quantized weights of one width that read the same input, in one
+        launch (a layer's gate/up or q/k/v; one quantized type, or one type plus Q8_0 small tensors). Same
+        results as one qmv per weight; no counterpart in the reference's per-op runtime, whose callers issue
+        one qmv each (qwen_gpu.py:865-867)."""
         if not 1 <= len(weights) <= 4 or len(weights) != len(ys):
             raise ValueError("qmv_group takes 1 to 4 weights and as many outputs")
         if ntok < 1:
             raise ValueError("ntok must be positive")
         ts = [self._tensor(w) for w in weights]
         t0 = ts[0]
-        if any(t.type != t0.type or t.cols != t0.cols for t in ts) or t0.type in (0, 1):
-            raise ValueError("qmv_group weights must share one quantized type and cols")
+        if any(t.cols != t0.cols or t.type in (0, 1) for t in ts):
+            raise ValueError("qmv_group weights must be quantized and share cols")
         _check_qmv_args(weights[0], t0.cols, ntok)
         xb = self._f32_buffer(x, t0.cols * ntok)
         yb = [self._f32_buffer(y, t.rows * ntok) for y, t in zip(ys, ts)]
@@ -274,7 +275,11 @@ class Runtime:
         ra = (ctypes.c_int * n)(*[t.rows for t in ts])
         ya = (ctypes.c_void_p * n)(*[b.data_ptr() for b in yb])
         nws = self._lib.vq_qmv_workspace_bytes(t0.cols, ntok)
-        if nws == 0:
+        if any(t.type != t0.type for t in ts):
+            # Mixed types (e.g. Q5_K projections with Q8_0 small tensors): one launch for a main type + Q8_0.
+            ta = (ctypes.c_int * n)(*[t.type for t in ts])
+            st = self._lib.vq_qmv_group_mixed_f32(n, ta, wa, ra, ya, t0.cols, xb.data_ptr(), ntok, self._stream())
+        elif nws == 0:
             st = self._lib.vq_qmv_group_f32(t0.type, n, wa, ra, ya, t0.cols, xb.data_ptr(), ntok, self._stream())
         else:
             xp = self._workspace(nws)
