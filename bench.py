@@ -166,10 +166,29 @@ def make_weights(torch, ty, rows, cols, seed, copies=1):
     return [torch_baseline_rows(ty, rows, cols, seed + 7919 * c, "cuda") for c in range(copies)]
 
 
-def time_kernel_loop(torch, fn, n_iter):
-    """Average duration (ms) of fn() launches bracketed by HIP events on the current stream."""
+def time_kernel_loop(torch, fn, n_iter, graph=True):
+    """Average duration (ms) of fn(i) for i < n_iter, bracketed by HIP events on the stream the launches run
+    on. With graph=True the n_iter launches are captured once in a hipGraph and replayed (back-to-back
+    kernels, as in a decode step, without the host's per-launch cost); else launched eagerly."""
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                for i in range(n_iter):
+                    fn(i)
+        torch.cuda.synchronize()
+        g.replay()  # warm
+        torch.cuda.synchronize()
+        start.record()
+        g.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        del g
+        return start.elapsed_time(stop) / n_iter
     start.record()
     for i in range(n_iter):
         fn(i)
@@ -179,8 +198,9 @@ def time_kernel_loop(torch, fn, n_iter):
 
 
 def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=640 << 20, group=1):
-    """Per-launch µs and GB/s of the matvec kernel alone: `group` matrices of rows x cols (one vq_qmv_group
-    launch) on activations packed beforehand, rotating over weight copies larger than the MALL."""
+    """Per-launch µs and GB/s of the matvec kernel alone: `group` matrices of rows x cols (one
+    vq_qmv_group_f32 launch, which quantizes the fp32 activations in-kernel, as in the sweep), rotating over
+    weight copies larger than the MALL; launches captured in a hipGraph."""
     from vinf_3080ti_amd import row_bytes
 
     nbytes = rows * row_bytes(ty, cols) * group
@@ -193,7 +213,7 @@ def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=
 
     def launch(i):
         c = i % copies
-        hip.group(ty, ws[c * group:(c + 1) * group], [rows] * group, ys, cols, xp, ntok)
+        hip.group_f32(ty, ws[c * group:(c + 1) * group], [rows] * group, ys, cols, x, ntok)
 
     for i in range(copies):  # warm-up
         launch(i)
@@ -236,10 +256,11 @@ def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 <
             "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
 
 
-def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20):
+def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=None):
     """the qwen35 SwiGLU MLP block's three matvecs (gate/up Q3_K 17408x5120, down
-    Q6_K 5120x17408) at batch ntok, weights rotating beyond the MALL. Small batches (>= 6 tokens) take the
-    int8-MFMA path through vq_qmv with its workspace; smaller ones one pack + grouped gate/up + down launch."""
+    Q6_K 5120x17408) at batch ntok, weights rotating beyond the MALL. mfma=True: the int8-MFMA small-batch
+    path through vq_qmv with its workspace (what vq_qmv picks from 6 tokens on); else the streaming kernel
+    (grouped gate/up + down, activations quantized in-kernel). Default: as vq_qmv routes."""
     from vinf_3080ti_amd import row_bytes
 
     H, F = 5120, 17408
@@ -252,10 +273,9 @@ def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20):
     g, u, d = (torch.empty(ntok, F, device="cuda"), torch.empty(ntok, F, device="cuda"),
                torch.empty(ntok, H, device="cuda"))
     lib = hip.lib
-    mfma = ntok >= 6
+    mfma = ntok >= 6 if mfma is None else mfma
     nws = max(lib.vq_qmv_workspace_bytes_for(Q3_K, F, H, ntok), lib.vq_qmv_workspace_bytes_for(Q6_K, H, F, ntok))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
-    xp, hp = hip.xpack(H, ntok), hip.xpack(F, ntok)
 
     def launch(i):
         wg, wu, wd = sets[i % copies]
@@ -265,10 +285,8 @@ def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20):
                                 yo.data_ptr(), ws.data_ptr(), nws, hip.s())
                 assert st == 0, st
         else:
-            hip.pack(x, ntok, H, xp)
-            hip.group(Q3_K, [wg, wu], [F, F], [g, u], H, xp, ntok)
-            hip.pack(h, ntok, F, hp)
-            hip.group(Q6_K, [wd], [H], [d], F, hp, ntok)
+            hip.group_f32(Q3_K, [wg, wu], [F, F], [g, u], H, x, ntok)
+            hip.group_f32(Q6_K, [wd], [H], [d], F, h, ntok)
 
     for i in range(copies):
         launch(i)
@@ -508,6 +526,7 @@ def main() -> None:
         for n in (1, 4, 8):
             log(f"SwiGLU MLP block, batch {n}")
             mlp[f"batch{n}"] = bench_mlp(torch, hip, n)
+        mlp["batch8_stream"] = bench_mlp(torch, hip, 8, mfma=False)
         for rows, cols in ((17408, 5120), (5120, 17408)):
             log(f"prefill: 512 tokens x Q4_K {rows}x{cols}")
             prefill[f"Q4_K_{rows}x{cols}_M512"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512)
