@@ -173,6 +173,22 @@ struct Sl<VQ_Q4_K> {
         mn[0] = dmin * ubyte0(m2);
         mn[1] = dmin * ubyte1(m2);
     }
+    // Integer form: part p weighs d * isc[p] and its min dmin * imn[p].
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.hd[0]); }
+    static __device__ __forceinline__ float dmin(const W &w) { return half_to_float(w.hd[0] >> 16); }
+    static __device__ __forceinline__ void iscales(const W &w, int s, int (&isc)[NP]) {
+        uint32_t sc2, m2;
+        k4sm_pair(w.hd[1], w.hd[2], w.hd[3], s >> 1, sc2, m2);
+        isc[0] = static_cast<int>(sc2 & 0xFFu);
+        isc[1] = static_cast<int>((sc2 >> 8) & 0xFFu);
+    }
+    static __device__ __forceinline__ void imins(const W &w, int s, int (&imn)[NP]) {
+        uint32_t sc2, m2;
+        k4sm_pair(w.hd[1], w.hd[2], w.hd[3], s >> 1, sc2, m2);
+        imn[0] = static_cast<int>(m2 & 0xFFu);
+        imn[1] = static_cast<int>((m2 >> 8) & 0xFFu);
+    }
 };
 
 // ---- Q5_K: 176 B = d, dmin, scales[12], qh[32], qs[128]. Like Q4_K plus qh bit j of element l.
@@ -205,6 +221,22 @@ struct Sl<VQ_Q5_K> {
 #pragma unroll
         for (int i = 0; i < 4; ++i) t.hd[i] = w.hd[i];
         Sl<VQ_Q4_K>::scales(t, s, sc, mn);
+    }
+    // Integer form (the Q4_K header layout).
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.hd[0]); }
+    static __device__ __forceinline__ float dmin(const W &w) { return half_to_float(w.hd[0] >> 16); }
+    static __device__ __forceinline__ void iscales(const W &w, int s, int (&isc)[NP]) {
+        uint32_t sc2, m2;
+        k4sm_pair(w.hd[1], w.hd[2], w.hd[3], s >> 1, sc2, m2);
+        isc[0] = static_cast<int>(sc2 & 0xFFu);
+        isc[1] = static_cast<int>((sc2 >> 8) & 0xFFu);
+    }
+    static __device__ __forceinline__ void imins(const W &w, int s, int (&imn)[NP]) {
+        uint32_t sc2, m2;
+        k4sm_pair(w.hd[1], w.hd[2], w.hd[3], s >> 1, sc2, m2);
+        imn[0] = static_cast<int>(m2 & 0xFFu);
+        imn[1] = static_cast<int>((m2 >> 8) & 0xFFu);
     }
 };
 
@@ -254,6 +286,16 @@ struct Sl<VQ_Q6_K> {
             sc[q] = d * static_cast<float>(v);
             mn[q] = 0.0f;
         }
+    }
+    // Integer form: part q weighs d * isc[q] (the signed 8-bit scale).
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.d.lo()); }
+    static __device__ __forceinline__ void iscales(const W &w, int s, int (&isc)[NP]) {
+        const int hh = s & 1;
+        const uint32_t sc0 = w.sc.word(0), sc1 = w.sc.word(1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            isc[q] = __builtin_amdgcn_sbfe(static_cast<int>(q < 2 ? sc0 : sc1), 16 * (q & 1) + 8 * hh, 8);
     }
 };
 
