@@ -23,10 +23,10 @@ namespace vq {
 #endif
 
 // ---- global -> LDS DMA ---------------------------------------------------------------------------------
-// The weight stream reaches LDS through global_load_lds_dwordx4 (each lane moves 16 bytes; a wave writes
-// 1 KB contiguously at M0), so bytes in flight cost no VGPRs. The DMA is issued from inline asm: the
-// compiler then neither counts it nor inserts its own vmcnt(0) before every LDS read, and the kernel waits
-// on vmcnt itself (loads retire in order, so "at most N outstanding" means "all but the last N landed").
+// IQ grid tables and packed activation records reach LDS through global_load_lds_dwordx4 (each lane moves
+// 16 bytes; a wave writes 1 KB contiguously at M0). The DMA is issued from inline asm, so the compiler does
+// not count it; the kernel waits on vmcnt itself (loads retire in order, so "at most N outstanding" means
+// "all but the last N landed").
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void *)p));
 }
