@@ -117,10 +117,17 @@ struct Stream {
     static_assert(S::SPB % LPU == 0 && NL >= 1 && NL <= 16, "stage geometry");
 };
 
-// Partial row sums of one workgroup: [stage][row of the stage][token] fp32, at most this many floats.
+// Partial row sums of one workgroup, at most this many fp32 floats. Two layouts: [stage][lane][token] (one
+// part per lane, no reduction inside a stage) when the workgroup's stages fit, else [stage][row of the
+// stage][token] (a segmented scan over the lanes gives each row's part of the stage).
 constexpr int kSlotFloats = 4096;
 // Rows a stage of SU consecutive units can touch when rows have nu units.
 __host__ __device__ constexpr int rows_per_stage(int su, int nu) { return (su - 1) / nu + 2; }
+// Whether a job of rwg rows per workgroup uses the per-lane layout (one value for the whole job; one token
+// only: at several tokens the extra registers of both reductions cost more than the scan).
+__host__ __device__ constexpr bool lane_slots(long rwg, int nu, int su, int nt) {
+    return nt == 1 && (rwg * nu + su - 1) / su * 64 <= kSlotFloats;
+}
 
 template <int T>
 constexpr int grid_table_bytes() {
@@ -211,6 +218,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     uint8_t *const sbuf = s_dyn + xreg + wv * G::STAGE_LDS;
     float *const slots = reinterpret_cast<float *>(s_dyn + xreg + NW * G::STAGE_LDS);
     const int rs = rows_per_stage(SU, nu);
+    const bool per_lane = lane_slots(jobs.j[jb].rwg, nu, SU, NT);
 
     // This workgroup's rows and stages (all 32-bit unit indices: a matrix has < 2^31 units).
     const int b = blockIdx.x;
@@ -249,6 +257,8 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
 
     // Start-up: table pieces and activations first, alone (waiting for them then waits behind no weight
     // traffic), then the first stage.
+    int s = wv < nst ? wv : -1;
+    u32x4 RA[NL];
     if constexpr (TB > 0) {
         const uint8_t *src = grid_table_src<T>();
         for (int p = wv; p < TB / 1024; p += NW) dma16(src + p * 1024, lane * 16, lds_addr(s_grid) + p * 1024);
@@ -284,8 +294,6 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     }
     wait_vm<0>();
     __builtin_amdgcn_sched_barrier(0);
-    int s = wv < nst ? wv : -1;
-    u32x4 RA[NL];
     load_stage(s >= 0 ? s : 0, RA);
     if (threadIdx.x == 0) s_next = NW;
     Tabs tb{};
@@ -318,12 +326,12 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
         const int col = ua - rf * nu;                    // its unit index within that row
         const bool valid = ul < nval;
         const uint8_t *up = sbuf + ((static_cast<long>(ua) + (valid ? ul : 0)) * UB - ((static_cast<long>(ua) * UB >> 4) << 4));
-        // Row and column unit of this lane's unit: c = col + ul = q*nu + cu with q small.
+        // Row and column unit of this lane's unit: c = col + ul = q*nu + cu. c < nu + 64 and nu < 2^13, so
+        // (c + 1/2) / nu lies at least 1/(2nu) from an integer, far beyond the fp32 error of (c + 1/2) * inv_nu:
+        // the truncation is the exact quotient.
         const int c = col + ul;
-        int q = static_cast<int>(static_cast<float>(c) * inv_nu);
-        q = (q + 1) * nu <= c ? q + 1 : q;
-        q = q * nu > c ? q - 1 : q;
-        const int cu = c - q * nu;
+        const int q = static_cast<int>((static_cast<float>(c) + 0.5f) * inv_nu);
+        const int cu = __mul24(-q, nu) + c;
         const int G0 = cu * S::UG;
 
         float v[NT];
@@ -430,6 +438,11 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             }
         }
 #endif
+        if (per_lane) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) slots[(s * 64 + lane) * NT + t] = v[t];
+            return;
+        }
         // Segmented inclusive scan over the lanes; segments are the stage's rows (q is non-decreasing in lane
         // order). The last lane of each segment holds that row's part of the stage.
         const int key = valid ? q : 0x7FFFFFFF;
@@ -457,14 +470,32 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     // One lane takes the ticket (a wave-wide atomic would take one per lane); readfirstlane shares it.
     auto take = [&]() { return lane == 0 ? atomicAdd(&s_next, 1) : 0; };
     int ask = s >= 0 ? take() : nst;  // the stage after s (valid in lane 0)
+#ifdef VQ_TIMING
+    unsigned long long t_dec = 0, t_wait = 0, n_st = 0;
+#endif
     while (s >= 0) {
+#ifdef VQ_TIMING
+        const unsigned long long ta = __builtin_amdgcn_s_memrealtime();
+#endif
         store_stage(RA);
         const int sn = __builtin_amdgcn_readfirstlane(ask);
+#ifdef VQ_TIMING
+        wait_vm<0>();
+        wait_lgkm0();
+        const unsigned long long tb = __builtin_amdgcn_s_memrealtime();
+#endif
         if (sn < nst) {
             load_stage(sn, RA);
             ask = take();
         }
         run_stage(s);
+#ifdef VQ_TIMING
+        wait_lgkm0();
+        const unsigned long long tc = __builtin_amdgcn_s_memrealtime();
+        t_wait += tb - ta;
+        t_dec += tc - tb;
+        ++n_st;
+#endif
         s = sn < nst ? sn : -1;
     }
 #ifdef VQ_TIMING
@@ -472,11 +503,41 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
 #endif
     __syncthreads();
 
-    // Each row's parts in stage order: the row's units are [r*nu - U0, (r+1)*nu - U0) of the range.
+    // Each row's parts in a fixed order: the row's units are [r*nu - U0, (r+1)*nu - U0) of the range.
     unsigned long long best[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) best[t] = 0ull;
-    for (int r = R0 + static_cast<int>(threadIdx.x); r < R1; r += blockDim.x) {
+    if (per_lane) {
+        // Eight threads per row: thread k adds parts k, k+8, ... of the row's nu*LPU, then three xor steps.
+        const int k = threadIdx.x & 7;
+        for (int r0 = R0; r0 < R1; r0 += blockDim.x >> 3) {
+            const int r = r0 + static_cast<int>(threadIdx.x >> 3);
+            const bool ok = r < R1;
+            const int e0 = ok ? (r * nu - U0) * LPU : 0, ne = ok ? nu * LPU : 0;
+            float tot[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) tot[t] = 0.0f;
+            for (int e = k; e < ne; e += 8) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) tot[t] += slots[(e0 + e) * NT + t];
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                tot[t] += __shfl_xor(tot[t], 1, 64);
+                tot[t] += __shfl_xor(tot[t], 2, 64);
+                tot[t] += __shfl_xor(tot[t], 4, 64);
+            }
+            if (ok && k == 0) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    if (y != nullptr) y[static_cast<size_t>(t) * rows + r] = tot[t];
+                    const unsigned long long key = argmax_key(tot[t], r);
+                    best[t] = key > best[t] ? key : best[t];
+                }
+            }
+        }
+    }
+    for (int r = R0 + static_cast<int>(threadIdx.x); !per_lane && r < R1; r += blockDim.x) {
         const int ua = r * nu - U0, ue = ua + nu - 1;
         const int s0 = ua / SU, s1 = ue / SU;
         float tot[NT];
@@ -522,7 +583,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             unsigned long long *o = jobs.tm + 6 * static_cast<size_t>(gw);
             o[0] = tm0; o[1] = tm1; o[2] = tm2; o[3] = __builtin_amdgcn_s_memrealtime();
             o[4] = (static_cast<unsigned long long>(xcc) << 32) | hw;
-            o[5] = 0;
+            o[5] = (n_st << 48) | ((t_wait & 0xFFFFFF) << 24) | (t_dec & 0xFFFFFF);
         }
     }
 #endif
@@ -681,7 +742,8 @@ template <int TT, int N>
 long slot_floats(int cols, long rwg) {
     using G = Stream<TT>;
     const int nu = (cols / 32) / Sl<TT>::UG;
-    return (rwg * nu + G::SU - 1) / G::SU * rows_per_stage(G::SU, nu) * N;
+    const long st = (rwg * nu + G::SU - 1) / G::SU;
+    return lane_slots(rwg, nu, G::SU, N) ? st * 64 * N : st * rows_per_stage(G::SU, nu) * N;
 }
 template <int TT, int N>
 long max_rwg(int cols) {
@@ -839,6 +901,9 @@ template <int T, int T2>
 int launch_jobs(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y, int cols,
                 const void *x, bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s) {
     if (n < 1 || n > kMaxJobs || (amax && n != 1)) return static_cast<int>(hipErrorInvalidValue);
+    // Units per row stay below 2^13 (the kernels' unit-to-row quotient relies on it); the activation image of
+    // one token would not fit LDS long before that.
+    if (cols >= (1 << 18)) return static_cast<int>(hipErrorInvalidConfiguration);
     const size_t tok_bytes = x_f32 ? static_cast<size_t>(cols) * 4 : static_cast<size_t>(vq_xpack_stride(cols));
     const int chunk = token_chunk(cols) < max_tokens<T, T2>() ? token_chunk(cols) : max_tokens<T, T2>();
     // One split for every token chunk (the first is the widest), so the argmax key layout is the same.
