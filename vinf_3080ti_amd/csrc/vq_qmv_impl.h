@@ -368,7 +368,10 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
                 typename S::W wr;
                 S::load(up, ss, wr);
                 uint32_t cd[NP][4];
-                S::codes(wr, ss, tb, cd);
+                if constexpr (kScaledCodes<T>())
+                    S::codes_scaled(wr, ss, tb, cd);
+                else
+                    S::codes(wr, ss, tb, cd);
                 int isc[NP], imn[NP];
                 S::iscales(wr, ss, isc);
                 if constexpr (kHasMin<T>) S::imins(wr, ss, imn);
@@ -388,8 +391,11 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
                         const int X = kNeedsX<T> ? static_cast<int>(static_cast<int16_t>(
                                                        static_cast<uint32_t>(xhu[t][pg]) >> (16 * ph)))
                                                  : 0;
+                        constexpr int OFFS = S::OFF;
+                        int off = OFFS;
+                        if constexpr (kScaledCodes<T>()) off = OFFS << S::gsh(pg);
                         const int Sv = dot4(cd[p][3], xv4.w, dot4(cd[p][2], xv4.z, dot4(cd[p][1], xv4.y,
-                                            dot4(cd[p][0], xv4.x, -S::OFF * X))));
+                                            dot4(cd[p][0], xv4.x, -off * X))));
                         gs[t][pg] += __mul24(Sv, isc[p]);
                         if constexpr (kHasMin<T>) gm[t][pg] += __mul24(X, imn[p]);
                     }
@@ -400,7 +406,9 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
                 float a = 0.0f, m = 0.0f;
 #pragma unroll
                 for (int g = 0; g < S::UG; ++g) {
-                    a = fmaf(static_cast<float>(gs[t][g]), xdu[t][g], a);
+                    int gsum = gs[t][g];
+                    if constexpr (kScaledCodes<T>()) gsum >>= S::gsh(g);  // exact: a multiple of 2^gsh
+                    a = fmaf(static_cast<float>(gsum), xdu[t][g], a);
                     if constexpr (kHasMin<T>) m = fmaf(static_cast<float>(gm[t][g]), xdu[t][g], m);
                 }
                 v[t] = kHasMin<T> ? fmaf(a, dmul, -m * dmn) : a * dmul;

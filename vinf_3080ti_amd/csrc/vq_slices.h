@@ -63,7 +63,8 @@ __device__ __forceinline__ uint32_t mis(const uint8_t *p) { return static_cast<u
 __device__ __forceinline__ const uint32_t *al4(const uint8_t *p) { return reinterpret_cast<const uint32_t *>(p - mis(p)); }
 // A raw span: the N+1 aligned dwords covering N dwords that start at a 2-byte-aligned address, plus that
 // address's misalignment. Loading keeps the raw words (so the load has no consumer until the slice is
-// decoded, one pipeline trip later); word(i) re-slices on use.
+// decoded, one pipeline trip later); word(i) re-slices on use. (Unaligned LDS dword reads are legal on
+// gfx950 but measured slower than aligned reads plus v_alignbyte_b32: the matvec lost 10-35 %.)
 template <int N>
 struct Span {
     uint32_t t[N + 1];
@@ -332,6 +333,26 @@ struct Sl<VQ_Q3_K> {
             }
         }
     }
+    // Streaming form of the codes: part p keeps its 2-bit field in place (bits 2p, 2p+1; part 3 shifted down
+    // to bits 4, 5) with the hmask bit just above it, i.e. code << gsh(p) with gsh = 0, 2, 4, 4 -- one shift
+    // fewer per word for parts 1 and 2. Values stay <= 112 (positive int8). Every part of group g has
+    // p = g & 3, so the caller divides the group's exact integer sum by 2^gsh once.
+    static __device__ __forceinline__ constexpr int gsh(int g) { return (g & 3) == 0 ? 0 : (g & 3) == 1 ? 2 : 4; }
+    static __device__ __forceinline__ void codes_scaled(const W &w, int s, const Tabs &, uint32_t (&c)[NP][4]) {
+        const int j0 = 4 * (s >> 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t qs = w.qs.word(i), hm = w.hm.word(i);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int lb = p < 3 ? 2 * p : 4;           // bit of the 2-bit field in the code byte
+                const uint32_t lo = p < 3 ? qs & (0x03030303u << lb) : (qs >> 2) & 0x30303030u;
+                const int d = j0 + p - (lb + 2);            // hmask bit j0 + p moves to bit lb + 2
+                const uint32_t hb = (d >= 0 ? hm >> d : hm << -d) & (0x04040404u << lb);
+                c[p][i] = lo | hb;
+            }
+        }
+    }
     static __device__ __forceinline__ void scales(const W &w, int s, float *sc, float *mn) {
         const uint32_t sw[4] = {w.sw.word(0), w.sw.word(1), w.sw.word(2), w.sw.word(3)};
         const float d = half_to_float(sw[3]);
@@ -356,15 +377,20 @@ struct Sl<VQ_Q3_K> {
     static constexpr bool kInt = true;
     static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.sw.word(3)); }
     static __device__ __forceinline__ void iscales(const W &w, int s, int (&isc)[NP]) {
-        const uint32_t sw0 = w.sw.word(0), sw1 = w.sw.word(1), sw2 = w.sw.word(2);
-        const int hh = s & 1, q2 = s >> 1;
-        const uint32_t lo4 = ((sw0 >> (8 * hh + 4 * q2)) & 0x000F000Fu) | (((sw1 >> (8 * hh + 4 * q2)) & 0x000F000Fu) << 8);
-        const uint32_t hb = sw2 >> (8 * hh + 4 * q2);
-        const uint32_t v = lo4 | ((hb & 0x00030003u) << 4) | ((((hb >> 2) & 0x00030003u) << 4) << 8);
-        isc[0] = static_cast<int>(v & 0xFFu) - 32;
-        isc[1] = static_cast<int>((v >> 16) & 0xFFu) - 32;
-        isc[2] = static_cast<int>((v >> 8) & 0xFFu) - 32;
-        isc[3] = static_cast<int>(v >> 24) - 32;
+        // Scales 4m..4m+3 as the bytes of one word: low nibbles from scales[0..7] (nibble m >> 1 of bytes
+        // 4(m & 1)..), bit pair m of scales[8..11] above them. sc - 32 of a 6-bit sc is the 6-bit two's
+        // complement sc ^ 32: bit 1 of every pair is flipped once, and each part takes a signed 6-bit field.
+        const uint32_t sw0 = w.sw.word(0), sw1 = w.sw.word(1), hx = w.sw.word(2) ^ 0xAAAAAAAAu;
+        const int q2 = s >> 1, hh = s & 1;
+        const uint32_t wlo = q2 == 0 ? ((sw0 & 0x0F0F0F0Fu) | ((hx << 4) & 0x30303030u))
+                                     : (((sw0 >> 4) & 0x0F0F0F0Fu) | (hx & 0x30303030u));
+        const uint32_t whi = q2 == 0 ? ((sw1 & 0x0F0F0F0Fu) | ((hx << 2) & 0x30303030u))
+                                     : (((sw1 >> 4) & 0x0F0F0F0Fu) | ((hx >> 2) & 0x30303030u));
+        // part p is scale 8 q2 + hh + 2p: byte hh + 2(p & 1) of wlo (p < 2) or whi
+        isc[0] = __builtin_amdgcn_sbfe(static_cast<int>(wlo), 8 * hh, 6);
+        isc[1] = __builtin_amdgcn_sbfe(static_cast<int>(wlo), 8 * hh + 16, 6);
+        isc[2] = __builtin_amdgcn_sbfe(static_cast<int>(whi), 8 * hh, 6);
+        isc[3] = __builtin_amdgcn_sbfe(static_cast<int>(whi), 8 * hh + 16, 6);
     }
 };
 
@@ -705,6 +731,12 @@ constexpr bool kNeedsX = kHasMin<T> || T == VQ_Q3_K || T == VQ_Q6_K;
 template <int T>
 constexpr bool kIntScales() {
     if constexpr (requires { Sl<T>::kInt; }) return Sl<T>::kInt;
+    return false;
+}
+// Types with a streaming code form scaled by 2^gsh(g) per group (the integer-scale path only).
+template <int T>
+constexpr bool kScaledCodes() {
+    if constexpr (requires { Sl<T>::gsh(0); }) return true;
     return false;
 }
 
