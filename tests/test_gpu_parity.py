@@ -344,6 +344,76 @@ def test_qgemm_matches_oracle(env, oracle_mod, ty, rows, cols, M):
         assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, t)
 
 
+def _qgemm_ws(torch, lib, ty, w_dev, rows, cols, xp, M, y):
+    need = lib.vq_qgemm_workspace_bytes(int(ty), rows, cols, M)
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device="cuda")
+    st = lib.vq_qgemm_ws(int(ty), P(w_dev), rows, cols, P(xp), M, P(y), P(ws), need, None)
+    assert st == 0, lib.vq_status_string(st)
+    return need
+
+
+@pytest.mark.parametrize("ty", [T.Q4_K, T.Q5_K], ids=lambda t: t.name)
+@pytest.mark.parametrize("rows,cols,M", [(300, 2048, 50), (256, 256, 130), (520, 1024, 129), (17, 512, 1),
+                                         (64, 2560, 300)])
+def test_qgemm_f16_matches_oracle(env, oracle_mod, ty, rows, cols, M):
+    """The f16-MFMA prefill contraction (exact code * scale, activations as two f16): within the fp32 bar of
+    the CPU path for ragged row/token tiles, one or several K splits, and bit-identical on a second run."""
+    torch, lib = env
+    rng = np.random.default_rng(rows * 7 + M + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((M, cols)).astype(np.float32)
+    x[:, :32] *= 1e-3  # a group far below the token's maximum
+    xp = _pack(torch, lib, x, M, cols)
+    wd = wdev(torch, w)
+    y = torch.full((M, rows), np.nan, dtype=torch.float32, device="cuda")
+    assert _qgemm_ws(torch, lib, ty, wd, rows, cols, xp, M, y) > 0
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x, M, threads=16)
+    assert np.isfinite(got).all()
+    for t in range(M):
+        assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, t)
+    y2 = torch.full((M, rows), np.nan, dtype=torch.float32, device="cuda")
+    _qgemm_ws(torch, lib, ty, wd, rows, cols, xp, M, y2)
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy(), got)
+
+
+@pytest.mark.parametrize("ty,rows,cols", [(T.Q4_K, 17408, 5120), (T.Q4_K, 5120, 17408), (T.Q5_K, 4096, 5120)],
+                         ids=lambda v: v.name if isinstance(v, T) else str(v))
+def test_qgemm_f16_prefill_shapes(env, oracle_mod, ty, rows, cols):
+    """The benchmark's prefill shapes at 512 tokens (several K splits on the narrow one)."""
+    torch, lib = env
+    M = 512
+    rng = np.random.default_rng(rows + cols + 1)
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((M, cols)).astype(np.float32)
+    xp = _pack(torch, lib, x, M, cols)
+    y = torch.empty(M, rows, dtype=torch.float32, device="cuda")
+    _qgemm_ws(torch, lib, ty, wdev(torch, w), rows, cols, xp, M, y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    sel = np.r_[0:2, 255:257, M - 2:M]
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x[sel], len(sel), threads=16)
+    assert rel_l2(got[sel], ref) <= REL_L2_TOL
+
+
+@pytest.mark.parametrize("ty", [T.Q3_K, T.Q6_K, T.IQ4_XS], ids=lambda t: t.name)
+def test_qgemm_ws_other_types_run_the_int8_path(env, oracle_mod, ty):
+    torch, lib = env
+    rows, cols, M = 70, 512, 20
+    rng = np.random.default_rng(5)
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((M, cols)).astype(np.float32)
+    xp = _pack(torch, lib, x, M, cols)
+    y = torch.empty(M, rows, dtype=torch.float32, device="cuda")
+    assert lib.vq_qgemm_workspace_bytes(int(ty), rows, cols, M) == 0
+    assert lib.vq_qgemm_ws(int(ty), P(wdev(torch, w)), rows, cols, P(xp), M, P(y), None, 0, None) == 0
+    torch.cuda.synchronize()
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x, M)
+    assert rel_l2(y.cpu().numpy(), ref) <= REL_L2_TOL
+
+
 @pytest.mark.parametrize("ty,rows,cols", [(T.Q4_K, 17408, 5120), (T.Q4_K, 5120, 17408), (T.Q3_K, 1000, 5120)],
                          ids=lambda v: v.name if isinstance(v, T) else str(v))
 def test_qgemm_prefill_shapes(env, oracle_mod, ty, rows, cols):

@@ -31,6 +31,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_qmv_group_f32": (I, [I, I, P, P, P, I, P, I, P]),
     "vq_qmv_group_mixed_f32": (I, [I, P, P, P, P, I, P, I, P]),
     "vq_qgemm": (I, [I, P, I, I, P, I, P, P]),
+    "vq_qgemm_workspace_bytes": (SZ, [I, I, I, I]),
+    "vq_qgemm_ws": (I, [I, P, I, I, P, I, P, P, SZ, P]),
     "vq_lmhead_argmax_workspace_bytes": (SZ, [I, I, I, I]),
     "vq_lmhead_argmax": (I, [I, P, I, I, P, I, P, P, P, SZ, P]),
     "vq_dequant_rows": (I, [I, P, I, I, P, P]),

@@ -236,6 +236,99 @@ int launch_float(const uint8_t *w, int rows, int cols, const float *x, int ntok,
 
 bool misaligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
+// ---- f16 prefill path (vq_gemm16_impl.h): activation split and split-K reduction -----------------------------
+// The split needs b as the fp32 product and hi + lo as its split: without the barrier the backend rounds the
+// product straight to f16 for hi (v_fma_mix) but through fp32 for lo, and at double-rounding ties the pair
+// misses b by an f16 ulp of hi (rel-L2 up to 2e-4 on the affected tokens).
+__device__ __forceinline__ void opaque(float &v) { asm volatile("" : "+v"(v)); }
+
+// One workgroup per token: b = xq * (xd 2^e) (exact scaling of the fp32 product xq * xd) as f16 hi + lo,
+// 2^e the power of two with 127 max(xd) 2^e < 2^15 (every |b| 2^e fits f16); per super-block the mins' terms
+// X_g xd_g 2^e / 32 (X_g = the group's code sum, |X_g| <= 32 * 127) likewise; inv = 2^-e.
+__global__ __launch_bounds__(256) void gemm_xsplit_kernel(const uint8_t *__restrict__ xpack, int cols,
+                                                          _Float16 *__restrict__ bh, _Float16 *__restrict__ bl,
+                                                          _Float16 *__restrict__ xs, float *__restrict__ inv) {
+    const int t = blockIdx.x, tid = threadIdx.x, ng = cols >> 5;
+    const uint8_t *rec = xpack + static_cast<size_t>(t) * vq_xpack_stride(cols);
+    const float *xd = reinterpret_cast<const float *>(rec + cols);
+    const uint32_t *xh = reinterpret_cast<const uint32_t *>(rec + vq_xpack_h_offset(cols));
+    __shared__ float red[4];
+    float m = 0.0f;
+    for (int g = tid; g < ng; g += 256) m = fmaxf(m, xd[g]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int E = 0;
+    (void)frexpf(127.0f * m, &E);  // 127 m < 2^E
+    const float sc = m > 0.0f ? ldexpf(1.0f, 15 - E) : 1.0f;
+    const size_t base = static_cast<size_t>(t) * cols;
+    for (int c = tid; c < cols / 8; c += 256) {
+        const float ds = xd[c >> 2] * sc;
+        const uint2 q = *reinterpret_cast<const uint2 *>(rec + 8 * c);
+        _Float16 h[8], l[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t wd = i < 4 ? q.x : q.y;
+            float v = static_cast<float>(static_cast<int8_t>(wd >> (8 * (i & 3)))) * ds;
+            opaque(v);
+            h[i] = static_cast<_Float16>(v);
+            l[i] = static_cast<_Float16>(v - static_cast<float>(h[i]));
+        }
+        *reinterpret_cast<uint4 *>(bh + base + 8 * c) = __builtin_bit_cast(uint4, h);
+        *reinterpret_cast<uint4 *>(bl + base + 8 * c) = __builtin_bit_cast(uint4, l);
+    }
+    const int nsb = cols >> 8;
+    for (int sb = tid; sb < nsb; sb += 256) {
+        _Float16 o[16];
+#pragma unroll
+        for (int gg = 0; gg < 8; ++gg) {
+            const int g = 8 * sb + gg;
+            const uint32_t hx = xh[g];
+            const int X = static_cast<int>(static_cast<int16_t>(hx & 0xFFFFu)) + static_cast<int>(static_cast<int16_t>(hx >> 16));
+            float v = static_cast<float>(X) * (xd[g] * sc) * 0.03125f;
+            opaque(v);
+            o[gg] = static_cast<_Float16>(v);
+            o[8 + gg] = static_cast<_Float16>(v - static_cast<float>(o[gg]));
+        }
+        uint4 *dst = reinterpret_cast<uint4 *>(xs + (static_cast<size_t>(t) * nsb + sb) * 16);
+        dst[0] = __builtin_bit_cast(uint4, *reinterpret_cast<const _Float16(*)[8]>(o));
+        dst[1] = __builtin_bit_cast(uint4, *reinterpret_cast<const _Float16(*)[8]>(o + 8));
+    }
+    if (tid == 0) inv[t] = 1.0f / sc;
+}
+
+// y = sum of the split partial tiles, in split order (deterministic).
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ part, int splits, size_t n,
+                                                          float *__restrict__ y) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
+        float v = part[i];
+        for (int s = 1; s < splits; ++s) v += part[static_cast<size_t>(s) * n + i];
+        y[i] = v;
+    }
+}
+
+// The f16 path: Q4_K/Q5_K, with the activation split addressable by the kernel's 32-bit DMA offsets.
+bool gemm16_ok(int type, int cols, int M) {
+    return (type == VQ_Q4_K || type == VQ_Q5_K) && static_cast<long>(M) * cols < (1L << 30);
+}
+
+// Compute units of the current device (256 when there is none: workspace sizes stay computable).
+int device_cus() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    return n;
+}
+
+int gemm16_splits(int rows, int cols, int M) {
+    const int tiles = ((rows + vq::kG16BM - 1) / vq::kG16BM) * ((M + vq::kG16BN - 1) / vq::kG16BN);
+    return vq::g16_splits(tiles, cols >> 8, device_cus());
+}
+
 size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
 }  // namespace
@@ -458,6 +551,42 @@ int vq_qgemm(int type, const uint8_t *w, int rows, int cols, const void *xpack, 
     return dispatch_quant(type, [&](auto tc) {
         return vq::launch_gemm<decltype(tc)::value>(w, rows, cols, rb, xp, M, y, s);
     });
+}
+
+size_t vq_qgemm_workspace_bytes(int type, int rows, int cols, int M) {
+    if (check_matrix(type, rows, cols) || M < 1 || !gemm16_ok(type, cols, M)) return 0;
+    return vq::g16_layout(cols, M, rows, gemm16_splits(rows, cols, M)).total;
+}
+
+int vq_qgemm_ws(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *workspace,
+                size_t workspace_bytes, void *stream) {
+    int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;
+    if (!w || !xpack || !y || misaligned16(w) || misaligned16(xpack)) return VQ_ERR_ARG;
+    if (M < 1) return VQ_ERR_SHAPE;
+    const size_t need = vq_qgemm_workspace_bytes(type, rows, cols, M);
+    if (need == 0) return vq_qgemm(type, w, rows, cols, xpack, M, y, stream);
+    if (!workspace || workspace_bytes < need || misaligned16(workspace)) return VQ_ERR_WORKSPACE;
+    const long rb = row_bytes_of(type, cols);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int splits = gemm16_splits(rows, cols, M);
+    const vq::G16Ws l = vq::g16_layout(cols, M, rows, splits);
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    gemm_xsplit_kernel<<<M, 256, 0, s>>>(static_cast<const uint8_t *>(xpack), cols, reinterpret_cast<_Float16 *>(ws + l.bh),
+                                         reinterpret_cast<_Float16 *>(ws + l.bl), reinterpret_cast<_Float16 *>(ws + l.xs),
+                                         reinterpret_cast<float *>(ws + l.inv));
+    st = hip_status(hipGetLastError());
+    if (st) return st;
+    float *out = splits > 1 ? reinterpret_cast<float *>(ws + l.part) : y;
+    st = dispatch_quant(type, [&](auto tc) {
+        return vq::launch_gemm16<decltype(tc)::value>(w, rows, cols, rb, ws, M, out, splits, s);
+    });
+    if (st || splits == 1) return st;
+    const size_t n = static_cast<size_t>(M) * rows;
+    const int blocks = static_cast<int>((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+    gemm_reduce_kernel<<<blocks, 256, 0, s>>>(out, splits, n, y);
+    return hip_status(hipGetLastError());
 }
 
 size_t vq_lmhead_argmax_workspace_bytes(int type, int rows, int cols, int ntok) {

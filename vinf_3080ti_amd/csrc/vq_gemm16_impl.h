@@ -1,0 +1,327 @@
+// vq_gemm16_impl.h -- prefill contraction Y[t][r] = W[r] . x[t] on CDNA4 f16 MFMA (v_mfma_f32_16x16x32_f16) for
+// the K-quants whose integer sub-block products are exact in f16 and whose blocks are 16-byte multiples
+// (Q4_K, Q5_K).
+//
+// Numerics. The reference CPU path (Cpu_qmv, qwen_cpu.c:581-641) computes per 32-group
+//   y += d * sc * xd * S - dmin * m * xd * X,   S = sum(code * xq) exact, X = sum(xq)
+// with xq/xd the int8 activation codes and group scale of vq_pack_x. Here every weight element becomes the
+// integer a = code * sc (<= 945 for Q4_K, 1953 for Q5_K: exact in f16), every activation element
+// b = xq * xd * 2^e (one fp32 rounding; 2^e per token keeps the token in f16 range) as the f16 pair
+// b_hi + b_lo (22 significant bits), and each super-block's
+//   C = sum_k a * (b_hi + b_lo)   (MFMA products are exact, fp32 accumulation)
+// is applied once per 256 elements: acc += d * C - dmin * sum_g m_g * (X_g xd_g 2^e). Only fp32 rounding of
+// sums differs from the CPU path (rel-L2 ~2e-7 against its 1e-5 bar); the int8 path (vq_gemm_impl.h) pays a
+// VALU scale per 32-group instead, which caps it near 15 % of MFMA peak.
+//
+// Work split: a workgroup of 8 waves computes a 256-row x 128-token tile over a range of super-blocks (split
+// K when the tiles alone would leave CUs idle; partial tiles are added in a fixed order by the library's
+// reduction, so results are deterministic). Wave w owns rows 64 (w % 4) .. +64 and tokens 64 (w / 4) .. +64:
+// 4 x 4 blocks of 16 x 16. A K step is 64 elements (a quarter super-block). All global data reaches LDS by
+// global_load_lds_dwordx4, two steps ahead, into a ring of three step slots (the step's 32 code bytes of
+// every row; the tokens' b_hi/b_lo tile, 16-byte chunks XOR-swizzled by row against bank conflicts) and two
+// super-block slots (the first 16/48 bytes of every row's block -- d, dmin, scales, Q5_K's high bits -- and
+// the tokens' min terms). Every wave issues the same number of DMAs per step, so one vmcnt wait and one
+// barrier per step cover the ring. Each wave decodes its own A fragments (code * scale -> f16 via v_perm_b32
+// and v_pk_fma_f16) from the raw bytes while its MFMAs run: 2 x 16 x 2 v_mfma_f32_16x16x32_f16 per step. A
+// super-block's min term is one v_mfma_f32_16x16x16_f16 per block over [m_0..m_7, m_0..m_7] x
+// [XS_hi_0..7, XS_lo_0..7].
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vq_qmv.h"
+#include "vq_tables.h"
+
+namespace vq {
+
+template <int T>
+constexpr bool kGemm16 = T == VQ_Q4_K || T == VQ_Q5_K;
+
+constexpr int kG16BM = 256, kG16BN = 128, kG16KS = 64, kG16Waves = 8, kG16Ring = 3;
+
+typedef _Float16 g16h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 g16h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 g16h2 __attribute__((ext_vector_type(2)));
+typedef float g16f4 __attribute__((ext_vector_type(4)));
+
+// Workspace layout of the f16 path for M tokens of `cols` columns: b_hi [M][cols] f16, b_lo [M][cols] f16,
+// xs [M][cols/256][16] f16 (per super-block: X_g xd_g 2^e / 32 as 8 hi then 8 lo), inv [M] fp32 (2^-e),
+// then the split-K partial tiles [splits][M][rows] fp32 (none for one split).
+struct G16Ws {
+    size_t bh, bl, xs, inv, part, total;
+};
+inline G16Ws g16_layout(int cols, int M, int rows, int splits) {
+    auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+    G16Ws l{};
+    const size_t nb = static_cast<size_t>(M) * cols * 2;
+    l.bh = 0;
+    l.bl = al(nb);
+    l.xs = l.bl + al(nb);
+    l.inv = l.xs + al(static_cast<size_t>(M) * (cols / 256) * 32);
+    l.part = l.inv + al(static_cast<size_t>(M) * 4);
+    l.total = l.part + (splits > 1 ? al(static_cast<size_t>(splits) * M * rows * 4) : 0);
+    return l;
+}
+
+// Two f16 (1024 + c) from bytes of a code word (c < 256): v_perm_b32 puts 0x64 above each byte.
+__device__ __forceinline__ g16h2 g16_pair(uint32_t codes, uint32_t sel) {
+    return __builtin_bit_cast(g16h2, __builtin_amdgcn_perm(0x64646464u, codes, sel));
+}
+// Eight codes (bytes of c0, c1, each < 64) times sc as the f16 fragment: (1024 + c) sc - 1024 sc in one rounding
+// (v_pk_fma_f16), exact because c sc is.
+__device__ __forceinline__ g16h8 g16_frag(uint32_t c0, uint32_t c1, _Float16 sc) {
+    const g16h2 s2 = {sc, sc};
+    const _Float16 nb = static_cast<_Float16>(-1024.0f) * sc;  // exact: sc < 64
+    const g16h2 n2 = {nb, nb};
+    const g16h2 p0 = __builtin_elementwise_fma(g16_pair(c0, 0x04010400u), s2, n2);
+    const g16h2 p1 = __builtin_elementwise_fma(g16_pair(c0, 0x04030402u), s2, n2);
+    const g16h2 p2 = __builtin_elementwise_fma(g16_pair(c1, 0x04010400u), s2, n2);
+    const g16h2 p3 = __builtin_elementwise_fma(g16_pair(c1, 0x04030402u), s2, n2);
+    return g16h8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+template <int T>
+struct G16Geo {
+    static constexpr int UB = Sl<T>::UB;
+    static constexpr int HB = T == VQ_Q5_K ? 48 : 16;          // leading block bytes kept per super-block
+    static constexpr int QOFF = T == VQ_Q5_K ? 48 : 16;        // offset of qs in the block
+    static constexpr int SB_CHUNKS = kG16BM * HB / 16 + kG16BN * 2;  // 16-byte chunks of a super-block slot
+    static constexpr int SB_DMA = SB_CHUNKS / (64 * kG16Waves);      // per wave per step
+    static constexpr int NDMA = 1 + 4 + SB_DMA;                      // DMAs per wave per step
+    static constexpr int STEP_BYTES = kG16BM * 32 + 2 * kG16BN * 128;  // codes + b_hi + b_lo
+    static constexpr int SB_BYTES = SB_CHUNKS * 16;
+    static_assert(SB_CHUNKS % (64 * kG16Waves) == 0, "super-block slot split");
+};
+
+template <int T>
+__global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *__restrict__ w, int rows, int cols,
+                                                                  long row_bytes, const _Float16 *__restrict__ bh,
+                                                                  const _Float16 *__restrict__ bl,
+                                                                  const _Float16 *__restrict__ xs,
+                                                                  const float *__restrict__ inv, int M, int nrt,
+                                                                  int ntt, int splits, float *__restrict__ out,
+                                                                  int per_xcd) {
+    using G = G16Geo<T>;
+    __shared__ __attribute__((aligned(1024))) uint8_t s_step[kG16Ring][G::STEP_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_sb[2][G::SB_BYTES];
+
+    // Workgroup -> (row tile, token tile, split): consecutive ids go round-robin over the 8 XCDs; the ids one
+    // XCD receives map to a contiguous range of tiles, so the workgroups sharing a token tile's activations
+    // and a row tile's weights meet in one L2.
+    const int b = blockIdx.x;
+    const int v = (b & 7) * per_xcd + (b >> 3);
+    const int ntile = nrt * ntt;
+    if (v >= ntile * splits) return;
+    const int ks = v / ntile, tile = v - ks * ntile;
+    const int rt = tile / ntt, tt = tile - rt * ntt;
+    const int r0 = rt * kG16BM, t0 = tt * kG16BN;
+    const int nsb = cols >> 8;
+    const int sb0 = static_cast<int>(static_cast<long>(ks) * nsb / splits);
+    const int sb1 = static_cast<int>(static_cast<long>(ks + 1) * nsb / splits);
+    const int nsteps = (sb1 - sb0) * 4;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int wr = 64 * (wv & 3), wt = 64 * (wv >> 2);
+    const int lr = lane & 15, lk = lane >> 4;
+    const uint8_t *const wbase = w + static_cast<size_t>(r0) * row_bytes;  // wave-uniform
+
+    // DMA of step st (j = st % 4 of super-block sb0 + st / 4) into ring slot st % 3 and super-block slot sb & 1.
+    // Per wave: codes (rows 32 wv .. +32, two lanes per row), 4 of the 32 KB of b_hi/b_lo (8 tokens per 1 KB,
+    // chunk position p of token row r holds chunk p ^ ((r >> 1) & 7): the 16 rows an MFMA fragment reads then
+    // hit 16 distinct 16-byte bank groups), SB_DMA KB of the super-block slot.
+    auto issue = [&](int st) {
+        const int sb = sb0 + (st >> 2), j = st & 3;
+        uint8_t *const slot = s_step[st % kG16Ring];
+        {
+            const int row = min(r0 + 32 * wv + (lane >> 1), rows - 1) - r0;
+            const uint32_t off = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + G::QOFF + 32 * j + 16 * (lane & 1));
+            dma16(wbase, off, slot + 1024 * wv);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * wv + k, ii = i & 15;
+            const int row = 8 * ii + (lane >> 3);
+            const int tok = min(t0 + row, M - 1);
+            const int c = (lane & 7) ^ ((row >> 1) & 7);
+            const uint32_t off = static_cast<uint32_t>((static_cast<long>(tok) * cols + 256L * sb + 64 * j + 8 * c) * 2);
+            dma16(i < 16 ? static_cast<const void *>(bh) : static_cast<const void *>(bl), off,
+                  slot + kG16BM * 32 + (i < 16 ? 0 : kG16BN * 128) + 1024 * ii);
+        }
+        uint8_t *const sbs = s_sb[sb & 1];
+#pragma unroll
+        for (int k = 0; k < G::SB_DMA; ++k) {
+            const int i = G::SB_DMA * wv + k;
+            const int ci = 64 * i + lane;
+            constexpr int CH = G::HB / 16, NHC = kG16BM * G::HB / 16;
+            if (i * 64 < NHC) {
+                const int row = min(r0 + ci / CH, rows - 1) - r0;
+                const uint32_t off = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + 16 * (ci % CH));
+                dma16(wbase, off, sbs + 1024 * i);
+            } else {
+                const int cj = ci - NHC;
+                const int tok = min(t0 + (cj >> 1), M - 1);
+                const uint32_t off = static_cast<uint32_t>(((static_cast<long>(tok) * nsb + sb) * 16 + 8 * (cj & 1)) * 2);
+                dma16(xs, off, sbs + 1024 * i);
+            }
+        }
+    };
+
+    g16f4 acc[4][4], C[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[i][q] = C[i][q] = g16f4{0.f, 0.f, 0.f, 0.f};
+
+    if (nsteps > 0) issue(0);
+    if (nsteps > 1) issue(1);
+    uint32_t scl[4] = {0u, 0u, 0u, 0u}, sch[4] = {0u, 0u, 0u, 0u};  // [rb]: 6-bit scales of groups 0..3 / 4..7 of
+                                                                      // row wr + 16 rb + lr, one per byte
+    const g16h2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+    for (int st = 0; st < nsteps; ++st) {
+        if (st + 1 < nsteps)
+            wait_vm<G::NDMA>();
+        else
+            wait_vm<0>();
+        __syncthreads();  // step st landed for every wave; step st - 1's slot is free
+        if (st + 2 < nsteps) issue(st + 2);
+        const int sb = sb0 + (st >> 2), j = st & 3;
+        const uint8_t *const slot = s_step[st % kG16Ring];
+        const uint8_t *const sbs = s_sb[sb & 1];
+        const uint8_t *const sBh = slot + kG16BM * 32, *const sBl = sBh + kG16BN * 128;
+        if (j == 0) {
+            // The super-block's 6-bit scales, four per dword (the k4_scale_min packing, qwen_cpu.c:54-62):
+            // groups 0..3 from scales[0..3], groups 4..7 from scales[8..11] plus the top bits of scales[0..3].
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const uint4 h = *reinterpret_cast<const uint4 *>(sbs + (wr + 16 * rb + lr) * G::HB);
+                scl[rb] = h.y & 0x3F3F3F3Fu;
+                sch[rb] = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+            }
+        }
+        // A fragments: rows wr + 16 rb + lr, elements 8 lk .. +8 of groups 2j (c = 0) and 2j + 1 (c = 1).
+        const uint32_t ssel = (j & 1) ? 0x04030402u : 0x04010400u;
+        g16h8 a[2][4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int row = wr + 16 * rb + lr;
+            const uint32_t sw = j < 2 ? scl[rb] : sch[rb];
+            const g16h2 sc = g16_pair(sw, ssel) - k1024;
+            const uint2 q = *reinterpret_cast<const uint2 *>(slot + row * 32 + 8 * lk);
+            uint32_t lo0 = q.x & 0x0F0F0F0Fu, lo1 = q.y & 0x0F0F0F0Fu;
+            uint32_t hi0 = (q.x >> 4) & 0x0F0F0F0Fu, hi1 = (q.y >> 4) & 0x0F0F0F0Fu;
+            if constexpr (T == VQ_Q5_K) {
+                const uint2 qh = *reinterpret_cast<const uint2 *>(sbs + row * G::HB + 16 + 8 * lk);
+                lo0 |= ((qh.x >> (2 * j)) & 0x01010101u) << 4;
+                lo1 |= ((qh.y >> (2 * j)) & 0x01010101u) << 4;
+                hi0 |= ((qh.x >> (2 * j + 1)) & 0x01010101u) << 4;
+                hi1 |= ((qh.y >> (2 * j + 1)) & 0x01010101u) << 4;
+            }
+            a[0][rb] = g16_frag(lo0, lo1, sc[0]);
+            a[1][rb] = g16_frag(hi0, hi1, sc[1]);
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            g16h8 bhf[4], blf[4];
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                const int r = wt + 16 * tb + lr;
+                const int o = r * 128 + (((4 * c + lk) ^ ((r >> 1) & 7)) << 4);
+                bhf[tb] = *reinterpret_cast<const g16h8 *>(sBh + o);
+                blf[tb] = *reinterpret_cast<const g16h8 *>(sBl + o);
+            }
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+                    C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][rb], bhf[tb], C[rb][tb], 0, 0, 0);
+                    C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][rb], blf[tb], C[rb][tb], 0, 0, 0);
+                }
+        }
+        if (j == 3) {
+            // Super-block end: acc += d C - 32 dmin (m . XS); C restarts at zero. C element q of a block is row
+            // 4 lk + q, token lr.
+            const uint8_t *const sxs = sbs + kG16BM * G::HB;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                float dq[4], mq[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t hd = *reinterpret_cast<const uint32_t *>(sbs + (wr + 16 * rb + 4 * lk + q) * G::HB);
+                    dq[q] = half_to_float(hd);
+                    mq[q] = 32.0f * half_to_float(hd >> 16);
+                }
+                // A_min fragment: row wr + 16 rb + lr, k = 4 lk .. +4 -> mins of groups 4 (lk & 1) .. +4.
+                const uint4 h = *reinterpret_cast<const uint4 *>(sbs + (wr + 16 * rb + lr) * G::HB);
+                const uint32_t mw = (lk & 1) ? (((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u)) : (h.z & 0x3F3F3F3Fu);
+                const g16h2 m01 = g16_pair(mw, 0x04010400u) - k1024, m23 = g16_pair(mw, 0x04030402u) - k1024;
+                const g16h4 amin = {m01[0], m01[1], m23[0], m23[1]};
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+                    const g16h4 bm = *reinterpret_cast<const g16h4 *>(sxs + (wt + 16 * tb + lr) * 32 + 8 * lk);
+                    const g16f4 cm = __builtin_amdgcn_mfma_f32_16x16x16f16(amin, bm, g16f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[rb][tb][q] = fmaf(dq[q], C[rb][tb][q], fmaf(-mq[q], cm[q], acc[rb][tb][q]));
+                    C[rb][tb] = g16f4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+    }
+
+    // Write y (one split) or this split's partial tile: element q of block (rb, tb) is row r0 + wr + 16 rb +
+    // 4 lk + q, token t0 + wt + 16 tb + lr; values leave the 2^e token scale here.
+    float *dst = splits > 1 ? out + static_cast<size_t>(ks) * M * rows : out;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const int t = t0 + wt + 16 * tb + lr;
+        if (t >= M) continue;
+        const float is = inv[t];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = r0 + wr + 16 * rb + 4 * lk + q;
+                if (r < rows) dst[static_cast<size_t>(t) * rows + r] = acc[rb][tb][q] * is;
+            }
+    }
+}
+
+// Splits of the K range: the fewest workgroup rounds times super-blocks per split, counting each extra split's
+// partial-tile traffic as 3 super-blocks of work.
+inline int g16_splits(int tiles, int nsb, int cus) {
+    int best = 1;
+    long best_cost = -1;
+    for (int s = 1; s <= 8 && s <= nsb; ++s) {
+        const long rounds = (static_cast<long>(tiles) * s + cus - 1) / cus;
+        const long cost = rounds * ((nsb + s - 1) / s) + 3L * (s - 1);
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = s;
+        }
+    }
+    return best;
+}
+
+template <int T>
+int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *out, int splits,
+                  hipStream_t s) {
+    if constexpr (!kGemm16<T>) {
+        (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)out, (void)splits, (void)s;
+        return static_cast<int>(hipErrorInvalidValue);
+    } else {
+        const G16Ws l = g16_layout(cols, M, rows, splits);
+        const uint8_t *base = static_cast<const uint8_t *>(ws);
+        const int nrt = (rows + kG16BM - 1) / kG16BM, ntt = (M + kG16BN - 1) / kG16BN;
+        const int nwg = nrt * ntt * splits;
+        const int per_xcd = (nwg + 7) / 8;
+        qgemm16_kernel<T><<<dim3(8 * per_xcd), dim3(64 * kG16Waves), 0, s>>>(
+            w, rows, cols, rb, reinterpret_cast<const _Float16 *>(base + l.bh),
+            reinterpret_cast<const _Float16 *>(base + l.bl), reinterpret_cast<const _Float16 *>(base + l.xs),
+            reinterpret_cast<const float *>(base + l.inv), M, nrt, ntt, splits,
+            splits > 1 ? reinterpret_cast<float *>(const_cast<uint8_t *>(base) + l.part) : out, per_xcd);
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : static_cast<int>(e);
+    }
+}
+
+}  // namespace vq

@@ -21,6 +21,7 @@
 #include <stdint.h>
 
 #include "vq_gemm_impl.h"
+#include "vq_gemm16_impl.h"
 #include "vq_qmv.h"
 #include "vq_tables.h"
 

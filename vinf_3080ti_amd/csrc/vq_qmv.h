@@ -25,6 +25,12 @@ int launch_mixed_q8(int n, const int *types, const uint8_t *const *w, const int 
 template <int T>
 int launch_gemm(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int M, float *y,
                 hipStream_t s);
+// Prefill contraction on f16 MFMA (Q3_K, Q4_K, Q5_K; other types return hipErrorInvalidValue): `ws` holds
+// the split activations written by the library's pre-pass (layout g16_layout), `splits` K ranges whose partial
+// tiles vq_gemm_reduce adds (out = the partial buffer then, else y).
+template <int T>
+int launch_gemm16(const uint8_t *w, int rows, int cols, long row_bytes, const void *ws, int M, float *out, int splits,
+                  hipStream_t s);
 // Small-batch (2..16 tokens) matvec on int8 MFMA; `part` holds mfma_part_bytes(rows, cols, ntok) bytes (unused
 // when that is 0).
 template <int T>

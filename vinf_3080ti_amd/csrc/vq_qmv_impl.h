@@ -22,24 +22,6 @@ namespace vq {
 #define VQ_X_LDS_MAX (64 * 1024)  // bytes of activation records one launch keeps in LDS
 #endif
 
-// ---- global -> LDS DMA ---------------------------------------------------------------------------------
-// IQ grid tables and packed activation records reach LDS through global_load_lds_dwordx4 (each lane moves
-// 16 bytes; a wave writes 1 KB contiguously at M0). The DMA is issued from inline asm, so the compiler does
-// not count it; the kernel waits on vmcnt itself (loads retire in order, so "at most N outstanding" means
-// "all but the last N landed").
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void *)p));
-}
-// 64 lanes x 16 bytes: lane i copies base[voff_i .. +16) to LDS lds + 16 i. base and lds are wave-uniform.
-__device__ __forceinline__ void dma16(const void *base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, %0" ::"s"(base), "v"(voff), "s"(lds) : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // Sum over the 64 lanes with DPP moves (no LDS round trips): pairs, quads, half rows, rows, then rows 1/3
 // take row 0/2 (row_bcast:15) and rows 2/3 take lane 31 (row_bcast:31); lane 63 ends with the total.
@@ -261,7 +243,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     u32x4 RA[NL];
     if constexpr (TB > 0) {
         const uint8_t *src = grid_table_src<T>();
-        for (int p = wv; p < TB / 1024; p += NW) dma16(src + p * 1024, lane * 16, lds_addr(s_grid) + p * 1024);
+        for (int p = wv; p < TB / 1024; p += NW) dma16(src + p * 1024, lane * 16, s_grid + p * 1024);
     }
     if constexpr (XF32) {
         const float *xf = static_cast<const float *>(xin);
@@ -289,7 +271,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             const int o = p * 1024 + lane * 16;  // LDS image byte of this lane's chunk
             const int t = o / xi.bytes;
             const int src = t < NT ? xi.src_of(o - t * xi.bytes, cols) : -1;
-            dma16(xin, static_cast<uint32_t>(src >= 0 ? t * xb + src : 0), lds_addr(s_dyn) + p * 1024);
+            dma16(xin, static_cast<uint32_t>(src >= 0 ? t * xb + src : 0), s_dyn + p * 1024);
         }
     }
     wait_vm<0>();
@@ -1000,6 +982,7 @@ int launch_dequant(const uint8_t *w, int rows, int cols, long rb, float *out, hi
     template int vq::launch_mixed_q8<T>(int, const int *, const uint8_t *const *, const int *, float *const *, int, \
                                         const float *, int, hipStream_t);                                          \
     template int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \
+    template int vq::launch_gemm16<T>(const uint8_t *, int, int, long, const void *, int, float *, int, hipStream_t); \
     template int vq::launch_mfma<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, float *,       \
                                     hipStream_t);                                                                \
     template int vq::launch_partials<T>(const uint8_t *, int, int, long, const uint8_t *, int, int32_t *,          \
