@@ -226,12 +226,15 @@ def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=
 
 
 MFMA_INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, AMD-published (no sparsity)
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA, AMD-published (no sparsity)
 
 
 def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 << 20):
-    """Prefill contraction: M tokens x (rows x cols) weights on int8 MFMA, with the
-    activations packed beforehand; µs per launch, int8 TOPS (2*M*rows*cols ops) and utilisation of the MFMA
-    peak."""
+    """Prefill contraction: M tokens x (rows x cols) weights through vq_qgemm_ws (f16
+    MFMA for Q4_K/Q5_K: exact code*scale weights, activations as two f16 -> two MFMAs per useful multiply-add;
+    the int8-MFMA vq_qgemm for other types), activations packed beforehand. Reports us per launch (the
+    activation split, the contraction and the reduction of split tiles), useful TFLOP/s (2*M*rows*cols) and
+    its fraction of the path's dense MFMA peak; `mfma_issued_util` counts the hi/lo MFMAs actually issued."""
     from vinf_3080ti_amd import row_bytes
 
     nbytes = rows * row_bytes(ty, cols)
@@ -241,9 +244,12 @@ def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 <
     xp = hip.xpack(cols, M)
     hip.pack(x, M, cols, xp)
     y = torch.empty(M, rows, device="cuda")
+    need = hip.lib.vq_qgemm_workspace_bytes(ty, rows, cols, M)
+    wk = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
 
     def launch(i):
-        st = hip.lib.vq_qgemm(ty, ws[i % copies].data_ptr(), rows, cols, xp.data_ptr(), M, y.data_ptr(), hip.s())
+        st = hip.lib.vq_qgemm_ws(ty, ws[i % copies].data_ptr(), rows, cols, xp.data_ptr(), M, y.data_ptr(),
+                                 wk.data_ptr() if need else None, need, hip.s())
         assert st == 0, st
 
     for i in range(copies):
@@ -252,8 +258,13 @@ def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 <
     del ws
     torch.cuda.empty_cache()
     tops = 2.0 * M * rows * cols / (ms * 1e-3) / 1e12
-    return {"us": round(ms * 1e3, 3), "int8_tops": round(tops, 2), "mfma_util": round(tops / MFMA_INT8_PEAK_TOPS, 4),
-            "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    f16 = need > 0
+    peak = MFMA_F16_PEAK_TFLOPS if f16 else MFMA_INT8_PEAK_TOPS
+    out = {"us": round(ms * 1e3, 3), "path": "f16-mfma" if f16 else "int8-mfma", "tflops": round(tops, 2),
+           "mfma_util": round(tops / peak, 4), "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    if f16:
+        out["mfma_issued_util"] = round(2 * tops / peak, 4)
+    return out
 
 
 def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=None):

@@ -299,16 +299,6 @@ __global__ __launch_bounds__(256) void gemm_xsplit_kernel(const uint8_t *__restr
     if (tid == 0) inv[t] = 1.0f / sc;
 }
 
-// y = sum of the split partial tiles, in split order (deterministic).
-__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ part, int splits, size_t n,
-                                                          float *__restrict__ y) {
-    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
-        float v = part[i];
-        for (int s = 1; s < splits; ++s) v += part[static_cast<size_t>(s) * n + i];
-        y[i] = v;
-    }
-}
-
 // The f16 path: Q4_K/Q5_K, with the activation split addressable by the kernel's 32-bit DMA offsets.
 bool gemm16_ok(int type, int cols, int M) {
     return (type == VQ_Q4_K || type == VQ_Q5_K) && static_cast<long>(M) * cols < (1L << 30);
@@ -324,10 +314,6 @@ int device_cus() {
     return n;
 }
 
-int gemm16_splits(int rows, int cols, int M) {
-    const int tiles = ((rows + vq::kG16BM - 1) / vq::kG16BM) * ((M + vq::kG16BN - 1) / vq::kG16BN);
-    return vq::g16_splits(tiles, cols >> 8, device_cus());
-}
 
 size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
@@ -555,7 +541,7 @@ int vq_qgemm(int type, const uint8_t *w, int rows, int cols, const void *xpack, 
 
 size_t vq_qgemm_workspace_bytes(int type, int rows, int cols, int M) {
     if (check_matrix(type, rows, cols) || M < 1 || !gemm16_ok(type, cols, M)) return 0;
-    return vq::g16_layout(cols, M, rows, gemm16_splits(rows, cols, M)).total;
+    return vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, device_cus())).total;
 }
 
 int vq_qgemm_ws(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *workspace,
@@ -570,23 +556,17 @@ int vq_qgemm_ws(int type, const uint8_t *w, int rows, int cols, const void *xpac
     if (!workspace || workspace_bytes < need || misaligned16(workspace)) return VQ_ERR_WORKSPACE;
     const long rb = row_bytes_of(type, cols);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int splits = gemm16_splits(rows, cols, M);
-    const vq::G16Ws l = vq::g16_layout(cols, M, rows, splits);
+    const int cus = device_cus();
+    const vq::G16Ws l = vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, cus));
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     gemm_xsplit_kernel<<<M, 256, 0, s>>>(static_cast<const uint8_t *>(xpack), cols, reinterpret_cast<_Float16 *>(ws + l.bh),
                                          reinterpret_cast<_Float16 *>(ws + l.bl), reinterpret_cast<_Float16 *>(ws + l.xs),
                                          reinterpret_cast<float *>(ws + l.inv));
     st = hip_status(hipGetLastError());
     if (st) return st;
-    float *out = splits > 1 ? reinterpret_cast<float *>(ws + l.part) : y;
-    st = dispatch_quant(type, [&](auto tc) {
-        return vq::launch_gemm16<decltype(tc)::value>(w, rows, cols, rb, ws, M, out, splits, s);
+    return dispatch_quant(type, [&](auto tc) {
+        return vq::launch_gemm16<decltype(tc)::value>(w, rows, cols, rb, ws, M, y, cus, s);
     });
-    if (st || splits == 1) return st;
-    const size_t n = static_cast<size_t>(M) * rows;
-    const int blocks = static_cast<int>((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-    gemm_reduce_kernel<<<blocks, 256, 0, s>>>(out, splits, n, y);
-    return hip_status(hipGetLastError());
 }
 
 size_t vq_lmhead_argmax_workspace_bytes(int type, int rows, int cols, int ntok) {

@@ -32,6 +32,9 @@
 #include "vq_qmv.h"
 #include "vq_tables.h"
 
+#ifdef VQ_TIMING
+extern "C" void *vq_debug_timing_buffer();
+#endif
 namespace vq {
 
 template <int T>
@@ -44,13 +47,46 @@ typedef _Float16 g16h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 g16h2 __attribute__((ext_vector_type(2)));
 typedef float g16f4 __attribute__((ext_vector_type(4)));
 
+// Work split: W workgroups each take an equal contiguous share of the U = tiles x super-blocks work units in
+// tile-major order (unit u = tile * nsb + sb; workgroup b owns [b U / W, (b+1) U / W)). With more tiles than CUs,
+// W = CUs (stream-K: no CU idles through a partial last round); else W is the largest multiple of the tile count
+// that fits the CUs (plain split-K). A workgroup that covers a whole tile writes y; the parts of a
+// tile split between workgroups go to slots [tile][k] (k = the workgroup's order among the tile's) that
+// vq_gemm16_reduce adds in slot order (deterministic).
+struct G16Plan {
+    int tiles, ntt, nsb, W, per_xcd, maxseg;
+    long U;
+    __host__ __device__ int wg_of(long u) const { return static_cast<int>(((u + 1) * W - 1) / U); }  // owner of u
+    __host__ __device__ long u0(int b) const { return static_cast<long>(b) * U / W; }
+};
+inline G16Plan g16_plan(int rows, int cols, int M, int cus) {
+    G16Plan p{};
+    p.ntt = (M + kG16BN - 1) / kG16BN;
+    p.tiles = ((rows + kG16BM - 1) / kG16BM) * p.ntt;
+    p.nsb = cols >> 8;
+    p.U = static_cast<long>(p.tiles) * p.nsb;
+    // Fewer tiles than CUs: an equal whole number of workgroups per tile (each tile splits at super-block
+    // boundaries into that many segments, no workgroup straddles two tiles); else one workgroup per CU.
+    if (p.tiles <= cus) {
+        const int per = cus / p.tiles < p.nsb ? cus / p.tiles : p.nsb;
+        p.W = p.tiles * per;
+    } else {
+        p.W = cus;
+    }
+    p.per_xcd = (p.W + 7) / 8;
+    const long share = p.U / p.W;  // >= 1
+    p.maxseg = static_cast<int>((p.nsb + share - 1) / share + 1);
+    return p;
+}
+
 // Workspace layout of the f16 path for M tokens of `cols` columns: b_hi [M][cols] f16, b_lo [M][cols] f16,
 // xs [M][cols/256][16] f16 (per super-block: X_g xd_g 2^e / 32 as 8 hi then 8 lo), inv [M] fp32 (2^-e),
-// then the split-K partial tiles [splits][M][rows] fp32 (none for one split).
+// then the partial-tile slots [tiles][maxseg][64 values][512 threads] fp32.
+constexpr size_t kG16TileFloats = static_cast<size_t>(kG16BM) * kG16BN;
 struct G16Ws {
     size_t bh, bl, xs, inv, part, total;
 };
-inline G16Ws g16_layout(int cols, int M, int rows, int splits) {
+inline G16Ws g16_layout(int cols, int M, const G16Plan &p) {
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
     G16Ws l{};
     const size_t nb = static_cast<size_t>(M) * cols * 2;
@@ -59,7 +95,7 @@ inline G16Ws g16_layout(int cols, int M, int rows, int splits) {
     l.xs = l.bl + al(nb);
     l.inv = l.xs + al(static_cast<size_t>(M) * (cols / 256) * 32);
     l.part = l.inv + al(static_cast<size_t>(M) * 4);
-    l.total = l.part + (splits > 1 ? al(static_cast<size_t>(splits) * M * rows * 4) : 0);
+    l.total = l.part + al(static_cast<size_t>(p.tiles) * p.maxseg * kG16TileFloats * 4);
     return l;
 }
 
@@ -98,32 +134,45 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
                                                                   long row_bytes, const _Float16 *__restrict__ bh,
                                                                   const _Float16 *__restrict__ bl,
                                                                   const _Float16 *__restrict__ xs,
-                                                                  const float *__restrict__ inv, int M, int nrt,
-                                                                  int ntt, int splits, float *__restrict__ out,
-                                                                  int per_xcd) {
+                                                                  const float *__restrict__ inv, int M, G16Plan pl,
+                                                                  float *__restrict__ y, float *__restrict__ part,
+                                                                  unsigned long long *tm) {
     using G = G16Geo<T>;
+#ifdef VQ_TIMING
+    const unsigned long long tm0 = __builtin_amdgcn_s_memrealtime();
+    unsigned long long t_wait = 0, t_loop0 = 0;
+#else
+    (void)tm;
+#endif
     __shared__ __attribute__((aligned(1024))) uint8_t s_step[kG16Ring][G::STEP_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t s_sb[2][G::SB_BYTES];
 
-    // Workgroup -> (row tile, token tile, split): consecutive ids go round-robin over the 8 XCDs; the ids one
-    // XCD receives map to a contiguous range of tiles, so the workgroups sharing a token tile's activations
-    // and a row tile's weights meet in one L2.
+    // Workgroup id -> share: consecutive ids go round-robin over the 8 XCDs; the ids one XCD receives own
+    // consecutive shares, i.e. a contiguous range of tiles (all token tiles of a row tile share its weights in
+    // that XCD's L2).
     const int b = blockIdx.x;
-    const int v = (b & 7) * per_xcd + (b >> 3);
-    const int ntile = nrt * ntt;
-    if (v >= ntile * splits) return;
-    const int ks = v / ntile, tile = v - ks * ntile;
-    const int rt = tile / ntt, tt = tile - rt * ntt;
-    const int r0 = rt * kG16BM, t0 = tt * kG16BN;
-    const int nsb = cols >> 8;
-    const int sb0 = static_cast<int>(static_cast<long>(ks) * nsb / splits);
-    const int sb1 = static_cast<int>(static_cast<long>(ks + 1) * nsb / splits);
-    const int nsteps = (sb1 - sb0) * 4;
-
+    const int v = (b & 7) * pl.per_xcd + (b >> 3);
+    if (v >= pl.W) return;
+    const int nsb = pl.nsb;
+    const long ue = pl.u0(v + 1);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int wr = 64 * (wv & 3), wt = 64 * (wv >> 2);
     const int lr = lane & 15, lk = lane >> 4;
+#ifdef VQ_TIMING
+    int nsteps_all = 0;
+#endif
+    // The share's tile segments: tile t, super-blocks [sb0, sb1).
+    for (long u = pl.u0(v); u < ue;) {
+    const int tile = static_cast<int>(u / nsb);
+    const int sb0 = static_cast<int>(u - static_cast<long>(tile) * nsb);
+    const int sb1 = ue - u < nsb - sb0 ? sb0 + static_cast<int>(ue - u) : nsb;
+    const int rt = tile / pl.ntt, tt = tile - rt * pl.ntt;
+    const int r0 = rt * kG16BM, t0 = tt * kG16BN;
+    const int nsteps = (sb1 - sb0) * 4;
+#ifdef VQ_TIMING
+    nsteps_all += nsteps;
+#endif
     const uint8_t *const wbase = w + static_cast<size_t>(r0) * row_bytes;  // wave-uniform
 
     // DMA of step st (j = st % 4 of super-block sb0 + st / 4) into ring slot st % 3 and super-block slot sb & 1.
@@ -268,58 +317,122 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
         }
     }
 
-    // Write y (one split) or this split's partial tile: element q of block (rb, tb) is row r0 + wr + 16 rb +
-    // 4 lk + q, token t0 + wt + 16 tb + lr; values leave the 2^e token scale here.
-    float *dst = splits > 1 ? out + static_cast<size_t>(ks) * M * rows : out;
+#ifdef VQ_TIMING
+    const unsigned long long t_loop1 = __builtin_amdgcn_s_memrealtime();
+#endif
+    // Output: element q of block (rb, tb) is row r0 + wr + 16 rb + 4 lk + q, token t0 + wt + 16 tb + lr; values
+    // leave the 2^e token scale here. A whole tile goes to y (four rows per 16-byte store where rows allow); a
+    // part of a tile to its slot, in thread order (coalesced: value i of thread x at [i][x]).
+    if (sb0 == 0 && sb1 == nsb) {
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-        const int t = t0 + wt + 16 * tb + lr;
-        if (t >= M) continue;
-        const float is = inv[t];
+        for (int tb = 0; tb < 4; ++tb) {
+            const int t = t0 + wt + 16 * tb + lr;
+            if (t >= M) continue;
+            const float is = inv[t];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
+            for (int rb = 0; rb < 4; ++rb) {
+                const int r = r0 + wr + 16 * rb + 4 * lk;
+                float *const dst = y + static_cast<size_t>(t) * rows + r;
+                if ((rows & 3) == 0 && r + 3 < rows) {
+                    *reinterpret_cast<float4 *>(dst) = float4{acc[rb][tb][0] * is, acc[rb][tb][1] * is, acc[rb][tb][2] * is, acc[rb][tb][3] * is};
+                } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int r = r0 + wr + 16 * rb + 4 * lk + q;
-                if (r < rows) dst[static_cast<size_t>(t) * rows + r] = acc[rb][tb][q] * is;
+                    for (int q = 0; q < 4; ++q)
+                        if (r + q < rows) dst[q] = acc[rb][tb][q] * is;
+                }
             }
-    }
-}
-
-// Splits of the K range: the fewest workgroup rounds times super-blocks per split, counting each extra split's
-// partial-tile traffic as 3 super-blocks of work.
-inline int g16_splits(int tiles, int nsb, int cus) {
-    int best = 1;
-    long best_cost = -1;
-    for (int s = 1; s <= 8 && s <= nsb; ++s) {
-        const long rounds = (static_cast<long>(tiles) * s + cus - 1) / cus;
-        const long cost = rounds * ((nsb + s - 1) / s) + 3L * (s - 1);
-        if (best_cost < 0 || cost < best_cost) {
-            best_cost = cost;
-            best = s;
+        }
+    } else {
+        const int k = v - pl.wg_of(static_cast<long>(tile) * nsb);
+        float *const slot = part + (static_cast<size_t>(tile) * pl.maxseg + k) * kG16TileFloats;
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const int t = min(t0 + wt + 16 * tb + lr, M - 1);
+            const float is = inv[t];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) slot[static_cast<size_t>((rb * 4 + tb) * 4 + q) * 512 + tid] = acc[rb][tb][q] * is;
         }
     }
-    return best;
+    __syncthreads();  // the ring is reused by the next segment's first DMAs
+    u += sb1 - sb0;
+    }
+#ifdef VQ_TIMING
+    const unsigned long long t_loop1 = tm0;
+    if (tm != nullptr && lane == 0) {
+        const long gw = static_cast<long>(v) * kG16Waves + wv;
+        if (gw < 65536) {
+            unsigned long long *o = tm + 6 * static_cast<size_t>(gw);
+            unsigned xcc;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+            o[0] = tm0; o[1] = t_loop0; o[2] = t_loop1; o[3] = __builtin_amdgcn_s_memrealtime();
+            o[4] = t_wait; o[5] = (static_cast<unsigned long long>(xcc) << 32) | static_cast<unsigned>(nsteps_all);
+        }
+    }
+#endif
+}
+
+// Partial tiles: y = the sum of a tile's slots in slot order. Workgroup (tile, block pair (rb, tb)) of 512
+// threads, thread x summing the four values the GEMM's thread x held for that pair (independent loads, so the
+// slots stream); tiles that one workgroup covered are already in y.
+__global__ __launch_bounds__(512) inline void g16_reduce_kernel(const float *__restrict__ part, G16Plan pl, int rows,
+                                                                int M, float *__restrict__ y) {
+    const int tile = blockIdx.x >> 4, pair = blockIdx.x & 15;
+    const int k0 = pl.wg_of(static_cast<long>(tile) * pl.nsb), k1 = pl.wg_of(static_cast<long>(tile) * pl.nsb + pl.nsb - 1);
+    if (k1 == k0) return;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wr = 64 * (wv & 3), wt = 64 * (wv >> 2), lr = lane & 15, lk = lane >> 4;
+    const int rb = pair >> 2, tb = pair & 3;
+    const int rt = tile / pl.ntt, tt = tile - rt * pl.ntt;
+    const int t = tt * kG16BN + wt + 16 * tb + lr, r = rt * kG16BM + wr + 16 * rb + 4 * lk;
+    const float *const base = part + static_cast<size_t>(tile) * pl.maxseg * kG16TileFloats +
+                              static_cast<size_t>((rb * 4 + tb) * 4) * 512 + tid;
+    float v4[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k <= k1 - k0; ++k) {
+        const float *const sk = base + static_cast<size_t>(k) * kG16TileFloats;
+        const float a0 = sk[0], a1 = sk[512], a2 = sk[1024], a3 = sk[1536];
+        v4[0] += a0;
+        v4[1] += a1;
+        v4[2] += a2;
+        v4[3] += a3;
+    }
+    if (t >= M) return;
+    float *const dst = y + static_cast<size_t>(t) * rows + r;
+    if ((rows & 3) == 0 && r + 3 < rows) {
+        *reinterpret_cast<float4 *>(dst) = float4{v4[0], v4[1], v4[2], v4[3]};
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (r + q < rows) dst[q] = v4[q];
+    }
 }
 
 template <int T>
-int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *out, int splits,
+int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
                   hipStream_t s) {
     if constexpr (!kGemm16<T>) {
-        (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)out, (void)splits, (void)s;
+        (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)y, (void)cus, (void)s;
         return static_cast<int>(hipErrorInvalidValue);
     } else {
-        const G16Ws l = g16_layout(cols, M, rows, splits);
-        const uint8_t *base = static_cast<const uint8_t *>(ws);
-        const int nrt = (rows + kG16BM - 1) / kG16BM, ntt = (M + kG16BN - 1) / kG16BN;
-        const int nwg = nrt * ntt * splits;
-        const int per_xcd = (nwg + 7) / 8;
-        qgemm16_kernel<T><<<dim3(8 * per_xcd), dim3(64 * kG16Waves), 0, s>>>(
+        const G16Plan pl = g16_plan(rows, cols, M, cus);
+        const G16Ws l = g16_layout(cols, M, pl);
+        uint8_t *base = static_cast<uint8_t *>(const_cast<void *>(ws));
+        float *const part = reinterpret_cast<float *>(base + l.part);
+        qgemm16_kernel<T><<<dim3(8 * pl.per_xcd), dim3(64 * kG16Waves), 0, s>>>(
             w, rows, cols, rb, reinterpret_cast<const _Float16 *>(base + l.bh),
             reinterpret_cast<const _Float16 *>(base + l.bl), reinterpret_cast<const _Float16 *>(base + l.xs),
-            reinterpret_cast<const float *>(base + l.inv), M, nrt, ntt, splits,
-            splits > 1 ? reinterpret_cast<float *>(const_cast<uint8_t *>(base) + l.part) : out, per_xcd);
-        const hipError_t e = hipGetLastError();
+            reinterpret_cast<const float *>(base + l.inv), M, pl, y, part,
+#ifdef VQ_TIMING
+            static_cast<unsigned long long *>(vq_debug_timing_buffer())
+#else
+            nullptr
+#endif
+        );
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return static_cast<int>(e);
+        g16_reduce_kernel<<<dim3(16 * pl.tiles), dim3(512), 0, s>>>(part, pl, rows, M, y);
+        e = hipGetLastError();
         return e == hipSuccess ? 0 : static_cast<int>(e);
     }
 }

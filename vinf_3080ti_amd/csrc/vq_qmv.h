@@ -25,11 +25,11 @@ int launch_mixed_q8(int n, const int *types, const uint8_t *const *w, const int 
 template <int T>
 int launch_gemm(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int M, float *y,
                 hipStream_t s);
-// Prefill contraction on f16 MFMA (Q3_K, Q4_K, Q5_K; other types return hipErrorInvalidValue): `ws` holds
-// the split activations written by the library's pre-pass (layout g16_layout), `splits` K ranges whose partial
-// tiles vq_gemm_reduce adds (out = the partial buffer then, else y).
+// Prefill contraction on f16 MFMA (Q4_K, Q5_K; other types return hipErrorInvalidValue): `ws` holds the split
+// activations written by the library's pre-pass and the partial-tile slots (layout g16_layout for
+// g16_plan(rows, cols, M, cus)); one workgroup per CU (cus of them) and the reduction of split tiles.
 template <int T>
-int launch_gemm16(const uint8_t *w, int rows, int cols, long row_bytes, const void *ws, int M, float *out, int splits,
+int launch_gemm16(const uint8_t *w, int rows, int cols, long row_bytes, const void *ws, int M, float *y, int cus,
                   hipStream_t s);
 // Small-batch (2..16 tokens) matvec on int8 MFMA; `part` holds mfma_part_bytes(rows, cols, ntok) bytes (unused
 // when that is 0).

@@ -237,12 +237,15 @@ class Runtime:
 
     def _qmv_ptrs(self, t: _Tensor, x_ptr: int, y_ptr: int, ntok: int) -> None:
         if t.type not in (0, 1) and self.gemm_min_rows > 0 and ntok >= self.gemm_min_rows:
-            # Prompt pass: the MFMA contraction (the prefill branch of Runtime_qmv, qwen_runtime.cu:1886-1902).
-            nws = self._lib.vq_xpack_bytes(t.cols, ntok)
-            xp = self._workspace(nws)
-            _lib.check(self._lib.vq_pack_x(x_ptr, ntok, t.cols, xp.data_ptr(), self._stream()), "pack_x")
-            st = self._lib.vq_qgemm(t.type, t.data.data_ptr(), t.rows, t.cols, xp.data_ptr(), ntok, y_ptr,
-                                    self._stream())
+            # Prompt pass: the MFMA contraction (the prefill branch of Runtime_qmv, qwen_runtime.cu:1886-1902):
+            # packed activations, then the contraction's own workspace (f16 path of Q4_K/Q5_K; 0 bytes otherwise).
+            nx = (self._lib.vq_xpack_bytes(t.cols, ntok) + 255) // 256 * 256
+            ng = self._lib.vq_qgemm_workspace_bytes(t.type, t.rows, t.cols, ntok)
+            buf = self._workspace(nx + ng)
+            xp = buf.data_ptr()
+            _lib.check(self._lib.vq_pack_x(x_ptr, ntok, t.cols, xp, self._stream()), "pack_x")
+            st = self._lib.vq_qgemm_ws(t.type, t.data.data_ptr(), t.rows, t.cols, xp, ntok, y_ptr,
+                                       (xp + nx) if ng else None, ng, self._stream())
             _lib.check(st, "qgemm launch")
             return
         if t.type in (0, 1):
