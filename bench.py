@@ -490,6 +490,8 @@ def main() -> None:
     ap.add_argument("--no-per-type", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant launch (plus a 256 MiB device copy that calibrates PMC byte counters)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prefill contraction legs (512 tokens x Q4_K, both shapes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (weights shard by rows; see "
@@ -500,6 +502,13 @@ def main() -> None:
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     hip = Hip(torch)
+
+    if args.prefill_only:
+        out = {}
+        for rows, cols in ((17408, 5120), (5120, 17408)):
+            out[f"Q4_K_{rows}x{cols}_M512"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512)
+        print(json.dumps({"prefill": out}), flush=True)
+        return
 
     # Roofline of the dominant kernel: the FFN gate+up launch (2 x Q3_K 17408x5120, 64 launches per step).
     log("roofline: grouped Q3_K 2 x 17408x5120 matvec")
