@@ -269,8 +269,8 @@ def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 <
 
 def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=None):
     """the qwen35 SwiGLU MLP block's three matvecs (gate/up Q3_K 17408x5120, down
-    Q6_K 5120x17408) at batch ntok, weights rotating beyond the MALL. mfma=True: the int8-MFMA small-batch
-    path through vq_qmv with its workspace (what vq_qmv picks from 6 tokens on); else the streaming kernel
+    Q6_K 5120x17408) at batch ntok, weights rotating beyond the MALL. mfma=True: vq_qmv with its workspace,
+    which takes the f16-MFMA small-batch matvec for these types from 5 tokens on; else the streaming kernel
     (grouped gate/up + down, activations quantized in-kernel). Default: as vq_qmv routes."""
     from vinf_3080ti_amd import row_bytes
 
@@ -284,7 +284,7 @@ def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=Non
     g, u, d = (torch.empty(ntok, F, device="cuda"), torch.empty(ntok, F, device="cuda"),
                torch.empty(ntok, H, device="cuda"))
     lib = hip.lib
-    mfma = ntok >= 6 if mfma is None else mfma
+    mfma = ntok >= 5 if mfma is None else mfma
     nws = max(lib.vq_qmv_workspace_bytes_for(Q3_K, F, H, ntok), lib.vq_qmv_workspace_bytes_for(Q6_K, H, F, ntok))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
 

@@ -447,6 +447,25 @@ def test_qmv_mfma_small_batch_matches_oracle(env, oracle_mod, ty, ntok):
         assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, ntok, t)
 
 
+@pytest.mark.parametrize("ty", [T.Q3_K, T.Q4_K, T.Q5_K, T.Q6_K], ids=lambda t: t.name)
+@pytest.mark.parametrize("ntok,rows,cols", [(5, 300, 768), (6, 17, 256), (7, 513, 2048), (8, 256, 1280),
+                                            (16, 40, 768)])
+def test_qmv_small16_matches_oracle(env, oracle_mod, ty, ntok, rows, cols):
+    """The f16-MFMA small-batch matvec (5..16 tokens): ragged 256-row blocks, a short last K range, one K range
+    without partials, tokens of very different magnitudes (per-token scales), bit-identical on a rerun."""
+    torch, lib = env
+    rng = np.random.default_rng(9000 + 37 * ntok + rows + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    x[0] *= 1e-3
+    x[-1, :64] *= 40.0
+    got = gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok, fast=True)
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok)
+    for t in range(ntok):
+        assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, ntok, t)
+    assert np.array_equal(gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok, fast=True), got)
+
+
 @pytest.mark.parametrize("ty,rows,cols", [(T.Q3_K, 17408, 5120), (T.Q4_K, 5120, 17408), (T.Q6_K, 5120, 6144),
                                           (T.IQ2_XXS, 5120, 17408), (T.Q8_0, 48, 5120), (T.Q5_K, 1000, 5120)],
                          ids=lambda v: v.name if isinstance(v, T) else str(v))

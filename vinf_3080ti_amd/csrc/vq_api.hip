@@ -11,6 +11,7 @@
 // Data layout in HBM: weights are the GGUF tensor bytes as uploaded (row-major, row_bytes =
 // cols/block_size*type_size, rows back to back, >= VQ_TAIL_PAD readable bytes after the last row).
 // Activations x[t*cols + c] fp32, outputs y[t*rows + r] fp32 (the reference's token-major layout).
+#include <atomic>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -306,11 +307,18 @@ bool gemm16_ok(int type, int cols, int M) {
 
 // Compute units of the current device (256 when there is none: workspace sizes stay computable).
 int device_cus() {
+    static std::atomic<int> cached[64];  // per device ordinal, 0 = not yet asked
     int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) {
+    if (hipGetDevice(&dev) != hipSuccess) {
         (void)hipGetLastError();
         return 256;
     }
+    if (dev >= 0 && dev < 64 && (n = cached[dev].load(std::memory_order_relaxed)) > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (dev >= 0 && dev < 64) cached[dev].store(n, std::memory_order_relaxed);
     return n;
 }
 
@@ -379,8 +387,18 @@ size_t vq_qmv_workspace_bytes(int cols, int ntok) {
 constexpr int kMfmaMinTok = 6;
 bool mfma_batch(int type, int ntok) { return type != VQ_F32 && type != VQ_F16 && ntok >= kMfmaMinTok && ntok <= 16; }
 
+// 5..16 tokens of Q3_K/Q4_K/Q5_K/Q6_K take the f16-MFMA matvec (vq_small16_impl.h) when the workspace holds its
+// K-range partials (none for cols <= 512); below 5 tokens the streaming kernel is faster (measured on MI355X on
+// the SwiGLU block: 2 tokens 49 vs 91 us, 4 tokens 85 vs 96 us, 8 tokens 171 vs 103 us).
+constexpr int kSmall16MinTok = 5;
+bool small16_batch(int type, int cols, int ntok) {
+    return (type == VQ_Q3_K || type == VQ_Q4_K || type == VQ_Q5_K || type == VQ_Q6_K) && cols % 256 == 0 &&
+           ntok >= kSmall16MinTok && ntok <= 16;
+}
+
 size_t vq_qmv_workspace_bytes_for(int type, int rows, int cols, int ntok) {
     if (check_matrix(type, rows, cols) || ntok < 1) return 0;
+    if (small16_batch(type, cols, ntok)) return vq::s16_part_bytes(rows, cols, ntok);
     if (mfma_batch(type, ntok)) return align256(vq_xpack_bytes(cols, ntok)) + vq::mfma_part_bytes(rows, cols, ntok);
     return (type == VQ_F32 || type == VQ_F16) ? 0 : vq_qmv_workspace_bytes(cols, ntok);
 }
@@ -429,6 +447,15 @@ int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int n
     if (type == VQ_F32) return launch_float<VQ_F32>(w, rows, cols, x, ntok, y, s);
     if (type == VQ_F16) return launch_float<VQ_F16>(w, rows, cols, x, ntok, y, s);
     const long rb = row_bytes_of(type, cols);
+    if (small16_batch(type, cols, ntok)) {
+        const size_t np = vq::s16_part_bytes(rows, cols, ntok);
+        if (np == 0 || (workspace && !misaligned16(workspace) && workspace_bytes >= np)) {
+            float *part = np ? static_cast<float *>(workspace) : nullptr;
+            return dispatch_quant(type, [&](auto tc) {
+                return vq::launch_small16<decltype(tc)::value>(w, rows, cols, rb, x, ntok, y, part, s);
+            });
+        }
+    }
     if (mfma_batch(type, ntok) && workspace && !misaligned16(workspace) &&
         workspace_bytes >= vq_qmv_workspace_bytes_for(type, rows, cols, ntok)) {
         const size_t xpb = align256(vq_xpack_bytes(cols, ntok));

@@ -1,0 +1,329 @@
+// vq_small16_impl.h -- matvec for a few tokens (1..16: speculative verify, small batches) on f16 MFMA, for the K-quants
+// whose sub-block products fit f16 exactly (Q3_K, Q4_K, Q5_K; Q6_K as two exact terms).
+//
+// Numerics: those of the prefill path (vq_gemm16_impl.h). Each weight element is the integer a = code * sc
+// (exact in f16: |a| <= 128 for Q3_K, 945 for Q4_K, 1953 for Q5_K; Q6_K's |(q - 32) * sc| <= 4096 is split into
+// 16 * ((q - 32) * (sc >> 4)) + (q - 32) * (sc & 15), both exact), each activation element b = xq * xd * 2^e
+// (the CPU path's int8 codes and group scale, one fp32 rounding, 2^e per token and K range) is two f16
+// (b_hi + b_lo), and each super-block's C = sum a * (b_hi + b_lo) comes from v_mfma_f32_16x16x32_f16 (exact
+// products, fp32 sums) before acc += d * C - 32 * dmin * (m . XS) once per super-block (qwen_cpu.c:581-641
+// regrouped per super-block).
+//
+// Work split: workgroup (128-row block, K range of 512 columns) of 8 waves, one tile each (a persistent walk over
+// row tiles with the next tile's slices prefetched measured slower, as did 16 waves, 1024-column ranges and
+// weight bytes staged through LDS with 16-byte loads); wave w owns 16 rows and the whole range (two super-blocks), a 16-row x 16-token MFMA tile (tokens beyond ntok are zero lanes). At start each
+// wave loads its rows' raw slices of both super-blocks (lane = (row, quarter of the super-block); the slice
+// decoders of vq_slices.h), while the workgroup quantizes its slice of the fp32 activations (quantize_group,
+// the CPU path's IEEE operations) and splits it into the f16 pair in LDS. Lane (row, q) decodes its quarter into
+// 8 MFMA chunks of 8 elements; the B operand of lane (token, q) is the same 8 positions of that token. K ranges
+// write partial sums [range][t][r] (scaled back from 2^e) that a second kernel adds in range order
+// (deterministic).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vq_gemm16_impl.h"
+#include "vq_qmv.h"
+#include "vq_quant.h"
+#include "vq_tables.h"
+
+namespace vq {
+
+template <int T>
+constexpr bool kSmall16 = T == VQ_Q3_K || T == VQ_Q4_K || T == VQ_Q5_K || T == VQ_Q6_K;
+
+#ifndef VQ_S16_WAVES
+#define VQ_S16_WAVES 8
+#endif
+#ifndef VQ_S16_OCC
+#define VQ_S16_OCC 2
+#endif
+#ifndef VQ_S16_KR
+#define VQ_S16_KR 512
+#endif
+constexpr int kS16Occ = VQ_S16_OCC;  // waves per SIMD the register budget is set for
+constexpr int kS16Waves = VQ_S16_WAVES, kS16Rows = 16 * kS16Waves, kS16KR = VQ_S16_KR, kS16NSB = kS16KR / 256;
+constexpr int kS16RowHalves = kS16KR + 8;  // f16 per token row of the activation image (16-byte pad)
+
+// LDS of one workgroup for ntok tokens: b_hi, b_lo [ntok][kS16RowHalves] f16, xs [ntok][2][16] f16,
+// codes [ntok][kS16KR] int8, xd [ntok][KR/32] fp32, X [ntok][KR/32] int32, token scale [16] fp32.
+__host__ __device__ inline size_t s16_lds(int ntok) {
+    return static_cast<size_t>(ntok) * (2 * kS16RowHalves * 2 + kS16NSB * 16 * 2 + kS16KR + (kS16KR / 32) * 4 * 2) + 64;
+}
+inline int s16_ranges(int cols) { return (cols + kS16KR - 1) / kS16KR; }
+inline size_t s16_part_bytes(int rows, int cols, int ntok) {
+    const int nkr = s16_ranges(cols);
+    return nkr > 1 ? (static_cast<size_t>(nkr) * ntok * rows * 4 + 255) / 256 * 256 : 0;
+}
+
+// Eight codes (bytes of c0, c1) times the part's scale, as f16: exact for every type here.
+template <int T>
+__device__ __forceinline__ void s16_frag(uint32_t c0, uint32_t c1, int isc, g16h8 &a1, g16h8 &a2) {
+    const g16h2 k = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+    g16h2 v[4] = {g16_pair(c0, 0x04010400u), g16_pair(c0, 0x04030402u), g16_pair(c1, 0x04010400u),
+                  g16_pair(c1, 0x04030402u)};  // 1024 + code
+    if constexpr (T == VQ_Q4_K || T == VQ_Q5_K) {
+        const _Float16 s = static_cast<_Float16>(isc);
+        const g16h2 s2 = {s, s};
+        const _Float16 nb = static_cast<_Float16>(-1024.0f) * s;  // exact: sc < 64
+        const g16h2 n2 = {nb, nb};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = __builtin_elementwise_fma(v[i], s2, n2);  // code * sc in one rounding
+        a1 = g16h8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
+    } else if constexpr (T == VQ_Q3_K) {
+        const g16h2 off = {static_cast<_Float16>(1028.0f), static_cast<_Float16>(1028.0f)};
+        const _Float16 s = static_cast<_Float16>(isc);
+        const g16h2 s2 = {s, s};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (v[i] - off) * s2;  // (code - 4) * (sc - 32): exact, |.| <= 128
+        a1 = g16h8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
+    } else {  // Q6_K: (q - 32) * sc = (q - 32) * 16 (sc >> 4) + (q - 32) * (sc & 15)
+        const g16h2 off = {static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
+        const _Float16 sh = static_cast<_Float16>(16 * (isc >> 4)), sl = static_cast<_Float16>(isc & 15);
+        const g16h2 h2 = {sh, sh}, l2 = {sl, sl};
+        g16h2 w1[4], w2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const g16h2 q = v[i] - off;  // q - 32, exact
+            w1[i] = q * h2;              // multiple of 16, |.| <= 4096: exact
+            w2[i] = q * l2;              // |.| <= 480: exact
+        }
+        a1 = g16h8{w1[0][0], w1[0][1], w1[1][0], w1[1][1], w1[2][0], w1[2][1], w1[3][0], w1[3][1]};
+        a2 = g16h8{w2[0][0], w2[0][1], w2[1][0], w2[1][1], w2[2][0], w2[2][1], w2[3][0], w2[3][1]};
+    }
+    (void)k;
+}
+
+__device__ __forceinline__ void s16_opaque(float &v) { asm volatile("" : "+v"(v)); }
+
+template <int T>
+__global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const uint8_t *__restrict__ w, int rows, int cols,
+                                                              long row_bytes, const float *__restrict__ x, int ntok,
+                                                              float *__restrict__ out) {
+    using S = Sl<T>;
+    constexpr int SPL = S::SPB / 4;  // slices per lane per super-block: a lane owns a quarter of it
+    constexpr int NP = S::NP;
+    constexpr bool MIN = kHasMin<T>;
+    static_assert(SPL * NP * 16 == 64, "a quarter super-block per lane");
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
+    _Float16 *const xh = reinterpret_cast<_Float16 *>(s_dyn);
+    _Float16 *const xl = xh + ntok * kS16RowHalves;
+    _Float16 *const xsd = xl + ntok * kS16RowHalves;                      // [t][sb][16]
+    int8_t *const xq = reinterpret_cast<int8_t *>(xsd + ntok * kS16NSB * 16);  // [t][KR]
+    float *const xdg = reinterpret_cast<float *>(xq + ntok * kS16KR);    // [t][KR/32]
+    int *const xsum = reinterpret_cast<int *>(xdg + ntok * (kS16KR / 32));  // [t][KR/32]
+    float *const tsc = reinterpret_cast<float *>(xsum + ntok * (kS16KR / 32));  // [16]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lr = lane & 15, lk = lane >> 4;
+    const int kr = blockIdx.y, k0 = kr * kS16KR;
+    const int kw = cols - k0 < kS16KR ? cols - k0 : kS16KR;  // a multiple of 256
+    const int nsb = kw >> 8, sbg0 = k0 >> 8;
+    const int ngr = kw >> 5;
+
+    // 1. This lane's raw slices of the workgroup's row tile: row 16 wv + lr of it, quarter lk of each super-block
+    // of the range (issued first, in flight while the activations are quantized).
+    auto load_tile = [&](int tile, typename S::W (&wr)[kS16NSB][SPL]) {
+        const int row = min(tile * kS16Rows + 16 * wv + lr, rows - 1);
+        const uint8_t *const wrow = w + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(sbg0) * S::UB;
+#pragma unroll
+        for (int sb = 0; sb < kS16NSB; ++sb)
+#pragma unroll
+            for (int si = 0; si < SPL; ++si) S::load(wrow + (sb < nsb ? sb : 0) * S::UB, SPL * lk + si, wr[sb][si]);
+    };
+    const int tile = blockIdx.x;
+    typename S::W wr[kS16NSB][SPL];
+    load_tile(tile, wr);
+
+    // 2. The activation slice: int8 codes per 32-group (the CPU path's quantize_group), then per token the
+    // power of two 2^e with 127 max(xd) 2^e < 2^15, then b = xq * (xd 2^e) split into two f16.
+    for (int i = tid; i < ntok * ngr; i += blockDim.x) {
+        const int t = i / ngr, g = i - t * ngr;
+        const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols + k0 + 32 * g);
+        float v[32];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 f = src[q];
+            v[4 * q] = f.x;
+            v[4 * q + 1] = f.y;
+            v[4 * q + 2] = f.z;
+            v[4 * q + 3] = f.w;
+        }
+        const QGroup qg = quantize_group(v);
+        uint4 *dq = reinterpret_cast<uint4 *>(xq + t * kS16KR + 32 * g);
+        dq[0] = uint4{qg.q[0], qg.q[1], qg.q[2], qg.q[3]};
+        dq[1] = uint4{qg.q[4], qg.q[5], qg.q[6], qg.q[7]};
+        xdg[t * (kS16KR / 32) + g] = qg.d;
+        xsum[t * (kS16KR / 32) + g] = qg.hs0 + qg.hs1;
+    }
+    __syncthreads();
+    if (tid < ntok) {
+        float m = 0.0f;
+        for (int g = 0; g < ngr; ++g) m = fmaxf(m, xdg[tid * (kS16KR / 32) + g]);
+        int E = 0;
+        (void)frexpf(127.0f * m, &E);
+        tsc[tid] = m > 0.0f ? ldexpf(1.0f, 15 - E) : 1.0f;
+    }
+    __syncthreads();
+    for (int i = tid; i < ntok * (kw / 4); i += blockDim.x) {
+        const int t = i / (kw / 4), c = 4 * (i - t * (kw / 4));
+        const float ds = xdg[t * (kS16KR / 32) + (c >> 5)] * tsc[t];
+        const uint32_t q4 = *reinterpret_cast<const uint32_t *>(xq + t * kS16KR + c);
+        _Float16 h[4], l[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float v = static_cast<float>(static_cast<int8_t>(q4 >> (8 * j))) * ds;
+            s16_opaque(v);  // the split of the fp32 product (no contraction into a mixed-precision fma)
+            h[j] = static_cast<_Float16>(v);
+            l[j] = static_cast<_Float16>(v - static_cast<float>(h[j]));
+        }
+        *reinterpret_cast<uint2 *>(xh + t * kS16RowHalves + c) = __builtin_bit_cast(uint2, h);
+        *reinterpret_cast<uint2 *>(xl + t * kS16RowHalves + c) = __builtin_bit_cast(uint2, l);
+    }
+    if constexpr (MIN) {
+        for (int i = tid; i < ntok * ngr; i += blockDim.x) {
+            const int t = i / ngr, g = i - t * ngr;
+            float v = static_cast<float>(xsum[t * (kS16KR / 32) + g]) * (xdg[t * (kS16KR / 32) + g] * tsc[t]) * 0.03125f;
+            s16_opaque(v);
+            const _Float16 hi = static_cast<_Float16>(v);
+            xsd[(t * kS16NSB + (g >> 3)) * 16 + (g & 7)] = hi;
+            xsd[(t * kS16NSB + (g >> 3)) * 16 + 8 + (g & 7)] = static_cast<_Float16>(v - static_cast<float>(hi));
+        }
+    }
+    __syncthreads();
+
+    // 3. Per super-block: 8 chunks x (b_hi, b_lo) MFMAs (Q6_K: both weight terms), the min MFMA, the scaling.
+    // C element j is row 4 lk + j of the wave's 16, token lr.
+    const bool tok_ok = lr < ntok;
+    const int tb = tok_ok ? lr : 0;
+    const float is = 1.0f / tsc[tb];
+    float *const o = out + (static_cast<size_t>(kr) * ntok + tb) * rows;
+    g16f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sb = 0; sb < kS16NSB; ++sb) {
+        if (sb >= nsb) break;
+        g16f4 C = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int si = 0; si < SPL; ++si) {
+            const int sl = SPL * lk + si;
+            uint32_t cd[NP][4];
+            S::codes(wr[sb][si], sl, Tabs{}, cd);
+            int isc[NP];
+            S::iscales(wr[sb][si], sl, isc);
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                int pg, ph;
+                S::part(sl, p, pg, ph);
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    g16h8 a1, a2;
+                    s16_frag<T>(cd[p][2 * hf], cd[p][2 * hf + 1], isc[p], a1, a2);
+                    // this lane's 8 positions of the chunk: pg, ph, hf of its own slice; the B lanes (token, lk)
+                    // of the same lk take the same positions
+                    const int e = 256 * sb + 32 * pg + 16 * ph + 8 * hf;
+                    g16h8 bh = *reinterpret_cast<const g16h8 *>(xh + tb * kS16RowHalves + e);
+                    g16h8 bl = *reinterpret_cast<const g16h8 *>(xl + tb * kS16RowHalves + e);
+                    if (!tok_ok) bh = bl = g16h8{};
+                    C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bh, C, 0, 0, 0);
+                    C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bl, C, 0, 0, 0);
+                    if constexpr (T == VQ_Q6_K) {
+                        C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bh, C, 0, 0, 0);
+                        C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bl, C, 0, 0, 0);
+                    }
+                }
+            }
+        }
+        // d (and dmin) of the C rows: row 4 lk + j's values sit in lane 4 lk + j (lk = 0 there).
+        const float dmy = S::dmul(wr[sb][0]);
+        float dmn = 0.0f;
+        if constexpr (MIN) dmn = 32.0f * S::dmin(wr[sb][0]);
+        g16f4 cm = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (MIN) {
+            // A_min: row lr, k = 4 lk .. +4 -> mins of groups 4 (lk & 1) .. +4 (k4_scale_min packing, qwen_cpu.c:54-62)
+            const uint32_t hy = wr[sb][0].hd[1], hz = wr[sb][0].hd[2], hw = wr[sb][0].hd[3];
+            const uint32_t mw = (lk & 1) ? (((hw >> 4) & 0x0F0F0F0Fu) | ((hz >> 2) & 0x30303030u)) : (hz & 0x3F3F3F3Fu);
+            const g16h2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+            const g16h2 m01 = g16_pair(mw, 0x04010400u) - k1024, m23 = g16_pair(mw, 0x04030402u) - k1024;
+            const g16h4 am = {m01[0], m01[1], m23[0], m23[1]};
+            g16h4 bm = *reinterpret_cast<const g16h4 *>(xsd + (tb * kS16NSB + sb) * 16 + 4 * lk);
+            if (!tok_ok) bm = g16h4{};
+            cm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, cm, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float dj = __shfl(dmy, 4 * lk + j, 64);
+            const float mj = MIN ? __shfl(dmn, 4 * lk + j, 64) : 0.0f;
+            acc[j] = fmaf(dj, C[j], fmaf(-mj, cm[j], acc[j]));
+        }
+    }
+
+    // 4. Out: rows 16 wv + 4 lk + j of the tile for token lr, back from the token's 2^e (partials of K range kr
+    // when the columns span several ranges).
+    if (tok_ok) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = tile * kS16Rows + 16 * wv + 4 * lk + j;
+            if (r < rows) o[r] = acc[j] * is;
+        }
+    }
+}
+
+// y = sum of the K ranges' partials, in range order; four outputs per thread (n % 4 == 0), loads four ranges ahead.
+__global__ __launch_bounds__(256) inline void s16_sum_kernel(const float *__restrict__ part, int nkr, long n,
+                                                            float *__restrict__ y) {
+    const long i = (static_cast<long>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    const float4 *p = reinterpret_cast<const float4 *>(part + i);
+    const long st = n / 4;
+    float4 v = p[0];
+    int k = 1;
+    for (; k + 4 <= nkr; k += 4) {
+        const float4 a = p[k * st], b = p[(k + 1) * st], c = p[(k + 2) * st], d = p[(k + 3) * st];
+        v.x += a.x, v.y += a.y, v.z += a.z, v.w += a.w;
+        v.x += b.x, v.y += b.y, v.z += b.z, v.w += b.w;
+        v.x += c.x, v.y += c.y, v.z += c.z, v.w += c.w;
+        v.x += d.x, v.y += d.y, v.z += d.z, v.w += d.w;
+    }
+    for (; k < nkr; ++k) {
+        const float4 a = p[k * st];
+        v.x += a.x, v.y += a.y, v.z += a.z, v.w += a.w;
+    }
+    *reinterpret_cast<float4 *>(y + i) = v;
+}
+
+// The same, one output per thread (any n).
+__global__ __launch_bounds__(256) inline void s16_sum1_kernel(const float *__restrict__ part, int nkr, long n,
+                                                             float *__restrict__ y) {
+    const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    float v = part[i];
+    for (int k = 1; k < nkr; ++k) v += part[static_cast<size_t>(k) * n + i];
+    y[i] = v;
+}
+
+template <int T>
+int launch_small16(const uint8_t *w, int rows, int cols, long rb, const float *x, int ntok, float *y, float *part,
+                   hipStream_t s) {
+    if constexpr (!kSmall16<T>) {
+        (void)w, (void)rows, (void)cols, (void)rb, (void)x, (void)ntok, (void)y, (void)part, (void)s;
+        return static_cast<int>(hipErrorInvalidValue);
+    } else {
+        if (ntok < 1 || ntok > 16 || cols % 256 != 0) return static_cast<int>(hipErrorInvalidValue);
+        const int nkr = s16_ranges(cols);
+        if (nkr > 1 && part == nullptr) return static_cast<int>(hipErrorInvalidValue);
+        const dim3 grid((rows + kS16Rows - 1) / kS16Rows, nkr), block(64 * kS16Waves);
+        qmv16_kernel<T><<<grid, block, s16_lds(ntok), s>>>(w, rows, cols, rb, x, ntok, nkr > 1 ? part : y);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess || nkr == 1) return static_cast<int>(e);
+        const long n = static_cast<long>(ntok) * rows;
+        if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(y)) % 16 == 0)
+            s16_sum_kernel<<<static_cast<unsigned>((n / 4 + 255) / 256), 256, 0, s>>>(part, nkr, n, y);
+        else
+            s16_sum1_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(part, nkr, n, y);
+        e = hipGetLastError();
+        return e == hipSuccess ? 0 : static_cast<int>(e);
+    }
+}
+
+}  // namespace vq
