@@ -45,10 +45,12 @@ constexpr int kS16Occ = VQ_S16_OCC;  // waves per SIMD the register budget is se
 constexpr int kS16Waves = VQ_S16_WAVES, kS16Rows = 16 * kS16Waves, kS16KR = VQ_S16_KR, kS16NSB = kS16KR / 256;
 constexpr int kS16RowHalves = kS16KR + 8;  // f16 per token row of the activation image (16-byte pad)
 
-// LDS of one workgroup for ntok tokens: b_hi, b_lo [ntok][kS16RowHalves] f16, xs [ntok][2][16] f16,
-// codes [ntok][kS16KR] int8, xd [ntok][KR/32] fp32, X [ntok][KR/32] int32, token scale [16] fp32.
+// LDS of one workgroup for ntok tokens: b_hi, b_lo [ntok + 1][kS16RowHalves] f16, xs [ntok + 1][2][16] f16 (row
+// ntok all zero: the B rows of the MFMA lanes past the last token), codes [ntok][kS16KR] int8, xd [ntok][KR/32]
+// fp32, X [ntok][KR/32] int32, token scale [16] fp32.
 __host__ __device__ inline size_t s16_lds(int ntok) {
-    return static_cast<size_t>(ntok) * (2 * kS16RowHalves * 2 + kS16NSB * 16 * 2 + kS16KR + (kS16KR / 32) * 4 * 2) + 64;
+    return static_cast<size_t>(ntok + 1) * (2 * kS16RowHalves * 2 + kS16NSB * 16 * 2) +
+           static_cast<size_t>(ntok) * (kS16KR + (kS16KR / 32) * 4 * 2) + 64;
 }
 inline int s16_ranges(int cols) { return (cols + kS16KR - 1) / kS16KR; }
 inline size_t s16_part_bytes(int rows, int cols, int ntok) {
@@ -107,9 +109,9 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const ui
     static_assert(SPL * NP * 16 == 64, "a quarter super-block per lane");
     extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
     _Float16 *const xh = reinterpret_cast<_Float16 *>(s_dyn);
-    _Float16 *const xl = xh + ntok * kS16RowHalves;
-    _Float16 *const xsd = xl + ntok * kS16RowHalves;                      // [t][sb][16]
-    int8_t *const xq = reinterpret_cast<int8_t *>(xsd + ntok * kS16NSB * 16);  // [t][KR]
+    _Float16 *const xl = xh + (ntok + 1) * kS16RowHalves;
+    _Float16 *const xsd = xl + (ntok + 1) * kS16RowHalves;                      // [t][sb][16]
+    int8_t *const xq = reinterpret_cast<int8_t *>(xsd + (ntok + 1) * kS16NSB * 16);  // [t][KR]
     float *const xdg = reinterpret_cast<float *>(xq + ntok * kS16KR);    // [t][KR/32]
     int *const xsum = reinterpret_cast<int *>(xdg + ntok * (kS16KR / 32));  // [t][KR/32]
     float *const tsc = reinterpret_cast<float *>(xsum + ntok * (kS16KR / 32));  // [16]
@@ -138,6 +140,11 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const ui
 
     // 2. The activation slice: int8 codes per 32-group (the CPU path's quantize_group), then per token the
     // power of two 2^e with 127 max(xd) 2^e < 2^15, then b = xq * (xd 2^e) split into two f16.
+    for (int i = tid; i < kS16KR / 4; i += blockDim.x) {  // the zero token row (8 bytes of b_hi, b_lo each)
+        *reinterpret_cast<uint2 *>(xh + ntok * kS16RowHalves + 4 * i) = uint2{0u, 0u};
+        *reinterpret_cast<uint2 *>(xl + ntok * kS16RowHalves + 4 * i) = uint2{0u, 0u};
+    }
+    if (tid < kS16NSB * 16 / 2) reinterpret_cast<uint32_t *>(xsd + ntok * kS16NSB * 16)[tid] = 0u;
     for (int i = tid; i < ntok * ngr; i += blockDim.x) {
         const int t = i / ngr, g = i - t * ngr;
         const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols + k0 + 32 * g);
@@ -196,9 +203,9 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const ui
     // 3. Per super-block: 8 chunks x (b_hi, b_lo) MFMAs (Q6_K: both weight terms), the min MFMA, the scaling.
     // C element j is row 4 lk + j of the wave's 16, token lr.
     const bool tok_ok = lr < ntok;
-    const int tb = tok_ok ? lr : 0;
-    const float is = 1.0f / tsc[tb];
-    float *const o = out + (static_cast<size_t>(kr) * ntok + tb) * rows;
+    const int tb = tok_ok ? lr : ntok;  // the zero row
+    const float is = 1.0f / tsc[tok_ok ? lr : 0];
+    float *const o = out + (static_cast<size_t>(kr) * ntok + (tok_ok ? lr : 0)) * rows;
     g16f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sb = 0; sb < kS16NSB; ++sb) {
@@ -224,7 +231,6 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const ui
                     const int e = 256 * sb + 32 * pg + 16 * ph + 8 * hf;
                     g16h8 bh = *reinterpret_cast<const g16h8 *>(xh + tb * kS16RowHalves + e);
                     g16h8 bl = *reinterpret_cast<const g16h8 *>(xl + tb * kS16RowHalves + e);
-                    if (!tok_ok) bh = bl = g16h8{};
                     C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bh, C, 0, 0, 0);
                     C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bl, C, 0, 0, 0);
                     if constexpr (T == VQ_Q6_K) {
@@ -246,8 +252,7 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const ui
             const g16h2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
             const g16h2 m01 = g16_pair(mw, 0x04010400u) - k1024, m23 = g16_pair(mw, 0x04030402u) - k1024;
             const g16h4 am = {m01[0], m01[1], m23[0], m23[1]};
-            g16h4 bm = *reinterpret_cast<const g16h4 *>(xsd + (tb * kS16NSB + sb) * 16 + 4 * lk);
-            if (!tok_ok) bm = g16h4{};
+            const g16h4 bm = *reinterpret_cast<const g16h4 *>(xsd + (tb * kS16NSB + sb) * 16 + 4 * lk);
             cm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, cm, 0, 0, 0);
         }
 #pragma unroll
