@@ -134,6 +134,24 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const ui
 #pragma unroll
             for (int si = 0; si < SPL; ++si) S::load(wrow + (sb < nsb ? sb : 0) * S::UB, SPL * lk + si, wr[sb][si]);
     };
+    // The activation group this thread quantizes (at most one: 16 tokens x KR/32 groups fit the workgroup),
+    // loaded before the weights: loads return in order, and waiting for it behind the weight burst would
+    // serialize the two.
+    static_assert(16 * (kS16KR / 32) <= 64 * kS16Waves, "one activation group per thread");
+    const bool has_group = tid < ntok * ngr;
+    const int gt = has_group ? tid / ngr : 0, gg = has_group ? tid - gt * ngr : 0;
+    float v[32];
+    if (has_group) {
+        const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(gt) * cols + k0 + 32 * gg);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 f = src[q];
+            v[4 * q] = f.x;
+            v[4 * q + 1] = f.y;
+            v[4 * q + 2] = f.z;
+            v[4 * q + 3] = f.w;
+        }
+    }
     const int tile = blockIdx.x;
     typename S::W wr[kS16NSB][SPL];
     load_tile(tile, wr);
@@ -145,24 +163,13 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const ui
         *reinterpret_cast<uint2 *>(xl + ntok * kS16RowHalves + 4 * i) = uint2{0u, 0u};
     }
     if (tid < kS16NSB * 16 / 2) reinterpret_cast<uint32_t *>(xsd + ntok * kS16NSB * 16)[tid] = 0u;
-    for (int i = tid; i < ntok * ngr; i += blockDim.x) {
-        const int t = i / ngr, g = i - t * ngr;
-        const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols + k0 + 32 * g);
-        float v[32];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float4 f = src[q];
-            v[4 * q] = f.x;
-            v[4 * q + 1] = f.y;
-            v[4 * q + 2] = f.z;
-            v[4 * q + 3] = f.w;
-        }
+    if (has_group) {
         const QGroup qg = quantize_group(v);
-        uint4 *dq = reinterpret_cast<uint4 *>(xq + t * kS16KR + 32 * g);
+        uint4 *dq = reinterpret_cast<uint4 *>(xq + gt * kS16KR + 32 * gg);
         dq[0] = uint4{qg.q[0], qg.q[1], qg.q[2], qg.q[3]};
         dq[1] = uint4{qg.q[4], qg.q[5], qg.q[6], qg.q[7]};
-        xdg[t * (kS16KR / 32) + g] = qg.d;
-        xsum[t * (kS16KR / 32) + g] = qg.hs0 + qg.hs1;
+        xdg[gt * (kS16KR / 32) + gg] = qg.d;
+        xsum[gt * (kS16KR / 32) + gg] = qg.hs0 + qg.hs1;
     }
     __syncthreads();
     if (tid < ntok) {
