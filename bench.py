@@ -492,6 +492,8 @@ def main() -> None:
                     help="only the dominant launch (plus a 256 MiB device copy that calibrates PMC byte counters)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill contraction legs (512 tokens x Q4_K, both shapes)")
+    ap.add_argument("--mlp-only", action="store_true",
+                    help="only the SwiGLU MLP block at batch 1, 4, 8 (as vq_qmv routes) and 8 on the streaming kernel")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (weights shard by rows; see "
@@ -508,6 +510,11 @@ def main() -> None:
         for rows, cols in ((17408, 5120), (5120, 17408)):
             out[f"Q4_K_{rows}x{cols}_M512"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512)
         print(json.dumps({"prefill": out}), flush=True)
+        return
+    if args.mlp_only:
+        out = {f"batch{n}": bench_mlp(torch, hip, n) for n in (1, 4, 8)}
+        out["batch8_stream"] = bench_mlp(torch, hip, 8, mfma=False)
+        print(json.dumps({"mlp_block": out}), flush=True)
         return
 
     # Roofline of the dominant kernel: the FFN gate+up launch (2 x Q3_K 17408x5120, 64 launches per step).
