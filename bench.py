@@ -269,9 +269,10 @@ def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 <
 
 def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=None):
     """the qwen35 SwiGLU MLP block's three matvecs (gate/up Q3_K 17408x5120, down
-    Q6_K 5120x17408) at batch ntok, weights rotating beyond the MALL. mfma=True: vq_qmv with its workspace,
-    which takes the f16-MFMA small-batch matvec for these types from 5 tokens on; else the streaming kernel
-    (grouped gate/up + down, activations quantized in-kernel). Default: as vq_qmv routes."""
+    Q6_K 5120x17408) at batch ntok, weights rotating beyond the MALL. mfma=True: vq_qmv with its workspace for
+    all three (the f16-MFMA small-batch matvec for these types from 5 tokens on, and from 3 over the 17408-wide
+    down input); mfma=False: the streaming kernel (grouped gate/up + down, activations quantized in-kernel).
+    Default: per matrix, vq_qmv where vq_qmv_path picks an MFMA path, else the grouped streaming launch."""
     from vinf_3080ti_amd import row_bytes
 
     H, F = 5120, 17408
@@ -284,19 +285,31 @@ def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=Non
     g, u, d = (torch.empty(ntok, F, device="cuda"), torch.empty(ntok, F, device="cuda"),
                torch.empty(ntok, H, device="cuda"))
     lib = hip.lib
-    mfma = ntok >= 5 if mfma is None else mfma
     nws = max(lib.vq_qmv_workspace_bytes_for(Q3_K, F, H, ntok), lib.vq_qmv_workspace_bytes_for(Q6_K, H, F, ntok))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
+    # Per matrix: vq_qmv (its own routing, with the workspace) or the grouped streaming launches.
+    if mfma is None:
+        own_gu = lib.vq_qmv_path(Q3_K, F, H, ntok, nws) > 0
+        own_d = lib.vq_qmv_path(Q6_K, H, F, ntok, nws) > 0
+    else:
+        own_gu = own_d = bool(mfma)
+    path = "mfma" if own_gu and own_d else "mixed" if own_gu or own_d else "stream"
+
+    def qmv(ty, w, rows, cols, xi, yo):
+        st = lib.vq_qmv(ty, w.data_ptr(), rows, cols, xi.data_ptr(), ntok, yo.data_ptr(), ws.data_ptr(), nws,
+                        hip.s())
+        assert st == 0, st
 
     def launch(i):
         wg, wu, wd = sets[i % copies]
-        if mfma:
-            for w, rows, cols, xi, yo in ((wg, F, H, x, g), (wu, F, H, x, u), (wd, H, F, h, d)):
-                st = lib.vq_qmv(Q3_K if w is not wd else Q6_K, w.data_ptr(), rows, cols, xi.data_ptr(), ntok,
-                                yo.data_ptr(), ws.data_ptr(), nws, hip.s())
-                assert st == 0, st
+        if own_gu:
+            qmv(Q3_K, wg, F, H, x, g)
+            qmv(Q3_K, wu, F, H, x, u)
         else:
             hip.group_f32(Q3_K, [wg, wu], [F, F], [g, u], H, x, ntok)
+        if own_d:
+            qmv(Q6_K, wd, H, F, h, d)
+        else:
             hip.group_f32(Q6_K, [wd], [H], [d], F, h, ntok)
 
     for i in range(copies):
@@ -306,7 +319,7 @@ def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=Non
     del sets
     torch.cuda.empty_cache()
     return {"us": round(ms * 1e3, 2), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
-            "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "path": "mfma" if mfma else "stream"}
+            "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "path": path}
 
 
 class Sweep:
@@ -356,9 +369,34 @@ class Sweep:
                 if j < len(self.plan):
                     ty, cols = self.plan[j][1], self.plan[j][3]
             i = j
+        # Several tokens: matrices for which vq_qmv takes an MFMA path (e.g. 3..4 tokens over the 17408-wide FFN
+        # down input, which the streaming kernel reads twice) leave their group for a vq_qmv call of their own.
+        lib = hip.lib
+        self.qmv_ws = None
+        if ntok > 1:
+            ops, nws = [], 0
+            for op in self.ops:
+                if op[0] != "group" or op[2]:
+                    ops.append(op)
+                    continue
+                keep, own = [], []
+                for i in op[1]:
+                    _, ty_i, rows_i, cols_i, _ = self.plan[i]
+                    need = lib.vq_qmv_workspace_bytes_for(ty_i, rows_i, cols_i, ntok)
+                    if lib.vq_qmv_path(ty_i, rows_i, cols_i, ntok, need) > 0:
+                        own.append(i)
+                        nws = max(nws, need)
+                    else:
+                        keep.append(i)
+                if keep:
+                    ops.append(("group", keep, False))
+                ops.extend(("qmv", i) for i in own)
+            self.ops = ops
+            if nws:
+                self.qmv_ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
         for _, _, rows, _, _ in self.plan:
             self.ys.setdefault(rows, torch.empty(ntok, rows, device="cuda"))
-        self.launches = sum(1 if op[0] != "head" else 2 for op in self.ops)
+        self.launches = sum(2 if op[0] in ("head", "qmv") else 1 for op in self.ops)  # qmv: matvec + range sums
 
     def step(self):
         """One decode-step sweep: every matrix read once."""
@@ -380,6 +418,13 @@ class Sweep:
                     hip.group(ty, [self.w[i] for i in idx], rows, ys, cols, self.xp, ntok)
                 else:
                     hip.group_f32(ty, [self.w[i] for i in idx], rows, ys, cols, self.x, ntok)
+            elif op[0] == "qmv":
+                _, ty, rows, cols, _ = self.plan[op[1]]
+                ws = self.qmv_ws
+                st = hip.lib.vq_qmv(ty, self.w[op[1]].data_ptr(), rows, cols, self.x.data_ptr(), ntok,
+                                    self.ys[rows].data_ptr(), ws.data_ptr() if ws is not None else None,
+                                    ws.numel() if ws is not None else 0, hip.s())
+                assert st == 0, st
             else:
                 _, ty, rows, cols, _ = self.plan[op[1]]
                 hip.lmhead(ty, self.w[op[1]], rows, cols, self.x, ntok, self.ids, self.head_ws)

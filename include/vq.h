@@ -86,6 +86,17 @@ size_t vq_qmv_workspace_bytes(int cols, int ntok);
  * works and selects the streaming matvec. */
 size_t vq_qmv_workspace_bytes_for(int type, int rows, int cols, int ntok);
 
+/* Paths of vq_qmv (the values vq_qmv_path returns). */
+#define VQ_PATH_STREAM 0   /* streaming matvec (float weights: their own matvec)                */
+#define VQ_PATH_MFMA_I8 1  /* int8-MFMA small-batch matvec                                      */
+#define VQ_PATH_MFMA_F16 2 /* f16-MFMA small-batch matvec (Q3_K, Q4_K, Q5_K, Q6_K)               */
+
+/* The path vq_qmv takes for this matrix and ntok with a 16-byte aligned workspace of workspace_bytes (0: no
+ * workspace), or the negative VQ_ERR_* status of a shape vq_qmv rejects. No counterpart in the reference
+ * (its qmv has one path): for callers that choose between the grouped launches (streaming only) and
+ * per-matrix vq_qmv calls. */
+int vq_qmv_path(int type, int rows, int cols, int ntok, size_t workspace_bytes);
+
 /* Quantize activations to int8 per 32-group: d = amax/127, id = 1/d, q = rint(x*id), xs = d*sum(q).
  * xs may be NULL. Replaces: the activation quantizer of Cpu_qmv (qwen_cpu.c:607-627). */
 int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, float *xs, void *stream);

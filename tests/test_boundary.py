@@ -93,6 +93,29 @@ def test_host_side_argument_checks(lib):
     assert b"workspace" in lib.vq_status_string(_lib.VQ_ERR_WORKSPACE)
 
 
+def test_qmv_path_routing(lib):
+    """vq_qmv_path: which path vq_qmv takes (host-side; no device needed)."""
+    STREAM, I8, F16 = 0, 1, 2
+    ws_for = lib.vq_qmv_workspace_bytes_for
+    q6, q3, q4 = int(T.Q6_K), int(T.Q3_K), int(T.Q4_K)
+    # 5120x17408: the streaming image holds 2 tokens at 17408 columns, so 3..4 tokens take the f16 path
+    for ntok, want in ((1, STREAM), (2, STREAM), (3, F16), (4, F16), (8, F16), (16, F16), (17, STREAM)):
+        assert lib.vq_qmv_path(q6, 5120, 17408, ntok, ws_for(q6, 5120, 17408, ntok)) == want, ntok
+    assert lib.vq_qmv_path(q6, 5120, 17408, 4, 0) == STREAM  # the K-range partials need the workspace
+    # 17408x5120: one streaming pass holds 8 tokens, so the f16 path starts at 5
+    for ntok, want in ((4, STREAM), (5, F16), (8, F16)):
+        assert lib.vq_qmv_path(q3, 17408, 5120, ntok, ws_for(q3, 17408, 5120, ntok)) == want, ntok
+    assert lib.vq_qmv_path(q4, 100, 512, 5, 0) == F16  # one K range: no partials, no workspace
+    iq = int(T.IQ4_XS)
+    assert lib.vq_qmv_path(iq, 5120, 17408, 8, ws_for(iq, 5120, 17408, 8)) == I8
+    assert lib.vq_qmv_path(iq, 5120, 17408, 8, 0) == STREAM
+    assert lib.vq_qmv_path(iq, 5120, 17408, 5, ws_for(iq, 5120, 17408, 5)) == STREAM
+    assert lib.vq_qmv_path(int(T.F32), 64, 64, 8, 1 << 20) == STREAM
+    assert lib.vq_qmv_path(99, 64, 256, 1, 0) == -1
+    assert lib.vq_qmv_path(q4, 64, 256, 0, 0) == -2
+    assert lib.vq_qmv_path(q4, 64, 100, 1, 0) == -2
+
+
 def test_python_error_mapping(lib):
     with pytest.raises(ValueError):
         _lib.check(_lib.VQ_ERR_SHAPE, "qmv")

@@ -449,11 +449,13 @@ def test_qmv_mfma_small_batch_matches_oracle(env, oracle_mod, ty, ntok):
 
 @pytest.mark.parametrize("ty", [T.Q3_K, T.Q4_K, T.Q5_K, T.Q6_K], ids=lambda t: t.name)
 @pytest.mark.parametrize("ntok,rows,cols", [(5, 300, 768), (6, 17, 256), (7, 513, 2048), (8, 256, 1280),
-                                            (16, 40, 768)])
+                                            (16, 40, 768), (3, 40, 17408), (4, 33, 17408)])
 def test_qmv_small16_matches_oracle(env, oracle_mod, ty, ntok, rows, cols):
-    """The f16-MFMA small-batch matvec (5..16 tokens): ragged 256-row blocks, a short last K range, one K range
-    without partials, tokens of very different magnitudes (per-token scales), bit-identical on a rerun."""
+    """The f16-MFMA small-batch matvec (5..16 tokens; 3..4 where the streaming kernel would need two passes):
+    ragged row blocks, a short last K range, one K range without partials, tokens of very different
+    magnitudes (per-token scales), bit-identical on a rerun."""
     torch, lib = env
+    assert lib.vq_qmv_path(int(ty), rows, cols, ntok, lib.vq_qmv_workspace_bytes_for(int(ty), rows, cols, ntok)) == 2
     rng = np.random.default_rng(9000 + 37 * ntok + rows + int(ty))
     w = synth.baseline_rows(ty, rows, cols, rng)
     x = rng.standard_normal((ntok, cols)).astype(np.float32)

@@ -22,6 +22,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_xpack_bytes": (SZ, [I, I]),
     "vq_qmv_workspace_bytes": (SZ, [I, I]),
     "vq_qmv_workspace_bytes_for": (SZ, [I, I, I, I]),
+    "vq_qmv_path": (I, [I, I, I, I, SZ]),
     "vq_quantize_x": (I, [P, I, I, P, P, P, P]),
     "vq_pack_x": (I, [P, I, I, P, P]),
     "vq_qmv_packed": (I, [I, P, I, I, P, I, P, P]),

@@ -385,15 +385,30 @@ size_t vq_qmv_workspace_bytes(int cols, int ntok) {
 // split-K partial sums: from about 6 tokens on it beats the streaming kernel, whose per-token work is VALU
 // (measured on MI355X at 17408x5120 and 5120x17408).
 constexpr int kMfmaMinTok = 6;
-bool mfma_batch(int type, int ntok) { return type != VQ_F32 && type != VQ_F16 && ntok >= kMfmaMinTok && ntok <= 16; }
+static bool mfma_batch(int type, int ntok) { return type != VQ_F32 && type != VQ_F16 && ntok >= kMfmaMinTok && ntok <= 16; }
 
 // 5..16 tokens of Q3_K/Q4_K/Q5_K/Q6_K take the f16-MFMA matvec (vq_small16_impl.h) when the workspace holds its
-// K-range partials (none for cols <= 512); below 5 tokens the streaming kernel is faster (measured on MI355X on
-// the SwiGLU block: 2 tokens 49 vs 91 us, 4 tokens 85 vs 96 us, 8 tokens 171 vs 103 us).
-constexpr int kSmall16MinTok = 5;
-bool small16_batch(int type, int cols, int ntok) {
+// K-range partials (none for cols <= 512); below 5 tokens the streaming kernel is faster where it reads the
+// weights once (measured on MI355X on the SwiGLU block: 2 tokens 49 vs 91 us, 4 tokens 85 vs 96 us, 8 tokens
+// 171 vs 103 us). From 3 tokens on, matrices whose activation image holds fewer tokens than ntok (token_chunk:
+// 2 at 17408 columns), which the streaming kernel would read twice or more, go there too.
+constexpr int kSmall16MinTok = 5, kSmall16MinTokWide = 3;
+static bool small16_batch(int type, int cols, int ntok) {
     return (type == VQ_Q3_K || type == VQ_Q4_K || type == VQ_Q5_K || type == VQ_Q6_K) && cols % 256 == 0 &&
-           ntok >= kSmall16MinTok && ntok <= 16;
+           ntok <= 16 && (ntok >= kSmall16MinTok || (ntok >= kSmall16MinTokWide && ntok > vq::token_chunk(cols)));
+}
+
+// The path vq_qmv takes (VQ_PATH_*), given whether a usable (non-NULL, 16-byte aligned) workspace of wsb
+// bytes comes with the call.
+static int qmv_route(int type, int rows, int cols, int ntok, bool ws, size_t wsb) {
+    if (type == VQ_F32 || type == VQ_F16) return VQ_PATH_STREAM;
+    if (small16_batch(type, cols, ntok)) {
+        const size_t np = vq::s16_part_bytes(rows, cols, ntok);
+        if (np == 0 || (ws && wsb >= np)) return VQ_PATH_MFMA_F16;
+    }
+    if (mfma_batch(type, ntok) && ws && wsb >= vq_qmv_workspace_bytes_for(type, rows, cols, ntok))
+        return VQ_PATH_MFMA_I8;
+    return VQ_PATH_STREAM;
 }
 
 size_t vq_qmv_workspace_bytes_for(int type, int rows, int cols, int ntok) {
@@ -401,6 +416,13 @@ size_t vq_qmv_workspace_bytes_for(int type, int rows, int cols, int ntok) {
     if (small16_batch(type, cols, ntok)) return vq::s16_part_bytes(rows, cols, ntok);
     if (mfma_batch(type, ntok)) return align256(vq_xpack_bytes(cols, ntok)) + vq::mfma_part_bytes(rows, cols, ntok);
     return (type == VQ_F32 || type == VQ_F16) ? 0 : vq_qmv_workspace_bytes(cols, ntok);
+}
+
+int vq_qmv_path(int type, int rows, int cols, int ntok, size_t workspace_bytes) {
+    const int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    return qmv_route(type, rows, cols, ntok, workspace_bytes > 0, workspace_bytes);
 }
 
 int vq_quantize_x(const float *x, int ntok, int cols, int8_t *xq, float *xd, float *xs, void *stream) {
@@ -447,17 +469,15 @@ int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int n
     if (type == VQ_F32) return launch_float<VQ_F32>(w, rows, cols, x, ntok, y, s);
     if (type == VQ_F16) return launch_float<VQ_F16>(w, rows, cols, x, ntok, y, s);
     const long rb = row_bytes_of(type, cols);
-    if (small16_batch(type, cols, ntok)) {
-        const size_t np = vq::s16_part_bytes(rows, cols, ntok);
-        if (np == 0 || (workspace && !misaligned16(workspace) && workspace_bytes >= np)) {
-            float *part = np ? static_cast<float *>(workspace) : nullptr;
-            return dispatch_quant(type, [&](auto tc) {
-                return vq::launch_small16<decltype(tc)::value>(w, rows, cols, rb, x, ntok, y, part, s);
-            });
-        }
+    const bool ws = workspace && !misaligned16(workspace);
+    const int path = qmv_route(type, rows, cols, ntok, ws, workspace_bytes);
+    if (path == VQ_PATH_MFMA_F16) {
+        float *part = vq::s16_part_bytes(rows, cols, ntok) ? static_cast<float *>(workspace) : nullptr;
+        return dispatch_quant(type, [&](auto tc) {
+            return vq::launch_small16<decltype(tc)::value>(w, rows, cols, rb, x, ntok, y, part, s);
+        });
     }
-    if (mfma_batch(type, ntok) && workspace && !misaligned16(workspace) &&
-        workspace_bytes >= vq_qmv_workspace_bytes_for(type, rows, cols, ntok)) {
+    if (path == VQ_PATH_MFMA_I8) {
         const size_t xpb = align256(vq_xpack_bytes(cols, ntok));
         st = vq_pack_x(x, ntok, cols, workspace, stream);
         if (st) return st;

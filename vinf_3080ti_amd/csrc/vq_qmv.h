@@ -6,6 +6,23 @@
 
 namespace vq {
 
+// Activation image geometry of the streaming kernel (compile-time; overridable for tuning builds).
+#ifndef VQ_X_LDS_MAX
+#define VQ_X_LDS_MAX (64 * 1024)  // bytes of activation records one launch keeps in LDS
+#endif
+#ifndef VQ_XPAD
+#define VQ_XPAD 32  // bytes of padding after each 256 codes of the image
+#endif
+// Bytes of one token's activation image (codes padded per 256, then 8 bytes of scales per 32-group).
+__host__ __device__ inline int x_image_bytes(int cols) {
+    return (((cols / 32 + 7) / 8) * (256 + VQ_XPAD) + (cols / 32) * 8 + 15) / 16 * 16;
+}
+// Tokens per streaming launch (one weight pass): as many (<= 8) as the activation image budget holds.
+inline int token_chunk(int cols) {
+    const int chunk = VQ_X_LDS_MAX / x_image_bytes(cols);
+    return chunk > 8 ? 8 : chunk < 1 ? 1 : chunk;
+}
+
 template <int T>
 int launch_quant(const uint8_t *w, int rows, int cols, long row_bytes, const void *x, bool x_f32, int ntok, float *y,
                  hipStream_t s);

@@ -18,9 +18,6 @@ extern "C" void *vq_debug_timing_buffer();
 namespace vq {
 
 // Streaming geometry (compile-time; overridable for tuning builds).
-#ifndef VQ_X_LDS_MAX
-#define VQ_X_LDS_MAX (64 * 1024)  // bytes of activation records one launch keeps in LDS
-#endif
 
 
 // Sum over the 64 lanes with DPP moves (no LDS round trips): pairs, quads, half rows, rows, then rows 1/3
@@ -57,14 +54,11 @@ struct StageShape {
 // of padding (so that the codes lanes of neighbouring units read fall in different LDS banks), then the
 // group scales xd and the half sums xh as in the packed record. Built by DMA from a packed record, or by
 // quantizing fp32 activations in the kernel.
-#ifndef VQ_XPAD
-#define VQ_XPAD 32
-#endif
 struct XImage {
     int ng, nblk, xq_bytes, bytes;  // bytes: one token's image (16-byte multiple)
     __host__ __device__ explicit XImage(int cols)
         : ng(cols / 32), nblk((cols / 32 + 7) / 8), xq_bytes(((cols / 32 + 7) / 8) * (256 + VQ_XPAD)),
-          bytes((((cols / 32 + 7) / 8) * (256 + VQ_XPAD) + (cols / 32) * 8 + 15) / 16 * 16) {}
+          bytes(x_image_bytes(cols)) {}
     __device__ int code_off(int G, int h) const { return (G >> 3) * (256 + VQ_XPAD) + (G & 7) * 32 + 16 * h; }
     // Byte of the packed record (vq_xpack_h_offset layout) that LDS image byte o (16-byte aligned) holds,
     // or -1 for padding.
@@ -871,11 +865,6 @@ int launch_stream(const QJobs &jobs, const int *types, int cols, const void *xp,
     return hip_status(hipGetLastError());
 }
 
-// Tokens per launch: as many (<= 8) as the activation image budget holds.
-inline int token_chunk(int cols) {
-    const int chunk = VQ_X_LDS_MAX / XImage(cols).bytes;
-    return chunk > 8 ? 8 : chunk < 1 ? 1 : chunk;
-}
 
 // Workgroups of a single-job launch (the argmax key count per token).
 template <int T>
