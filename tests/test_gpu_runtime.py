@@ -198,3 +198,36 @@ def test_gemm_min_rows_routes_prompts_to_the_mfma_contraction(rt, oracle_mod):
     with pytest.raises(ValueError):
         rt.set_gemm_min_rows(-1)
     rt.free("pf")
+
+
+def test_upload_gguf_tensor_from_a_file(rt, oracle_mod, tmp_path):
+    """upload_gguf_tensor (cuda/qwen_runtime.py:68-86): raw blocks straight from the file's mapping, cols =
+    innermost dimension, rows = product of the others, the byte size returned; types without a matvec
+    raise UnsupportedModelError."""
+    from gguf_writer import write_gguf
+    from vinf_3080ti_amd.gguf import GGUFValueType, UnsupportedModelError, load_gguf
+
+    rows, cols = 6, 768
+    raw = synth.synthetic_rows(T.Q5_K, rows, cols, 77)
+    f32 = np.random.default_rng(78).uniform(-1, 1, (2, 3, 64)).astype(np.float32)
+    p = tmp_path / "m.gguf"
+    write_gguf(p, [("general.architecture", GGUFValueType.STRING, "qwen35")],
+               [("blk.0.attn_q.weight", (cols, rows), T.Q5_K, raw.tobytes()),
+                ("stacked", (64, 3, 2), T.F32, f32.tobytes()), ("legacy", (32, 2), T.Q4_0, bytes(36))],
+               alignment=64)
+    g = load_gguf(p)
+    assert rt.upload_gguf_tensor(g, "blk.0.attn_q.weight") == raw.nbytes
+    x = np.random.default_rng(79).uniform(-1, 1, cols).astype(np.float32)
+    got = np.array(rt.matvec("blk.0.attn_q.weight", x.tolist()), np.float32)
+    assert rel_l2(got, oracle_mod.qmv(int(T.Q5_K), raw, rows, cols, x, 1)[0]) <= 1e-5
+    assert rt.upload_gguf_tensor(g, "stacked", device_name="s") == f32.nbytes
+    assert rt.tensor_info("s")[2:4] == (6, 64)  # rows = 3 * 2, cols = 64
+    xs = np.random.default_rng(80).uniform(-1, 1, 64).astype(np.float32)
+    got = np.array(rt.matvec("s", xs.tolist()), np.float32)
+    assert rel_l2(got, f32.reshape(6, 64).astype(np.float64) @ xs) <= 1e-6
+    with pytest.raises(UnsupportedModelError):
+        rt.upload_gguf_tensor(g, "legacy")
+    with pytest.raises(ValueError):
+        rt.upload_gguf_tensor(g, "blk.0.attn_q.weight", group=0)
+    rt.free("blk.0.attn_q.weight")
+    rt.free("s")

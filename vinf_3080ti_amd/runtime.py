@@ -129,12 +129,14 @@ class Runtime:
         Every tensor is resident in HBM: `resident=False` (pinned-host streaming on the 12 GB card) is
         accepted and ignored. Weight groups (CUDA VMM regions) do not exist here: group >= 0 is rejected.
         """
-        view = memoryview(data).cast("B")
-        row_bytes, nbytes = _check_upload_args(name, view.nbytes, int(type_id), int(cols), int(rows))
         if group >= 0:
             raise ValueError(f"unknown weight group {group}")
+        # The views are released on every exit: a caller's mapping (upload_gguf_tensor) can then be closed
+        # even when this raises.
+        with memoryview(data) as src, src.cast("B") as view:
+            row_bytes, nbytes = _check_upload_args(name, view.nbytes, int(type_id), int(cols), int(rows))
+            host = torch.frombuffer(bytearray(view), dtype=torch.uint8)
         self.tensors.pop(name, None)
-        host = torch.frombuffer(bytearray(view), dtype=torch.uint8)
         padded = (nbytes + 16 + _PAD - 1) // _PAD * _PAD
         dev = torch.zeros(padded, dtype=torch.uint8, device=self.device)
         dev[:nbytes].copy_(host)
@@ -389,6 +391,29 @@ class HipWeightRuntime:
 
     def free(self, name: str) -> None:
         self._rt.free(name)
+
+    def upload_gguf_tensor(self, gguf, name: str, *, device_name: str | None = None, resident: bool = True,
+                           group: int = -1) -> int:
+        """Upload one tensor's raw blocks straight from the file's mapping (cuda/qwen_runtime.py:68-86): cols is
+        the innermost GGUF dimension, rows the product of the others; returns the tensor's byte size. Types
+        without a HIP matvec raise UnsupportedModelError. `gguf` is a GGUFFile (vinf_3080ti_amd.gguf)."""
+        from .gguf import UnsupportedModelError
+
+        info = gguf.tensors[name]
+        if int(info.tensor_type) not in HIP_MATVEC_TYPES:
+            raise UnsupportedModelError(f"{name}: no HIP matvec for {info.tensor_type.name}")
+        cols = info.dimensions[0]
+        rows = 1
+        for d in info.dimensions[1:]:
+            rows *= d
+        f, mm, view = gguf.mmap_tensor(name)
+        try:
+            self._rt.upload(device_name or name, view, int(info.tensor_type), cols, rows, resident, group)
+        finally:
+            view.release()
+            mm.close()
+            f.close()
+        return info.nbytes
 
     def upload_raw(self, name: str, data, tensor_type: GGUFTensorType, cols: int, rows: int, *, resident: bool = True) -> None:
         if int(tensor_type) not in HIP_MATVEC_TYPES:
