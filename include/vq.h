@@ -113,6 +113,19 @@ int vq_pack_x(const float *x, int ntok, int cols, void *xpack, void *stream);
 int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, float *y, void *workspace,
            size_t workspace_bytes, void *stream);
 
+/* Activation staging flags of vq_qmv_staged: the bits of the reference megakernel's QMV flags
+ * (runtime/instructions.py:179-182; QMV_FLAG_ARGMAX = 4 is vq_lmhead_argmax here). */
+#define VQ_QMV_ADD 1      /* y[t][r] += (W v)[r] instead of =                                      */
+#define VQ_QMV_NORM 2     /* v = rmsnorm(v) * norm_w: v * norm_w[i] / sqrt(mean(v^2) + eps), per token */
+#define VQ_QMV_SILU_MUL 8 /* v = silu(x) * x2 (applied before NORM), silu(z) = z / (1 + exp(-z))  */
+
+/* y = W v with v staged from fp32 activations inside the matvec (flags VQ_QMV_*, 0 = plain x): x, x2
+ * [ntok][cols], norm_w [cols], all 16-byte aligned; quantized types, cols <= 24576, no workspace.
+ * Replaces: the megakernel's op_qmv staging (qwen_megakernel.cu:468-551), which removes the separate
+ * silu_mul / rmsnorm / add passes around a projection. */
+int vq_qmv_staged(int type, const uint8_t *w, int rows, int cols, const float *x, const float *x2,
+                  const float *norm_w, float eps, int flags, int ntok, float *y, void *stream);
+
 /* Same as vq_qmv with activations already packed by vq_pack_x (quantized types only), so several
  * matrices that share one input (gate/up, q/k/v) quantize it once. Replaces: dot_row_q's caller loop
  * (qwen_cpu.c:628-637). */

@@ -7,6 +7,7 @@ Functions mirror the reference CPU path (/root/reference/engine/csrc/cpu/qwen_cp
   int_partials   exact int32 sum of code*xq per (token, row, group, 16-half)
   decode_codes   integer codes + per-16 scales/mins with dequant == scale*code - min
   argmax_rows    argmax_kernel (qwen_runtime.cu:850-876), ties to the lowest index
+  stage_x        the megakernel's QMV activation staging (qwen_megakernel.cu:485-551), float64 numpy
 """
 from __future__ import annotations
 
@@ -125,3 +126,20 @@ def argmax_rows(x: np.ndarray, n: int, ntok: int) -> list[int]:
     out = np.empty(ntok, np.int32)
     lib().vqo_argmax_rows(_p(x), n, ntok, _p(out))
     return [int(v) for v in out]
+
+
+# Activation staging flags (runtime/instructions.py:179-182).
+STAGE_ADD, STAGE_NORM, STAGE_SILU_MUL = 1, 2, 8
+
+
+def stage_x(x: np.ndarray, x2: np.ndarray | None, norm_w: np.ndarray | None, eps: float, flags: int) -> np.ndarray:
+    """float64 restatement of op_qmv's staging (qwen_megakernel.cu:485-551): v = silu(x) * x2 with SILU_MUL
+    (silu(z) = z / (1 + exp(-z)), silu_f), then with NORM v * norm_w / sqrt(mean(v^2) + eps) per token (the
+    megakernel's rsqrtf(block_sum(v^2) / cols + eps), :500)."""
+    v = np.asarray(x, np.float64).copy()
+    if flags & STAGE_SILU_MUL:
+        v = v / (1.0 + np.exp(-v)) * np.asarray(x2, np.float64)
+    if flags & STAGE_NORM:
+        ms = (v * v).mean(axis=-1, keepdims=True)
+        v = v / np.sqrt(ms + eps) * np.asarray(norm_w, np.float64)
+    return v

@@ -481,3 +481,64 @@ def test_qmv_mfma_baseline_shapes(env, oracle_mod, ty, rows, cols):
         got = gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok, fast=True)
         ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok, threads=16)
         assert rel_l2(got, ref) <= REL_L2_TOL, (ty.name, ntok)
+
+
+STAGE_FLAG_SETS = [8, 2, 10, 1, 3, 11]  # SILU_MUL, NORM, SILU_MUL|NORM, ADD, NORM|ADD, all three
+
+
+@pytest.mark.parametrize("ty", [T.Q4_K, T.Q3_K, T.Q6_K, T.IQ4_XS, T.Q8_0], ids=lambda t: t.name)
+@pytest.mark.parametrize("flags", STAGE_FLAG_SETS)
+@pytest.mark.parametrize("ntok,rows,cols", [(1, 40, 768), (3, 33, 5120), (9, 20, 512)])
+def test_qmv_staged_matches_float_reference_within_int8_bound(env, oracle_mod, ty, flags, ntok, rows, cols):
+    """vq_qmv_staged (the megakernel's fused SILU_MUL / NORM staging and ADD, qwen_megakernel.cu:468-551) vs
+    the float64 dequant matvec of the float64-staged activations, within the reference's int8-path bound
+    1.05 * sum_g sum|w| * amax_g(v) / 254 + 1e-4 (1 + |ref|) (test_phase31b_megakernel.py:184-199); ntok 9
+    spans two launches (per-chunk x2 offset); bit-identical on a rerun."""
+    torch, lib = env
+    rng = np.random.default_rng(4400 + 10 * flags + ntok + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = (rng.standard_normal((ntok, cols)) * 2.0).astype(np.float32)
+    x2 = rng.standard_normal((ntok, cols)).astype(np.float32)
+    nw = rng.uniform(0.2, 1.5, cols).astype(np.float32)
+    y0 = rng.standard_normal((ntok, rows)).astype(np.float32)
+    eps = 1e-6
+    wd, xd, x2d, nwd = wdev(torch, w), dev(torch, x), dev(torch, x2), dev(torch, nw)
+
+    def run():
+        y = dev(torch, y0.copy())
+        st = lib.vq_qmv_staged(int(ty), P(wd), rows, cols, P(xd), P(x2d), P(nwd), eps, flags, ntok, P(y), None)
+        assert st == 0, lib.vq_status_string(st)
+        torch.cuda.synchronize()
+        return y.cpu().numpy()
+
+    got = run()
+    v = oracle_mod.stage_x(x, x2, nw, eps, flags)
+    wf = oracle_mod.dequant_rows(int(ty), w, rows, cols).astype(np.float64)
+    for t in range(ntok):
+        ref = wf @ v[t] + (y0[t].astype(np.float64) if flags & 1 else 0.0)
+        amax = np.abs(v[t].reshape(-1, 32)).max(1)
+        bound = (np.abs(wf).reshape(rows, -1, 32).sum(2) * amax / 254.0).sum(1)
+        assert np.all(np.abs(got[t] - ref) <= 1.05 * bound + 1e-4 * (1 + np.abs(ref))), (ty.name, flags, t)
+    assert np.array_equal(run(), got)
+
+
+def test_qmv_staged_without_flags_equals_vq_qmv_and_rejects_bad_arguments(env):
+    torch, lib = env
+    rng = np.random.default_rng(4501)
+    rows, cols, ntok = 70, 1024, 2
+    w = synth.baseline_rows(T.Q5_K, rows, cols, rng)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    wd, xd = wdev(torch, w), dev(torch, x)
+    y = torch.empty(ntok, rows, dtype=torch.float32, device="cuda")
+    assert lib.vq_qmv_staged(int(T.Q5_K), P(wd), rows, cols, P(xd), None, None, 0.0, 0, ntok, P(y), None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), gpu_qmv(torch, lib, T.Q5_K, w, rows, cols, x, ntok))
+    bad = lambda **k: lib.vq_qmv_staged(k.get("ty", int(T.Q5_K)), P(wd), rows, k.get("cols", cols), P(xd),  # noqa: E731
+                                         k.get("x2"), k.get("nw"), k.get("eps", 1e-6), k.get("flags", 0), ntok,
+                                         P(y), None)
+    assert bad(flags=4) == -4  # ARGMAX is vq_lmhead_argmax's job
+    assert bad(flags=8) == -4  # SILU_MUL without x2
+    assert bad(flags=2) == -4  # NORM without weights
+    assert bad(flags=2, nw=P(xd), eps=-1.0) == -4
+    assert bad(ty=int(T.F32)) == -1
+    assert bad(cols=32768) == -2

@@ -231,3 +231,41 @@ def test_upload_gguf_tensor_from_a_file(rt, oracle_mod, tmp_path):
         rt.upload_gguf_tensor(g, "blk.0.attn_q.weight", group=0)
     rt.free("blk.0.attn_q.weight")
     rt.free("s")
+
+
+def test_qmv_staged_fuses_silu_mul_norm_and_add(rt, oracle_mod):
+    """Runtime.qmv_staged: v = rmsnorm(silu(x) * x2) * norm, y += W v (the megakernel's QMV flags,
+    qwen_megakernel.cu:468-551), against the float64 staged reference within the int8-path bound; the norm
+    weights as an uploaded F32 tensor and as a buffer give the same result."""
+    rows, cols, ntok = 24, 1024, 2
+    rng = np.random.default_rng(91)
+    raw = synth.synthetic_rows(T.Q4_K, rows, cols, 91)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    x2 = rng.standard_normal((ntok, cols)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    y0 = rng.standard_normal((ntok, rows)).astype(np.float32)
+    rt.upload_raw("sw", raw.tobytes(), T.Q4_K, cols, rows)
+    rt.upload_raw("sw.norm", nw.tobytes(), T.F32, cols, 1)
+    for name, n in (("sx", x), ("sx2", x2), ("snw", nw)):
+        rt.alloc(name, n.size)
+        rt.write_floats(name, n.reshape(-1).tolist())
+    outs = []
+    for norm in ("sw.norm", "snw"):
+        rt.alloc("sy", rows * ntok)
+        rt.write_floats("sy", y0.reshape(-1).tolist())
+        rt.qmv_staged("sw", "sx", "sy", ntok, x2="sx2", norm=norm, eps=1e-6, add=True)
+        outs.append(np.array(rt.read_floats("sy"), np.float64).reshape(ntok, rows))
+    assert np.array_equal(outs[0], outs[1])
+    v = oracle_mod.stage_x(x, x2, nw, 1e-6, oracle_mod.STAGE_SILU_MUL | oracle_mod.STAGE_NORM)
+    wf = oracle_mod.dequant_rows(int(T.Q4_K), raw, rows, cols).astype(np.float64)
+    for t in range(ntok):
+        ref = wf @ v[t] + y0[t]
+        amax = np.abs(v[t].reshape(-1, 32)).max(1)
+        bound = (np.abs(wf).reshape(rows, -1, 32).sum(2) * amax / 254.0).sum(1)
+        assert np.all(np.abs(outs[0][t] - ref) <= 1.05 * bound + 1e-4 * (1 + np.abs(ref)))
+    with pytest.raises(ValueError):
+        rt.qmv_staged("sw.norm", "sx", "sy", 1)  # float weights have no staged path
+    with pytest.raises(ValueError):
+        rt.qmv_staged("sw", "sx", "sy", 1, norm="sw")  # norm must be F32 cols values
+    for name in ("sw", "sw.norm"):
+        rt.free(name)

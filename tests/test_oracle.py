@@ -232,3 +232,39 @@ def test_quantizer_closed_form(oracle_mod):
 def test_argmax_semantics(oracle_mod):
     x = np.array([[1, 5, 5, 2], [np.nan, 3, np.nan, 3], [-np.inf] * 4], np.float32)
     assert oracle_mod.argmax_rows(x, 4, 3) == [1, 1, 2**31 - 1]
+
+
+def test_stage_x_is_pinned_by_closed_forms(oracle_mod):
+    """stage_x (the megakernel's activation staging): identities that a dropped term, a wrong sign or a
+    misplaced eps would break."""
+    from scipy.special import expit
+
+    st = oracle_mod.stage_x
+    rng = np.random.default_rng(61)
+    x = rng.standard_normal((3, 256)) * 4.0
+    x2 = rng.standard_normal((3, 256))
+    nw = rng.uniform(0.5, 2.0, 256)
+    assert np.array_equal(st(x, None, None, 0.0, 0), x)
+    # silu(z) = z * sigmoid(z) (textbook logistic), silu(-z) = silu(z) - z, silu(0) = 0
+    s = st(x, np.ones_like(x), None, 0.0, oracle_mod.STAGE_SILU_MUL)
+    assert np.allclose(s, x * expit(x), rtol=1e-14, atol=1e-300)
+    assert np.allclose(st(-x, np.ones_like(x), None, 0.0, oracle_mod.STAGE_SILU_MUL), s - x, rtol=1e-12, atol=1e-12)
+    assert st(np.zeros((1, 32)), np.ones((1, 32)), None, 0.0, oracle_mod.STAGE_SILU_MUL).any() == False  # noqa: E712
+    # the second input multiplies elementwise
+    assert np.allclose(st(x, x2, None, 0.0, oracle_mod.STAGE_SILU_MUL), s * x2, rtol=1e-14, atol=1e-300)
+    # NORM with unit weights and eps = 0: unit RMS per token, scale invariance, sign kept
+    n = st(x, None, np.ones(256), 0.0, oracle_mod.STAGE_NORM)
+    assert np.allclose(np.sqrt((n * n).mean(axis=1)), 1.0, rtol=1e-14)
+    assert np.allclose(st(7.5 * x, None, np.ones(256), 0.0, oracle_mod.STAGE_NORM), n, rtol=1e-13)
+    assert np.array_equal(np.sign(n), np.sign(x))
+    # weights multiply after the normalisation; eps adds to the mean square: a constant row c gives
+    # c / sqrt(c^2 + eps)
+    assert np.allclose(st(x, None, nw, 0.0, oracle_mod.STAGE_NORM), n * nw, rtol=1e-13)
+    c = st(np.full((1, 64), 3.0), None, np.ones(64), 7.0, oracle_mod.STAGE_NORM)
+    assert np.allclose(c, 3.0 / 4.0, rtol=1e-15)
+    # SILU_MUL is applied before NORM
+    both = st(x, x2, nw, 1e-6, oracle_mod.STAGE_SILU_MUL | oracle_mod.STAGE_NORM)
+    assert np.allclose(both, st(st(x, x2, None, 0.0, oracle_mod.STAGE_SILU_MUL), None, nw, 1e-6,
+                                oracle_mod.STAGE_NORM), rtol=1e-14)
+    # ADD does not change the staged activations
+    assert np.array_equal(st(x, None, None, 0.0, oracle_mod.STAGE_ADD), x)

@@ -10,7 +10,10 @@ from pathlib import Path
 
 from .build import LIB
 
-P, I, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+P, I, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_float
+
+# Activation staging flags of vq_qmv_staged (include/vq.h).
+VQ_QMV_ADD, VQ_QMV_NORM, VQ_QMV_SILU_MUL = 1, 2, 8
 
 # name -> (restype, argtypes); every symbol include/vq.h declares.
 SIGNATURES: dict[str, tuple[object, list]] = {
@@ -23,6 +26,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_qmv_workspace_bytes": (SZ, [I, I]),
     "vq_qmv_workspace_bytes_for": (SZ, [I, I, I, I]),
     "vq_qmv_path": (I, [I, I, I, I, SZ]),
+    "vq_qmv_staged": (I, [I, P, I, I, P, P, P, F, I, I, P, P]),
     "vq_quantize_x": (I, [P, I, I, P, P, P, P]),
     "vq_pack_x": (I, [P, I, I, P, P]),
     "vq_qmv_packed": (I, [I, P, I, I, P, I, P, P]),

@@ -446,6 +446,28 @@ int vq_pack_x(const float *x, int ntok, int cols, void *xpack, void *stream) {
     return hip_status(hipGetLastError());
 }
 
+static_assert(VQ_QMV_ADD == VQ_STAGE_ADD && VQ_QMV_NORM == VQ_STAGE_NORM && VQ_QMV_SILU_MUL == VQ_STAGE_SILU_MUL,
+              "public and kernel staging flags agree");
+
+int vq_qmv_staged(int type, const uint8_t *w, int rows, int cols, const float *x, const float *x2,
+                  const float *norm_w, float eps, int flags, int ntok, float *y, void *stream) {
+    const int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;  // staging feeds the int8 activation path
+    if (ntok < 1 || cols > kFusedQuantMaxCols) return VQ_ERR_SHAPE;
+    if (flags & ~(VQ_QMV_ADD | VQ_QMV_NORM | VQ_QMV_SILU_MUL)) return VQ_ERR_ARG;
+    if (!w || !x || !y || misaligned16(w) || misaligned16(x)) return VQ_ERR_ARG;
+    if ((flags & VQ_QMV_SILU_MUL) && (!x2 || misaligned16(x2))) return VQ_ERR_ARG;
+    if ((flags & VQ_QMV_NORM) && (!norm_w || misaligned16(norm_w) || !(eps >= 0.0f))) return VQ_ERR_ARG;
+    const vq::XStage xs{(flags & VQ_QMV_SILU_MUL) ? x2 : nullptr, (flags & VQ_QMV_NORM) ? norm_w : nullptr, eps,
+                        flags};
+    const long rb = row_bytes_of(type, cols);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return dispatch_quant(type, [&](auto tc) {
+        return vq::launch_quant_staged<decltype(tc)::value>(w, rows, cols, rb, x, xs, ntok, y, s);
+    });
+}
+
 int vq_qmv_packed(int type, const uint8_t *w, int rows, int cols, const void *xpack, int ntok, float *y, void *stream) {
     int st = check_matrix(type, rows, cols);
     if (st) return st;

@@ -17,6 +17,19 @@ namespace vq {
 __host__ __device__ inline int x_image_bytes(int cols) {
     return (((cols / 32 + 7) / 8) * (256 + VQ_XPAD) + (cols / 32) * 8 + 15) / 16 * 16;
 }
+// Activation staging of the fp32-input streaming matvec (the bits of the reference megakernel's QMV flags,
+// runtime/instructions.py:179-182): ADD accumulates into y, NORM stages rmsnorm(v) * nw, SILU_MUL stages
+// silu(x) * x2.
+#define VQ_STAGE_ADD 1
+#define VQ_STAGE_NORM 2
+#define VQ_STAGE_SILU_MUL 8
+struct XStage {
+    const float *x2;  // [ntok][cols] second input of SILU_MUL
+    const float *nw;  // [cols] RMS norm weights of NORM
+    float eps;
+    int flags;
+};
+
 // Tokens per streaming launch (one weight pass): as many (<= 8) as the activation image budget holds.
 inline int token_chunk(int cols) {
     const int chunk = VQ_X_LDS_MAX / x_image_bytes(cols);
@@ -33,6 +46,10 @@ int launch_quant_jobs(int n, const uint8_t *const *w, const int *rows, float *co
                       bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s);
 template <int T>
 long argmax_waves(int rows, int cols, int ntok);
+// y = W v for fp32 activations staged per `xs` (flags VQ_STAGE_*; x2 and nw already offset to token 0).
+template <int T>
+int launch_quant_staged(const uint8_t *w, int rows, int cols, long row_bytes, const float *x, const XStage &xs,
+                        int ntok, float *y, hipStream_t s);
 // y_j = W_j x for n <= 4 matrices sharing cols and fp32 x, of type T or Q8_0 (types[j]), in one launch.
 constexpr int kMixedMaxTokens = 4;  // tokens per launch of a mixed-type group (more go in several launches)
 template <int T>

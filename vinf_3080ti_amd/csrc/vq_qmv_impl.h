@@ -168,8 +168,9 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, long r) {
 // LDS: [grid table | activation image of the NT tokens | stage buffer per wave | row-part slots]. At start-up
 // the waves load the table and the activations (DMA of the packed record, or quantization of fp32 values),
 // then request their first stage, and meet at one barrier.
-template <int T, int NT, bool XF32, int NW>
-__device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const int cols, const void *__restrict__ xin) {
+template <int T, int NT, bool XF32, int NW, bool STG = false>
+__device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const int cols, const void *__restrict__ xin,
+                                          const XStage &xst) {
     using S = Sl<T>;
     using G = Stream<T>;
     constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, NL = G::NL;
@@ -195,6 +196,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     float *const slots = reinterpret_cast<float *>(s_dyn + xreg + NW * G::STAGE_LDS);
     const int rs = rows_per_stage(SU, nu);
     const bool per_lane = lane_slots(jobs.j[jb].rwg, nu, SU, NT);
+    const bool add = STG && (xst.flags & VQ_STAGE_ADD) != 0 && jobs.j[jb].y != nullptr;
 
     // This workgroup's rows and stages (all 32-bit unit indices: a matrix has < 2^31 units).
     const int b = blockIdx.x;
@@ -241,6 +243,84 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     }
     if constexpr (XF32) {
         const float *xf = static_cast<const float *>(xin);
+        const bool silu = (xst.flags & VQ_STAGE_SILU_MUL) != 0, norm = (xst.flags & VQ_STAGE_NORM) != 0;
+        // Staged activation element i of token t: silu(x) * x2 with SILU_MUL, times rms * nw[i] with NORM
+        // (qwen_megakernel.cu:485-551). The RMS sums of squares use the stage buffers, free until the first
+        // stage lands: partial[t][k] over groups g = k mod 256 in order, then a fixed pairwise tree.
+        float *const nsum = reinterpret_cast<float *>(s_dyn + xreg);
+        auto staged = [&](int t, int g, float (&v)[32]) {
+            const float4 *src = reinterpret_cast<const float4 *>(xf + static_cast<size_t>(t) * cols + 32 * g);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float4 f = src[k];
+                v[4 * k] = f.x;
+                v[4 * k + 1] = f.y;
+                v[4 * k + 2] = f.z;
+                v[4 * k + 3] = f.w;
+            }
+            if (silu) {
+                const float4 *s2 = reinterpret_cast<const float4 *>(xst.x2 + static_cast<size_t>(t) * cols + 32 * g);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float4 f = s2[k];
+                    const float m[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float z = v[4 * k + q];
+                        v[4 * k + q] = z / (1.0f + expf(-z)) * m[q];
+                    }
+                }
+            }
+        };
+        bool do_stage = false;  // STG instances only: the plain kernels compile exactly as without staging
+        if constexpr (STG) do_stage = (xst.flags & (VQ_STAGE_SILU_MUL | VQ_STAGE_NORM)) != 0;
+        if (do_stage) {
+            if (norm) {
+                for (int i = threadIdx.x; i < NT * 256; i += blockDim.x) {
+                    const int t = i >> 8, k = i & 255;
+                    float acc = 0.0f;
+                    for (int g = k; g < xi.ng; g += 256) {
+                        float v[32];
+                        staged(t, g, v);
+#pragma unroll
+                        for (int e = 0; e < 32; ++e) acc = fmaf(v[e], v[e], acc);
+                    }
+                    nsum[i] = acc;
+                }
+                for (int h = 128; h > 0; h >>= 1) {
+                    __syncthreads();
+                    for (int i = threadIdx.x; i < NT * h; i += blockDim.x) {
+                        const int t = i / h, k = i - t * h;
+                        nsum[t * 256 + k] += nsum[t * 256 + k + h];
+                    }
+                }
+                __syncthreads();
+            }
+            for (int i = threadIdx.x; i < NT * xi.ng; i += blockDim.x) {
+                const int t = i / xi.ng, g = i - t * xi.ng;
+                float v[32];
+                staged(t, g, v);
+                if (norm) {
+                    const float rs = 1.0f / sqrtf(nsum[t * 256] / static_cast<float>(cols) + xst.eps);
+                    const float4 *nw = reinterpret_cast<const float4 *>(xst.nw + 32 * g);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const float4 f = nw[k];
+                        v[4 * k] *= rs * f.x;
+                        v[4 * k + 1] *= rs * f.y;
+                        v[4 * k + 2] *= rs * f.z;
+                        v[4 * k + 3] *= rs * f.w;
+                    }
+                }
+                const QGroup qg = quantize_group(v);
+                uint8_t *img = s_dyn + t * xi.bytes;
+                *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 0)) = u32x4{qg.q[0], qg.q[1], qg.q[2], qg.q[3]};
+                *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 1)) = u32x4{qg.q[4], qg.q[5], qg.q[6], qg.q[7]};
+                reinterpret_cast<float *>(img + xi.xq_bytes)[g] = qg.d;
+                reinterpret_cast<uint32_t *>(img + xi.xq_bytes + 4 * xi.ng)[g] = qg.half_sums();
+            }
+            __syncthreads();  // the RMS sums' LDS is a stage buffer again from here
+        } else {
         for (int i = threadIdx.x; i < NT * xi.ng; i += blockDim.x) {
             const int t = i / xi.ng, g = i - t * xi.ng;
             const float4 *src = reinterpret_cast<const float4 *>(xf + static_cast<size_t>(t) * cols + 32 * g);
@@ -259,6 +339,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 1)) = u32x4{qg.q[4], qg.q[5], qg.q[6], qg.q[7]};
             reinterpret_cast<float *>(img + xi.xq_bytes)[g] = qg.d;
             reinterpret_cast<uint32_t *>(img + xi.xq_bytes + 4 * xi.ng)[g] = qg.half_sums();
+        }
         }
     } else {
         for (int p = wv; p < xreg / 1024; p += NW) {
@@ -514,6 +595,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             if (ok && k == 0) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
+                    if (add) tot[t] += y[static_cast<size_t>(t) * rows + r];
                     if (y != nullptr) y[static_cast<size_t>(t) * rows + r] = tot[t];
                     const unsigned long long key = argmax_key(tot[t], r);
                     best[t] = key > best[t] ? key : best[t];
@@ -534,6 +616,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
+            if (add) tot[t] += y[static_cast<size_t>(t) * rows + r];
             if (y != nullptr) y[static_cast<size_t>(t) * rows + r] = tot[t];
             const unsigned long long key = argmax_key(tot[t], r);
             best[t] = key > best[t] ? key : best[t];
@@ -584,11 +667,21 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(const QJobs jobs, i
     for (int k = 1; k < kMaxJobs; ++k) jb = (k < jobs.n && b >= jobs.j[k].b0) ? k : jb;
     if constexpr (T2 != T) {
         if (jobs.j[jb].type == T2) {
-            stream_wg<T2, NT, XF32, NW>(jobs, jb, cols, xin);
+            stream_wg<T2, NT, XF32, NW>(jobs, jb, cols, xin, XStage{});
             return;
         }
     }
-    stream_wg<T, NT, XF32, NW>(jobs, jb, cols, xin);
+    stream_wg<T, NT, XF32, NW>(jobs, jb, cols, xin, XStage{});
+}
+// The same with fp32 activations staged per `xs` (vq_qmv_staged): single-type launches only.
+template <int T, int NT, int NW>
+__global__ __launch_bounds__(64 * NW) void qmv_staged_kernel(const QJobs jobs, const XStage xs, int cols,
+                                                             const float *__restrict__ xin) {
+    const int b = blockIdx.x;
+    int jb = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxJobs; ++k) jb = (k < jobs.n && b >= jobs.j[k].b0) ? k : jb;
+    stream_wg<T, NT, true, NW, true>(jobs, jb, cols, xin, xs);
 }
 
 // Final argmax over the per-workgroup keys: one workgroup per token; INT32_MAX when no value qualifies.
@@ -843,12 +936,30 @@ Plan plan_launch(const int *types, const int *rows, int n, int cols, int n_tok) 
 // holds them, else kFallbackWaves (the rows per workgroup come from the launch's plan, so every token chunk
 // splits the rows alike).
 template <int T, int T2, int N>
-int launch_stream(const QJobs &jobs, const int *types, int cols, const void *xp, bool x_f32, hipStream_t s) {
+int launch_stream(const QJobs &jobs, const int *types, int cols, const void *xp, bool x_f32, hipStream_t s,
+                  const XStage &xs) {
     int rwg[kMaxJobs];
     for (int k = 0; k < jobs.n; ++k) rwg[k] = jobs.j[k].rwg;
     constexpr int NWP = wg_waves<N>(), NWF = kFallbackWaves;
     const dim3 grid(static_cast<unsigned>(jobs.blocks));
     const size_t ldsp = plan_lds<T, T2, N, NWP>(types, jobs.n, cols, rwg);
+    if constexpr (T2 == T) {
+        // Staged fp32 activations (vq_qmv_staged): their own instances, with the plain kernel's geometry.
+        if (x_f32 && xs.flags != 0) {
+            static const int raised_p = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_staged_kernel<T, N, NWP>));
+            static const int raised_f = raise_dynamic_lds(reinterpret_cast<const void *>(&qmv_staged_kernel<T, N, NWF>));
+            (void)raised_p, (void)raised_f;
+            const float *xf = static_cast<const float *>(xp);
+            if (resident_chip<T, T2, N, NWP>(ldsp) > 0) {
+                qmv_staged_kernel<T, N, NWP><<<grid, dim3(64 * NWP), ldsp, s>>>(jobs, xs, cols, xf);
+            } else {
+                const size_t ldsf = plan_lds<T, T2, N, NWF>(types, jobs.n, cols, rwg);
+                if (resident_chip<T, T2, N, NWF>(ldsf) == 0) return static_cast<int>(hipErrorInvalidConfiguration);
+                qmv_staged_kernel<T, N, NWF><<<grid, dim3(64 * NWF), ldsf, s>>>(jobs, xs, cols, xf);
+            }
+            return hip_status(hipGetLastError());
+        }
+    }
     if (resident_chip<T, T2, N, NWP>(ldsp) > 0) {
         if (x_f32)
             qmv_stream_kernel<T, T2, N, true, NWP><<<grid, dim3(64 * NWP), ldsp, s>>>(jobs, cols, xp);
@@ -878,7 +989,8 @@ long argmax_waves(int rows, int cols, int ntok) {
 // ([ntok][argmax_waves] keys, single job), also amax_out[t] = argmax_r y[t][r].
 template <int T, int T2>
 int launch_jobs(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y, int cols,
-                const void *x, bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s) {
+                const void *x, bool x_f32, int ntok, unsigned long long *amax, int32_t *amax_out, hipStream_t s,
+                const XStage &xs = XStage{}) {
     if (n < 1 || n > kMaxJobs || (amax && n != 1)) return static_cast<int>(hipErrorInvalidValue);
     // Units per row stay below 2^13 (the kernels' unit-to-row quotient relies on it); the activation image of
     // one token would not fit LDS long before that.
@@ -901,13 +1013,15 @@ int launch_jobs(int n, const int *types, const uint8_t *const *w, const int *row
             jobs.j[k].type = types[k];
         }
         jobs.blocks = pl.blocks;
+        XStage xsc = xs;
+        if (xs.x2 != nullptr) xsc.x2 = xs.x2 + static_cast<size_t>(c) * cols;
 #ifdef VQ_TIMING
         jobs.tm = static_cast<unsigned long long *>(vq_debug_timing_buffer());
 #endif
         jobs.amax = amax ? amax + static_cast<size_t>(c) * pl.blocks : nullptr;
         const void *xp = static_cast<const uint8_t *>(x) + static_cast<size_t>(c) * tok_bytes;
         const int st = with_tokens<max_tokens<T, T2>()>(m, [&](auto nt) {
-            return launch_stream<T, T2, decltype(nt)::value>(jobs, types, cols, xp, x_f32, s);
+            return launch_stream<T, T2, decltype(nt)::value>(jobs, types, cols, xp, x_f32, s, xsc);
         });
         if (st) return st;
     }
@@ -934,6 +1048,14 @@ int launch_mixed_q8(int n, const int *types, const uint8_t *const *w, const int 
         return launch_jobs<T, T>(n, types, w, rows, y, cols, x, true, ntok, nullptr, nullptr, s);
     else
         return launch_jobs<T, VQ_Q8_0>(n, types, w, rows, y, cols, x, true, ntok, nullptr, nullptr, s);
+}
+
+template <int T>
+int launch_quant_staged(const uint8_t *w, int rows, int cols, long rb, const float *x, const XStage &xs, int ntok,
+                        float *y, hipStream_t s) {
+    (void)rb;
+    const int types[1] = {T};
+    return launch_jobs<T, T>(1, types, &w, &rows, &y, cols, x, true, ntok, nullptr, nullptr, s, xs);
 }
 
 template <int T>
@@ -968,6 +1090,8 @@ int launch_dequant(const uint8_t *w, int rows, int cols, long rb, float *out, hi
     template int vq::launch_quant_jobs<T>(int, const uint8_t *const *, const int *, float *const *, int, const void *, \
                                           bool, int, unsigned long long *, int32_t *, hipStream_t);                 \
     template long vq::argmax_waves<T>(int, int, int);                                                                \
+    template int vq::launch_quant_staged<T>(const uint8_t *, int, int, long, const float *, const vq::XStage &, int, \
+                                            float *, hipStream_t);                                                   \
     template int vq::launch_mixed_q8<T>(int, const int *, const uint8_t *const *, const int *, float *const *, int, \
                                         const float *, int, hipStream_t);                                          \
     template int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \

@@ -259,6 +259,39 @@ class Runtime:
         st = self._lib.vq_qmv(t.type, t.data.data_ptr(), t.rows, t.cols, x_ptr, ntok, y_ptr, ws, nws, self._stream())
         _lib.check(st, "qmv launch")
 
+    def qmv_staged(self, weight: str, x: str, y: str, ntok: int = 1, *, x2: str | None = None,
+                   norm: str | None = None, eps: float = 1e-6, add: bool = False) -> None:
+        """y[t] (+)= W v[t] with the activations staged inside the matvec, as the megakernel's QMV flags do
+        (qwen_megakernel.cu:468-551; runtime/instructions.py:179-182): v = silu(x) * x2 when x2 is given, then
+        rmsnorm(v) * norm when norm (an F32 tensor or fp32 buffer of cols values) is given; add=True
+        accumulates into y. Quantized weights, cols <= 24576. No counterpart in the per-op runtime, whose
+        callers run silu_mul, rmsnorm and add as passes of their own."""
+        if ntok < 1:
+            raise ValueError("ntok must be positive")
+        t = self._tensor(weight)
+        if t.type in (0, 1):
+            raise ValueError(f"{weight}: qmv_staged needs a quantized weight")
+        _check_qmv_args(weight, t.cols, ntok)
+        xb = self._f32_buffer(x, t.cols * ntok)
+        yb = self._f32_buffer(y, t.rows * ntok)
+        flags = _lib.VQ_QMV_ADD if add else 0
+        x2p = nwp = None
+        if x2 is not None:
+            flags |= _lib.VQ_QMV_SILU_MUL
+            x2p = self._f32_buffer(x2, t.cols * ntok).data_ptr()
+        if norm is not None:
+            flags |= _lib.VQ_QMV_NORM
+            if norm in self.tensors:
+                nt = self._tensor(norm)
+                if nt.type != 0 or nt.rows * nt.cols != t.cols:
+                    raise ValueError(f"{norm}: norm weights must be an F32 tensor of {t.cols} values")
+                nwp = nt.data.data_ptr()
+            else:
+                nwp = self._f32_buffer(norm, t.cols).data_ptr()
+        st = self._lib.vq_qmv_staged(t.type, t.data.data_ptr(), t.rows, t.cols, xb.data_ptr(), x2p, nwp, float(eps),
+                                     flags, ntok, yb.data_ptr(), self._stream())
+        _lib.check(st, "qmv_staged launch")
+
     def qmv_group(self, weights: Sequence[str], x: str, ys: Sequence[str], ntok: int = 1) -> None:
         """ys[k][t] = W_k x[t] for up to 4 quantized weights of one width that read the same input, in one
         launch (a layer's gate/up or q/k/v; one quantized type, or one type plus Q8_0 small tensors). Same
