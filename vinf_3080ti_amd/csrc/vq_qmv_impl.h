@@ -266,8 +266,11 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
                     const float m[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
+                        // silu(z) = z / (1 + e^-z) with the hardware exp2 and reciprocal (~1 ulp each;
+                        // v_exp_f32 flushes to 0 / inf at the ends, where silu is 0 or z)
                         const float z = v[4 * k + q];
-                        v[4 * k + q] = z / (1.0f + expf(-z)) * m[q];
+                        const float e = __builtin_amdgcn_exp2f(-z * 1.4426950408889634f);
+                        v[4 * k + q] = z * __builtin_amdgcn_rcpf(1.0f + e) * m[q];
                     }
                 }
             }
