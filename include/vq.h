@@ -113,6 +113,15 @@ int vq_pack_x(const float *x, int ntok, int cols, void *xpack, void *stream);
 int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, float *y, void *workspace,
            size_t workspace_bytes, void *stream);
 
+/* Group g of x (n floats each): y = x * rsqrt(mean(x^2) + eps) * w, times silu(z) elementwise when z is not
+ * NULL; in-place (y == x) allowed. Replaces: Runtime.rmsnorm / Runtime.gated_rmsnorm (qwen_runtime.cu:36-52,
+ * 1914-1939). */
+int vq_rmsnorm(const float *x, const float *w, const float *z, float *y, int n, int groups, float eps, void *stream);
+
+/* out[i] = a[i] + b[i] (op 0), silu(a[i]) * b[i] (op 1), a[i] * sigmoid(b[i]) (op 2), i < n. Replaces:
+ * Runtime.add / silu_mul / sigmoid_mul (binary_op, qwen_runtime.cu:54-67, 1941-1958; same op codes). */
+int vq_binary(int op, const float *a, const float *b, float *out, long n, void *stream);
+
 /* Activation staging flags of vq_qmv_staged: the bits of the reference megakernel's QMV flags
  * (runtime/instructions.py:179-182; QMV_FLAG_ARGMAX = 4 is vq_lmhead_argmax here). */
 #define VQ_QMV_ADD 1      /* y[t][r] += (W v)[r] instead of =                                      */

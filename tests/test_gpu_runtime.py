@@ -269,3 +269,53 @@ def test_qmv_staged_fuses_silu_mul_norm_and_add(rt, oracle_mod):
         rt.qmv_staged("sw", "sx", "sy", 1, norm="sw")  # norm must be F32 cols values
     for name in ("sw", "sw.norm"):
         rt.free(name)
+
+
+def test_norm_and_elementwise_ops(rt, oracle_mod):
+    """rmsnorm / gated_rmsnorm / add / silu_mul / sigmoid_mul / copy (qwen_runtime.cu:36-67,1914-1958,
+    2200-2218) against the float64 staging restatement (rmsnorm = NORM staging, silu_mul = SILU_MUL staging)
+    and scipy's logistic; in-place rmsnorm; deterministic reruns."""
+    from scipy.special import expit
+
+    rng = np.random.default_rng(93)
+    n, groups = 1000, 3
+    x = (rng.standard_normal(n * groups) * 3).astype(np.float32)
+    z = rng.standard_normal(n * groups).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    rt.upload_raw("nw", w.tobytes(), T.F32, n, 1)
+    for name, v in (("ex", x), ("ez", z), ("ey", np.zeros_like(x))):
+        rt.alloc(name, v.size)
+        rt.write_floats(name, v.tolist())
+    rt.rmsnorm("ex", "nw", "ey", n, 1e-6, groups)
+    got = np.array(rt.read_floats("ey")).reshape(groups, n)
+    ref = oracle_mod.stage_x(x.reshape(groups, n), None, w, 1e-6, oracle_mod.STAGE_NORM)
+    assert np.allclose(got, ref, rtol=2e-6, atol=1e-7)
+    rt.rmsnorm("ex", "nw", "ey", n, 1e-6, groups)
+    assert np.array_equal(np.array(rt.read_floats("ey")).reshape(groups, n), got)
+    rt.gated_rmsnorm("ex", "nw", "ez", "ey", n, 1e-6, groups)
+    silu_z = oracle_mod.stage_x(z, np.ones_like(z), None, 0.0, oracle_mod.STAGE_SILU_MUL).reshape(groups, n)
+    assert np.allclose(np.array(rt.read_floats("ey")).reshape(groups, n), ref * silu_z, rtol=4e-6, atol=1e-7)
+    rt.rmsnorm("ex", "nw", "ex", n, 1e-6, groups)  # in place
+    assert np.allclose(np.array(rt.read_floats("ex")).reshape(groups, n), ref, rtol=2e-6, atol=1e-7)
+    rt.write_floats("ex", x.tolist())
+    m = n * groups - 3  # a ragged tail
+    rt.add("ex", "ez", "ey", m)
+    assert np.array_equal(np.array(rt.read_floats("ey"), np.float32)[:m], (x + z)[:m])
+    rt.silu_mul("ex", "ez", "ey", m)
+    assert np.allclose(np.array(rt.read_floats("ey"))[:m],
+                       oracle_mod.stage_x(x, z, None, 0.0, oracle_mod.STAGE_SILU_MUL)[:m], rtol=2e-6, atol=1e-7)
+    rt.sigmoid_mul("ex", "ez", "ey", m)
+    assert np.allclose(np.array(rt.read_floats("ey"))[:m], (x.astype(np.float64) * expit(z.astype(np.float64)))[:m],
+                       rtol=2e-6, atol=1e-7)
+    rt.copy("ey", 10, "ex", 20, 100)
+    rt.synchronize()
+    assert np.array_equal(np.array(rt.read_floats("ey"), np.float32)[10:110], x[20:120])
+    with pytest.raises(ValueError):
+        rt.copy("ey", n * groups - 5, "ex", 0, 10)
+    with pytest.raises(ValueError):
+        rt.copy("ey", -1, "ex", 0, 1)
+    with pytest.raises(ValueError):
+        rt.rmsnorm("ex", "nw", "ey", n + 1, 1e-6, groups)  # weights hold n values
+    with pytest.raises(KeyError):
+        rt.add("ex", "nope", "ey", 4)
+    rt.free("nw")

@@ -27,6 +27,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_qmv_workspace_bytes_for": (SZ, [I, I, I, I]),
     "vq_qmv_path": (I, [I, I, I, I, SZ]),
     "vq_qmv_staged": (I, [I, P, I, I, P, P, P, F, I, I, P, P]),
+    "vq_rmsnorm": (I, [P, P, P, P, I, I, F, P]),
+    "vq_binary": (I, [I, P, P, P, ctypes.c_long, P]),
     "vq_quantize_x": (I, [P, I, I, P, P, P, P]),
     "vq_pack_x": (I, [P, I, I, P, P]),
     "vq_qmv_packed": (I, [I, P, I, I, P, I, P, P]),

@@ -28,7 +28,7 @@ HIPCC_FLAGS = [
 
 
 def sources() -> list[Path]:
-    return [CSRC / "vq_api.hip"] + sorted(CSRC.glob("vq_t_*.hip"))
+    return [CSRC / "vq_api.hip", CSRC / "vq_ops.hip"] + sorted(CSRC.glob("vq_t_*.hip"))
 
 
 def headers() -> list[Path]:

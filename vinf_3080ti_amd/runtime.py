@@ -292,6 +292,64 @@ class Runtime:
                                      flags, ntok, yb.data_ptr(), self._stream())
         _lib.check(st, "qmv_staged launch")
 
+    # ---- ops around the matvec (the reference runtime's elementwise / norm ops) ------------------------------
+    def _f32_weight(self, name: str, n: int) -> torch.Tensor:
+        """find_f32_weight: an uploaded F32 tensor of n values."""
+        t = self._tensor(name)
+        if t.type != 0 or t.rows * t.cols != n:
+            raise ValueError(f"{name}: expected an F32 tensor of {n} values")
+        return t.data
+
+    def rmsnorm(self, x: str, w: str, y: str, n: int, eps: float = 1e-6, groups: int = 1) -> None:
+        """y[g] = x[g] * rsqrt(mean(x[g]^2) + eps) * w for each of `groups` rows of n (Runtime_rmsnorm,
+        qwen_runtime.cu:36-44,1914-1925); w an F32 tensor; y may be x."""
+        if n < 1 or groups < 1:
+            raise ValueError("n and groups must be positive")
+        xb, yb = self._f32_buffer(x, n * groups), self._f32_buffer(y, n * groups)
+        wt = self._f32_weight(w, n)
+        _lib.check(self._lib.vq_rmsnorm(xb.data_ptr(), wt.data_ptr(), None, yb.data_ptr(), n, groups, float(eps),
+                                        self._stream()), "rmsnorm")
+
+    def gated_rmsnorm(self, x: str, w: str, z: str, y: str, n: int, eps: float, groups: int) -> None:
+        """y = rmsnorm(x) * w * silu(z) per group of n (Runtime_gated_rmsnorm, qwen_runtime.cu:46-52,1927-1939)."""
+        if n < 1 or groups < 1:
+            raise ValueError("n and groups must be positive")
+        xb, zb = self._f32_buffer(x, n * groups), self._f32_buffer(z, n * groups)
+        yb = self._f32_buffer(y, n * groups)
+        wt = self._f32_weight(w, n)
+        _lib.check(self._lib.vq_rmsnorm(xb.data_ptr(), wt.data_ptr(), zb.data_ptr(), yb.data_ptr(), n, groups,
+                                        float(eps), self._stream()), "gated_rmsnorm")
+
+    def _binary(self, op: int, a: str, b: str, out: str, n: int) -> None:
+        """binary_op (qwen_runtime.cu:1941-1954)."""
+        if n < 0:
+            raise ValueError("n must be non-negative")
+        ab, bb, ob = self._f32_buffer(a, n), self._f32_buffer(b, n), self._f32_buffer(out, n)
+        _lib.check(self._lib.vq_binary(op, ab.data_ptr(), bb.data_ptr(), ob.data_ptr(), n, self._stream()),
+                   "elementwise")
+
+    def add(self, a: str, b: str, out: str, n: int) -> None:
+        self._binary(0, a, b, out, n)
+
+    def silu_mul(self, gate: str, up: str, out: str, n: int) -> None:
+        self._binary(1, gate, up, out, n)
+
+    def sigmoid_mul(self, x: str, gate: str, out: str, n: int) -> None:
+        self._binary(2, x, gate, out, n)
+
+    def copy(self, dst: str, dst_off: int, src: str, src_off: int, n: int) -> None:
+        """dst[dst_off:+n] = src[src_off:+n] in elements, buffers of one precision (Runtime_copy,
+        qwen_runtime.cu:2200-2218); asynchronous on the current stream."""
+        if dst_off < 0 or src_off < 0 or n < 0:
+            raise ValueError("offsets and count must be non-negative")
+        db, sb = self._any_buffer(dst), self._any_buffer(src)
+        if db.elem != sb.elem:
+            raise TypeError("copy between buffers of different precision")
+        if dst_off + n > db.data.numel() or src_off + n > sb.data.numel():
+            raise ValueError(f"copy out of bounds ({dst} <- {src})")
+        if n:
+            db.data[dst_off:dst_off + n].copy_(sb.data[src_off:src_off + n], non_blocking=True)
+
     def qmv_group(self, weights: Sequence[str], x: str, ys: Sequence[str], ntok: int = 1) -> None:
         """ys[k][t] = W_k x[t] for up to 4 quantized weights of one width that read the same input, in one
         launch (a layer's gate/up or q/k/v; one quantized type, or one type plus Q8_0 small tensors). Same
