@@ -122,6 +122,14 @@ int vq_rmsnorm(const float *x, const float *w, const float *z, float *y, int n, 
  * Runtime.add / silu_mul / sigmoid_mul (binary_op, qwen_runtime.cu:54-67, 1941-1958; same op codes). */
 int vq_binary(int op, const float *a, const float *b, float *out, long n, void *stream);
 
+/* q[h][d] = raw[h][d], gate[h][d] = raw[h][hd + d] for heads x hd (raw rows are [query, gate]). Replaces:
+ * Runtime.split_gated_q (qwen_runtime.cu:70-76). */
+int vq_split_gated_q(const float *raw, float *q, float *gate, int heads, int hd, void *stream);
+
+/* NeoX RoPE in place on x [ntok][heads][hd], dims [0, rot) of each head, token t at position pos0 + t:
+ * (x[j], x[j + rot/2]) turns by (pos0 + t) * base^(-2j/rot). Replaces: Runtime.rope (qwen_runtime.cu:81-92). */
+int vq_rope(float *x, int ntok, int heads, int hd, int rot, int pos0, double base, void *stream);
+
 /* Activation staging flags of vq_qmv_staged: the bits of the reference megakernel's QMV flags
  * (runtime/instructions.py:179-182; QMV_FLAG_ARGMAX = 4 is vq_lmhead_argmax here). */
 #define VQ_QMV_ADD 1      /* y[t][r] += (W v)[r] instead of =                                      */

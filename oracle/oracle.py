@@ -8,6 +8,7 @@ Functions mirror the reference CPU path (/root/reference/engine/csrc/cpu/qwen_cp
   decode_codes   integer codes + per-16 scales/mins with dequant == scale*code - min
   argmax_rows    argmax_kernel (qwen_runtime.cu:850-876), ties to the lowest index
   stage_x        the megakernel's QMV activation staging (qwen_megakernel.cu:485-551), float64 numpy
+  rope_neox      NeoX partial RoPE (rope_neox_kernel, qwen_runtime.cu:81-92), float64 numpy
 """
 from __future__ import annotations
 
@@ -142,4 +143,18 @@ def stage_x(x: np.ndarray, x2: np.ndarray | None, norm_w: np.ndarray | None, eps
     if flags & STAGE_NORM:
         ms = (v * v).mean(axis=-1, keepdims=True)
         v = v / np.sqrt(ms + eps) * np.asarray(norm_w, np.float64)
+    return v
+
+
+def rope_neox(x: np.ndarray, heads: int, hd: int, rot: int, pos0: int, base: float) -> np.ndarray:
+    """float64 NeoX RoPE of x [ntok][heads][hd] (rope_neox_kernel, qwen_runtime.cu:81-92): for j < rot/2 the
+    pair (x[j], x[j + rot/2]) of token t turns by (pos0 + t) * base^(-2j/rot); dims >= rot are untouched."""
+    v = np.array(x, np.float64).reshape(-1, heads, hd)
+    half = rot // 2
+    j = np.arange(half)
+    ang = (pos0 + np.arange(v.shape[0]))[:, None] * base ** (-2.0 * j / rot)[None, :]
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    a, b = v[..., :half].copy(), v[..., half:rot].copy()
+    v[..., :half] = a * c - b * s
+    v[..., half:rot] = b * c + a * s
     return v

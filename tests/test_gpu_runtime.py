@@ -319,3 +319,28 @@ def test_norm_and_elementwise_ops(rt, oracle_mod):
     with pytest.raises(KeyError):
         rt.add("ex", "nope", "ey", 4)
     rt.free("nw")
+
+
+def test_split_gated_q_and_rope(rt, oracle_mod):
+    """split_gated_q (exact) and NeoX rope (qwen_runtime.cu:70-92) against the float64 rope_neox restatement;
+    ntok 3 at a non-zero start position; argument errors as in the reference."""
+    rng = np.random.default_rng(95)
+    heads, hd, rot, ntok, pos = 4, 32, 16, 3, 1000
+    raw = rng.standard_normal(2 * heads * hd).astype(np.float32)
+    x = rng.standard_normal(ntok * heads * hd).astype(np.float32)
+    for name, v in (("graw", raw), ("gq", np.zeros(heads * hd)), ("gg", np.zeros(heads * hd)), ("rx", x)):
+        rt.alloc(name, v.size)
+        rt.write_floats(name, np.asarray(v, np.float32).tolist())
+    rt.split_gated_q("graw", "gq", "gg", heads, hd)
+    r2 = raw.reshape(heads, 2, hd)
+    assert np.array_equal(np.array(rt.read_floats("gq"), np.float32), r2[:, 0].reshape(-1))
+    assert np.array_equal(np.array(rt.read_floats("gg"), np.float32), r2[:, 1].reshape(-1))
+    rt.rope("rx", heads, hd, rot, pos, 1e6, ntok)
+    got = np.array(rt.read_floats("rx")).reshape(ntok, heads, hd)
+    ref = oracle_mod.rope_neox(x.reshape(ntok, heads, hd), heads, hd, rot, pos, 1e6)
+    assert np.allclose(got, ref, rtol=1e-5, atol=2e-6)
+    assert np.array_equal(got[..., rot:], x.reshape(ntok, heads, hd)[..., rot:])
+    for bad in (dict(rot=15), dict(rot=0), dict(rot=hd + 2), dict(ntok=0)):
+        kw = dict(rot=rot, ntok=1) | bad
+        with pytest.raises(ValueError):
+            rt.rope("rx", heads, hd, kw["rot"], 0, 1e4, kw["ntok"])

@@ -268,3 +268,23 @@ def test_stage_x_is_pinned_by_closed_forms(oracle_mod):
                                 oracle_mod.STAGE_NORM), rtol=1e-14)
     # ADD does not change the staged activations
     assert np.array_equal(st(x, None, None, 0.0, oracle_mod.STAGE_ADD), x)
+
+
+def test_rope_neox_is_pinned_by_rotation_properties(oracle_mod):
+    """rope_neox: position 0 is the identity; each (j, j + rot/2) pair keeps its length; rotations compose
+    (pos a then pos b == pos a + b per token); pair 0 turns by exactly pos radians; dims >= rot untouched."""
+    r = oracle_mod.rope_neox
+    rng = np.random.default_rng(62)
+    heads, hd, rot = 3, 16, 10
+    x = rng.standard_normal((1, heads, hd))
+    assert np.allclose(r(x, heads, hd, rot, 0, 1e4), x, rtol=0, atol=0)
+    y = r(x, heads, hd, rot, 7, 1e4)
+    half = rot // 2
+    assert np.allclose(np.hypot(y[..., :half], y[..., half:rot]), np.hypot(x[..., :half], x[..., half:rot]), rtol=1e-13)
+    assert np.array_equal(y[..., rot:], x[..., rot:])
+    assert np.allclose(r(r(x, heads, hd, rot, 3, 1e4), heads, hd, rot, 4, 1e4), y, rtol=1e-12, atol=1e-12)
+    c, s = np.cos(7.0), np.sin(7.0)
+    assert np.allclose(y[..., 0], x[..., 0] * c - x[..., half] * s, rtol=1e-14)
+    # token t sits at pos0 + t
+    x2 = rng.standard_normal((2, heads, hd))
+    assert np.allclose(r(x2, heads, hd, rot, 5, 1e4)[1], r(x2[1:], heads, hd, rot, 6, 1e4)[0], rtol=1e-14)

@@ -1,6 +1,6 @@
-// vq_ops.hip -- the runtime's elementwise and normalisation ops around the matvec (the reference runtime's
-// rmsnorm_kernel, gated_rmsnorm_kernel, add/silu_mul/sigmoid_mul kernels, qwen_runtime.cu:36-67): HBM-bound
-// streams in fp32.
+// vq_ops.hip -- the runtime's elementwise, normalisation and layout ops around the matvec (the reference
+// runtime's rmsnorm, gated_rmsnorm, add / silu_mul / sigmoid_mul, split_gated_q and NeoX rope kernels,
+// qwen_runtime.cu:36-92): HBM-bound streams in fp32.
 //
 // RMS sums: each thread adds its strided elements in order, then a fixed pairwise tree over the 256 threads in
 // LDS, so a group's result does not depend on timing. silu / sigmoid use expf and an IEEE division (these
@@ -60,6 +60,34 @@ __global__ __launch_bounds__(256) void binary_kernel(const float *a, const float
     }
 }
 
+// Gated query: head h's raw row is [query (hd), gate (hd)]; q and gate get the halves.
+__global__ __launch_bounds__(256) void split_gated_q_kernel(const float *__restrict__ raw, float *__restrict__ q,
+                                                           float *__restrict__ gate, int heads, int hd) {
+    const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= static_cast<long>(heads) * hd) return;
+    const long h = i / hd, d = i - h * hd;
+    q[i] = raw[2 * h * hd + d];
+    gate[i] = raw[2 * h * hd + hd + d];
+}
+
+// NeoX RoPE in place over dims [0, rot) of each head of token t (position pos0 + t): pair (j, j + rot/2)
+// turns by (pos0 + t) * base^(-2j / rot), the angle and its cosine / sine in fp64, the rotation in fp32.
+__global__ __launch_bounds__(128) void rope_neox_kernel(float *x, int ntok, int heads, int hd, int rot, int pos0,
+                                                        double base) {
+    const int half = rot / 2;
+    const long i = static_cast<long>(blockIdx.x) * 128 + threadIdx.x;
+    if (i >= static_cast<long>(ntok) * heads * half) return;
+    const int j = static_cast<int>(i % half);
+    const long th = i / half;  // token * heads + head
+    const int t = static_cast<int>(th / heads);
+    const double ang = static_cast<double>(pos0 + t) * pow(base, -2.0 * j / rot);
+    const float c = static_cast<float>(cos(ang)), sn = static_cast<float>(sin(ang));
+    float *head = x + th * hd;
+    const float a = head[j], b = head[j + half];
+    head[j] = a * c - b * sn;
+    head[j + half] = b * c + a * sn;
+}
+
 int status_of(hipError_t e) { return e == hipSuccess ? VQ_OK : static_cast<int>(e); }
 
 }  // namespace
@@ -83,6 +111,25 @@ int vq_binary(int op, const float *a, const float *b, float *out, long n, void *
     if (op == 0) binary_kernel<0><<<blocks, 256, 0, s>>>(a, b, out, n);
     else if (op == 1) binary_kernel<1><<<blocks, 256, 0, s>>>(a, b, out, n);
     else binary_kernel<2><<<blocks, 256, 0, s>>>(a, b, out, n);
+    return status_of(hipGetLastError());
+}
+
+int vq_split_gated_q(const float *raw, float *q, float *gate, int heads, int hd, void *stream) {
+    if (!raw || !q || !gate) return VQ_ERR_ARG;
+    if (heads < 1 || hd < 1) return VQ_ERR_SHAPE;
+    const long n = static_cast<long>(heads) * hd;
+    split_gated_q_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        raw, q, gate, heads, hd);
+    return status_of(hipGetLastError());
+}
+
+int vq_rope(float *x, int ntok, int heads, int hd, int rot, int pos0, double base, void *stream) {
+    if (!x) return VQ_ERR_ARG;
+    if (ntok < 1 || heads < 1 || hd < 1 || rot <= 0 || rot % 2 || rot > hd || pos0 < 0 || !(base > 0.0))
+        return VQ_ERR_SHAPE;
+    const long n = static_cast<long>(ntok) * heads * (rot / 2);
+    rope_neox_kernel<<<static_cast<unsigned>((n + 127) / 128), 128, 0, static_cast<hipStream_t>(stream)>>>(
+        x, ntok, heads, hd, rot, pos0, base);
     return status_of(hipGetLastError());
 }
 

@@ -337,6 +337,27 @@ class Runtime:
     def sigmoid_mul(self, x: str, gate: str, out: str, n: int) -> None:
         self._binary(2, x, gate, out, n)
 
+    def split_gated_q(self, raw: str, q: str, gate: str, heads: int, hd: int) -> None:
+        """Per head, raw [query(hd), gate(hd)] -> q, gate (Runtime_split_gated_q, qwen_runtime.cu:70-76)."""
+        if heads < 1 or hd < 1:
+            raise ValueError("heads and hd must be positive")
+        n = heads * hd
+        rb, qb, gb = self._f32_buffer(raw, 2 * n), self._f32_buffer(q, n), self._f32_buffer(gate, n)
+        _lib.check(self._lib.vq_split_gated_q(rb.data_ptr(), qb.data_ptr(), gb.data_ptr(), heads, hd, self._stream()),
+                   "split_gated_q")
+
+    def rope(self, x: str, heads: int, hd: int, rot: int, pos: int, base: float = 10000.0, ntok: int = 1) -> None:
+        """NeoX partial RoPE in place over the first rot dims of each head, token t at position pos + t
+        (Runtime_rope, qwen_runtime.cu:81-92)."""
+        if rot <= 0 or rot % 2 != 0 or rot > hd:
+            raise ValueError(f"invalid rotary dim {rot}")
+        if ntok < 1:
+            raise ValueError("ntok must be positive")
+        if heads < 1 or pos < 0:
+            raise ValueError("heads must be positive and pos non-negative")
+        xb = self._f32_buffer(x, heads * hd * ntok)
+        _lib.check(self._lib.vq_rope(xb.data_ptr(), ntok, heads, hd, rot, pos, float(base), self._stream()), "rope")
+
     def copy(self, dst: str, dst_off: int, src: str, src_off: int, n: int) -> None:
         """dst[dst_off:+n] = src[src_off:+n] in elements, buffers of one precision (Runtime_copy,
         qwen_runtime.cu:2200-2218); asynchronous on the current stream."""
