@@ -130,6 +130,12 @@ int vq_split_gated_q(const float *raw, float *q, float *gate, int heads, int hd,
  * (x[j], x[j + rot/2]) turns by (pos0 + t) * base^(-2j/rot). Replaces: Runtime.rope (qwen_runtime.cu:81-92). */
 int vq_rope(float *x, int ntok, int heads, int hd, int rot, int pos0, double base, void *stream);
 
+/* k, v [ntok][kv_heads][hd] fp32 into contiguous caches kc, vc [kv_heads][max_seq][hd] of `elem` bytes per
+ * value (4: fp32, 2: fp16 rounded to nearest) at positions pos0 .. pos0 + ntok - 1. Replaces:
+ * Runtime.kv_append (qwen_runtime.cu:115-128, contiguous caches). */
+int vq_kv_append(const float *k, const float *v, void *kc, void *vc, int elem, int ntok, int kv_heads, int max_seq,
+                 int hd, int pos0, void *stream);
+
 /* Activation staging flags of vq_qmv_staged: the bits of the reference megakernel's QMV flags
  * (runtime/instructions.py:179-182; QMV_FLAG_ARGMAX = 4 is vq_lmhead_argmax here). */
 #define VQ_QMV_ADD 1      /* y[t][r] += (W v)[r] instead of =                                      */

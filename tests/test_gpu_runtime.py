@@ -344,3 +344,30 @@ def test_split_gated_q_and_rope(rt, oracle_mod):
         kw = dict(rot=rot, ntok=1) | bad
         with pytest.raises(ValueError):
             rt.rope("rx", heads, hd, kw["rot"], 0, 1e4, kw["ntok"])
+
+
+@pytest.mark.parametrize("elem", [4, 2])
+def test_kv_append_contiguous_caches(rt, elem):
+    """kv_append (qwen_runtime.cu:115-128): token t's k/v rows land at position pos + t of each head's
+    [max_seq][hd] block (fp16 caches rounded to nearest); other positions keep their contents; errors."""
+    rng = np.random.default_rng(97 + elem)
+    kvh, hd, max_seq, pos, ntok = 2, 8, 10, 6, 3
+    k = rng.standard_normal((ntok, kvh, hd)).astype(np.float32)
+    v = rng.standard_normal((ntok, kvh, hd)).astype(np.float32)
+    for name, a in (("kk", k), ("kv", v)):
+        rt.alloc(name, a.size)
+        rt.write_floats(name, a.reshape(-1).tolist())
+    for name in ("kc", "vc"):
+        rt.alloc(name, kvh * max_seq * hd, elem)
+    rt.kv_append("kk", "kv", "kc", "vc", kvh, max_seq, hd, pos, ntok)
+    dt = np.float32 if elem == 4 else np.float16
+    for name, a in (("kc", k), ("vc", v)):
+        got = np.array(rt.read_floats(name), np.float32).reshape(kvh, max_seq, hd)
+        want = np.zeros((kvh, max_seq, hd), np.float32)
+        want[:, pos:pos + ntok] = a.astype(dt).astype(np.float32).transpose(1, 0, 2)
+        assert np.array_equal(got, want), name
+    with pytest.raises(ValueError):
+        rt.kv_append("kk", "kv", "kc", "vc", kvh, max_seq, hd, max_seq - 2, ntok)
+    rt.alloc("vc32" if elem == 2 else "vc16", kvh * max_seq * hd, 4 if elem == 2 else 2)
+    with pytest.raises(TypeError):
+        rt.kv_append("kk", "kv", "kc", "vc32" if elem == 2 else "vc16", kvh, max_seq, hd, 0, 1)

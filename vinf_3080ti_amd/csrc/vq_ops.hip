@@ -1,6 +1,6 @@
 // vq_ops.hip -- the runtime's elementwise, normalisation and layout ops around the matvec (the reference
-// runtime's rmsnorm, gated_rmsnorm, add / silu_mul / sigmoid_mul, split_gated_q and NeoX rope kernels,
-// qwen_runtime.cu:36-92): HBM-bound streams in fp32.
+// runtime's rmsnorm, gated_rmsnorm, add / silu_mul / sigmoid_mul, split_gated_q, NeoX rope and kv_append
+// kernels, qwen_runtime.cu:36-128): HBM-bound streams in fp32 (fp16 KV caches).
 //
 // RMS sums: each thread adds its strided elements in order, then a fixed pairwise tree over the 256 threads in
 // LDS, so a group's result does not depend on timing. silu / sigmoid use expf and an IEEE division (these
@@ -88,6 +88,23 @@ __global__ __launch_bounds__(128) void rope_neox_kernel(float *x, int ntok, int 
     head[j + half] = b * c + a * sn;
 }
 
+// KV append into contiguous caches [kv_head][max_seq][hd] (fp32, or fp16 rounded to nearest): element d of
+// head h of token t goes to position pos0 + t.
+__device__ __forceinline__ void kv_put(float *c, size_t i, float v) { c[i] = v; }
+__device__ __forceinline__ void kv_put(_Float16 *c, size_t i, float v) { c[i] = static_cast<_Float16>(v); }
+template <typename C>
+__global__ __launch_bounds__(256) void kv_append_kernel(const float *__restrict__ k, const float *__restrict__ v,
+                                                        C *__restrict__ kc, C *__restrict__ vc, int ntok,
+                                                        int kv_heads, int max_seq, int hd, int pos0) {
+    const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= static_cast<long>(ntok) * kv_heads * hd) return;
+    const long d = i % hd, th = i / hd;
+    const long h = th % kv_heads, t = th / kv_heads;
+    const size_t dst = (static_cast<size_t>(h) * max_seq + pos0 + t) * hd + d;
+    kv_put(kc, dst, k[i]);
+    kv_put(vc, dst, v[i]);
+}
+
 int status_of(hipError_t e) { return e == hipSuccess ? VQ_OK : static_cast<int>(e); }
 
 }  // namespace
@@ -130,6 +147,22 @@ int vq_rope(float *x, int ntok, int heads, int hd, int rot, int pos0, double bas
     const long n = static_cast<long>(ntok) * heads * (rot / 2);
     rope_neox_kernel<<<static_cast<unsigned>((n + 127) / 128), 128, 0, static_cast<hipStream_t>(stream)>>>(
         x, ntok, heads, hd, rot, pos0, base);
+    return status_of(hipGetLastError());
+}
+
+int vq_kv_append(const float *k, const float *v, void *kc, void *vc, int elem, int ntok, int kv_heads, int max_seq,
+                 int hd, int pos0, void *stream) {
+    if (!k || !v || !kc || !vc || (elem != 2 && elem != 4)) return VQ_ERR_ARG;
+    if (ntok < 1 || kv_heads < 1 || hd < 1 || pos0 < 0 || pos0 + ntok > max_seq) return VQ_ERR_SHAPE;
+    const long n = static_cast<long>(ntok) * kv_heads * hd;
+    const unsigned blocks = static_cast<unsigned>((n + 255) / 256);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (elem == 2)
+        kv_append_kernel<_Float16><<<blocks, 256, 0, s>>>(k, v, static_cast<_Float16 *>(kc), static_cast<_Float16 *>(vc),
+                                                          ntok, kv_heads, max_seq, hd, pos0);
+    else
+        kv_append_kernel<float><<<blocks, 256, 0, s>>>(k, v, static_cast<float *>(kc), static_cast<float *>(vc), ntok,
+                                                       kv_heads, max_seq, hd, pos0);
     return status_of(hipGetLastError());
 }
 

@@ -358,6 +358,23 @@ class Runtime:
         xb = self._f32_buffer(x, heads * hd * ntok)
         _lib.check(self._lib.vq_rope(xb.data_ptr(), ntok, heads, hd, rot, pos, float(base), self._stream()), "rope")
 
+    def kv_append(self, k: str, v: str, kc: str, vc: str, kv_heads: int, max_seq: int, hd: int, pos: int,
+                  ntok: int = 1) -> None:
+        """k, v [ntok][kv_heads][hd] into the caches [kv_heads][max_seq][hd] at positions pos .. pos + ntok - 1
+        (Runtime_kv_append, qwen_runtime.cu:115-128); fp16 caches are written rounded to nearest."""
+        if ntok < 1 or pos < 0 or pos + ntok > max_seq:
+            raise ValueError(f"positions [{pos}, {pos + ntok}) outside KV cache of {max_seq}")
+        n, cache = kv_heads * hd * ntok, kv_heads * hd * max_seq
+        kb, vb = self._f32_buffer(k, n), self._f32_buffer(v, n)
+        kcb, vcb = self._any_buffer(kc), self._any_buffer(vc)
+        for name, b in ((kc, kcb), (vc, vcb)):
+            if b.data.numel() < cache:
+                raise ValueError(f"device buffer {name} has {b.data.numel()} values, need {cache}")
+        if kcb.elem != vcb.elem:
+            raise TypeError("K and V caches differ in precision")
+        _lib.check(self._lib.vq_kv_append(kb.data_ptr(), vb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(),
+                                          kcb.elem, ntok, kv_heads, max_seq, hd, pos, self._stream()), "kv_append")
+
     def copy(self, dst: str, dst_off: int, src: str, src_off: int, n: int) -> None:
         """dst[dst_off:+n] = src[src_off:+n] in elements, buffers of one precision (Runtime_copy,
         qwen_runtime.cu:2200-2218); asynchronous on the current stream."""
