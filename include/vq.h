@@ -136,6 +136,14 @@ int vq_rope(float *x, int ntok, int heads, int hd, int rot, int pos0, double bas
 int vq_kv_append(const float *k, const float *v, void *kc, void *vc, int elem, int ntok, int kv_heads, int max_seq,
                  int hd, int pos0, void *stream);
 
+/* GQA attention: out[t][h] = softmax(q[t][h] . K / sqrt(hd)) V over the positions query token t sees, with K,
+ * V the rows of kv head h / (heads / kv_heads) in caches [kv_heads][max_seq][hd] (`elem` 4: fp32, 2: fp16).
+ * Token t sees [start, seq_len + t) (causal) or [start, seq_len + ntok - 1) (bidirectional != 0); start =
+ * seq_len + t - window when window > 0 and that is positive, else 0. hd <= 256. Replaces: Runtime.attention
+ * (qwen_runtime.cu:128-162, 2000-2030, contiguous caches). */
+int vq_attention(const float *q, const void *kc, const void *vc, float *out, int elem, int heads, int kv_heads, int hd,
+                 int max_seq, int seq_len, int ntok, int bidirectional, int window, void *stream);
+
 /* Activation staging flags of vq_qmv_staged: the bits of the reference megakernel's QMV flags
  * (runtime/instructions.py:179-182; QMV_FLAG_ARGMAX = 4 is vq_lmhead_argmax here). */
 #define VQ_QMV_ADD 1      /* y[t][r] += (W v)[r] instead of =                                      */

@@ -9,6 +9,7 @@ Functions mirror the reference CPU path (/root/reference/engine/csrc/cpu/qwen_cp
   argmax_rows    argmax_kernel (qwen_runtime.cu:850-876), ties to the lowest index
   stage_x        the megakernel's QMV activation staging (qwen_megakernel.cu:485-551), float64 numpy
   rope_neox      NeoX partial RoPE (rope_neox_kernel, qwen_runtime.cu:81-92), float64 numpy
+  attention      GQA attention with causal / bidirectional / window visibility (qwen_runtime.cu:128-162)
 """
 from __future__ import annotations
 
@@ -158,3 +159,25 @@ def rope_neox(x: np.ndarray, heads: int, hd: int, rot: int, pos0: int, base: flo
     v[..., :half] = a * c - b * s
     v[..., half:rot] = b * c + a * s
     return v
+
+
+def attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, heads: int, kv_heads: int, seq_len: int,
+              bidirectional: bool = False, window: int = 0) -> np.ndarray:
+    """float64 GQA attention (attention_kernel, qwen_runtime.cu:128-162): q [ntok][heads][hd], caches
+    [kv_heads][max_seq][hd]; token t sees positions [start, seq_len + t) (causal) or [start, seq_len + ntok - 1)
+    (bidirectional), start = seq_len + t - window when window > 0 and positive; scores scaled by 1/sqrt(hd)."""
+    q = np.asarray(q, np.float64)
+    ntok, _, hd = q.shape
+    out = np.zeros_like(q)
+    for t in range(ntok):
+        qend = seq_len + t
+        end = seq_len + ntok - 1 if bidirectional else qend
+        start = qend - window if window > 0 and qend > window else 0
+        for h in range(heads):
+            kvh = h // (heads // kv_heads)
+            k = np.asarray(kc[kvh, start:end], np.float64)
+            v = np.asarray(vc[kvh, start:end], np.float64)
+            s = k @ q[t, h] / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            out[t, h] = (p / p.sum()) @ v
+    return out

@@ -371,3 +371,31 @@ def test_kv_append_contiguous_caches(rt, elem):
     rt.alloc("vc32" if elem == 2 else "vc16", kvh * max_seq * hd, 4 if elem == 2 else 2)
     with pytest.raises(TypeError):
         rt.kv_append("kk", "kv", "kc", "vc32" if elem == 2 else "vc16", kvh, max_seq, hd, 0, 1)
+
+
+@pytest.mark.parametrize("elem", [4, 2])
+@pytest.mark.parametrize("ntok,seq_len,bidirectional,window", [(1, 300, 0, 0), (3, 77, 0, 0), (4, 129, 1, 0),
+                                                               (2, 500, 0, 64), (1, 1, 0, 0)])
+def test_attention_matches_oracle(rt, oracle_mod, elem, ntok, seq_len, bidirectional, window):
+    """attention (qwen_runtime.cu:128-162) vs the float64 restatement: GQA 8 heads over 2 kv heads, hd 128,
+    causal / bidirectional / sliding window, fp32 and fp16 caches (the cache values as stored)."""
+    rng = np.random.default_rng(1000 + 7 * ntok + seq_len + elem)
+    heads, kvh, hd, max_seq = 8, 2, 128, 520
+    q = rng.standard_normal((ntok, heads, hd)).astype(np.float32)
+    dt = np.float32 if elem == 4 else np.float16
+    kc = (rng.standard_normal((kvh, max_seq, hd)) * 0.3).astype(dt)
+    vc = rng.standard_normal((kvh, max_seq, hd)).astype(dt)
+    rt.alloc("aq", q.size)
+    rt.write_floats("aq", q.reshape(-1).tolist())
+    rt.alloc("ao", q.size)
+    for name, a in (("akc", kc), ("avc", vc)):
+        rt.alloc(name, a.size, elem)
+        rt.write(name, a.tobytes())
+    rt.attention("aq", "akc", "avc", "ao", heads, kvh, hd, max_seq, seq_len, ntok, bidirectional, window)
+    got = np.array(rt.read_floats("ao")).reshape(ntok, heads, hd)
+    ref = oracle_mod.attention(q, kc, vc, heads, kvh, seq_len, bool(bidirectional), window)
+    assert np.allclose(got, ref, rtol=2e-5, atol=2e-5)
+    with pytest.raises(ValueError):
+        rt.attention("aq", "akc", "avc", "ao", heads, 3, hd, max_seq, seq_len, ntok)
+    with pytest.raises(ValueError):
+        rt.attention("aq", "akc", "avc", "ao", heads, kvh, hd, max_seq, max_seq, 2)

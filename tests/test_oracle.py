@@ -288,3 +288,30 @@ def test_rope_neox_is_pinned_by_rotation_properties(oracle_mod):
     # token t sits at pos0 + t
     x2 = rng.standard_normal((2, heads, hd))
     assert np.allclose(r(x2, heads, hd, rot, 5, 1e4)[1], r(x2[1:], heads, hd, rot, 6, 1e4)[0], rtol=1e-14)
+
+
+def test_attention_is_pinned_by_closed_forms(oracle_mod):
+    """attention: equal keys average V; one visible position returns its V row; a window of 1 returns the
+    query's own position; a score gap of ln(3) weights 3:1; GQA heads read kv head h // (heads / kv_heads)."""
+    at = oracle_mod.attention
+    rng = np.random.default_rng(63)
+    kvh, heads, hd, ms = 2, 4, 8, 12
+    v = rng.standard_normal((kvh, ms, hd))
+    q = rng.standard_normal((1, heads, hd))
+    zero_k = np.zeros((kvh, ms, hd))
+    o = at(q, zero_k, v, heads, kvh, 5)
+    assert np.allclose(o[0, 0], v[0, :5].mean(0)) and np.allclose(o[0, 3], v[1, :5].mean(0))
+    assert np.allclose(at(q, rng.standard_normal((kvh, ms, hd)), v, heads, kvh, 1)[0, 2], v[1, 0])
+    assert np.allclose(at(q, rng.standard_normal((kvh, ms, hd)), v, heads, kvh, 7, window=1)[0, 1], v[0, 6])
+    k = np.zeros((kvh, ms, hd))
+    qq = np.zeros((1, heads, hd))
+    qq[0, :, 0] = 1.0
+    k[:, 1, 0] = np.log(3.0) * np.sqrt(hd)  # position 1 scores ln 3 above position 0
+    assert np.allclose(at(qq, k, v, heads, kvh, 2)[0, 0], 0.25 * v[0, 0] + 0.75 * v[0, 1])
+    # token t of a causal block sees one position more than token t - 1; bidirectional tokens all see the block
+    q3 = rng.standard_normal((3, heads, hd))
+    kk = rng.standard_normal((kvh, ms, hd))
+    c = at(q3, kk, v, heads, kvh, 4)
+    assert np.allclose(c[2], at(q3[2:], kk, v, heads, kvh, 6)[0])
+    b = at(q3, kk, v, heads, kvh, 4, bidirectional=True)
+    assert np.allclose(b[0], at(q3[:1], kk, v, heads, kvh, 6)[0]) and np.allclose(b[2], c[2])

@@ -105,6 +105,95 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float *__restrict_
     kv_put(vc, dst, v[i]);
 }
 
+// GQA attention of query token t, head h (workgroup (h, t), 4 waves): positions [start, end) with end =
+// seq_len0 + t (causal) or seq_len0 + ntok - 1 (bidirectional), start = end_q - window when a window is set
+// (end_q = seq_len0 + t). Wave w takes the 64-position chunks w, w + 4, ...: lane = position for q . k, an
+// online softmax (running max m, sum l, output acc rescaled by e^(m_old - m_new)), lane = output dims for the
+// V sum; the four waves' (m, l, acc) are merged in wave order. Caches [kv_head][max_seq][hd], fp32 or fp16.
+constexpr int kAttnWaves = 4, kAttnMaxHd = 256;
+__device__ __forceinline__ float kv_get(const float *c, size_t i) { return c[i]; }
+__device__ __forceinline__ float kv_get(const _Float16 *c, size_t i) { return static_cast<float>(c[i]); }
+template <typename C>
+__global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(const float *__restrict__ q, const C *__restrict__ kc,
+                                                                    const C *__restrict__ vc, float *__restrict__ out,
+                                                                    int heads, int kv_heads, int hd, int max_seq,
+                                                                    int seq_len0, int bidirectional, int window) {
+    __shared__ float sq[kAttnMaxHd];
+    __shared__ float sp[kAttnWaves][64];
+    __shared__ float sm[kAttnWaves], sl[kAttnWaves];
+    __shared__ float sacc[kAttnWaves][kAttnMaxHd];
+    const int h = blockIdx.x, t = blockIdx.y, ntok = gridDim.y;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int qend = seq_len0 + t;
+    const int end = bidirectional ? seq_len0 + ntok - 1 : qend;
+    const int start = window > 0 && qend > window ? qend - window : 0;
+    const int kvh = h / (heads / kv_heads);
+    const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+    const float *qh = q + (static_cast<size_t>(t) * heads + h) * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) sq[d] = qh[d];
+    __syncthreads();
+    const size_t hbase = static_cast<size_t>(kvh) * max_seq;
+    float m = -INFINITY, l = 0.0f;
+    float acc[kAttnMaxHd / 64];
+#pragma unroll
+    for (int r = 0; r < kAttnMaxHd / 64; ++r) acc[r] = 0.0f;
+    for (int p0 = start + 64 * wv; p0 < end; p0 += 64 * kAttnWaves) {
+        const int p = p0 + lane;
+        float sc = -INFINITY;
+        if (p < end) {
+            const size_t row = (hbase + p) * hd;
+            float dot = 0.0f;
+            for (int d = 0; d < hd; ++d) dot = fmaf(sq[d], kv_get(kc, row + d), dot);
+            sc = dot * scale;
+        }
+        float cm = sc;
+        for (int o = 32; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o, 64));
+        const float mn = fmaxf(m, cm);
+        const float pr = p < end ? expf(sc - mn) : 0.0f;
+        float ps = pr;
+        for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o, 64);
+        const float rs = expf(m - mn);  // 0 on the first chunk (m = -inf)
+        l = l * rs + ps;
+        m = mn;
+        sp[wv][lane] = pr;
+        __builtin_amdgcn_wave_barrier();
+        const int np = end - p0 < 64 ? end - p0 : 64;
+#pragma unroll
+        for (int r = 0; r < kAttnMaxHd / 64; ++r) {
+            const int d = lane + 64 * r;
+            if (d < hd) {
+                float a = acc[r] * rs;
+                for (int j = 0; j < np; ++j) a = fmaf(sp[wv][j], kv_get(vc, (hbase + p0 + j) * hd + d), a);
+                acc[r] = a;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (lane == 0) {
+        sm[wv] = m;
+        sl[wv] = l;
+    }
+#pragma unroll
+    for (int r = 0; r < kAttnMaxHd / 64; ++r)
+        if (lane + 64 * r < hd) sacc[wv][lane + 64 * r] = acc[r];
+    __syncthreads();
+    if (wv == 0) {
+        float M = -INFINITY;
+        for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, sm[w]);
+        float L = 0.0f, f[kAttnWaves];
+        for (int w = 0; w < kAttnWaves; ++w) {
+            f[w] = sm[w] == -INFINITY ? 0.0f : expf(sm[w] - M);
+            L += sl[w] * f[w];
+        }
+        float *o = out + (static_cast<size_t>(t) * heads + h) * hd;
+        for (int d = lane; d < hd; d += 64) {
+            float a = 0.0f;
+            for (int w = 0; w < kAttnWaves; ++w) a += sacc[w][d] * f[w];
+            o[d] = a / L;
+        }
+    }
+}
+
 int status_of(hipError_t e) { return e == hipSuccess ? VQ_OK : static_cast<int>(e); }
 
 }  // namespace
@@ -163,6 +252,25 @@ int vq_kv_append(const float *k, const float *v, void *kc, void *vc, int elem, i
     else
         kv_append_kernel<float><<<blocks, 256, 0, s>>>(k, v, static_cast<float *>(kc), static_cast<float *>(vc), ntok,
                                                        kv_heads, max_seq, hd, pos0);
+    return status_of(hipGetLastError());
+}
+
+int vq_attention(const float *q, const void *kc, const void *vc, float *out, int elem, int heads, int kv_heads, int hd,
+                 int max_seq, int seq_len, int ntok, int bidirectional, int window, void *stream) {
+    if (!q || !kc || !vc || !out || (elem != 2 && elem != 4)) return VQ_ERR_ARG;
+    if (kv_heads < 1 || heads < kv_heads || heads % kv_heads || hd < 1 || hd > kAttnMaxHd || ntok < 1 ||
+        seq_len < 1 || seq_len + ntok - 1 > max_seq || window < 0)
+        return VQ_ERR_SHAPE;
+    const dim3 grid(heads, ntok);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (elem == 2)
+        attention_kernel<_Float16><<<grid, 64 * kAttnWaves, 0, s>>>(q, static_cast<const _Float16 *>(kc),
+                                                                    static_cast<const _Float16 *>(vc), out, heads,
+                                                                    kv_heads, hd, max_seq, seq_len, bidirectional, window);
+    else
+        attention_kernel<float><<<grid, 64 * kAttnWaves, 0, s>>>(q, static_cast<const float *>(kc),
+                                                                 static_cast<const float *>(vc), out, heads, kv_heads,
+                                                                 hd, max_seq, seq_len, bidirectional, window);
     return status_of(hipGetLastError());
 }
 

@@ -375,6 +375,28 @@ class Runtime:
         _lib.check(self._lib.vq_kv_append(kb.data_ptr(), vb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(),
                                           kcb.elem, ntok, kv_heads, max_seq, hd, pos, self._stream()), "kv_append")
 
+    def attention(self, q: str, kc: str, vc: str, out: str, heads: int, kv_heads: int, hd: int, max_seq: int,
+                  seq_len: int, ntok: int = 1, bidirectional: int = 0, window: int = 0) -> None:
+        """GQA attention of ntok query tokens over contiguous KV caches (Runtime_attention, qwen_runtime.cu:
+        128-162); token t sees seq_len + t positions (causal) or seq_len + ntok - 1 (bidirectional), the last
+        `window` of them when window > 0."""
+        if kv_heads <= 0 or heads % kv_heads != 0:
+            raise ValueError("heads must be divisible by kv_heads")
+        if ntok < 1 or seq_len <= 0 or seq_len + ntok - 1 > max_seq:
+            raise ValueError(f"invalid seq_len {seq_len} for {ntok} tokens")
+        n, cache = heads * hd * ntok, kv_heads * hd * max_seq
+        qb = self._f32_buffer(q, n)
+        kcb, vcb = self._any_buffer(kc), self._any_buffer(vc)
+        for name, b in ((kc, kcb), (vc, vcb)):
+            if b.data.numel() < cache:
+                raise ValueError(f"device buffer {name} has {b.data.numel()} values, need {cache}")
+        ob = self._f32_buffer(out, n)
+        if kcb.elem != vcb.elem:
+            raise TypeError("K and V caches differ in precision")
+        _lib.check(self._lib.vq_attention(qb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(), ob.data_ptr(),
+                                          kcb.elem, heads, kv_heads, hd, max_seq, seq_len, ntok, int(bidirectional),
+                                          int(window), self._stream()), "attention")
+
     def copy(self, dst: str, dst_off: int, src: str, src_off: int, n: int) -> None:
         """dst[dst_off:+n] = src[src_off:+n] in elements, buffers of one precision (Runtime_copy,
         qwen_runtime.cu:2200-2218); asynchronous on the current stream."""
