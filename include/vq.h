@@ -144,6 +144,13 @@ int vq_kv_append(const float *k, const float *v, void *kc, void *vc, int elem, i
 int vq_attention(const float *q, const void *kc, const void *vc, float *out, int elem, int heads, int kv_heads, int hd,
                  int max_seq, int seq_len, int ntok, int bidirectional, int window, void *stream);
 
+/* Causal depthwise conv + SiLU over ntok tokens: per channel the state [channels][K] (K <= 8) holds the last K
+ * inputs; per token it shifts, appends x[t][c], and out[t][c] = silu(state . w[c]). snap (may be NULL):
+ * [ntok - 1][channels][K] states after each token but the last. Replaces: Runtime.conv_update
+ * (qwen_runtime.cu:401-426, 2032-2050). */
+int vq_conv_update(const float *x, float *state, const float *w, float *out, int channels, int K, int ntok, float *snap,
+                   void *stream);
+
 /* Activation staging flags of vq_qmv_staged: the bits of the reference megakernel's QMV flags
  * (runtime/instructions.py:179-182; QMV_FLAG_ARGMAX = 4 is vq_lmhead_argmax here). */
 #define VQ_QMV_ADD 1      /* y[t][r] += (W v)[r] instead of =                                      */

@@ -10,6 +10,7 @@ Functions mirror the reference CPU path (/root/reference/engine/csrc/cpu/qwen_cp
   stage_x        the megakernel's QMV activation staging (qwen_megakernel.cu:485-551), float64 numpy
   rope_neox      NeoX partial RoPE (rope_neox_kernel, qwen_runtime.cu:81-92), float64 numpy
   attention      GQA attention with causal / bidirectional / window visibility (qwen_runtime.cu:128-162)
+  conv_update    causal depthwise conv + SiLU state stepping (conv_update_kernel, qwen_runtime.cu:401-426)
 """
 from __future__ import annotations
 
@@ -181,3 +182,18 @@ def attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, heads: int, kv_head
             p = np.exp(s - s.max())
             out[t, h] = (p / p.sum()) @ v
     return out
+
+
+def conv_update(x: np.ndarray, state: np.ndarray, w: np.ndarray):
+    """float64 conv_update_kernel (qwen_runtime.cu:401-426): x [ntok][channels], state and w [channels][K].
+    Returns (out [ntok][channels], final state, snapshots [ntok - 1][channels][K])."""
+    st = np.array(state, np.float64)
+    w = np.asarray(w, np.float64)
+    outs, snaps = [], []
+    for t, xt in enumerate(np.asarray(x, np.float64)):
+        st = np.concatenate([st[:, 1:], xt[:, None]], axis=1)
+        a = (st * w).sum(axis=1)
+        outs.append(a / (1.0 + np.exp(-a)))
+        if t < len(x) - 1:
+            snaps.append(st.copy())
+    return np.array(outs), st, np.array(snaps).reshape(-1, *st.shape)

@@ -399,3 +399,29 @@ def test_attention_matches_oracle(rt, oracle_mod, elem, ntok, seq_len, bidirecti
         rt.attention("aq", "akc", "avc", "ao", heads, 3, hd, max_seq, seq_len, ntok)
     with pytest.raises(ValueError):
         rt.attention("aq", "akc", "avc", "ao", heads, kvh, hd, max_seq, max_seq, 2)
+
+
+def test_conv_update_matches_oracle(rt, oracle_mod):
+    """conv_update (qwen_runtime.cu:401-426): outputs, final state and per-token snapshots vs the float64
+    restatement; K = 4 over 3 tokens, then one more token continuing from the updated state."""
+    rng = np.random.default_rng(99)
+    ch, K, ntok = 300, 4, 3
+    x = rng.standard_normal((ntok + 1, ch)).astype(np.float32)
+    s0 = rng.standard_normal((ch, K)).astype(np.float32)
+    w = (rng.standard_normal((ch, K)) * 0.5).astype(np.float32)
+    rt.upload_raw("cw", w.tobytes(), T.F32, K, ch)
+    for name, a in (("cx", x[:ntok]), ("cs", s0), ("co", np.zeros((ntok, ch))), ("csn", np.zeros((ntok - 1, ch, K))),
+                    ("cx1", x[ntok:])):
+        rt.alloc(name, a.size)
+        rt.write_floats(name, np.asarray(a, np.float32).reshape(-1).tolist())
+    rt.conv_update("cx", "cs", "cw", "co", ch, K, ntok, "csn")
+    out, st, snaps = oracle_mod.conv_update(x[:ntok], s0, w)
+    assert np.allclose(np.array(rt.read_floats("co")).reshape(ntok, ch), out, rtol=1e-5, atol=1e-6)
+    assert np.allclose(np.array(rt.read_floats("cs")).reshape(ch, K), st, rtol=0, atol=0)
+    assert np.allclose(np.array(rt.read_floats("csn")).reshape(ntok - 1, ch, K), snaps, rtol=0, atol=0)
+    rt.conv_update("cx1", "cs", "cw", "co", ch, K, 1)
+    out2, _, _ = oracle_mod.conv_update(x[ntok:], st, w)
+    assert np.allclose(np.array(rt.read_floats("co"))[:ch], out2[0], rtol=1e-5, atol=1e-6)
+    with pytest.raises(ValueError):
+        rt.conv_update("cx", "cs", "cw", "co", ch, K, 0)
+    rt.free("cw")

@@ -315,3 +315,25 @@ def test_attention_is_pinned_by_closed_forms(oracle_mod):
     assert np.allclose(c[2], at(q3[2:], kk, v, heads, kvh, 6)[0])
     b = at(q3, kk, v, heads, kvh, 4, bidirectional=True)
     assert np.allclose(b[0], at(q3[:1], kk, v, heads, kvh, 6)[0]) and np.allclose(b[2], c[2])
+
+
+def test_conv_update_is_pinned_by_closed_forms(oracle_mod):
+    """conv_update: a last-tap-only filter gives silu(x_t); after K tokens the state is exactly the last K
+    inputs; all-ones weights give silu(sum of the last K inputs, the old state filling the start)."""
+    from scipy.special import expit
+
+    cu = oracle_mod.conv_update
+    rng = np.random.default_rng(64)
+    ch, K, ntok = 5, 4, 6
+    x = rng.standard_normal((ntok, ch))
+    s0 = rng.standard_normal((ch, K))
+    w = np.zeros((ch, K))
+    w[:, -1] = 1.0
+    out, st, snaps = cu(x, s0, w)
+    assert np.allclose(out, x * expit(x), rtol=1e-14)
+    assert np.array_equal(st, x[-K:].T) and snaps.shape == (ntok - 1, ch, K)
+    assert np.array_equal(snaps[0], np.concatenate([s0[:, 1:], x[:1].T], axis=1))
+    out1, _, _ = cu(x, s0, np.ones((ch, K)))
+    seq = np.concatenate([s0.T, x])  # [K + ntok][ch]
+    want = np.array([seq[t + 1:t + 1 + K].sum(0) for t in range(ntok)])
+    assert np.allclose(out1, want * expit(want), rtol=1e-13)

@@ -194,6 +194,39 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(const float 
     }
 }
 
+// Causal depthwise conv + SiLU through ntok tokens, one thread per channel: the state row [K] holds the last K
+// inputs; per token it shifts left, takes x, and out = silu(state . w). snap (optional) receives the state
+// after each token but the last, [ntok - 1][channel][K]; the state keeps the final one.
+constexpr int kConvMaxK = 8;
+__global__ __launch_bounds__(256) void conv_update_kernel(const float *__restrict__ x, float *__restrict__ state,
+                                                          const float *__restrict__ w, float *__restrict__ out,
+                                                          int channels, int K, int ntok, float *__restrict__ snap) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= channels) return;
+    float st[kConvMaxK], wc[kConvMaxK];
+#pragma unroll
+    for (int k = 0; k < kConvMaxK; ++k) {
+        st[k] = k < K ? state[static_cast<size_t>(c) * K + k] : 0.0f;
+        wc[k] = k < K ? w[static_cast<size_t>(c) * K + k] : 0.0f;
+    }
+    for (int t = 0; t < ntok; ++t) {
+#pragma unroll
+        for (int k = 0; k < kConvMaxK - 1; ++k)
+            if (k < K - 1) st[k] = st[k + 1];
+        const float xi = x[static_cast<size_t>(t) * channels + c];
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kConvMaxK; ++k) {
+            if (k == K - 1) st[k] = xi;
+            if (k < K) acc = fmaf(st[k], wc[k], acc);
+        }
+        out[static_cast<size_t>(t) * channels + c] = silu_ieee(acc);
+        if (snap != nullptr && t < ntok - 1)
+            for (int k = 0; k < K; ++k) snap[(static_cast<size_t>(t) * channels + c) * K + k] = st[k];
+    }
+    for (int k = 0; k < K; ++k) state[static_cast<size_t>(c) * K + k] = st[k];
+}
+
 int status_of(hipError_t e) { return e == hipSuccess ? VQ_OK : static_cast<int>(e); }
 
 }  // namespace
@@ -271,6 +304,15 @@ int vq_attention(const float *q, const void *kc, const void *vc, float *out, int
         attention_kernel<float><<<grid, 64 * kAttnWaves, 0, s>>>(q, static_cast<const float *>(kc),
                                                                  static_cast<const float *>(vc), out, heads, kv_heads,
                                                                  hd, max_seq, seq_len, bidirectional, window);
+    return status_of(hipGetLastError());
+}
+
+int vq_conv_update(const float *x, float *state, const float *w, float *out, int channels, int K, int ntok, float *snap,
+                   void *stream) {
+    if (!x || !state || !w || !out) return VQ_ERR_ARG;
+    if (channels < 1 || K < 1 || K > kConvMaxK || ntok < 1) return VQ_ERR_SHAPE;
+    conv_update_kernel<<<static_cast<unsigned>((channels + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        x, state, w, out, channels, K, ntok, snap);
     return status_of(hipGetLastError());
 }
 

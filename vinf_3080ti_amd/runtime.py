@@ -397,6 +397,22 @@ class Runtime:
                                           kcb.elem, heads, kv_heads, hd, max_seq, seq_len, ntok, int(bidirectional),
                                           int(window), self._stream()), "attention")
 
+    def conv_update(self, x: str, state: str, w: str, out: str, channels: int, K: int, ntok: int = 1,
+                    snap: str | None = None) -> None:
+        """Causal depthwise conv + SiLU stepping through ntok tokens, state [channels][K] updated in place, w an
+        F32 tensor [channels][K] (Runtime_conv_update, qwen_runtime.cu:401-426)."""
+        if ntok < 1:
+            raise ValueError("ntok must be positive")
+        xb = self._f32_buffer(x, channels * ntok)
+        sb = self._f32_buffer(state, channels * K)
+        ob = self._f32_buffer(out, channels * ntok)
+        wt = self._f32_weight(w, channels * K)
+        snp = self._f32_buffer(snap, channels * K * (ntok - 1)).data_ptr() if snap is not None else None
+        if K > 8:
+            raise ValueError(f"conv kernel size {K} > 8")
+        _lib.check(self._lib.vq_conv_update(xb.data_ptr(), sb.data_ptr(), wt.data_ptr(), ob.data_ptr(), channels, K,
+                                            ntok, snp, self._stream()), "conv_update")
+
     def copy(self, dst: str, dst_off: int, src: str, src_off: int, n: int) -> None:
         """dst[dst_off:+n] = src[src_off:+n] in elements, buffers of one precision (Runtime_copy,
         qwen_runtime.cu:2200-2218); asynchronous on the current stream."""
