@@ -151,6 +151,14 @@ int vq_attention(const float *q, const void *kc, const void *vc, float *out, int
 int vq_conv_update(const float *x, float *state, const float *w, float *out, int channels, int K, int ntok, float *snap,
                    void *stream);
 
+/* Gated delta rule over ntok tokens, state [value_heads][kd][vd] fp32 updated in place (kd <= 256): conv rows
+ * [q (key_heads*kd) | k (key_heads*kd) | v (value_heads*vd)], b / a [ntok][value_heads] raw beta / alpha,
+ * ssm_a / dt [value_heads]; head_order 0: key head h / (vh / kh), 1: h % kh. out [ntok][value_heads][vd];
+ * snap (may be NULL) [ntok - 1][vh][kd][vd]. Replaces: Runtime.gated_delta (qwen_runtime.cu:515-567, 2052-2080). */
+int vq_gated_delta(const float *conv, const float *b, const float *a, const float *ssm_a, const float *dt, float *state,
+                   float *out, int key_heads, int value_heads, int kd, int vd, float eps, int head_order, int ntok,
+                   float *snap, void *stream);
+
 /* Activation staging flags of vq_qmv_staged: the bits of the reference megakernel's QMV flags
  * (runtime/instructions.py:179-182; QMV_FLAG_ARGMAX = 4 is vq_lmhead_argmax here). */
 #define VQ_QMV_ADD 1      /* y[t][r] += (W v)[r] instead of =                                      */

@@ -11,6 +11,7 @@ Functions mirror the reference CPU path (/root/reference/engine/csrc/cpu/qwen_cp
   rope_neox      NeoX partial RoPE (rope_neox_kernel, qwen_runtime.cu:81-92), float64 numpy
   attention      GQA attention with causal / bidirectional / window visibility (qwen_runtime.cu:128-162)
   conv_update    causal depthwise conv + SiLU state stepping (conv_update_kernel, qwen_runtime.cu:401-426)
+  gated_delta    gated delta rule state stepping (gated_delta_kernel, qwen_runtime.cu:515-567)
 """
 from __future__ import annotations
 
@@ -197,3 +198,32 @@ def conv_update(x: np.ndarray, state: np.ndarray, w: np.ndarray):
         if t < len(x) - 1:
             snaps.append(st.copy())
     return np.array(outs), st, np.array(snaps).reshape(-1, *st.shape)
+
+
+def gated_delta(conv, b, a, ssm_a, dt, state, key_heads: int, value_heads: int, kd: int, vd: int, eps: float,
+                head_order: int):
+    """float64 gated_delta_kernel (qwen_runtime.cu:515-567). conv [ntok][2 kh kd + vh vd], b / a [ntok][vh],
+    ssm_a / dt [vh], state [vh][kd][vd]. Returns (out [ntok][vh][vd], final state, snapshots [ntok - 1])."""
+    S = np.array(state, np.float64).reshape(value_heads, kd, vd)
+    conv = np.asarray(conv, np.float64)
+    outs, snaps = [], []
+    for t in range(conv.shape[0]):
+        o = np.zeros((value_heads, vd))
+        for h in range(value_heads):
+            kh = h // (value_heads // key_heads) if head_order == 0 else h % key_heads
+            q = conv[t, kh * kd:(kh + 1) * kd]
+            k = conv[t, (key_heads + kh) * kd:(key_heads + kh + 1) * kd]
+            v = conv[t, 2 * key_heads * kd + h * vd:2 * key_heads * kd + (h + 1) * vd]
+            qh = q / (np.sqrt(q @ q + eps) * np.sqrt(kd))
+            kh_ = k / np.sqrt(k @ k + eps)
+            beta = 1.0 / (1.0 + np.exp(-float(b[t][h])))
+            xa = float(a[t][h]) + float(dt[h])
+            sp = xa if xa > 20.0 else np.log1p(np.exp(xa))
+            S[h] *= np.exp(float(ssm_a[h]) * sp)
+            delta = (v - kh_ @ S[h]) * beta
+            S[h] += np.outer(kh_, delta)
+            o[h] = qh @ S[h]
+        outs.append(o)
+        if t < conv.shape[0] - 1:
+            snaps.append(S.copy())
+    return np.array(outs), S, np.array(snaps).reshape(-1, value_heads, kd, vd)

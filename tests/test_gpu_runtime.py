@@ -425,3 +425,33 @@ def test_conv_update_matches_oracle(rt, oracle_mod):
     with pytest.raises(ValueError):
         rt.conv_update("cx", "cs", "cw", "co", ch, K, 0)
     rt.free("cw")
+
+
+@pytest.mark.parametrize("head_order", [0, 1])
+def test_gated_delta_matches_oracle(rt, oracle_mod, head_order):
+    """gated_delta (qwen_runtime.cu:515-567): 3 tokens, 2 key heads over 4 value heads, kd 128, vd 96;
+    outputs, final state and snapshots vs the float64 restatement."""
+    rng = np.random.default_rng(101 + head_order)
+    kh, vh, kd, vd, ntok = 2, 4, 128, 96, 3
+    cdim = 2 * kh * kd + vh * vd
+    conv = rng.standard_normal((ntok, cdim)).astype(np.float32)
+    b = rng.standard_normal((ntok, vh)).astype(np.float32)
+    a = rng.standard_normal((ntok, vh)).astype(np.float32)
+    ssm_a = -rng.uniform(0.1, 2.0, vh).astype(np.float32)
+    dt = rng.standard_normal(vh).astype(np.float32)
+    s0 = (rng.standard_normal((vh, kd, vd)) * 0.1).astype(np.float32)
+    rt.upload_raw("gda", ssm_a.tobytes(), T.F32, vh, 1)
+    rt.upload_raw("gdt", dt.tobytes(), T.F32, vh, 1)
+    for name, arr in (("gc", conv), ("gb", b), ("ga", a), ("gs", s0), ("go", np.zeros((ntok, vh, vd))),
+                      ("gsn", np.zeros((ntok - 1, vh, kd, vd)))):
+        rt.alloc(name, arr.size)
+        rt.write_floats(name, np.asarray(arr, np.float32).reshape(-1).tolist())
+    rt.gated_delta("gc", "gb", "ga", "gda", "gdt", "gs", "go", kh, vh, kd, vd, 1e-6, head_order, ntok, "gsn")
+    out, S, snaps = oracle_mod.gated_delta(conv, b, a, ssm_a, dt, s0, kh, vh, kd, vd, 1e-6, head_order)
+    assert np.allclose(np.array(rt.read_floats("go")).reshape(ntok, vh, vd), out, rtol=1e-4, atol=2e-5)
+    assert np.allclose(np.array(rt.read_floats("gs")).reshape(vh, kd, vd), S, rtol=1e-4, atol=2e-5)
+    assert np.allclose(np.array(rt.read_floats("gsn")).reshape(ntok - 1, vh, kd, vd), snaps, rtol=1e-4, atol=2e-5)
+    with pytest.raises(ValueError):
+        rt.gated_delta("gc", "gb", "ga", "gda", "gdt", "gs", "go", 3, vh, kd, vd, 1e-6, head_order, ntok)
+    rt.free("gda")
+    rt.free("gdt")

@@ -337,3 +337,32 @@ def test_conv_update_is_pinned_by_closed_forms(oracle_mod):
     seq = np.concatenate([s0.T, x])  # [K + ntok][ch]
     want = np.array([seq[t + 1:t + 1 + K].sum(0) for t in range(ntok)])
     assert np.allclose(out1, want * expit(want), rtol=1e-13)
+
+
+def test_gated_delta_is_pinned_by_delta_rule_properties(oracle_mod):
+    """gated_delta: with no decay (ssm_a = 0) and beta -> 1, writing k -> v into an empty state and reading
+    with q = k returns v / sqrt(kd) (eps = 0); a second write of the same k overwrites v (delta rule, not a
+    sum); beta -> 0 leaves the state decayed only; head_order picks grouped or tiled key heads."""
+    gd = oracle_mod.gated_delta
+    rng = np.random.default_rng(65)
+    kh, vh, kd, vd = 1, 2, 8, 4
+    k = rng.standard_normal(kd)
+    v1, v2 = rng.standard_normal(vh * vd), rng.standard_normal(vh * vd)
+    conv = np.stack([np.concatenate([k, k, v1]), np.concatenate([k, k, v2])])
+    big = np.full((2, vh), 60.0)
+    z = np.zeros(vh)
+    out, S, snaps = gd(conv, big, np.full((2, vh), -40.0), z, z, np.zeros((vh, kd, vd)), kh, vh, kd, vd, 0.0, 0)
+    assert np.allclose(out[0], v1.reshape(vh, vd) / np.sqrt(kd), rtol=1e-12)
+    assert np.allclose(out[1], v2.reshape(vh, vd) / np.sqrt(kd), rtol=1e-12)
+    assert np.allclose(snaps[0], np.einsum("i,hj->hij", k / np.linalg.norm(k), v1.reshape(vh, vd)), rtol=1e-12)
+    s0 = rng.standard_normal((vh, kd, vd))
+    ssm = np.array([-1.0, -0.5])
+    _, S2, _ = gd(conv[:1], np.full((1, vh), -60.0), np.zeros((1, vh)), ssm, z, s0, kh, vh, kd, vd, 1e-6, 0)
+    assert np.allclose(S2, s0 * np.exp(ssm * np.log(2.0))[:, None, None], rtol=1e-12)  # softplus(0) = ln 2
+    kh2 = 2
+    conv2 = rng.standard_normal((1, 2 * kh2 * kd + 4 * vd))
+    o_g, _, _ = gd(conv2, big[:1, :1].repeat(4, 1), np.zeros((1, 4)), np.zeros(4), np.zeros(4), np.zeros((4, kd, vd)),
+                   kh2, 4, kd, vd, 1e-6, 0)
+    o_t, _, _ = gd(conv2, big[:1, :1].repeat(4, 1), np.zeros((1, 4)), np.zeros(4), np.zeros(4), np.zeros((4, kd, vd)),
+                   kh2, 4, kd, vd, 1e-6, 1)
+    assert np.allclose(o_g[0, 0], o_t[0, 0]) and not np.allclose(o_g[0, 1], o_t[0, 1])  # head 1: key 0 vs key 1

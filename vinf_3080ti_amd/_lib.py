@@ -34,6 +34,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_kv_append": (I, [P, P, P, P, I, I, I, I, I, I, P]),
     "vq_attention": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, P]),
     "vq_conv_update": (I, [P, P, P, P, I, I, I, P, P]),
+    "vq_gated_delta": (I, [P, P, P, P, P, P, P, I, I, I, I, F, I, I, P, P]),
     "vq_quantize_x": (I, [P, I, I, P, P, P, P]),
     "vq_pack_x": (I, [P, I, I, P, P]),
     "vq_qmv_packed": (I, [I, P, I, I, P, I, P, P]),

@@ -1,6 +1,6 @@
 // vq_ops.hip -- the runtime's elementwise, normalisation and layout ops around the matvec (the reference
-// runtime's rmsnorm, gated_rmsnorm, add / silu_mul / sigmoid_mul, split_gated_q, NeoX rope and kv_append
-// kernels, qwen_runtime.cu:36-128): HBM-bound streams in fp32 (fp16 KV caches).
+// runtime's rmsnorm, gated_rmsnorm, add / silu_mul / sigmoid_mul, split_gated_q, NeoX rope, kv_append,
+// attention, conv_update and gated-delta kernels, qwen_runtime.cu:36-567): fp32, fp16 KV caches allowed.
 //
 // RMS sums: each thread adds its strided elements in order, then a fixed pairwise tree over the 256 threads in
 // LDS, so a group's result does not depend on timing. silu / sigmoid use expf and an IEEE division (these
@@ -227,6 +227,77 @@ __global__ __launch_bounds__(256) void conv_update_kernel(const float *__restric
     for (int k = 0; k < K; ++k) state[static_cast<size_t>(c) * K + k] = st[k];
 }
 
+// Gated delta rule through ntok tokens, one workgroup per value head h (state S [kd][vd] of that head): conv
+// rows are [q (key_heads kd) | k (key_heads kd) | v (value_heads vd)]; key head kh = h / (vh / kh) (head_order
+// 0) or h % kh (1). Per token: q^ = q / (sqrt(|q|^2 + eps) sqrt(kd)), k^ = k / sqrt(|k|^2 + eps) (sums in a fixed
+// tree), beta = sigmoid(b), decay = exp(ssm_a softplus(a + dt)); S *= decay; delta = (v - S^T k^) beta;
+// S += k^ delta^T; out = S^T q^. Thread j owns state columns j, j + 256, ...; snap: states after each token
+// but the last, [ntok - 1][vh][kd][vd].
+constexpr int kGdMaxKd = 256;
+__global__ __launch_bounds__(256) void gated_delta_kernel(const float *__restrict__ conv, const float *__restrict__ braw,
+                                                          const float *__restrict__ araw, const float *__restrict__ ssm_a,
+                                                          const float *__restrict__ dt, float *__restrict__ S,
+                                                          float *__restrict__ out, int key_heads, int value_heads,
+                                                          int kd, int vd, float eps, int head_order, int ntok,
+                                                          float *__restrict__ snap) {
+    __shared__ float sq[kGdMaxKd], sk[kGdMaxKd], red[2][256];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int kh = head_order == 0 ? h / (value_heads / key_heads) : h % key_heads;
+    const size_t cdim = static_cast<size_t>(2) * key_heads * kd + static_cast<size_t>(value_heads) * vd;
+    float *const Sh = S + static_cast<size_t>(h) * kd * vd;
+    for (int t = 0; t < ntok; ++t) {
+        const float *row = conv + static_cast<size_t>(t) * cdim;
+        const float *qs = row + static_cast<size_t>(kh) * kd, *ks = row + static_cast<size_t>(key_heads + kh) * kd;
+        const float *vs = row + static_cast<size_t>(2) * key_heads * kd + static_cast<size_t>(h) * vd;
+        float aq = 0.0f, ak = 0.0f;
+        for (int i = tid; i < kd; i += 256) {
+            aq = fmaf(qs[i], qs[i], aq);
+            ak = fmaf(ks[i], ks[i], ak);
+        }
+        red[0][tid] = aq;
+        red[1][tid] = ak;
+        for (int w = 128; w > 0; w >>= 1) {
+            __syncthreads();
+            if (tid < w) {
+                red[0][tid] += red[0][tid + w];
+                red[1][tid] += red[1][tid + w];
+            }
+        }
+        __syncthreads();
+        const float qscale = 1.0f / (sqrtf(red[0][0] + eps) * sqrtf(static_cast<float>(kd)));
+        const float kscale = 1.0f / sqrtf(red[1][0] + eps);
+        for (int i = tid; i < kd; i += 256) {
+            sq[i] = qs[i] * qscale;
+            sk[i] = ks[i] * kscale;
+        }
+        __syncthreads();
+        const float beta = sigmoid_ieee(braw[static_cast<size_t>(t) * value_heads + h]);
+        const float xa = araw[static_cast<size_t>(t) * value_heads + h] + dt[h];
+        const float sp = xa > 20.0f ? xa : log1pf(expf(xa));
+        const float decay = expf(ssm_a[h] * sp);
+        float *const sn = snap != nullptr && t < ntok - 1 ? snap + (static_cast<size_t>(t) * value_heads + h) * kd * vd
+                                                          : nullptr;
+        for (int j = tid; j < vd; j += 256) {
+            float mem = 0.0f;
+            for (int i = 0; i < kd; ++i) {
+                const float v = Sh[static_cast<size_t>(i) * vd + j] * decay;
+                Sh[static_cast<size_t>(i) * vd + j] = v;
+                mem = fmaf(v, sk[i], mem);
+            }
+            const float delta = (vs[j] - mem) * beta;
+            float o = 0.0f;
+            for (int i = 0; i < kd; ++i) {
+                const float v = fmaf(sk[i], delta, Sh[static_cast<size_t>(i) * vd + j]);
+                Sh[static_cast<size_t>(i) * vd + j] = v;
+                o = fmaf(v, sq[i], o);
+                if (sn != nullptr) sn[static_cast<size_t>(i) * vd + j] = v;
+            }
+            out[(static_cast<size_t>(t) * value_heads + h) * vd + j] = o;
+        }
+        __syncthreads();  // sq / sk / red are rewritten for the next token
+    }
+}
+
 int status_of(hipError_t e) { return e == hipSuccess ? VQ_OK : static_cast<int>(e); }
 
 }  // namespace
@@ -313,6 +384,18 @@ int vq_conv_update(const float *x, float *state, const float *w, float *out, int
     if (channels < 1 || K < 1 || K > kConvMaxK || ntok < 1) return VQ_ERR_SHAPE;
     conv_update_kernel<<<static_cast<unsigned>((channels + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
         x, state, w, out, channels, K, ntok, snap);
+    return status_of(hipGetLastError());
+}
+
+int vq_gated_delta(const float *conv, const float *b, const float *a, const float *ssm_a, const float *dt, float *state,
+                   float *out, int key_heads, int value_heads, int kd, int vd, float eps, int head_order, int ntok,
+                   float *snap, void *stream) {
+    if (!conv || !b || !a || !ssm_a || !dt || !state || !out) return VQ_ERR_ARG;
+    if (key_heads < 1 || value_heads < key_heads || value_heads % key_heads || kd < 1 || kd > kGdMaxKd || vd < 1 ||
+        ntok < 1 || (head_order != 0 && head_order != 1) || !(eps >= 0.0f))
+        return VQ_ERR_SHAPE;
+    gated_delta_kernel<<<value_heads, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        conv, b, a, ssm_a, dt, state, out, key_heads, value_heads, kd, vd, eps, head_order, ntok, snap);
     return status_of(hipGetLastError());
 }
 

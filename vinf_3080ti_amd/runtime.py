@@ -413,6 +413,26 @@ class Runtime:
         _lib.check(self._lib.vq_conv_update(xb.data_ptr(), sb.data_ptr(), wt.data_ptr(), ob.data_ptr(), channels, K,
                                             ntok, snp, self._stream()), "conv_update")
 
+    def gated_delta(self, conv: str, b: str, a: str, ssm_a: str, dt: str, state: str, out: str, key_heads: int,
+                    value_heads: int, kd: int, vd: int, eps: float, head_order: int, ntok: int = 1,
+                    snap: str | None = None) -> None:
+        """Gated delta rule stepping through ntok tokens, state [vh][kd][vd] in place; ssm_a and dt are F32
+        tensors of value_heads values (Runtime_gated_delta, qwen_runtime.cu:515-567)."""
+        if key_heads <= 0 or value_heads % key_heads != 0:
+            raise ValueError("value heads must be a multiple of key heads")
+        if ntok < 1:
+            raise ValueError("ntok must be positive")
+        conv_dim = 2 * key_heads * kd + value_heads * vd
+        state_n = value_heads * kd * vd
+        cb = self._f32_buffer(conv, conv_dim * ntok)
+        bb, ab = self._f32_buffer(b, value_heads * ntok), self._f32_buffer(a, value_heads * ntok)
+        sb, ob = self._f32_buffer(state, state_n), self._f32_buffer(out, value_heads * vd * ntok)
+        sa, dtt = self._f32_weight(ssm_a, value_heads), self._f32_weight(dt, value_heads)
+        snp = self._f32_buffer(snap, state_n * (ntok - 1)).data_ptr() if snap is not None else None
+        _lib.check(self._lib.vq_gated_delta(cb.data_ptr(), bb.data_ptr(), ab.data_ptr(), sa.data_ptr(), dtt.data_ptr(),
+                                            sb.data_ptr(), ob.data_ptr(), key_heads, value_heads, kd, vd, float(eps),
+                                            int(head_order), ntok, snp, self._stream()), "gated_delta")
+
     def copy(self, dst: str, dst_off: int, src: str, src_off: int, n: int) -> None:
         """dst[dst_off:+n] = src[src_off:+n] in elements, buffers of one precision (Runtime_copy,
         qwen_runtime.cu:2200-2218); asynchronous on the current stream."""
