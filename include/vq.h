@@ -75,7 +75,7 @@ int vq_set_iq3s_grid(const uint8_t *grid);
 /* Bytes of the packed activations (xpack) of `ntok` tokens of `cols` columns; 0 if cols % 32 != 0. */
 size_t vq_xpack_bytes(int cols, int ntok);
 
-/* Workspace bytes vq_qmv needs: 0 for cols <= 8192 (the activations are quantized inside the matvec),
+/* Workspace bytes vq_qmv needs: 0 for cols <= 24576 (the activations are quantized inside the matvec),
  * else vq_xpack_bytes(cols, ntok) (they are packed into the workspace by vq_pack_x first). */
 size_t vq_qmv_workspace_bytes(int cols, int ntok);
 
@@ -126,38 +126,88 @@ int vq_binary(int op, const float *a, const float *b, float *out, long n, void *
  * Runtime.split_gated_q (qwen_runtime.cu:70-76). */
 int vq_split_gated_q(const float *raw, float *q, float *gate, int heads, int hd, void *stream);
 
+/* dst[r] = [a[r] | b[r]] for rows of `width` floats (dst holds rows x 2*width). Replaces: Runtime.concat_rows
+ * (qwen_runtime.cu:2567-2587). */
+int vq_concat_rows(float *dst, const float *a, const float *b, int rows, int width, void *stream);
+
+/* Clear nbytes bytes at p with a fill kernel (no hipMemsetAsync, so the call can be captured in a graph).
+ * Replaces: Runtime.zero_range (qwen_runtime.cu:2589-2600) and Runtime.zero. */
+int vq_zero(void *p, size_t nbytes, void *stream);
+
+/* ---- sequence ops -------------------------------------------------------------------------------------
+ * The multi-sequence (_seg) forms take the pass's segment table as a HOST array segs[nseg][4] of int32
+ * (slot, pos0, rows, row0): segment i is `rows` consecutive positions pos0.. of sequence slot `slot`, stored
+ * in buffer rows row0 .. row0 + rows - 1 (the layout set_segments defines, qwen_runtime.cu:2352-2385).
+ * nseg <= VQ_MAX_SEGMENTS; the table is copied into the launch arguments, so each op is one launch for the
+ * whole pass. Paged KV caches are page pools [page][kv_head][page_size][hd] (fp32 or fp16) with the int32
+ * DEVICE page table page_table[slot * pages_per_seq + pos / page_size] (set_paging, qwen_runtime.cu:100-110,
+ * 2333-2350); every pos0 + rows must fit in page_size * pages_per_seq. */
+#define VQ_MAX_SEGMENTS 64
+#define VQ_CONV_MAX_K 8
+
 /* NeoX RoPE in place on x [ntok][heads][hd], dims [0, rot) of each head, token t at position pos0 + t:
- * (x[j], x[j + rot/2]) turns by (pos0 + t) * base^(-2j/rot). Replaces: Runtime.rope (qwen_runtime.cu:81-92). */
+ * (x[j], x[j + rot/2]) turns by (pos0 + t) * base^(-2j/rot). Replaces: Runtime.rope (qwen_runtime.cu:81-92,
+ * 1966-1977). */
 int vq_rope(float *x, int ntok, int heads, int hd, int rot, int pos0, double base, void *stream);
+
+/* vq_rope with each segment's positions (row row0 + t at position pos0 + t). Replaces: Runtime.rope_seg
+ * (qwen_runtime.cu:2400-2417). */
+int vq_rope_seg(float *x, const int32_t *segs, int nseg, int heads, int hd, int rot, double base, void *stream);
 
 /* k, v [ntok][kv_heads][hd] fp32 into contiguous caches kc, vc [kv_heads][max_seq][hd] of `elem` bytes per
  * value (4: fp32, 2: fp16 rounded to nearest) at positions pos0 .. pos0 + ntok - 1. Replaces:
- * Runtime.kv_append (qwen_runtime.cu:115-128, contiguous caches). */
+ * Runtime.kv_append (qwen_runtime.cu:115-128, 1979-2000, contiguous caches). */
 int vq_kv_append(const float *k, const float *v, void *kc, void *vc, int elem, int ntok, int kv_heads, int max_seq,
                  int hd, int pos0, void *stream);
+
+/* Each segment's k, v rows into its sequence's pages of the paged caches kc, vc. Replaces: Runtime.kv_append_seg
+ * (qwen_runtime.cu:2419-2447). */
+int vq_kv_append_seg(const float *k, const float *v, void *kc, void *vc, int elem, const int32_t *segs, int nseg,
+                     int kv_heads, int hd, const int32_t *page_table, int page_size, int pages_per_seq, void *stream);
 
 /* GQA attention: out[t][h] = softmax(q[t][h] . K / sqrt(hd)) V over the positions query token t sees, with K,
  * V the rows of kv head h / (heads / kv_heads) in caches [kv_heads][max_seq][hd] (`elem` 4: fp32, 2: fp16).
  * Token t sees [start, seq_len + t) (causal) or [start, seq_len + ntok - 1) (bidirectional != 0); start =
  * seq_len + t - window when window > 0 and that is positive, else 0. hd <= 256. Replaces: Runtime.attention
- * (qwen_runtime.cu:128-162, 2000-2030, contiguous caches). */
+ * (qwen_runtime.cu:128-162, 2043-2067, contiguous caches). */
 int vq_attention(const float *q, const void *kc, const void *vc, float *out, int elem, int heads, int kv_heads, int hd,
                  int max_seq, int seq_len, int ntok, int bidirectional, int window, void *stream);
 
-/* Causal depthwise conv + SiLU over ntok tokens: per channel the state [channels][K] (K <= 8) holds the last K
- * inputs; per token it shifts, appends x[t][c], and out[t][c] = silu(state . w[c]). snap (may be NULL):
- * [ntok - 1][channels][K] states after each token but the last. Replaces: Runtime.conv_update
- * (qwen_runtime.cu:401-426, 2032-2050). */
-int vq_conv_update(const float *x, float *state, const float *w, float *out, int channels, int K, int ntok, float *snap,
-                   void *stream);
+/* Causal attention of each segment's rows over its own pages: row t of a segment sees positions
+ * [0, pos0 + t + 1). Replaces: Runtime.attention_seg (qwen_runtime.cu:2449-2478). */
+int vq_attention_seg(const float *q, const void *kc, const void *vc, float *out, int elem, const int32_t *segs,
+                     int nseg, int heads, int kv_heads, int hd, const int32_t *page_table, int page_size,
+                     int pages_per_seq, void *stream);
 
-/* Gated delta rule over ntok tokens, state [value_heads][kd][vd] fp32 updated in place (kd <= 256): conv rows
- * [q (key_heads*kd) | k (key_heads*kd) | v (value_heads*vd)], b / a [ntok][value_heads] raw beta / alpha,
- * ssm_a / dt [value_heads]; head_order 0: key head h / (vh / kh), 1: h % kh. out [ntok][value_heads][vd];
- * snap (may be NULL) [ntok - 1][vh][kd][vd]. Replaces: Runtime.gated_delta (qwen_runtime.cu:515-567, 2052-2080). */
-int vq_gated_delta(const float *conv, const float *b, const float *a, const float *ssm_a, const float *dt, float *state,
-                   float *out, int key_heads, int value_heads, int kd, int vd, float eps, int head_order, int ntok,
-                   float *snap, void *stream);
+/* Causal depthwise conv + SiLU over ntok tokens: per channel the state [channels][K] (K <= VQ_CONV_MAX_K) holds
+ * the last K inputs; per token it shifts, appends x[t][c], and out[t][c] = silu(state . w[c]). snap (may be
+ * NULL): [ntok - 1][channels][K] states after each token but the last. write_state = 0 leaves the state
+ * untouched (a speculative verification pass). Replaces: Runtime.conv_update (qwen_runtime.cu:397-426,
+ * 2081-2100). */
+int vq_conv_update(const float *x, float *state, const float *w, float *out, int channels, int K, int ntok, float *snap,
+                   int write_state, void *stream);
+
+/* vq_conv_update per segment over the slot's state (state [slot][channels][K]); snap needs a single segment.
+ * Replaces: Runtime.conv_update_seg (qwen_runtime.cu:2480-2511). */
+int vq_conv_update_seg(const float *x, float *state, const float *w, float *out, int channels, int K,
+                       const int32_t *segs, int nseg, float *snap, int write_state, void *stream);
+
+/* Gated delta rule over ntok tokens, state [value_heads][kd][vd] of state_elem bytes per value (4: fp32, 2: fp16,
+ * widened to fp32 for the pass and rounded once at its end), kd <= 256: conv rows [q (key_heads*kd) |
+ * k (key_heads*kd) | v (value_heads*vd)], b / a [ntok][value_heads] raw beta / alpha, ssm_a / dt [value_heads];
+ * head_order 0: key head h / (vh / kh), 1: h % kh. out [ntok][value_heads][vd]; snap (fp32 state only, may be
+ * NULL) [ntok - 1][vh][kd][vd]; write_state = 0 leaves the state untouched. Replaces: Runtime.gated_delta
+ * (qwen_runtime.cu:433-567, 2102-2165; fp16 state as its launch_gated_delta_h). */
+int vq_gated_delta(const float *conv, const float *b, const float *a, const float *ssm_a, const float *dt, void *state,
+                   int state_elem, float *out, int key_heads, int value_heads, int kd, int vd, float eps,
+                   int head_order, int ntok, float *snap, int write_state, void *stream);
+
+/* vq_gated_delta per segment over the slot's state ([slot][vh][kd][vd]); snap needs a single segment and fp32
+ * state. Replaces: Runtime.gated_delta_seg (qwen_runtime.cu:2513-2565). */
+int vq_gated_delta_seg(const float *conv, const float *b, const float *a, const float *ssm_a, const float *dt,
+                       void *state, int state_elem, float *out, int key_heads, int value_heads, int kd, int vd,
+                       float eps, int head_order, const int32_t *segs, int nseg, float *snap, int write_state,
+                       void *stream);
 
 /* Activation staging flags of vq_qmv_staged: the bits of the reference megakernel's QMV flags
  * (runtime/instructions.py:179-182; QMV_FLAG_ARGMAX = 4 is vq_lmhead_argmax here). */

@@ -227,3 +227,19 @@ def gated_delta(conv, b, a, ssm_a, dt, state, key_heads: int, value_heads: int, 
         if t < conv.shape[0] - 1:
             snaps.append(S.copy())
     return np.array(outs), S, np.array(snaps).reshape(-1, value_heads, kd, vd)
+
+
+def paged_rows(pt_row, page_size: int, kv_heads: int, kvh: int, positions) -> np.ndarray:
+    """Rows of a paged KV pool [page][kv_head][page_size][hd] (viewed as [page * kv_heads * page_size] rows)
+    that hold kv head kvh at the given positions of a sequence whose page ids are pt_row (KvAddr::row, qwen_runtime.cu:
+    100-110): page pt_row[pos // page_size], slot pos % page_size."""
+    pos = np.asarray(positions, np.int64)
+    pg = np.asarray(pt_row, np.int64)[pos // page_size]
+    return (pg * kv_heads + kvh) * page_size + pos % page_size
+
+
+def gather_paged(pool: np.ndarray, pt_row, page_size: int, kv_heads: int, length: int) -> np.ndarray:
+    """The first `length` positions of one sequence of a paged pool as a contiguous cache [kv_heads][length][hd]."""
+    hd = pool.shape[-1]
+    flat = pool.reshape(-1, hd)
+    return np.stack([flat[paged_rows(pt_row, page_size, kv_heads, h, np.arange(length))] for h in range(kv_heads)])

@@ -366,3 +366,26 @@ def test_gated_delta_is_pinned_by_delta_rule_properties(oracle_mod):
     o_t, _, _ = gd(conv2, big[:1, :1].repeat(4, 1), np.zeros((1, 4)), np.zeros(4), np.zeros(4), np.zeros((4, kd, vd)),
                    kh2, 4, kd, vd, 1e-6, 1)
     assert np.allclose(o_g[0, 0], o_t[0, 0]) and not np.allclose(o_g[0, 1], o_t[0, 1])  # head 1: key 0 vs key 1
+
+
+def test_paged_rows_round_trip():
+    """oracle.paged_rows / gather_paged (KvAddr::row, qwen_runtime.cu:100-110): scattering each position's row of
+    a contiguous cache through a permuted page table and gathering it back is the identity; every row lands in
+    a distinct pool row, on the page the table names, at slot pos % page_size."""
+    from oracle import oracle
+
+    rng = np.random.default_rng(0)
+    page, pps, kvh, hd, length = 4, 5, 3, 2, 18
+    pt = rng.permutation(pps * 2)[:pps]
+    pool = np.full((pps * 2, kvh, page, hd), np.nan)
+    cont = rng.standard_normal((kvh, length, hd))
+    flat = pool.reshape(-1, hd)
+    seen = set()
+    for h in range(kvh):
+        rows = oracle.paged_rows(pt, page, kvh, h, np.arange(length))
+        assert len(set(rows.tolist()) & seen) == 0
+        seen |= set(rows.tolist())
+        flat[rows] = cont[h]
+        for p, r in zip(range(length), rows):
+            assert r // (kvh * page) == pt[p // page] and r % page == p % page and (r // page) % kvh == h
+    assert np.array_equal(oracle.gather_paged(pool, pt, page, kvh, length), cont)

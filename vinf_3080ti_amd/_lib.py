@@ -15,6 +15,9 @@ P, I, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_float
 # Activation staging flags of vq_qmv_staged (include/vq.h).
 VQ_QMV_ADD, VQ_QMV_NORM, VQ_QMV_SILU_MUL = 1, 2, 8
 
+# Sequence ops (include/vq.h).
+VQ_MAX_SEGMENTS, VQ_CONV_MAX_K = 64, 8
+
 # name -> (restype, argtypes); every symbol include/vq.h declares.
 SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_type_traits": (I, [I, ctypes.POINTER(I), ctypes.POINTER(I)]),
@@ -30,11 +33,18 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_rmsnorm": (I, [P, P, P, P, I, I, F, P]),
     "vq_binary": (I, [I, P, P, P, ctypes.c_long, P]),
     "vq_split_gated_q": (I, [P, P, P, I, I, P]),
+    "vq_concat_rows": (I, [P, P, P, I, I, P]),
+    "vq_zero": (I, [P, SZ, P]),
     "vq_rope": (I, [P, I, I, I, I, I, ctypes.c_double, P]),
+    "vq_rope_seg": (I, [P, P, I, I, I, I, ctypes.c_double, P]),
     "vq_kv_append": (I, [P, P, P, P, I, I, I, I, I, I, P]),
+    "vq_kv_append_seg": (I, [P, P, P, P, I, P, I, I, I, P, I, I, P]),
     "vq_attention": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, P]),
-    "vq_conv_update": (I, [P, P, P, P, I, I, I, P, P]),
-    "vq_gated_delta": (I, [P, P, P, P, P, P, P, I, I, I, I, F, I, I, P, P]),
+    "vq_attention_seg": (I, [P, P, P, P, I, P, I, I, I, I, P, I, I, P]),
+    "vq_conv_update": (I, [P, P, P, P, I, I, I, P, I, P]),
+    "vq_conv_update_seg": (I, [P, P, P, P, I, I, P, I, P, I, P]),
+    "vq_gated_delta": (I, [P, P, P, P, P, P, I, P, I, I, I, I, F, I, I, P, I, P]),
+    "vq_gated_delta_seg": (I, [P, P, P, P, P, P, I, P, I, I, I, I, F, I, P, I, P, I, P]),
     "vq_quantize_x": (I, [P, I, I, P, P, P, P]),
     "vq_pack_x": (I, [P, I, I, P, P]),
     "vq_qmv_packed": (I, [I, P, I, I, P, I, P, P]),

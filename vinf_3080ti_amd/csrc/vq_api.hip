@@ -23,15 +23,6 @@
 #include "vq_mfma_impl.h"
 #include "../../include/vq.h"
 
-#ifdef VQ_TIMING
-// Diagnostic builds only: device buffer that the streaming kernels fill with per-wave timestamps.
-static void *g_vq_timing = nullptr;
-extern "C" void *vq_debug_timing_buffer() { return g_vq_timing; }
-extern "C" int vq_debug_set_timing_buffer(void *p) {
-    g_vq_timing = p;
-    return 0;
-}
-#endif
 
 namespace {
 

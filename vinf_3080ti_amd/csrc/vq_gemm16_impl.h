@@ -32,9 +32,6 @@
 #include "vq_qmv.h"
 #include "vq_tables.h"
 
-#ifdef VQ_TIMING
-extern "C" void *vq_debug_timing_buffer();
-#endif
 namespace vq {
 
 template <int T>
@@ -138,12 +135,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
                                                                   float *__restrict__ y, float *__restrict__ part,
                                                                   unsigned long long *tm) {
     using G = G16Geo<T>;
-#ifdef VQ_TIMING
-    const unsigned long long tm0 = __builtin_amdgcn_s_memrealtime();
-    unsigned long long t_wait = 0, t_loop0 = 0;
-#else
     (void)tm;
-#endif
     __shared__ __attribute__((aligned(1024))) uint8_t s_step[kG16Ring][G::STEP_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t s_sb[2][G::SB_BYTES];
 
@@ -159,9 +151,6 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int wr = 64 * (wv & 3), wt = 64 * (wv >> 2);
     const int lr = lane & 15, lk = lane >> 4;
-#ifdef VQ_TIMING
-    int nsteps_all = 0;
-#endif
     // The share's tile segments: tile t, super-blocks [sb0, sb1).
     for (long u = pl.u0(v); u < ue;) {
     const int tile = static_cast<int>(u / nsb);
@@ -170,9 +159,6 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     const int rt = tile / pl.ntt, tt = tile - rt * pl.ntt;
     const int r0 = rt * kG16BM, t0 = tt * kG16BN;
     const int nsteps = (sb1 - sb0) * 4;
-#ifdef VQ_TIMING
-    nsteps_all += nsteps;
-#endif
     const uint8_t *const wbase = w + static_cast<size_t>(r0) * row_bytes;  // wave-uniform
 
     // DMA of step st (j = st % 4 of super-block sb0 + st / 4) into ring slot st % 3 and super-block slot sb & 1.
@@ -317,9 +303,6 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
         }
     }
 
-#ifdef VQ_TIMING
-    const unsigned long long t_loop1 = __builtin_amdgcn_s_memrealtime();
-#endif
     // Output: element q of block (rb, tb) is row r0 + wr + 16 rb + 4 lk + q, token t0 + wt + 16 tb + lr; values
     // leave the 2^e token scale here. A whole tile goes to y (four rows per 16-byte store where rows allow); a
     // part of a tile to its slot, in thread order (coalesced: value i of thread x at [i][x]).
@@ -358,19 +341,6 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     __syncthreads();  // the ring is reused by the next segment's first DMAs
     u += sb1 - sb0;
     }
-#ifdef VQ_TIMING
-    const unsigned long long t_loop1 = tm0;
-    if (tm != nullptr && lane == 0) {
-        const long gw = static_cast<long>(v) * kG16Waves + wv;
-        if (gw < 65536) {
-            unsigned long long *o = tm + 6 * static_cast<size_t>(gw);
-            unsigned xcc;
-            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-            o[0] = tm0; o[1] = t_loop0; o[2] = t_loop1; o[3] = __builtin_amdgcn_s_memrealtime();
-            o[4] = t_wait; o[5] = (static_cast<unsigned long long>(xcc) << 32) | static_cast<unsigned>(nsteps_all);
-        }
-    }
-#endif
 }
 
 // Partial tiles: y = the sum of a tile's slots in slot order. Workgroup (tile, block pair (rb, tb)) of 512
@@ -423,11 +393,7 @@ int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws,
             w, rows, cols, rb, reinterpret_cast<const _Float16 *>(base + l.bh),
             reinterpret_cast<const _Float16 *>(base + l.bl), reinterpret_cast<const _Float16 *>(base + l.xs),
             reinterpret_cast<const float *>(base + l.inv), M, pl, y, part,
-#ifdef VQ_TIMING
-            static_cast<unsigned long long *>(vq_debug_timing_buffer())
-#else
             nullptr
-#endif
         );
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return static_cast<int>(e);

@@ -1,6 +1,12 @@
-// vq_ops.hip -- the runtime's elementwise, normalisation and layout ops around the matvec (the reference
-// runtime's rmsnorm, gated_rmsnorm, add / silu_mul / sigmoid_mul, split_gated_q, NeoX rope, kv_append,
-// attention, conv_update and gated-delta kernels, qwen_runtime.cu:36-567): fp32, fp16 KV caches allowed.
+// vq_ops.hip -- the runtime's sequence ops around the matvec: norms and elementwise passes, the gated query
+// split, NeoX rope, KV append and GQA attention over contiguous or paged caches, the causal conv update and
+// the gated delta rule (the reference runtime's per-op kernels, qwen_runtime.cu:36-567, and its
+// multi-sequence forms, qwen_runtime.cu:2333-2600).
+//
+// One launch per pass. The multi-sequence forms take the pass's segment table by value (each segment is a
+// sequence slot, the position of its first row, its row count and the buffer row it starts at): a block finds
+// its segment from blockIdx, so a pass of many sequences is still one launch. The single-sequence entry points
+// are a one-segment table with contiguous caches.
 //
 // RMS sums: each thread adds its strided elements in order, then a fixed pairwise tree over the 256 threads in
 // LDS, so a group's result does not depend on timing. silu / sigmoid use expf and an IEEE division (these
@@ -12,15 +18,83 @@
 
 namespace {
 
+int status_of(hipError_t e) { return e == hipSuccess ? VQ_OK : static_cast<int>(e); }
+
+// ---- segments and cache addressing ---------------------------------------------------------------------
+
+// A pass's segment table, passed by value in the kernel arguments (1 KB at the maximum).
+struct Seg {
+    int slot, pos0, rows, row0;
+};
+struct SegTable {
+    int n;
+    int total;  // sum of rows (the blocks of a per-row grid)
+    Seg s[VQ_MAX_SEGMENTS];
+};
+
+// Global row index g (segments in table order) -> (segment, row within it).
+__device__ __forceinline__ const Seg &seg_of_row(const SegTable &T, int g, int &local) {
+    int i = 0;
+    while (i + 1 < T.n && g >= T.s[i].rows) {
+        g -= T.s[i].rows;
+        ++i;
+    }
+    local = g;
+    return T.s[i];
+}
+
+// KV cache rows: contiguous [kv_head][max_seq][hd] when pt is null, else a page pool
+// [page][kv_head][page_size][hd] with the sequence slot's page ids at pt[slot * pps + pos / page_size].
+struct KvMap {
+    const int32_t *pt;
+    int max_seq;  // contiguous caches
+    int page, pps, kv_heads;
+    __device__ __forceinline__ size_t row(int slot, int kvh, int pos) const {
+        if (pt == nullptr) return static_cast<size_t>(kvh) * max_seq + pos;
+        const int pg = pt[slot * pps + pos / page];
+        return (static_cast<size_t>(pg) * kv_heads + kvh) * page + pos % page;
+    }
+};
+
+__device__ __forceinline__ float kv_get(const float *c, size_t i) { return c[i]; }
+__device__ __forceinline__ float kv_get(const _Float16 *c, size_t i) { return static_cast<float>(c[i]); }
+
+// Host side: validate a segment table ([n][4] int32: slot, pos0, rows, row0) into a SegTable.
+int make_table(const int32_t *segs, int nseg, SegTable &T, int *rows_spanned) {
+    if (segs == nullptr || nseg < 1 || nseg > VQ_MAX_SEGMENTS) return VQ_ERR_ARG;
+    T.n = nseg;
+    T.total = 0;
+    int span = 0;
+    for (int i = 0; i < nseg; ++i) {
+        const Seg s{segs[4 * i], segs[4 * i + 1], segs[4 * i + 2], segs[4 * i + 3]};
+        if (s.slot < 0 || s.pos0 < 0 || s.rows < 1 || s.row0 < 0) return VQ_ERR_SHAPE;
+        T.s[i] = s;
+        T.total += s.rows;
+        span = s.row0 + s.rows > span ? s.row0 + s.rows : span;
+    }
+    if (rows_spanned) *rows_spanned = span;
+    return VQ_OK;
+}
+
+SegTable one_segment(int pos0, int rows) {
+    SegTable T{};
+    T.n = 1;
+    T.total = rows;
+    T.s[0] = Seg{0, pos0, rows, 0};
+    return T;
+}
+
+// ---- norms and elementwise -------------------------------------------------------------------------------
+
 constexpr int kNormThreads = 256;
 
 __device__ __forceinline__ float silu_ieee(float z) { return z / (1.0f + expf(-z)); }
 __device__ __forceinline__ float sigmoid_ieee(float z) { return 1.0f / (1.0f + expf(-z)); }
 
-// Group g: y = x * rsqrt(mean(x^2) + eps) * w (* silu(z) when z is given). In-place safe (every element is
-// read before it is written, by the same thread).
-__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                               const float *__restrict__ z, float *y, int n, float eps) {
+// Group g: y = x * rsqrt(mean(x^2) + eps) * w (* silu(z) when z is given). y may be x: every element is read
+// before it is written, by the same thread (so x, z and y are not restrict).
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float *x, const float *__restrict__ w,
+                                                               const float *z, float *y, int n, float eps) {
     __shared__ float part[kNormThreads];
     const size_t base = static_cast<size_t>(blockIdx.x) * n;
     const int tid = threadIdx.x;
@@ -60,79 +134,138 @@ __global__ __launch_bounds__(256) void binary_kernel(const float *a, const float
     }
 }
 
-// Gated query: head h's raw row is [query (hd), gate (hd)]; q and gate get the halves.
-__global__ __launch_bounds__(256) void split_gated_q_kernel(const float *__restrict__ raw, float *__restrict__ q,
-                                                           float *__restrict__ gate, int heads, int hd) {
+// ---- layout ops ------------------------------------------------------------------------------------------
+
+// Gated query split as a 16-byte copy: quad e of the output (heads * hd / 4 of them) comes from quad
+// e + (e / hq) * hq of raw (query half) and hq quads further on (gate half), hq = hd / 4. Needs hd % 4 == 0
+// and 16-byte aligned buffers (checked on the host; else the element kernel below).
+__global__ __launch_bounds__(256) void split_gated_q4_kernel(const float4 *__restrict__ raw, float4 *__restrict__ q,
+                                                             float4 *__restrict__ gate, int hq, long nq) {
+    const long e = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= nq) return;
+    const long src = e + (e / hq) * hq;
+    q[e] = raw[src];
+    gate[e] = raw[src + hq];
+}
+__global__ __launch_bounds__(256) void split_gated_q1_kernel(const float *__restrict__ raw, float *__restrict__ q,
+                                                             float *__restrict__ gate, int hd, long n) {
+    const long e = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= n) return;
+    const long src = e + (e / hd) * hd;
+    q[e] = raw[src];
+    gate[e] = raw[src + hd];
+}
+
+// dst[r] = [a[r] | b[r]], rows of `width` floats.
+__global__ __launch_bounds__(256) void concat_rows_kernel(float *__restrict__ dst, const float *__restrict__ a,
+                                                          const float *__restrict__ b, int width, long n) {
     const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= static_cast<long>(heads) * hd) return;
-    const long h = i / hd, d = i - h * hd;
-    q[i] = raw[2 * h * hd + d];
-    gate[i] = raw[2 * h * hd + hd + d];
+    if (i >= n) return;
+    const long r = i / (2 * width), c = i - r * 2 * width;
+    dst[i] = c < width ? a[r * width + c] : b[r * width + c - width];
 }
 
-// NeoX RoPE in place over dims [0, rot) of each head of token t (position pos0 + t): pair (j, j + rot/2)
-// turns by (pos0 + t) * base^(-2j / rot), the angle and its cosine / sine in fp64, the rotation in fp32.
-__global__ __launch_bounds__(128) void rope_neox_kernel(float *x, int ntok, int heads, int hd, int rot, int pos0,
-                                                        double base) {
-    const int half = rot / 2;
-    const long i = static_cast<long>(blockIdx.x) * 128 + threadIdx.x;
-    if (i >= static_cast<long>(ntok) * heads * half) return;
-    const int j = static_cast<int>(i % half);
-    const long th = i / half;  // token * heads + head
-    const int t = static_cast<int>(th / heads);
-    const double ang = static_cast<double>(pos0 + t) * pow(base, -2.0 * j / rot);
-    const float c = static_cast<float>(cos(ang)), sn = static_cast<float>(sin(ang));
-    float *head = x + th * hd;
-    const float a = head[j], b = head[j + half];
-    head[j] = a * c - b * sn;
-    head[j + half] = b * c + a * sn;
+// Fill with zeros (a kernel, not hipMemsetAsync, so the op can sit in a captured graph).
+__global__ __launch_bounds__(256) void zero_kernel(uint32_t *__restrict__ p, long nwords) {
+    for (long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; i < nwords; i += static_cast<long>(gridDim.x) * 256)
+        p[i] = 0u;
+}
+__global__ void zero_bytes_kernel(uint8_t *__restrict__ p, int n) {
+    if (static_cast<int>(threadIdx.x) < n) p[threadIdx.x] = 0;
 }
 
-// KV append into contiguous caches [kv_head][max_seq][hd] (fp32, or fp16 rounded to nearest): element d of
-// head h of token t goes to position pos0 + t.
-__device__ __forceinline__ void kv_put(float *c, size_t i, float v) { c[i] = v; }
-__device__ __forceinline__ void kv_put(_Float16 *c, size_t i, float v) { c[i] = static_cast<_Float16>(v); }
-template <typename C>
+// ---- rope ------------------------------------------------------------------------------------------------
+
+// NeoX RoPE in place, one workgroup per row (token): the row's rot/2 rotations (angle (pos) * base^(-2j/rot)
+// and its cosine / sine in fp64, rounded to fp32) are computed once into LDS and applied to every head, pair
+// (x[j], x[j + rot/2]) of each head's first rot dims.
+constexpr int kRopeThreads = 128, kRopeMaxHalf = 512;
+__global__ __launch_bounds__(kRopeThreads) void rope_kernel(float *x, SegTable T, int heads, int hd, int rot,
+                                                            double base) {
+    __shared__ float2 cs[kRopeMaxHalf];
+    int t;
+    const Seg &s = seg_of_row(T, blockIdx.x, t);
+    const int half = rot / 2, pos = s.pos0 + t;
+    for (int j = threadIdx.x; j < half; j += kRopeThreads) {
+        const double ang = static_cast<double>(pos) * pow(base, -2.0 * j / rot);
+        cs[j] = float2{static_cast<float>(cos(ang)), static_cast<float>(sin(ang))};
+    }
+    __syncthreads();
+    float *row = x + static_cast<size_t>(s.row0 + t) * heads * hd;
+    for (int e = threadIdx.x; e < heads * half; e += kRopeThreads) {
+        const int h = e / half, j = e - h * half;
+        float *p = row + static_cast<size_t>(h) * hd;
+        const float2 c = cs[j];
+        const float a = p[j], b = p[j + half];
+        p[j] = a * c.x - b * c.y;
+        p[j + half] = b * c.x + a * c.y;
+    }
+}
+
+// ---- KV append -------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ void put4(float *c, size_t i, float4 v) { *reinterpret_cast<float4 *>(c + i) = v; }
+__device__ __forceinline__ void put4(_Float16 *c, size_t i, float4 v) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<h4 *>(c + i) = h4{static_cast<_Float16>(v.x), static_cast<_Float16>(v.y),
+                                        static_cast<_Float16>(v.z), static_cast<_Float16>(v.w)};
+}
+__device__ __forceinline__ void put1(float *c, size_t i, float v) { c[i] = v; }
+__device__ __forceinline__ void put1(_Float16 *c, size_t i, float v) { c[i] = static_cast<_Float16>(v); }
+
+// One workgroup per row: the row's k, v [kv_heads][hd] go to position pos0 + t of the segment's sequence. Quads
+// (VEC = 4, hd % 4 == 0 and aligned buffers) or single values; fp16 caches are written rounded to nearest.
+template <typename C, int VEC>
 __global__ __launch_bounds__(256) void kv_append_kernel(const float *__restrict__ k, const float *__restrict__ v,
-                                                        C *__restrict__ kc, C *__restrict__ vc, int ntok,
-                                                        int kv_heads, int max_seq, int hd, int pos0) {
-    const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= static_cast<long>(ntok) * kv_heads * hd) return;
-    const long d = i % hd, th = i / hd;
-    const long h = th % kv_heads, t = th / kv_heads;
-    const size_t dst = (static_cast<size_t>(h) * max_seq + pos0 + t) * hd + d;
-    kv_put(kc, dst, k[i]);
-    kv_put(vc, dst, v[i]);
+                                                        C *__restrict__ kc, C *__restrict__ vc, SegTable T, KvMap M,
+                                                        int hd) {
+    int t;
+    const Seg &s = seg_of_row(T, blockIdx.x, t);
+    const int pos = s.pos0 + t, n = M.kv_heads * hd;
+    const size_t src = static_cast<size_t>(s.row0 + t) * n;
+    for (int e = threadIdx.x * VEC; e < n; e += 256 * VEC) {
+        const int kvh = e / hd, d = e - kvh * hd;
+        const size_t dst = M.row(s.slot, kvh, pos) * hd + d;
+        if constexpr (VEC == 4) {
+            put4(kc, dst, *reinterpret_cast<const float4 *>(k + src + e));
+            put4(vc, dst, *reinterpret_cast<const float4 *>(v + src + e));
+        } else {
+            put1(kc, dst, k[src + e]);
+            put1(vc, dst, v[src + e]);
+        }
+    }
 }
 
-// GQA attention of query token t, head h (workgroup (h, t), 4 waves): positions [start, end) with end =
-// seq_len0 + t (causal) or seq_len0 + ntok - 1 (bidirectional), start = end_q - window when a window is set
-// (end_q = seq_len0 + t). Wave w takes the 64-position chunks w, w + 4, ...: lane = position for q . k, an
-// online softmax (running max m, sum l, output acc rescaled by e^(m_old - m_new)), lane = output dims for the
-// V sum; the four waves' (m, l, acc) are merged in wave order. Caches [kv_head][max_seq][hd], fp32 or fp16.
+// ---- attention (decode and verify rows) -------------------------------------------------------------------
+
+// GQA attention of query row t of a segment, head h (workgroup (h, global row), 4 waves). The row sees positions
+// [start, end) with end = seq_len0 + t (causal) or seq_len0 + rows - 1 (bidirectional), seq_len0 = pos0 + 1,
+// and start = end_q - window when a window is set (end_q = seq_len0 + t). Wave w takes the 64-position chunks
+// w, w + 4, ...: lane = position for q . k, an online softmax (running max m, sum l, output acc rescaled by
+// e^(m_old - m_new)), lane = output dims for the V sum; the four waves' (m, l, acc) are merged in wave order.
 constexpr int kAttnWaves = 4, kAttnMaxHd = 256;
-__device__ __forceinline__ float kv_get(const float *c, size_t i) { return c[i]; }
-__device__ __forceinline__ float kv_get(const _Float16 *c, size_t i) { return static_cast<float>(c[i]); }
 template <typename C>
 __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(const float *__restrict__ q, const C *__restrict__ kc,
                                                                     const C *__restrict__ vc, float *__restrict__ out,
-                                                                    int heads, int kv_heads, int hd, int max_seq,
-                                                                    int seq_len0, int bidirectional, int window) {
+                                                                    SegTable T, KvMap M, int heads, int hd,
+                                                                    int bidirectional, int window) {
     __shared__ float sq[kAttnMaxHd];
     __shared__ float sp[kAttnWaves][64];
     __shared__ float sm[kAttnWaves], sl[kAttnWaves];
     __shared__ float sacc[kAttnWaves][kAttnMaxHd];
-    const int h = blockIdx.x, t = blockIdx.y, ntok = gridDim.y;
+    int t;
+    const Seg &s = seg_of_row(T, blockIdx.y, t);
+    const int h = blockIdx.x;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int seq_len0 = s.pos0 + 1;
     const int qend = seq_len0 + t;
-    const int end = bidirectional ? seq_len0 + ntok - 1 : qend;
+    const int end = bidirectional ? seq_len0 + s.rows - 1 : qend;
     const int start = window > 0 && qend > window ? qend - window : 0;
-    const int kvh = h / (heads / kv_heads);
+    const int kvh = h / (heads / M.kv_heads);
     const float scale = 1.0f / sqrtf(static_cast<float>(hd));
-    const float *qh = q + (static_cast<size_t>(t) * heads + h) * hd;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) sq[d] = qh[d];
+    const size_t qrow = (static_cast<size_t>(s.row0 + t) * heads + h) * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) sq[d] = q[qrow + d];
     __syncthreads();
-    const size_t hbase = static_cast<size_t>(kvh) * max_seq;
     float m = -INFINITY, l = 0.0f;
     float acc[kAttnMaxHd / 64];
 #pragma unroll
@@ -141,7 +274,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(const float 
         const int p = p0 + lane;
         float sc = -INFINITY;
         if (p < end) {
-            const size_t row = (hbase + p) * hd;
+            const size_t row = M.row(s.slot, kvh, p) * hd;
             float dot = 0.0f;
             for (int d = 0; d < hd; ++d) dot = fmaf(sq[d], kv_get(kc, row + d), dot);
             sc = dot * scale;
@@ -163,7 +296,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(const float 
             const int d = lane + 64 * r;
             if (d < hd) {
                 float a = acc[r] * rs;
-                for (int j = 0; j < np; ++j) a = fmaf(sp[wv][j], kv_get(vc, (hbase + p0 + j) * hd + d), a);
+                for (int j = 0; j < np; ++j) a = fmaf(sp[wv][j], kv_get(vc, M.row(s.slot, kvh, p0 + j) * hd + d), a);
                 acc[r] = a;
             }
         }
@@ -178,14 +311,14 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(const float 
         if (lane + 64 * r < hd) sacc[wv][lane + 64 * r] = acc[r];
     __syncthreads();
     if (wv == 0) {
-        float M = -INFINITY;
-        for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, sm[w]);
+        float Mx = -INFINITY;
+        for (int w = 0; w < kAttnWaves; ++w) Mx = fmaxf(Mx, sm[w]);
         float L = 0.0f, f[kAttnWaves];
         for (int w = 0; w < kAttnWaves; ++w) {
-            f[w] = sm[w] == -INFINITY ? 0.0f : expf(sm[w] - M);
+            f[w] = sm[w] == -INFINITY ? 0.0f : expf(sm[w] - Mx);
             L += sl[w] * f[w];
         }
-        float *o = out + (static_cast<size_t>(t) * heads + h) * hd;
+        float *o = out + qrow;
         for (int d = lane; d < hd; d += 64) {
             float a = 0.0f;
             for (int w = 0; w < kAttnWaves; ++w) a += sacc[w][d] * f[w];
@@ -194,111 +327,260 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(const float 
     }
 }
 
-// Causal depthwise conv + SiLU through ntok tokens, one thread per channel: the state row [K] holds the last K
-// inputs; per token it shifts left, takes x, and out = silu(state . w). snap (optional) receives the state
-// after each token but the last, [ntok - 1][channel][K]; the state keeps the final one.
-constexpr int kConvMaxK = 8;
+// ---- causal conv update ----------------------------------------------------------------------------------
+
+// Depthwise causal conv + SiLU, one thread per (channel, segment), the K-tap window in registers (K a template
+// parameter: the shift is register renaming). Per row: window <- [window[1:], x], out = silu(window . w).
+// snap (one segment only) gets the window after each row but the last, [rows - 1][channels][K]; the state
+// [slot][channels][K] gets the last window unless write_state is 0 (a verification pass leaves it untouched).
+template <int K>
 __global__ __launch_bounds__(256) void conv_update_kernel(const float *__restrict__ x, float *__restrict__ state,
                                                           const float *__restrict__ w, float *__restrict__ out,
-                                                          int channels, int K, int ntok, float *__restrict__ snap) {
+                                                          int channels, SegTable T, float *__restrict__ snap,
+                                                          int write_state) {
     const int c = blockIdx.x * 256 + threadIdx.x;
     if (c >= channels) return;
-    float st[kConvMaxK], wc[kConvMaxK];
+    const Seg &s = T.s[blockIdx.y];
+    float *st = state + (static_cast<size_t>(s.slot) * channels + c) * K;
+    float win[K], wc[K];
 #pragma unroll
-    for (int k = 0; k < kConvMaxK; ++k) {
-        st[k] = k < K ? state[static_cast<size_t>(c) * K + k] : 0.0f;
-        wc[k] = k < K ? w[static_cast<size_t>(c) * K + k] : 0.0f;
+    for (int k = 0; k < K; ++k) {
+        win[k] = st[k];
+        wc[k] = w[static_cast<size_t>(c) * K + k];
     }
-    for (int t = 0; t < ntok; ++t) {
+    const size_t row = static_cast<size_t>(s.row0) * channels + c;
+    for (int t = 0; t < s.rows; ++t) {
+        const float xi = x[row + static_cast<size_t>(t) * channels];
 #pragma unroll
-        for (int k = 0; k < kConvMaxK - 1; ++k)
-            if (k < K - 1) st[k] = st[k + 1];
-        const float xi = x[static_cast<size_t>(t) * channels + c];
+        for (int k = 0; k + 1 < K; ++k) win[k] = win[k + 1];
+        win[K - 1] = xi;
         float acc = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kConvMaxK; ++k) {
-            if (k == K - 1) st[k] = xi;
-            if (k < K) acc = fmaf(st[k], wc[k], acc);
+        for (int k = 0; k < K; ++k) acc = fmaf(win[k], wc[k], acc);
+        out[row + static_cast<size_t>(t) * channels] = silu_ieee(acc);
+        if (snap != nullptr && t + 1 < s.rows) {
+            float *sn = snap + (static_cast<size_t>(t) * channels + c) * K;
+#pragma unroll
+            for (int k = 0; k < K; ++k) sn[k] = win[k];
         }
-        out[static_cast<size_t>(t) * channels + c] = silu_ieee(acc);
-        if (snap != nullptr && t < ntok - 1)
-            for (int k = 0; k < K; ++k) snap[(static_cast<size_t>(t) * channels + c) * K + k] = st[k];
     }
-    for (int k = 0; k < K; ++k) state[static_cast<size_t>(c) * K + k] = st[k];
+    if (write_state) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) st[k] = win[k];
+    }
 }
 
-// Gated delta rule through ntok tokens, one workgroup per value head h (state S [kd][vd] of that head): conv
-// rows are [q (key_heads kd) | k (key_heads kd) | v (value_heads vd)]; key head kh = h / (vh / kh) (head_order
-// 0) or h % kh (1). Per token: q^ = q / (sqrt(|q|^2 + eps) sqrt(kd)), k^ = k / sqrt(|k|^2 + eps) (sums in a fixed
-// tree), beta = sigmoid(b), decay = exp(ssm_a softplus(a + dt)); S *= decay; delta = (v - S^T k^) beta;
-// S += k^ delta^T; out = S^T q^. Thread j owns state columns j, j + 256, ...; snap: states after each token
-// but the last, [ntok - 1][vh][kd][vd].
-constexpr int kGdMaxKd = 256;
+// ---- gated delta rule ------------------------------------------------------------------------------------
+
+// State S [slot][vh][kd][vd] of the gated delta rule, held in VGPRs for the whole pass. A wave owns 8 state
+// columns of one value head: lane = (column c = lane & 7, row group g = lane >> 3), and the lane keeps rows
+// g*R .. g*R + R - 1 of its column (R = rows per lane, kd <= 8R; rows past kd are zero and never stored). Per
+// token every sum over the kd rows is the lane's own R-term chain plus three xor steps over the row groups
+// (lanes 8, 16 and 32 apart), so no LDS and no barrier is involved; waves are independent.
+//
+// Per token (row rr of the segment): q^ = q / (sqrt(|q|^2 + eps) sqrt(kd)), k^ = k / sqrt(|k|^2 + eps),
+// beta = sigmoid(b), decay = exp(ssm_a * softplus(a + dt)) with torch's softplus (identity above 20);
+// S *= decay; delta = (v - S^T k^) beta; S += k^ delta^T; out = S^T q^. The state is read once and written
+// once per pass (fp32, or fp16 widened to fp32 in registers and rounded once when written back).
+constexpr int kGdCols = 8, kGdGroups = 64 / kGdCols, kGdMaxKd = 256;
+
+__device__ __forceinline__ float gsum(float v) {  // sum over the 8 row groups of a column
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+__device__ __forceinline__ float ld_state(const float *p) { return *p; }
+__device__ __forceinline__ float ld_state(const _Float16 *p) { return static_cast<float>(*p); }
+__device__ __forceinline__ void st_state(float *p, float v) { *p = v; }
+__device__ __forceinline__ void st_state(_Float16 *p, float v) { *p = static_cast<_Float16>(v); }
+
+template <int R, typename ST>
 __global__ __launch_bounds__(256) void gated_delta_kernel(const float *__restrict__ conv, const float *__restrict__ braw,
                                                           const float *__restrict__ araw, const float *__restrict__ ssm_a,
-                                                          const float *__restrict__ dt, float *__restrict__ S,
+                                                          const float *__restrict__ dt, ST *__restrict__ state,
                                                           float *__restrict__ out, int key_heads, int value_heads,
-                                                          int kd, int vd, float eps, int head_order, int ntok,
-                                                          float *__restrict__ snap) {
-    __shared__ float sq[kGdMaxKd], sk[kGdMaxKd], red[2][256];
-    const int h = blockIdx.x, tid = threadIdx.x;
+                                                          int kd, int vd, float eps, int head_order, SegTable T,
+                                                          float *__restrict__ snap, int write_state) {
+    const int lane = threadIdx.x & 63;
+    const int tiles = (vd + kGdCols - 1) / kGdCols;
+    const int wid = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    if (wid >= value_heads * tiles) return;  // whole waves leave; nothing below synchronises across waves
+    const int h = wid / tiles, c0 = (wid - h * tiles) * kGdCols;
+    const int c = lane & (kGdCols - 1), g = lane / kGdCols;
+    const int col = c0 + c, r0 = g * R;
+    const bool col_ok = col < vd;
     const int kh = head_order == 0 ? h / (value_heads / key_heads) : h % key_heads;
+    const Seg &s = T.s[blockIdx.y];
+    const size_t hstate = static_cast<size_t>(kd) * vd;
+    ST *S = state + (static_cast<size_t>(s.slot) * value_heads + h) * hstate;
     const size_t cdim = static_cast<size_t>(2) * key_heads * kd + static_cast<size_t>(value_heads) * vd;
-    float *const Sh = S + static_cast<size_t>(h) * kd * vd;
-    for (int t = 0; t < ntok; ++t) {
-        const float *row = conv + static_cast<size_t>(t) * cdim;
-        const float *qs = row + static_cast<size_t>(kh) * kd, *ks = row + static_cast<size_t>(key_heads + kh) * kd;
-        const float *vs = row + static_cast<size_t>(2) * key_heads * kd + static_cast<size_t>(h) * vd;
-        float aq = 0.0f, ak = 0.0f;
-        for (int i = tid; i < kd; i += 256) {
-            aq = fmaf(qs[i], qs[i], aq);
-            ak = fmaf(ks[i], ks[i], ak);
+
+    float st[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+        st[i] = col_ok && r0 + i < kd ? ld_state(S + static_cast<size_t>(r0 + i) * vd + col) : 0.0f;
+    const float a_h = ssm_a[h], dt_h = dt[h];
+    const float rkd = 1.0f / sqrtf(static_cast<float>(kd));
+
+    for (int t = 0; t < s.rows; ++t) {
+        const size_t rr = static_cast<size_t>(s.row0) + t;
+        const float *qs = conv + rr * cdim + static_cast<size_t>(kh) * kd;
+        const float *ks = qs + static_cast<size_t>(key_heads) * kd;
+        float qv[R], kv[R];
+        float qq = 0.0f, kk = 0.0f;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const bool ok = r0 + i < kd;
+            qv[i] = ok ? qs[r0 + i] : 0.0f;
+            kv[i] = ok ? ks[r0 + i] : 0.0f;
+            qq = fmaf(qv[i], qv[i], qq);
+            kk = fmaf(kv[i], kv[i], kk);
         }
-        red[0][tid] = aq;
-        red[1][tid] = ak;
-        for (int w = 128; w > 0; w >>= 1) {
-            __syncthreads();
-            if (tid < w) {
-                red[0][tid] += red[0][tid + w];
-                red[1][tid] += red[1][tid + w];
-            }
+        const float v = col_ok ? conv[rr * cdim + static_cast<size_t>(2) * key_heads * kd + static_cast<size_t>(h) * vd + col]
+                               : 0.0f;
+        const float beta = sigmoid_ieee(braw[rr * value_heads + h]);
+        const float xa = araw[rr * value_heads + h] + dt_h;
+        const float decay = expf(a_h * (xa > 20.0f ? xa : log1pf(expf(xa))));
+        qq = gsum(qq);
+        kk = gsum(kk);
+        const float qscale = rkd / sqrtf(qq + eps);
+        const float kscale = 1.0f / sqrtf(kk + eps);
+        float mem = 0.0f;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            st[i] *= decay;
+            mem = fmaf(st[i], kv[i], mem);
         }
-        __syncthreads();
-        const float qscale = 1.0f / (sqrtf(red[0][0] + eps) * sqrtf(static_cast<float>(kd)));
-        const float kscale = 1.0f / sqrtf(red[1][0] + eps);
-        for (int i = tid; i < kd; i += 256) {
-            sq[i] = qs[i] * qscale;
-            sk[i] = ks[i] * kscale;
+        mem = gsum(mem) * kscale;
+        const float upd = (v - mem) * beta * kscale;  // S[i] += k[i] * kscale * delta
+        float o = 0.0f;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            st[i] = fmaf(kv[i], upd, st[i]);
+            o = fmaf(st[i], qv[i], o);
         }
-        __syncthreads();
-        const float beta = sigmoid_ieee(braw[static_cast<size_t>(t) * value_heads + h]);
-        const float xa = araw[static_cast<size_t>(t) * value_heads + h] + dt[h];
-        const float sp = xa > 20.0f ? xa : log1pf(expf(xa));
-        const float decay = expf(ssm_a[h] * sp);
-        float *const sn = snap != nullptr && t < ntok - 1 ? snap + (static_cast<size_t>(t) * value_heads + h) * kd * vd
-                                                          : nullptr;
-        for (int j = tid; j < vd; j += 256) {
-            float mem = 0.0f;
-            for (int i = 0; i < kd; ++i) {
-                const float v = Sh[static_cast<size_t>(i) * vd + j] * decay;
-                Sh[static_cast<size_t>(i) * vd + j] = v;
-                mem = fmaf(v, sk[i], mem);
-            }
-            const float delta = (vs[j] - mem) * beta;
-            float o = 0.0f;
-            for (int i = 0; i < kd; ++i) {
-                const float v = fmaf(sk[i], delta, Sh[static_cast<size_t>(i) * vd + j]);
-                Sh[static_cast<size_t>(i) * vd + j] = v;
-                o = fmaf(v, sq[i], o);
-                if (sn != nullptr) sn[static_cast<size_t>(i) * vd + j] = v;
-            }
-            out[(static_cast<size_t>(t) * value_heads + h) * vd + j] = o;
+        o = gsum(o) * qscale;
+        if (g == 0 && col_ok) out[(rr * value_heads + h) * vd + col] = o;
+        if (snap != nullptr && t + 1 < s.rows && col_ok) {
+            float *sn = snap + (static_cast<size_t>(t) * value_heads + h) * hstate;
+#pragma unroll
+            for (int i = 0; i < R; ++i)
+                if (r0 + i < kd) sn[static_cast<size_t>(r0 + i) * vd + col] = st[i];
         }
-        __syncthreads();  // sq / sk / red are rewritten for the next token
+    }
+    if (write_state && col_ok) {
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+            if (r0 + i < kd) st_state(S + static_cast<size_t>(r0 + i) * vd + col, st[i]);
     }
 }
 
-int status_of(hipError_t e) { return e == hipSuccess ? VQ_OK : static_cast<int>(e); }
+// ---- host launchers --------------------------------------------------------------------------------------
+
+int launch_rope(float *x, const SegTable &T, int heads, int hd, int rot, double base, hipStream_t s) {
+    if (!x) return VQ_ERR_ARG;
+    if (heads < 1 || hd < 1 || rot <= 0 || rot % 2 || rot > hd || rot / 2 > kRopeMaxHalf || !(base > 0.0))
+        return VQ_ERR_SHAPE;
+    rope_kernel<<<T.total, kRopeThreads, 0, s>>>(x, T, heads, hd, rot, base);
+    return status_of(hipGetLastError());
+}
+
+int launch_kv_append(const float *k, const float *v, void *kc, void *vc, int elem, const SegTable &T, const KvMap &M,
+                     int hd, hipStream_t s) {
+    if (!k || !v || !kc || !vc || (elem != 2 && elem != 4)) return VQ_ERR_ARG;
+    if (M.kv_heads < 1 || hd < 1) return VQ_ERR_SHAPE;
+    const bool quad = hd % 4 == 0 && ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15) == 0 &&
+                      ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & (elem == 4 ? 15 : 7)) == 0;
+    const dim3 grid(T.total);
+    if (elem == 2) {
+        auto *kh = static_cast<_Float16 *>(kc), *vh = static_cast<_Float16 *>(vc);
+        if (quad) kv_append_kernel<_Float16, 4><<<grid, 256, 0, s>>>(k, v, kh, vh, T, M, hd);
+        else kv_append_kernel<_Float16, 1><<<grid, 256, 0, s>>>(k, v, kh, vh, T, M, hd);
+    } else {
+        auto *kf = static_cast<float *>(kc), *vf = static_cast<float *>(vc);
+        if (quad) kv_append_kernel<float, 4><<<grid, 256, 0, s>>>(k, v, kf, vf, T, M, hd);
+        else kv_append_kernel<float, 1><<<grid, 256, 0, s>>>(k, v, kf, vf, T, M, hd);
+    }
+    return status_of(hipGetLastError());
+}
+
+int launch_attention(const float *q, const void *kc, const void *vc, float *out, int elem, const SegTable &T,
+                     const KvMap &M, int heads, int hd, int bidirectional, int window, hipStream_t s) {
+    if (!q || !kc || !vc || !out || (elem != 2 && elem != 4)) return VQ_ERR_ARG;
+    if (M.kv_heads < 1 || heads < M.kv_heads || heads % M.kv_heads || hd < 1 || hd > kAttnMaxHd || window < 0)
+        return VQ_ERR_SHAPE;
+    const dim3 grid(heads, T.total);
+    if (elem == 2)
+        attention_kernel<_Float16><<<grid, 64 * kAttnWaves, 0, s>>>(q, static_cast<const _Float16 *>(kc),
+                                                                    static_cast<const _Float16 *>(vc), out, T, M, heads,
+                                                                    hd, bidirectional, window);
+    else
+        attention_kernel<float><<<grid, 64 * kAttnWaves, 0, s>>>(q, static_cast<const float *>(kc),
+                                                                 static_cast<const float *>(vc), out, T, M, heads, hd,
+                                                                 bidirectional, window);
+    return status_of(hipGetLastError());
+}
+
+int launch_conv_update(const float *x, float *state, const float *w, float *out, int channels, int K,
+                       const SegTable &T, float *snap, int write_state, hipStream_t s) {
+    if (!x || !state || !w || !out) return VQ_ERR_ARG;
+    if (channels < 1 || K < 1 || K > VQ_CONV_MAX_K) return VQ_ERR_SHAPE;
+    if (snap != nullptr && T.n != 1) return VQ_ERR_ARG;
+    const dim3 grid((channels + 255) / 256, T.n);
+    switch (K) {
+#define VQ_CONV_CASE(KK) \
+    case KK: conv_update_kernel<KK><<<grid, 256, 0, s>>>(x, state, w, out, channels, T, snap, write_state); break;
+        VQ_CONV_CASE(1) VQ_CONV_CASE(2) VQ_CONV_CASE(3) VQ_CONV_CASE(4)
+        VQ_CONV_CASE(5) VQ_CONV_CASE(6) VQ_CONV_CASE(7) VQ_CONV_CASE(8)
+#undef VQ_CONV_CASE
+    }
+    return status_of(hipGetLastError());
+}
+
+template <typename ST>
+void gd_dispatch(int R, dim3 grid, hipStream_t s, const float *conv, const float *b, const float *a, const float *ssm_a,
+                 const float *dt, ST *state, float *out, int kh, int vh, int kd, int vd, float eps, int head_order,
+                 const SegTable &T, float *snap, int write_state) {
+#define VQ_GD_CASE(RR)                                                                                              \
+    case RR:                                                                                                        \
+        gated_delta_kernel<RR, ST><<<grid, 256, 0, s>>>(conv, b, a, ssm_a, dt, state, out, kh, vh, kd, vd, eps,      \
+                                                        head_order, T, snap, write_state);                         \
+        break;
+    switch (R) { VQ_GD_CASE(4) VQ_GD_CASE(8) VQ_GD_CASE(16) VQ_GD_CASE(32) }
+#undef VQ_GD_CASE
+}
+
+int launch_gated_delta(const float *conv, const float *b, const float *a, const float *ssm_a, const float *dt,
+                       void *state, int state_elem, float *out, int kh, int vh, int kd, int vd, float eps,
+                       int head_order, const SegTable &T, float *snap, int write_state, hipStream_t s) {
+    if (!conv || !b || !a || !ssm_a || !dt || !state || !out || (state_elem != 4 && state_elem != 2)) return VQ_ERR_ARG;
+    if (kh < 1 || vh < kh || vh % kh || kd < 1 || kd > kGdMaxKd || vd < 1 || (head_order != 0 && head_order != 1) ||
+        !(eps >= 0.0f))
+        return VQ_ERR_SHAPE;
+    if (snap != nullptr && (T.n != 1 || state_elem != 4)) return VQ_ERR_ARG;
+    const int R = kd <= 4 * kGdGroups ? 4 : kd <= 8 * kGdGroups ? 8 : kd <= 16 * kGdGroups ? 16 : 32;
+    const long waves = static_cast<long>(vh) * ((vd + kGdCols - 1) / kGdCols);
+    const dim3 grid(static_cast<unsigned>((waves + 3) / 4), T.n);
+    if (state_elem == 4)
+        gd_dispatch<float>(R, grid, s, conv, b, a, ssm_a, dt, static_cast<float *>(state), out, kh, vh, kd, vd, eps,
+                           head_order, T, snap, write_state);
+    else
+        gd_dispatch<_Float16>(R, grid, s, conv, b, a, ssm_a, dt, static_cast<_Float16 *>(state), out, kh, vh, kd, vd,
+                              eps, head_order, T, snap, write_state);
+    return status_of(hipGetLastError());
+}
+
+KvMap paged(const int32_t *pt, int page_size, int pps, int kv_heads) { return KvMap{pt, 0, page_size, pps, kv_heads}; }
+KvMap contiguous(int max_seq, int kv_heads) { return KvMap{nullptr, max_seq, 1, 1, kv_heads}; }
+
+int check_paging(const int32_t *pt, int page_size, int pps, const SegTable &T) {
+    if (pt == nullptr) return VQ_ERR_ARG;
+    if (page_size < 1 || pps < 1) return VQ_ERR_SHAPE;
+    for (int i = 0; i < T.n; ++i)
+        if (static_cast<long>(T.s[i].pos0) + T.s[i].rows > static_cast<long>(page_size) * pps) return VQ_ERR_SHAPE;
+    return VQ_OK;
+}
 
 }  // namespace
 
@@ -327,76 +609,130 @@ int vq_binary(int op, const float *a, const float *b, float *out, long n, void *
 int vq_split_gated_q(const float *raw, float *q, float *gate, int heads, int hd, void *stream) {
     if (!raw || !q || !gate) return VQ_ERR_ARG;
     if (heads < 1 || hd < 1) return VQ_ERR_SHAPE;
+    hipStream_t s = static_cast<hipStream_t>(stream);
     const long n = static_cast<long>(heads) * hd;
-    split_gated_q_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
-        raw, q, gate, heads, hd);
+    if (hd % 4 == 0 && ((reinterpret_cast<uintptr_t>(raw) | reinterpret_cast<uintptr_t>(q) |
+                         reinterpret_cast<uintptr_t>(gate)) & 15) == 0) {
+        const long nq = n / 4;
+        split_gated_q4_kernel<<<static_cast<unsigned>((nq + 255) / 256), 256, 0, s>>>(
+            reinterpret_cast<const float4 *>(raw), reinterpret_cast<float4 *>(q), reinterpret_cast<float4 *>(gate),
+            hd / 4, nq);
+    } else {
+        split_gated_q1_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(raw, q, gate, hd, n);
+    }
+    return status_of(hipGetLastError());
+}
+
+int vq_concat_rows(float *dst, const float *a, const float *b, int rows, int width, void *stream) {
+    if (!dst || !a || !b) return VQ_ERR_ARG;
+    if (rows < 0 || width < 0) return VQ_ERR_SHAPE;
+    const long n = 2L * rows * width;
+    if (n == 0) return VQ_OK;
+    concat_rows_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        dst, a, b, width, n);
+    return status_of(hipGetLastError());
+}
+
+int vq_zero(void *p, size_t nbytes, void *stream) {
+    if (!p && nbytes) return VQ_ERR_ARG;
+    if (nbytes == 0) return VQ_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto *b = static_cast<uint8_t *>(p);
+    // Unaligned head and tail bytes, aligned words between.
+    const size_t head = (4 - (reinterpret_cast<uintptr_t>(b) & 3)) & 3;
+    if (nbytes <= head + 3) {
+        zero_bytes_kernel<<<1, 64, 0, s>>>(b, static_cast<int>(nbytes));
+        return status_of(hipGetLastError());
+    }
+    if (head) zero_bytes_kernel<<<1, 64, 0, s>>>(b, static_cast<int>(head));
+    const size_t words = (nbytes - head) / 4, tail = (nbytes - head) % 4;
+    const long blocks = static_cast<long>((words + 255) / 256);
+    zero_kernel<<<static_cast<unsigned>(blocks < 4096 ? blocks : 4096), 256, 0, s>>>(
+        reinterpret_cast<uint32_t *>(b + head), static_cast<long>(words));
+    if (tail) zero_bytes_kernel<<<1, 64, 0, s>>>(b + head + 4 * words, static_cast<int>(tail));
     return status_of(hipGetLastError());
 }
 
 int vq_rope(float *x, int ntok, int heads, int hd, int rot, int pos0, double base, void *stream) {
-    if (!x) return VQ_ERR_ARG;
-    if (ntok < 1 || heads < 1 || hd < 1 || rot <= 0 || rot % 2 || rot > hd || pos0 < 0 || !(base > 0.0))
-        return VQ_ERR_SHAPE;
-    const long n = static_cast<long>(ntok) * heads * (rot / 2);
-    rope_neox_kernel<<<static_cast<unsigned>((n + 127) / 128), 128, 0, static_cast<hipStream_t>(stream)>>>(
-        x, ntok, heads, hd, rot, pos0, base);
-    return status_of(hipGetLastError());
+    if (ntok < 1 || pos0 < 0) return VQ_ERR_SHAPE;
+    return launch_rope(x, one_segment(pos0, ntok), heads, hd, rot, base, static_cast<hipStream_t>(stream));
+}
+
+int vq_rope_seg(float *x, const int32_t *segs, int nseg, int heads, int hd, int rot, double base, void *stream) {
+    SegTable T;
+    const int st = make_table(segs, nseg, T, nullptr);
+    return st != VQ_OK ? st : launch_rope(x, T, heads, hd, rot, base, static_cast<hipStream_t>(stream));
 }
 
 int vq_kv_append(const float *k, const float *v, void *kc, void *vc, int elem, int ntok, int kv_heads, int max_seq,
                  int hd, int pos0, void *stream) {
-    if (!k || !v || !kc || !vc || (elem != 2 && elem != 4)) return VQ_ERR_ARG;
-    if (ntok < 1 || kv_heads < 1 || hd < 1 || pos0 < 0 || pos0 + ntok > max_seq) return VQ_ERR_SHAPE;
-    const long n = static_cast<long>(ntok) * kv_heads * hd;
-    const unsigned blocks = static_cast<unsigned>((n + 255) / 256);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (elem == 2)
-        kv_append_kernel<_Float16><<<blocks, 256, 0, s>>>(k, v, static_cast<_Float16 *>(kc), static_cast<_Float16 *>(vc),
-                                                          ntok, kv_heads, max_seq, hd, pos0);
-    else
-        kv_append_kernel<float><<<blocks, 256, 0, s>>>(k, v, static_cast<float *>(kc), static_cast<float *>(vc), ntok,
-                                                       kv_heads, max_seq, hd, pos0);
-    return status_of(hipGetLastError());
+    if (ntok < 1 || kv_heads < 1 || pos0 < 0 || pos0 + ntok > max_seq) return VQ_ERR_SHAPE;
+    return launch_kv_append(k, v, kc, vc, elem, one_segment(pos0, ntok), contiguous(max_seq, kv_heads), hd,
+                            static_cast<hipStream_t>(stream));
+}
+
+int vq_kv_append_seg(const float *k, const float *v, void *kc, void *vc, int elem, const int32_t *segs, int nseg,
+                     int kv_heads, int hd, const int32_t *page_table, int page_size, int pages_per_seq, void *stream) {
+    SegTable T;
+    int st = make_table(segs, nseg, T, nullptr);
+    if (st == VQ_OK) st = check_paging(page_table, page_size, pages_per_seq, T);
+    if (st != VQ_OK) return st;
+    return launch_kv_append(k, v, kc, vc, elem, T, paged(page_table, page_size, pages_per_seq, kv_heads), hd,
+                            static_cast<hipStream_t>(stream));
 }
 
 int vq_attention(const float *q, const void *kc, const void *vc, float *out, int elem, int heads, int kv_heads, int hd,
                  int max_seq, int seq_len, int ntok, int bidirectional, int window, void *stream) {
-    if (!q || !kc || !vc || !out || (elem != 2 && elem != 4)) return VQ_ERR_ARG;
-    if (kv_heads < 1 || heads < kv_heads || heads % kv_heads || hd < 1 || hd > kAttnMaxHd || ntok < 1 ||
-        seq_len < 1 || seq_len + ntok - 1 > max_seq || window < 0)
-        return VQ_ERR_SHAPE;
-    const dim3 grid(heads, ntok);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (elem == 2)
-        attention_kernel<_Float16><<<grid, 64 * kAttnWaves, 0, s>>>(q, static_cast<const _Float16 *>(kc),
-                                                                    static_cast<const _Float16 *>(vc), out, heads,
-                                                                    kv_heads, hd, max_seq, seq_len, bidirectional, window);
-    else
-        attention_kernel<float><<<grid, 64 * kAttnWaves, 0, s>>>(q, static_cast<const float *>(kc),
-                                                                 static_cast<const float *>(vc), out, heads, kv_heads,
-                                                                 hd, max_seq, seq_len, bidirectional, window);
-    return status_of(hipGetLastError());
+    if (kv_heads < 1 || ntok < 1 || seq_len < 1 || seq_len + ntok - 1 > max_seq) return VQ_ERR_SHAPE;
+    return launch_attention(q, kc, vc, out, elem, one_segment(seq_len - 1, ntok), contiguous(max_seq, kv_heads), heads,
+                            hd, bidirectional, window, static_cast<hipStream_t>(stream));
+}
+
+int vq_attention_seg(const float *q, const void *kc, const void *vc, float *out, int elem, const int32_t *segs,
+                     int nseg, int heads, int kv_heads, int hd, const int32_t *page_table, int page_size,
+                     int pages_per_seq, void *stream) {
+    SegTable T;
+    int st = make_table(segs, nseg, T, nullptr);
+    if (st == VQ_OK) st = check_paging(page_table, page_size, pages_per_seq, T);
+    if (st != VQ_OK) return st;
+    if (kv_heads < 1) return VQ_ERR_SHAPE;
+    return launch_attention(q, kc, vc, out, elem, T, paged(page_table, page_size, pages_per_seq, kv_heads), heads, hd,
+                            0, 0, static_cast<hipStream_t>(stream));
 }
 
 int vq_conv_update(const float *x, float *state, const float *w, float *out, int channels, int K, int ntok, float *snap,
-                   void *stream) {
-    if (!x || !state || !w || !out) return VQ_ERR_ARG;
-    if (channels < 1 || K < 1 || K > kConvMaxK || ntok < 1) return VQ_ERR_SHAPE;
-    conv_update_kernel<<<static_cast<unsigned>((channels + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
-        x, state, w, out, channels, K, ntok, snap);
-    return status_of(hipGetLastError());
+                   int write_state, void *stream) {
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    return launch_conv_update(x, state, w, out, channels, K, one_segment(0, ntok), snap, write_state,
+                              static_cast<hipStream_t>(stream));
 }
 
-int vq_gated_delta(const float *conv, const float *b, const float *a, const float *ssm_a, const float *dt, float *state,
-                   float *out, int key_heads, int value_heads, int kd, int vd, float eps, int head_order, int ntok,
-                   float *snap, void *stream) {
-    if (!conv || !b || !a || !ssm_a || !dt || !state || !out) return VQ_ERR_ARG;
-    if (key_heads < 1 || value_heads < key_heads || value_heads % key_heads || kd < 1 || kd > kGdMaxKd || vd < 1 ||
-        ntok < 1 || (head_order != 0 && head_order != 1) || !(eps >= 0.0f))
-        return VQ_ERR_SHAPE;
-    gated_delta_kernel<<<value_heads, 256, 0, static_cast<hipStream_t>(stream)>>>(
-        conv, b, a, ssm_a, dt, state, out, key_heads, value_heads, kd, vd, eps, head_order, ntok, snap);
-    return status_of(hipGetLastError());
+int vq_conv_update_seg(const float *x, float *state, const float *w, float *out, int channels, int K,
+                       const int32_t *segs, int nseg, float *snap, int write_state, void *stream) {
+    SegTable T;
+    const int st = make_table(segs, nseg, T, nullptr);
+    return st != VQ_OK ? st
+                       : launch_conv_update(x, state, w, out, channels, K, T, snap, write_state,
+                                            static_cast<hipStream_t>(stream));
+}
+
+int vq_gated_delta(const float *conv, const float *b, const float *a, const float *ssm_a, const float *dt, void *state,
+                   int state_elem, float *out, int key_heads, int value_heads, int kd, int vd, float eps,
+                   int head_order, int ntok, float *snap, int write_state, void *stream) {
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    return launch_gated_delta(conv, b, a, ssm_a, dt, state, state_elem, out, key_heads, value_heads, kd, vd, eps,
+                              head_order, one_segment(0, ntok), snap, write_state, static_cast<hipStream_t>(stream));
+}
+
+int vq_gated_delta_seg(const float *conv, const float *b, const float *a, const float *ssm_a, const float *dt,
+                       void *state, int state_elem, float *out, int key_heads, int value_heads, int kd, int vd,
+                       float eps, int head_order, const int32_t *segs, int nseg, float *snap, int write_state,
+                       void *stream) {
+    SegTable T;
+    const int st = make_table(segs, nseg, T, nullptr);
+    return st != VQ_OK ? st
+                       : launch_gated_delta(conv, b, a, ssm_a, dt, state, state_elem, out, key_heads, value_heads, kd,
+                                            vd, eps, head_order, T, snap, write_state, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -6,16 +6,12 @@
 
 namespace vq {
 
-// Activation image geometry of the streaming kernel (compile-time; overridable for tuning builds).
-#ifndef VQ_X_LDS_MAX
-#define VQ_X_LDS_MAX (64 * 1024)  // bytes of activation records one launch keeps in LDS
-#endif
-#ifndef VQ_XPAD
-#define VQ_XPAD 32  // bytes of padding after each 256 codes of the image
-#endif
+// Activation image geometry of the streaming kernel.
+constexpr int kXLdsMax = 64 * 1024;  // bytes of activation records one launch keeps in LDS
+constexpr int kXPad = 32;            // bytes of padding after each 256 codes of the image
 // Bytes of one token's activation image (codes padded per 256, then 8 bytes of scales per 32-group).
 __host__ __device__ inline int x_image_bytes(int cols) {
-    return (((cols / 32 + 7) / 8) * (256 + VQ_XPAD) + (cols / 32) * 8 + 15) / 16 * 16;
+    return (((cols / 32 + 7) / 8) * (256 + kXPad) + (cols / 32) * 8 + 15) / 16 * 16;
 }
 // Activation staging of the fp32-input streaming matvec (the bits of the reference megakernel's QMV flags,
 // runtime/instructions.py:179-182): ADD accumulates into y, NORM stages rmsnorm(v) * nw, SILU_MUL stages
@@ -32,7 +28,7 @@ struct XStage {
 
 // Tokens per streaming launch (one weight pass): as many (<= 8) as the activation image budget holds.
 inline int token_chunk(int cols) {
-    const int chunk = VQ_X_LDS_MAX / x_image_bytes(cols);
+    const int chunk = kXLdsMax / x_image_bytes(cols);
     return chunk > 8 ? 8 : chunk < 1 ? 1 : chunk;
 }
 

@@ -12,9 +12,6 @@
 #include "vq_quant.h"
 #include "vq_tables.h"
 
-#ifdef VQ_TIMING
-extern "C" void *vq_debug_timing_buffer();
-#endif
 namespace vq {
 
 // Streaming geometry (compile-time; overridable for tuning builds).
@@ -38,16 +35,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // Per-type stage shape: LPU lanes decode one unit (each takes SPB/LPU of its slices), so a stage is the
 // SU = 64/LPU consecutive units of a workgroup's byte range, about 2-7 KB: a wave holds one stage of raw
-// bytes in VGPRs while it decodes the previous one. Tuning builds override with VQ_LPU.
+// bytes in VGPRs while it decodes the previous one.
 template <int T>
 struct StageShape {
     static constexpr int LPU_DEFAULT =
         (T == VQ_Q8_0 || T == VQ_IQ4_NL || T == VQ_IQ2_XXS || T == VQ_IQ2_XS || T == VQ_IQ2_S || T == VQ_Q3_K) ? 1 : 2;
-#ifdef VQ_LPU
-    static constexpr int LPU = VQ_LPU < Sl<T>::SPB ? VQ_LPU : Sl<T>::SPB;
-#else
     static constexpr int LPU = LPU_DEFAULT;
-#endif
 };
 
 // LDS image of the activation records: per token, the int8 codes in blocks of 256 followed by XPAD bytes
@@ -57,14 +50,14 @@ struct StageShape {
 struct XImage {
     int ng, nblk, xq_bytes, bytes;  // bytes: one token's image (16-byte multiple)
     __host__ __device__ explicit XImage(int cols)
-        : ng(cols / 32), nblk((cols / 32 + 7) / 8), xq_bytes(((cols / 32 + 7) / 8) * (256 + VQ_XPAD)),
+        : ng(cols / 32), nblk((cols / 32 + 7) / 8), xq_bytes(((cols / 32 + 7) / 8) * (256 + kXPad)),
           bytes(x_image_bytes(cols)) {}
-    __device__ int code_off(int G, int h) const { return (G >> 3) * (256 + VQ_XPAD) + (G & 7) * 32 + 16 * h; }
+    __device__ int code_off(int G, int h) const { return (G >> 3) * (256 + kXPad) + (G & 7) * 32 + 16 * h; }
     // Byte of the packed record (vq_xpack_h_offset layout) that LDS image byte o (16-byte aligned) holds,
     // or -1 for padding.
     __device__ int src_of(int o, int cols) const {
         if (o < xq_bytes) {
-            const int blk = o / (256 + VQ_XPAD), w = o - blk * (256 + VQ_XPAD);
+            const int blk = o / (256 + kXPad), w = o - blk * (256 + kXPad);
             return w < 256 && blk * 256 + w < cols ? blk * 256 + w : -1;
         }
         return cols + (o - xq_bytes);
@@ -135,9 +128,6 @@ struct QJobs {
     int n;
     int blocks;   // workgroups of the launch
     unsigned long long *amax;  // null, or [NT][blocks] per-workgroup argmax keys (see argmax_key)
-#ifdef VQ_TIMING
-    unsigned long long *tm;  // diagnostic builds: per-wave {start, after prologue, loop end, exit, hw id}
-#endif
 };
 
 // Argmax key of a value at row r: larger key = larger value, then lower row. NaN and -inf never win (the
@@ -184,10 +174,6 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
 
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-#ifdef VQ_TIMING
-    const unsigned long long tm0 = __builtin_amdgcn_s_memrealtime();
-    unsigned long long tm1 = 0, tm2 = 0;
-#endif
     const int nu = (cols >> 5) / S::UG;
     const int xb = vq_xpack_stride(cols);
     const XImage xi(cols);
@@ -370,9 +356,6 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-#ifdef VQ_TIMING
-    tm1 = __builtin_amdgcn_s_memrealtime();
-#endif
 
     const int ul = lane / LPU;  // unit of this lane within a stage
     const int lj = lane % LPU;  // which of the unit's lanes
@@ -397,9 +380,6 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
         float v[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) v[t] = 0.0f;
-#ifdef VQ_NODECODE
-        v[0] = static_cast<float>(*reinterpret_cast<const uint32_t *>(up + 4 * lj) & 0xFF) * static_cast<float>(G0);
-#else
         // The unit's group scales and half sums of every token.
         float xdu[NT][S::UG];
         int32_t xhu[NT][S::UG];
@@ -505,7 +485,6 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
                 }
             }
         }
-#endif
         if (per_lane) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) slots[(s * 64 + lane) * NT + t] = v[t];
@@ -538,37 +517,16 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     // One lane takes the ticket (a wave-wide atomic would take one per lane); readfirstlane shares it.
     auto take = [&]() { return lane == 0 ? atomicAdd(&s_next, 1) : 0; };
     int ask = s >= 0 ? take() : nst;  // the stage after s (valid in lane 0)
-#ifdef VQ_TIMING
-    unsigned long long t_dec = 0, t_wait = 0, n_st = 0;
-#endif
     while (s >= 0) {
-#ifdef VQ_TIMING
-        const unsigned long long ta = __builtin_amdgcn_s_memrealtime();
-#endif
         store_stage(RA);
         const int sn = __builtin_amdgcn_readfirstlane(ask);
-#ifdef VQ_TIMING
-        wait_vm<0>();
-        wait_lgkm0();
-        const unsigned long long tb = __builtin_amdgcn_s_memrealtime();
-#endif
         if (sn < nst) {
             load_stage(sn, RA);
             ask = take();
         }
         run_stage(s);
-#ifdef VQ_TIMING
-        wait_lgkm0();
-        const unsigned long long tc = __builtin_amdgcn_s_memrealtime();
-        t_wait += tb - ta;
-        t_dec += tc - tb;
-        ++n_st;
-#endif
         s = sn < nst ? sn : -1;
     }
-#ifdef VQ_TIMING
-    tm2 = __builtin_amdgcn_s_memrealtime();
-#endif
     __syncthreads();
 
     // Each row's parts in a fixed order: the row's units are [r*nu - U0, (r+1)*nu - U0) of the range.
@@ -643,20 +601,6 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             jobs.amax[static_cast<size_t>(threadIdx.x) * jobs.blocks + b] = k;
         }
     }
-#ifdef VQ_TIMING
-    if (jobs.tm != nullptr && lane == 0) {
-        const long gw = static_cast<long>(b) * NW + wv;
-        if (gw < 65536) {
-            unsigned hw, xcc;
-            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
-            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-            unsigned long long *o = jobs.tm + 6 * static_cast<size_t>(gw);
-            o[0] = tm0; o[1] = tm1; o[2] = tm2; o[3] = __builtin_amdgcn_s_memrealtime();
-            o[4] = (static_cast<unsigned long long>(xcc) << 32) | hw;
-            o[5] = (n_st << 48) | ((t_wait & 0xFFFFFF) << 24) | (t_dec & 0xFFFFFF);
-        }
-    }
-#endif
 }
 
 // The kernel: workgroup b runs the body of its job's type. T2 == T for one-type launches; otherwise jobs of
@@ -1018,9 +962,6 @@ int launch_jobs(int n, const int *types, const uint8_t *const *w, const int *row
         jobs.blocks = pl.blocks;
         XStage xsc = xs;
         if (xs.x2 != nullptr) xsc.x2 = xs.x2 + static_cast<size_t>(c) * cols;
-#ifdef VQ_TIMING
-        jobs.tm = static_cast<unsigned long long *>(vq_debug_timing_buffer());
-#endif
         jobs.amax = amax ? amax + static_cast<size_t>(c) * pl.blocks : nullptr;
         const void *xp = static_cast<const uint8_t *>(x) + static_cast<size_t>(c) * tok_bytes;
         const int st = with_tokens<max_tokens<T, T2>()>(m, [&](auto nt) {

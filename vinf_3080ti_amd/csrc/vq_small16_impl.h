@@ -32,17 +32,8 @@ namespace vq {
 template <int T>
 constexpr bool kSmall16 = T == VQ_Q3_K || T == VQ_Q4_K || T == VQ_Q5_K || T == VQ_Q6_K;
 
-#ifndef VQ_S16_WAVES
-#define VQ_S16_WAVES 8
-#endif
-#ifndef VQ_S16_OCC
-#define VQ_S16_OCC 2
-#endif
-#ifndef VQ_S16_KR
-#define VQ_S16_KR 512
-#endif
-constexpr int kS16Occ = VQ_S16_OCC;  // waves per SIMD the register budget is set for
-constexpr int kS16Waves = VQ_S16_WAVES, kS16Rows = 16 * kS16Waves, kS16KR = VQ_S16_KR, kS16NSB = kS16KR / 256;
+constexpr int kS16Occ = 2;  // waves per SIMD the register budget is set for
+constexpr int kS16Waves = 8, kS16Rows = 16 * kS16Waves, kS16KR = 512, kS16NSB = kS16KR / 256;
 constexpr int kS16RowHalves = kS16KR + 8;  // f16 per token row of the activation image (16-byte pad)
 
 // LDS of one workgroup for ntok tokens: b_hi, b_lo [ntok + 1][kS16RowHalves] f16, xs [ntok + 1][2][16] f16 (row

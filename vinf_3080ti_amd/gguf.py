@@ -15,6 +15,7 @@ zero-copy source `HipWeightRuntime.upload_gguf_tensor` uploads from (cuda/qwen_r
 """
 from __future__ import annotations
 
+import math
 import mmap
 import struct
 from dataclasses import dataclass
@@ -112,28 +113,19 @@ class GGUFTensorInfo:
     relative_offset: int
     absolute_offset: int
 
-    @property
-    def numel(self) -> int:
-        n = 1
-        for d in self.dimensions:
-            n *= d
-        return n
+    def _trait(self, i: int):
+        return GGUF_TYPE_TRAITS[self.tensor_type][i]
 
-    @property
-    def block_size(self) -> int:
-        return GGUF_TYPE_TRAITS[self.tensor_type][0]
-
-    @property
-    def type_size(self) -> int:
-        return GGUF_TYPE_TRAITS[self.tensor_type][1]
-
-    @property
-    def is_quantized(self) -> bool:
-        return GGUF_TYPE_TRAITS[self.tensor_type][2]
+    numel = property(lambda self: math.prod(self.dimensions), doc="number of elements")
+    block_size = property(lambda self: self._trait(0), doc="elements per block")
+    type_size = property(lambda self: self._trait(1), doc="bytes per block")
+    is_quantized = property(lambda self: self._trait(2), doc="block-quantized type")
 
     @property
     def nbytes(self) -> int:
-        return -(-self.numel // self.block_size) * self.type_size
+        """Bytes of the tensor's data: whole blocks, the last one possibly partial."""
+        nblocks, rem = divmod(self.numel, self.block_size)
+        return (nblocks + (rem > 0)) * self.type_size
 
 
 @dataclass
@@ -146,28 +138,27 @@ class GGUFFile:
     alignment: int
 
     def metadata_value(self, key: str, default: Any = None) -> Any:
-        item = self.metadata.get(key)
-        return default if item is None else item.value
+        """The decoded value stored under `key`, or `default` when the file has no such key."""
+        return self.metadata[key].value if key in self.metadata else default
 
     def quantized_tensors(self) -> list[GGUFTensorInfo]:
-        return [t for t in self.tensors.values() if t.is_quantized]
+        return list(filter(lambda info: info.is_quantized, self.tensors.values()))
 
     def mmap_tensor(self, name: str):
         """(file object, mmap, memoryview of the tensor's nbytes bytes). The caller releases the view, then
         closes the mmap and the file."""
         info = self.tensors[name]
-        f = self.path.open("rb")
+        lo, hi = info.absolute_offset, info.absolute_offset + info.nbytes
+        fh = self.path.open("rb")
         try:
-            mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
-        except Exception:
-            f.close()
+            mapping = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+            if hi > (size := len(mapping)):
+                mapping.close()
+                raise UnsupportedModelError(f"tensor {name} ends at byte {hi}, beyond the {size}-byte file")
+        except BaseException:
+            fh.close()
             raise
-        end = info.absolute_offset + info.nbytes
-        if end > len(mm):
-            mm.close()
-            f.close()
-            raise UnsupportedModelError(f"{name}: tensor data runs past the end of the file")
-        return f, mm, memoryview(mm)[info.absolute_offset:end]
+        return fh, mapping, memoryview(mapping)[lo:hi]
 
 
 class _Header:
@@ -180,7 +171,7 @@ class _Header:
     def take(self, n: int) -> bytes:
         b = self.f.read(n)
         if len(b) != n:
-            raise UnsupportedModelError("truncated GGUF file")
+            raise UnsupportedModelError(f"GGUF header ends early: wanted {n} bytes at offset {self.pos}")
         self.pos += n
         return b
 
@@ -200,14 +191,14 @@ class _Header:
         if vt is GGUFValueType.ARRAY:
             item = _value_type(self.scalar("<I"))
             return [self.value(item) for _ in range(self.scalar("<Q"))]
-        raise UnsupportedModelError(f"unsupported metadata value type: {vt}")
+        raise UnsupportedModelError(f"metadata values of type {vt.name} cannot be decoded")
 
 
 def _value_type(raw: int) -> GGUFValueType:
     try:
         return GGUFValueType(raw)
     except ValueError:
-        raise UnsupportedModelError(f"unknown GGUF metadata type: {raw}") from None
+        raise UnsupportedModelError(f"metadata value type id {raw} is not defined by GGUF") from None
 
 
 def load_gguf(path: str | Path, *, require_supported_tensors: bool = False) -> GGUFFile:
@@ -217,10 +208,10 @@ def load_gguf(path: str | Path, *, require_supported_tensors: bool = False) -> G
     with path.open("rb") as f:
         h = _Header(f)
         if h.take(4) != GGUF_MAGIC:
-            raise UnsupportedModelError("not a GGUF file")
+            raise UnsupportedModelError(f"{path}: missing GGUF magic")
         version = h.scalar("<I")
         if version not in (2, 3):
-            raise UnsupportedModelError(f"unsupported GGUF version: {version}")
+            raise UnsupportedModelError(f"{path}: GGUF version {version} is not 2 or 3")
         n_tensors, n_meta = h.scalar("<Q"), h.scalar("<Q")
         metadata: dict[str, GGUFMetadataValue] = {}
         for _ in range(n_meta):
@@ -235,18 +226,18 @@ def load_gguf(path: str | Path, *, require_supported_tensors: bool = False) -> G
             try:
                 tt = GGUFTensorType(raw)
             except ValueError:
-                raise UnsupportedModelError(f"unknown GGUF tensor type: {raw}") from None
+                raise UnsupportedModelError(f"tensor {name}: type id {raw} is not a GGUF tensor type") from None
             entries.append((name, dims, tt, h.scalar("<Q")))
         header_end = h.pos
     align_item = metadata.get("general.alignment")
     alignment = int(align_item.value) if align_item is not None else DEFAULT_ALIGNMENT
     if alignment <= 0:
-        raise UnsupportedModelError("GGUF alignment must be positive")
+        raise UnsupportedModelError(f"{path}: general.alignment = {alignment} (must be > 0)")
     data_start = -(-header_end // alignment) * alignment
     tensors = {name: GGUFTensorInfo(name, dims, tt, rel, data_start + rel) for name, dims, tt, rel in entries}
     out = GGUFFile(path, version, metadata, tensors, data_start, alignment)
     if require_supported_tensors:
         for t in tensors.values():
             if t.tensor_type not in GGUF_TYPE_TRAITS:
-                raise UnsupportedModelError(f"unsupported GGUF tensor type {t.tensor_type.name} for {t.name}")
+                raise UnsupportedModelError(f"tensor {t.name}: no block size known for {t.tensor_type.name}")
     return out

@@ -90,6 +90,8 @@ class Runtime:
         self._argmax_out = torch.empty(MAX_ARGMAX_ROWS, dtype=torch.int32, device=self.device)
         self._ws = torch.empty(0, dtype=torch.uint8, device=self.device)
         self.gemm_min_rows = 0
+        self._paging: tuple[torch.Tensor, int, int, int] | None = None
+        self._segments: list[tuple[int, int, int, int]] = []
 
     # ---- helpers ----------------------------------------------------------------------------------
     def _stream(self) -> int:
@@ -190,7 +192,8 @@ class Runtime:
         self.buffers[name] = _Buffer(torch.zeros(int(n), dtype=dtype, device=self.device), elem)
 
     def zero(self, name: str) -> None:
-        self._any_buffer(name).data.zero_()
+        buf = self._any_buffer(name)
+        _lib.check(self._lib.vq_zero(buf.data.data_ptr(), buf.data.numel() * buf.elem, self._stream()), "zero")
 
     def write(self, name: str, data, offset: int = 0) -> None:
         b = self._any_buffer(name)
@@ -209,11 +212,6 @@ class Runtime:
         if offset + count > avail:
             raise ValueError(f"read of {count} elements exceeds buffer {name}")
         return b.data[offset : offset + count].cpu().numpy().tobytes()
-
-    def copy(self, dst: str, dst_offset: int, src: str, src_offset: int, n: int) -> None:
-        d = self._f32_buffer(dst, dst_offset + n)
-        s = self._f32_buffer(src, src_offset + n)
-        d[dst_offset : dst_offset + n].copy_(s[src_offset : src_offset + n].clone())
 
     def buffer_ptr(self, name: str) -> tuple[int, int]:
         b = self._f32_buffer(name, 0)
@@ -398,9 +396,10 @@ class Runtime:
                                           int(window), self._stream()), "attention")
 
     def conv_update(self, x: str, state: str, w: str, out: str, channels: int, K: int, ntok: int = 1,
-                    snap: str | None = None) -> None:
-        """Causal depthwise conv + SiLU stepping through ntok tokens, state [channels][K] updated in place, w an
-        F32 tensor [channels][K] (Runtime_conv_update, qwen_runtime.cu:401-426)."""
+                    snap: str | None = None, write_state: int = 1) -> None:
+        """Causal depthwise conv + SiLU stepping through ntok tokens, state [channels][K] updated in place unless
+        write_state is 0 (a verification pass), w an F32 tensor [channels][K] (Runtime_conv_update,
+        qwen_runtime.cu:397-426,2078-2100)."""
         if ntok < 1:
             raise ValueError("ntok must be positive")
         xb = self._f32_buffer(x, channels * ntok)
@@ -408,16 +407,17 @@ class Runtime:
         ob = self._f32_buffer(out, channels * ntok)
         wt = self._f32_weight(w, channels * K)
         snp = self._f32_buffer(snap, channels * K * (ntok - 1)).data_ptr() if snap is not None else None
-        if K > 8:
-            raise ValueError(f"conv kernel size {K} > 8")
+        if K > _lib.VQ_CONV_MAX_K:
+            raise ValueError(f"conv kernel size {K} > {_lib.VQ_CONV_MAX_K}")
         _lib.check(self._lib.vq_conv_update(xb.data_ptr(), sb.data_ptr(), wt.data_ptr(), ob.data_ptr(), channels, K,
-                                            ntok, snp, self._stream()), "conv_update")
+                                            ntok, snp, int(bool(write_state)), self._stream()), "conv_update")
 
     def gated_delta(self, conv: str, b: str, a: str, ssm_a: str, dt: str, state: str, out: str, key_heads: int,
                     value_heads: int, kd: int, vd: int, eps: float, head_order: int, ntok: int = 1,
-                    snap: str | None = None) -> None:
-        """Gated delta rule stepping through ntok tokens, state [vh][kd][vd] in place; ssm_a and dt are F32
-        tensors of value_heads values (Runtime_gated_delta, qwen_runtime.cu:515-567)."""
+                    snap: str | None = None, write_state: int = 1) -> None:
+        """Gated delta rule stepping through ntok tokens, fp32 state [vh][kd][vd] in place (unless write_state
+        is 0); ssm_a and dt are F32 tensors of value_heads values (Runtime_gated_delta, qwen_runtime.cu:433-567,
+        2139-2165)."""
         if key_heads <= 0 or value_heads % key_heads != 0:
             raise ValueError("value heads must be a multiple of key heads")
         if ntok < 1:
@@ -430,8 +430,176 @@ class Runtime:
         sa, dtt = self._f32_weight(ssm_a, value_heads), self._f32_weight(dt, value_heads)
         snp = self._f32_buffer(snap, state_n * (ntok - 1)).data_ptr() if snap is not None else None
         _lib.check(self._lib.vq_gated_delta(cb.data_ptr(), bb.data_ptr(), ab.data_ptr(), sa.data_ptr(), dtt.data_ptr(),
-                                            sb.data_ptr(), ob.data_ptr(), key_heads, value_heads, kd, vd, float(eps),
-                                            int(head_order), ntok, snp, self._stream()), "gated_delta")
+                                            sb.data_ptr(), 4, ob.data_ptr(), key_heads, value_heads, kd, vd, float(eps),
+                                            int(head_order), ntok, snp, int(bool(write_state)), self._stream()),
+                   "gated_delta")
+
+    def concat_rows(self, dst: str, a: str, b: str, rows: int, width: int) -> None:
+        """dst[r] = [a[r] | b[r]] for rows of width floats (Runtime_concat_rows, qwen_runtime.cu:2567-2587)."""
+        if rows < 0 or width < 0:
+            raise ValueError("rows and width must be non-negative")
+        n = rows * width
+        ab, bb, db = self._f32_buffer(a, n), self._f32_buffer(b, n), self._f32_buffer(dst, 2 * n)
+        _lib.check(self._lib.vq_concat_rows(db.data_ptr(), ab.data_ptr(), bb.data_ptr(), rows, width, self._stream()),
+                   "concat_rows")
+
+    def zero_range(self, name: str, offset: int, n: int) -> None:
+        """Clear n elements of a buffer from offset (Runtime_zero_range, qwen_runtime.cu:2589-2600)."""
+        buf = self._any_buffer(name)
+        if offset < 0 or n < 0 or offset + n > buf.data.numel():
+            raise ValueError("zero_range out of bounds")
+        _lib.check(self._lib.vq_zero(buf.data.data_ptr() + offset * buf.elem, n * buf.elem, self._stream()),
+                   "zero_range")
+
+    # ---- multi-sequence passes (paged KV caches, per-slot recurrent state) --------------------------------------
+    def set_paging(self, page_table: str, page_size: int, pages_per_seq: int, max_slots: int) -> None:
+        """KV caches of the *_seg ops are page pools [page][kv_head][page_size][hd]; the buffer page_table holds
+        int32 page ids [max_slots][pages_per_seq] (Runtime_set_paging, qwen_runtime.cu:2333-2350)."""
+        if page_size < 1 or pages_per_seq < 1 or max_slots < 1:
+            raise ValueError("invalid paging shape")
+        pt = self._f32_buffer(page_table, pages_per_seq * max_slots)
+        self._paging = (pt, int(page_size), int(pages_per_seq), int(max_slots))
+
+    def set_segments(self, segments) -> int:
+        """Row layout of the next *_seg ops: [(slot, pos0, rows[, row0]), ...], rows of a segment being
+        consecutive positions of one sequence slot, stacked in order unless row0 places them. Returns the row
+        after the last segment (Runtime_set_segments, qwen_runtime.cu:2352-2385)."""
+        if self._paging is None:
+            raise RuntimeError("set_paging first")
+        _, page, pps, slots = self._paging
+        table: list[tuple[int, int, int, int]] = []
+        row0 = 0
+        for seg in segments:
+            if not 3 <= len(seg) <= 4:
+                raise TypeError("a segment is (slot, pos0, rows[, row0])")
+            slot, pos0, rows = (int(v) for v in seg[:3])
+            if len(seg) == 4 and int(seg[3]) >= 0:
+                row0 = int(seg[3])
+            if slot < 0 or slot >= slots or pos0 < 0 or rows < 1 or pos0 + rows > page * pps:
+                raise ValueError(f"segment ({slot}, {pos0}, {rows}) outside the paged context")
+            table.append((slot, pos0, rows, row0))
+            row0 += rows
+        if not table:
+            raise ValueError("no segments")
+        self._segments = table
+        return row0
+
+    def _seg_ready(self) -> list[tuple[int, int, int, int]]:
+        if not self._segments or self._paging is None:
+            raise RuntimeError("set_paging and set_segments must be called before *_seg ops")
+        return self._segments
+
+    def _seg_rows(self) -> int:
+        return max(r0 + n for _, _, n, r0 in self._seg_ready())
+
+    def _seg_chunks(self):
+        """The segment table as int32 arrays of at most VQ_MAX_SEGMENTS segments (one launch each)."""
+        segs = self._seg_ready()
+        for i in range(0, len(segs), _lib.VQ_MAX_SEGMENTS):
+            part = segs[i:i + _lib.VQ_MAX_SEGMENTS]
+            yield (ctypes.c_int32 * (4 * len(part)))(*[v for sg in part for v in sg]), len(part)
+
+    def _kv_pair(self, kc: str, vc: str, min_n: int) -> tuple[_Buffer, _Buffer]:
+        """find_kv_buffer for a K/V cache pair of one precision (qwen_runtime.cu:1226-1248)."""
+        kcb, vcb = self._any_buffer(kc), self._any_buffer(vc)
+        for name, buf in ((kc, kcb), (vc, vcb)):
+            if buf.data.numel() < min_n:
+                raise ValueError(f"device buffer {name} has {buf.data.numel()} values, need {min_n}")
+        if kcb.elem != vcb.elem:
+            raise TypeError("K and V caches differ in precision")
+        return kcb, vcb
+
+    def rope_seg(self, x: str, heads: int, hd: int, rot: int, base: float) -> None:
+        """NeoX RoPE with each segment's positions (Runtime_rope_seg, qwen_runtime.cu:2400-2417)."""
+        self._seg_ready()
+        if rot <= 0 or rot % 2 != 0 or rot > hd:
+            raise ValueError(f"invalid rotary dim {rot}")
+        xb = self._f32_buffer(x, heads * hd * self._seg_rows())
+        for arr, n in self._seg_chunks():
+            _lib.check(self._lib.vq_rope_seg(xb.data_ptr(), arr, n, heads, hd, rot, float(base), self._stream()),
+                       "rope_seg")
+
+    def kv_append_seg(self, k: str, v: str, kc: str, vc: str, kv_heads: int, hd: int) -> None:
+        """Append each segment's K/V rows to its sequence's pages (Runtime_kv_append_seg, qwen_runtime.cu:
+        2419-2447)."""
+        self._seg_ready()
+        rowsz = kv_heads * hd
+        kb, vb = self._f32_buffer(k, rowsz * self._seg_rows()), self._f32_buffer(v, rowsz * self._seg_rows())
+        kcb, vcb = self._kv_pair(kc, vc, rowsz)
+        pt, page, pps, _ = self._paging
+        for arr, n in self._seg_chunks():
+            _lib.check(self._lib.vq_kv_append_seg(kb.data_ptr(), vb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(),
+                                                  kcb.elem, arr, n, kv_heads, hd, pt.data_ptr(), page, pps,
+                                                  self._stream()), "kv_append_seg")
+
+    def attention_seg(self, q: str, kc: str, vc: str, out: str, heads: int, kv_heads: int, hd: int) -> None:
+        """Causal attention of each segment over its own pages (Runtime_attention_seg, qwen_runtime.cu:
+        2449-2478)."""
+        self._seg_ready()
+        if kv_heads <= 0 or heads % kv_heads != 0:
+            raise ValueError("heads must be divisible by kv_heads")
+        rowsz = heads * hd
+        qb = self._f32_buffer(q, rowsz * self._seg_rows())
+        kcb, vcb = self._kv_pair(kc, vc, 1)
+        ob = self._f32_buffer(out, rowsz * self._seg_rows())
+        pt, page, pps, _ = self._paging
+        for arr, n in self._seg_chunks():
+            _lib.check(self._lib.vq_attention_seg(qb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(), ob.data_ptr(),
+                                                  kcb.elem, arr, n, heads, kv_heads, hd, pt.data_ptr(), page, pps,
+                                                  self._stream()), "attention_seg")
+
+    def conv_update_seg(self, x: str, state: str, w: str, out: str, channels: int, K: int, snap: str | None = None,
+                        write_state: int = 1) -> None:
+        """Per-segment causal conv over the slot's state [slots][channels][K]; snapshots need a single segment
+        (Runtime_conv_update_seg, qwen_runtime.cu:2480-2511)."""
+        segs = self._seg_ready()
+        if K > _lib.VQ_CONV_MAX_K:
+            raise ValueError(f"conv kernel size {K} > {_lib.VQ_CONV_MAX_K}")
+        ntok, stride = self._seg_rows(), channels * K
+        xb = self._f32_buffer(x, channels * ntok)
+        sb = self._f32_buffer(state, stride * self._paging[3])
+        ob = self._f32_buffer(out, channels * ntok)
+        wt = self._f32_weight(w, stride)
+        snp = None
+        if snap is not None:
+            if len(segs) != 1:
+                raise ValueError("snapshots need a single-segment pass")
+            snp = self._f32_buffer(snap, stride * (ntok - 1)).data_ptr()
+        for arr, n in self._seg_chunks():
+            _lib.check(self._lib.vq_conv_update_seg(xb.data_ptr(), sb.data_ptr(), wt.data_ptr(), ob.data_ptr(), channels,
+                                                    K, arr, n, snp, int(bool(write_state)), self._stream()),
+                       "conv_update_seg")
+
+    def gated_delta_seg(self, conv: str, b: str, a: str, ssm_a: str, dt: str, state: str, out: str, key_heads: int,
+                        value_heads: int, kd: int, vd: int, eps: float, head_order: int, snap: str | None = None,
+                        write_state: int = 1) -> None:
+        """Per-segment gated delta rule over the slot's state [slots][vh][kd][vd], fp32 or fp16 (fp16: no
+        snapshots) (Runtime_gated_delta_seg, qwen_runtime.cu:2513-2565)."""
+        segs = self._seg_ready()
+        if key_heads <= 0 or value_heads % key_heads != 0:
+            raise ValueError("value heads must be a multiple of key heads")
+        ntok = self._seg_rows()
+        conv_dim = 2 * key_heads * kd + value_heads * vd
+        state_n = value_heads * kd * vd
+        cb = self._f32_buffer(conv, conv_dim * ntok)
+        bb, ab = self._f32_buffer(b, value_heads * ntok), self._f32_buffer(a, value_heads * ntok)
+        sbuf = self._any_buffer(state)
+        if sbuf.data.numel() < state_n * self._paging[3]:
+            raise ValueError(f"device buffer {state} has {sbuf.data.numel()} values, need {state_n * self._paging[3]}")
+        ob = self._f32_buffer(out, value_heads * vd * ntok)
+        sa, dtt = self._f32_weight(ssm_a, value_heads), self._f32_weight(dt, value_heads)
+        snp = None
+        if snap is not None:
+            if sbuf.elem == 2:
+                raise ValueError("fp16 SSM state does not support snapshots")
+            if len(segs) != 1:
+                raise ValueError("snapshots need a single-segment pass")
+            snp = self._f32_buffer(snap, state_n * (ntok - 1)).data_ptr()
+        for arr, n in self._seg_chunks():
+            _lib.check(self._lib.vq_gated_delta_seg(cb.data_ptr(), bb.data_ptr(), ab.data_ptr(), sa.data_ptr(),
+                                                    dtt.data_ptr(), sbuf.data.data_ptr(), sbuf.elem, ob.data_ptr(),
+                                                    key_heads, value_heads, kd, vd, float(eps), int(head_order), arr, n,
+                                                    snp, int(bool(write_state)), self._stream()), "gated_delta_seg")
 
     def copy(self, dst: str, dst_off: int, src: str, src_off: int, n: int) -> None:
         """dst[dst_off:+n] = src[src_off:+n] in elements, buffers of one precision (Runtime_copy,
