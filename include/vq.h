@@ -37,6 +37,7 @@ extern "C" {
 #define VQ_ERR_WORKSPACE (-3) /* workspace NULL or smaller than the matching *_bytes query  */
 #define VQ_ERR_ARG (-4)       /* NULL pointer or other invalid argument                     */
 #define VQ_ERR_NOT_INIT (-5)  /* vq_init() has not run on this device                        */
+#define VQ_ERR_TOO_LARGE (-6) /* the call needs more than VQ_NOALLOC_SCRATCH_BYTES of scratch   */
 
 /* GGUF type ids accepted by every entry point (qwen_quant.cuh:17-33, parser.py:33-63). */
 #define VQ_TYPE_F32 0
@@ -112,6 +113,17 @@ int vq_pack_x(const float *x, int ntok, int cols, void *xpack, void *stream);
  * whose numerics contract is Cpu_qmv (qwen_cpu.c:581-641). */
 int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, float *y, void *workspace,
            size_t workspace_bytes, void *stream);
+
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). vq_qmv with no workspace argument: the
+ * small-batch paths' scratch (split-K partial sums, packed activations) lives in one static device array of
+ * VQ_NOALLOC_SCRATCH_BYTES per GPU, set up by vq_init (VQ_ERR_NOT_INIT before it). Same kernels, routing and
+ * results as vq_qmv with vq_qmv_workspace_bytes_for bytes of workspace; calls that would need more scratch
+ * than the array holds return VQ_ERR_TOO_LARGE (e.g. 5 or more tokens of a 248320-row LM head). It allocates
+ * nothing. Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU (different
+ * streams, or several host threads) race and must be serialised by the caller. */
+#define VQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+int vq_qmv_noalloc(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, float *y, void *stream);
 
 /* Group g of x (n floats each): y = x * rsqrt(mean(x^2) + eps) * w, times silu(z) elementwise when z is not
  * NULL; in-place (y == x) allowed. Replaces: Runtime.rmsnorm / Runtime.gated_rmsnorm (qwen_runtime.cu:36-52,

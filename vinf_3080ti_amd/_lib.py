@@ -49,6 +49,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_pack_x": (I, [P, I, I, P, P]),
     "vq_qmv_packed": (I, [I, P, I, I, P, I, P, P]),
     "vq_qmv": (I, [I, P, I, I, P, I, P, P, SZ, P]),
+    "vq_qmv_noalloc": (I, [I, P, I, I, P, I, P, P]),
     "vq_int_partials": (I, [I, P, I, I, P, I, P, P]),
     "vq_qmv_group": (I, [I, I, P, P, P, I, P, I, P]),
     "vq_qmv_group_f32": (I, [I, I, P, P, P, I, P, I, P]),
@@ -62,7 +63,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_argmax_rows": (I, [P, I, I, P, P]),
 }
 
-VQ_OK, VQ_ERR_TYPE, VQ_ERR_SHAPE, VQ_ERR_WORKSPACE, VQ_ERR_ARG, VQ_ERR_NOT_INIT = 0, -1, -2, -3, -4, -5
+VQ_OK, VQ_ERR_TYPE, VQ_ERR_SHAPE, VQ_ERR_WORKSPACE, VQ_ERR_ARG, VQ_ERR_NOT_INIT, VQ_ERR_TOO_LARGE = 0, -1, -2, -3, -4, -5, -6
+VQ_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _lib: ctypes.CDLL | None = None
 

@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include <type_traits>
 
 #include "vq_common.h"
@@ -23,6 +25,14 @@
 #include "vq_mfma_impl.h"
 #include "../../include/vq.h"
 
+
+// ---- static scratch of the no-allocation entry point (vq_qmv_noalloc) -----------------------------------
+// One fixed array in device memory per GPU the library runs on, held until the process ends. Host code never
+// uses the array's name as an address (on the host it names a stand-in, not device memory): vq_init looks up
+// each device's copy with hipGetSymbolAddress and vq_qmv_noalloc passes that pointer to the kernels.
+namespace vq {
+__device__ __align__(256) uint8_t scratch[VQ_NOALLOC_SCRATCH_BYTES];
+}  // namespace vq
 
 namespace {
 
@@ -340,9 +350,16 @@ const char *vq_status_string(int status) {
         case VQ_ERR_WORKSPACE: return "workspace too small";
         case VQ_ERR_ARG: return "invalid argument";
         case VQ_ERR_NOT_INIT: return "library not initialised on this device";
+        case VQ_ERR_TOO_LARGE: return "needs more than the static scratch of the no-allocation entry point";
         default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown error";
     }
 }
+
+namespace {
+constexpr int kMaxDevices = 64;
+void *g_scratch[kMaxDevices];  // per-device address of vq::scratch, set by vq_init
+std::mutex g_scratch_mu;
+}  // namespace
 
 int vq_init(void) {
     int dev = 0;
@@ -350,7 +367,17 @@ int vq_init(void) {
     if (e != hipSuccess) return hip_status(e);
     hipDeviceProp_t prop;
     e = hipGetDeviceProperties(&prop, dev);
-    return hip_status(e);
+    if (e != hipSuccess) return hip_status(e);
+    if (dev < 0 || dev >= kMaxDevices) return VQ_ERR_ARG;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(vq::scratch));
+        if (e != hipSuccess) return hip_status(e);
+        if (p == nullptr) return VQ_ERR_NOT_INIT;
+        g_scratch[dev] = p;
+    }
+    return VQ_OK;
 }
 
 int vq_set_iq3s_grid(const uint8_t *grid) {
@@ -510,6 +537,22 @@ int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int n
     return dispatch_quant(type, [&](auto tc) {
         return vq::launch_quant<decltype(tc)::value>(w, rows, cols, rb, x, true, ntok, y, s);
     });
+}
+
+int vq_qmv_noalloc(int type, const uint8_t *w, int rows, int cols, const float *x, int ntok, float *y, void *stream) {
+    int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    const size_t need = vq_qmv_workspace_bytes_for(type, rows, cols, ntok);
+    if (need > VQ_NOALLOC_SCRATCH_BYTES) return VQ_ERR_TOO_LARGE;
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    void *ws = dev >= 0 && dev < kMaxDevices ? g_scratch[dev] : nullptr;  // written once by vq_init
+    if (ws == nullptr) return VQ_ERR_NOT_INIT;
+    // The same kernels and routing as vq_qmv with a workspace of `need` bytes (none of them needs the scratch
+    // cleared first: every byte a kernel reads back was written earlier in the same call).
+    return vq_qmv(type, w, rows, cols, x, ntok, y, need ? ws : nullptr, need, stream);
 }
 
 static int qmv_group_any(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
