@@ -457,19 +457,42 @@ def time_sweep(torch, sw, steps, warmup, use_graph=True):
     return start.elapsed_time(stop) / steps, graph is not None
 
 
-def cpu_baseline(budget_s=12.0):
-    """The reference's own CPU path (oracle/_ref, compiled from qwen_cpu.c) on a bounded sample of the sweep:
-    each distinct matrix shape timed once at batch 1 (LM head on 1/16 of its rows, scaled), then combined
-    with the per-step counts into an estimated ms per sweep and GB/s."""
+def host_cpu() -> dict:
+    """The box's CPU as lscpu reports it, and the CPUs this process may run on."""
+    info = {"model": None, "sockets": None, "physical_cores": None, "cpus_in_affinity": len(os.sched_getaffinity(0))}
+    try:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        kv = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+        kv = {k.strip(): v.strip() for k, v in kv.items()}
+        info["model"] = kv.get("Model name")
+        sockets = int(kv.get("Socket(s)", "0") or 0)
+        per = int(kv.get("Core(s) per socket", "0") or 0)
+        info["sockets"] = sockets or None
+        info["physical_cores"] = sockets * per or None
+    except (OSError, ValueError):
+        pass
+    return info
+
+
+CPU_SHARE = 16  # host CPUs one GPU's share of the box may keep busy
+
+
+def cpu_child(threads: int) -> dict:
+    """Runs in a child process without torch (OMP_PROC_BIND is fixed when OpenMP starts): the reference's own
+    CPU path (oracle/_ref, compiled from qwen_cpu.c; the C restatement in oracle/ when it is absent) on
+    BASELINE.json configs 1-3 (median of 10 timed calls after one warm-up call each) and on a sample of the
+    27B sweep (each distinct matrix shape, median of 3 calls; the LM head on 1/16 of its rows, scaled)."""
     import glob
     import importlib.util
+    import statistics
 
     import numpy as np
 
     from vinf_3080ti_amd import synth, tables
 
     paths = glob.glob(str(ROOT / "oracle" / "_ref" / "_cpu_qwen*.so"))
-    threads = max(1, min(16, (os.cpu_count() or 2) // 2))
     if paths:
         spec = importlib.util.spec_from_file_location("_cpu_qwen", paths[0])
         mod = importlib.util.module_from_spec(spec)
@@ -477,51 +500,100 @@ def cpu_baseline(budget_s=12.0):
         rt = mod.CpuRuntime(tables.table("iq3s_grid"), threads)
         kind = "reference"
 
-        def run(ty, w, rows, cols, x):
-            rt.add_tensor(f"w{id(w)}", w, ty, cols, rows)
-            rt.alloc("x", cols)
-            rt.alloc("y", rows)
-            rt.write("x", x.tobytes())
-            t0 = time.perf_counter()
-            n = 0
-            while True:
-                rt.qmv(f"w{id(w)}", "x", "y", 1)
-                n += 1
-                if time.perf_counter() - t0 > budget_s / 13:
-                    break
-            return (time.perf_counter() - t0) / n
+        made = []
+
+        def prepare(ty, w, rows, cols, x, ntok):
+            k = len(made)
+            made.append(k)
+            rt.add_tensor(f"w{k}", w, ty, cols, rows)
+            rt.alloc(f"x{k}", cols * ntok)
+            rt.alloc(f"y{k}", rows * ntok)
+            rt.write(f"x{k}", x.tobytes())
+            return lambda: rt.qmv(f"w{k}", f"x{k}", f"y{k}", ntok)
     else:
         from oracle import oracle
 
         kind = "port"
 
-        def run(ty, w, rows, cols, x):
+        def prepare(ty, w, rows, cols, x, ntok):
+            return lambda: oracle.qmv(ty, w, rows, cols, x, ntok, threads=threads)
+
+    def med(fns, reps):
+        for f in fns:
+            f()
+        ts = []
+        for _ in range(reps):
             t0 = time.perf_counter()
-            n = 0
-            while True:
-                oracle.qmv(ty, w, rows, cols, x, 1, threads=threads)
-                n += 1
-                if time.perf_counter() - t0 > budget_s / 13:
-                    break
-            return (time.perf_counter() - t0) / n
+            for f in fns:
+                f()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
 
     rng = np.random.default_rng(5)
-    total_s, total_b = 0.0, 0
+    H, F = 5120, 17408
+    res = {}
+    w1 = synth.baseline_rows(Q4_K, 4096, 4096, rng)
+    x1 = rng.standard_normal(4096).astype(np.float32)
+    t = med([prepare(Q4_K, w1, 4096, 4096, x1, 1)], 10)
+    res["config1_Q4_K_4096x4096_b1"] = {"ms": t * 1e3, "GBps": alg_bytes(Q4_K, 4096, 4096, 1) / t / 1e9}
+    wg, wu = synth.baseline_rows(Q3_K, F, H, rng), synth.baseline_rows(Q3_K, F, H, rng)
+    wd = synth.baseline_rows(Q6_K, H, F, rng)
+    for n in (1, 4, 8):
+        xh, xf = rng.standard_normal(n * H).astype(np.float32), rng.standard_normal(n * F).astype(np.float32)
+        fns = [prepare(Q3_K, wg, F, H, xh, n), prepare(Q3_K, wu, F, H, xh, n), prepare(Q6_K, wd, H, F, xf, n)]
+        t = med(fns, 10)
+        b = 2 * alg_bytes(Q3_K, F, H, n) + alg_bytes(Q6_K, H, F, n)
+        res[f"config2_mlp_b{n}"] = {"ms": t * 1e3, "GBps": b / t / 1e9}
+    for ty in (IQ4_XS, IQ3_S, IQ2_XXS):
+        w3 = synth.baseline_rows(ty, H, F, rng)
+        for n in (1, 8):
+            x3 = rng.standard_normal(n * F).astype(np.float32)
+            t = med([prepare(ty, w3, H, F, x3, n)], 10)
+            res[f"config3_{TYPE_NAMES[ty]}_{H}x{F}_b{n}"] = {"ms": t * 1e3, "GBps": alg_bytes(ty, H, F, n) / t / 1e9}
     counts = {}
     for name, ty, rows, cols, _ in sweep_plan():
-        key = (name.split(".", 2)[-1], ty, rows, cols)
+        key = (ty, rows, cols)
         counts[key] = counts.get(key, 0) + 1
-    for (name, ty, rows, cols), count in counts.items():
+    total_s, total_b = 0.0, 0
+    for (ty, rows, cols), count in counts.items():
         r = rows if rows < 100000 else rows // 16
         w = synth.baseline_rows(ty, r, cols, rng)
         x = rng.standard_normal(cols).astype(np.float32)
-        t = run(ty, w, r, cols, x) * (rows / r)
-        total_s += t * count
+        total_s += med([prepare(ty, w, r, cols, x, 1)], 3) * (rows / r) * count
         total_b += alg_bytes(ty, rows, cols, 1) * count
-    return {"value": total_b / total_s / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
-            "ms_per_step": total_s * 1e3,
-            "sample": "27B sweep, batch 1: each distinct matrix shape timed once (LM head on 1/16 of its rows), "
-                      "weighted by its per-step count"}
+    res["config4_sweep_b1"] = {"ms": total_s * 1e3, "GBps": total_b / total_s / 1e9}
+    return {"kind": kind, "threads": threads, "configs": {k: {a: round(v, 3) for a, v in d.items()} for k, d in res.items()}}
+
+
+def cpu_baseline() -> dict:
+    """The reference CPU path at two thread settings, each in a child process (before this process touches the
+    GPU): the reference's default omp_get_num_procs() / 2 (qwen_cpu.c:438) and all physical cores bound close
+    (OMP_PROC_BIND=close, OMP_PLACES=cores), both capped at the GPU's host share of CPU_SHARE CPUs."""
+    import subprocess
+
+    host = host_cpu()
+    nprocs = host["cpus_in_affinity"]
+    phys = min(host["physical_cores"] or nprocs, nprocs)
+    settings = {"ref_default": (max(1, min(CPU_SHARE, nprocs // 2)), {}),
+                "all_cores_close": (max(1, min(CPU_SHARE, phys)), {"OMP_PROC_BIND": "close", "OMP_PLACES": "cores"})}
+    runs = {}
+    for label, (threads, extra) in settings.items():
+        env = dict(os.environ, **extra, OMP_NUM_THREADS=str(threads))
+        out = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--cpu-child", str(threads)], env=env,
+                             capture_output=True, text=True, timeout=600)
+        if out.returncode != 0:
+            raise RuntimeError(f"cpu baseline child failed: {out.stderr[-2000:]}")
+        runs[label] = json.loads(out.stdout.strip().splitlines()[-1])
+    main_run = runs["ref_default"]
+    sweep = main_run["configs"]["config4_sweep_b1"]
+    return {"value": sweep["GBps"], "unit": "GB/s", "cores": main_run["threads"], "threads": main_run["threads"],
+            "kind": main_run["kind"], "ms_per_step": sweep["ms"], "host": host,
+            "sample": "27B sweep at batch 1 estimated from each distinct matrix shape (median of 3 calls, LM head on "
+                      "1/16 of its rows, scaled) weighted by its per-step count; configs 1-3 timed whole, median "
+                      "of 10 calls after a warm-up call; threads capped at the GPU's host share "
+                      f"({CPU_SHARE})",
+            "settings": {k: {"threads": v["threads"], "env": settings[k][1], "configs": v["configs"]}
+                         for k, v in runs.items()}}
 
 
 def main() -> None:
@@ -537,19 +609,45 @@ def main() -> None:
                     help="only the dominant launch (plus a 256 MiB device copy that calibrates PMC byte counters)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill contraction legs (512 tokens x Q4_K, both shapes)")
+    ap.add_argument("--matvec", default="",
+                    help="only these matvec launches: comma-separated TYPE:ROWS:COLS[:NTOK[:GROUP]] "
+                         "(e.g. IQ2_XXS:5120:17408:1), timed as the per-type legs are")
     ap.add_argument("--mlp-only", action="store_true",
                     help="only the SwiGLU MLP block at batch 1, 4, 8 (as vq_qmv routes) and 8 on the streaming kernel")
+    ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cpu_child:
+        print(json.dumps(cpu_child(args.cpu_child)), flush=True)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (weights shard by rows; see "
               "DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    full = not (args.matvec or args.prefill_only or args.mlp_only or args.roofline_only)
+    cpu = None
+    if full and not args.no_cpu:  # child processes, started before this process initialises the GPU
+        log("cpu baseline: reference CPU path, configs 1-3 and a sample of the sweep, two thread settings")
+        cpu = cpu_baseline()
 
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     hip = Hip(torch)
 
+    if args.matvec:
+        out = {}
+        by_name = {v: k for k, v in TYPE_NAMES.items()}
+        for spec in args.matvec.split(","):
+            f = spec.split(":")
+            ty, rows, cols = by_name[f[0]], int(f[1]), int(f[2])
+            ntok = int(f[3]) if len(f) > 3 else 1
+            group = int(f[4]) if len(f) > 4 else 1
+            r = bench_matvec(torch, hip, ty, rows, cols, ntok, iters=100, group=group)
+            out[spec] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+            log(f"{spec}: {out[spec]['us']} us, {out[spec]['GBps']} GB/s")
+        print(json.dumps({"matvec": out}), flush=True)
+        return
     if args.prefill_only:
         out = {}
         for rows, cols in ((17408, 5120), (5120, 17408)):
@@ -575,6 +673,8 @@ def main() -> None:
         "frac": round(dom["frac"], 4),
         "avg_us": round(dom["us"], 3),
         "traffic": traffic,
+        # not counted in this run: the committed rocprofv3 PMC summary of the same launch and command
+        "traffic_source": "profiles/qmv_q3k_gateup_2x17408x5120_pmc.md (rocprofv3 FETCH_SIZE / WRITE_SIZE)",
     }
     if args.roofline_only:
         a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -641,11 +741,6 @@ def main() -> None:
         sweep4 = {"ms_per_step": round(ms4, 4), "GBps": round(sw4.bytes / (ms4 * 1e-3) / 1e9, 2),
                   "frac": round(sw4.bytes / (ms4 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
         del sw4
-
-    cpu = None
-    if not args.no_cpu:
-        log("cpu baseline: reference CPU path on a bounded sample")
-        cpu = cpu_baseline()
 
     out = {
         "metric": METRIC,
