@@ -96,11 +96,11 @@ def alg_bytes(ty, rows, cols, ntok):
 class Hip:
     """Thin layer over the C ABI with torch-owned device memory."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, lib_path=None):
         from vinf_3080ti_amd import _lib
 
         self.torch = torch
-        self.lib = _lib.load()
+        self.lib = _lib.load(Path(lib_path) if lib_path else None)
         _lib.check(self.lib.vq_init(), "vq_init")
         self.stream = torch.cuda.current_stream()
 
@@ -223,6 +223,40 @@ def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=
     torch.cuda.empty_cache()
     return {"us": ms * 1e3, "GBps": b / (ms * 1e-3) / 1e9, "bytes": b, "frac": b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
             "copies": copies}
+
+
+def ab_matvec(torch, hips, ty, rows, cols, ntok, group=1, reps=5, iters=100, min_rotation_bytes=640 << 20):
+    """The bench_matvec launch for several builds of the library (one Hip per build) on the same weights,
+    interleaved rep by rep, so that box-to-box and run-to-run drift hits every build alike: per build the
+    median and minimum µs per launch over `reps` graph replays of `iters` launches."""
+    import statistics
+
+    nbytes = rows * row_bytes_of(ty, cols) * group
+    copies = max(2, -(-min_rotation_bytes // nbytes))
+    ws = make_weights(torch, ty, rows, cols, 1234 + ty, copies * group)
+    x = torch.randn(ntok, cols, device="cuda")
+    ys = [torch.empty(ntok, rows, device="cuda") for _ in range(group)]
+    times = [[] for _ in hips]
+    for _ in range(reps):
+        for k, hip in enumerate(hips):
+            def launch(i, hip=hip):
+                c = i % copies
+                hip.group_f32(ty, ws[c * group:(c + 1) * group], [rows] * group, ys, cols, x, ntok)
+
+            for i in range(copies):
+                launch(i)
+            times[k].append(time_kernel_loop(torch, launch, iters) * 1e3)
+    b = alg_bytes(ty, rows, cols, ntok) * group
+    del ws
+    torch.cuda.empty_cache()
+    return [{"med_us": round(statistics.median(t), 3), "min_us": round(min(t), 3),
+             "GBps_med": round(b / (statistics.median(t) * 1e-6) / 1e9, 1)} for t in times]
+
+
+def row_bytes_of(ty, cols):
+    from vinf_3080ti_amd import row_bytes
+
+    return row_bytes(ty, cols)
 
 
 MFMA_INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, AMD-published (no sparsity)
@@ -612,6 +646,8 @@ def main() -> None:
     ap.add_argument("--matvec", default="",
                     help="only these matvec launches: comma-separated TYPE:ROWS:COLS[:NTOK[:GROUP]] "
                          "(e.g. IQ2_XXS:5120:17408:1), timed as the per-type legs are")
+    ap.add_argument("--libs", default="",
+                    help="with --matvec: comma-separated builds of libvq_hip.so compared launch for launch")
     ap.add_argument("--mlp-only", action="store_true",
                     help="only the SwiGLU MLP block at batch 1, 4, 8 (as vq_qmv routes) and 8 on the streaming kernel")
     ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
@@ -635,9 +671,26 @@ def main() -> None:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     hip = Hip(torch)
 
+    if args.matvec and args.libs:
+        hips = [Hip(torch, p) for p in args.libs.split(",")]
+        from vinf_3080ti_amd import GGUFTensorType
+
+        by_name = {t.name: int(t) for t in GGUFTensorType}
+        out = {}
+        for spec in args.matvec.split(","):
+            f = spec.split(":")
+            ntok = int(f[3]) if len(f) > 3 else 1
+            group = int(f[4]) if len(f) > 4 else 1
+            r = ab_matvec(torch, hips, by_name[f[0]], int(f[1]), int(f[2]), ntok, group)
+            out[spec] = dict(zip(args.libs.split(","), r))
+            log(spec + ": " + "  ".join(f"{Path(p).stem} {v['med_us']} (min {v['min_us']})" for p, v in out[spec].items()))
+        print(json.dumps({"ab": out}), flush=True)
+        return
     if args.matvec:
         out = {}
-        by_name = {v: k for k, v in TYPE_NAMES.items()}
+        from vinf_3080ti_amd import GGUFTensorType
+
+        by_name = {t.name: int(t) for t in GGUFTensorType}
         for spec in args.matvec.split(","):
             f = spec.split(":")
             ty, rows, cols = by_name[f[0]], int(f[1]), int(f[2])

@@ -11,9 +11,9 @@
 // (/root/reference/engine/csrc/cpu/qwen_cpu.c:125-342) regrouped per 16 elements.
 //
 // Codes with an offset (Q3_K: lo|hb<<2 - 4, Q6_K: q - 32) are dotted unsigned and corrected with the
-// integer X (S = dot(q) - off*X): exact, and cheaper than a bytewise subtract. Sign-coded IQ grids
-// apply signs as (g ^ m) + e with per-byte masks m in {0x00, 0xFF} and e = m & 1 from an LDS table
-// (grid magnitudes are >= 1, so no byte carries).
+// integer X (S = dot(q) - off*X): exact, and cheaper than a bytewise subtract. Sign-coded IQ grids take
+// their signs in registers (sign4: a byte permute between the magnitudes and their negation), so the only
+// LDS table an IQ slice reads is its grid.
 //
 // Block layouts: qwen_quant.cuh:151-279 / dequant.py:121-500 (ggml).
 #pragma once
@@ -130,6 +130,23 @@ __device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t width
     return __builtin_amdgcn_ubfe(v, off, width);
 }
 __device__ __forceinline__ uint32_t sgn(uint32_t g, uint32_t m, uint32_t e) { return (g ^ m) + e; }
+
+// Bytes of g (grid magnitudes, every byte >= 1) negated where bit k of s4 (4 sign bits) is set, in registers:
+// v_perm_b32 picks byte k of g or of -g, the bytewise negation (~g) + 0x01010101 (carry-free since no byte of
+// g is 0). The selector puts bit k at bit 2 of byte k (s4 * 0x00810204 moves bit k to bit 8k + 2 without
+// overlap, s4 < 16) over the identity 0x03020100.
+__device__ __forceinline__ uint32_t sign4(uint32_t g, uint32_t s4) {
+    const uint32_t neg = (g ^ 0xFFFFFFFFu) + 0x01010101u;
+    const uint32_t sel = (__umul24(s4, 0x00810204u) & 0x04040404u) | 0x03020100u;
+    return __builtin_amdgcn_perm(neg, g, sel);
+}
+// ggml's 7 stored sign bits with the even-parity 8th at bit 7 (bits above 7 may be set: callers take bits 0-7).
+__device__ __forceinline__ uint32_t ksigns8(uint32_t b7) { return b7 | (__builtin_popcount(b7) << 7); }
+// Signs of 8 magnitudes (two words) from 8 sign bits.
+__device__ __forceinline__ void sign8(uint2 g, uint32_t s8, uint32_t &lo, uint32_t &hi) {
+    lo = sign4(g.x, bfe(s8, 0, 4));
+    hi = sign4(g.y, bfe(s8, 4, 4));
+}
 
 // IQ4_NL codebook lookup of 4 nibbles (one per byte, 0..15): two v_perm_b32 over the 16 table bytes and a
 // third that picks per byte by bit 3.
@@ -547,6 +564,12 @@ struct Sl<VQ_IQ4_XS> {
         sc[0] = sc[1] = half_to_float(w.hd[0]) * static_cast<float>(static_cast<int>(ls) - 32);
         mn[0] = mn[1] = 0.0f;
     }
+    // Integer form: group s weighs d (ls - 32).
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.hd[0]); }
+    static __device__ __forceinline__ void iscales(const W &w, int s, int (&isc)[NP]) {
+        isc[0] = isc[1] = static_cast<int>(bfe(w.hd[1], 4 * s, 4) | (bfe(w.hd[0], 16 + 2 * s, 2) << 4)) - 32;
+    }
 };
 
 // ---- IQ2_XXS: 66 B = d, then per group j: aux0 (4 grid indices), aux1 (4 x 7 sign bits, 4-bit scale).
@@ -569,16 +592,19 @@ struct Sl<VQ_IQ2_XXS> {
     static __device__ __forceinline__ void codes(const W &w, int, const Tabs &tb, uint32_t (&cc)[NP][4]) {
         const uint32_t a0 = w.a.word(0), a1 = w.a.word(1);
 #pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            const uint2 g = tb.grid8[bfe(a0, 8 * l, 8)];
-            const uint4 m = tb.ks128[bfe(a1, 7 * l, 7)];
-            cc[l >> 1][2 * (l & 1)] = sgn(g.x, m.x, m.z);
-            cc[l >> 1][2 * (l & 1) + 1] = sgn(g.y, m.y, m.w);
-        }
+        for (int l = 0; l < 4; ++l)
+            sign8(tb.grid8[bfe(a0, 8 * l, 8)], ksigns8(bfe(a1, 7 * l, 7)), cc[l >> 1][2 * (l & 1)],
+                  cc[l >> 1][2 * (l & 1) + 1]);
     }
     static __device__ __forceinline__ void scales(const W &w, int, float *sc, float *mn) {
         sc[0] = sc[1] = half_to_float(w.d.lo()) * (0.5f + static_cast<float>(w.a.word(1) >> 28)) * 0.25f;
         mn[0] = mn[1] = 0.0f;
+    }
+    // Integer form: d (0.5 + s) / 4 = (d / 8) (2 s + 1).
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.d.lo()) * 0.125f; }
+    static __device__ __forceinline__ void iscales(const W &w, int, int (&isc)[NP]) {
+        isc[0] = isc[1] = static_cast<int>(2 * (w.a.word(1) >> 28) + 1);
     }
 };
 
@@ -605,10 +631,7 @@ struct Sl<VQ_IQ2_XS> {
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             const uint32_t q = bfe(a[l >> 1], 16 * (l & 1), 16);
-            const uint2 g = tb.grid8[q & 511u];
-            const uint4 m = tb.ks128[q >> 9];
-            cc[l >> 1][2 * (l & 1)] = sgn(g.x, m.x, m.z);
-            cc[l >> 1][2 * (l & 1) + 1] = sgn(g.y, m.y, m.w);
+            sign8(tb.grid8[q & 511u], ksigns8(q >> 9), cc[l >> 1][2 * (l & 1)], cc[l >> 1][2 * (l & 1) + 1]);
         }
     }
     static __device__ __forceinline__ void scales(const W &w, int, float *sc, float *mn) {
@@ -617,6 +640,14 @@ struct Sl<VQ_IQ2_XS> {
         sc[0] = d * (0.5f + static_cast<float>(b & 15)) * 0.25f;
         sc[1] = d * (0.5f + static_cast<float>(bfe(b, 4, 4))) * 0.25f;
         mn[0] = mn[1] = 0.0f;
+    }
+    // Integer form: half h weighs (d / 8) (2 s_h + 1).
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.d.lo()) * 0.125f; }
+    static __device__ __forceinline__ void iscales(const W &w, int, int (&isc)[NP]) {
+        const uint32_t b = w.sc.lo();
+        isc[0] = static_cast<int>(2 * (b & 15) + 1);
+        isc[1] = static_cast<int>(2 * bfe(b, 4, 4) + 1);
     }
 };
 
@@ -645,10 +676,7 @@ struct Sl<VQ_IQ2_S> {
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             const uint32_t idx = bfe(qs, 8 * l, 8) | (bfe(qh, 2 * l, 2) << 8);
-            const uint2 g = tb.grid8[idx];
-            const uint4 m = tb.sm256[bfe(sg, 8 * l, 8)];
-            cc[l >> 1][2 * (l & 1)] = sgn(g.x, m.x, m.z);
-            cc[l >> 1][2 * (l & 1) + 1] = sgn(g.y, m.y, m.w);
+            sign8(tb.grid8[idx], bfe(sg, 8 * l, 8), cc[l >> 1][2 * (l & 1)], cc[l >> 1][2 * (l & 1) + 1]);
         }
     }
     static __device__ __forceinline__ void scales(const W &w, int, float *sc, float *mn) {
@@ -657,6 +685,14 @@ struct Sl<VQ_IQ2_S> {
         sc[0] = d * (0.5f + static_cast<float>(b & 15)) * 0.25f;
         sc[1] = d * (0.5f + static_cast<float>(bfe(b, 4, 4))) * 0.25f;
         mn[0] = mn[1] = 0.0f;
+    }
+    // Integer form: half h weighs (d / 8) (2 s_h + 1).
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.d.lo()) * 0.125f; }
+    static __device__ __forceinline__ void iscales(const W &w, int, int (&isc)[NP]) {
+        const uint32_t b = w.sc.lo();
+        isc[0] = static_cast<int>(2 * (b & 15) + 1);
+        isc[1] = static_cast<int>(2 * bfe(b, 4, 4) + 1);
     }
 };
 
@@ -684,16 +720,19 @@ struct Sl<VQ_IQ3_XXS> {
         const uint32_t aux = w.aux.word(0);
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            const uint32_t g1 = tb.grid4[bfe(q[l >> 1], 16 * (l & 1), 8)];
-            const uint32_t g2 = tb.grid4[bfe(q[l >> 1], 16 * (l & 1) + 8, 8)];
-            const uint4 m = tb.ks128[bfe(aux, 7 * l, 7)];
-            cc[l >> 1][2 * (l & 1)] = sgn(g1, m.x, m.z);
-            cc[l >> 1][2 * (l & 1) + 1] = sgn(g2, m.y, m.w);
+            const uint2 g{tb.grid4[bfe(q[l >> 1], 16 * (l & 1), 8)], tb.grid4[bfe(q[l >> 1], 16 * (l & 1) + 8, 8)]};
+            sign8(g, ksigns8(bfe(aux, 7 * l, 7)), cc[l >> 1][2 * (l & 1)], cc[l >> 1][2 * (l & 1) + 1]);
         }
     }
     static __device__ __forceinline__ void scales(const W &w, int, float *sc, float *mn) {
         sc[0] = sc[1] = half_to_float(w.d.lo()) * (0.5f + static_cast<float>(w.aux.word(0) >> 28)) * 0.5f;
         mn[0] = mn[1] = 0.0f;
+    }
+    // Integer form: d (0.5 + s) / 2 = (d / 4) (2 s + 1).
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.d.lo()) * 0.25f; }
+    static __device__ __forceinline__ void iscales(const W &w, int, int (&isc)[NP]) {
+        isc[0] = isc[1] = static_cast<int>(2 * (w.aux.word(0) >> 28) + 1);
     }
 };
 
@@ -729,9 +768,9 @@ struct Sl<VQ_IQ3_S> {
                 const int l0 = 2 * m2, l1 = 2 * m2 + 1;
                 const uint32_t i0 = bfe(q[l0 >> 2], 8 * (l0 & 3), 8) | (bfe(qh, 8 * gg + l0, 1) << 8);
                 const uint32_t i1 = bfe(q[l1 >> 2], 8 * (l1 & 3), 8) | (bfe(qh, 8 * gg + l1, 1) << 8);
-                const uint4 m = tb.sm256[bfe(sg, 8 * m2, 8)];
-                cc[2 * gg + (l0 >> 2)][l0 & 3] = sgn(tb.grid4[i0], m.x, m.z);
-                cc[2 * gg + (l1 >> 2)][l1 & 3] = sgn(tb.grid4[i1], m.y, m.w);
+                const uint32_t s8 = bfe(sg, 8 * m2, 8);
+                cc[2 * gg + (l0 >> 2)][l0 & 3] = sign4(tb.grid4[i0], s8 & 15u);
+                cc[2 * gg + (l1 >> 2)][l1 & 3] = sign4(tb.grid4[i1], s8 >> 4);
             }
         }
     }
@@ -744,6 +783,14 @@ struct Sl<VQ_IQ3_S> {
             sc[2 * gg] = sc[2 * gg + 1] = v;
             mn[2 * gg] = mn[2 * gg + 1] = 0.0f;
         }
+    }
+    // Integer form: group gg of the slice weighs d (1 + 2 s_gg).
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ float dmul(const W &w) { return half_to_float(w.d.lo()); }
+    static __device__ __forceinline__ void iscales(const W &w, int, int (&isc)[NP]) {
+        const uint32_t b = w.sc.lo();
+        isc[0] = isc[1] = static_cast<int>(1 + 2 * (b & 15));
+        isc[2] = isc[3] = static_cast<int>(1 + 2 * bfe(b, 4, 4));
     }
 };
 

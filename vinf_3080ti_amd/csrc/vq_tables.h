@@ -81,8 +81,9 @@ template <int T>
 struct TabSpec {
     static constexpr int n8 = T == VQ_IQ2_XXS ? 256 : T == VQ_IQ2_XS ? 512 : T == VQ_IQ2_S ? 1024 : 0;
     static constexpr int n4 = T == VQ_IQ3_XXS ? 256 : T == VQ_IQ3_S ? 512 : 0;
-    static constexpr bool ks = T == VQ_IQ2_XXS || T == VQ_IQ2_XS || T == VQ_IQ3_XXS;
-    static constexpr bool sm = T == VQ_IQ2_S || T == VQ_IQ3_S;
+    // Sign tables: no decoder reads them any more (signs are built in registers, sign4 in vq_slices.h).
+    static constexpr bool ks = false;
+    static constexpr bool sm = false;
 };
 
 // Workgroup-wide: fill the LDS tables type T needs (caller synchronises afterwards).
