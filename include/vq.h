@@ -156,6 +156,10 @@ int vq_zero(void *p, size_t nbytes, void *stream);
  * 2333-2350); every pos0 + rows must fit in page_size * pages_per_seq. */
 #define VQ_MAX_SEGMENTS 64
 #define VQ_CONV_MAX_K 8
+/* Attention of a pass whose longest segment has more rows than this (a prompt pass) runs on the tiled MFMA
+ * kernel (K/V read once per 16 query rows), else on the per-row decode kernel; results agree within fp32
+ * rounding. The reference switches at the same row count (kMaxTokens, qwen_runtime.cu:572,2003). */
+#define VQ_ATTN_ROW_MAX 8
 
 /* NeoX RoPE in place on x [ntok][heads][hd], dims [0, rot) of each head, token t at position pos0 + t:
  * (x[j], x[j + rot/2]) turns by (pos0 + t) * base^(-2j/rot). Replaces: Runtime.rope (qwen_runtime.cu:81-92,

@@ -366,3 +366,52 @@ def test_gated_delta_seg_snapshots_single_segment(rt, oracle_mod):
     assert np.array_equal(st[0], s0[0]) and np.array_equal(st[2], s0[2])
     rt.free("gsa")
     rt.free("gdt")
+
+
+# ---- prompt passes: the tiled MFMA attention (more than VQ_ATTN_ROW_MAX rows) -------------------------------
+
+@pytest.mark.parametrize("elem", [4, 2])
+@pytest.mark.parametrize("heads,kvh,hd", [(QW_HEADS, QW_KVH, QW_HD), (8, 2, 128), (6, 6, 64), (4, 1, 40)])
+@pytest.mark.parametrize("ntok,seq_len,bidirectional,window", [(37, 1, 0, 0), (16, 300, 0, 0), (9, 50, 1, 0),
+                                                               (70, 20, 0, 33)])
+def test_prompt_attention_matches_oracle(rt, oracle_mod, elem, heads, kvh, hd, ntok, seq_len, bidirectional, window):
+    """attention over more than 8 query rows (the MFMA kernel; the reference's tiled / tensor-core prompt kernels,
+    qwen_runtime.cu:181-393): GQA groups of 6, 4, 1 and 4 heads (one workgroup holds 4), hd 256 / 128 / 64 and a
+    ragged 40, causal from position 0, after a cached prefix, bidirectional and sliding window; fp32 operands
+    and accumulation, so held to the decode kernel's bar."""
+    rng = np.random.default_rng(ntok * 31 + hd + heads + elem + window)
+    max_seq = seq_len + ntok + 3
+    q = rng.standard_normal((ntok, heads, hd)).astype(np.float32)
+    dt = np.float32 if elem == 4 else np.float16
+    kc = (rng.standard_normal((kvh, max_seq, hd)) * 0.3).astype(dt)
+    vc = rng.standard_normal((kvh, max_seq, hd)).astype(dt)
+    put(rt, "aq", q)
+    put(rt, "ao", np.full(q.size, np.nan))
+    put(rt, "akc", kc, elem)
+    put(rt, "avc", vc, elem)
+    rt.attention("aq", "akc", "avc", "ao", heads, kvh, hd, max_seq, seq_len, ntok, bidirectional, window)
+    ref = oracle_mod.attention(q, kc, vc, heads, kvh, seq_len, bool(bidirectional), window)
+    assert np.allclose(get(rt, "ao", (ntok, heads, hd)), ref, rtol=2e-5, atol=2e-5)
+
+
+@pytest.mark.parametrize("elem", [4, 2])
+def test_prompt_attention_seg(rt, oracle_mod, elem):
+    """attention_seg of a mixed pass: a 45-row prompt segment, an 11-row one after a cached prefix and two decode
+    rows, over paged caches (the MFMA kernel takes the whole pass)."""
+    rng = np.random.default_rng(123 + elem)
+    heads, kvh, hd = QW_HEADS, QW_KVH, QW_HD
+    pt, pool_k, pool_v = paging(rt, rng, kvh, hd, elem)
+    segs = [(1, 0, 45), (4, 100, 11), (2, 150, 1), (0, 7, 1)]
+    n = rt.set_segments(segs)
+    q = rng.standard_normal((n, heads, hd)).astype(np.float32)
+    put(rt, "sq", q)
+    put(rt, "so", np.full(q.size, np.nan))
+    rt.attention_seg("sq", "pk", "pv", "so", heads, kvh, hd)
+    got = get(rt, "so", (n, heads, hd))
+    row = 0
+    for slot, pos0, m in segs:
+        kc = oracle_mod.gather_paged(pool_k, pt[slot], PAGE, kvh, pos0 + m)
+        vc = oracle_mod.gather_paged(pool_v, pt[slot], PAGE, kvh, pos0 + m)
+        ref = oracle_mod.attention(q[row:row + m], kc, vc, heads, kvh, pos0 + 1)
+        assert np.allclose(got[row:row + m], ref, rtol=2e-5, atol=2e-5), (slot, pos0, m)
+        row += m

@@ -327,6 +327,133 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(const float 
     }
 }
 
+// ---- attention over many query rows (prompt passes): flash-style on fp32 MFMA ----------------------------------
+
+// A workgroup takes 16 query rows (tokens) of one segment and up to four query heads of one kv head (one wave
+// each), so the K/V tiles it stages in LDS serve all of them. Per 16 keys a wave computes S^T = K Q^T (16 keys x
+// 16 query rows) with v_mfma_f32_16x16x4f32 over the head dims (Q, pre-scaled by 1/sqrt(hd), stays in registers
+// as the B operand for the whole pass), keeps an online softmax per query row (running max m, sum l; the output
+// rescaled by e^(m_old - m_new)), and adds O^T += V^T P^T. The accumulator of S^T already holds P^T in the
+// layout the second product's B operand needs: its step r takes key 4 g + r in the k slot of lane group g (the
+// contraction runs over the keys in that order), so no transpose goes through LDS. fp32 operands and
+// accumulation throughout. Visibility rules of attention_kernel.
+constexpr int kFaKeys = 32;  // keys per LDS tile
+typedef float fa4 __attribute__((ext_vector_type(4)));
+
+template <typename C, int HD>
+__global__ __launch_bounds__(256) void attention_mfma_kernel(const float *__restrict__ q, const C *__restrict__ kc,
+                                                             const C *__restrict__ vc, float *__restrict__ out,
+                                                             SegTable T, KvMap M, int heads, int hd, int bidirectional,
+                                                             int window, int chunks) {
+    constexpr int LD = HD + 4;  // row stride of the tiles: fragment reads of 16 rows x 4 or 4 rows x 16 hit 64 banks
+    __shared__ float sk[kFaKeys * LD], sv[kFaKeys * LD];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    int tb = blockIdx.x, si = 0;  // (segment, 16-row tile) of this workgroup
+    while (si + 1 < T.n && tb >= (T.s[si].rows + 15) / 16) {
+        tb -= (T.s[si].rows + 15) / 16;
+        ++si;
+    }
+    const Seg &s = T.s[si];
+    const int G = heads / M.kv_heads;
+    const int kvh = blockIdx.y / chunks, gi = (blockIdx.y - kvh * chunks) * 4 + wv;
+    const bool wave_on = gi < G;
+    const int h = kvh * G + (wave_on ? gi : 0);
+    const int t0 = 16 * tb, nq = min(16, s.rows - t0);
+    const int seq_len0 = s.pos0 + 1;
+    auto q_end = [&](int t) { return bidirectional ? seq_len0 + s.rows - 1 : seq_len0 + t; };
+    auto q_start = [&](int t) { return window > 0 && seq_len0 + t > window ? seq_len0 + t - window : 0; };
+    const int kbeg = q_start(t0), kend = q_end(t0 + nq - 1);
+    const int tq = t0 + min(col, nq - 1);  // this lane's query row (rows past nq repeat the last; not written)
+    const int qs = q_start(tq), qe = q_end(tq);
+    const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+    float qf[HD / 4];
+    {
+        const float *qrow = q + (static_cast<size_t>(s.row0 + tq) * heads + h) * hd;
+#pragma unroll
+        for (int st = 0; st < HD / 4; ++st) {
+            const int d = 4 * st + grp;
+            qf[st] = d < hd ? qrow[d] * scale : 0.0f;
+        }
+    }
+    float m = -INFINITY, l = 0.0f;
+    fa4 o[HD / 16];
+#pragma unroll
+    for (int b = 0; b < HD / 16; ++b) o[b] = fa4{0.f, 0.f, 0.f, 0.f};
+
+    for (int k0 = kbeg; k0 < kend; k0 += kFaKeys) {
+        __syncthreads();  // the previous tile is consumed
+        for (int i = threadIdx.x; i < kFaKeys * (HD / 4); i += 256) {
+            const int key = i / (HD / 4), d = 4 * (i - key * (HD / 4)), p = k0 + key;
+            float4 kv4{0.f, 0.f, 0.f, 0.f}, vv4{0.f, 0.f, 0.f, 0.f};
+            if (p < kend && d < hd) {
+                const size_t r = M.row(s.slot, kvh, p) * hd + d;
+                kv4.x = kv_get(kc, r);
+                vv4.x = kv_get(vc, r);
+                if (d + 1 < hd) kv4.y = kv_get(kc, r + 1), vv4.y = kv_get(vc, r + 1);
+                if (d + 2 < hd) kv4.z = kv_get(kc, r + 2), vv4.z = kv_get(vc, r + 2);
+                if (d + 3 < hd) kv4.w = kv_get(kc, r + 3), vv4.w = kv_get(vc, r + 3);
+            }
+            *reinterpret_cast<float4 *>(sk + key * LD + d) = kv4;
+            *reinterpret_cast<float4 *>(sv + key * LD + d) = vv4;
+        }
+        __syncthreads();
+        if (!wave_on) continue;
+#pragma unroll
+        for (int sub = 0; sub < kFaKeys / 16; ++sub) {
+            const int kb = k0 + 16 * sub;
+            if (kb >= kend) break;
+            const float *kt = sk + (16 * sub) * LD, *vt = sv + (16 * sub) * LD;
+            fa4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < HD / 4; ++st)
+                sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kt[col * LD + 4 * st + grp], qf[st], sc, 0, 0, 0);
+            // sc[r]: key kb + 4 grp + r, query row tq
+            float v[4], bm = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int p = kb + 4 * grp + r;
+                v[r] = p >= qs && p < qe ? sc[r] : -INFINITY;
+                bm = fmaxf(bm, v[r]);
+            }
+            bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+            const float mn = fmaxf(m, bm);
+            const float alpha = mn == -INFINITY ? 1.0f : expf(m - mn);  // 0 on the first visible block
+            float pr[4], ps = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pr[r] = v[r] == -INFINITY ? 0.0f : expf(v[r] - mn);
+                ps += pr[r];
+            }
+            ps += __shfl_xor(ps, 16, 64);
+            ps += __shfl_xor(ps, 32, 64);
+            l = l * alpha + ps;
+            m = mn;
+#pragma unroll
+            for (int b = 0; b < HD / 16; ++b) o[b] *= alpha;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int b = 0; b < HD / 16; ++b)
+                    o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(vt[(4 * grp + r) * LD + 16 * b + col], pr[r], o[b], 0,
+                                                                0, 0);
+        }
+    }
+    // o[b][r]: head dim 16 b + 4 grp + r of query row tq
+    if (wave_on && col < nq) {
+        float *orow = out + (static_cast<size_t>(s.row0 + t0 + col) * heads + h) * hd;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int b = 0; b < HD / 16; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int d = 16 * b + 4 * grp + r;
+                if (d < hd) orow[d] = o[b][r] * inv;
+            }
+    }
+}
+
 // ---- causal conv update ----------------------------------------------------------------------------------
 
 // Depthwise causal conv + SiLU, one thread per (channel, segment), the K-tap window in registers (K a template
@@ -505,11 +632,39 @@ int launch_kv_append(const float *k, const float *v, void *kc, void *vc, int ele
     return status_of(hipGetLastError());
 }
 
+template <typename C>
+void launch_attention_mfma(const float *q, const C *kc, const C *vc, float *out, const SegTable &T, const KvMap &M,
+                           int heads, int hd, int bidirectional, int window, hipStream_t s) {
+    int tiles = 0;
+    for (int i = 0; i < T.n; ++i) tiles += (T.s[i].rows + 15) / 16;
+    const int chunks = (heads / M.kv_heads + 3) / 4;
+    const dim3 grid(tiles, M.kv_heads * chunks);
+    if (hd <= 64)
+        attention_mfma_kernel<C, 64><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
+    else if (hd <= 128)
+        attention_mfma_kernel<C, 128><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
+    else
+        attention_mfma_kernel<C, 256><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
+}
+
 int launch_attention(const float *q, const void *kc, const void *vc, float *out, int elem, const SegTable &T,
                      const KvMap &M, int heads, int hd, int bidirectional, int window, hipStream_t s) {
     if (!q || !kc || !vc || !out || (elem != 2 && elem != 4)) return VQ_ERR_ARG;
     if (M.kv_heads < 1 || heads < M.kv_heads || heads % M.kv_heads || hd < 1 || hd > kAttnMaxHd || window < 0)
         return VQ_ERR_SHAPE;
+    // Passes with a segment of more than VQ_ATTN_ROW_MAX rows (prompt passes): the MFMA kernel reads each K/V
+    // tile once per 16 query rows and 4 heads; decode and verify passes: one workgroup per (head, row).
+    int max_rows = 0;
+    for (int i = 0; i < T.n; ++i) max_rows = T.s[i].rows > max_rows ? T.s[i].rows : max_rows;
+    if (max_rows > VQ_ATTN_ROW_MAX) {
+        if (elem == 2)
+            launch_attention_mfma(q, static_cast<const _Float16 *>(kc), static_cast<const _Float16 *>(vc), out, T, M,
+                                  heads, hd, bidirectional, window, s);
+        else
+            launch_attention_mfma(q, static_cast<const float *>(kc), static_cast<const float *>(vc), out, T, M, heads,
+                                  hd, bidirectional, window, s);
+        return status_of(hipGetLastError());
+    }
     const dim3 grid(heads, T.total);
     if (elem == 2)
         attention_kernel<_Float16><<<grid, 64 * kAttnWaves, 0, s>>>(q, static_cast<const _Float16 *>(kc),
