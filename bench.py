@@ -253,6 +253,85 @@ def ab_matvec(torch, hips, ty, rows, cols, ntok, group=1, reps=5, iters=100, min
              "GBps_med": round(b / (statistics.median(t) * 1e-6) / 1e9, 1)} for t in times]
 
 
+MFMA_F32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA, AMD-published
+
+
+def bench_ops(torch, hip):
+    """The sequence ops around the matvec at the qwen35-27B shapes (48 value heads x kd 128 x vd 128 gated delta
+    with a 10240-channel K=4 conv; 24 query heads over 4 kv heads, hd 256 attention), each timed alone in a
+    hipGraph of back-to-back launches. HBM-bound ops report bytes per call (state read + written once, inputs,
+    outputs) and their fraction of 8 TB/s; the prompt attention reports fp32 MFMA TFLOP/s (2 * 2 * visible
+    (query, key) pairs * hd * heads) against the 157.3 TFLOP/s dense fp32 peak."""
+    import ctypes
+
+    lib, st = hip.lib, hip.s
+    kh, vh, kd, vd, K = 16, 48, 128, 128, 4
+    cdim = 2 * kh * kd + vh * vd
+    out = {}
+    for ntok in (1, 8):
+        for elem in (4, 2):
+            conv = torch.randn(ntok, cdim, device="cuda")
+            b, a = torch.randn(ntok, vh, device="cuda"), torch.randn(ntok, vh, device="cuda")
+            sa, dt = -torch.rand(vh, device="cuda") - 0.1, torch.randn(vh, device="cuda")
+            S = (torch.randn(vh * kd * vd, device="cuda") * 0.1).to(torch.float32 if elem == 4 else torch.float16)
+            o = torch.empty(ntok, vh, vd, device="cuda")
+
+            def gd(i):
+                r = lib.vq_gated_delta(conv.data_ptr(), b.data_ptr(), a.data_ptr(), sa.data_ptr(), dt.data_ptr(),
+                                       S.data_ptr(), elem, o.data_ptr(), kh, vh, kd, vd, 1e-6, 0, ntok, None, 1, st())
+                assert r == 0, r
+
+            ms = time_kernel_loop(torch, gd, 200)
+            nb = 2 * vh * kd * vd * elem + ntok * (cdim + 2 * vh + vh * vd) * 4
+            out[f"gated_delta_ntok{ntok}_state{'f32' if elem == 4 else 'f16'}"] = {
+                "us": round(ms * 1e3, 3), "bytes": nb, "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
+                "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    for ntok in (1, 8):
+        x = torch.randn(ntok, cdim, device="cuda")
+        state = torch.randn(cdim, K, device="cuda")
+        w = torch.randn(cdim, K, device="cuda")
+        y = torch.empty(ntok, cdim, device="cuda")
+
+        def cu(i):
+            r = lib.vq_conv_update(x.data_ptr(), state.data_ptr(), w.data_ptr(), y.data_ptr(), cdim, K, ntok, None, 1,
+                                   st())
+            assert r == 0, r
+
+        ms = time_kernel_loop(torch, cu, 200)
+        nb = (3 * cdim * K + 2 * ntok * cdim) * 4
+        out[f"conv_update_ntok{ntok}"] = {"us": round(ms * 1e3, 3), "bytes": nb,
+                                          "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
+                                          "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    heads, kvh, hd = 24, 4, 256
+    for ntok, seq_len in ((1, 4096), (8, 4096), (512, 1)):
+        max_seq = seq_len + ntok
+        q = torch.randn(ntok, heads, hd, device="cuda")
+        kc = (torch.randn(kvh, max_seq, hd, device="cuda") * 0.3).half()
+        vc = torch.randn(kvh, max_seq, hd, device="cuda").half()
+        o = torch.empty_like(q)
+
+        nws = lib.vq_attention_workspace_bytes(heads, kvh, hd, seq_len, ntok, 0)
+        wsb = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
+
+        def at(i):
+            r = lib.vq_attention_ws(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(), 2, heads, kvh, hd,
+                                    max_seq, seq_len, ntok, 0, 0, wsb.data_ptr() if nws else None, nws, st())
+            assert r == 0, r
+
+        ms = time_kernel_loop(torch, at, 50)
+        pairs = sum(seq_len + t for t in range(ntok))
+        rec = {"us": round(ms * 1e3, 3)}
+        if ntok > 8:
+            tf = 2 * 2 * pairs * hd * heads / (ms * 1e-3) / 1e12
+            rec.update(kernel="attention_mfma (fp32 MFMA)", tflops=round(tf, 2), frac=round(tf / MFMA_F32_PEAK_TFLOPS, 4))
+        else:
+            nb = 2 * kvh * (seq_len + ntok - 1) * hd * 2 + 2 * ntok * heads * hd * 4
+            rec.update(kernel="attention_split + merge (fp32 MFMA, flash decoding)", bytes=nb, GBps=round(nb / (ms * 1e-3) / 1e9, 1),
+                       frac=round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+        out[f"attention_fp16kv_ntok{ntok}_ctx{seq_len + ntok - 1}"] = rec
+    return out
+
+
 def row_bytes_of(ty, cols):
     from vinf_3080ti_amd import row_bytes
 
@@ -648,6 +727,8 @@ def main() -> None:
                          "(e.g. IQ2_XXS:5120:17408:1), timed as the per-type legs are")
     ap.add_argument("--libs", default="",
                     help="with --matvec: comma-separated builds of libvq_hip.so compared launch for launch")
+    ap.add_argument("--ops-only", action="store_true",
+                    help="only the sequence ops (gated delta, conv update, attention) at the qwen35 shapes")
     ap.add_argument("--mlp-only", action="store_true",
                     help="only the SwiGLU MLP block at batch 1, 4, 8 (as vq_qmv routes) and 8 on the streaming kernel")
     ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
@@ -660,7 +741,7 @@ def main() -> None:
               "DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    full = not (args.matvec or args.prefill_only or args.mlp_only or args.roofline_only)
+    full = not (args.matvec or args.prefill_only or args.mlp_only or args.roofline_only or args.ops_only)
     cpu = None
     if full and not args.no_cpu:  # child processes, started before this process initialises the GPU
         log("cpu baseline: reference CPU path, configs 1-3 and a sample of the sweep, two thread settings")
@@ -700,6 +781,9 @@ def main() -> None:
             out[spec] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
             log(f"{spec}: {out[spec]['us']} us, {out[spec]['GBps']} GB/s")
         print(json.dumps({"matvec": out}), flush=True)
+        return
+    if args.ops_only:
+        print(json.dumps({"ops": bench_ops(torch, hip)}), flush=True)
         return
     if args.prefill_only:
         out = {}
@@ -746,7 +830,7 @@ def main() -> None:
         r = bench_matvec(torch, hip, Q4_K, 4096, 4096, args.ntok)
         per_type["Q4_K@4096x4096"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
 
-    prefill, mlp = {}, {}
+    prefill, mlp, ops = {}, {}, {}
     if not args.no_per_type:
         for n in (1, 4, 8):
             log(f"SwiGLU MLP block, batch {n}")
@@ -755,6 +839,8 @@ def main() -> None:
         for rows, cols in ((17408, 5120), (5120, 17408)):
             log(f"prefill: 512 tokens x Q4_K {rows}x{cols}")
             prefill[f"Q4_K_{rows}x{cols}_M512"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512)
+        log("sequence ops (gated delta, conv update, attention)")
+        ops = bench_ops(torch, hip)
 
     log("sweep: allocating 13.4 GiB of weights")
     sw = Sweep(torch, hip, args.ntok)
@@ -823,6 +909,7 @@ def main() -> None:
         "per_type": per_type,
         "prefill": prefill,
         "mlp_block": mlp,
+        "ops": ops,
         "sweep_batch4": sweep4,
     }
     print(json.dumps(out), flush=True)

@@ -195,6 +195,30 @@ int vq_attention_seg(const float *q, const void *kc, const void *vc, float *out,
                      int nseg, int heads, int kv_heads, int hd, const int32_t *page_table, int page_size,
                      int pages_per_seq, void *stream);
 
+/* Workspace bytes of vq_attention_ws for these shapes (0: the call takes the per-row kernel, ntok > VQ_ATTN_ROW_MAX
+ * or invalid arguments). */
+size_t vq_attention_workspace_bytes(int heads, int kv_heads, int hd, int seq_len, int ntok, int window);
+
+/* vq_attention for decode and verify passes (ntok <= VQ_ATTN_ROW_MAX) with a workspace (>=
+ * vq_attention_workspace_bytes, 16-byte aligned): the context is cut into chunks over about 512 workgroups, each
+ * running every query head of a kv head on fp32 MFMA against its chunk, and the chunks' partial softmax
+ * results are merged in chunk order (flash decoding; deterministic). Longer passes run as vq_attention.
+ * Replaces: Runtime.attention on its decode path (qwen_runtime.cu:128-162, 2003-2050), which runs one block per
+ * (head, token) over the whole context. */
+int vq_attention_ws(const float *q, const void *kc, const void *vc, float *out, int elem, int heads, int kv_heads,
+                    int hd, int max_seq, int seq_len, int ntok, int bidirectional, int window, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+/* Workspace bytes of vq_attention_seg_ws for this segment table (0 when a segment has more than VQ_ATTN_ROW_MAX rows:
+ * the call then takes the prompt kernel and needs none). */
+size_t vq_attention_seg_workspace_bytes(const int32_t *segs, int nseg, int heads, int kv_heads, int hd);
+
+/* vq_attention_seg with the workspace of the split-context decode kernel (as vq_attention_ws). Replaces:
+ * Runtime.attention_seg (qwen_runtime.cu:2449-2478). */
+int vq_attention_seg_ws(const float *q, const void *kc, const void *vc, float *out, int elem, const int32_t *segs,
+                        int nseg, int heads, int kv_heads, int hd, const int32_t *page_table, int page_size,
+                        int pages_per_seq, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Causal depthwise conv + SiLU over ntok tokens: per channel the state [channels][K] (K <= VQ_CONV_MAX_K) holds
  * the last K inputs; per token it shifts, appends x[t][c], and out[t][c] = silu(state . w[c]). snap (may be
  * NULL): [ntok - 1][channels][K] states after each token but the last. write_state = 0 leaves the state

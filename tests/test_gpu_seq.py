@@ -415,3 +415,47 @@ def test_prompt_attention_seg(rt, oracle_mod, elem):
         ref = oracle_mod.attention(q[row:row + m], kc, vc, heads, kvh, pos0 + 1)
         assert np.allclose(got[row:row + m], ref, rtol=2e-5, atol=2e-5), (slot, pos0, m)
         row += m
+
+
+@pytest.mark.parametrize("elem", [4, 2])
+@pytest.mark.parametrize("ntok,seq_len,window", [(1, 4096, 0), (8, 1000, 0), (3, 2, 0), (5, 700, 100)])
+def test_decode_attention_split_and_per_row_kernels(oracle_mod, elem, ntok, seq_len, window):
+    """Both decode kernels through the C ABI on the same inputs: vq_attention (one workgroup per head and row) and
+    vq_attention_ws (the context split over ~512 workgroups on fp32 MFMA, chunks merged in order), at the qwen35
+    head shape, against the float64 restatement; the split kernel is bit-identical on a rerun."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from vinf_3080ti_amd import _lib
+
+    lib = _lib.load()
+    assert lib.vq_init() == 0
+    rng = np.random.default_rng(seq_len + ntok + elem)
+    heads, kvh, hd = QW_HEADS, QW_KVH, QW_HD
+    max_seq = seq_len + ntok + 5
+    dt = np.float32 if elem == 4 else np.float16
+    q = rng.standard_normal((ntok, heads, hd)).astype(np.float32)
+    kc = (rng.standard_normal((kvh, max_seq, hd)) * 0.3).astype(dt)
+    vc = rng.standard_normal((kvh, max_seq, hd)).astype(dt)
+    qd, kd_, vd_ = (torch.from_numpy(a).cuda() for a in (q, kc, vc))
+    nws = lib.vq_attention_workspace_bytes(heads, kvh, hd, seq_len, ntok, window)
+    assert nws > 0
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+    outs = []
+    for use_ws in (False, True, True):
+        o = torch.full_like(qd, float("nan"))
+        if use_ws:
+            st = lib.vq_attention_ws(qd.data_ptr(), kd_.data_ptr(), vd_.data_ptr(), o.data_ptr(), elem, heads, kvh, hd,
+                                     max_seq, seq_len, ntok, 0, window, ws.data_ptr(), nws, None)
+        else:
+            st = lib.vq_attention(qd.data_ptr(), kd_.data_ptr(), vd_.data_ptr(), o.data_ptr(), elem, heads, kvh, hd,
+                                  max_seq, seq_len, ntok, 0, window, None)
+        assert st == 0, lib.vq_status_string(st)
+        torch.cuda.synchronize()
+        outs.append(o.cpu().numpy())
+    ref = oracle_mod.attention(q, kc, vc, heads, kvh, seq_len, False, window)
+    for got in outs:
+        assert np.allclose(got, ref, rtol=2e-5, atol=2e-5)
+    assert np.array_equal(outs[1].view(np.uint32), outs[2].view(np.uint32))
+    assert lib.vq_attention_ws(qd.data_ptr(), kd_.data_ptr(), vd_.data_ptr(), qd.data_ptr(), elem, heads, kvh, hd,
+                               max_seq, seq_len, ntok, 0, window, ws.data_ptr(), nws - 300, None) == _lib.VQ_ERR_WORKSPACE

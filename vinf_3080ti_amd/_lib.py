@@ -41,6 +41,10 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_kv_append_seg": (I, [P, P, P, P, I, P, I, I, I, P, I, I, P]),
     "vq_attention": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, P]),
     "vq_attention_seg": (I, [P, P, P, P, I, P, I, I, I, I, P, I, I, P]),
+    "vq_attention_workspace_bytes": (SZ, [I, I, I, I, I, I]),
+    "vq_attention_ws": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, P, SZ, P]),
+    "vq_attention_seg_workspace_bytes": (SZ, [P, I, I, I, I]),
+    "vq_attention_seg_ws": (I, [P, P, P, P, I, P, I, I, I, I, P, I, I, P, SZ, P]),
     "vq_conv_update": (I, [P, P, P, P, I, I, I, P, I, P]),
     "vq_conv_update_seg": (I, [P, P, P, P, I, I, P, I, P, I, P]),
     "vq_gated_delta": (I, [P, P, P, P, P, P, I, P, I, I, I, I, F, I, I, P, I, P]),

@@ -58,6 +58,13 @@ struct KvMap {
 
 __device__ __forceinline__ float kv_get(const float *c, size_t i) { return c[i]; }
 __device__ __forceinline__ float kv_get(const _Float16 *c, size_t i) { return static_cast<float>(c[i]); }
+// Elements i .. i + 3 of a cache as one vector load (the caller checks the alignment), widened to fp32.
+__device__ __forceinline__ float4 ld4(const float *c, size_t i) { return *reinterpret_cast<const float4 *>(c + i); }
+__device__ __forceinline__ float4 ld4(const _Float16 *c, size_t i) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 a = *reinterpret_cast<const h4 *>(c + i);
+    return float4{static_cast<float>(a[0]), static_cast<float>(a[1]), static_cast<float>(a[2]), static_cast<float>(a[3])};
+}
 
 // Host side: validate a segment table ([n][4] int32: slot, pos0, rows, row0) into a SegTable.
 int make_table(const int32_t *segs, int nseg, SegTable &T, int *rows_spanned) {
@@ -340,80 +347,97 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(const float 
 constexpr int kFaKeys = 32;  // keys per LDS tile
 typedef float fa4 __attribute__((ext_vector_type(4)));
 
-template <typename C, int HD>
-__global__ __launch_bounds__(256) void attention_mfma_kernel(const float *__restrict__ q, const C *__restrict__ kc,
-                                                             const C *__restrict__ vc, float *__restrict__ out,
-                                                             SegTable T, KvMap M, int heads, int hd, int bidirectional,
-                                                             int window, int chunks) {
-    constexpr int LD = HD + 4;  // row stride of the tiles: fragment reads of 16 rows x 4 or 4 rows x 16 hit 64 banks
-    __shared__ float sk[kFaKeys * LD], sv[kFaKeys * LD];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int col = lane & 15, grp = lane >> 4;
-    int tb = blockIdx.x, si = 0;  // (segment, 16-row tile) of this workgroup
-    while (si + 1 < T.n && tb >= (T.s[si].rows + 15) / 16) {
-        tb -= (T.s[si].rows + 15) / 16;
-        ++si;
-    }
-    const Seg &s = T.s[si];
-    const int G = heads / M.kv_heads;
-    const int kvh = blockIdx.y / chunks, gi = (blockIdx.y - kvh * chunks) * 4 + wv;
-    const bool wave_on = gi < G;
-    const int h = kvh * G + (wave_on ? gi : 0);
-    const int t0 = 16 * tb, nq = min(16, s.rows - t0);
-    const int seq_len0 = s.pos0 + 1;
-    auto q_end = [&](int t) { return bidirectional ? seq_len0 + s.rows - 1 : seq_len0 + t; };
-    auto q_start = [&](int t) { return window > 0 && seq_len0 + t > window ? seq_len0 + t - window : 0; };
-    const int kbeg = q_start(t0), kend = q_end(t0 + nq - 1);
-    const int tq = t0 + min(col, nq - 1);  // this lane's query row (rows past nq repeat the last; not written)
-    const int qs = q_start(tq), qe = q_end(tq);
-    const float scale = 1.0f / sqrtf(static_cast<float>(hd));
-    float qf[HD / 4];
-    {
-        const float *qrow = q + (static_cast<size_t>(s.row0 + tq) * heads + h) * hd;
-#pragma unroll
-        for (int st = 0; st < HD / 4; ++st) {
-            const int d = 4 * st + grp;
-            qf[st] = d < hd ? qrow[d] * scale : 0.0f;
-        }
-    }
-    float m = -INFINITY, l = 0.0f;
-    fa4 o[HD / 16];
-#pragma unroll
-    for (int b = 0; b < HD / 16; ++b) o[b] = fa4{0.f, 0.f, 0.f, 0.f};
+// The keys [k_lo, k_hi) of kv head kvh of a sequence, 32 per LDS tile (all four waves stage each tile; fp16 caches
+// widened to fp32), against the 16 query vectors a wave holds in qf (query vector col = lane & 15 sees keys
+// [qs, qe)). Updates the online softmax (m, l) and the unnormalised output o of the lane's query vector.
+// Tile layouts in LDS: K row-major k[key][HD + 4], V transposed vt[dim][kFaKeys + 4]. Both products then read
+// their A operand as four consecutive floats per lane (one ds_read_b128 per four MFMAs): the head-dim
+// contraction of S^T runs step 4u + v over dims 16 u + 4 g + v in lane group g (the query vector in qf is held
+// in the same order), the key contraction of O^T over keys 4 g + r.
+constexpr int kFaLdk = kFaKeys + 4;
+template <int HD>
+struct FaTiles {
+    float k[kFaKeys * (HD + 4)];
+    float vt[HD * kFaLdk];
+};
 
-    for (int k0 = kbeg; k0 < kend; k0 += kFaKeys) {
+template <typename C, int HD, bool FAST>
+__device__ __forceinline__ void fa_keys(const C *__restrict__ kc, const C *__restrict__ vc, const KvMap &M, int slot,
+                                        int kvh, int hd, int k_lo, int k_hi, int qs, int qe, bool wave_on,
+                                        const float (&qf)[HD / 4], FaTiles<HD> &tl, float &m, float &l,
+                                        fa4 (&o)[HD / 16]) {
+    constexpr int LD = HD + 4;
+    constexpr int NQ = kFaKeys * (HD / 4) / 256;  // quads of K (and of V) per thread per tile
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    for (int k0 = k_lo; k0 < k_hi; k0 += kFaKeys) {
         __syncthreads();  // the previous tile is consumed
-        for (int i = threadIdx.x; i < kFaKeys * (HD / 4); i += 256) {
-            const int key = i / (HD / 4), d = 4 * (i - key * (HD / 4)), p = k0 + key;
-            float4 kv4{0.f, 0.f, 0.f, 0.f}, vv4{0.f, 0.f, 0.f, 0.f};
-            if (p < kend && d < hd) {
-                const size_t r = M.row(s.slot, kvh, p) * hd + d;
-                kv4.x = kv_get(kc, r);
-                vv4.x = kv_get(vc, r);
-                if (d + 1 < hd) kv4.y = kv_get(kc, r + 1), vv4.y = kv_get(vc, r + 1);
-                if (d + 2 < hd) kv4.z = kv_get(kc, r + 2), vv4.z = kv_get(vc, r + 2);
-                if (d + 3 < hd) kv4.w = kv_get(kc, r + 3), vv4.w = kv_get(vc, r + 3);
+        // K quad i: key i / (HD/4), dims 4 (i % (HD/4)) .. (row-major writes); V quad i: key i % kFaKeys, dims
+        // 4 (i / kFaKeys) .. (consecutive lanes write consecutive keys of the transposed tile).
+        if constexpr (FAST) {
+            // hd % 4 == 0 and aligned caches: every thread's loads of the tile are issued before any is stored
+            // (addresses clamped into the tile, values past its edge zeroed afterwards).
+            // Two rounds of NQ / 2 quads each keep the staging registers small beside qf and o.
+            constexpr int NH = NQ > 1 ? NQ / 2 : 1;
+#pragma unroll
+            for (int u0 = 0; u0 < NQ; u0 += NH) {
+                float4 kq[NH], vq[NH];
+#pragma unroll
+                for (int u = 0; u < NH; ++u) {
+                    const int i = threadIdx.x + 256 * (u0 + u);
+                    const int kk = i / (HD / 4), kd = 4 * (i - kk * (HD / 4));
+                    const int vk = i % kFaKeys, vd = 4 * (i / kFaKeys);
+                    const int pk = k0 + kk < k_hi ? k0 + kk : k_hi - 1, pv = k0 + vk < k_hi ? k0 + vk : k_hi - 1;
+                    kq[u] = ld4(kc, M.row(slot, kvh, pk) * hd + (kd < hd ? kd : 0));
+                    vq[u] = ld4(vc, M.row(slot, kvh, pv) * hd + (vd < hd ? vd : 0));
+                }
+#pragma unroll
+                for (int u = 0; u < NH; ++u) {
+                    const int i = threadIdx.x + 256 * (u0 + u);
+                    const int kk = i / (HD / 4), kd = 4 * (i - kk * (HD / 4));
+                    const int vk = i % kFaKeys, vd = 4 * (i / kFaKeys);
+                    const float mk = k0 + kk < k_hi && kd < hd ? 1.0f : 0.0f;  // zero past the tile's edge
+                    const float mv = k0 + vk < k_hi && vd < hd ? 1.0f : 0.0f;
+                    *reinterpret_cast<float4 *>(tl.k + kk * LD + kd) =
+                        float4{kq[u].x * mk, kq[u].y * mk, kq[u].z * mk, kq[u].w * mk};
+                    tl.vt[(vd + 0) * kFaLdk + vk] = vq[u].x * mv;
+                    tl.vt[(vd + 1) * kFaLdk + vk] = vq[u].y * mv;
+                    tl.vt[(vd + 2) * kFaLdk + vk] = vq[u].z * mv;
+                    tl.vt[(vd + 3) * kFaLdk + vk] = vq[u].w * mv;
+                }
             }
-            *reinterpret_cast<float4 *>(sk + key * LD + d) = kv4;
-            *reinterpret_cast<float4 *>(sv + key * LD + d) = vv4;
+        } else {
+            for (int i = threadIdx.x; i < kFaKeys * HD; i += blockDim.x) {
+                const int kk = i / HD, kd = i - kk * HD;      // K element
+                const int vk = i % kFaKeys, vd = i / kFaKeys;  // V element
+                const bool okk = k0 + kk < k_hi && kd < hd, okv = k0 + vk < k_hi && vd < hd;
+                tl.k[kk * LD + kd] = okk ? kv_get(kc, M.row(slot, kvh, k0 + kk) * hd + kd) : 0.0f;
+                tl.vt[vd * kFaLdk + vk] = okv ? kv_get(vc, M.row(slot, kvh, k0 + vk) * hd + vd) : 0.0f;
+            }
         }
         __syncthreads();
         if (!wave_on) continue;
 #pragma unroll
         for (int sub = 0; sub < kFaKeys / 16; ++sub) {
             const int kb = k0 + 16 * sub;
-            if (kb >= kend) break;
-            const float *kt = sk + (16 * sub) * LD, *vt = sv + (16 * sub) * LD;
-            fa4 sc = {0.f, 0.f, 0.f, 0.f};
+            if (kb >= k_hi) break;
+            // S^T: four independent accumulator chains (one per v of dims 16 u + 4 g + v), added at the end.
+            fa4 sc4[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+            const float *krow = tl.k + (16 * sub + col) * LD + 4 * grp;
 #pragma unroll
-            for (int st = 0; st < HD / 4; ++st)
-                sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kt[col * LD + 4 * st + grp], qf[st], sc, 0, 0, 0);
-            // sc[r]: key kb + 4 grp + r, query row tq
+            for (int u = 0; u < HD / 16; ++u) {
+                const float4 a = *reinterpret_cast<const float4 *>(krow + 16 * u);
+                sc4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, qf[4 * u], sc4[0], 0, 0, 0);
+                sc4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, qf[4 * u + 1], sc4[1], 0, 0, 0);
+                sc4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, qf[4 * u + 2], sc4[2], 0, 0, 0);
+                sc4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, qf[4 * u + 3], sc4[3], 0, 0, 0);
+            }
+            const fa4 sc = (sc4[0] + sc4[1]) + (sc4[2] + sc4[3]);
+            // sc[r]: key kb + 4 grp + r against query vector col
             float v[4], bm = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int p = kb + 4 * grp + r;
-                v[r] = p >= qs && p < qe ? sc[r] : -INFINITY;
+                v[r] = p >= qs && p < qe && p < k_hi ? sc[r] : -INFINITY;
                 bm = fmaxf(bm, v[r]);
             }
             bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
@@ -430,16 +454,66 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float *__rest
             ps += __shfl_xor(ps, 32, 64);
             l = l * alpha + ps;
             m = mn;
+            const float *vrow = tl.vt + col * kFaLdk + 16 * sub + 4 * grp;
 #pragma unroll
-            for (int b = 0; b < HD / 16; ++b) o[b] *= alpha;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int b = 0; b < HD / 16; ++b)
-                    o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(vt[(4 * grp + r) * LD + 16 * b + col], pr[r], o[b], 0,
-                                                                0, 0);
+            for (int b = 0; b < HD / 16; ++b) {
+                const float4 a = *reinterpret_cast<const float4 *>(vrow + 16 * b * kFaLdk);
+                fa4 ob = o[b] * alpha;
+                ob = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, pr[0], ob, 0, 0, 0);
+                ob = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, pr[1], ob, 0, 0, 0);
+                ob = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, pr[2], ob, 0, 0, 0);
+                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, pr[3], ob, 0, 0, 0);
+            }
         }
     }
+}
+
+// Query vector held in the B-operand order of fa_keys: lane group g keeps dims 16 u + 4 g + v at step 4 u + v,
+// times scale.
+template <int HD>
+__device__ __forceinline__ void fa_load_q(const float *qrow, int hd, float scale, float (&qf)[HD / 4]) {
+    const int grp = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int st = 0; st < HD / 4; ++st) {
+        const int d = 16 * (st >> 2) + 4 * grp + (st & 3);
+        qf[st] = d < hd ? qrow[d] * scale : 0.0f;
+    }
+}
+
+// Prompt passes: a workgroup takes 16 query rows (tokens) of one segment and up to four query heads of one kv head
+// (one wave each), so the K/V tiles it stages in LDS serve all of them, and walks every key the rows see.
+template <typename C, int HD, bool FAST>
+__global__ __launch_bounds__(256) void attention_mfma_kernel(const float *__restrict__ q, const C *__restrict__ kc,
+                                                             const C *__restrict__ vc, float *__restrict__ out,
+                                                             SegTable T, KvMap M, int heads, int hd, int bidirectional,
+                                                             int window, int chunks) {
+    __shared__ FaTiles<HD> tl;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    int tb = blockIdx.x, si = 0;  // (segment, 16-row tile) of this workgroup
+    while (si + 1 < T.n && tb >= (T.s[si].rows + 15) / 16) {
+        tb -= (T.s[si].rows + 15) / 16;
+        ++si;
+    }
+    const Seg &s = T.s[si];
+    const int G = heads / M.kv_heads;
+    const int kvh = blockIdx.y / chunks, gi = (blockIdx.y - kvh * chunks) * 4 + wv;
+    const bool wave_on = gi < G;
+    const int h = kvh * G + (wave_on ? gi : 0);
+    const int t0 = 16 * tb, nq = min(16, s.rows - t0);
+    const int seq_len0 = s.pos0 + 1;
+    auto q_end = [&](int t) { return bidirectional ? seq_len0 + s.rows - 1 : seq_len0 + t; };
+    auto q_start = [&](int t) { return window > 0 && seq_len0 + t > window ? seq_len0 + t - window : 0; };
+    const int tq = t0 + min(col, nq - 1);  // this lane's query row (rows past nq repeat the last; not written)
+    float qf[HD / 4];
+    fa_load_q<HD>(q + (static_cast<size_t>(s.row0 + tq) * heads + h) * hd, hd, 1.0f / sqrtf(static_cast<float>(hd)),
+                  qf);
+    float m = -INFINITY, l = 0.0f;
+    fa4 o[HD / 16];
+#pragma unroll
+    for (int b = 0; b < HD / 16; ++b) o[b] = fa4{0.f, 0.f, 0.f, 0.f};
+    fa_keys<C, HD, FAST>(kc, vc, M, s.slot, kvh, hd, q_start(t0), q_end(t0 + nq - 1), q_start(tq), q_end(tq), wave_on, qf,
+                   tl, m, l, o);
     // o[b][r]: head dim 16 b + 4 grp + r of query row tq
     if (wave_on && col < nq) {
         float *orow = out + (static_cast<size_t>(s.row0 + t0 + col) * heads + h) * hd;
@@ -452,6 +526,128 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float *__rest
                 if (d < hd) orow[d] = o[b][r] * inv;
             }
     }
+}
+
+// Decode and verify passes (at most VQ_ATTN_ROW_MAX rows per segment): the keys of a sequence are cut into nch
+// chunks, one workgroup per (segment, kv head, chunk, block of 64 query vectors). Query vector j of the block is
+// (row j / G, head j % G of the kv head's group): every query head of the group shares the staged K/V. Each
+// writes its unnormalised partial output and its (max, sum) to the workspace; attention_merge_kernel combines
+// the chunks in chunk order (deterministic).
+template <typename C, int HD, bool FAST>
+__global__ __launch_bounds__(256) void attention_split_kernel(const float *__restrict__ q, const C *__restrict__ kc,
+                                                              const C *__restrict__ vc, float *__restrict__ part,
+                                                              float *__restrict__ pml, SegTable T, KvMap M, int heads,
+                                                              int hd, int bidirectional, int window, int nch) {
+    __shared__ FaTiles<HD> tl;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int c = blockIdx.x % nch, sk_id = blockIdx.x / nch;
+    const int kvh = sk_id % M.kv_heads, si = sk_id / M.kv_heads;
+    const Seg &s = T.s[si];
+    const int G = heads / M.kv_heads;
+    const int j = blockIdx.y * 64 + wv * 16 + col;  // query vector of this lane
+    const int t = j / G, g = j - t * G;
+    const bool valid = t < s.rows;
+    const bool wave_on = blockIdx.y * 64 + wv * 16 < s.rows * G;
+    const int tq = valid ? t : s.rows - 1, h = kvh * G + (valid ? g : 0);
+    const int seq_len0 = s.pos0 + 1;
+    const int qe = bidirectional ? seq_len0 + s.rows - 1 : seq_len0 + tq;
+    const int qs = window > 0 && seq_len0 + tq > window ? seq_len0 + tq - window : 0;
+    const int ctx = seq_len0 + s.rows - 1;                                // keys any row of the segment sees
+    const int lo0 = window > 0 && seq_len0 > window ? seq_len0 - window : 0;  // the earliest key any row sees
+    const int ch = ((ctx - lo0 + nch - 1) / nch + kFaKeys - 1) / kFaKeys * kFaKeys;
+    const int k_lo = lo0 + c * ch, k_hi = min(ctx, k_lo + ch);
+    float qf[HD / 4];
+    fa_load_q<HD>(q + (static_cast<size_t>(s.row0 + tq) * heads + h) * hd, hd, 1.0f / sqrtf(static_cast<float>(hd)),
+                  qf);
+    float m = -INFINITY, l = 0.0f;
+    fa4 o[HD / 16];
+#pragma unroll
+    for (int b = 0; b < HD / 16; ++b) o[b] = fa4{0.f, 0.f, 0.f, 0.f};
+    fa_keys<C, HD, FAST>(kc, vc, M, s.slot, kvh, hd, k_lo, k_hi, qs, qe, wave_on, qf, tl, m, l, o);
+    if (valid) {
+        const size_t qv = static_cast<size_t>(s.row0 + t) * heads + h;  // [buffer row][head]
+        float *pp = part + (qv * nch + c) * HD;
+#pragma unroll
+        for (int b = 0; b < HD / 16; ++b)
+            *reinterpret_cast<fa4 *>(pp + 16 * b + 4 * grp) = o[b];
+        if (grp == 0) {
+            pml[(qv * nch + c) * 2] = m;
+            pml[(qv * nch + c) * 2 + 1] = l;
+        }
+    }
+}
+
+// out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, M = max_c m_c; one workgroup of four waves per (row of the
+// pass, head): the chunks' maxima through LDS, then wave w adds chunks w, w + 4, ... (lane = four head dims, one
+// 16-byte load per chunk) and the four waves' sums are added in wave order (deterministic).
+template <int HD>
+__global__ __launch_bounds__(256) void attention_merge_kernel(const float *__restrict__ part, const float *__restrict__ pml,
+                                                              float *__restrict__ out, SegTable T, int heads, int hd,
+                                                              int nch) {
+    __shared__ float smx[256];
+    __shared__ float4 sacc[4][HD / 4];
+    __shared__ float sl[4];
+    int t;
+    const Seg &s = seg_of_row(T, blockIdx.x / heads, t);
+    const int h = blockIdx.x % heads;
+    const size_t qv = static_cast<size_t>(s.row0 + t) * heads + h;
+    const float *ml = pml + qv * nch * 2;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    float mx = -INFINITY;
+    for (int c = tid; c < nch; c += 256) mx = fmaxf(mx, ml[2 * c]);
+    smx[tid] = mx;
+    for (int w = 128; w > 0; w >>= 1) {
+        __syncthreads();
+        if (tid < w) smx[tid] = fmaxf(smx[tid], smx[tid + w]);
+    }
+    __syncthreads();
+    const float M = smx[0];
+    float4 acc{0.f, 0.f, 0.f, 0.f};
+    float L = 0.0f;
+    if (4 * lane < HD) {
+        for (int c = wv; c < nch; c += 4) {
+            const float f = ml[2 * c] == -INFINITY ? 0.0f : expf(ml[2 * c] - M);
+            L = fmaf(ml[2 * c + 1], f, L);
+            const float4 p4 = *reinterpret_cast<const float4 *>(part + (qv * nch + c) * HD + 4 * lane);
+            acc.x = fmaf(p4.x, f, acc.x);
+            acc.y = fmaf(p4.y, f, acc.y);
+            acc.z = fmaf(p4.z, f, acc.z);
+            acc.w = fmaf(p4.w, f, acc.w);
+        }
+        sacc[wv][lane] = acc;
+    }
+    if (lane == 0) sl[wv] = L;
+    __syncthreads();
+    if (wv == 0 && 4 * lane < HD) {
+        const float Lt = ((sl[0] + sl[1]) + sl[2]) + sl[3];
+        const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
+        const float4 a = sacc[0][lane], b = sacc[1][lane], c = sacc[2][lane], d = sacc[3][lane];
+        const float r[4] = {((a.x + b.x) + c.x) + d.x, ((a.y + b.y) + c.y) + d.y, ((a.z + b.z) + c.z) + d.z,
+                            ((a.w + b.w) + c.w) + d.w};
+        float *o = out + qv * hd;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (4 * lane + k < hd) o[4 * lane + k] = r[k] * inv;
+    }
+}
+
+// Chunks per sequence of a split decode pass: about 512 workgroups for the whole pass, at least 32 keys each.
+int split_chunks(const SegTable &T, int kv_heads, int window) {
+    int ctx = 1;
+    for (int i = 0; i < T.n; ++i) {
+        int c = T.s[i].pos0 + T.s[i].rows;
+        if (window > 0 && c > window + T.s[i].rows) c = window + T.s[i].rows;
+        ctx = c > ctx ? c : ctx;
+    }
+    const int want = (512 + T.n * kv_heads - 1) / (T.n * kv_heads);
+    const int most = (ctx + kFaKeys - 1) / kFaKeys;
+    return want < 1 ? 1 : want > most ? most : want;
+}
+int fa_hd(int hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : 256; }
+size_t split_ws_bytes(const SegTable &T, int span_rows, int heads, int kv_heads, int hd, int window) {
+    const int nch = split_chunks(T, kv_heads, window);
+    return static_cast<size_t>(span_rows) * heads * nch * (fa_hd(hd) + 2) * 4 + 256;
 }
 
 // ---- causal conv update ----------------------------------------------------------------------------------
@@ -633,25 +829,90 @@ int launch_kv_append(const float *k, const float *v, void *kc, void *vc, int ele
 }
 
 template <typename C>
+bool fa_fast(const C *kc, const C *vc, int hd) {
+    return hd % 4 == 0 && ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & (4 * sizeof(C) - 1)) == 0;
+}
+
+template <typename C, int HD>
+void launch_mfma_hd(bool fast, dim3 grid, hipStream_t s, const float *q, const C *kc, const C *vc, float *out,
+                    const SegTable &T, const KvMap &M, int heads, int hd, int bidirectional, int window, int chunks) {
+    if (fast)
+        attention_mfma_kernel<C, HD, true><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, hd, bidirectional, window,
+                                                               chunks);
+    else
+        attention_mfma_kernel<C, HD, false><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, hd, bidirectional, window,
+                                                                chunks);
+}
+
+template <typename C>
 void launch_attention_mfma(const float *q, const C *kc, const C *vc, float *out, const SegTable &T, const KvMap &M,
                            int heads, int hd, int bidirectional, int window, hipStream_t s) {
     int tiles = 0;
     for (int i = 0; i < T.n; ++i) tiles += (T.s[i].rows + 15) / 16;
     const int chunks = (heads / M.kv_heads + 3) / 4;
     const dim3 grid(tiles, M.kv_heads * chunks);
-    if (hd <= 64)
-        attention_mfma_kernel<C, 64><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
-    else if (hd <= 128)
-        attention_mfma_kernel<C, 128><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
+    const bool fast = fa_fast(kc, vc, hd);
+    if (hd <= 64) launch_mfma_hd<C, 64>(fast, grid, s, q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
+    else if (hd <= 128) launch_mfma_hd<C, 128>(fast, grid, s, q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
+    else launch_mfma_hd<C, 256>(fast, grid, s, q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
+}
+
+template <typename C, int HD>
+void launch_split_hd(bool fast, dim3 grid, dim3 mgrid, hipStream_t s, const float *q, const C *kc, const C *vc,
+                     float *part, float *pml, float *out, const SegTable &T, const KvMap &M, int heads, int hd,
+                     int bidirectional, int window, int nch) {
+    if (fast)
+        attention_split_kernel<C, HD, true><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, T, M, heads, hd, bidirectional,
+                                                                window, nch);
     else
-        attention_mfma_kernel<C, 256><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
+        attention_split_kernel<C, HD, false><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, T, M, heads, hd, bidirectional,
+                                                                 window, nch);
+    attention_merge_kernel<HD><<<mgrid, 256, 0, s>>>(part, pml, out, T, heads, hd, nch);
+}
+
+template <typename C>
+void launch_attention_split(const float *q, const C *kc, const C *vc, float *out, const SegTable &T, const KvMap &M,
+                            int heads, int hd, int bidirectional, int window, int span_rows, void *ws, hipStream_t s) {
+    const int nch = split_chunks(T, M.kv_heads, window);
+    const int HD = fa_hd(hd);
+    float *part = static_cast<float *>(ws);
+    float *pml = part + static_cast<size_t>(span_rows) * heads * nch * HD;
+    int max_rows = 0;
+    for (int i = 0; i < T.n; ++i) max_rows = T.s[i].rows > max_rows ? T.s[i].rows : max_rows;
+    const int G = heads / M.kv_heads;
+    const dim3 grid(T.n * M.kv_heads * nch, (max_rows * G + 63) / 64);
+    const dim3 mgrid(T.total * heads);
+    const bool fast = fa_fast(kc, vc, hd);
+    if (HD == 64)
+        launch_split_hd<C, 64>(fast, grid, mgrid, s, q, kc, vc, part, pml, out, T, M, heads, hd, bidirectional, window, nch);
+    else if (HD == 128)
+        launch_split_hd<C, 128>(fast, grid, mgrid, s, q, kc, vc, part, pml, out, T, M, heads, hd, bidirectional, window, nch);
+    else
+        launch_split_hd<C, 256>(fast, grid, mgrid, s, q, kc, vc, part, pml, out, T, M, heads, hd, bidirectional, window, nch);
 }
 
 int launch_attention(const float *q, const void *kc, const void *vc, float *out, int elem, const SegTable &T,
-                     const KvMap &M, int heads, int hd, int bidirectional, int window, hipStream_t s) {
+                     const KvMap &M, int heads, int hd, int bidirectional, int window, hipStream_t s,
+                     void *ws = nullptr, size_t ws_bytes = 0, int span_rows = 0) {
     if (!q || !kc || !vc || !out || (elem != 2 && elem != 4)) return VQ_ERR_ARG;
     if (M.kv_heads < 1 || heads < M.kv_heads || heads % M.kv_heads || hd < 1 || hd > kAttnMaxHd || window < 0)
         return VQ_ERR_SHAPE;
+    if (ws != nullptr) {  // decode / verify passes with a workspace: the split-context MFMA kernel
+        int max_rows = 0;
+        for (int i = 0; i < T.n; ++i) max_rows = T.s[i].rows > max_rows ? T.s[i].rows : max_rows;
+        if (max_rows <= VQ_ATTN_ROW_MAX) {
+            if (ws_bytes < split_ws_bytes(T, span_rows, heads, M.kv_heads, hd, window) ||
+                (reinterpret_cast<uintptr_t>(ws) & 15))
+                return VQ_ERR_WORKSPACE;
+            if (elem == 2)
+                launch_attention_split(q, static_cast<const _Float16 *>(kc), static_cast<const _Float16 *>(vc), out, T,
+                                       M, heads, hd, bidirectional, window, span_rows, ws, s);
+            else
+                launch_attention_split(q, static_cast<const float *>(kc), static_cast<const float *>(vc), out, T, M,
+                                       heads, hd, bidirectional, window, span_rows, ws, s);
+            return status_of(hipGetLastError());
+        }
+    }
     // Passes with a segment of more than VQ_ATTN_ROW_MAX rows (prompt passes): the MFMA kernel reads each K/V
     // tile once per 16 query rows and 4 heads; decode and verify passes: one workgroup per (head, row).
     int max_rows = 0;
@@ -853,6 +1114,46 @@ int vq_attention_seg(const float *q, const void *kc, const void *vc, float *out,
     if (kv_heads < 1) return VQ_ERR_SHAPE;
     return launch_attention(q, kc, vc, out, elem, T, paged(page_table, page_size, pages_per_seq, kv_heads), heads, hd,
                             0, 0, static_cast<hipStream_t>(stream));
+}
+
+size_t vq_attention_workspace_bytes(int heads, int kv_heads, int hd, int seq_len, int ntok, int window) {
+    if (kv_heads < 1 || heads < kv_heads || heads % kv_heads || hd < 1 || hd > kAttnMaxHd || ntok < 1 || seq_len < 1 ||
+        window < 0)
+        return 0;
+    if (ntok > VQ_ATTN_ROW_MAX) return 0;
+    return split_ws_bytes(one_segment(seq_len - 1, ntok), ntok, heads, kv_heads, hd, window);
+}
+
+int vq_attention_ws(const float *q, const void *kc, const void *vc, float *out, int elem, int heads, int kv_heads,
+                    int hd, int max_seq, int seq_len, int ntok, int bidirectional, int window, void *workspace,
+                    size_t workspace_bytes, void *stream) {
+    if (kv_heads < 1 || ntok < 1 || seq_len < 1 || seq_len + ntok - 1 > max_seq) return VQ_ERR_SHAPE;
+    return launch_attention(q, kc, vc, out, elem, one_segment(seq_len - 1, ntok), contiguous(max_seq, kv_heads), heads,
+                            hd, bidirectional, window, static_cast<hipStream_t>(stream), workspace, workspace_bytes,
+                            ntok);
+}
+
+size_t vq_attention_seg_workspace_bytes(const int32_t *segs, int nseg, int heads, int kv_heads, int hd) {
+    SegTable T;
+    int span = 0;
+    if (make_table(segs, nseg, T, &span) != VQ_OK) return 0;
+    if (kv_heads < 1 || heads < kv_heads || heads % kv_heads || hd < 1 || hd > kAttnMaxHd) return 0;
+    for (int i = 0; i < T.n; ++i)
+        if (T.s[i].rows > VQ_ATTN_ROW_MAX) return 0;
+    return split_ws_bytes(T, span, heads, kv_heads, hd, 0);
+}
+
+int vq_attention_seg_ws(const float *q, const void *kc, const void *vc, float *out, int elem, const int32_t *segs,
+                        int nseg, int heads, int kv_heads, int hd, const int32_t *page_table, int page_size,
+                        int pages_per_seq, void *workspace, size_t workspace_bytes, void *stream) {
+    SegTable T;
+    int span = 0;
+    int st = make_table(segs, nseg, T, &span);
+    if (st == VQ_OK) st = check_paging(page_table, page_size, pages_per_seq, T);
+    if (st != VQ_OK) return st;
+    if (kv_heads < 1) return VQ_ERR_SHAPE;
+    return launch_attention(q, kc, vc, out, elem, T, paged(page_table, page_size, pages_per_seq, kv_heads), heads, hd,
+                            0, 0, static_cast<hipStream_t>(stream), workspace, workspace_bytes, span);
 }
 
 int vq_conv_update(const float *x, float *state, const float *w, float *out, int channels, int K, int ntok, float *snap,

@@ -391,9 +391,11 @@ class Runtime:
         ob = self._f32_buffer(out, n)
         if kcb.elem != vcb.elem:
             raise TypeError("K and V caches differ in precision")
-        _lib.check(self._lib.vq_attention(qb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(), ob.data_ptr(),
-                                          kcb.elem, heads, kv_heads, hd, max_seq, seq_len, ntok, int(bidirectional),
-                                          int(window), self._stream()), "attention")
+        nws = self._lib.vq_attention_workspace_bytes(heads, kv_heads, hd, seq_len, ntok, int(window))
+        ws = self._workspace(nws).data_ptr() if nws else None
+        _lib.check(self._lib.vq_attention_ws(qb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(), ob.data_ptr(),
+                                             kcb.elem, heads, kv_heads, hd, max_seq, seq_len, ntok, int(bidirectional),
+                                             int(window), ws, nws, self._stream()), "attention")
 
     def conv_update(self, x: str, state: str, w: str, out: str, channels: int, K: int, ntok: int = 1,
                     snap: str | None = None, write_state: int = 1) -> None:
@@ -544,9 +546,12 @@ class Runtime:
         ob = self._f32_buffer(out, rowsz * self._seg_rows())
         pt, page, pps, _ = self._paging
         for arr, n in self._seg_chunks():
-            _lib.check(self._lib.vq_attention_seg(qb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(), ob.data_ptr(),
-                                                  kcb.elem, arr, n, heads, kv_heads, hd, pt.data_ptr(), page, pps,
-                                                  self._stream()), "attention_seg")
+            nws = self._lib.vq_attention_seg_workspace_bytes(arr, n, heads, kv_heads, hd)
+            ws = self._workspace(nws).data_ptr() if nws else None
+            _lib.check(self._lib.vq_attention_seg_ws(qb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(),
+                                                     ob.data_ptr(), kcb.elem, arr, n, heads, kv_heads, hd,
+                                                     pt.data_ptr(), page, pps, ws, nws, self._stream()),
+                       "attention_seg")
 
     def conv_update_seg(self, x: str, state: str, w: str, out: str, channels: int, K: int, snap: str | None = None,
                         write_state: int = 1) -> None:
