@@ -340,7 +340,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     }
     wait_vm<0>();
     __builtin_amdgcn_sched_barrier(0);
-    load_stage(s >= 0 ? s : 0, RA);
+    if (s >= 0) load_stage(s, RA);  // waves without a stage load nothing
     if (threadIdx.x == 0) s_next = NW;
     Tabs tb{};
     if constexpr (TabSpec<T>::n8 > 0) tb.grid8 = reinterpret_cast<const uint2 *>(s_grid);

@@ -384,18 +384,19 @@ struct Sl<VQ_Q3_K> {
     // p = g & 3, so the caller divides the group's exact integer sum by 2^gsh once.
     static __device__ __forceinline__ constexpr int gsh(int g) { return (g & 3) == 0 ? 0 : (g & 3) == 1 ? 2 : 4; }
     static __device__ __forceinline__ void codes_scaled(const W &w, int s, const Tabs &, uint32_t (&c)[NP][4]) {
-        const int j0 = 4 * (s >> 1);
+        // hmask bit j0 + p goes to bit lb + 2: shifted left by 2, 3, 4, 3 (j0 = 0) or right by 2, 1, 0, 1 (j0 = 4);
+        // parts 1 and 3 share their shifted copy.
+        const bool lo_half = (s >> 1) == 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t qs = w.qs.word(i), hm = w.hm.word(i);
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const int lb = p < 3 ? 2 * p : 4;           // bit of the 2-bit field in the code byte
-                const uint32_t lo = p < 3 ? qs & (0x03030303u << lb) : (qs >> 2) & 0x30303030u;
-                const int d = j0 + p - (lb + 2);            // hmask bit j0 + p moves to bit lb + 2
-                const uint32_t hb = (d >= 0 ? hm >> d : hm << -d) & (0x04040404u << lb);
-                c[p][i] = lo | hb;
-            }
+            const uint32_t h0 = lo_half ? hm << 2 : hm >> 2;
+            const uint32_t h13 = lo_half ? hm << 3 : hm >> 1;
+            const uint32_t h2 = lo_half ? hm << 4 : hm;
+            c[0][i] = (h0 & 0x04040404u) | (qs & 0x03030303u);
+            c[1][i] = (h13 & 0x10101010u) | (qs & 0x0C0C0C0Cu);
+            c[2][i] = (h2 & 0x40404040u) | (qs & 0x30303030u);
+            c[3][i] = ((qs >> 2) & 0x30303030u) | (h13 & 0x40404040u);
         }
     }
     static __device__ __forceinline__ void scales(const W &w, int s, float *sc, float *mn) {
