@@ -219,6 +219,16 @@ int vq_attention_seg_ws(const float *q, const void *kc, const void *vc, float *o
                         int nseg, int heads, int kv_heads, int hd, const int32_t *page_table, int page_size,
                         int pages_per_seq, void *workspace, size_t workspace_bytes, void *stream);
 
+/* vq_attention / vq_attention_seg on the tiled MFMA kernel whatever the row count: each row's result then depends
+ * only on its own sequence (the same key tiles in the same order whatever else runs in the pass), the
+ * attention half of the batch-invariant mode (the reference runs its tensor-core prompt kernel for every
+ * pass then, qwen_runtime.cu:2003-2050, qwen_gpu.py:738-744). */
+int vq_attention_tiled(const float *q, const void *kc, const void *vc, float *out, int elem, int heads, int kv_heads,
+                       int hd, int max_seq, int seq_len, int ntok, int bidirectional, int window, void *stream);
+int vq_attention_seg_tiled(const float *q, const void *kc, const void *vc, float *out, int elem, const int32_t *segs,
+                           int nseg, int heads, int kv_heads, int hd, const int32_t *page_table, int page_size,
+                           int pages_per_seq, void *stream);
+
 /* Causal depthwise conv + SiLU over ntok tokens: per channel the state [channels][K] (K <= VQ_CONV_MAX_K) holds
  * the last K inputs; per token it shifts, appends x[t][c], and out[t][c] = silu(state . w[c]). snap (may be
  * NULL): [ntok - 1][channels][K] states after each token but the last. write_state = 0 leaves the state
@@ -307,6 +317,16 @@ size_t vq_qgemm_workspace_bytes(int type, int rows, int cols, int M);
  * below vq_qgemm_workspace_bytes -> VQ_ERR_WORKSPACE. Replaces: as vq_qgemm (qwen_runtime.cu:1886-1902). */
 int vq_qgemm_ws(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *workspace,
                 size_t workspace_bytes, void *stream);
+
+/* vq_qgemm_ws with flags. VQ_GEMM_BATCH_INVARIANT: the f16 path cuts every tile's K range at boundaries that
+ * depend only on the matrix (not on M), so each token's outputs are bit-identical whatever batch it runs in
+ * (the int8 path, every other type, takes the whole K range per tile and is so already). This is the contract
+ * of the reference's prompt kernels (K order independent of tiling, qwen_runtime.cu:650-654,1883-1885) and of
+ * its --batch-invariant mode (qwen_cli.py:47-49); it costs 10-20 % at 512 tokens. */
+#define VQ_GEMM_BATCH_INVARIANT 1
+size_t vq_qgemm_workspace_bytes_ex(int type, int rows, int cols, int M, int flags);
+int vq_qgemm_ws_ex(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *workspace,
+                   size_t workspace_bytes, int flags, void *stream);
 
 /* Workspace bytes vq_lmhead_argmax needs for this matrix and ntok (0 for invalid arguments). */
 size_t vq_lmhead_argmax_workspace_bytes(int type, int rows, int cols, int ntok);

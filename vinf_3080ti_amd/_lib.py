@@ -45,6 +45,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_attention_ws": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, P, SZ, P]),
     "vq_attention_seg_workspace_bytes": (SZ, [P, I, I, I, I]),
     "vq_attention_seg_ws": (I, [P, P, P, P, I, P, I, I, I, I, P, I, I, P, SZ, P]),
+    "vq_attention_tiled": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, P]),
+    "vq_attention_seg_tiled": (I, [P, P, P, P, I, P, I, I, I, I, P, I, I, P]),
     "vq_conv_update": (I, [P, P, P, P, I, I, I, P, I, P]),
     "vq_conv_update_seg": (I, [P, P, P, P, I, I, P, I, P, I, P]),
     "vq_gated_delta": (I, [P, P, P, P, P, P, I, P, I, I, I, I, F, I, I, P, I, P]),
@@ -61,6 +63,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_qgemm": (I, [I, P, I, I, P, I, P, P]),
     "vq_qgemm_workspace_bytes": (SZ, [I, I, I, I]),
     "vq_qgemm_ws": (I, [I, P, I, I, P, I, P, P, SZ, P]),
+    "vq_qgemm_workspace_bytes_ex": (SZ, [I, I, I, I, I]),
+    "vq_qgemm_ws_ex": (I, [I, P, I, I, P, I, P, P, SZ, I, P]),
     "vq_lmhead_argmax_workspace_bytes": (SZ, [I, I, I, I]),
     "vq_lmhead_argmax": (I, [I, P, I, I, P, I, P, P, P, SZ, P]),
     "vq_dequant_rows": (I, [I, P, I, I, P, P]),
@@ -69,6 +73,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
 
 VQ_OK, VQ_ERR_TYPE, VQ_ERR_SHAPE, VQ_ERR_WORKSPACE, VQ_ERR_ARG, VQ_ERR_NOT_INIT, VQ_ERR_TOO_LARGE = 0, -1, -2, -3, -4, -5, -6
 VQ_NOALLOC_SCRATCH_BYTES = 32 << 20
+VQ_GEMM_BATCH_INVARIANT = 1
 
 _lib: ctypes.CDLL | None = None
 

@@ -642,25 +642,32 @@ int vq_qgemm(int type, const uint8_t *w, int rows, int cols, const void *xpack, 
     });
 }
 
-size_t vq_qgemm_workspace_bytes(int type, int rows, int cols, int M) {
-    if (check_matrix(type, rows, cols) || M < 1 || !gemm16_ok(type, cols, M)) return 0;
-    return vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, device_cus())).total;
+size_t vq_qgemm_workspace_bytes_ex(int type, int rows, int cols, int M, int flags) {
+    if (check_matrix(type, rows, cols) || M < 1 || !gemm16_ok(type, cols, M) || (flags & ~VQ_GEMM_BATCH_INVARIANT))
+        return 0;
+    return vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, device_cus(), flags & VQ_GEMM_BATCH_INVARIANT)).total;
 }
 
-int vq_qgemm_ws(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *workspace,
-                size_t workspace_bytes, void *stream) {
+size_t vq_qgemm_workspace_bytes(int type, int rows, int cols, int M) {
+    return vq_qgemm_workspace_bytes_ex(type, rows, cols, M, 0);
+}
+
+int vq_qgemm_ws_ex(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *workspace,
+                   size_t workspace_bytes, int flags, void *stream) {
     int st = check_matrix(type, rows, cols);
     if (st) return st;
     if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;
+    if (flags & ~VQ_GEMM_BATCH_INVARIANT) return VQ_ERR_ARG;
     if (!w || !xpack || !y || misaligned16(w) || misaligned16(xpack)) return VQ_ERR_ARG;
     if (M < 1) return VQ_ERR_SHAPE;
-    const size_t need = vq_qgemm_workspace_bytes(type, rows, cols, M);
-    if (need == 0) return vq_qgemm(type, w, rows, cols, xpack, M, y, stream);
+    const bool inv = (flags & VQ_GEMM_BATCH_INVARIANT) != 0;
+    const size_t need = vq_qgemm_workspace_bytes_ex(type, rows, cols, M, flags);
+    if (need == 0) return vq_qgemm(type, w, rows, cols, xpack, M, y, stream);  // int8 path: full K per tile
     if (!workspace || workspace_bytes < need || misaligned16(workspace)) return VQ_ERR_WORKSPACE;
     const long rb = row_bytes_of(type, cols);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int cus = device_cus();
-    const vq::G16Ws l = vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, cus));
+    const vq::G16Ws l = vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, cus, inv));
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     gemm_xsplit_kernel<<<M, 256, 0, s>>>(static_cast<const uint8_t *>(xpack), cols, reinterpret_cast<_Float16 *>(ws + l.bh),
                                          reinterpret_cast<_Float16 *>(ws + l.bl), reinterpret_cast<_Float16 *>(ws + l.xs),
@@ -668,8 +675,13 @@ int vq_qgemm_ws(int type, const uint8_t *w, int rows, int cols, const void *xpac
     st = hip_status(hipGetLastError());
     if (st) return st;
     return dispatch_quant(type, [&](auto tc) {
-        return vq::launch_gemm16<decltype(tc)::value>(w, rows, cols, rb, ws, M, y, cus, s);
+        return vq::launch_gemm16<decltype(tc)::value>(w, rows, cols, rb, ws, M, y, cus, s, inv);
     });
+}
+
+int vq_qgemm_ws(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *workspace,
+                size_t workspace_bytes, void *stream) {
+    return vq_qgemm_ws_ex(type, w, rows, cols, xpack, M, y, workspace, workspace_bytes, 0, stream);
 }
 
 size_t vq_lmhead_argmax_workspace_bytes(int type, int rows, int cols, int ntok) {

@@ -45,23 +45,36 @@ typedef _Float16 g16h2 __attribute__((ext_vector_type(2)));
 typedef float g16f4 __attribute__((ext_vector_type(4)));
 
 // Work split: W workgroups each take an equal contiguous share of the U = tiles x super-blocks work units in
-// tile-major order (unit u = tile * nsb + sb; workgroup b owns [b U / W, (b+1) U / W)). With more tiles than CUs,
-// W = CUs (stream-K: no CU idles through a partial last round); else W is the largest multiple of the tile count
-// that fits the CUs (plain split-K). A workgroup that covers a whole tile writes y; the parts of a
-// tile split between workgroups go to slots [tile][k] (k = the workgroup's order among the tile's) that
-// vq_gemm16_reduce adds in slot order (deterministic).
+// tile-major order (unit u = tile * nsb + sb; workgroup b owns [b U / W, (b+1) U / W)). A workgroup that covers a
+// whole tile writes y; the parts of a tile split between workgroups go to slots [tile][k] (k = the workgroup's
+// order among the tile's) that vq_gemm16_reduce adds in slot order (deterministic). Two plans:
+//  - default: with more tiles than CUs, W = CUs (stream-K: no CU idles through a partial last round); else W is
+//    the largest multiple of the tile count that fits the CUs (plain split-K). The split depends on M.
+//  - batch-invariant: every tile's super-blocks are cut at the same P - 1 boundaries (P = CUs / row tiles,
+//    rounded, at most nsb), W = tiles x P. P depends only on the matrix, so a token's result is the same whatever
+//    batch it runs in (the reference's contract for its prompt kernels, qwen_runtime.cu:1883-1885), at 10-20 %
+//    more time at 512 tokens (more partial tiles to add).
 struct G16Plan {
     int tiles, ntt, nsb, W, per_xcd, maxseg;
     long U;
     __host__ __device__ int wg_of(long u) const { return static_cast<int>(((u + 1) * W - 1) / U); }  // owner of u
     __host__ __device__ long u0(int b) const { return static_cast<long>(b) * U / W; }
 };
-inline G16Plan g16_plan(int rows, int cols, int M, int cus) {
+inline G16Plan g16_plan(int rows, int cols, int M, int cus, bool invariant = false) {
     G16Plan p{};
     p.ntt = (M + kG16BN - 1) / kG16BN;
-    p.tiles = ((rows + kG16BM - 1) / kG16BM) * p.ntt;
+    const int row_tiles = (rows + kG16BM - 1) / kG16BM;
+    p.tiles = row_tiles * p.ntt;
     p.nsb = cols >> 8;
     p.U = static_cast<long>(p.tiles) * p.nsb;
+    if (invariant) {
+        int P = (cus + row_tiles / 2) / row_tiles;
+        P = P < 1 ? 1 : P > p.nsb ? p.nsb : P;
+        p.W = p.tiles * P;
+        p.per_xcd = (p.W + 7) / 8;
+        p.maxseg = P;
+        return p;
+    }
     // Fewer tiles than CUs: an equal whole number of workgroups per tile (each tile splits at super-block
     // boundaries into that many segments, no workgroup straddles two tiles); else one workgroup per CU.
     if (p.tiles <= cus) {
@@ -380,12 +393,12 @@ __global__ __launch_bounds__(512) inline void g16_reduce_kernel(const float *__r
 
 template <int T>
 int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
-                  hipStream_t s) {
+                  hipStream_t s, bool invariant) {
     if constexpr (!kGemm16<T>) {
-        (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)y, (void)cus, (void)s;
+        (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)y, (void)cus, (void)s, (void)invariant;
         return static_cast<int>(hipErrorInvalidValue);
     } else {
-        const G16Plan pl = g16_plan(rows, cols, M, cus);
+        const G16Plan pl = g16_plan(rows, cols, M, cus, invariant);
         const G16Ws l = g16_layout(cols, M, pl);
         uint8_t *base = static_cast<uint8_t *>(const_cast<void *>(ws));
         float *const part = reinterpret_cast<float *>(base + l.part);

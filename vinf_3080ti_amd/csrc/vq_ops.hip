@@ -893,7 +893,7 @@ void launch_attention_split(const float *q, const C *kc, const C *vc, float *out
 
 int launch_attention(const float *q, const void *kc, const void *vc, float *out, int elem, const SegTable &T,
                      const KvMap &M, int heads, int hd, int bidirectional, int window, hipStream_t s,
-                     void *ws = nullptr, size_t ws_bytes = 0, int span_rows = 0) {
+                     void *ws = nullptr, size_t ws_bytes = 0, int span_rows = 0, bool force_tiled = false) {
     if (!q || !kc || !vc || !out || (elem != 2 && elem != 4)) return VQ_ERR_ARG;
     if (M.kv_heads < 1 || heads < M.kv_heads || heads % M.kv_heads || hd < 1 || hd > kAttnMaxHd || window < 0)
         return VQ_ERR_SHAPE;
@@ -917,7 +917,7 @@ int launch_attention(const float *q, const void *kc, const void *vc, float *out,
     // tile once per 16 query rows and 4 heads; decode and verify passes: one workgroup per (head, row).
     int max_rows = 0;
     for (int i = 0; i < T.n; ++i) max_rows = T.s[i].rows > max_rows ? T.s[i].rows : max_rows;
-    if (max_rows > VQ_ATTN_ROW_MAX) {
+    if (max_rows > VQ_ATTN_ROW_MAX || force_tiled) {
         if (elem == 2)
             launch_attention_mfma(q, static_cast<const _Float16 *>(kc), static_cast<const _Float16 *>(vc), out, T, M,
                                   heads, hd, bidirectional, window, s);
@@ -1154,6 +1154,25 @@ int vq_attention_seg_ws(const float *q, const void *kc, const void *vc, float *o
     if (kv_heads < 1) return VQ_ERR_SHAPE;
     return launch_attention(q, kc, vc, out, elem, T, paged(page_table, page_size, pages_per_seq, kv_heads), heads, hd,
                             0, 0, static_cast<hipStream_t>(stream), workspace, workspace_bytes, span);
+}
+
+int vq_attention_tiled(const float *q, const void *kc, const void *vc, float *out, int elem, int heads, int kv_heads,
+                       int hd, int max_seq, int seq_len, int ntok, int bidirectional, int window, void *stream) {
+    if (kv_heads < 1 || ntok < 1 || seq_len < 1 || seq_len + ntok - 1 > max_seq) return VQ_ERR_SHAPE;
+    return launch_attention(q, kc, vc, out, elem, one_segment(seq_len - 1, ntok), contiguous(max_seq, kv_heads), heads,
+                            hd, bidirectional, window, static_cast<hipStream_t>(stream), nullptr, 0, 0, true);
+}
+
+int vq_attention_seg_tiled(const float *q, const void *kc, const void *vc, float *out, int elem, const int32_t *segs,
+                           int nseg, int heads, int kv_heads, int hd, const int32_t *page_table, int page_size,
+                           int pages_per_seq, void *stream) {
+    SegTable T;
+    int st = make_table(segs, nseg, T, nullptr);
+    if (st == VQ_OK) st = check_paging(page_table, page_size, pages_per_seq, T);
+    if (st != VQ_OK) return st;
+    if (kv_heads < 1) return VQ_ERR_SHAPE;
+    return launch_attention(q, kc, vc, out, elem, T, paged(page_table, page_size, pages_per_seq, kv_heads), heads, hd,
+                            0, 0, static_cast<hipStream_t>(stream), nullptr, 0, 0, true);
 }
 
 int vq_conv_update(const float *x, float *state, const float *w, float *out, int channels, int K, int ntok, float *snap,

@@ -57,10 +57,11 @@ int launch_gemm(const uint8_t *w, int rows, int cols, long row_bytes, const uint
                 hipStream_t s);
 // Prefill contraction on f16 MFMA (Q4_K, Q5_K; other types return hipErrorInvalidValue): `ws` holds the split
 // activations written by the library's pre-pass and the partial-tile slots (layout g16_layout for
-// g16_plan(rows, cols, M, cus)); one workgroup per CU (cus of them) and the reduction of split tiles.
+// g16_plan(rows, cols, M, cus, invariant)) and the reduction of split tiles; invariant: the K split depends on the
+// matrix only (batch-invariant results).
 template <int T>
 int launch_gemm16(const uint8_t *w, int rows, int cols, long row_bytes, const void *ws, int M, float *y, int cus,
-                  hipStream_t s);
+                  hipStream_t s, bool invariant);
 // Matvec of 1..16 tokens on f16 MFMA (Q3_K, Q4_K, Q5_K, Q6_K; other types return hipErrorInvalidValue), fp32
 // activations; `part` holds s16_part_bytes(rows, cols, ntok) bytes (unused when that is 0).
 template <int T>

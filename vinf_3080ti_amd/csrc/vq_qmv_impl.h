@@ -1039,7 +1039,7 @@ int launch_dequant(const uint8_t *w, int rows, int cols, long rb, float *out, hi
     template int vq::launch_mixed_q8<T>(int, const int *, const uint8_t *const *, const int *, float *const *, int, \
                                         const float *, int, hipStream_t);                                          \
     template int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \
-    template int vq::launch_gemm16<T>(const uint8_t *, int, int, long, const void *, int, float *, int, hipStream_t); \
+    template int vq::launch_gemm16<T>(const uint8_t *, int, int, long, const void *, int, float *, int, hipStream_t, bool); \
     template int vq::launch_small16<T>(const uint8_t *, int, int, long, const float *, int, float *, float *,          \
                                        hipStream_t);                                                               \
     template int vq::launch_mfma<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, float *,       \

@@ -90,6 +90,7 @@ class Runtime:
         self._argmax_out = torch.empty(MAX_ARGMAX_ROWS, dtype=torch.int32, device=self.device)
         self._ws = torch.empty(0, dtype=torch.uint8, device=self.device)
         self.gemm_min_rows = 0
+        self.batch_invariant = False
         self._paging: tuple[torch.Tensor, int, int, int] | None = None
         self._segments: list[tuple[int, int, int, int]] = []
 
@@ -239,13 +240,14 @@ class Runtime:
         if t.type not in (0, 1) and self.gemm_min_rows > 0 and ntok >= self.gemm_min_rows:
             # Prompt pass: the MFMA contraction (the prefill branch of Runtime_qmv, qwen_runtime.cu:1886-1902):
             # packed activations, then the contraction's own workspace (f16 path of Q4_K/Q5_K; 0 bytes otherwise).
+            flags = _lib.VQ_GEMM_BATCH_INVARIANT if self.batch_invariant else 0
             nx = (self._lib.vq_xpack_bytes(t.cols, ntok) + 255) // 256 * 256
-            ng = self._lib.vq_qgemm_workspace_bytes(t.type, t.rows, t.cols, ntok)
+            ng = self._lib.vq_qgemm_workspace_bytes_ex(t.type, t.rows, t.cols, ntok, flags)
             buf = self._workspace(nx + ng)
             xp = buf.data_ptr()
             _lib.check(self._lib.vq_pack_x(x_ptr, ntok, t.cols, xp, self._stream()), "pack_x")
-            st = self._lib.vq_qgemm_ws(t.type, t.data.data_ptr(), t.rows, t.cols, xp, ntok, y_ptr,
-                                       (xp + nx) if ng else None, ng, self._stream())
+            st = self._lib.vq_qgemm_ws_ex(t.type, t.data.data_ptr(), t.rows, t.cols, xp, ntok, y_ptr,
+                                          (xp + nx) if ng else None, ng, flags, self._stream())
             _lib.check(st, "qgemm launch")
             return
         if t.type in (0, 1):
@@ -391,6 +393,11 @@ class Runtime:
         ob = self._f32_buffer(out, n)
         if kcb.elem != vcb.elem:
             raise TypeError("K and V caches differ in precision")
+        if self._tiled_attention(ntok):
+            _lib.check(self._lib.vq_attention_tiled(qb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(),
+                                                    ob.data_ptr(), kcb.elem, heads, kv_heads, hd, max_seq, seq_len, ntok,
+                                                    int(bidirectional), int(window), self._stream()), "attention")
+            return
         nws = self._lib.vq_attention_workspace_bytes(heads, kv_heads, hd, seq_len, ntok, int(window))
         ws = self._workspace(nws).data_ptr() if nws else None
         _lib.check(self._lib.vq_attention_ws(qb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(), ob.data_ptr(),
@@ -545,7 +552,13 @@ class Runtime:
         kcb, vcb = self._kv_pair(kc, vc, 1)
         ob = self._f32_buffer(out, rowsz * self._seg_rows())
         pt, page, pps, _ = self._paging
+        tiled = self._tiled_attention(max(r for _, _, r, _ in self._segments))
         for arr, n in self._seg_chunks():
+            if tiled:  # prompt rows in the pass, or batch-invariant mode
+                _lib.check(self._lib.vq_attention_seg_tiled(qb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(),
+                                                            ob.data_ptr(), kcb.elem, arr, n, heads, kv_heads, hd,
+                                                            pt.data_ptr(), page, pps, self._stream()), "attention_seg")
+                continue
             nws = self._lib.vq_attention_seg_workspace_bytes(arr, n, heads, kv_heads, hd)
             ws = self._workspace(nws).data_ptr() if nws else None
             _lib.check(self._lib.vq_attention_seg_ws(qb.data_ptr(), kcb.data.data_ptr(), vcb.data.data_ptr(),
@@ -633,6 +646,10 @@ class Runtime:
         if any(t.cols != t0.cols or t.type in (0, 1) for t in ts):
             raise ValueError("qmv_group weights must be quantized and share cols")
         _check_qmv_args(weights[0], t0.cols, ntok)
+        if self.gemm_min_rows > 0 and ntok >= self.gemm_min_rows:  # prompt (or batch-invariant) passes: as qmv
+            for w, y in zip(weights, ys):
+                self.qmv(w, x, y, ntok)
+            return
         xb = self._f32_buffer(x, t0.cols * ntok)
         yb = [self._f32_buffer(y, t.rows * ntok) for y, t in zip(ys, ts)]
         n = len(ts)
@@ -664,6 +681,13 @@ class Runtime:
             raise ValueError(f"{weight}: lmhead_argmax needs a quantized weight")
         _check_qmv_args(weight, t.cols, ntok)
         xb = self._f32_buffer(x, t.cols * ntok)
+        if self.batch_invariant:  # the matvec on the invariant path, then the row argmax
+            yt = (self._f32_buffer(logits, t.rows * ntok) if logits is not None
+                  else torch.empty(t.rows * ntok, dtype=torch.float32, device=self.device))
+            self._qmv_ptrs(t, xb.data_ptr(), yt.data_ptr(), ntok)
+            _lib.check(self._lib.vq_argmax_rows(yt.data_ptr(), t.rows, ntok, self._argmax_out.data_ptr(),
+                                                self._stream()), "argmax_rows")
+            return [int(v) for v in self._argmax_out[:ntok].tolist()]
         lp = self._f32_buffer(logits, t.rows * ntok).data_ptr() if logits is not None else None
         nws = self._lib.vq_lmhead_argmax_workspace_bytes(t.type, t.rows, t.cols, ntok)
         ws = self._workspace(nws)
@@ -722,6 +746,18 @@ class Runtime:
         if n < 0:
             raise ValueError("gemm_min_rows must be >= 0")
         self.gemm_min_rows = int(n)
+
+    def set_batch_invariant(self, on: bool = True) -> None:
+        """Every pass on the kernels whose per-row results do not depend on the other rows of the pass: qmv through
+        the prompt contraction with a K split fixed by the matrix (gemm_min_rows = 1), attention through the tiled
+        kernel. The reference's --batch-invariant mode (qwen_cli.py:47-49; it sets gemm_min_rows to 1 for every
+        pass, qwen_gpu.py:738-744): slower for a lone request, and a request's outputs never depend on what runs
+        beside it. Off restores gemm_min_rows = 0."""
+        self.batch_invariant = bool(on)
+        self.gemm_min_rows = 1 if on else 0
+
+    def _tiled_attention(self, rows: int) -> bool:
+        return self.batch_invariant or (self.gemm_min_rows > 0 and rows >= self.gemm_min_rows)
 
     def synchronize(self) -> None:
         torch.cuda.synchronize(self.device)
