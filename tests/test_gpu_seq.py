@@ -459,3 +459,39 @@ def test_decode_attention_split_and_per_row_kernels(oracle_mod, elem, ntok, seq_
     assert np.array_equal(outs[1].view(np.uint32), outs[2].view(np.uint32))
     assert lib.vq_attention_ws(qd.data_ptr(), kd_.data_ptr(), vd_.data_ptr(), qd.data_ptr(), elem, heads, kvh, hd,
                                max_seq, seq_len, ntok, 0, window, ws.data_ptr(), nws - 300, None) == _lib.VQ_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("heads,kvh,hd,ntok,seq_len,qmag", [(32, 2, 128, 8, 2000, 1.0), (8, 8, 64, 1, 5000, 1.0),
+                                                            (24, 4, 256, 1, 33, 1e3), (24, 4, 256, 3, 300, 1e-3),
+                                                            (4, 1, 128, 7, 129, 1.0), (24, 4, 256, 8, 9000, 1.0)])
+def test_decode_attention_fp16_cache_shapes(oracle_mod, heads, kvh, hd, ntok, seq_len, qmag):
+    """The fp16-cache decode kernel (f16 MFMA on exact hi/lo splits of the query and the softmax weights) over
+    head shapes 64/128/256, groups of 1 to 16 query heads per kv head (up to 8 query groups of 16 vectors), one
+    chunk (no merge) and many, and queries of magnitude 1e3 and 1e-3 (the per-vector power-of-two scaling):
+    within the fp32 bar of the float64 restatement, bit-identical on a rerun."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from vinf_3080ti_amd import _lib
+
+    lib = _lib.load()
+    assert lib.vq_init() == 0
+    rng = np.random.default_rng(heads * hd + ntok + seq_len)
+    max_seq = seq_len + ntok + 3
+    q = (rng.standard_normal((ntok, heads, hd)) * qmag).astype(np.float32)
+    kc = (rng.standard_normal((kvh, max_seq, hd)) * 0.3 / max(qmag, 1.0) ** 0.5).astype(np.float16)
+    vc = rng.standard_normal((kvh, max_seq, hd)).astype(np.float16)
+    qd, kd_, vd_ = (torch.from_numpy(a).cuda() for a in (q, kc, vc))
+    nws = lib.vq_attention_workspace_bytes(heads, kvh, hd, seq_len, ntok, 0)
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+    outs = []
+    for _ in range(2):
+        o = torch.full_like(qd, float("nan"))
+        st = lib.vq_attention_ws(qd.data_ptr(), kd_.data_ptr(), vd_.data_ptr(), o.data_ptr(), 2, heads, kvh, hd,
+                                 max_seq, seq_len, ntok, 0, 0, ws.data_ptr(), nws, None)
+        assert st == 0, lib.vq_status_string(st)
+        torch.cuda.synchronize()
+        outs.append(o.cpu().numpy())
+    ref = oracle_mod.attention(q, kc, vc, heads, kvh, seq_len, False, 0)
+    assert np.allclose(outs[0], ref, rtol=2e-5, atol=2e-5), float(np.abs(outs[0] - ref).max())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))

@@ -359,6 +359,7 @@ template <int HD>
 struct FaTiles {
     float k[kFaKeys * (HD + 4)];
     float vt[HD * kFaLdk];
+    size_t rows[2][kFaKeys];  // cache row of each key of the current / next tile (page-table lookups done once)
 };
 
 template <typename C, int HD, bool FAST>
@@ -369,8 +370,13 @@ __device__ __forceinline__ void fa_keys(const C *__restrict__ kc, const C *__res
     constexpr int LD = HD + 4;
     constexpr int NQ = kFaKeys * (HD / 4) / 256;  // quads of K (and of V) per thread per tile
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    for (int k0 = k_lo; k0 < k_hi; k0 += kFaKeys) {
-        __syncthreads();  // the previous tile is consumed
+    // Cache rows of the keys of a tile (clamped into [.., k_hi)): the first tile's here, each next tile's while
+    // the current one is staged, so a paged cache costs one page-table load per key and no serial round trips.
+    auto key_row = [&](int p) { return M.row(slot, kvh, p < k_hi ? p : k_hi - 1); };
+    if (threadIdx.x < kFaKeys && k_lo < k_hi) tl.rows[0][threadIdx.x] = key_row(k_lo + threadIdx.x);
+    for (int k0 = k_lo, cur = 0; k0 < k_hi; k0 += kFaKeys, cur ^= 1) {
+        __syncthreads();  // the previous tile is consumed; this tile's rows are visible
+        const size_t *rw = tl.rows[cur];
         // K quad i: key i / (HD/4), dims 4 (i % (HD/4)) .. (row-major writes); V quad i: key i % kFaKeys, dims
         // 4 (i / kFaKeys) .. (consecutive lanes write consecutive keys of the transposed tile).
         if constexpr (FAST) {
@@ -386,9 +392,8 @@ __device__ __forceinline__ void fa_keys(const C *__restrict__ kc, const C *__res
                     const int i = threadIdx.x + 256 * (u0 + u);
                     const int kk = i / (HD / 4), kd = 4 * (i - kk * (HD / 4));
                     const int vk = i % kFaKeys, vd = 4 * (i / kFaKeys);
-                    const int pk = k0 + kk < k_hi ? k0 + kk : k_hi - 1, pv = k0 + vk < k_hi ? k0 + vk : k_hi - 1;
-                    kq[u] = ld4(kc, M.row(slot, kvh, pk) * hd + (kd < hd ? kd : 0));
-                    vq[u] = ld4(vc, M.row(slot, kvh, pv) * hd + (vd < hd ? vd : 0));
+                    kq[u] = ld4(kc, rw[kk] * hd + (kd < hd ? kd : 0));
+                    vq[u] = ld4(vc, rw[vk] * hd + (vd < hd ? vd : 0));
                 }
 #pragma unroll
                 for (int u = 0; u < NH; ++u) {
@@ -410,10 +415,11 @@ __device__ __forceinline__ void fa_keys(const C *__restrict__ kc, const C *__res
                 const int kk = i / HD, kd = i - kk * HD;      // K element
                 const int vk = i % kFaKeys, vd = i / kFaKeys;  // V element
                 const bool okk = k0 + kk < k_hi && kd < hd, okv = k0 + vk < k_hi && vd < hd;
-                tl.k[kk * LD + kd] = okk ? kv_get(kc, M.row(slot, kvh, k0 + kk) * hd + kd) : 0.0f;
-                tl.vt[vd * kFaLdk + vk] = okv ? kv_get(vc, M.row(slot, kvh, k0 + vk) * hd + vd) : 0.0f;
+                tl.k[kk * LD + kd] = okk ? kv_get(kc, rw[kk] * hd + kd) : 0.0f;
+                tl.vt[vd * kFaLdk + vk] = okv ? kv_get(vc, rw[vk] * hd + vd) : 0.0f;
             }
         }
+        if (threadIdx.x < kFaKeys && k0 + kFaKeys < k_hi) tl.rows[cur ^ 1][threadIdx.x] = key_row(k0 + kFaKeys + threadIdx.x);
         __syncthreads();
         if (!wave_on) continue;
 #pragma unroll
@@ -476,7 +482,9 @@ __device__ __forceinline__ void fa_load_q(const float *qrow, int hd, float scale
 #pragma unroll
     for (int st = 0; st < HD / 4; ++st) {
         const int d = 16 * (st >> 2) + 4 * grp + (st & 3);
-        qf[st] = d < hd ? qrow[d] * scale : 0.0f;
+        // Clamped address and a multiplied mask rather than a branch: all HD/4 loads are issued before the
+        // first wait (guarded loads are each issued and waited for on their own).
+        qf[st] = qrow[d < hd ? d : hd - 1] * (d < hd ? scale : 0.0f);
     }
 }
 
@@ -578,6 +586,254 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float *__res
     }
 }
 
+// ---- fp16 caches on f16 MFMA (v_mfma_f32_16x16x32_f16) --------------------------------------------------------
+// The fp32 products of the kernels above become exact f16 products: K and V are fp16 already; each fp32 operand
+// that is not (the query, pre-scaled by 1/sqrt(hd) and by a power of two 2^s per query vector that puts its
+// largest element near 2^14, and the softmax weights p in [0, 1]) is split into an f16 pair hi + lo with
+// hi = f16(x), lo = f16(x - hi), 22 significant bits. Each MFMA adds exact products in fp32, so S and O differ
+// from an fp32 evaluation only by the representation error of the pair (2^-22 relative per element) and by
+// fp32 rounding of sums; S is scaled back by 2^-s exactly. Per 32 keys a wave issues HD/32 x 2 x 2 MFMAs for S
+// and HD/16 x 2 for O (a quarter of the fp32 MFMA count, each at twice the rate).
+//
+// Operand layout of v_mfma_f32_16x16x32_f16 as used here: lane l = (col c = l & 15, group g = l >> 4) gives row c
+// of A and column c of B at the same eight k slots (g, j), j < 8; the result has rows 4 g + r, column c.
+//  - S^T (keys x query vectors) of key half h of a 32-key block: A = K rows (key kb + 16 h + c; dims 32 u + 8 g + j,
+//    one 16-byte load), B = the query vector c at the same dims; lane (c, g) ends with keys kb + 16 h + 4 g + r.
+//  - O^T (dims x query vectors) += V^T P^T: k slot (g, j) is key kb + 4 g + j (j < 4) or kb + 16 + 4 g + j - 4
+//    (j >= 4), so B is the lane's own eight softmax weights and A is row 16 b + c of V^T at positions 8 g .. 8 g + 7:
+//    V^T is staged per wave in LDS, [dim][32 positions] f16, 16-byte chunks XOR-swizzled by (dim >> 2) & 3
+//    (the 16 rows a read instruction touches land on distinct banks).
+typedef _Float16 fh8 __attribute__((ext_vector_type(8)));
+typedef _Float16 fh4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ fh8 ld_h8(const _Float16 *p) {
+    const uint4 v = *reinterpret_cast<const uint4 *>(p);
+    return __builtin_bit_cast(fh8, v);
+}
+__device__ __forceinline__ void split_h(float x, _Float16 &hi, _Float16 &lo) {
+    hi = static_cast<_Float16>(x);
+    lo = static_cast<_Float16>(x - static_cast<float>(hi));
+}
+// Position of key k (0..31 of a block) among the 32 k slots of the O^T product.
+__device__ __forceinline__ int fa16_pos(int k) { return k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3); }
+__device__ __forceinline__ int fa16_vt(int d, int pos) { return d * 32 + (((pos >> 3) ^ ((d >> 2) & 3)) << 3) + (pos & 7); }
+
+// The query vector of lane column c as B operands (dims 32 u + 8 g + j), times 1/sqrt(hd) * 2^s; returns 2^-s.
+template <int HD>
+__device__ __forceinline__ float fa16_load_q(const float *qrow, float scale, fh8 (&qh)[HD / 32], fh8 (&ql)[HD / 32]) {
+    const int g = (threadIdx.x & 63) >> 4;
+    float qv[HD / 32][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int u = 0; u < HD / 32; ++u) {
+        const float4 a = *reinterpret_cast<const float4 *>(qrow + 32 * u + 8 * g);
+        const float4 b = *reinterpret_cast<const float4 *>(qrow + 32 * u + 8 * g + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            qv[u][j] = v[j] * scale;
+            amax = fmaxf(amax, fabsf(qv[u][j]));
+        }
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    int ex = 0;
+    if (amax > 0.0f && amax <= 3.0e38f) frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
+    const float up = ldexpf(1.0f, 14 - ex);
+#pragma unroll
+    for (int u = 0; u < HD / 32; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            _Float16 h, l;
+            split_h(qv[u][j] * up, h, l);
+            qh[u][j] = h;
+            ql[u][j] = l;
+        }
+    return ldexpf(1.0f, ex - 14);
+}
+
+// One 32-key block [kb, kb + 32) of kv head kvh against the wave's 16 query vectors (lane column c sees keys
+// [qs, qe)); keys at or past k_hi are masked. vt is the wave's V^T area (HD x 32 f16).
+template <int HD>
+__device__ __forceinline__ void fa16_block(const _Float16 *__restrict__ kc, const _Float16 *__restrict__ vc,
+                                           const KvMap &M, int slot, int kvh, int kb, int k_hi, int qs, int qe,
+                                           const fh8 (&qh)[HD / 32], const fh8 (&ql)[HD / 32], float sinv,
+                                           _Float16 *vt, float &m, float &l, fa4 (&o)[HD / 16]) {
+    constexpr int CR = HD / 8;       // 16-byte chunks per row
+    constexpr int UPL = CR / 8;      // V units (4 keys x one chunk) per lane
+    const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+    // Cache rows of the block's keys: lane k < 32 looks up key kb + k (clamped), the others read it by shuffle.
+    const size_t myrow = M.row(slot, kvh, min(kb + (lane & 31), k_hi - 1));
+    auto row_of = [&](int k) {
+        const uint32_t lo32 = __shfl(static_cast<uint32_t>(myrow), k, 64);
+        const uint32_t hi32 = __shfl(static_cast<uint32_t>(myrow >> 32), k, 64);
+        return (static_cast<size_t>(hi32) << 32) | lo32;
+    };
+    fh8 ka[2][HD / 32];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const size_t kr = row_of(16 * h + c) * HD + 8 * g;
+#pragma unroll
+        for (int u = 0; u < HD / 32; ++u) ka[h][u] = ld_h8(kc + kr + 32 * u);
+    }
+    // V: unit (key quad qd, chunk dc) -> four 16-byte loads, then eight 8-byte LDS writes of V^T.
+    fh8 vv[UPL][4];
+#pragma unroll
+    for (int it = 0; it < UPL; ++it) {
+        const int unit = lane + 64 * it, dc = unit % CR, qd = unit / CR;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vv[it][i] = ld_h8(vc + row_of(4 * qd + i) * HD + 8 * dc);
+    }
+#pragma unroll
+    for (int it = 0; it < UPL; ++it) {
+        const int unit = lane + 64 * it, dc = unit % CR, qd = unit / CR;
+        const int pos = fa16_pos(4 * qd);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int d = 8 * dc + j;
+            const fh4 w{vv[it][0][j], vv[it][1][j], vv[it][2][j], vv[it][3][j]};
+            *reinterpret_cast<fh4 *>(vt + fa16_vt(d, pos)) = w;
+        }
+    }
+    // S^T for both key halves: hi and lo query parts in separate chains.
+    fa4 s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        fa4 a0{0.f, 0.f, 0.f, 0.f}, a1{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < HD / 32; ++u) {
+            a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][u], qh[u], a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][u], ql[u], a1, 0, 0, 0);
+        }
+        s[h] = (a0 + a1) * sinv;
+    }
+    float v[8], bm = -INFINITY;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int p = kb + 16 * h + 4 * g + r;
+            v[4 * h + r] = p >= qs && p < qe && p < k_hi ? s[h][r] : -INFINITY;
+            bm = fmaxf(bm, v[4 * h + r]);
+        }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);
+    const float alpha = mn == -INFINITY ? 1.0f : expf(m - mn);
+    fh8 ph, pl;
+    float ps = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float p = v[j] == -INFINITY ? 0.0f : expf(v[j] - mn);
+        ps += p;
+        _Float16 hh, ll;
+        split_h(p, hh, ll);
+        ph[j] = hh;
+        pl[j] = ll;
+    }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * alpha + ps;
+    m = mn;
+    // A wave's LDS operations complete in issue order; the fence keeps the compiler from moving the V^T reads
+    // above the writes of other lanes.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int b = 0; b < HD / 16; ++b) {
+        const fh8 a = *reinterpret_cast<const fh8 *>(vt + fa16_vt(16 * b + c, 8 * g));
+        fa4 ob = o[b] * alpha;
+        ob = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph, ob, 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, ob, 0, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // every lane has read V^T before the next block's writes
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Decode and verify passes on fp16 caches: one workgroup per (segment, kv head, chunk of the keys, group of 16
+// query vectors); its four waves take the chunk's 32-key blocks in turn (wave w: blocks w, w + 4, ...) with their
+// own online softmax, then combine in wave order through LDS. With one chunk the workgroup writes the output;
+// otherwise its unnormalised output and (max, sum) go to the workspace for attention_merge_kernel.
+template <int HD>
+__global__ __launch_bounds__(256) void attention_split16_kernel(const float *__restrict__ q,
+                                                                const _Float16 *__restrict__ kc,
+                                                                const _Float16 *__restrict__ vc, float *__restrict__ part,
+                                                                float *__restrict__ pml, float *__restrict__ out,
+                                                                SegTable T, KvMap M, int heads, int bidirectional,
+                                                                int window, int nch) {
+    __shared__ __align__(16) _Float16 vts[4][HD * 32];  // per-wave V^T; reused as the per-wave [16][HD] fp32 output
+    __shared__ float sm[4][16], sl[4][16];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int ci = blockIdx.x % nch, sk_id = blockIdx.x / nch;
+    const int kvh = sk_id % M.kv_heads, si = sk_id / M.kv_heads;
+    const Seg &s = T.s[si];
+    const int G = heads / M.kv_heads;
+    const int j = blockIdx.y * 16 + c;  // query vector of this lane's column
+    const int t = j / G, gi = j - t * G;
+    const bool valid = t < s.rows;
+    const int tq = valid ? t : s.rows - 1, h = kvh * G + (valid ? gi : 0);
+    const int seq_len0 = s.pos0 + 1;
+    const int qe = bidirectional ? seq_len0 + s.rows - 1 : seq_len0 + tq;
+    const int qs = window > 0 && seq_len0 + tq > window ? seq_len0 + tq - window : 0;
+    const int ctx = seq_len0 + s.rows - 1;
+    const int lo0 = window > 0 && seq_len0 > window ? seq_len0 - window : 0;
+    const int ch = ((ctx - lo0 + nch - 1) / nch + kFaKeys - 1) / kFaKeys * kFaKeys;
+    const int k_lo = lo0 + ci * ch, k_hi = min(ctx, k_lo + ch);
+    float m = -INFINITY, l = 0.0f;
+    fa4 o[HD / 16];
+#pragma unroll
+    for (int b = 0; b < HD / 16; ++b) o[b] = fa4{0.f, 0.f, 0.f, 0.f};
+    if (blockIdx.y * 16 < s.rows * G) {  // groups past the segment's query vectors only wait at the barrier
+        fh8 qh[HD / 32], ql[HD / 32];
+        const float sinv = fa16_load_q<HD>(q + (static_cast<size_t>(s.row0 + tq) * heads + h) * HD,
+                                           1.0f / sqrtf(static_cast<float>(HD)), qh, ql);
+        for (int kb = k_lo + 32 * wv; kb < k_hi; kb += 128)
+            fa16_block<HD>(kc, vc, M, s.slot, kvh, kb, k_hi, qs, qe, qh, ql, sinv, vts[wv], m, l, o);
+    }
+    // Combine the four waves in wave order: o[b][r] is dim 16 b + 4 g + r of query vector c.
+    __syncthreads();
+    float *ow = reinterpret_cast<float *>(vts[wv]);  // [16][HD]
+#pragma unroll
+    for (int b = 0; b < HD / 16; ++b)
+        *reinterpret_cast<fa4 *>(ow + c * HD + 16 * b + 4 * g) = o[b];
+    if (g == 0) {
+        sm[wv][c] = m;
+        sl[wv][c] = l;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < 16 * (HD / 4); e += 256) {
+        const int qc = e / (HD / 4), d4 = 4 * (e - qc * (HD / 4));
+        const int jj = blockIdx.y * 16 + qc, tt = jj / G;
+        if (tt >= s.rows) continue;
+        const int hh = kvh * G + (jj - tt * G);
+        const float mx = fmaxf(fmaxf(sm[0][qc], sm[1][qc]), fmaxf(sm[2][qc], sm[3][qc]));
+        float L = 0.0f;
+        float4 acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float f = sm[w][qc] == -INFINITY ? 0.0f : expf(sm[w][qc] - mx);
+            L = fmaf(sl[w][qc], f, L);
+            const float4 p4 = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(vts[w]) + qc * HD + d4);
+            acc.x = fmaf(p4.x, f, acc.x);
+            acc.y = fmaf(p4.y, f, acc.y);
+            acc.z = fmaf(p4.z, f, acc.z);
+            acc.w = fmaf(p4.w, f, acc.w);
+        }
+        const size_t qv = static_cast<size_t>(s.row0 + tt) * heads + hh;
+        if (nch == 1) {
+            const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+            *reinterpret_cast<float4 *>(out + qv * HD + d4) = float4{acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+        } else {
+            *reinterpret_cast<float4 *>(part + (qv * nch + ci) * HD + d4) = acc;
+            if (d4 == 0) {
+                pml[(qv * nch + ci) * 2] = mx;
+                pml[(qv * nch + ci) * 2 + 1] = L;
+            }
+        }
+    }
+}
+
 // out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, M = max_c m_c; one workgroup of four waves per (row of the
 // pass, head): the chunks' maxima through LDS, then wave w adds chunks w, w + 4, ... (lane = four head dims, one
 // 16-byte load per chunk) and the four waves' sums are added in wave order (deterministic).
@@ -645,8 +901,28 @@ int split_chunks(const SegTable &T, int kv_heads, int window) {
     return want < 1 ? 1 : want > most ? most : want;
 }
 int fa_hd(int hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : 256; }
+int max_seg_rows(const SegTable &T) {
+    int r = 0;
+    for (int i = 0; i < T.n; ++i) r = T.s[i].rows > r ? T.s[i].rows : r;
+    return r;
+}
+// Chunks per sequence of the fp16 decode kernel: one 32-key block per wave where the keys allow it, at most about
+// 512 workgroups for the pass.
+int split16_chunks(const SegTable &T, int heads, int kv_heads, int window) {
+    int ctx = 1;
+    for (int i = 0; i < T.n; ++i) {
+        int c = T.s[i].pos0 + T.s[i].rows;
+        if (window > 0 && c > window + T.s[i].rows) c = window + T.s[i].rows;
+        ctx = c > ctx ? c : ctx;
+    }
+    const int qgroups = (max_seg_rows(T) * (heads / kv_heads) + 15) / 16;
+    const int want = ((ctx + kFaKeys - 1) / kFaKeys + 3) / 4;
+    const int cap = 512 / (T.n * kv_heads * qgroups);
+    return want < 1 ? 1 : want < cap ? want : cap < 1 ? 1 : cap;
+}
 size_t split_ws_bytes(const SegTable &T, int span_rows, int heads, int kv_heads, int hd, int window) {
-    const int nch = split_chunks(T, kv_heads, window);
+    const int n32 = split_chunks(T, kv_heads, window), n16 = split16_chunks(T, heads, kv_heads, window);
+    const int nch = n32 > n16 ? n32 : n16;
     return static_cast<size_t>(span_rows) * heads * nch * (fa_hd(hd) + 2) * 4 + 256;
 }
 
@@ -870,6 +1146,34 @@ void launch_split_hd(bool fast, dim3 grid, dim3 mgrid, hipStream_t s, const floa
     attention_merge_kernel<HD><<<mgrid, 256, 0, s>>>(part, pml, out, T, heads, hd, nch);
 }
 
+// fp16 caches with hd 64, 128 or 256 and 16-byte aligned q, K and V: the f16 MFMA decode kernel.
+bool fa16_ok(const float *q, const void *kc, const void *vc, int hd) {
+    return (hd == 64 || hd == 128 || hd == 256) &&
+           ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15) == 0;
+}
+
+void launch_attention_split16(const float *q, const _Float16 *kc, const _Float16 *vc, float *out, const SegTable &T,
+                              const KvMap &M, int heads, int hd, int bidirectional, int window, int span_rows, void *ws,
+                              hipStream_t s) {
+    const int nch = split16_chunks(T, heads, M.kv_heads, window);
+    float *part = static_cast<float *>(ws);
+    float *pml = part + static_cast<size_t>(span_rows) * heads * nch * fa_hd(hd);
+    const int G = heads / M.kv_heads;
+    const dim3 grid(T.n * M.kv_heads * nch, (max_seg_rows(T) * G + 15) / 16);
+    if (hd == 64)
+        attention_split16_kernel<64><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, out, T, M, heads, bidirectional, window, nch);
+    else if (hd == 128)
+        attention_split16_kernel<128><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, out, T, M, heads, bidirectional, window, nch);
+    else
+        attention_split16_kernel<256><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, out, T, M, heads, bidirectional, window, nch);
+    if (nch > 1) {
+        const dim3 mgrid(T.total * heads);
+        if (hd == 64) attention_merge_kernel<64><<<mgrid, 256, 0, s>>>(part, pml, out, T, heads, hd, nch);
+        else if (hd == 128) attention_merge_kernel<128><<<mgrid, 256, 0, s>>>(part, pml, out, T, heads, hd, nch);
+        else attention_merge_kernel<256><<<mgrid, 256, 0, s>>>(part, pml, out, T, heads, hd, nch);
+    }
+}
+
 template <typename C>
 void launch_attention_split(const float *q, const C *kc, const C *vc, float *out, const SegTable &T, const KvMap &M,
                             int heads, int hd, int bidirectional, int window, int span_rows, void *ws, hipStream_t s) {
@@ -904,7 +1208,10 @@ int launch_attention(const float *q, const void *kc, const void *vc, float *out,
             if (ws_bytes < split_ws_bytes(T, span_rows, heads, M.kv_heads, hd, window) ||
                 (reinterpret_cast<uintptr_t>(ws) & 15))
                 return VQ_ERR_WORKSPACE;
-            if (elem == 2)
+            if (elem == 2 && fa16_ok(q, kc, vc, hd))
+                launch_attention_split16(q, static_cast<const _Float16 *>(kc), static_cast<const _Float16 *>(vc), out,
+                                         T, M, heads, hd, bidirectional, window, span_rows, ws, s);
+            else if (elem == 2)
                 launch_attention_split(q, static_cast<const _Float16 *>(kc), static_cast<const _Float16 *>(vc), out, T,
                                        M, heads, hd, bidirectional, window, span_rows, ws, s);
             else
