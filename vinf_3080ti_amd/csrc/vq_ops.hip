@@ -618,83 +618,89 @@ __device__ __forceinline__ void split_h(float x, _Float16 &hi, _Float16 &lo) {
 __device__ __forceinline__ int fa16_pos(int k) { return k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3); }
 __device__ __forceinline__ int fa16_vt(int d, int pos) { return d * 32 + (((pos >> 3) ^ ((d >> 2) & 3)) << 3) + (pos & 7); }
 
-// The query vector of lane column c as B operands (dims 32 u + 8 g + j), times 1/sqrt(hd) * 2^s; returns 2^-s.
+// The query vector of lane column c (dims 32 u + 8 g .. + 7), loaded raw; fa16_q_split turns it into the B
+// operands, times 1/sqrt(hd) * 2^s, and returns 2^-s. Split in two so that a block's K/V loads can be issued
+// between them.
 template <int HD>
-__device__ __forceinline__ float fa16_load_q(const float *qrow, float scale, fh8 (&qh)[HD / 32], fh8 (&ql)[HD / 32]) {
+__device__ __forceinline__ void fa16_q_load(const float *qrow, float4 (&qr)[HD / 16]) {
     const int g = (threadIdx.x & 63) >> 4;
-    float qv[HD / 32][8];
-    float amax = 0.0f;
 #pragma unroll
     for (int u = 0; u < HD / 32; ++u) {
-        const float4 a = *reinterpret_cast<const float4 *>(qrow + 32 * u + 8 * g);
-        const float4 b = *reinterpret_cast<const float4 *>(qrow + 32 * u + 8 * g + 4);
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            qv[u][j] = v[j] * scale;
-            amax = fmaxf(amax, fabsf(qv[u][j]));
-        }
+        qr[2 * u] = *reinterpret_cast<const float4 *>(qrow + 32 * u + 8 * g);
+        qr[2 * u + 1] = *reinterpret_cast<const float4 *>(qrow + 32 * u + 8 * g + 4);
     }
+}
+template <int HD>
+__device__ __forceinline__ float fa16_q_split(const float4 (&qr)[HD / 16], float scale, fh8 (&qh)[HD / 32],
+                                              fh8 (&ql)[HD / 32]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < HD / 16; ++i)
+        amax = fmaxf(fmaxf(amax, fmaxf(fabsf(qr[i].x), fabsf(qr[i].y))), fmaxf(fabsf(qr[i].z), fabsf(qr[i].w)));
+    amax *= scale;
     amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
     amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
     int ex = 0;
     if (amax > 0.0f && amax <= 3.0e38f) frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
     const float up = ldexpf(1.0f, 14 - ex);
 #pragma unroll
-    for (int u = 0; u < HD / 32; ++u)
+    for (int u = 0; u < HD / 32; ++u) {
+        const float v[8] = {qr[2 * u].x, qr[2 * u].y, qr[2 * u].z, qr[2 * u].w,
+                            qr[2 * u + 1].x, qr[2 * u + 1].y, qr[2 * u + 1].z, qr[2 * u + 1].w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             _Float16 h, l;
-            split_h(qv[u][j] * up, h, l);
+            split_h(v[j] * scale * up, h, l);
             qh[u][j] = h;
             ql[u][j] = l;
         }
+    }
     return ldexpf(1.0f, ex - 14);
 }
 
-// One 32-key block [kb, kb + 32) of kv head kvh against the wave's 16 query vectors (lane column c sees keys
-// [qs, qe)); keys at or past k_hi are masked. vt is the wave's V^T area (HD x 32 f16).
+// The raw K and V of one 32-key block in registers: K as S^T A operands, V as units of four keys x one
+// 16-byte chunk (unit lane + 64 it: chunk unit % (HD / 8), key quad unit / (HD / 8)).
 template <int HD>
-__device__ __forceinline__ void fa16_block(const _Float16 *__restrict__ kc, const _Float16 *__restrict__ vc,
-                                           const KvMap &M, int slot, int kvh, int kb, int k_hi, int qs, int qe,
-                                           const fh8 (&qh)[HD / 32], const fh8 (&ql)[HD / 32], float sinv,
-                                           _Float16 *vt, float &m, float &l, fa4 (&o)[HD / 16]) {
-    constexpr int CR = HD / 8;       // 16-byte chunks per row
-    constexpr int UPL = CR / 8;      // V units (4 keys x one chunk) per lane
+struct Fa16Raw {
+    fh8 ka[2][HD / 32];
+    fh8 vv[HD / 64][4];
+};
+
+// Issue the loads of block [kb, kb + 32) of kv head kvh (keys at or past k_hi read the last key's row).
+template <int HD>
+__device__ __forceinline__ void fa16_issue(const _Float16 *__restrict__ kc, const _Float16 *__restrict__ vc,
+                                           const KvMap &M, int slot, int kvh, int kb, int k_hi, Fa16Raw<HD> &rw) {
+    constexpr int CR = HD / 8;  // 16-byte chunks per row
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-    // Cache rows of the block's keys: lane k < 32 looks up key kb + k (clamped), the others read it by shuffle.
+    // Cache rows of the block's keys: lane k < 32 looks up key kb + k, the others read it by shuffle.
     const size_t myrow = M.row(slot, kvh, min(kb + (lane & 31), k_hi - 1));
     auto row_of = [&](int k) {
         const uint32_t lo32 = __shfl(static_cast<uint32_t>(myrow), k, 64);
         const uint32_t hi32 = __shfl(static_cast<uint32_t>(myrow >> 32), k, 64);
         return (static_cast<size_t>(hi32) << 32) | lo32;
     };
-    fh8 ka[2][HD / 32];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const size_t kr = row_of(16 * h + c) * HD + 8 * g;
 #pragma unroll
-        for (int u = 0; u < HD / 32; ++u) ka[h][u] = ld_h8(kc + kr + 32 * u);
+        for (int u = 0; u < HD / 32; ++u) rw.ka[h][u] = ld_h8(kc + kr + 32 * u);
     }
-    // V: unit (key quad qd, chunk dc) -> four 16-byte loads, then eight 8-byte LDS writes of V^T.
-    fh8 vv[UPL][4];
 #pragma unroll
-    for (int it = 0; it < UPL; ++it) {
+    for (int it = 0; it < HD / 64; ++it) {
         const int unit = lane + 64 * it, dc = unit % CR, qd = unit / CR;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vv[it][i] = ld_h8(vc + row_of(4 * qd + i) * HD + 8 * dc);
+        for (int i = 0; i < 4; ++i) rw.vv[it][i] = ld_h8(vc + row_of(4 * qd + i) * HD + 8 * dc);
     }
-#pragma unroll
-    for (int it = 0; it < UPL; ++it) {
-        const int unit = lane + 64 * it, dc = unit % CR, qd = unit / CR;
-        const int pos = fa16_pos(4 * qd);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int d = 8 * dc + j;
-            const fh4 w{vv[it][0][j], vv[it][1][j], vv[it][2][j], vv[it][3][j]};
-            *reinterpret_cast<fh4 *>(vt + fa16_vt(d, pos)) = w;
-        }
-    }
+}
+
+// Block kb (loaded in rw) against the wave's 16 query vectors (lane column c sees keys [qs, qe)); keys at or past
+// k_hi are masked. vt is the wave's V^T area (HD x 32 f16).
+template <int HD>
+__device__ __forceinline__ void fa16_consume(const Fa16Raw<HD> &rw, int kb, int k_hi, int qs, int qe,
+                                             const fh8 (&qh)[HD / 32], const fh8 (&ql)[HD / 32], float sinv,
+                                             _Float16 *vt, float &m, float &l, fa4 (&o)[HD / 16]) {
+    constexpr int CR = HD / 8;
+    const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
     // S^T for both key halves: hi and lo query parts in separate chains.
     fa4 s[2];
 #pragma unroll
@@ -702,10 +708,21 @@ __device__ __forceinline__ void fa16_block(const _Float16 *__restrict__ kc, cons
         fa4 a0{0.f, 0.f, 0.f, 0.f}, a1{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < HD / 32; ++u) {
-            a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][u], qh[u], a0, 0, 0, 0);
-            a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][u], ql[u], a1, 0, 0, 0);
+            a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(rw.ka[h][u], qh[u], a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(rw.ka[h][u], ql[u], a1, 0, 0, 0);
         }
         s[h] = (a0 + a1) * sinv;
+    }
+    // V^T into LDS: eight 8-byte writes per unit (four keys of one dim at consecutive positions).
+#pragma unroll
+    for (int it = 0; it < HD / 64; ++it) {
+        const int unit = lane + 64 * it, dc = unit % CR, qd = unit / CR;
+        const int pos = fa16_pos(4 * qd);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const fh4 w{rw.vv[it][0][j], rw.vv[it][1][j], rw.vv[it][2][j], rw.vv[it][3][j]};
+            *reinterpret_cast<fh4 *>(vt + fa16_vt(8 * dc + j, pos)) = w;
+        }
     }
     float v[8], bm = -INFINITY;
 #pragma unroll
@@ -785,11 +802,18 @@ __global__ __launch_bounds__(256) void attention_split16_kernel(const float *__r
 #pragma unroll
     for (int b = 0; b < HD / 16; ++b) o[b] = fa4{0.f, 0.f, 0.f, 0.f};
     if (blockIdx.y * 16 < s.rows * G) {  // groups past the segment's query vectors only wait at the barrier
+        // The query's loads, then the first block's, in flight together.
+        float4 qr[HD / 16];
+        fa16_q_load<HD>(q + (static_cast<size_t>(s.row0 + tq) * heads + h) * HD, qr);
+        Fa16Raw<HD> rw;
+        int kb = k_lo + 32 * wv;
+        if (kb < k_hi) fa16_issue<HD>(kc, vc, M, s.slot, kvh, kb, k_hi, rw);
         fh8 qh[HD / 32], ql[HD / 32];
-        const float sinv = fa16_load_q<HD>(q + (static_cast<size_t>(s.row0 + tq) * heads + h) * HD,
-                                           1.0f / sqrtf(static_cast<float>(HD)), qh, ql);
-        for (int kb = k_lo + 32 * wv; kb < k_hi; kb += 128)
-            fa16_block<HD>(kc, vc, M, s.slot, kvh, kb, k_hi, qs, qe, qh, ql, sinv, vts[wv], m, l, o);
+        const float sinv = fa16_q_split<HD>(qr, 1.0f / sqrtf(static_cast<float>(HD)), qh, ql);
+        for (; kb < k_hi; kb += 128) {
+            fa16_consume<HD>(rw, kb, k_hi, qs, qe, qh, ql, sinv, vts[wv], m, l, o);
+            if (kb + 128 < k_hi) fa16_issue<HD>(kc, vc, M, s.slot, kvh, kb + 128, k_hi, rw);
+        }
     }
     // Combine the four waves in wave order: o[b][r] is dim 16 b + 4 g + r of query vector c.
     __syncthreads();
@@ -841,7 +865,7 @@ template <int HD>
 __global__ __launch_bounds__(256) void attention_merge_kernel(const float *__restrict__ part, const float *__restrict__ pml,
                                                               float *__restrict__ out, SegTable T, int heads, int hd,
                                                               int nch) {
-    __shared__ float smx[256];
+    __shared__ float smx[4];
     __shared__ float4 sacc[4][HD / 4];
     __shared__ float sl[4];
     int t;
@@ -852,24 +876,35 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float *__res
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     float mx = -INFINITY;
     for (int c = tid; c < nch; c += 256) mx = fmaxf(mx, ml[2 * c]);
-    smx[tid] = mx;
-    for (int w = 128; w > 0; w >>= 1) {
-        __syncthreads();
-        if (tid < w) smx[tid] = fmaxf(smx[tid], smx[tid + w]);
-    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) smx[wv] = mx;
     __syncthreads();
-    const float M = smx[0];
+    const float M = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
     float4 acc{0.f, 0.f, 0.f, 0.f};
     float L = 0.0f;
     if (4 * lane < HD) {
-        for (int c = wv; c < nch; c += 4) {
-            const float f = ml[2 * c] == -INFINITY ? 0.0f : expf(ml[2 * c] - M);
-            L = fmaf(ml[2 * c + 1], f, L);
-            const float4 p4 = *reinterpret_cast<const float4 *>(part + (qv * nch + c) * HD + 4 * lane);
-            acc.x = fmaf(p4.x, f, acc.x);
-            acc.y = fmaf(p4.y, f, acc.y);
-            acc.z = fmaf(p4.z, f, acc.z);
-            acc.w = fmaf(p4.w, f, acc.w);
+        // Chunks wv, wv + 4, ... in order, four at a time with all their loads in flight.
+        for (int c0 = wv; c0 < nch; c0 += 16) {
+            float4 p4[4];
+            float mc[4], lc[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int c = c0 + 4 * k < nch ? c0 + 4 * k : c0;
+                p4[k] = *reinterpret_cast<const float4 *>(part + (qv * nch + c) * HD + 4 * lane);
+                mc[k] = ml[2 * c];
+                lc[k] = ml[2 * c + 1];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (c0 + 4 * k >= nch) break;
+                const float f = mc[k] == -INFINITY ? 0.0f : expf(mc[k] - M);
+                L = fmaf(lc[k], f, L);
+                acc.x = fmaf(p4[k].x, f, acc.x);
+                acc.y = fmaf(p4[k].y, f, acc.y);
+                acc.z = fmaf(p4[k].z, f, acc.z);
+                acc.w = fmaf(p4[k].w, f, acc.w);
+            }
         }
         sacc[wv][lane] = acc;
     }
