@@ -15,6 +15,7 @@
 #include <stdint.h>
 
 #include "../../include/vq.h"
+#include "vq_lds.h"
 
 namespace {
 
@@ -1110,6 +1111,168 @@ __global__ __launch_bounds__(256) void gated_delta_kernel(const float *__restric
     }
 }
 
+// The same rule with four adjacent state columns per lane (vd % 4 == 0, aligned state): lane = (row group
+// g = lane & 7, column quad cq = lane >> 3), a wave owns 32 columns and each row segment it reads or writes is
+// 128 bytes (fp32) or 64 bytes (fp16) long instead of 32 or 16. One wave per workgroup, so the 48 x 4 waves of
+// the qwen35 shape spread over the CUs. Sums over rows: the lane's R-term chains (one per column) plus three
+// DPP steps over the eight row groups, which sit in adjacent lanes (no LDS-path shuffles on the per-token
+// recurrence). Every lane of a group ends with the same bits: each step adds the same two values.
+__device__ __forceinline__ float dpp_add(float v, int ctrl_sel) {
+    int p;
+    switch (ctrl_sel) {
+        case 0: p = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false); break;   // quad_perm 1,0,3,2
+        case 1: p = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false); break;   // quad_perm 2,3,0,1
+        default: p = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false); break; // row_half_mirror
+    }
+    return v + __int_as_float(p);
+}
+__device__ __forceinline__ float gsum8(float v) { return dpp_add(dpp_add(dpp_add(v, 0), 1), 2); }
+__device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+__device__ __forceinline__ void st4(_Float16 *p, float4 v) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<h4 *>(p) = h4{static_cast<_Float16>(v.x), static_cast<_Float16>(v.y), static_cast<_Float16>(v.z),
+                                    static_cast<_Float16>(v.w)};
+}
+
+// The pass walks its tokens in chunks of up to kGdChunk: a chunk's inputs (per token the q and k rows of the head's
+// key head and the wave's 32 v columns, a record of 2 kd + 32 floats) reach LDS by DMA, all in flight at once,
+// and the recurrence then reads them from LDS, so a pass costs one memory round trip per chunk, not per token.
+constexpr int kGdChunk = 16;
+size_t gd_lds_bytes(int kd, int tc) { return (static_cast<size_t>(tc) * (2 * kd + 32) + 256) * sizeof(float); }
+
+template <int R, typename ST, bool FULL>  // FULL: kd == 8 R, every row of every lane is a state row
+__global__ __launch_bounds__(64) void gated_delta4_kernel(const float *__restrict__ conv, const float *__restrict__ braw,
+                                                          const float *__restrict__ araw, const float *__restrict__ ssm_a,
+                                                          const float *__restrict__ dt, ST *__restrict__ state,
+                                                          float *__restrict__ out, int key_heads, int value_heads,
+                                                          int kd, int vd, float eps, int head_order, SegTable T,
+                                                          float *__restrict__ snap, int write_state, int tc) {
+    extern __shared__ __align__(16) float gd_in[];  // [tc][2 kd + 32] + 1 KB of slack for the last DMA's spare lanes
+    const int lane = threadIdx.x;
+    const int tiles = (vd + 31) / 32;
+    const int h = blockIdx.x / tiles, c0 = (blockIdx.x - h * tiles) * 32;
+    const int col = c0 + 4 * (lane >> 3), r0 = (lane & 7) * R;
+    const bool col_ok = col < vd;  // vd % 4 == 0: a quad is whole or absent
+    const int cc = col_ok ? col : 0;
+    const int kh = head_order == 0 ? h / (value_heads / key_heads) : h % key_heads;
+    const Seg &s = T.s[blockIdx.y];
+    const size_t hstate = static_cast<size_t>(kd) * vd;
+    ST *S = state + (static_cast<size_t>(s.slot) * value_heads + h) * hstate;
+    const size_t cdim = static_cast<size_t>(2) * key_heads * kd + static_cast<size_t>(value_heads) * vd;
+    const float *cbase = conv + static_cast<size_t>(s.row0) * cdim;
+    const int rec = 2 * kd + 32, rec4 = rec / 4;
+    float4 st[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const bool ok = col_ok && r0 + i < kd;
+        const float4 v = ld4(S, static_cast<size_t>(ok ? r0 + i : 0) * vd + cc);
+        const float m = ok ? 1.0f : 0.0f;
+        st[i] = float4{v.x * m, v.y * m, v.z * m, v.w * m};
+    }
+    const float a_h = ssm_a[h], dt_h = dt[h];
+    const float rkd = 1.0f / sqrtf(static_cast<float>(kd));
+    for (int t0 = 0; t0 < s.rows; t0 += tc) {
+        const int nt = min(tc, s.rows - t0);
+        __syncthreads();  // the previous chunk's records are consumed
+        const int units = nt * rec4;
+        for (int u0 = 0; u0 < units; u0 += 64) {
+            const int u = min(u0 + lane, units - 1);
+            const int tt = u / rec4, w = 4 * (u - tt * rec4);
+            const size_t row = static_cast<size_t>(t0 + tt) * cdim;
+            size_t off;
+            if (w < kd) off = row + static_cast<size_t>(kh) * kd + w;
+            else if (w < 2 * kd) off = row + static_cast<size_t>(key_heads + kh) * kd + (w - kd);
+            else off = row + static_cast<size_t>(2) * key_heads * kd + static_cast<size_t>(h) * vd +
+                       (c0 + w - 2 * kd < vd ? c0 + w - 2 * kd : 0);
+            vq::dma16(cbase, static_cast<uint32_t>(off * sizeof(float)), gd_in + 4 * u0);
+        }
+        const float bt = lane < nt ? braw[static_cast<size_t>(s.row0 + t0 + lane) * value_heads + h] : 0.0f;
+        const float at = lane < nt ? araw[static_cast<size_t>(s.row0 + t0 + lane) * value_heads + h] : 0.0f;
+        vq::wait_vm<0>();
+        __syncthreads();
+        // Everything of a token that does not depend on the state, for all the chunk's tokens at once: lane l
+        // holds beta and the decay of token l, and (four lanes per token) the q and k norm scales of token l / 4.
+        // The per-token recurrence below then only reads them (v_readlane).
+        const float beta_l = sigmoid_ieee(bt);
+        const float xa_l = at + dt_h;
+        const float decay_l = expf(a_h * (xa_l > 20.0f ? xa_l : log1pf(expf(xa_l))));
+        float qsc_l, ksc_l;
+        {
+            const float4 *rp = reinterpret_cast<const float4 *>(gd_in + min(lane >> 2, nt - 1) * rec);
+            float pq = 0.0f, pk = 0.0f;
+            for (int f4 = lane & 3; f4 < kd / 4; f4 += 4) {
+                const float4 a = rp[f4], b = rp[kd / 4 + f4];
+                pq = fmaf(a.x, a.x, fmaf(a.y, a.y, fmaf(a.z, a.z, fmaf(a.w, a.w, pq))));
+                pk = fmaf(b.x, b.x, fmaf(b.y, b.y, fmaf(b.z, b.z, fmaf(b.w, b.w, pk))));
+            }
+            pq = dpp_add(dpp_add(pq, 0), 1);  // the four lanes of a token
+            pk = dpp_add(dpp_add(pk, 0), 1);
+            qsc_l = rkd / sqrtf(pq + eps);
+            ksc_l = 1.0f / sqrtf(pk + eps);
+        }
+        auto lane_val = [](float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); };
+        for (int tt = 0; tt < nt; ++tt) {
+            const size_t rr = static_cast<size_t>(s.row0) + t0 + tt;
+            const float *rq = gd_in + tt * rec;
+            float qv[R], kv[R];
+#pragma unroll
+            for (int i4 = 0; i4 < R / 4; ++i4) {
+                const int r = r0 + 4 * i4;
+                const bool ok = FULL || r < kd;  // kd % 4 == 0: a row quad is whole or absent
+                const float4 a = *reinterpret_cast<const float4 *>(rq + (ok ? r : 0));
+                const float4 b = *reinterpret_cast<const float4 *>(rq + kd + (ok ? r : 0));
+                if (FULL) {
+                    qv[4 * i4] = a.x, qv[4 * i4 + 1] = a.y, qv[4 * i4 + 2] = a.z, qv[4 * i4 + 3] = a.w;
+                    kv[4 * i4] = b.x, kv[4 * i4 + 1] = b.y, kv[4 * i4 + 2] = b.z, kv[4 * i4 + 3] = b.w;
+                } else {
+                    const float m = ok ? 1.0f : 0.0f;
+                    qv[4 * i4] = a.x * m, qv[4 * i4 + 1] = a.y * m, qv[4 * i4 + 2] = a.z * m, qv[4 * i4 + 3] = a.w * m;
+                    kv[4 * i4] = b.x * m, kv[4 * i4 + 1] = b.y * m, kv[4 * i4 + 2] = b.z * m, kv[4 * i4 + 3] = b.w * m;
+                }
+            }
+            const float4 v = *reinterpret_cast<const float4 *>(rq + 2 * kd + 4 * (lane >> 3));
+            const float beta = lane_val(beta_l, tt), decay = lane_val(decay_l, tt);
+            const float qscale = lane_val(qsc_l, 4 * tt), kscale = lane_val(ksc_l, 4 * tt);
+            float4 mem{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                st[i] = float4{st[i].x * decay, st[i].y * decay, st[i].z * decay, st[i].w * decay};
+                mem.x = fmaf(st[i].x, kv[i], mem.x);
+                mem.y = fmaf(st[i].y, kv[i], mem.y);
+                mem.z = fmaf(st[i].z, kv[i], mem.z);
+                mem.w = fmaf(st[i].w, kv[i], mem.w);
+            }
+            const float4 upd{(v.x - gsum8(mem.x) * kscale) * beta * kscale,
+                             (v.y - gsum8(mem.y) * kscale) * beta * kscale,
+                             (v.z - gsum8(mem.z) * kscale) * beta * kscale,
+                             (v.w - gsum8(mem.w) * kscale) * beta * kscale};
+            float4 o{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                st[i] = float4{fmaf(kv[i], upd.x, st[i].x), fmaf(kv[i], upd.y, st[i].y), fmaf(kv[i], upd.z, st[i].z),
+                               fmaf(kv[i], upd.w, st[i].w)};
+                o.x = fmaf(st[i].x, qv[i], o.x);
+                o.y = fmaf(st[i].y, qv[i], o.y);
+                o.z = fmaf(st[i].z, qv[i], o.z);
+                o.w = fmaf(st[i].w, qv[i], o.w);
+            }
+            o = float4{gsum8(o.x) * qscale, gsum8(o.y) * qscale, gsum8(o.z) * qscale, gsum8(o.w) * qscale};
+            if ((lane & 7) == 0 && col_ok) *reinterpret_cast<float4 *>(out + (rr * value_heads + h) * vd + col) = o;
+            if (snap != nullptr && t0 + tt + 1 < s.rows && col_ok) {
+                float *sn = snap + (static_cast<size_t>(t0 + tt) * value_heads + h) * hstate;
+#pragma unroll
+                for (int i = 0; i < R; ++i)
+                    if (r0 + i < kd) st4(sn + static_cast<size_t>(r0 + i) * vd + col, st[i]);
+            }
+        }
+    }
+    if (write_state && col_ok) {
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+            if (r0 + i < kd) st4(S + static_cast<size_t>(r0 + i) * vd + col, st[i]);
+    }
+}
+
 // ---- host launchers --------------------------------------------------------------------------------------
 
 int launch_rope(float *x, const SegTable &T, int heads, int hd, int rot, double base, hipStream_t s) {
@@ -1309,6 +1472,26 @@ void gd_dispatch(int R, dim3 grid, hipStream_t s, const float *conv, const float
 #undef VQ_GD_CASE
 }
 
+template <typename ST>
+void gd4_dispatch(int R, dim3 grid, hipStream_t s, const float *conv, const float *b, const float *a, const float *ssm_a,
+                  const float *dt, ST *state, float *out, int kh, int vh, int kd, int vd, float eps, int head_order,
+                  const SegTable &T, float *snap, int write_state) {
+    int rows = 1;
+    for (int i = 0; i < T.n; ++i) rows = T.s[i].rows > rows ? T.s[i].rows : rows;
+    const int tc = rows < kGdChunk ? rows : kGdChunk;
+#define VQ_GD_CASE(RR)                                                                                              \
+    case RR:                                                                                                        \
+        if (kd == 8 * RR)                                                                                           \
+            gated_delta4_kernel<RR, ST, true><<<grid, 64, gd_lds_bytes(kd, tc), s>>>(                                \
+                conv, b, a, ssm_a, dt, state, out, kh, vh, kd, vd, eps, head_order, T, snap, write_state, tc);      \
+        else                                                                                                        \
+            gated_delta4_kernel<RR, ST, false><<<grid, 64, gd_lds_bytes(kd, tc), s>>>(                               \
+                conv, b, a, ssm_a, dt, state, out, kh, vh, kd, vd, eps, head_order, T, snap, write_state, tc);      \
+        break;
+    switch (R) { VQ_GD_CASE(4) VQ_GD_CASE(8) VQ_GD_CASE(16) VQ_GD_CASE(32) }
+#undef VQ_GD_CASE
+}
+
 int launch_gated_delta(const float *conv, const float *b, const float *a, const float *ssm_a, const float *dt,
                        void *state, int state_elem, float *out, int kh, int vh, int kd, int vd, float eps,
                        int head_order, const SegTable &T, float *snap, int write_state, hipStream_t s) {
@@ -1318,6 +1501,22 @@ int launch_gated_delta(const float *conv, const float *b, const float *a, const 
         return VQ_ERR_SHAPE;
     if (snap != nullptr && (T.n != 1 || state_elem != 4)) return VQ_ERR_ARG;
     const int R = kd <= 4 * kGdGroups ? 4 : kd <= 8 * kGdGroups ? 8 : kd <= 16 * kGdGroups ? 16 : 32;
+    const uintptr_t align = reinterpret_cast<uintptr_t>(state) | reinterpret_cast<uintptr_t>(conv) |
+                            reinterpret_cast<uintptr_t>(out) | (snap ? reinterpret_cast<uintptr_t>(snap) : 0);
+    int max_rows = 1;
+    for (int i = 0; i < T.n; ++i) max_rows = T.s[i].rows > max_rows ? T.s[i].rows : max_rows;
+    const double seg_bytes = static_cast<double>(max_rows) * (2.0 * kh * kd + static_cast<double>(vh) * vd) * 4.0;
+    // Column quads: every row offset stays 16-byte aligned; a segment's inputs within 32-bit DMA offsets.
+    if (vd % 4 == 0 && kd % 4 == 0 && (align & 15) == 0 && seg_bytes < 4.0e9) {
+        const dim3 grid(static_cast<unsigned>(vh * ((vd + 31) / 32)), T.n);
+        if (state_elem == 4)
+            gd4_dispatch<float>(R, grid, s, conv, b, a, ssm_a, dt, static_cast<float *>(state), out, kh, vh, kd, vd,
+                                eps, head_order, T, snap, write_state);
+        else
+            gd4_dispatch<_Float16>(R, grid, s, conv, b, a, ssm_a, dt, static_cast<_Float16 *>(state), out, kh, vh, kd,
+                                   vd, eps, head_order, T, snap, write_state);
+        return status_of(hipGetLastError());
+    }
     const long waves = static_cast<long>(vh) * ((vd + kGdCols - 1) / kGdCols);
     const dim3 grid(static_cast<unsigned>((waves + 3) / 4), T.n);
     if (state_elem == 4)
