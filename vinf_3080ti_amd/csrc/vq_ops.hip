@@ -13,6 +13,7 @@
 // passes are bound by bytes, not by VALU).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 #include "../../include/vq.h"
 #include "vq_lds.h"
@@ -52,6 +53,14 @@ struct KvMap {
     int page, pps, kv_heads;
     __device__ __forceinline__ size_t row(int slot, int kvh, int pos) const {
         if (pt == nullptr) return static_cast<size_t>(kvh) * max_seq + pos;
+        const int pg = pt[slot * pps + pos / page];
+        return (static_cast<size_t>(pg) * kv_heads + kvh) * page + pos % page;
+    }
+    // The same with the layout fixed at compile time: no branch around the page-table load, so the compiler can
+    // keep the loads that follow in flight (a load under a branch makes it wait for every outstanding load).
+    template <bool PAGED>
+    __device__ __forceinline__ size_t row_t(int slot, int kvh, int pos) const {
+        if constexpr (!PAGED) return static_cast<size_t>(kvh) * max_seq + pos;
         const int pg = pt[slot * pps + pos / page];
         return (static_cast<size_t>(pg) * kv_heads + kvh) * page + pos % page;
     }
@@ -620,7 +629,9 @@ __device__ __forceinline__ int fa16_pos(int k) { return k < 16 ? 8 * (k >> 2) + 
 __device__ __forceinline__ int fa16_vt(int d, int pos) { return d * 32 + (((pos >> 3) ^ ((d >> 2) & 3)) << 3) + (pos & 7); }
 
 // The query vector of lane column c (dims 32 u + 8 g .. + 7), loaded raw; fa16_q_split turns it into the B
-// operands, times 1/sqrt(hd) * 2^s, and returns 2^-s. Split in two so that a block's K/V loads can be issued
+// operands, times 1/sqrt(hd) * 2^s, and returns 2^-s log2(e): scores leave the S product in base-2 units, so
+// the softmax weights are exp2 (v_exp_f32) of their differences, and maxima are converted back (times ln 2) only
+// where they leave the kernel. Split in two so that a block's K/V loads can be issued
 // between them.
 template <int HD>
 __device__ __forceinline__ void fa16_q_load(const float *qrow, float4 (&qr)[HD / 16]) {
@@ -656,11 +667,12 @@ __device__ __forceinline__ float fa16_q_split(const float4 (&qr)[HD / 16], float
             ql[u][j] = l;
         }
     }
-    return ldexpf(1.0f, ex - 14);
+    return ldexpf(1.0f, ex - 14) * 1.44269504088896341f;  // S in base-2 units: the softmax uses exp2
 }
 
 // The raw K and V of one 32-key block in registers: K as S^T A operands, V as units of four keys x one
-// 16-byte chunk (unit lane + 64 it: chunk unit % (HD / 8), key quad unit / (HD / 8)).
+// 16-byte chunk (unit lane + 64 it: key quad unit & 7, chunk unit >> 3; the eight key quads of a chunk sit in
+// adjacent lanes, which spreads a V^T write instruction over 32 banks instead of 8).
 template <int HD>
 struct Fa16Raw {
     fh8 ka[2][HD / 32];
@@ -668,13 +680,13 @@ struct Fa16Raw {
 };
 
 // Issue the loads of block [kb, kb + 32) of kv head kvh (keys at or past k_hi read the last key's row).
-template <int HD>
+template <int HD, bool PAGED>
 __device__ __forceinline__ void fa16_issue(const _Float16 *__restrict__ kc, const _Float16 *__restrict__ vc,
                                            const KvMap &M, int slot, int kvh, int kb, int k_hi, Fa16Raw<HD> &rw) {
     constexpr int CR = HD / 8;  // 16-byte chunks per row
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
     // Cache rows of the block's keys: lane k < 32 looks up key kb + k, the others read it by shuffle.
-    const size_t myrow = M.row(slot, kvh, min(kb + (lane & 31), k_hi - 1));
+    const size_t myrow = M.row_t<PAGED>(slot, kvh, min(kb + (lane & 31), k_hi - 1));
     auto row_of = [&](int k) {
         const uint32_t lo32 = __shfl(static_cast<uint32_t>(myrow), k, 64);
         const uint32_t hi32 = __shfl(static_cast<uint32_t>(myrow >> 32), k, 64);
@@ -688,43 +700,19 @@ __device__ __forceinline__ void fa16_issue(const _Float16 *__restrict__ kc, cons
     }
 #pragma unroll
     for (int it = 0; it < HD / 64; ++it) {
-        const int unit = lane + 64 * it, dc = unit % CR, qd = unit / CR;
+        const int unit = lane + 64 * it, dc = unit >> 3, qd = unit & 7;
 #pragma unroll
         for (int i = 0; i < 4; ++i) rw.vv[it][i] = ld_h8(vc + row_of(4 * qd + i) * HD + 8 * dc);
     }
 }
 
-// Block kb (loaded in rw) against the wave's 16 query vectors (lane column c sees keys [qs, qe)); keys at or past
-// k_hi are masked. vt is the wave's V^T area (HD x 32 f16).
+// Online softmax over the S^T values of block [kb, kb + 32) (s[h][r]: key kb + 16 h + 4 g + r, query column c sees
+// keys [qs, qe), keys at or past k_hi masked), then O^T += V^T P^T from the block's V^T in LDS (vt, read at rows
+// 16 b + c, positions 8 g ..). The caller makes vt visible first.
 template <int HD>
-__device__ __forceinline__ void fa16_consume(const Fa16Raw<HD> &rw, int kb, int k_hi, int qs, int qe,
-                                             const fh8 (&qh)[HD / 32], const fh8 (&ql)[HD / 32], float sinv,
-                                             _Float16 *vt, float &m, float &l, fa4 (&o)[HD / 16]) {
-    constexpr int CR = HD / 8;
+__device__ __forceinline__ void fa16_softmax_pv(const fa4 (&s)[2], int kb, int k_hi, int qs, int qe, const _Float16 *vt,
+                                                float &m, float &l, fa4 (&o)[HD / 16]) {
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-    // S^T for both key halves: hi and lo query parts in separate chains.
-    fa4 s[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        fa4 a0{0.f, 0.f, 0.f, 0.f}, a1{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < HD / 32; ++u) {
-            a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(rw.ka[h][u], qh[u], a0, 0, 0, 0);
-            a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(rw.ka[h][u], ql[u], a1, 0, 0, 0);
-        }
-        s[h] = (a0 + a1) * sinv;
-    }
-    // V^T into LDS: eight 8-byte writes per unit (four keys of one dim at consecutive positions).
-#pragma unroll
-    for (int it = 0; it < HD / 64; ++it) {
-        const int unit = lane + 64 * it, dc = unit % CR, qd = unit / CR;
-        const int pos = fa16_pos(4 * qd);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const fh4 w{rw.vv[it][0][j], rw.vv[it][1][j], rw.vv[it][2][j], rw.vv[it][3][j]};
-            *reinterpret_cast<fh4 *>(vt + fa16_vt(8 * dc + j, pos)) = w;
-        }
-    }
     float v[8], bm = -INFINITY;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -737,12 +725,12 @@ __device__ __forceinline__ void fa16_consume(const Fa16Raw<HD> &rw, int kb, int 
     bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
     const float mn = fmaxf(m, bm);
-    const float alpha = mn == -INFINITY ? 1.0f : expf(m - mn);
+    const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
     fh8 ph, pl;
     float ps = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const float p = v[j] == -INFINITY ? 0.0f : expf(v[j] - mn);
+        const float p = v[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(v[j] - mn);
         ps += p;
         _Float16 hh, ll;
         split_h(p, hh, ll);
@@ -753,10 +741,6 @@ __device__ __forceinline__ void fa16_consume(const Fa16Raw<HD> &rw, int kb, int 
     ps += __shfl_xor(ps, 32, 64);
     l = l * alpha + ps;
     m = mn;
-    // A wave's LDS operations complete in issue order; the fence keeps the compiler from moving the V^T reads
-    // above the writes of other lanes.
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int b = 0; b < HD / 16; ++b) {
         const fh8 a = *reinterpret_cast<const fh8 *>(vt + fa16_vt(16 * b + c, 8 * g));
@@ -764,15 +748,170 @@ __device__ __forceinline__ void fa16_consume(const Fa16Raw<HD> &rw, int kb, int 
         ob = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph, ob, 0, 0, 0);
         o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, ob, 0, 0, 0);
     }
+}
+
+// V unit (key quad qd, 16-byte chunk dc) of a block into V^T: eight 8-byte writes (four keys of one dim at
+// consecutive positions).
+template <int HD>
+__device__ __forceinline__ void fa16_put_vt(_Float16 *vt, int qd, int dc, const fh8 (&v4)[4]) {
+    const int pos = fa16_pos(4 * qd);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const fh4 w{v4[0][j], v4[1][j], v4[2][j], v4[3][j]};
+        *reinterpret_cast<fh4 *>(vt + fa16_vt(8 * dc + j, pos)) = w;
+    }
+}
+
+// Block kb (loaded in rw) against the wave's 16 query vectors; vt is the wave's own V^T area (HD x 32 f16).
+template <int HD>
+__device__ __forceinline__ void fa16_consume(const Fa16Raw<HD> &rw, int kb, int k_hi, int qs, int qe,
+                                             const fh8 (&qh)[HD / 32], const fh8 (&ql)[HD / 32], float sinv,
+                                             _Float16 *vt, float &m, float &l, fa4 (&o)[HD / 16]) {
+    constexpr int CR = HD / 8;
+    const int lane = threadIdx.x & 63;
+    // S^T for both key halves: hi and lo query parts in separate chains.
+    fa4 s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        fa4 a0{0.f, 0.f, 0.f, 0.f}, a1{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < HD / 32; ++u) {
+            a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(rw.ka[h][u], qh[u], a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(rw.ka[h][u], ql[u], a1, 0, 0, 0);
+        }
+        s[h] = (a0 + a1) * sinv;
+    }
+#pragma unroll
+    for (int it = 0; it < HD / 64; ++it) {
+        const int unit = lane + 64 * it;
+        fa16_put_vt<HD>(vt, unit & 7, unit >> 3, rw.vv[it]);
+    }
+    // A wave's LDS operations complete in issue order; the fence keeps the compiler from moving the V^T reads
+    // above the writes of other lanes.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    fa16_softmax_pv<HD>(s, kb, k_hi, qs, qe, vt, m, l, o);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // every lane has read V^T before the next block's writes
     __builtin_amdgcn_wave_barrier();
+}
+
+// Prompt passes on fp16 caches: a workgroup takes 16 query rows of one segment and up to four query heads of one kv
+// head (one wave each). Its 256 threads stage each 32-key block once for all four: K row-major [32][HD + 8] f16
+// (the S^T A fragments are 16-byte reads, rows 528 bytes apart for HD 256: no two of a read's 16 rows share banks),
+// V^T as in the decode kernel; the next two blocks' loads are in flight while one is used.
+template <int HD, bool PAGED>
+__global__ __launch_bounds__(256) void attention_prompt16_kernel(const float *__restrict__ q,
+                                                                 const _Float16 *__restrict__ kc,
+                                                                 const _Float16 *__restrict__ vc, float *__restrict__ out,
+                                                                 SegTable T, KvMap M, int heads, int bidirectional,
+                                                                 int window, int chunks) {
+    constexpr int CR = HD / 8, LDK = HD + 8;
+    constexpr int KU = 32 * CR / 256;  // K chunks per thread per block
+    constexpr int VU = 8 * CR / 256;   // V units per thread per block (HD 64: half the threads take one)
+    __shared__ __align__(16) _Float16 ks[32 * LDK];
+    __shared__ __align__(16) _Float16 vts[HD * 32];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    int tb = blockIdx.x, si = 0;
+    while (si + 1 < T.n && tb >= (T.s[si].rows + 15) / 16) {
+        tb -= (T.s[si].rows + 15) / 16;
+        ++si;
+    }
+    const Seg &s = T.s[si];
+    const int G = heads / M.kv_heads;
+    const int kvh = blockIdx.y / chunks, gi = (blockIdx.y - kvh * chunks) * 4 + wv;
+    const bool wave_on = gi < G;
+    const int h = kvh * G + (wave_on ? gi : 0);
+    const int t0 = 16 * tb, nq = min(16, s.rows - t0);
+    const int seq_len0 = s.pos0 + 1;
+    auto q_end = [&](int t) { return bidirectional ? seq_len0 + s.rows - 1 : seq_len0 + t; };
+    auto q_start = [&](int t) { return window > 0 && seq_len0 + t > window ? seq_len0 + t - window : 0; };
+    const int tq = t0 + min(c, nq - 1);  // this lane's query row (rows past nq repeat the last; not written)
+    const int qs = q_start(tq), qe = q_end(tq);
+    const int k_lo = q_start(t0), k_hi = q_end(t0 + nq - 1);
+    float4 qr[HD / 16];
+    fa16_q_load<HD>(q + (static_cast<size_t>(s.row0 + tq) * heads + h) * HD, qr);
+    // Block loads of this thread: K chunks i = tid + 256 k (key i / CR, chunk i % CR); V unit tid (key quad tid & 7,
+    // chunk tid >> 3).
+    // Two blocks are in flight ahead of the one being used (register buffers A and B).
+    struct Buf {
+        fh8 k[KU];
+        fh8 v[VU > 0 ? VU : 1][4];
+    };
+    auto row_of = [&](int key) { return M.row_t<PAGED>(s.slot, kvh, min(key, k_hi - 1)); };
+    auto issue = [&](Buf &bf, int kb) {
+#pragma unroll
+        for (int k = 0; k < KU; ++k) {
+            const int i = threadIdx.x + 256 * k;
+            bf.k[k] = ld_h8(kc + row_of(kb + i / CR) * HD + 8 * (i % CR));
+        }
+#pragma unroll
+        for (int k = 0; k < (VU > 0 ? VU : 1); ++k) {
+            const int i = threadIdx.x + 256 * k;
+            if (i < 8 * CR)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bf.v[k][j] = ld_h8(vc + row_of(kb + 4 * (i & 7) + j) * HD + 8 * (i >> 3));
+        }
+    };
+    Buf ba, bb;
+    if (k_lo < k_hi) issue(ba, k_lo);
+    if (k_lo + 32 < k_hi) issue(bb, k_lo + 32);
+    fh8 qh[HD / 32], ql[HD / 32];
+    const float sinv = fa16_q_split<HD>(qr, 1.0f / sqrtf(static_cast<float>(HD)), qh, ql);
+    float m = -INFINITY, l = 0.0f;
+    fa4 o[HD / 16];
+#pragma unroll
+    for (int b = 0; b < HD / 16; ++b) o[b] = fa4{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](Buf &bf, int kb) {
+        __syncthreads();  // the previous block is consumed
+#pragma unroll
+        for (int k = 0; k < KU; ++k) {
+            const int i = threadIdx.x + 256 * k;
+            *reinterpret_cast<fh8 *>(ks + (i / CR) * LDK + 8 * (i % CR)) = bf.k[k];
+        }
+#pragma unroll
+        for (int k = 0; k < (VU > 0 ? VU : 1); ++k) {
+            const int i = threadIdx.x + 256 * k;
+            if (i < 8 * CR) fa16_put_vt<HD>(vts, i & 7, i >> 3, bf.v[k]);
+        }
+        __syncthreads();
+        if (kb + 64 < k_hi) issue(bf, kb + 64);
+        if (!wave_on) return;
+        fa4 sc[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            fa4 a0{0.f, 0.f, 0.f, 0.f}, a1{0.f, 0.f, 0.f, 0.f};
+            const _Float16 *kp = ks + (16 * hh + c) * LDK + 8 * g;
+#pragma unroll
+            for (int u = 0; u < HD / 32; ++u) {
+                const fh8 a = *reinterpret_cast<const fh8 *>(kp + 32 * u);
+                a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[u], a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[u], a1, 0, 0, 0);
+            }
+            sc[hh] = (a0 + a1) * sinv;
+        }
+        fa16_softmax_pv<HD>(sc, kb, k_hi, qs, qe, vts, m, l, o);
+    };
+    for (int kb = k_lo; kb < k_hi; kb += 64) {
+        consume(ba, kb);
+        if (kb + 32 < k_hi) consume(bb, kb + 32);
+    }
+    // o[b][r]: head dim 16 b + 4 g + r of query row tq
+    if (wave_on && c < nq) {
+        float *orow = out + (static_cast<size_t>(s.row0 + t0 + c) * heads + h) * HD;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int b = 0; b < HD / 16; ++b)
+            *reinterpret_cast<float4 *>(orow + 16 * b + 4 * g) =
+                float4{o[b][0] * inv, o[b][1] * inv, o[b][2] * inv, o[b][3] * inv};
+    }
 }
 
 // Decode and verify passes on fp16 caches: one workgroup per (segment, kv head, chunk of the keys, group of 16
 // query vectors); its four waves take the chunk's 32-key blocks in turn (wave w: blocks w, w + 4, ...) with their
 // own online softmax, then combine in wave order through LDS. With one chunk the workgroup writes the output;
 // otherwise its unnormalised output and (max, sum) go to the workspace for attention_merge_kernel.
-template <int HD>
+template <int HD, bool PAGED>
 __global__ __launch_bounds__(256) void attention_split16_kernel(const float *__restrict__ q,
                                                                 const _Float16 *__restrict__ kc,
                                                                 const _Float16 *__restrict__ vc, float *__restrict__ part,
@@ -808,12 +947,12 @@ __global__ __launch_bounds__(256) void attention_split16_kernel(const float *__r
         fa16_q_load<HD>(q + (static_cast<size_t>(s.row0 + tq) * heads + h) * HD, qr);
         Fa16Raw<HD> rw;
         int kb = k_lo + 32 * wv;
-        if (kb < k_hi) fa16_issue<HD>(kc, vc, M, s.slot, kvh, kb, k_hi, rw);
+        if (kb < k_hi) fa16_issue<HD, PAGED>(kc, vc, M, s.slot, kvh, kb, k_hi, rw);
         fh8 qh[HD / 32], ql[HD / 32];
         const float sinv = fa16_q_split<HD>(qr, 1.0f / sqrtf(static_cast<float>(HD)), qh, ql);
         for (; kb < k_hi; kb += 128) {
             fa16_consume<HD>(rw, kb, k_hi, qs, qe, qh, ql, sinv, vts[wv], m, l, o);
-            if (kb + 128 < k_hi) fa16_issue<HD>(kc, vc, M, s.slot, kvh, kb + 128, k_hi, rw);
+            if (kb + 128 < k_hi) fa16_issue<HD, PAGED>(kc, vc, M, s.slot, kvh, kb + 128, k_hi, rw);
         }
     }
     // Combine the four waves in wave order: o[b][r] is dim 16 b + 4 g + r of query vector c.
@@ -837,7 +976,7 @@ __global__ __launch_bounds__(256) void attention_split16_kernel(const float *__r
         float4 acc{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            const float f = sm[w][qc] == -INFINITY ? 0.0f : expf(sm[w][qc] - mx);
+            const float f = sm[w][qc] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sm[w][qc] - mx);
             L = fmaf(sl[w][qc], f, L);
             const float4 p4 = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(vts[w]) + qc * HD + d4);
             acc.x = fmaf(p4.x, f, acc.x);
@@ -852,7 +991,7 @@ __global__ __launch_bounds__(256) void attention_split16_kernel(const float *__r
         } else {
             *reinterpret_cast<float4 *>(part + (qv * nch + ci) * HD + d4) = acc;
             if (d4 == 0) {
-                pml[(qv * nch + ci) * 2] = mx;
+                pml[(qv * nch + ci) * 2] = mx * 0.693147180559945309f;  // natural units for the merge
                 pml[(qv * nch + ci) * 2 + 1] = L;
             }
         }
@@ -1318,6 +1457,24 @@ void launch_mfma_hd(bool fast, dim3 grid, hipStream_t s, const float *q, const C
                                                                 chunks);
 }
 
+template <bool PAGED>
+void launch_prompt16(dim3 grid, hipStream_t s, const float *q, const _Float16 *kc, const _Float16 *vc, float *out,
+                     const SegTable &T, const KvMap &M, int heads, int hd, int bidirectional, int window, int chunks) {
+    if (hd == 64)
+        attention_prompt16_kernel<64, PAGED><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, bidirectional, window, chunks);
+    else if (hd == 128)
+        attention_prompt16_kernel<128, PAGED><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, bidirectional, window, chunks);
+    else
+        attention_prompt16_kernel<256, PAGED><<<grid, 256, 0, s>>>(q, kc, vc, out, T, M, heads, bidirectional, window, chunks);
+}
+
+// fp16 caches with hd 64, 128 or 256 and 16-byte aligned q, K, V and out: the f16 MFMA kernels.
+bool fa16_ok(const float *q, const void *kc, const void *vc, const float *out, int hd) {
+    return (hd == 64 || hd == 128 || hd == 256) &&
+           ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc) |
+             reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+}
+
 template <typename C>
 void launch_attention_mfma(const float *q, const C *kc, const C *vc, float *out, const SegTable &T, const KvMap &M,
                            int heads, int hd, int bidirectional, int window, hipStream_t s) {
@@ -1325,6 +1482,13 @@ void launch_attention_mfma(const float *q, const C *kc, const C *vc, float *out,
     for (int i = 0; i < T.n; ++i) tiles += (T.s[i].rows + 15) / 16;
     const int chunks = (heads / M.kv_heads + 3) / 4;
     const dim3 grid(tiles, M.kv_heads * chunks);
+    if constexpr (sizeof(C) == 2) {
+        if (fa16_ok(q, kc, vc, out, hd)) {
+            if (M.pt != nullptr) launch_prompt16<true>(grid, s, q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
+            else launch_prompt16<false>(grid, s, q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
+            return;
+        }
+    }
     const bool fast = fa_fast(kc, vc, hd);
     if (hd <= 64) launch_mfma_hd<C, 64>(fast, grid, s, q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
     else if (hd <= 128) launch_mfma_hd<C, 128>(fast, grid, s, q, kc, vc, out, T, M, heads, hd, bidirectional, window, chunks);
@@ -1344,11 +1508,6 @@ void launch_split_hd(bool fast, dim3 grid, dim3 mgrid, hipStream_t s, const floa
     attention_merge_kernel<HD><<<mgrid, 256, 0, s>>>(part, pml, out, T, heads, hd, nch);
 }
 
-// fp16 caches with hd 64, 128 or 256 and 16-byte aligned q, K and V: the f16 MFMA decode kernel.
-bool fa16_ok(const float *q, const void *kc, const void *vc, int hd) {
-    return (hd == 64 || hd == 128 || hd == 256) &&
-           ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15) == 0;
-}
 
 void launch_attention_split16(const float *q, const _Float16 *kc, const _Float16 *vc, float *out, const SegTable &T,
                               const KvMap &M, int heads, int hd, int bidirectional, int window, int span_rows, void *ws,
@@ -1358,12 +1517,17 @@ void launch_attention_split16(const float *q, const _Float16 *kc, const _Float16
     float *pml = part + static_cast<size_t>(span_rows) * heads * nch * fa_hd(hd);
     const int G = heads / M.kv_heads;
     const dim3 grid(T.n * M.kv_heads * nch, (max_seg_rows(T) * G + 15) / 16);
-    if (hd == 64)
-        attention_split16_kernel<64><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, out, T, M, heads, bidirectional, window, nch);
-    else if (hd == 128)
-        attention_split16_kernel<128><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, out, T, M, heads, bidirectional, window, nch);
-    else
-        attention_split16_kernel<256><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, out, T, M, heads, bidirectional, window, nch);
+    auto go = [&](auto paged) {
+        constexpr bool P = decltype(paged)::value;
+        if (hd == 64)
+            attention_split16_kernel<64, P><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, out, T, M, heads, bidirectional, window, nch);
+        else if (hd == 128)
+            attention_split16_kernel<128, P><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, out, T, M, heads, bidirectional, window, nch);
+        else
+            attention_split16_kernel<256, P><<<grid, 256, 0, s>>>(q, kc, vc, part, pml, out, T, M, heads, bidirectional, window, nch);
+    };
+    if (M.pt != nullptr) go(std::true_type{});
+    else go(std::false_type{});
     if (nch > 1) {
         const dim3 mgrid(T.total * heads);
         if (hd == 64) attention_merge_kernel<64><<<mgrid, 256, 0, s>>>(part, pml, out, T, heads, hd, nch);
@@ -1406,7 +1570,7 @@ int launch_attention(const float *q, const void *kc, const void *vc, float *out,
             if (ws_bytes < split_ws_bytes(T, span_rows, heads, M.kv_heads, hd, window) ||
                 (reinterpret_cast<uintptr_t>(ws) & 15))
                 return VQ_ERR_WORKSPACE;
-            if (elem == 2 && fa16_ok(q, kc, vc, hd))
+            if (elem == 2 && fa16_ok(q, kc, vc, out, hd))
                 launch_attention_split16(q, static_cast<const _Float16 *>(kc), static_cast<const _Float16 *>(vc), out,
                                          T, M, heads, hd, bidirectional, window, span_rows, ws, s);
             else if (elem == 2)
