@@ -497,3 +497,26 @@ def test_decode_attention_fp16_cache_shapes(oracle_mod, heads, kvh, hd, ntok, se
     ref = oracle_mod.attention(q, kc, vc, heads, kvh, seq_len, False, 0)
     assert np.allclose(outs[0], ref, rtol=2e-5, atol=2e-5), float(np.abs(outs[0] - ref).max())
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("elem", [2, 4])
+def test_decode_attention_seg_paged_head_dim_256(rt, oracle_mod, elem):
+    """Decode and verify rows of three sequences over paged caches at the qwen35 head shape (24 heads over 4 kv
+    heads, hd 256): the split kernel (f16 MFMA for the fp16 pool) with the page table read per key block."""
+    rng = np.random.default_rng(77 + elem)
+    heads, kvh, hd = QW_HEADS, QW_KVH, QW_HD
+    pt, pool_k, pool_v = paging(rt, rng, kvh, hd, elem)
+    segs = [(0, 150, 1), (2, 120, 4), (1, 17, 3)]
+    n = rt.set_segments(segs)
+    q = rng.standard_normal((n, heads, hd)).astype(np.float32)
+    put(rt, "sq", q)
+    put(rt, "so", np.full(q.size, np.nan))
+    rt.attention_seg("sq", "pk", "pv", "so", heads, kvh, hd)
+    got = get(rt, "so", (n, heads, hd))
+    row = 0
+    for slot, pos0, m in segs:
+        kc = oracle_mod.gather_paged(pool_k, pt[slot], PAGE, kvh, pos0 + m)
+        vc = oracle_mod.gather_paged(pool_v, pt[slot], PAGE, kvh, pos0 + m)
+        ref = oracle_mod.attention(q[row:row + m], kc, vc, heads, kvh, pos0 + 1)
+        assert np.allclose(got[row:row + m], ref, rtol=2e-5, atol=2e-5), (slot, pos0, m)
+        row += m
