@@ -470,8 +470,8 @@ class Sweep:
             while j < len(self.plan) and self.plan[j][4] == key:
                 run = [k for k in range(j, min(j + 4, len(self.plan))) if self.plan[k][4] == key]
                 tys = {self.plan[k][1] for k in run}
-                if len(tys) > 1 and not packed and len(tys - {Q8_0}) == 1:
-                    # A main type and Q8_0 small tensors reading one input: one mixed launch.
+                if len(tys) > 1 and not packed and (len(tys - {Q8_0}) == 1 or tys == {Q5_K, Q6_K}):
+                    # A main type and Q8_0 small tensors, or Q5_K and Q6_K, reading one input: one mixed launch.
                     self.ops.append(("mixed", run))
                     j = run[-1] + 1
                     continue

@@ -294,7 +294,8 @@ int vq_qmv_group_f32(int type, int n, const uint8_t *const *w, const int *rows, 
 
 /* vq_qmv_group_f32 over matrices of up to two quantized types (types[k] per matrix): a main type and Q8_0,
  * the type GGUF mixes give a layer's small tensors (e.g. the gated-delta beta/alpha projections next to its
- * Q5_K qkv/gate). One launch per token chunk of at most 4; other type mixes run as one launch per type. No
+ * Q5_K qkv/gate), or Q5_K and Q6_K (a full-attention layer's q next to its k and v). One launch per token chunk
+ * of at most 4; other type mixes run as one launch per type. No
  * counterpart in the reference's per-matrix qmv (qwen_runtime.cu:1860); its effect equals n vq_qmv calls. */
 int vq_qmv_group_mixed_f32(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y,
                            int cols, const float *x, int ntok, void *stream);

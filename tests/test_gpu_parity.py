@@ -210,13 +210,14 @@ def test_zero_and_extreme_activations(env, oracle_mod):
 
 
 @pytest.mark.parametrize("mix", [[T.Q5_K, T.Q5_K, T.Q8_0, T.Q8_0], [T.Q8_0, T.Q6_K], [T.Q4_K, T.Q8_0, T.Q4_K],
-                                 [T.IQ4_XS, T.Q8_0], [T.Q5_K, T.Q6_K, T.Q8_0]],
+                                 [T.IQ4_XS, T.Q8_0], [T.Q5_K, T.Q6_K, T.Q8_0], [T.Q5_K, T.Q6_K, T.Q6_K],
+                                 [T.Q6_K, T.Q5_K]],
                          ids=lambda m: "+".join(t.name for t in m))
 @pytest.mark.parametrize("ntok", [1, 3, 6])
 def test_qmv_group_mixed_matches_oracle(env, oracle_mod, mix, ntok):
     """A grouped launch over a main type and Q8_0 (a gated-delta layer's qkv/gate + beta/alpha) == each matrix
-    on its own; more than 4 tokens run as several launches, and a mix of two non-Q8_0 types as one launch per
-    type."""
+    on its own; more than 4 tokens run as several launches; Q5_K with Q6_K (a full-attention layer's q, k, v) is
+    one launch, and other mixes of two non-Q8_0 types run as one launch per type."""
     torch, lib = env
     cols = 5120
     rng = np.random.default_rng(ntok + len(mix))

@@ -600,6 +600,10 @@ int vq_qmv_group_mixed_f32(int n, const int *types, const uint8_t *const *w, con
     if (!x || misaligned16(x)) return VQ_ERR_ARG;
     if (ntok < 1) return VQ_ERR_SHAPE;
     if (main_type < 0) main_type = VQ_Q8_0;
+    bool q5q6 = mixed;  // Q5_K with Q6_K, nothing else: one launch
+    for (int k = 0; k < n; ++k) q5q6 = q5q6 && (types[k] == VQ_Q5_K || types[k] == VQ_Q6_K);
+    if (q5q6)
+        return vq::launch_mixed2<VQ_Q5_K, VQ_Q6_K>(n, types, w, rows, y, cols, x, ntok, static_cast<hipStream_t>(stream));
     if (mixed) {
         // Other mixes: one grouped launch per type, in order of first appearance.
         bool done[VQ_MAX_GROUP] = {};

@@ -51,6 +51,11 @@ constexpr int kMixedMaxTokens = 4;  // tokens per launch of a mixed-type group (
 template <int T>
 int launch_mixed_q8(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y, int cols,
                     const float *x, int ntok, hipStream_t s);
+// Jobs of two K-quant types reading one fp32 input in one launch (a full-attention layer's Q5_K q next to its Q6_K
+// k and v); instantiated for (Q5_K, Q6_K).
+template <int T, int T2>
+int launch_mixed2(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                  const float *x, int ntok, hipStream_t s);
 // Prefill contraction on int8 MFMA: y[t][r] = W[r] . x[t] for t < M, activations packed (vq_pack_x).
 template <int T>
 int launch_gemm(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int M, float *y,

@@ -994,6 +994,12 @@ int launch_mixed_q8(int n, const int *types, const uint8_t *const *w, const int 
         return launch_jobs<T, VQ_Q8_0>(n, types, w, rows, y, cols, x, true, ntok, nullptr, nullptr, s);
 }
 
+template <int T, int T2>
+int launch_mixed2(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                  const float *x, int ntok, hipStream_t s) {
+    return launch_jobs<T, T2>(n, types, w, rows, y, cols, x, true, ntok, nullptr, nullptr, s);
+}
+
 template <int T>
 int launch_quant_staged(const uint8_t *w, int rows, int cols, long rb, const float *x, const XStage &xs, int ntok,
                         float *y, hipStream_t s) {

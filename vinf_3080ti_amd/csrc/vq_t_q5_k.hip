@@ -3,3 +3,5 @@
 #include "vq_mfma_impl.h"
 
 VQ_INSTANTIATE(VQ_Q5_K)
+template int vq::launch_mixed2<VQ_Q5_K, VQ_Q6_K>(int, const int *, const uint8_t *const *, const int *, float *const *,
+                                                 int, const float *, int, hipStream_t);
