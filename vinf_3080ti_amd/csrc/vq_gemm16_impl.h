@@ -132,8 +132,9 @@ struct G16Geo {
     static constexpr int HB = T == VQ_Q5_K ? 48 : 16;          // leading block bytes kept per super-block
     static constexpr int QOFF = T == VQ_Q5_K ? 48 : 16;        // offset of qs in the block
     static constexpr int SB_CHUNKS = kG16BM * HB / 16 + kG16BN * 2;  // 16-byte chunks of a super-block slot
-    static constexpr int SB_DMA = SB_CHUNKS / (64 * kG16Waves);      // per wave per step
-    static constexpr int NDMA = 1 + 4 + SB_DMA;                      // DMAs per wave per step
+    static constexpr int SB_DMA = SB_CHUNKS / (64 * kG16Waves);      // per wave, first step of a super-block
+    static constexpr int NDMA = 1 + 4;                               // per wave, every step
+    static constexpr int NDMA_SB = NDMA + SB_DMA;                    // per wave, first step of a super-block
     static constexpr int STEP_BYTES = kG16BM * 32 + 2 * kG16BN * 128;  // codes + b_hi + b_lo
     static constexpr int SB_BYTES = SB_CHUNKS * 16;
     static_assert(SB_CHUNKS % (64 * kG16Waves) == 0, "super-block slot split");
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     // DMA of step st (j = st % 4 of super-block sb0 + st / 4) into ring slot st % 3 and super-block slot sb & 1.
     // Per wave: codes (rows 32 wv .. +32, two lanes per row), 4 of the 32 KB of b_hi/b_lo (8 tokens per 1 KB,
     // chunk position p of token row r holds chunk p ^ ((r >> 1) & 7): the 16 rows an MFMA fragment reads then
-    // hit 16 distinct 16-byte bank groups), SB_DMA KB of the super-block slot.
+    // hit 16 distinct 16-byte bank groups), and on a super-block's first step SB_DMA KB of its slot.
     auto issue = [&](int st) {
         const int sb = sb0 + (st >> 2), j = st & 3;
         uint8_t *const slot = s_step[st % kG16Ring];
@@ -196,6 +197,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
             dma16(i < 16 ? static_cast<const void *>(bh) : static_cast<const void *>(bl), off,
                   slot + kG16BM * 32 + (i < 16 ? 0 : kG16BN * 128) + 1024 * ii);
         }
+        if (j != 0) return;  // the super-block slot: once, with the super-block's first step
         uint8_t *const sbs = s_sb[sb & 1];
 #pragma unroll
         for (int k = 0; k < G::SB_DMA; ++k) {
@@ -227,10 +229,13 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
                                                                       // row wr + 16 rb + lr, one per byte
     const g16h2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
     for (int st = 0; st < nsteps; ++st) {
-        if (st + 1 < nsteps)
-            wait_vm<G::NDMA>();
-        else
+        // Step st landed when at most the next step's DMAs are outstanding (loads retire in order).
+        if (st + 1 >= nsteps)
             wait_vm<0>();
+        else if (((st + 1) & 3) == 0)
+            wait_vm<G::NDMA_SB>();
+        else
+            wait_vm<G::NDMA>();
         __syncthreads();  // step st landed for every wave; step st - 1's slot is free
         if (st + 2 < nsteps) issue(st + 2);
         const int sb = sb0 + (st >> 2), j = st & 3;
