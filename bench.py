@@ -739,8 +739,8 @@ def main() -> None:
         print(json.dumps(cpu_child(args.cpu_child)), flush=True)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (weights shard by rows; see "
-              "DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the matvec would shard by weight "
+              "rows, one all-gather of y per layer). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     full = not (args.matvec or args.prefill_only or args.mlp_only or args.roofline_only or args.ops_only)
