@@ -225,6 +225,37 @@ def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=
             "copies": copies}
 
 
+def bench_matvec_routed(torch, hip, ty, rows, cols, ntok, iters=40, min_rotation_bytes=640 << 20):
+    """One vq_qmv call with the workspace vq_qmv_workspace_bytes_for asks, so the library routes the batch the way
+    a caller gets it (streaming, int8-MFMA or f16-MFMA small-batch kernel; `path`): µs, GB/s and fraction of
+    8 TB/s over the call's kernels, rotating over weight copies larger than the MALL in a hipGraph."""
+    from vinf_3080ti_amd import row_bytes
+
+    nbytes = rows * row_bytes(ty, cols)
+    copies = max(2, -(-min_rotation_bytes // nbytes))
+    ws = make_weights(torch, ty, rows, cols, 4321 + ty, copies)
+    x = torch.randn(ntok, cols, device="cuda")
+    y = torch.empty(ntok, rows, device="cuda")
+    nws = hip.lib.vq_qmv_workspace_bytes_for(ty, rows, cols, ntok)
+    wsb = torch.empty(max(nws, 256), dtype=torch.uint8, device="cuda")
+    path = hip.lib.vq_qmv_path(ty, rows, cols, ntok, nws)
+
+    def launch(i):
+        st = hip.lib.vq_qmv(ty, ws[i % copies].data_ptr(), rows, cols, x.data_ptr(), ntok, y.data_ptr(),
+                            wsb.data_ptr() if nws else None, nws, hip.s())
+        assert st == 0, st
+
+    for i in range(copies):
+        launch(i)
+    ms = time_kernel_loop(torch, launch, iters)
+    b = alg_bytes(ty, rows, cols, ntok)
+    del ws
+    torch.cuda.empty_cache()
+    return {"us": round(ms * 1e3, 3), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
+            "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "path": {0: "stream", 1: "mfma-int8", 2: "mfma-f16"}.get(path, str(path))}
+
+
 def ab_matvec(torch, hips, ty, rows, cols, ntok, group=1, reps=5, iters=100, min_rotation_bytes=640 << 20):
     """The bench_matvec launch for several builds of the library (one Hip per build) on the same weights,
     interleaved rep by rep, so that box-to-box and run-to-run drift hits every build alike: per build the
@@ -831,6 +862,9 @@ def main() -> None:
             per_type[TYPE_NAMES[ty]] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
         r = bench_matvec(torch, hip, Q4_K, 4096, 4096, args.ntok)
         per_type["Q4_K@4096x4096"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+        for ty in (IQ4_XS, IQ3_S, IQ2_XXS):  # config 3 at batch 8, routed as vq_qmv routes it
+            log(f"per-type batch 8: {TYPE_NAMES[ty]} 5120x17408")
+            per_type[f"{TYPE_NAMES[ty]}@batch8"] = bench_matvec_routed(torch, hip, ty, 5120, 17408, 8)
 
     prefill, mlp, ops = {}, {}, {}
     if not args.no_per_type:
