@@ -59,11 +59,13 @@ GD_TOL = dict(rtol=1e-4, atol=2e-5)
 
 @pytest.mark.parametrize("kh,vh,kd,vd,ntok", [(QW_KH, QW_VH, QW_KD, QW_VD, 1), (QW_KH, QW_VH, QW_KD, QW_VD, 8),
                                               (2, 6, 256, 64, 3), (1, 3, 40, 100, 2), (4, 4, 32, 8, 5),
-                                              (2, 4, 24, 10, 3), (1, 2, 66, 36, 2)])
+                                              (2, 4, 24, 10, 3), (1, 2, 66, 36, 2), (2, 4, 64, 32, 37),
+                                              (QW_KH, QW_VH, QW_KD, QW_VD, 20)])
 def test_gated_delta_shapes(rt, oracle_mod, kh, vh, kd, vd, ntok):
     """The register-resident gated delta at the qwen35 shape (decode and an 8-row verify pass), kd 256, and
     ragged kd / vd (rows and columns past the state's edge masked): outputs, state and snapshots. vd and kd
-    multiples of 4 take the column-quad kernel; vd 10 and kd 66 the one-column kernel."""
+    multiples of 4 take the column-quad kernel (20 and 37 rows: its 16-token input chunks, the last one partial);
+    vd 10 and kd 66 the one-column kernel."""
     rng = np.random.default_rng(kd * vd + ntok)
     inp = gd_inputs(rng, ntok, kh, vh, kd, vd)
     s0 = (rng.standard_normal((vh, kd, vd)) * 0.1).astype(np.float32)
