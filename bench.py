@@ -418,7 +418,8 @@ def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=Non
     Q6_K 5120x17408) at batch ntok, weights rotating beyond the MALL. mfma=True: vq_qmv with its workspace for
     all three (the f16-MFMA small-batch matvec for these types from 5 tokens on, and from 3 over the 17408-wide
     down input); mfma=False: the streaming kernel (grouped gate/up + down, activations quantized in-kernel).
-    Default: per matrix, vq_qmv where vq_qmv_path picks an MFMA path, else the grouped streaming launch."""
+    Default: vq_qmv (down) and vq_qmv_group_ws (gate and up together) where vq_qmv_path picks an MFMA path, else
+    the grouped streaming launch."""
     from vinf_3080ti_amd import row_bytes
 
     H, F = 5120, 17408
@@ -431,7 +432,11 @@ def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=Non
     g, u, d = (torch.empty(ntok, F, device="cuda"), torch.empty(ntok, F, device="cuda"),
                torch.empty(ntok, H, device="cuda"))
     lib = hip.lib
-    nws = max(lib.vq_qmv_workspace_bytes_for(Q3_K, F, H, ntok), lib.vq_qmv_workspace_bytes_for(Q6_K, H, F, ntok))
+    import ctypes
+
+    rows2 = (ctypes.c_int * 2)(F, F)
+    nws = max(lib.vq_qmv_group_workspace_bytes(Q3_K, 2, rows2, H, ntok),
+              lib.vq_qmv_workspace_bytes_for(Q6_K, H, F, ntok))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
     # Per matrix: vq_qmv (its own routing, with the workspace) or the grouped streaming launches.
     if mfma is None:
@@ -448,9 +453,11 @@ def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=Non
 
     def launch(i):
         wg, wu, wd = sets[i % copies]
-        if own_gu:
-            qmv(Q3_K, wg, F, H, x, g)
-            qmv(Q3_K, wu, F, H, x, u)
+        if own_gu:  # gate and up in one call: one MFMA launch over both matrices' row tiles
+            st = lib.vq_qmv_group_ws(Q3_K, 2, (ctypes.c_void_p * 2)(wg.data_ptr(), wu.data_ptr()), rows2,
+                                     (ctypes.c_void_p * 2)(g.data_ptr(), u.data_ptr()), H, x.data_ptr(), ntok,
+                                     ws.data_ptr(), nws, hip.s())
+            assert st == 0, st
         else:
             hip.group_f32(Q3_K, [wg, wu], [F, F], [g, u], H, x, ntok)
         if own_d:

@@ -292,6 +292,16 @@ int vq_qmv_group(int type, int n, const uint8_t *const *w, const int *rows, floa
 int vq_qmv_group_f32(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
                      const float *x, int ntok, void *stream);
 
+/* vq_qmv_group_f32 with vq_qmv's batch routing, for callers that pass a workspace: 5-16 tokens of Q3_K, Q4_K,
+ * Q5_K or Q6_K run all n matrices in one f16-MFMA launch (plus one launch adding the K ranges' partial sums);
+ * other MFMA batches run matrix by matrix as vq_qmv; everything else as vq_qmv_group_f32. The workspace size
+ * is vq_qmv_group_workspace_bytes (rows: the n row counts); with less, the call routes as if it had none. No
+ * counterpart in the reference's per-matrix qmv (qwen_runtime.cu:1860); its effect equals n vq_qmv calls with
+ * that workspace. */
+size_t vq_qmv_group_workspace_bytes(int type, int n, const int *rows, int cols, int ntok);
+int vq_qmv_group_ws(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                    const float *x, int ntok, void *workspace, size_t workspace_bytes, void *stream);
+
 /* vq_qmv_group_f32 over matrices of up to two quantized types (types[k] per matrix): a main type and Q8_0,
  * the type GGUF mixes give a layer's small tensors (e.g. the gated-delta beta/alpha projections next to its
  * Q5_K qkv/gate), or Q5_K and Q6_K (a full-attention layer's q next to its k and v). One launch per token chunk

@@ -543,3 +543,37 @@ def test_qmv_staged_without_flags_equals_vq_qmv_and_rejects_bad_arguments(env):
     assert bad(flags=2, nw=P(xd), eps=-1.0) == -4
     assert bad(ty=int(T.F32)) == -1
     assert bad(cols=32768) == -2
+
+
+@pytest.mark.parametrize("ty,cols,ntok", [(T.Q3_K, 5120, 8), (T.Q6_K, 5120, 5), (T.Q4_K, 512, 16), (T.Q5_K, 2048, 11),
+                                          (T.IQ4_XS, 2048, 8), (T.Q4_K, 2048, 2), (T.Q6_K, 25600, 3)],
+                         ids=lambda v: v.name if isinstance(v, T) else str(v))
+def test_qmv_group_ws_matches_single_calls(env, oracle_mod, ty, cols, ntok):
+    """vq_qmv_group_ws over three matrices of different heights: bit-identical to one vq_qmv per matrix with the
+    same workspace size rules (5-16 tokens of Q3_K..Q6_K in one f16-MFMA launch over all row tiles, with one
+    or several K ranges; IQ4_XS at 8 tokens matrix by matrix on int8 MFMA; 2 tokens streaming; a 25600-wide
+    input packed once), and within the bar of the oracle."""
+    torch, lib = env
+    rng = np.random.default_rng(int(ty) * 100 + ntok + cols)
+    rows = [300, 1000, 129]
+    ws_np = [synth.baseline_rows(ty, r, cols, rng) for r in rows]
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    xd_ = dev(torch, x)
+    wd = [wdev(torch, w) for w in ws_np]
+    ys = [torch.full((ntok, r), np.nan, dtype=torch.float32, device="cuda") for r in rows]
+    ra = (ctypes.c_int * 3)(*rows)
+    nws = lib.vq_qmv_group_workspace_bytes(int(ty), 3, ra, cols, ntok)
+    wsb = torch.empty(max(nws, 256), dtype=torch.uint8, device="cuda")
+    st = lib.vq_qmv_group_ws(int(ty), 3, (ctypes.c_void_p * 3)(*[P(t) for t in wd]), ra,
+                             (ctypes.c_void_p * 3)(*[P(t) for t in ys]), cols, P(xd_), ntok, P(wsb), nws, None)
+    assert st == 0, lib.vq_status_string(st)
+    torch.cuda.synchronize()
+    for w, r, yt, wdt in zip(ws_np, rows, ys, wd):
+        one = torch.full((ntok, r), np.nan, dtype=torch.float32, device="cuda")
+        n1 = lib.vq_qmv_workspace_bytes_for(int(ty), r, cols, ntok)
+        w1 = torch.empty(max(n1, 256), dtype=torch.uint8, device="cuda")
+        assert lib.vq_qmv(int(ty), P(wdt), r, cols, P(xd_), ntok, P(one), P(w1), n1, None) == 0
+        torch.cuda.synchronize()
+        got = yt.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), one.cpu().numpy().view(np.uint32)), r
+        assert rel_l2(got, oracle_mod.qmv(int(ty), w, r, cols, x, ntok)) <= REL_L2_TOL, r

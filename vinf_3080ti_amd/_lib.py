@@ -59,6 +59,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_int_partials": (I, [I, P, I, I, P, I, P, P]),
     "vq_qmv_group": (I, [I, I, P, P, P, I, P, I, P]),
     "vq_qmv_group_f32": (I, [I, I, P, P, P, I, P, I, P]),
+    "vq_qmv_group_workspace_bytes": (SZ, [I, I, P, I, I]),
+    "vq_qmv_group_ws": (I, [I, I, P, P, P, I, P, I, P, SZ, P]),
     "vq_qmv_group_mixed_f32": (I, [I, P, P, P, P, I, P, I, P]),
     "vq_qgemm": (I, [I, P, I, I, P, I, P, P]),
     "vq_qgemm_workspace_bytes": (SZ, [I, I, I, I]),

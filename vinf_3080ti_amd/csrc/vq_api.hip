@@ -582,6 +582,68 @@ int vq_qmv_group_f32(int type, int n, const uint8_t *const *w, const int *rows, 
     return qmv_group_any(type, n, w, rows, y, cols, x, true, ntok, stream);
 }
 
+// Grouped matvec with vq_qmv's batch routing: 5..16 tokens of Q3_K..Q6_K in one f16-MFMA launch over every
+// matrix's row tiles (plus one launch of K-range sums); other MFMA batches matrix by matrix through vq_qmv;
+// everything else as vq_qmv_group_f32 (one streaming launch) or, past the in-kernel quantizer's width, vq_qmv.
+static bool group_args_ok(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                          const float *x, int ntok, int *st) {
+    *st = VQ_OK;
+    if (n < 1 || n > VQ_MAX_GROUP || !w || !rows || !y || !x || misaligned16(x)) *st = VQ_ERR_ARG;
+    else if (type == VQ_F32 || type == VQ_F16) *st = VQ_ERR_TYPE;
+    else if (ntok < 1) *st = VQ_ERR_SHAPE;
+    for (int k = 0; *st == VQ_OK && k < n; ++k) {
+        *st = check_matrix(type, rows[k], cols);
+        if (*st == VQ_OK && (!w[k] || !y[k] || misaligned16(w[k]))) *st = VQ_ERR_ARG;
+    }
+    return *st == VQ_OK;
+}
+
+size_t vq_qmv_group_workspace_bytes(int type, int n, const int *rows, int cols, int ntok) {
+    if (n < 1 || n > VQ_MAX_GROUP || !rows || ntok < 1) return 0;
+    size_t s16 = 0, most = 0;
+    for (int k = 0; k < n; ++k) {
+        if (check_matrix(type, rows[k], cols)) return 0;
+        s16 += vq::s16_part_bytes(rows[k], cols, ntok);
+        const size_t one = vq_qmv_workspace_bytes_for(type, rows[k], cols, ntok);
+        most = one > most ? one : most;
+    }
+    return small16_batch(type, cols, ntok) ? s16 : most;
+}
+
+int vq_qmv_group_ws(int type, int n, const uint8_t *const *w, const int *rows, float *const *y, int cols,
+                    const float *x, int ntok, void *workspace, size_t workspace_bytes, void *stream) {
+    int st;
+    if (!group_args_ok(type, n, w, rows, y, cols, x, ntok, &st)) return st;
+    const bool ws = workspace && !misaligned16(workspace);
+    if (small16_batch(type, cols, ntok)) {
+        size_t need = 0;
+        for (int k = 0; k < n; ++k) need += vq::s16_part_bytes(rows[k], cols, ntok);
+        if (need == 0 || (ws && workspace_bytes >= need)) {
+            hipStream_t s = static_cast<hipStream_t>(stream);
+            const long rb = row_bytes_of(type, cols);
+            float *part = need ? static_cast<float *>(workspace) : nullptr;
+            return dispatch_quant(type, [&](auto tc) {
+                return vq::launch_small16_group<decltype(tc)::value>(n, w, rows, y, cols, rb, x, ntok, part, s);
+            });
+        }
+    }
+    bool each = false;
+    for (int k = 0; k < n && !each; ++k)
+        each = qmv_route(type, rows[k], cols, ntok, ws, workspace_bytes) != VQ_PATH_STREAM;
+    if (!each) {
+        const size_t pk = vq_qmv_workspace_bytes(cols, ntok);  // wide inputs: packed once for the group
+        if (pk == 0) return vq_qmv_group_f32(type, n, w, rows, y, cols, x, ntok, stream);
+        if (!ws || workspace_bytes < pk) return VQ_ERR_WORKSPACE;
+        st = vq_pack_x(x, ntok, cols, workspace, stream);
+        return st ? st : vq_qmv_group(type, n, w, rows, y, cols, workspace, ntok, stream);
+    }
+    for (int k = 0; k < n; ++k) {  // in stream order, each call done with the workspace before the next uses it
+        st = vq_qmv(type, w[k], rows[k], cols, x, ntok, y[k], workspace, workspace_bytes, stream);
+        if (st) return st;
+    }
+    return VQ_OK;
+}
+
 int vq_qmv_group_mixed_f32(int n, const int *types, const uint8_t *const *w, const int *rows, float *const *y,
                            int cols, const float *x, int ntok, void *stream) {
     if (n < 1 || n > VQ_MAX_GROUP || !types || !w || !rows || !y) return VQ_ERR_ARG;

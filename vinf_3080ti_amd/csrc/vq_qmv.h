@@ -70,6 +70,9 @@ int launch_gemm16(const uint8_t *w, int rows, int cols, long row_bytes, const vo
 // Matvec of 1..16 tokens on f16 MFMA (Q3_K, Q4_K, Q5_K, Q6_K; other types return hipErrorInvalidValue), fp32
 // activations; `part` holds s16_part_bytes(rows, cols, ntok) bytes (unused when that is 0).
 template <int T>
+int launch_small16_group(int n, const uint8_t *const *w, const int *rows, float *const *y, int cols, long row_bytes,
+                         const float *x, int ntok, float *part, hipStream_t s);
+template <int T>
 int launch_small16(const uint8_t *w, int rows, int cols, long row_bytes, const float *x, int ntok, float *y,
                    float *part, hipStream_t s);
 // Small-batch (2..16 tokens) matvec on int8 MFMA; `part` holds mfma_part_bytes(rows, cols, ntok) bytes (unused

@@ -1046,6 +1046,8 @@ int launch_dequant(const uint8_t *w, int rows, int cols, long rb, float *out, hi
                                         const float *, int, hipStream_t);                                          \
     template int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \
     template int vq::launch_gemm16<T>(const uint8_t *, int, int, long, const void *, int, float *, int, hipStream_t, bool); \
+    template int vq::launch_small16_group<T>(int, const uint8_t *const *, const int *, float *const *, int, long,    \
+                                             const float *, int, float *, hipStream_t);                            \
     template int vq::launch_small16<T>(const uint8_t *, int, int, long, const float *, int, float *, float *,          \
                                        hipStream_t);                                                               \
     template int vq::launch_mfma<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, float *,       \

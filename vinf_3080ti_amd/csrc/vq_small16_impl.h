@@ -49,6 +49,17 @@ inline size_t s16_part_bytes(int rows, int cols, int ntok) {
     return nkr > 1 ? (static_cast<size_t>(nkr) * ntok * rows * 4 + 255) / 256 * 256 : 0;
 }
 
+// Up to four matrices of one type and width reading the same activations, in one launch: job j owns the row
+// tiles [tile0[j], tile0[j + 1]) of the grid and writes out[j] (y, or its partial sums with several K ranges).
+constexpr int kS16MaxJobs = 4;
+struct S16Jobs {
+    const uint8_t *w[kS16MaxJobs];
+    float *out[kS16MaxJobs];
+    int rows[kS16MaxJobs];
+    int tile0[kS16MaxJobs + 1];
+    int n;
+};
+
 // Eight codes (bytes of c0, c1) times the part's scale, as f16: exact for every type here.
 template <int T>
 __device__ __forceinline__ void s16_frag(uint32_t c0, uint32_t c1, int isc, g16h8 &a1, g16h8 &a2) {
@@ -90,9 +101,8 @@ __device__ __forceinline__ void s16_frag(uint32_t c0, uint32_t c1, int isc, g16h
 __device__ __forceinline__ void s16_opaque(float &v) { asm volatile("" : "+v"(v)); }
 
 template <int T>
-__global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const uint8_t *__restrict__ w, int rows, int cols,
-                                                              long row_bytes, const float *__restrict__ x, int ntok,
-                                                              float *__restrict__ out) {
+__global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S16Jobs J, int cols, long row_bytes,
+                                                              const float *__restrict__ x, int ntok) {
     using S = Sl<T>;
     constexpr int SPL = S::SPB / 4;  // slices per lane per super-block: a lane owns a quarter of it
     constexpr int NP = S::NP;
@@ -110,6 +120,11 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const ui
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lr = lane & 15, lk = lane >> 4;
+    int jb = 0;
+    while (jb + 1 < J.n && static_cast<int>(blockIdx.x) >= J.tile0[jb + 1]) ++jb;
+    const uint8_t *const w = J.w[jb];
+    float *const out = J.out[jb];
+    const int rows = J.rows[jb];
     const int kr = blockIdx.y, k0 = kr * kS16KR;
     const int kw = cols - k0 < kS16KR ? cols - k0 : kS16KR;  // a multiple of 256
     const int nsb = kw >> 8, sbg0 = k0 >> 8;
@@ -143,7 +158,7 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const ui
             v[4 * q + 3] = f.w;
         }
     }
-    const int tile = blockIdx.x;
+    const int tile = blockIdx.x - J.tile0[jb];
     typename S::W wr[kS16NSB][SPL];
     load_tile(tile, wr);
 
@@ -305,28 +320,97 @@ __global__ __launch_bounds__(256) inline void s16_sum1_kernel(const float *__res
     y[i] = v;
 }
 
+// The K-range sums of several jobs in one launch: job j's n[j] outputs (a multiple of 4) are the float4
+// elements [e0[j], e0[j + 1]) of the grid; each is summed as s16_sum_kernel does.
+struct S16Sum {
+    const float *part[kS16MaxJobs];
+    float *y[kS16MaxJobs];
+    long n[kS16MaxJobs];
+    long e0[kS16MaxJobs + 1];
+    int jobs;
+};
+__global__ __launch_bounds__(256) inline void s16_sum_jobs_kernel(S16Sum P, int nkr) {
+    const long e = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= P.e0[P.jobs]) return;
+    int jb = 0;
+    while (jb + 1 < P.jobs && e >= P.e0[jb + 1]) ++jb;
+    const long i = (e - P.e0[jb]) * 4, n = P.n[jb];
+    const float4 *p = reinterpret_cast<const float4 *>(P.part[jb] + i);
+    const long st = n / 4;
+    float4 v = p[0];
+    int k = 1;
+    for (; k + 4 <= nkr; k += 4) {
+        const float4 a = p[k * st], b = p[(k + 1) * st], c = p[(k + 2) * st], d = p[(k + 3) * st];
+        v.x += a.x, v.y += a.y, v.z += a.z, v.w += a.w;
+        v.x += b.x, v.y += b.y, v.z += b.z, v.w += b.w;
+        v.x += c.x, v.y += c.y, v.z += c.z, v.w += c.w;
+        v.x += d.x, v.y += d.y, v.z += d.z, v.w += d.w;
+    }
+    for (; k < nkr; ++k) {
+        const float4 a = p[k * st];
+        v.x += a.x, v.y += a.y, v.z += a.z, v.w += a.w;
+    }
+    *reinterpret_cast<float4 *>(P.y[jb] + i) = v;
+}
+
+// n <= kS16MaxJobs matrices of type T sharing cols and x: one qmv16 launch over all their row tiles, then one
+// launch of K-range sums (several K ranges: `part` holds the sum of s16_part_bytes(rows[j], cols, ntok)).
 template <int T>
-int launch_small16(const uint8_t *w, int rows, int cols, long rb, const float *x, int ntok, float *y, float *part,
-                   hipStream_t s) {
+int launch_small16_group(int n, const uint8_t *const *w, const int *rows, float *const *y, int cols, long rb,
+                         const float *x, int ntok, float *part, hipStream_t s) {
     if constexpr (!kSmall16<T>) {
-        (void)w, (void)rows, (void)cols, (void)rb, (void)x, (void)ntok, (void)y, (void)part, (void)s;
+        (void)n, (void)w, (void)rows, (void)y, (void)cols, (void)rb, (void)x, (void)ntok, (void)part, (void)s;
         return static_cast<int>(hipErrorInvalidValue);
     } else {
-        if (ntok < 1 || ntok > 16 || cols % 256 != 0) return static_cast<int>(hipErrorInvalidValue);
+        if (n < 1 || n > kS16MaxJobs || ntok < 1 || ntok > 16 || cols % 256 != 0)
+            return static_cast<int>(hipErrorInvalidValue);
         const int nkr = s16_ranges(cols);
         if (nkr > 1 && part == nullptr) return static_cast<int>(hipErrorInvalidValue);
-        const dim3 grid((rows + kS16Rows - 1) / kS16Rows, nkr), block(64 * kS16Waves);
-        qmv16_kernel<T><<<grid, block, s16_lds(ntok), s>>>(w, rows, cols, rb, x, ntok, nkr > 1 ? part : y);
+        S16Jobs J{};
+        J.n = n;
+        J.tile0[0] = 0;
+        uint8_t *pp = reinterpret_cast<uint8_t *>(part);
+        for (int k = 0; k < n; ++k) {
+            J.w[k] = w[k];
+            J.rows[k] = rows[k];
+            J.out[k] = nkr > 1 ? reinterpret_cast<float *>(pp) : y[k];
+            if (nkr > 1) pp += s16_part_bytes(rows[k], cols, ntok);
+            J.tile0[k + 1] = J.tile0[k] + (rows[k] + kS16Rows - 1) / kS16Rows;
+        }
+        const dim3 grid(J.tile0[n], nkr), block(64 * kS16Waves);
+        qmv16_kernel<T><<<grid, block, s16_lds(ntok), s>>>(J, cols, rb, x, ntok);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || nkr == 1) return static_cast<int>(e);
-        const long n = static_cast<long>(ntok) * rows;
-        if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(y)) % 16 == 0)
-            s16_sum_kernel<<<static_cast<unsigned>((n / 4 + 255) / 256), 256, 0, s>>>(part, nkr, n, y);
-        else
-            s16_sum1_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(part, nkr, n, y);
+        bool vec = true;
+        for (int k = 0; k < n; ++k)
+            vec = vec && (static_cast<long>(ntok) * rows[k]) % 4 == 0 &&
+                  (reinterpret_cast<uintptr_t>(J.out[k]) | reinterpret_cast<uintptr_t>(y[k])) % 16 == 0;
+        if (vec) {
+            S16Sum P{};
+            P.jobs = n;
+            P.e0[0] = 0;
+            for (int k = 0; k < n; ++k) {
+                P.part[k] = J.out[k];
+                P.y[k] = y[k];
+                P.n[k] = static_cast<long>(ntok) * rows[k];
+                P.e0[k + 1] = P.e0[k] + P.n[k] / 4;
+            }
+            s16_sum_jobs_kernel<<<static_cast<unsigned>((P.e0[n] + 255) / 256), 256, 0, s>>>(P, nkr);
+        } else {
+            for (int k = 0; k < n; ++k) {
+                const long m = static_cast<long>(ntok) * rows[k];
+                s16_sum1_kernel<<<static_cast<unsigned>((m + 255) / 256), 256, 0, s>>>(J.out[k], nkr, m, y[k]);
+            }
+        }
         e = hipGetLastError();
         return e == hipSuccess ? 0 : static_cast<int>(e);
     }
+}
+
+template <int T>
+int launch_small16(const uint8_t *w, int rows, int cols, long rb, const float *x, int ntok, float *y, float *part,
+                   hipStream_t s) {
+    return launch_small16_group<T>(1, &w, &rows, &y, cols, rb, x, ntok, part, s);
 }
 
 }  // namespace vq

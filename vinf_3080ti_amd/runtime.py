@@ -656,17 +656,17 @@ class Runtime:
         wa = (ctypes.c_void_p * n)(*[t.data.data_ptr() for t in ts])
         ra = (ctypes.c_int * n)(*[t.rows for t in ts])
         ya = (ctypes.c_void_p * n)(*[b.data_ptr() for b in yb])
-        nws = self._lib.vq_qmv_workspace_bytes(t0.cols, ntok)
         if any(t.type != t0.type for t in ts):
-            # Mixed types (e.g. Q5_K projections with Q8_0 small tensors): one launch for a main type + Q8_0.
+            # Mixed types (Q5_K projections with Q8_0 small tensors, or Q5_K with Q6_K): one launch.
             ta = (ctypes.c_int * n)(*[t.type for t in ts])
             st = self._lib.vq_qmv_group_mixed_f32(n, ta, wa, ra, ya, t0.cols, xb.data_ptr(), ntok, self._stream())
-        elif nws == 0:
-            st = self._lib.vq_qmv_group_f32(t0.type, n, wa, ra, ya, t0.cols, xb.data_ptr(), ntok, self._stream())
         else:
-            xp = self._workspace(nws)
-            _lib.check(self._lib.vq_pack_x(xb.data_ptr(), ntok, t0.cols, xp.data_ptr(), self._stream()), "pack_x")
-            st = self._lib.vq_qmv_group(t0.type, n, wa, ra, ya, t0.cols, xp.data_ptr(), ntok, self._stream())
+            # One type: the streaming group launch, or for small batches the MFMA paths qmv would take (5-16
+            # tokens of Q3_K..Q6_K as one launch over all the matrices).
+            nws = self._lib.vq_qmv_group_workspace_bytes(t0.type, n, ra, t0.cols, ntok)
+            ws = self._workspace(nws).data_ptr() if nws else None
+            st = self._lib.vq_qmv_group_ws(t0.type, n, wa, ra, ya, t0.cols, xb.data_ptr(), ntok, ws, nws,
+                                           self._stream())
         _lib.check(st, "qmv_group launch")
 
     def lmhead_argmax(self, weight: str, x: str, ntok: int = 1, logits: str | None = None) -> list[int]:
