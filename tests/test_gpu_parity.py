@@ -577,3 +577,33 @@ def test_qmv_group_ws_matches_single_calls(env, oracle_mod, ty, cols, ntok):
         got = yt.cpu().numpy()
         assert np.array_equal(got.view(np.uint32), one.cpu().numpy().view(np.uint32)), r
         assert rel_l2(got, oracle_mod.qmv(int(ty), w, r, cols, x, ntok)) <= REL_L2_TOL, r
+
+
+def test_iq3s_grid_setter_reaches_every_path(env, oracle_mod):
+    """vq_set_iq3s_grid replaces the IQ3_S codebook for every kernel (the reference uploads it at Runtime init,
+    qwen_runtime.cu:1272-1286), including the streaming kernel's pre-signed copy of it. With the grid's
+    entries reversed (entry e <- entry 511 - e), the matvec of weights W equals the oracle's (default grid)
+    on W with every grid index i replaced by 511 - i (qs bytes and qh bits complemented), at 1 and 2 tokens
+    (pre-signed table), 3 tokens (register signs) and 8 tokens (int8-MFMA small-batch kernel)."""
+    torch, lib = env
+    rng = np.random.default_rng(353)
+    rows, cols = 200, 2048
+    w = synth.baseline_rows(T.IQ3_S, rows, cols, rng)
+    wflip = w.reshape(rows, cols // 256, 110).copy()
+    wflip[:, :, 2:74] ^= 0xFF
+    grid = np.frombuffer(oracle_mod.table("iq3s_grid"), np.uint8).reshape(512, 4)
+    rev = np.ascontiguousarray(grid[::-1])
+    buf = (ctypes.c_uint8 * 2048).from_buffer_copy(rev.tobytes())
+    assert lib.vq_set_iq3s_grid(ctypes.addressof(buf)) == 0
+    try:
+        for ntok, fast in ((1, False), (2, False), (3, False), (8, True)):
+            x = rng.standard_normal((ntok, cols)).astype(np.float32)
+            got = gpu_qmv(torch, lib, T.IQ3_S, w, rows, cols, x, ntok, fast)
+            ref = oracle_mod.qmv(int(T.IQ3_S), wflip.reshape(-1), rows, cols, x, ntok)
+            assert rel_l2(got, ref) <= REL_L2_TOL, ntok
+    finally:
+        orig = (ctypes.c_uint8 * 2048).from_buffer_copy(grid.tobytes())
+        assert lib.vq_set_iq3s_grid(ctypes.addressof(orig)) == 0
+    x = rng.standard_normal((1, cols)).astype(np.float32)
+    assert rel_l2(gpu_qmv(torch, lib, T.IQ3_S, w, rows, cols, x, 1),
+                  oracle_mod.qmv(int(T.IQ3_S), w, rows, cols, x, 1)) <= REL_L2_TOL

@@ -25,6 +25,21 @@
 #include "vq_mfma_impl.h"
 #include "../../include/vq.h"
 
+// Every per-type kernel lives in its vq_t_<type>.hip unit; here only declared (no second copy).
+VQ_KERNEL_TEMPLATES(extern template, VQ_Q8_0)
+VQ_KERNEL_TEMPLATES(extern template, VQ_Q2_K)
+VQ_KERNEL_TEMPLATES(extern template, VQ_Q3_K)
+VQ_KERNEL_TEMPLATES(extern template, VQ_Q4_K)
+VQ_KERNEL_TEMPLATES(extern template, VQ_Q5_K)
+VQ_KERNEL_TEMPLATES(extern template, VQ_Q6_K)
+VQ_KERNEL_TEMPLATES(extern template, VQ_IQ4_NL)
+VQ_KERNEL_TEMPLATES(extern template, VQ_IQ4_XS)
+VQ_KERNEL_TEMPLATES(extern template, VQ_IQ3_S)
+VQ_KERNEL_TEMPLATES(extern template, VQ_IQ2_XXS)
+VQ_KERNEL_TEMPLATES(extern template, VQ_IQ2_XS)
+VQ_KERNEL_TEMPLATES(extern template, VQ_IQ2_S)
+VQ_KERNEL_TEMPLATES(extern template, VQ_IQ3_XXS)
+
 
 // ---- static scratch of the no-allocation entry point (vq_qmv_noalloc) -----------------------------------
 // One fixed array in device memory per GPU the library runs on, held until the process ends. Host code never

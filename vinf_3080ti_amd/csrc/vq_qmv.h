@@ -90,3 +90,28 @@ int launch_dequant(const uint8_t *w, int rows, int cols, long row_bytes, float *
 int set_iq3s_grid(const uint8_t *grid);
 
 }  // namespace vq
+
+// The per-type kernel templates, instantiated once per type by VQ_INSTANTIATE (vq_qmv_impl.h) in
+// vq_t_<type>.hip; other translation units that see the definitions declare them extern with
+// VQ_KERNEL_TEMPLATES(extern template, T), so each kernel (and each copy of the device tables it reads, e.g.
+// the replaceable IQ3_S grid) exists once.
+#define VQ_KERNEL_TEMPLATES(KW, T)                                                                                       \
+    KW int vq::launch_quant<T>(const uint8_t *, int, int, long, const void *, bool, int, float *, hipStream_t); \
+    KW int vq::launch_quant_jobs<T>(int, const uint8_t *const *, const int *, float *const *, int, const void *, \
+                                          bool, int, unsigned long long *, int32_t *, hipStream_t);                 \
+    KW long vq::argmax_waves<T>(int, int, int);                                                                \
+    KW int vq::launch_quant_staged<T>(const uint8_t *, int, int, long, const float *, const vq::XStage &, int, \
+                                            float *, hipStream_t);                                                   \
+    KW int vq::launch_mixed_q8<T>(int, const int *, const uint8_t *const *, const int *, float *const *, int, \
+                                        const float *, int, hipStream_t);                                          \
+    KW int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \
+    KW int vq::launch_gemm16<T>(const uint8_t *, int, int, long, const void *, int, float *, int, hipStream_t, bool); \
+    KW int vq::launch_small16_group<T>(int, const uint8_t *const *, const int *, float *const *, int, long,    \
+                                             const float *, int, float *, hipStream_t);                            \
+    KW int vq::launch_small16<T>(const uint8_t *, int, int, long, const float *, int, float *, float *,          \
+                                       hipStream_t);                                                               \
+    KW int vq::launch_mfma<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, float *,       \
+                                    hipStream_t);                                                                \
+    KW int vq::launch_partials<T>(const uint8_t *, int, int, long, const uint8_t *, int, int32_t *,          \
+                                        hipStream_t);                                                            \
+    KW int vq::launch_dequant<T>(const uint8_t *, int, int, long, float *, hipStream_t);

@@ -98,12 +98,21 @@ __host__ __device__ constexpr bool lane_slots(long rwg, int nu, int su, int nt) 
     return nt == 1 && (rwg * nu + su - 1) / su * 64 <= kSlotFloats;
 }
 
-template <int T>
+// Launches of at most this many tokens of a kSignedGrid type read the pre-signed table (32 KB of LDS; wider
+// activation images leave no room for it).
+constexpr int kSignedGridMaxTok = 2;
+template <int T, int NT>
+constexpr bool use_signed_grid() {
+    return kSignedGrid<T> && NT <= kSignedGridMaxTok;
+}
+template <int T, int NT>
 constexpr int grid_table_bytes() {
+    if constexpr (use_signed_grid<T, NT>()) return 512 * 16 * 4;
     return TabSpec<T>::n8 * 8 + TabSpec<T>::n4 * 4;
 }
-template <int T>
+template <int T, int NT>
 __device__ __forceinline__ const uint8_t *grid_table_src() {
+    if constexpr (use_signed_grid<T, NT>()) return reinterpret_cast<const uint8_t *>(g_iq3s_sg.v);
     if constexpr (T == VQ_IQ2_XXS) return reinterpret_cast<const uint8_t *>(g_iq2xxs.v);
     if constexpr (T == VQ_IQ2_XS) return reinterpret_cast<const uint8_t *>(g_iq2xs.v);
     if constexpr (T == VQ_IQ2_S) return reinterpret_cast<const uint8_t *>(g_iq2s.v);
@@ -164,7 +173,8 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     using S = Sl<T>;
     using G = Stream<T>;
     constexpr int NP = S::NP, UB = S::UB, LPU = G::LPU, SU = G::SU, NL = G::NL;
-    constexpr int TB = grid_table_bytes<T>();
+    constexpr int TB = grid_table_bytes<T, NT>();
+    constexpr bool SG = use_signed_grid<T, NT>();
     extern __shared__ __attribute__((aligned(1024))) uint8_t s_dyn[];
     __shared__ __attribute__((aligned(1024))) uint8_t s_grid[TB > 0 ? TB : 16];
     __shared__ uint4 sks[TabSpec<T>::ks ? 128 : 1];
@@ -224,7 +234,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     int s = wv < nst ? wv : -1;
     u32x4 RA[NL];
     if constexpr (TB > 0) {
-        const uint8_t *src = grid_table_src<T>();
+        const uint8_t *src = grid_table_src<T, NT>();
         for (int p = wv; p < TB / 1024; p += NW) dma16(src + p * 1024, lane * 16, s_grid + p * 1024);
     }
     if constexpr (XF32) {
@@ -343,8 +353,12 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     if (s >= 0) load_stage(s, RA);  // waves without a stage load nothing
     if (threadIdx.x == 0) s_next = NW;
     Tabs tb{};
-    if constexpr (TabSpec<T>::n8 > 0) tb.grid8 = reinterpret_cast<const uint2 *>(s_grid);
-    if constexpr (TabSpec<T>::n4 > 0) tb.grid4 = reinterpret_cast<const uint32_t *>(s_grid);
+    if constexpr (SG) {
+        tb.sg = reinterpret_cast<const uint32_t *>(s_grid);
+    } else {
+        if constexpr (TabSpec<T>::n8 > 0) tb.grid8 = reinterpret_cast<const uint2 *>(s_grid);
+        if constexpr (TabSpec<T>::n4 > 0) tb.grid4 = reinterpret_cast<const uint32_t *>(s_grid);
+    }
     if constexpr (TabSpec<T>::ks) {
         for (int i = threadIdx.x; i < 128; i += blockDim.x) sks[i] = sign_entry(ksigns(i));
         tb.ks128 = sks;
@@ -383,16 +397,38 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
         // The unit's group scales and half sums of every token.
         float xdu[NT][S::UG];
         int32_t xhu[NT][S::UG];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const uint8_t *xt = s_dyn + t * xi.bytes + xi.xq_bytes;
-#pragma unroll
-            for (int g = 0; g < S::UG; ++g) {
-                xdu[t][g] = reinterpret_cast<const float *>(xt)[G0 + g];
-                if constexpr (kNeedsX<T>) xhu[t][g] = reinterpret_cast<const int32_t *>(xt + 4 * xi.ng)[G0 + g];
-            }
-        }
         if constexpr (kIntScales<T>()) {
+            // Every slice decoder's group index is affine in the slice with the lane's own slices lj + LPU k
+            // giving the groups of lane 0's slices shifted by one lane constant dg. Accumulators and activation
+            // scales are indexed by lane 0's group pg0 (a compile-time index after unrolling: runtime indices
+            // into register arrays become compare/select chains), the activation scales read at G0 + dg + pg0.
+            static_assert(!kScaledCodes<T>() || LPU == 1, "scaled codes index their shift by the group");
+            int dg, dh, d0, h0;
+            S::part(lj, 0, dg, dh);
+            S::part(0, 0, d0, h0);
+            dg -= d0;
+            const int Gd = G0 + dg;
+            bool used[S::UG];
+#pragma unroll
+            for (int g = 0; g < S::UG; ++g) used[g] = false;
+#pragma unroll
+            for (int k = 0; k < G::SPL; ++k)
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    int pg0, ph0;
+                    S::part(LPU * k, p, pg0, ph0);
+                    used[pg0] = true;
+                }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const uint8_t *xt = s_dyn + t * xi.bytes + xi.xq_bytes;
+#pragma unroll
+                for (int g = 0; g < S::UG; ++g) {
+                    if (!used[g]) continue;
+                    xdu[t][g] = reinterpret_cast<const float *>(xt)[Gd + g];
+                    if constexpr (kNeedsX<T>) xhu[t][g] = reinterpret_cast<const int32_t *>(xt + 4 * xi.ng)[Gd + g];
+                }
+            }
             // Integer scales: per (token, group) the exact int32 sum of S * scale (and X * min), then one
             // conversion and fp32 multiply-add per group with the activation scale; the unit's fp32 multipliers
             // (d, dmin) are applied once.
@@ -410,6 +446,8 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
                 uint32_t cd[NP][4];
                 if constexpr (kScaledCodes<T>())
                     S::codes_scaled(wr, ss, tb, cd);
+                else if constexpr (SG)
+                    S::codes_sg(wr, ss, tb, cd);
                 else
                     S::codes(wr, ss, tb, cd);
                 int isc[NP], imn[NP];
@@ -421,23 +459,24 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
                 }
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
-                    int pg, ph;
+                    int pg, ph, pg0, ph0;
                     S::part(ss, p, pg, ph);
-                    const int Gi = G0 + pg;
+                    S::part(LPU * k, p, pg0, ph0);
+                    const int Gi = Gd + pg0;
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         const uint8_t *xt = s_dyn + t * xi.bytes;
                         const u32x4 xv4 = *reinterpret_cast<const u32x4 *>(xt + xi.code_off(Gi, ph));
                         const int X = kNeedsX<T> ? static_cast<int>(static_cast<int16_t>(
-                                                       static_cast<uint32_t>(xhu[t][pg]) >> (16 * ph)))
+                                                       static_cast<uint32_t>(xhu[t][pg0]) >> (16 * ph)))
                                                  : 0;
                         constexpr int OFFS = S::OFF;
                         int off = OFFS;
-                        if constexpr (kScaledCodes<T>()) off = OFFS << S::gsh(pg);
+                        if constexpr (kScaledCodes<T>()) off = OFFS << S::gsh(pg0);
                         const int Sv = dot4(cd[p][3], xv4.w, dot4(cd[p][2], xv4.z, dot4(cd[p][1], xv4.y,
                                             dot4(cd[p][0], xv4.x, -off * X))));
-                        gs[t][pg] += __mul24(Sv, isc[p]);
-                        if constexpr (kHasMin<T>) gm[t][pg] += __mul24(X, imn[p]);
+                        gs[t][pg0] += __mul24(Sv, isc[p]);
+                        if constexpr (kHasMin<T>) gm[t][pg0] += __mul24(X, imn[p]);
                     }
                 }
             }
@@ -446,6 +485,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
                 float a = 0.0f, m = 0.0f;
 #pragma unroll
                 for (int g = 0; g < S::UG; ++g) {
+                    if (!used[g]) continue;
                     int gsum = gs[t][g];
                     if constexpr (kScaledCodes<T>()) gsum >>= S::gsh(g);  // exact: a multiple of 2^gsh
                     a = fmaf(static_cast<float>(gsum), xdu[t][g], a);
@@ -454,6 +494,17 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
                 v[t] = kHasMin<T> ? fmaf(a, dmul, -m * dmn) : a * dmul;
             }
         } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const uint8_t *xt = s_dyn + t * xi.bytes + xi.xq_bytes;
+#pragma unroll
+                for (int g = 0; g < S::UG; ++g) {
+                    xdu[t][g] = reinterpret_cast<const float *>(xt)[G0 + g];
+                    if constexpr (kNeedsX<T>) xhu[t][g] = reinterpret_cast<const int32_t *>(xt + 4 * xi.ng)[G0 + g];
+                }
+            }
+        }
+        if constexpr (!kIntScales<T>()) {
 #pragma unroll
             for (int k = 0; k < G::SPL; ++k) {
                 const int ss = lj + LPU * k;
@@ -1035,23 +1086,4 @@ int launch_dequant(const uint8_t *w, int rows, int cols, long rb, float *out, hi
 }  // namespace vq
 
 // Explicit instantiation of one type's entry points (used by the per-type translation units).
-#define VQ_INSTANTIATE(T)                                                                                       \
-    template int vq::launch_quant<T>(const uint8_t *, int, int, long, const void *, bool, int, float *, hipStream_t); \
-    template int vq::launch_quant_jobs<T>(int, const uint8_t *const *, const int *, float *const *, int, const void *, \
-                                          bool, int, unsigned long long *, int32_t *, hipStream_t);                 \
-    template long vq::argmax_waves<T>(int, int, int);                                                                \
-    template int vq::launch_quant_staged<T>(const uint8_t *, int, int, long, const float *, const vq::XStage &, int, \
-                                            float *, hipStream_t);                                                   \
-    template int vq::launch_mixed_q8<T>(int, const int *, const uint8_t *const *, const int *, float *const *, int, \
-                                        const float *, int, hipStream_t);                                          \
-    template int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \
-    template int vq::launch_gemm16<T>(const uint8_t *, int, int, long, const void *, int, float *, int, hipStream_t, bool); \
-    template int vq::launch_small16_group<T>(int, const uint8_t *const *, const int *, float *const *, int, long,    \
-                                             const float *, int, float *, hipStream_t);                            \
-    template int vq::launch_small16<T>(const uint8_t *, int, int, long, const float *, int, float *, float *,          \
-                                       hipStream_t);                                                               \
-    template int vq::launch_mfma<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, float *,       \
-                                    hipStream_t);                                                                \
-    template int vq::launch_partials<T>(const uint8_t *, int, int, long, const uint8_t *, int, int32_t *,          \
-                                        hipStream_t);                                                            \
-    template int vq::launch_dequant<T>(const uint8_t *, int, int, long, float *, hipStream_t);
+#define VQ_INSTANTIATE(T) VQ_KERNEL_TEMPLATES(template, T)

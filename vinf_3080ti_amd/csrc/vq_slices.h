@@ -46,6 +46,7 @@ struct Tabs {
     const uint32_t *grid4;  // IQ3_XXS / IQ3_S magnitudes (4 bytes per entry)
     const uint4 *ks128;     // ggml ksigns (7 bits + parity) -> {m lo, m hi, e lo, e hi}
     const uint4 *sm256;     // raw 8 sign bits -> {m lo, m hi, e lo, e hi}
+    const uint32_t *sg;     // pre-signed grid words (IQ3_S, streaming kernel): [entry][4 sign bits]
 };
 
 template <int N>
@@ -749,6 +750,20 @@ struct Sl<VQ_IQ3_S> {
             }
         }
     }
+    // Codes from the pre-signed table: word (entry, 4 sign bits) at sg[entry * 16 + bits].
+    static __device__ __forceinline__ void codes_sg(const W &w, int, const Tabs &tb, uint32_t (&cc)[NP][4]) {
+        const uint32_t qh = w.qh.lo();
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
+            const uint32_t q[2] = {w.qs.word(2 * gg), w.qs.word(2 * gg + 1)};
+            const uint32_t sg = w.sg.word(gg);
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                const uint32_t i = bfe(q[l >> 2], 8 * (l & 3), 8) | (bfe(qh, 8 * gg + l, 1) << 8);
+                cc[2 * gg + (l >> 2)][l & 3] = tb.sg[(i << 4) | bfe(sg, 4 * l, 4)];
+            }
+        }
+    }
     static __device__ __forceinline__ void scales(const W &w, int, float *sc, float *mn) {
         const float d = half_to_float(w.d.lo());
         const uint32_t b = w.sc.lo();
@@ -768,6 +783,10 @@ struct Sl<VQ_IQ3_S> {
         isc[2] = isc[3] = static_cast<int>(1 + 2 * bfe(b, 4, 4));
     }
 };
+
+// Slice decoders with a pre-signed-table form (Sl<T>::codes_sg, read through Tabs::sg).
+template <int T>
+constexpr bool kSignedGrid = T == VQ_IQ3_S;
 
 // Types whose float term uses X (the 16-element activation sum) with a min coefficient.
 template <int T>

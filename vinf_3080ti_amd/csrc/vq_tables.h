@@ -58,6 +58,28 @@ static __device__ const Tab32<256> g_iq3xxs = expand_iq3(vq_iq3xxs_codes, false)
 // IQ3_S grid: replaceable at run time (the reference uploads it at Runtime init, qwen_runtime.cu:1272-1286).
 static __device__ Tab32<512> g_iq3s = expand_iq3(vq_iq3s_codes, true);
 
+// Pre-signed IQ3_S grid words for the streaming matvec: entry (e, s) is grid entry e with byte k negated where
+// bit k of s is set (4 sign bits per 4 weights), [entry 512][signs 16] (32 KB), so one LDS read replaces the
+// sign expansion in registers. (For IQ2_XXS the same table, two reads per 8 weights, made LDS the limit: no
+// gain, measured.)
+constexpr uint32_t signed_word(uint32_t g, uint32_t s4) {
+    uint32_t r = 0;
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t b = (g >> (8 * k)) & 0xFFu;
+        r |= (((s4 >> k) & 1u) ? ((0x100u - b) & 0xFFu) : b) << (8 * k);
+    }
+    return r;
+}
+template <int N>
+constexpr Tab32<N * 16> sign_iq3(const Tab32<N> &g) {
+    Tab32<N * 16> t{};
+    for (int e = 0; e < N; ++e)
+        for (uint32_t s = 0; s < 16; ++s) t.v[e * 16 + s] = signed_word(g.v[e], s);
+    return t;
+}
+// Follows g_iq3s: the IQ3_S grid setter rewrites both.
+static __device__ Tab32<512 * 16> g_iq3s_sg = sign_iq3(expand_iq3(vq_iq3s_codes, true));
+
 __device__ __forceinline__ Grids global_grids() {
     Grids g;
     g.iq2xxs = reinterpret_cast<const uint2 *>(g_iq2xxs.v);
