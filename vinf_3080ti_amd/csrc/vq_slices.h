@@ -110,9 +110,17 @@ __device__ __forceinline__ uint32_t sgn(uint32_t g, uint32_t m, uint32_t e) { re
 // v_perm_b32 picks byte k of g or of -g, the bytewise negation (~g) + 0x01010101 (carry-free since no byte of
 // g is 0). The selector puts bit k at bit 2 of byte k (s4 * 0x00810204 moves bit k to bit 8k + 2 without
 // overlap, s4 < 16) over the identity 0x03020100.
+// A 32-bit constant in a VGPR. gfx9 VOP3 instructions take no literal and read at most one SGPR, so without this
+// the compiler splits (a & m) | (b & ~m) into two VOP2 operations; the asm has no side effects, so the move is
+// hoisted out of loops and shared.
+__device__ __forceinline__ uint32_t vconst(uint32_t c) {
+    uint32_t r;
+    asm("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
+    return r;
+}
 __device__ __forceinline__ uint32_t sign4(uint32_t g, uint32_t s4) {
     const uint32_t neg = (g ^ 0xFFFFFFFFu) + 0x01010101u;
-    const uint32_t sel = (__umul24(s4, 0x00810204u) & 0x04040404u) | 0x03020100u;
+    const uint32_t sel = (__umul24(s4, 0x00810204u) & vconst(0x04040404u)) | vconst(0x03020100u);
     return __builtin_amdgcn_perm(neg, g, sel);
 }
 // ggml's 7 stored sign bits with the even-parity 8th at bit 7 (bits above 7 may be set: callers take bits 0-7).
@@ -123,14 +131,17 @@ __device__ __forceinline__ void sign8(uint2 g, uint32_t s8, uint32_t &lo, uint32
     hi = sign4(g.y, bfe(s8, 4, 4));
 }
 
-// IQ4_NL codebook lookup of 4 nibbles (one per byte, 0..15): two v_perm_b32 over the 16 table bytes and a
-// third that picks per byte by bit 3.
-__device__ __forceinline__ uint32_t iq4nl4(uint32_t n) {
+// IQ4_NL codebook lookup of the four nibbles at bits 4s .. 4s + 3 of each byte of q (s = 0: low nibbles, 1: high
+// nibbles): two v_perm_b32 over the 16 table bytes, indexed by the nibbles' low 3 bits, and a third that picks
+// per byte by bit 3 (its selector k + 4 bit3 built with one v_bfi_b32).
+template <int SH>
+__device__ __forceinline__ uint32_t iq4nl4(uint32_t q) {
     constexpr uint32_t t0 = 0xBFAD9881u, t1 = 0xF6EADDCFu, t2 = 0x26190D01u, t3 = 0x71594535u;
-    const uint32_t sel = n & 0x07070707u;
+    const uint32_t sel = (q >> SH) & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
     const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
-    const uint32_t pick = ((n >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t m = vconst(0x04040404u), b = vconst(0x03020100u);
+    const uint32_t pick = (((q >> (SH + 1)) ^ b) & m) ^ b;  // bit 3 of each nibble to bit 2, over k
     return __builtin_amdgcn_perm(hi, lo, pick);
 }
 
@@ -502,8 +513,8 @@ struct Sl<VQ_IQ4_NL> {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t q = __builtin_amdgcn_alignbyte(t[i + 1], t[i], 2);
-            c[0][i] = iq4nl4(q & 0x0F0F0F0Fu);
-            c[1][i] = iq4nl4((q >> 4) & 0x0F0F0F0Fu);
+            c[0][i] = iq4nl4<0>(q);
+            c[1][i] = iq4nl4<4>(q);
         }
     }
     static __device__ __forceinline__ void scales(const W &w, int, float *sc, float *mn) {
@@ -531,8 +542,8 @@ struct Sl<VQ_IQ4_XS> {
     static __device__ __forceinline__ void codes(const W &w, int, const Tabs &, uint32_t (&c)[NP][4]) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            c[0][i] = iq4nl4(w.q[i] & 0x0F0F0F0Fu);
-            c[1][i] = iq4nl4((w.q[i] >> 4) & 0x0F0F0F0Fu);
+            c[0][i] = iq4nl4<0>(w.q[i]);
+            c[1][i] = iq4nl4<4>(w.q[i]);
         }
     }
     static __device__ __forceinline__ void scales(const W &w, int s, float *sc, float *mn) {
