@@ -763,8 +763,9 @@ def main() -> None:
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill contraction legs (512 tokens x Q4_K, both shapes)")
     ap.add_argument("--matvec", default="",
-                    help="only these matvec launches: comma-separated TYPE:ROWS:COLS[:NTOK[:GROUP]] "
-                         "(e.g. IQ2_XXS:5120:17408:1), timed as the per-type legs are")
+                    help="only these matvec launches: comma-separated TYPE:ROWS:COLS[:NTOK[:GROUP[:r]]] "
+                         "(e.g. IQ2_XXS:5120:17408:1), timed as the per-type legs are; r: one vq_qmv call "
+                         "routed with its workspace (the @batch8 legs)")
     ap.add_argument("--libs", default="",
                     help="with --matvec: comma-separated builds of libvq_hip.so compared launch for launch")
     ap.add_argument("--ops-only", action="store_true",
@@ -817,7 +818,10 @@ def main() -> None:
             ty, rows, cols = by_name[f[0]], int(f[1]), int(f[2])
             ntok = int(f[3]) if len(f) > 3 else 1
             group = int(f[4]) if len(f) > 4 else 1
-            r = bench_matvec(torch, hip, ty, rows, cols, ntok, iters=100, group=group)
+            if len(f) > 5 and f[5] == "r":  # routed: one vq_qmv call with its workspace, as a caller gets it
+                r = bench_matvec_routed(torch, hip, ty, rows, cols, ntok, iters=100)
+            else:
+                r = bench_matvec(torch, hip, ty, rows, cols, ntok, iters=100, group=group)
             out[spec] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
             log(f"{spec}: {out[spec]['us']} us, {out[spec]['GBps']} GB/s")
         print(json.dumps({"matvec": out}), flush=True)

@@ -82,8 +82,8 @@ size_t vq_qmv_workspace_bytes(int cols, int ntok);
 
 /* Workspace bytes with which vq_qmv takes its fastest path for this matrix and ntok: for 5..16 tokens of
  * Q3_K/Q4_K/Q5_K/Q6_K (cols a multiple of 256) the f16-MFMA small-batch matvec (its split-K partial sums; 0
- * when cols <= 512), for 6..16 tokens of the other quantized types the int8-MFMA small-batch matvec (packed
- * activations + split-K partial sums), else vq_qmv_workspace_bytes. A smaller (but sufficient) workspace still
+ * when cols <= 512), for 6..16 tokens of the other quantized types the int8-MFMA small-batch matvec (its
+ * split-K partial sums; 0 when the columns are not split), else vq_qmv_workspace_bytes. A smaller (but sufficient) workspace still
  * works and selects the streaming matvec. */
 size_t vq_qmv_workspace_bytes_for(int type, int rows, int cols, int ntok);
 

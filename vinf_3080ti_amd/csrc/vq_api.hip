@@ -439,15 +439,17 @@ static int qmv_route(int type, int rows, int cols, int ntok, bool ws, size_t wsb
         const size_t np = vq::s16_part_bytes(rows, cols, ntok);
         if (np == 0 || (ws && wsb >= np)) return VQ_PATH_MFMA_F16;
     }
-    if (mfma_batch(type, ntok) && ws && wsb >= vq_qmv_workspace_bytes_for(type, rows, cols, ntok))
-        return VQ_PATH_MFMA_I8;
+    if (mfma_batch(type, ntok)) {
+        const size_t np = vq::mfma_part_bytes(rows, cols, ntok);
+        if (np == 0 || (ws && wsb >= np)) return VQ_PATH_MFMA_I8;
+    }
     return VQ_PATH_STREAM;
 }
 
 size_t vq_qmv_workspace_bytes_for(int type, int rows, int cols, int ntok) {
     if (check_matrix(type, rows, cols) || ntok < 1) return 0;
     if (small16_batch(type, cols, ntok)) return vq::s16_part_bytes(rows, cols, ntok);
-    if (mfma_batch(type, ntok)) return align256(vq_xpack_bytes(cols, ntok)) + vq::mfma_part_bytes(rows, cols, ntok);
+    if (mfma_batch(type, ntok)) return vq::mfma_part_bytes(rows, cols, ntok);
     return (type == VQ_F32 || type == VQ_F16) ? 0 : vq_qmv_workspace_bytes(cols, ntok);
 }
 
@@ -533,13 +535,9 @@ int vq_qmv(int type, const uint8_t *w, int rows, int cols, const float *x, int n
         });
     }
     if (path == VQ_PATH_MFMA_I8) {
-        const size_t xpb = align256(vq_xpack_bytes(cols, ntok));
-        st = vq_pack_x(x, ntok, cols, workspace, stream);
-        if (st) return st;
-        const uint8_t *xp = static_cast<const uint8_t *>(workspace);
-        float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + xpb);
+        float *part = vq::mfma_part_bytes(rows, cols, ntok) ? static_cast<float *>(workspace) : nullptr;
         return dispatch_quant(type, [&](auto tc) {
-            return vq::launch_mfma<decltype(tc)::value>(w, rows, cols, rb, xp, ntok, y, part, s);
+            return vq::launch_mfma<decltype(tc)::value>(w, rows, cols, rb, x, ntok, y, part, s);
         });
     }
     const size_t need = vq_qmv_workspace_bytes(cols, ntok);

@@ -53,7 +53,7 @@ struct MfmaX {
 
 template <int T>
 __global__ __launch_bounds__(64 * kMfmaRowWaves) void qmv_mfma_kernel(const uint8_t *__restrict__ w, int rows, int cols,
-                                                                      long row_bytes, const uint8_t *__restrict__ xpack,
+                                                                      long row_bytes, const float *__restrict__ x,
                                                                       int ntok, int kw, float *__restrict__ y,
                                                                       float *__restrict__ part) {
     using S = Sl<T>;
@@ -70,7 +70,6 @@ __global__ __launch_bounds__(64 * kMfmaRowWaves) void qmv_mfma_kernel(const uint
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ng = cols >> 5, nu = ng / UG;
-    const int xb = vq_xpack_stride(cols), xh_off = vq_xpack_h_offset(cols);
     const int k0 = blockIdx.y * kw;                   // first column of this K range
     const int kend = min(k0 + kw, cols);
     const MfmaX xi(kw, ntok);
@@ -106,23 +105,36 @@ __global__ __launch_bounds__(64 * kMfmaRowWaves) void qmv_mfma_kernel(const uint
 #pragma unroll
     for (int p = 0; p < kMfmaPF; ++p)
         if (p < nsteps) load(p, wr[p]);
-    // Activation image of this K range: codes (16-byte chunks), scales, half sums times scale.
-    for (int i = tid; i < ntok * (kw / 16); i += blockDim.x) {
-        const int t = i / (kw / 16), c = 16 * (i % (kw / 16));
-        u32x4 v{0u, 0u, 0u, 0u};
-        if (k0 + c < kend) v = *reinterpret_cast<const u32x4 *>(xpack + static_cast<size_t>(t) * xb + k0 + c);
-        *reinterpret_cast<u32x4 *>(s_dyn + t * xi.stride + c) = v;
-    }
-    for (int i = tid; i < 16 * (kw / 32); i += blockDim.x) {
-        const int g = i / 16, t = i % 16;
-        const int gc = (k0 >> 5) + g;
+    // Activation image of this K range, quantized here from the fp32 input (the CPU path's quantize_group per
+    // 32-group, qwen_cpu.c:607-627, as vq_pack_x does): codes, scales, half sums times scale; zero past the
+    // matrix's last column and for tokens ntok..15.
+    const int ngk = kw >> 5;
+    for (int i = tid; i < 16 * ngk; i += blockDim.x) {
+        const int t = i / ngk, g = i - t * ngk;
+        const int c = k0 + 32 * g;
+        u32x4 q0{0u, 0u, 0u, 0u}, q1{0u, 0u, 0u, 0u};
         float xd = 0.0f, x0 = 0.0f, x1 = 0.0f;
-        if (t < ntok && gc < ng) {
-            const uint8_t *rec = xpack + static_cast<size_t>(t) * xb;
-            xd = reinterpret_cast<const float *>(rec + cols)[gc];
-            const uint32_t h = reinterpret_cast<const uint32_t *>(rec + xh_off)[gc];
-            x0 = static_cast<float>(static_cast<int16_t>(h & 0xFFFFu)) * xd;
-            x1 = static_cast<float>(static_cast<int16_t>(h >> 16)) * xd;
+        if (t < ntok && c < kend) {
+            const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols + c);
+            float v[32];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float4 f = src[k];
+                v[4 * k] = f.x;
+                v[4 * k + 1] = f.y;
+                v[4 * k + 2] = f.z;
+                v[4 * k + 3] = f.w;
+            }
+            const QGroup qg = quantize_group(v);
+            q0 = u32x4{qg.q[0], qg.q[1], qg.q[2], qg.q[3]};
+            q1 = u32x4{qg.q[4], qg.q[5], qg.q[6], qg.q[7]};
+            xd = qg.d;
+            x0 = static_cast<float>(qg.hs0) * xd;
+            x1 = static_cast<float>(qg.hs1) * xd;
+        }
+        if (t < ntok) {
+            *reinterpret_cast<u32x4 *>(s_dyn + t * xi.stride + 32 * g) = q0;
+            *reinterpret_cast<u32x4 *>(s_dyn + t * xi.stride + 32 * g + 16) = q1;
         }
         reinterpret_cast<float *>(s_dyn + xi.xd_off)[g * 16 + t] = xd;
         reinterpret_cast<float *>(s_dyn + xi.xs_off)[(g * 2) * 16 + t] = x0;
@@ -258,7 +270,7 @@ inline size_t mfma_part_bytes(int rows, int cols, int ntok) {
 }
 
 template <int T>
-int launch_mfma(const uint8_t *w, int rows, int cols, long rb, const uint8_t *xpack, int ntok, float *y, float *part,
+int launch_mfma(const uint8_t *w, int rows, int cols, long rb, const float *x, int ntok, float *y, float *part,
                 hipStream_t s) {
     if (ntok < 1 || ntok > 16) return static_cast<int>(hipErrorInvalidValue);
     const int steps = (cols + 255) / 256;
@@ -276,7 +288,7 @@ int launch_mfma(const uint8_t *w, int rows, int cols, long rb, const uint8_t *xp
     const dim3 grid((rows + 16 * kMfmaRowWaves - 1) / (16 * kMfmaRowWaves), nsplit), block(64 * kMfmaRowWaves);
     float *p = nsplit > 1 ? part : nullptr;
     if (nsplit > 1 && part == nullptr) return static_cast<int>(hipErrorInvalidValue);
-    qmv_mfma_kernel<T><<<grid, block, lds, s>>>(w, rows, cols, rb, xpack, ntok, kw, y, p);
+    qmv_mfma_kernel<T><<<grid, block, lds, s>>>(w, rows, cols, rb, x, ntok, kw, y, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     if (nsplit > 1) {

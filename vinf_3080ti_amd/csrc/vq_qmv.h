@@ -75,10 +75,10 @@ int launch_small16_group(int n, const uint8_t *const *w, const int *rows, float 
 template <int T>
 int launch_small16(const uint8_t *w, int rows, int cols, long row_bytes, const float *x, int ntok, float *y,
                    float *part, hipStream_t s);
-// Small-batch (2..16 tokens) matvec on int8 MFMA; `part` holds mfma_part_bytes(rows, cols, ntok) bytes (unused
-// when that is 0).
+// Small-batch (2..16 tokens) matvec on int8 MFMA over fp32 activations (quantized in the kernel); `part` holds
+// mfma_part_bytes(rows, cols, ntok) bytes (unused when that is 0).
 template <int T>
-int launch_mfma(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int ntok, float *y,
+int launch_mfma(const uint8_t *w, int rows, int cols, long row_bytes, const float *x, int ntok, float *y,
                 float *part, hipStream_t s);
 template <int T>
 int launch_partials(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int ntok,
@@ -110,7 +110,7 @@ int set_iq3s_grid(const uint8_t *grid);
                                              const float *, int, float *, hipStream_t);                            \
     KW int vq::launch_small16<T>(const uint8_t *, int, int, long, const float *, int, float *, float *,          \
                                        hipStream_t);                                                               \
-    KW int vq::launch_mfma<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, float *,       \
+    KW int vq::launch_mfma<T>(const uint8_t *, int, int, long, const float *, int, float *, float *,         \
                                     hipStream_t);                                                                \
     KW int vq::launch_partials<T>(const uint8_t *, int, int, long, const uint8_t *, int, int32_t *,          \
                                         hipStream_t);                                                            \
