@@ -81,16 +81,16 @@ size_t vq_xpack_bytes(int cols, int ntok);
 size_t vq_qmv_workspace_bytes(int cols, int ntok);
 
 /* Workspace bytes with which vq_qmv takes its fastest path for this matrix and ntok: for 5..16 tokens of
- * Q3_K/Q4_K/Q5_K/Q6_K (cols a multiple of 256) the f16-MFMA small-batch matvec (its split-K partial sums; 0
- * when cols <= 512), for 6..16 tokens of the other quantized types the int8-MFMA small-batch matvec (its
- * split-K partial sums; 0 when the columns are not split), else vq_qmv_workspace_bytes. A smaller (but sufficient) workspace still
- * works and selects the streaming matvec. */
+ * Q3_K/Q4_K/Q5_K/Q6_K and the IQ types except IQ4_NL (cols a multiple of 256) the f16-MFMA small-batch matvec
+ * (its split-K partial sums; 0 when cols <= 512), for 6..16 tokens of Q2_K, Q8_0 and IQ4_NL the int8-MFMA
+ * small-batch matvec (its split-K partial sums; 0 when the columns are not split), else
+ * vq_qmv_workspace_bytes. A smaller (but sufficient) workspace still works and selects the streaming matvec. */
 size_t vq_qmv_workspace_bytes_for(int type, int rows, int cols, int ntok);
 
 /* Paths of vq_qmv (the values vq_qmv_path returns). */
 #define VQ_PATH_STREAM 0   /* streaming matvec (float weights: their own matvec)                */
 #define VQ_PATH_MFMA_I8 1  /* int8-MFMA small-batch matvec                                      */
-#define VQ_PATH_MFMA_F16 2 /* f16-MFMA small-batch matvec (Q3_K, Q4_K, Q5_K, Q6_K)               */
+#define VQ_PATH_MFMA_F16 2 /* f16-MFMA small-batch matvec (Q3_K..Q6_K, IQ types but IQ4_NL)     */
 
 /* The path vq_qmv takes for this matrix and ntok with a 16-byte aligned workspace of workspace_bytes (0: no
  * workspace), or the negative VQ_ERR_* status of a shape vq_qmv rejects. No counterpart in the reference

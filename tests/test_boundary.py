@@ -106,10 +106,12 @@ def test_qmv_path_routing(lib):
     for ntok, want in ((4, STREAM), (5, F16), (8, F16)):
         assert lib.vq_qmv_path(q3, 17408, 5120, ntok, ws_for(q3, 17408, 5120, ntok)) == want, ntok
     assert lib.vq_qmv_path(q4, 100, 512, 5, 0) == F16  # one K range: no partials, no workspace
-    iq = int(T.IQ4_XS)
-    assert lib.vq_qmv_path(iq, 5120, 17408, 8, ws_for(iq, 5120, 17408, 8)) == I8
+    iq, q2, q8 = int(T.IQ4_XS), int(T.Q2_K), int(T.Q8_0)
+    assert lib.vq_qmv_path(iq, 5120, 17408, 8, ws_for(iq, 5120, 17408, 8)) == F16  # the IQ types too
     assert lib.vq_qmv_path(iq, 5120, 17408, 8, 0) == STREAM
-    assert lib.vq_qmv_path(iq, 5120, 17408, 5, ws_for(iq, 5120, 17408, 5)) == STREAM
+    assert lib.vq_qmv_path(q2, 5120, 17408, 8, ws_for(q2, 5120, 17408, 8)) == I8  # Q2_K, Q8_0, IQ4_NL: int8 MFMA
+    assert lib.vq_qmv_path(q8, 48, 5120, 8, ws_for(q8, 48, 5120, 8)) == I8
+    assert lib.vq_qmv_path(q2, 5120, 17408, 5, ws_for(q2, 5120, 17408, 5)) == STREAM
     assert lib.vq_qmv_path(int(T.F32), 64, 64, 8, 1 << 20) == STREAM
     assert lib.vq_qmv_path(99, 64, 256, 1, 0) == -1
     assert lib.vq_qmv_path(q4, 64, 256, 0, 0) == -2

@@ -448,13 +448,15 @@ def test_qmv_mfma_small_batch_matches_oracle(env, oracle_mod, ty, ntok):
         assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, ntok, t)
 
 
-@pytest.mark.parametrize("ty", [T.Q3_K, T.Q4_K, T.Q5_K, T.Q6_K], ids=lambda t: t.name)
+@pytest.mark.parametrize("ty", [T.Q3_K, T.Q4_K, T.Q5_K, T.Q6_K, T.IQ2_XXS, T.IQ2_XS, T.IQ2_S, T.IQ3_XXS, T.IQ3_S,
+                                T.IQ4_XS], ids=lambda t: t.name)
 @pytest.mark.parametrize("ntok,rows,cols", [(5, 300, 768), (6, 17, 256), (7, 513, 2048), (8, 256, 1280),
                                             (16, 40, 768), (3, 40, 17408), (4, 33, 17408)])
 def test_qmv_small16_matches_oracle(env, oracle_mod, ty, ntok, rows, cols):
-    """The f16-MFMA small-batch matvec (5..16 tokens; 3..4 where the streaming kernel would need two passes):
-    ragged row blocks, a short last K range, one K range without partials, tokens of very different
-    magnitudes (per-token scales), bit-identical on a rerun."""
+    """The f16-MFMA small-batch matvec (5..16 tokens; 3..4 where the streaming kernel would need two passes), for
+    the K-quants and the IQ types (signed codes; IQ3_S and IQ4_XS as two exact f16 terms): ragged row blocks, a
+    short last K range, one K range without partials, tokens of very different magnitudes (per-token scales),
+    bit-identical on a rerun."""
     torch, lib = env
     assert lib.vq_qmv_path(int(ty), rows, cols, ntok, lib.vq_qmv_workspace_bytes_for(int(ty), rows, cols, ntok)) == 2
     rng = np.random.default_rng(9000 + 37 * ntok + rows + int(ty))
@@ -470,7 +472,8 @@ def test_qmv_small16_matches_oracle(env, oracle_mod, ty, ntok, rows, cols):
 
 
 @pytest.mark.parametrize("ty,rows,cols", [(T.Q3_K, 17408, 5120), (T.Q4_K, 5120, 17408), (T.Q6_K, 5120, 6144),
-                                          (T.IQ2_XXS, 5120, 17408), (T.Q8_0, 48, 5120), (T.Q5_K, 1000, 5120)],
+                                          (T.IQ2_XXS, 5120, 17408), (T.IQ4_XS, 5120, 17408), (T.IQ3_S, 5120, 17408),
+                                          (T.Q8_0, 48, 5120), (T.Q2_K, 1000, 5120), (T.Q5_K, 1000, 5120)],
                          ids=lambda v: v.name if isinstance(v, T) else str(v))
 def test_qmv_mfma_baseline_shapes(env, oracle_mod, ty, rows, cols):
     """Split-K (several K ranges summed by the second kernel) at the sweep's shapes, batch 8 and 16."""
@@ -584,7 +587,7 @@ def test_iq3s_grid_setter_reaches_every_path(env, oracle_mod):
     qwen_runtime.cu:1272-1286), including the streaming kernel's pre-signed copy of it. With the grid's
     entries reversed (entry e <- entry 511 - e), the matvec of weights W equals the oracle's (default grid)
     on W with every grid index i replaced by 511 - i (qs bytes and qh bits complemented), at 1 and 2 tokens
-    (pre-signed table), 3 tokens (register signs) and 8 tokens (int8-MFMA small-batch kernel)."""
+    (pre-signed table), 3 tokens (register signs) and 8 tokens (f16-MFMA small-batch kernel, grid in LDS)."""
     torch, lib = env
     rng = np.random.default_rng(353)
     rows, cols = 200, 2048

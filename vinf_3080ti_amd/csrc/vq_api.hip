@@ -420,14 +420,16 @@ size_t vq_qmv_workspace_bytes(int cols, int ntok) {
 constexpr int kMfmaMinTok = 6;
 static bool mfma_batch(int type, int ntok) { return type != VQ_F32 && type != VQ_F16 && ntok >= kMfmaMinTok && ntok <= 16; }
 
-// 5..16 tokens of Q3_K/Q4_K/Q5_K/Q6_K take the f16-MFMA matvec (vq_small16_impl.h) when the workspace holds its
-// K-range partials (none for cols <= 512); below 5 tokens the streaming kernel is faster where it reads the
+// 5..16 tokens of Q3_K..Q6_K and the IQ types but IQ4_NL take the f16-MFMA matvec (vq_small16_impl.h) when the
+// workspace holds its K-range partials (none for cols <= 512); below 5 tokens the streaming kernel is faster where it reads the
 // weights once (measured on MI355X on the SwiGLU block: 2 tokens 49 vs 91 us, 4 tokens 85 vs 96 us, 8 tokens
 // 171 vs 103 us). From 3 tokens on, matrices whose activation image holds fewer tokens than ntok (token_chunk:
 // 2 at 17408 columns), which the streaming kernel would read twice or more, go there too.
 constexpr int kSmall16MinTok = 5, kSmall16MinTokWide = 3;
 static bool small16_batch(int type, int cols, int ntok) {
-    return (type == VQ_Q3_K || type == VQ_Q4_K || type == VQ_Q5_K || type == VQ_Q6_K) && cols % 256 == 0 &&
+    return (type == VQ_Q3_K || type == VQ_Q4_K || type == VQ_Q5_K || type == VQ_Q6_K || type == VQ_IQ2_XXS ||
+            type == VQ_IQ2_XS || type == VQ_IQ2_S || type == VQ_IQ3_XXS || type == VQ_IQ3_S || type == VQ_IQ4_XS) &&
+           cols % 256 == 0 &&
            ntok <= 16 && (ntok >= kSmall16MinTok || (ntok >= kSmall16MinTokWide && ntok > vq::token_chunk(cols)));
 }
 

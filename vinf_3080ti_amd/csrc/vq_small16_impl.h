@@ -1,5 +1,6 @@
 // vq_small16_impl.h -- matvec for a few tokens (1..16: speculative verify, small batches) on f16 MFMA, for the K-quants
-// whose sub-block products fit f16 exactly (Q3_K, Q4_K, Q5_K; Q6_K as two exact terms).
+// whose sub-block products fit f16 exactly (Q3_K, Q4_K, Q5_K; Q6_K as two exact terms) and the IQ types with signed
+// codes (IQ2_XXS/XS/S, IQ3_XXS; IQ3_S and IQ4_XS as two exact terms).
 //
 // Numerics: those of the prefill path (vq_gemm16_impl.h). Each weight element is the integer a = code * sc
 // (exact in f16: |a| <= 128 for Q3_K, 945 for Q4_K, 1953 for Q5_K; Q6_K's |(q - 32) * sc| <= 4096 is split into
@@ -29,8 +30,17 @@
 
 namespace vq {
 
+// IQ types: signed int8 codes (grid magnitude x sign, or the IQ4_NL value) times an integer sub-block scale.
 template <int T>
-constexpr bool kSmall16 = T == VQ_Q3_K || T == VQ_Q4_K || T == VQ_Q5_K || T == VQ_Q6_K;
+constexpr bool kS16Signed = T == VQ_IQ2_XXS || T == VQ_IQ2_XS || T == VQ_IQ2_S || T == VQ_IQ3_XXS || T == VQ_IQ3_S ||
+                            T == VQ_IQ4_XS;
+template <int T>
+constexpr bool kSmall16 = T == VQ_Q3_K || T == VQ_Q4_K || T == VQ_Q5_K || T == VQ_Q6_K || kS16Signed<T>;
+// Types whose element code * scale can exceed f16's exact integers (2048), so it goes in as two exact terms:
+// Q6_K (|q - 32| <= 32, sc <= 127), IQ4_XS (|code| <= 127, |ls - 32| <= 32) and IQ3_S (its grid is replaceable:
+// any magnitude up to 127, scale up to 31). The fixed IQ2 and IQ3_XXS grids stay below 64 (x 31 <= 1953).
+template <int T>
+constexpr bool kS16TwoTerm = T == VQ_Q6_K || T == VQ_IQ4_XS || T == VQ_IQ3_S;
 
 constexpr int kS16Occ = 2;  // waves per SIMD the register budget is set for
 constexpr int kS16Waves = 8, kS16Rows = 16 * kS16Waves, kS16KR = 512, kS16NSB = kS16KR / 256;
@@ -81,6 +91,32 @@ __device__ __forceinline__ void s16_frag(uint32_t c0, uint32_t c1, int isc, g16h
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = (v[i] - off) * s2;  // (code - 4) * (sc - 32): exact, |.| <= 128
         a1 = g16h8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
+    } else if constexpr (kS16Signed<T>) {
+        // signed byte c: 1024 + (c ^ 0x80) - 1152 = c, exact; two terms c * 16 (sc >> 4) + c * (sc & 15) where
+        // the product can leave f16's exact range (|c| <= 128: each term stays within it)
+        const g16h2 off = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+        g16h2 q[4] = {g16_pair(c0 ^ 0x80808080u, 0x04010400u), g16_pair(c0 ^ 0x80808080u, 0x04030402u),
+                      g16_pair(c1 ^ 0x80808080u, 0x04010400u), g16_pair(c1 ^ 0x80808080u, 0x04030402u)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = q[i] - off;
+        if constexpr (kS16TwoTerm<T>) {
+            const _Float16 sh = static_cast<_Float16>(16 * (isc >> 4)), sl = static_cast<_Float16>(isc & 15);
+            const g16h2 h2 = {sh, sh}, l2 = {sl, sl};
+            g16h2 w1[4], w2[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                w1[i] = q[i] * h2;  // multiple of 16, |.| <= 4096: exact
+                w2[i] = q[i] * l2;  // |.| <= 1920: exact
+            }
+            a1 = g16h8{w1[0][0], w1[0][1], w1[1][0], w1[1][1], w1[2][0], w1[2][1], w1[3][0], w1[3][1]};
+            a2 = g16h8{w2[0][0], w2[0][1], w2[1][0], w2[1][1], w2[2][0], w2[2][1], w2[3][0], w2[3][1]};
+        } else {
+            const _Float16 sc = static_cast<_Float16>(isc);
+            const g16h2 s2 = {sc, sc};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = q[i] * s2;  // |.| <= 63 * 31: exact
+            a1 = g16h8{q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
+        }
     } else {  // Q6_K: (q - 32) * sc = (q - 32) * 16 (sc >> 4) + (q - 32) * (sc & 15)
         const g16h2 off = {static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
         const _Float16 sh = static_cast<_Float16>(16 * (isc >> 4)), sl = static_cast<_Float16>(isc & 15);
@@ -117,9 +153,15 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S1
     int *const xsum = reinterpret_cast<int *>(xdg + ntok * (kS16KR / 32));  // [t][KR/32]
     float *const tsc = reinterpret_cast<float *>(xsum + ntok * (kS16KR / 32));  // [16]
 
+    __shared__ uint2 s8[TabSpec<T>::n8 > 0 ? TabSpec<T>::n8 : 1];  // IQ grids (staged before the first barrier)
+    __shared__ uint32_t s4[TabSpec<T>::n4 > 0 ? TabSpec<T>::n4 : 1];
+    __shared__ uint4 sks[1], ssm[1];
+
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lr = lane & 15, lk = lane >> 4;
+    static_assert(!TabSpec<T>::ks && !TabSpec<T>::sm, "sign tables are not staged here");
+    const Tabs tabs = stage_tabs<T>(s8, s4, sks, ssm);
     int jb = 0;
     while (jb + 1 < J.n && static_cast<int>(blockIdx.x) >= J.tile0[jb + 1]) ++jb;
     const uint8_t *const w = J.w[jb];
@@ -228,7 +270,7 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S1
         for (int si = 0; si < SPL; ++si) {
             const int sl = SPL * lk + si;
             uint32_t cd[NP][4];
-            S::codes(wr[sb][si], sl, Tabs{}, cd);
+            S::codes(wr[sb][si], sl, tabs, cd);
             int isc[NP];
             S::iscales(wr[sb][si], sl, isc);
 #pragma unroll
@@ -246,7 +288,7 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S1
                     g16h8 bl = *reinterpret_cast<const g16h8 *>(xl + tb * kS16RowHalves + e);
                     C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bh, C, 0, 0, 0);
                     C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bl, C, 0, 0, 0);
-                    if constexpr (T == VQ_Q6_K) {
+                    if constexpr (kS16TwoTerm<T>) {
                         C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bh, C, 0, 0, 0);
                         C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bl, C, 0, 0, 0);
                     }
