@@ -610,3 +610,27 @@ def test_iq3s_grid_setter_reaches_every_path(env, oracle_mod):
     x = rng.standard_normal((1, cols)).astype(np.float32)
     assert rel_l2(gpu_qmv(torch, lib, T.IQ3_S, w, rows, cols, x, 1),
                   oracle_mod.qmv(int(T.IQ3_S), w, rows, cols, x, 1)) <= REL_L2_TOL
+
+
+def test_iq3s_grid_setter_large_magnitudes(env, oracle_mod):
+    """A replacement IQ3_S grid of the default grid times 8 (magnitudes up to 120, the largest a signed byte code
+    holds after negation): every weight scales by exactly 8, so each path's output is 8 x the oracle's on the
+    default grid. At 8 tokens this drives the f16 small-batch kernel's two-term split (|code x scale| up to
+    3720, beyond f16's exact integers); at 1 token the pre-signed table's negation of bytes >= 64."""
+    torch, lib = env
+    rng = np.random.default_rng(909)
+    rows, cols = 160, 1536
+    w = synth.baseline_rows(T.IQ3_S, rows, cols, rng)
+    grid = np.frombuffer(oracle_mod.table("iq3s_grid"), np.uint8).reshape(512, 4)
+    assert int(grid.max()) * 8 <= 127
+    big = (ctypes.c_uint8 * 2048).from_buffer_copy((grid.astype(np.uint16) * 8).astype(np.uint8).tobytes())
+    assert lib.vq_set_iq3s_grid(ctypes.addressof(big)) == 0
+    try:
+        for ntok, fast in ((1, False), (3, False), (8, True)):
+            x = rng.standard_normal((ntok, cols)).astype(np.float32)
+            got = gpu_qmv(torch, lib, T.IQ3_S, w, rows, cols, x, ntok, fast)
+            ref = 8.0 * oracle_mod.qmv(int(T.IQ3_S), w, rows, cols, x, ntok)
+            assert rel_l2(got, ref) <= REL_L2_TOL, ntok
+    finally:
+        orig = (ctypes.c_uint8 * 2048).from_buffer_copy(grid.tobytes())
+        assert lib.vq_set_iq3s_grid(ctypes.addressof(orig)) == 0
