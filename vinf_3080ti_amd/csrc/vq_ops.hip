@@ -1277,20 +1277,24 @@ __device__ __forceinline__ void st4(_Float16 *p, float4 v) {
 // key head and the wave's 32 v columns, a record of 2 kd + 32 floats) reach LDS by DMA, all in flight at once,
 // and the recurrence then reads them from LDS, so a pass costs one memory round trip per chunk, not per token.
 constexpr int kGdChunk = 16;
+constexpr int kGdWaves = 4;  // waves per column tile of the multi-wave form (kd 128 or 256; 2 measured slower)
 size_t gd_lds_bytes(int kd, int tc) { return (static_cast<size_t>(tc) * (2 * kd + 32) + 256) * sizeof(float); }
 
-template <int R, typename ST, bool FULL>  // FULL: kd == 8 R, every row of every lane is a state row
-__global__ __launch_bounds__(64) void gated_delta4_kernel(const float *__restrict__ conv, const float *__restrict__ braw,
+// NW waves share a column tile and split its rows (wave w: rows 8 R w .. 8 R (w + 1) - 1); their partial sums over
+// rows meet in LDS and are added in wave order (two barriers per token).
+template <int R, typename ST, bool FULL, int NW = 1>  // FULL: kd == 8 R NW, every row of every lane is a state row
+__global__ __launch_bounds__(64 * NW) void gated_delta4_kernel(const float *__restrict__ conv, const float *__restrict__ braw,
                                                           const float *__restrict__ araw, const float *__restrict__ ssm_a,
                                                           const float *__restrict__ dt, ST *__restrict__ state,
                                                           float *__restrict__ out, int key_heads, int value_heads,
                                                           int kd, int vd, float eps, int head_order, SegTable T,
                                                           float *__restrict__ snap, int write_state, int tc) {
     extern __shared__ __align__(16) float gd_in[];  // [tc][2 kd + 32] + 1 KB of slack for the last DMA's spare lanes
-    const int lane = threadIdx.x;
+    __shared__ float4 red_m[NW][8], red_o[NW][8];   // per-wave partial sums of the 8 column quads
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int tiles = (vd + 31) / 32;
     const int h = blockIdx.x / tiles, c0 = (blockIdx.x - h * tiles) * 32;
-    const int col = c0 + 4 * (lane >> 3), r0 = (lane & 7) * R;
+    const int col = c0 + 4 * (lane >> 3), r0 = (wv * 8 + (lane & 7)) * R;
     const bool col_ok = col < vd;  // vd % 4 == 0: a quad is whole or absent
     const int cc = col_ok ? col : 0;
     const int kh = head_order == 0 ? h / (value_heads / key_heads) : h % key_heads;
@@ -1314,7 +1318,7 @@ __global__ __launch_bounds__(64) void gated_delta4_kernel(const float *__restric
         const int nt = min(tc, s.rows - t0);
         __syncthreads();  // the previous chunk's records are consumed
         const int units = nt * rec4;
-        for (int u0 = 0; u0 < units; u0 += 64) {
+        for (int u0 = 64 * wv; u0 < units; u0 += 64 * NW) {
             const int u = min(u0 + lane, units - 1);
             const int tt = u / rec4, w = 4 * (u - tt * rec4);
             const size_t row = static_cast<size_t>(t0 + tt) * cdim;
@@ -1381,10 +1385,19 @@ __global__ __launch_bounds__(64) void gated_delta4_kernel(const float *__restric
                 mem.z = fmaf(st[i].z, kv[i], mem.z);
                 mem.w = fmaf(st[i].w, kv[i], mem.w);
             }
-            const float4 upd{(v.x - gsum8(mem.x) * kscale) * beta * kscale,
-                             (v.y - gsum8(mem.y) * kscale) * beta * kscale,
-                             (v.z - gsum8(mem.z) * kscale) * beta * kscale,
-                             (v.w - gsum8(mem.w) * kscale) * beta * kscale};
+            mem = float4{gsum8(mem.x), gsum8(mem.y), gsum8(mem.z), gsum8(mem.w)};
+            if constexpr (NW > 1) {
+                if ((lane & 7) == 0) red_m[wv][lane >> 3] = mem;
+                __syncthreads();
+                mem = red_m[0][lane >> 3];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) {
+                    const float4 p = red_m[w][lane >> 3];
+                    mem = float4{mem.x + p.x, mem.y + p.y, mem.z + p.z, mem.w + p.w};
+                }
+            }
+            const float4 upd{(v.x - mem.x * kscale) * beta * kscale, (v.y - mem.y * kscale) * beta * kscale,
+                             (v.z - mem.z * kscale) * beta * kscale, (v.w - mem.w * kscale) * beta * kscale};
             float4 o{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int i = 0; i < R; ++i) {
@@ -1395,8 +1408,19 @@ __global__ __launch_bounds__(64) void gated_delta4_kernel(const float *__restric
                 o.z = fmaf(st[i].z, qv[i], o.z);
                 o.w = fmaf(st[i].w, qv[i], o.w);
             }
-            o = float4{gsum8(o.x) * qscale, gsum8(o.y) * qscale, gsum8(o.z) * qscale, gsum8(o.w) * qscale};
-            if ((lane & 7) == 0 && col_ok) *reinterpret_cast<float4 *>(out + (rr * value_heads + h) * vd + col) = o;
+            o = float4{gsum8(o.x), gsum8(o.y), gsum8(o.z), gsum8(o.w)};
+            if constexpr (NW > 1) {
+                if ((lane & 7) == 0) red_o[wv][lane >> 3] = o;
+                __syncthreads();
+                o = red_o[0][lane >> 3];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) {
+                    const float4 p = red_o[w][lane >> 3];
+                    o = float4{o.x + p.x, o.y + p.y, o.z + p.z, o.w + p.w};
+                }
+            }
+            o = float4{o.x * qscale, o.y * qscale, o.z * qscale, o.w * qscale};
+            if (wv == 0 && (lane & 7) == 0 && col_ok) *reinterpret_cast<float4 *>(out + (rr * value_heads + h) * vd + col) = o;
             if (snap != nullptr && t0 + tt + 1 < s.rows && col_ok) {
                 float *sn = snap + (static_cast<size_t>(t0 + tt) * value_heads + h) * hstate;
 #pragma unroll
@@ -1652,6 +1676,16 @@ void gd4_dispatch(int R, dim3 grid, hipStream_t s, const float *conv, const floa
             gated_delta4_kernel<RR, ST, false><<<grid, 64, gd_lds_bytes(kd, tc), s>>>(                               \
                 conv, b, a, ssm_a, dt, state, out, kh, vh, kd, vd, eps, head_order, T, snap, write_state, tc);      \
         break;
+    if (kd == 128 || kd == 256) {  // kGdWaves waves per column tile, each 8 R rows: FULL
+        const dim3 block(64 * kGdWaves);
+        if (kd == 128)
+            gated_delta4_kernel<128 / (8 * kGdWaves), ST, true, kGdWaves><<<grid, block, gd_lds_bytes(kd, tc), s>>>(
+                conv, b, a, ssm_a, dt, state, out, kh, vh, kd, vd, eps, head_order, T, snap, write_state, tc);
+        else
+            gated_delta4_kernel<256 / (8 * kGdWaves), ST, true, kGdWaves><<<grid, block, gd_lds_bytes(kd, tc), s>>>(
+                conv, b, a, ssm_a, dt, state, out, kh, vh, kd, vd, eps, head_order, T, snap, write_state, tc);
+        return;
+    }
     switch (R) { VQ_GD_CASE(4) VQ_GD_CASE(8) VQ_GD_CASE(16) VQ_GD_CASE(32) }
 #undef VQ_GD_CASE
 }
