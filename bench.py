@@ -413,6 +413,22 @@ def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 <
     return out
 
 
+MLP_H, MLP_F = 5120, 17408
+
+
+def mlp_routing(lib, ntok, mfma=None):
+    """(gate+up on vq_qmv_group_ws, down on vq_qmv, workspace bytes) for the MLP block at ntok tokens: per matrix,
+    vq_qmv's own routing with the workspace (an MFMA path) or the grouped streaming launch. mfma forces one."""
+    import ctypes
+
+    H, F = MLP_H, MLP_F
+    nws = max(lib.vq_qmv_group_workspace_bytes(Q3_K, 2, (ctypes.c_int * 2)(F, F), H, ntok),
+              lib.vq_qmv_workspace_bytes_for(Q6_K, H, F, ntok))
+    if mfma is None:
+        return lib.vq_qmv_path(Q3_K, F, H, ntok, nws) > 0, lib.vq_qmv_path(Q6_K, H, F, ntok, nws) > 0, nws
+    return bool(mfma), bool(mfma), nws
+
+
 def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=None):
     """the qwen35 SwiGLU MLP block's three matvecs (gate/up Q3_K 17408x5120, down
     Q6_K 5120x17408) at batch ntok, weights rotating beyond the MALL. mfma=True: vq_qmv with its workspace for
@@ -435,15 +451,8 @@ def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=Non
     import ctypes
 
     rows2 = (ctypes.c_int * 2)(F, F)
-    nws = max(lib.vq_qmv_group_workspace_bytes(Q3_K, 2, rows2, H, ntok),
-              lib.vq_qmv_workspace_bytes_for(Q6_K, H, F, ntok))
+    own_gu, own_d, nws = mlp_routing(lib, ntok, mfma)
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
-    # Per matrix: vq_qmv (its own routing, with the workspace) or the grouped streaming launches.
-    if mfma is None:
-        own_gu = lib.vq_qmv_path(Q3_K, F, H, ntok, nws) > 0
-        own_d = lib.vq_qmv_path(Q6_K, H, F, ntok, nws) > 0
-    else:
-        own_gu = own_d = bool(mfma)
     path = "mfma" if own_gu and own_d else "mixed" if own_gu or own_d else "stream"
 
     def qmv(ty, w, rows, cols, xi, yo):
@@ -475,6 +484,64 @@ def bench_mlp(torch, hip, ntok, iters=20, min_rotation_bytes=640 << 20, mfma=Non
             "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "path": path}
 
 
+def sweep_ops(lib, plan, ntok):
+    """The launch sequence of one sweep step, decided on the host from the plan and vq_qmv's routing queries:
+    ([("pack", cols) | ("mixed", [plan index]) | ("group", [plan index], packed) | ("qmv", i) | ("head", i)],
+    workspace bytes of the ("qmv", i) calls). Per distinct input one pack when it is wider than the in-kernel
+    quantizer takes, then one grouped launch per run of consecutive same-type matrices (<= 4) reading it, a mixed
+    launch for a main type plus Q8_0 or for Q5_K plus Q6_K; the LM head is the fused matvec + argmax."""
+    ops = []
+    i = 0
+    while i < len(plan):
+        name, ty, rows, cols, key = plan[i]
+        if name == "output":
+            ops.append(("head", i))
+            i += 1
+            continue
+        packed = cols > FUSED_QUANT_MAX_COLS
+        if packed:
+            ops.append(("pack", cols))
+        j = i
+        while j < len(plan) and plan[j][4] == key:
+            run = [k for k in range(j, min(j + 4, len(plan))) if plan[k][4] == key]
+            tys = {plan[k][1] for k in run}
+            if len(tys) > 1 and not packed and (len(tys - {Q8_0}) == 1 or tys == {Q5_K, Q6_K}):
+                ops.append(("mixed", run))
+                j = run[-1] + 1
+                continue
+            k = j
+            while k < len(plan) and k - j < 4 and plan[k][4] == key and plan[k][1] == ty and plan[k][3] == cols:
+                k += 1
+            ops.append(("group", list(range(j, k)), packed))
+            j = k
+            if j < len(plan):
+                ty, cols = plan[j][1], plan[j][3]
+        i = j
+    # Several tokens: matrices for which vq_qmv takes an MFMA path (e.g. 3..4 tokens over the 17408-wide FFN
+    # down input, which the streaming kernel reads twice) leave their group for a vq_qmv call of their own.
+    nws = 0
+    if ntok > 1:
+        routed = []
+        for op in ops:
+            if op[0] != "group" or op[2]:
+                routed.append(op)
+                continue
+            keep, own = [], []
+            for i in op[1]:
+                _, ty_i, rows_i, cols_i, _ = plan[i]
+                need = lib.vq_qmv_workspace_bytes_for(ty_i, rows_i, cols_i, ntok)
+                if lib.vq_qmv_path(ty_i, rows_i, cols_i, ntok, need) > 0:
+                    own.append(i)
+                    nws = max(nws, need)
+                else:
+                    keep.append(i)
+            if keep:
+                routed.append(("group", keep, False))
+            routed.extend(("qmv", i) for i in own)
+        ops = routed
+    return ops, nws
+
+
 class Sweep:
     """All weights of one 27B decode step resident in HBM, plus the per-step launch sequence."""
 
@@ -489,64 +556,13 @@ class Sweep:
         self.xp = hip.xpack(maxc, ntok)
         self.ys = {}  # one output per matrix shape of a group position (outputs are not consumed)
         self.ids = torch.empty(ntok, dtype=torch.int32, device="cuda")
-        # Launch sequence: per distinct input one pack, then one grouped matvec per run of consecutive
-        # same-type matrices (<= 4) reading it; the LM head is the fused matvec + argmax.
-        self.ops = []
-        i = 0
-        while i < len(self.plan):
-            name, ty, rows, cols, key = self.plan[i]
-            if name == "output":
-                nws = hip.lib.vq_lmhead_argmax_workspace_bytes(ty, rows, cols, ntok)
-                self.head_ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
-                self.ops.append(("head", i))
-                i += 1
-                continue
-            packed = cols > FUSED_QUANT_MAX_COLS
-            if packed:
-                self.ops.append(("pack", cols))
-            j = i
-            while j < len(self.plan) and self.plan[j][4] == key:
-                run = [k for k in range(j, min(j + 4, len(self.plan))) if self.plan[k][4] == key]
-                tys = {self.plan[k][1] for k in run}
-                if len(tys) > 1 and not packed and (len(tys - {Q8_0}) == 1 or tys == {Q5_K, Q6_K}):
-                    # A main type and Q8_0 small tensors, or Q5_K and Q6_K, reading one input: one mixed launch.
-                    self.ops.append(("mixed", run))
-                    j = run[-1] + 1
-                    continue
-                k = j
-                while (k < len(self.plan) and k - j < 4 and self.plan[k][4] == key and self.plan[k][1] == ty
-                       and self.plan[k][3] == cols):
-                    k += 1
-                self.ops.append(("group", list(range(j, k)), packed))
-                j = k
-                if j < len(self.plan):
-                    ty, cols = self.plan[j][1], self.plan[j][3]
-            i = j
-        # Several tokens: matrices for which vq_qmv takes an MFMA path (e.g. 3..4 tokens over the 17408-wide FFN
-        # down input, which the streaming kernel reads twice) leave their group for a vq_qmv call of their own.
-        lib = hip.lib
-        self.qmv_ws = None
-        if ntok > 1:
-            ops, nws = [], 0
-            for op in self.ops:
-                if op[0] != "group" or op[2]:
-                    ops.append(op)
-                    continue
-                keep, own = [], []
-                for i in op[1]:
-                    _, ty_i, rows_i, cols_i, _ = self.plan[i]
-                    need = lib.vq_qmv_workspace_bytes_for(ty_i, rows_i, cols_i, ntok)
-                    if lib.vq_qmv_path(ty_i, rows_i, cols_i, ntok, need) > 0:
-                        own.append(i)
-                        nws = max(nws, need)
-                    else:
-                        keep.append(i)
-                if keep:
-                    ops.append(("group", keep, False))
-                ops.extend(("qmv", i) for i in own)
-            self.ops = ops
-            if nws:
-                self.qmv_ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+        self.ops, nws = sweep_ops(hip.lib, self.plan, ntok)
+        for op in self.ops:
+            if op[0] == "head":
+                _, ty, rows, cols, _ = self.plan[op[1]]
+                nh = hip.lib.vq_lmhead_argmax_workspace_bytes(ty, rows, cols, ntok)
+                self.head_ws = torch.empty(nh, dtype=torch.uint8, device="cuda")
+        self.qmv_ws = torch.empty(nws, dtype=torch.uint8, device="cuda") if nws else None
         for _, _, rows, _, _ in self.plan:
             self.ys.setdefault(rows, torch.empty(ntok, rows, device="cuda"))
         self.launches = sum(2 if op[0] in ("head", "qmv") else 1 for op in self.ops)  # qmv: matvec + range sums

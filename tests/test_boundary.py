@@ -144,3 +144,23 @@ def test_product_does_not_import_oracle():
     for path in (ROOT / "vinf_3080ti_amd").rglob("*.py"):
         text = path.read_text()
         assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", text, re.M), path
+
+
+# Every runtime method the reference's executor calls on a model whose weights are all resident: the
+# QwenGpuExecutor in src/vinf/qwen_gpu.py (load path :575-630 incl. the dynamic weight groups, stats :673,833,
+# decode :1263-1286, forward passes) and the backend's stats in src/vinf/qwen_backend.py. A missing name makes
+# QwenGpuExecutor(..., runtime=HipWeightRuntime()) fail with AttributeError.
+EXECUTOR_RUNTIME_CALLS = (
+    "add add_weight_group alloc argmax argmax_rows attention attention_seg buffer_bytes concat_rows conv_update "
+    "conv_update_seg copy demote_group device_bytes gated_delta gated_delta_seg gated_rmsnorm kv_append "
+    "kv_append_seg map_cost map_range mem_info promote_group qmv read read_floats reserve_ring rmsnorm rope "
+    "rope_seg set_arena set_paging set_segments set_stream_order set_weight_space sigmoid_mul silu_mul "
+    "split_gated_q staging_bytes streamed_bytes unmap_range upload_gguf_tensor vmm_granularity vram_bytes "
+    "weight_groups write zero_range pinned_bytes synchronize"
+).split()
+
+
+def test_hip_weight_runtime_has_every_executor_call():
+    missing = [n for n in EXECUTOR_RUNTIME_CALLS
+               if not (hasattr(runtime.HipWeightRuntime, n) or hasattr(runtime.Runtime, n))]
+    assert missing == []

@@ -455,3 +455,82 @@ def test_gated_delta_matches_oracle(rt, oracle_mod, head_order):
         rt.gated_delta("gc", "gb", "ga", "gda", "gdt", "gs", "go", 3, vh, kd, vd, 1e-6, head_order, ntok)
     rt.free("gda")
     rt.free("gdt")
+
+
+def test_executor_load_path_with_arena_groups_and_stream_order(oracle_mod):
+    """The calls QwenGpuExecutor._load_weights makes on an all-resident model (src/vinf/qwen_gpu.py:575-630):
+    weight groups, the arena, uploads into each, the stream order, and the byte counters of :673,833,1263
+    (qwen_runtime.cu:1436-1811). Every tensor must still multiply correctly from wherever it was carved."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from vinf_3080ti_amd.runtime import HipWeightRuntime
+
+    rt = HipWeightRuntime()
+    rows, cols = 40, 512
+    rng = np.random.default_rng(604)
+    mats = {n: (ty, synth.synthetic_rows(ty, rows, cols, rng)) for n, ty in
+            (("g.a", T.Q4_K), ("g.b", T.Q6_K), ("s.a", T.Q3_K), ("s.b", T.Q8_0), ("p.a", T.IQ4_XS))}
+    padded = {n: (w.nbytes + 16 + 255) // 256 * 256 for n, (_, w) in mats.items()}
+    gran = rt.vmm_granularity()
+    with pytest.raises(RuntimeError):
+        rt.add_weight_group(gran)  # before set_weight_space
+    rt.set_weight_space(2 * gran)
+    gid = rt.add_weight_group(padded["g.a"] + padded["g.b"])
+    with pytest.raises(ValueError):
+        rt.add_weight_group(2 * gran)  # exhausted
+    rt.set_arena(padded["s.a"])  # room for s.a only: s.b falls back to its own allocation
+    for n in ("g.a", "g.b"):
+        rt.upload(n, mats[n][1].tobytes(), int(mats[n][0]), cols, rows, True, gid)
+    for n in ("s.a", "s.b"):
+        rt.upload_raw(n, mats[n][1].tobytes(), mats[n][0], cols, rows)
+    rt.upload_raw("p.a", mats["p.a"][1].tobytes(), T.IQ4_XS, cols, rows, resident=False)
+    big = synth.synthetic_rows(T.Q8_0, 4096, cols, rng)  # 2.2 MB: more than the rest of the 2 MiB group
+    with pytest.raises(ValueError):
+        rt.upload("g.c", big.tobytes(), int(T.Q8_0), cols, 4096, True, gid)  # group full
+    with pytest.raises(ValueError):
+        rt.upload("g.c", mats["g.a"][1].tobytes(), int(T.Q4_K), cols, rows, True, gid + 1)  # unknown group
+    with pytest.raises(RuntimeError):
+        rt.set_arena(1 << 20)  # s.a lives in it
+
+    x = rng.standard_normal((2, cols)).astype(np.float32)
+    rt.alloc("x", 2 * cols)
+    rt.alloc("y", 2 * rows)
+    rt.write_floats("x", x.reshape(-1))
+    for n, (ty, w) in mats.items():
+        rt.qmv(n, "x", "y", 2)
+        got = np.array(rt.read_floats("y"), np.float32).reshape(2, rows)
+        assert rel_l2(got, oracle_mod.qmv(int(ty), w, rows, cols, x, 2)) <= 1e-5, n
+
+    rt.set_stream_order(["p.a"], 3)
+    rt.set_stream_order([], 0)
+    with pytest.raises(ValueError):
+        rt.set_stream_order(["s.a"], 3)  # resident tensors do not stream
+    with pytest.raises(ValueError):
+        rt.set_stream_order(["p.a", "p.a"], 3)
+    with pytest.raises(ValueError):
+        rt.set_stream_order(["nope"], 3)
+    rt.reserve_ring(1 << 20, 3)
+
+    groups = rt.weight_groups()
+    assert groups == [(gran, True, ["g.a", "g.b"])]
+    assert rt.promote_group(gid) is True
+    with pytest.raises(RuntimeError):
+        rt.demote_group(gid)
+    with pytest.raises(ValueError):
+        rt.promote_group(gid + 1)
+    assert rt.staging_bytes() == rt.pinned_bytes() == rt.streamed_bytes() == 0
+    assert rt.buffer_bytes() == 4 * (2 * cols + 2 * rows)
+    own = padded["s.b"] + padded["p.a"]
+    assert rt.vram_bytes() >= gran + padded["s.a"] + own + rt.buffer_bytes()
+    assert rt.device_bytes() == sum(w.nbytes for _, w in mats.values())
+
+    rt.alloc("kv", 4096, 2, True)  # a "virtual" buffer is backed in full
+    assert rt.map_cost("kv", 0, 4096) == 0
+    assert rt.map_range("kv", 1024, 1024) is True
+    rt.unmap_range("kv", 1024, 1024)
+    with pytest.raises(ValueError):
+        rt.map_range("kv", 4000, 200)
+    for n in mats:
+        rt.free(n)
+    rt.set_arena(0)

@@ -90,6 +90,10 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     if _lib is not None and path is None:
         return _lib
     p = Path(path or os.environ.get("VQ_LIB_PATH") or LIB)
+    # torch ships its own HIP runtime; it has to be the process's one before libvq_hip.so resolves its HIP
+    # symbols, or the library and torch see two runtimes (vq_init then reports no device).
+    import torch  # noqa: F401
+
     if not p.exists():
         raise LibraryUnavailableError(f"{p} is not built; run `python -m vinf_3080ti_amd.build`")
     try:

@@ -14,13 +14,13 @@ bad shapes/sizes/types, TypeError for an fp16 buffer where fp32 is needed, Runti
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
-
-import struct
-from array import array
+import math
 from dataclasses import dataclass
 from typing import Sequence
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -39,6 +39,28 @@ class _Tensor:
     cols: int
     row_bytes: int
     nbytes: int
+    home: str = "own"  # where the bytes live: "own" allocation, "arena", or "group:<id>"
+    streamed: bool = False  # uploaded with resident=False (served from HBM all the same)
+
+
+@dataclass
+class _Region:
+    """A device allocation that resident uploads are carved from (the weight arena, or one weight group)."""
+
+    data: torch.Tensor  # uint8
+    used: int = 0
+    names: list[str] | None = None
+
+    def carve(self, padded: int) -> torch.Tensor | None:
+        if self.used + padded > self.data.numel():
+            return None
+        view = self.data[self.used : self.used + padded]
+        self.used += padded
+        return view
+
+
+# Granule that weight-group sizes are rounded to (the reference rounds to its VMM granularity).
+WEIGHT_GRANULE = 2 << 20
 
 
 @dataclass
@@ -93,6 +115,12 @@ class Runtime:
         self.batch_invariant = False
         self._paging: tuple[torch.Tensor, int, int, int] | None = None
         self._segments: list[tuple[int, int, int, int]] = []
+        # Resident-weight memory: an optional arena and the executor's per-layer weight groups. Nothing streams
+        # over PCIe here, so the stream order only records which uploads were requested as streamed.
+        self._arena: _Region | None = None
+        self._weight_space: int | None = None
+        self._groups: list[_Region] = []
+        self._stream_order: list[str] = []
 
     # ---- helpers ----------------------------------------------------------------------------------
     def _stream(self) -> int:
@@ -129,21 +157,34 @@ class Runtime:
     def upload(self, name: str, data, type_id: int, cols: int, rows: int, resident: bool = True, group: int = -1) -> None:
         """Copy raw GGUF blocks to the device (Runtime_upload, qwen_runtime.cu:1338-1409).
 
-        Every tensor is resident in HBM: `resident=False` (pinned-host streaming on the 12 GB card) is
-        accepted and ignored. Weight groups (CUDA VMM regions) do not exist here: group >= 0 is rejected.
+        Every tensor is resident in HBM: `resident=False` (pinned-host streaming on the 12 GB card) is recorded
+        (set_stream_order accepts such names) but the bytes go to HBM all the same. group >= 0 places the tensor
+        in that weight group's allocation, else the arena (set_arena) while it has room, else its own allocation.
         """
-        if group >= 0:
+        if group >= 0 and group >= len(self._groups):
             raise ValueError(f"unknown weight group {group}")
         # The views are released on every exit: a caller's mapping (upload_gguf_tensor) can then be closed
         # even when this raises.
         with memoryview(data) as src, src.cast("B") as view:
             row_bytes, nbytes = _check_upload_args(name, view.nbytes, int(type_id), int(cols), int(rows))
             host = torch.frombuffer(bytearray(view), dtype=torch.uint8)
-        self.tensors.pop(name, None)
         padded = (nbytes + 16 + _PAD - 1) // _PAD * _PAD
-        dev = torch.zeros(padded, dtype=torch.uint8, device=self.device)
+        dev, home = None, "own"
+        if group >= 0:
+            dev, home = self._groups[group].carve(padded), f"group:{group}"
+            if dev is None:
+                raise ValueError(f"weight group {group} has no room for {name}")
+            self._groups[group].names.append(name)
+        elif self._arena is not None:
+            dev = self._arena.carve(padded)
+            home = "arena" if dev is not None else "own"
+        if dev is None:
+            dev = torch.empty(padded, dtype=torch.uint8, device=self.device)
+        self.tensors.pop(name, None)
+        dev[nbytes:].zero_()
         dev[:nbytes].copy_(host)
-        self.tensors[name] = _Tensor(dev, int(type_id), int(rows), int(cols), row_bytes, nbytes)
+        self.tensors[name] = _Tensor(dev, int(type_id), int(rows), int(cols), row_bytes, nbytes, home,
+                                     streamed=not resident)
 
     def upload_device(self, name: str, data: torch.Tensor, type_id: int, cols: int, rows: int) -> None:
         """Register device-resident raw blocks (uint8 tensor of >= nbytes + 16 bytes) without a host copy."""
@@ -173,6 +214,121 @@ class Runtime:
 
     def device_bytes(self) -> int:
         return sum(t.nbytes for t in self.tensors.values())
+
+    # ---- resident-weight memory (the executor's load path) -----------------------------------------------
+    # The reference plans weights for a 12 GB card: an arena for resident tensors, VMM weight groups that can be
+    # demoted to pinned host memory, a ring that streams the rest over PCIe (qwen_runtime.cu:1436-1810). On one
+    # MI355X (288 GB) the whole model stays in HBM, so these calls keep their meaning for resident weights and
+    # report zero for everything that would stream.
+    def set_arena(self, nbytes: int) -> None:
+        """One allocation that later resident uploads are carved from, 256-byte aligned (qwen_runtime.cu:1486-1500).
+        RuntimeError while a tensor lives in the current arena; 0 drops it."""
+        busy = next((n for n, t in self.tensors.items() if t.home == "arena"), None)
+        if busy is not None:
+            raise RuntimeError(f"arena is in use by {busy}")
+        self._arena = None
+        if nbytes > 0:
+            self._arena = _Region(torch.empty(int(nbytes), dtype=torch.uint8, device=self.device))
+
+    def vmm_granularity(self) -> int:
+        return WEIGHT_GRANULE
+
+    def set_weight_space(self, nbytes: int) -> None:
+        """Capacity of the weight groups added next (qwen_runtime.cu:1713-1726)."""
+        if self._groups:
+            raise RuntimeError("weight space in use")
+        self._weight_space = int(nbytes)
+
+    def add_weight_group(self, nbytes: int) -> int:
+        """A device allocation of nbytes rounded up to the granule, for one layer's tensors; returns its id
+        (qwen_runtime.cu:1728-1744)."""
+        if self._weight_space is None:
+            raise RuntimeError("set_weight_space first")
+        size = -(-int(nbytes) // WEIGHT_GRANULE) * WEIGHT_GRANULE
+        if sum(g.data.numel() for g in self._groups) + size > self._weight_space:
+            raise ValueError("weight space exhausted")
+        self._groups.append(_Region(torch.empty(size, dtype=torch.uint8, device=self.device), names=[]))
+        return len(self._groups) - 1
+
+    def weight_groups(self) -> list[tuple[int, bool, list[str]]]:
+        """[(bytes, mapped, tensor names)] per group (qwen_runtime.cu:1794-1811); every group stays mapped."""
+        return [(g.data.numel(), True, list(g.names)) for g in self._groups]
+
+    def _group_id(self, gid: int) -> int:
+        if not 0 <= gid < len(self._groups):
+            raise ValueError(f"unknown weight group {gid}")
+        return gid
+
+    def demote_group(self, gid: int) -> None:
+        """Moving a group to pinned host memory (qwen_runtime.cu:1746-1770) is PCIe streaming, which this
+        runtime does not do: every weight stays in HBM. Raises RuntimeError for a known group."""
+        self._group_id(gid)
+        raise RuntimeError("demote_group: weights stay resident in HBM (no host streaming on this runtime)")
+
+    def promote_group(self, gid: int) -> bool:
+        """Groups are never demoted, so each one is already resident (qwen_runtime.cu:1772-1792)."""
+        self._group_id(gid)
+        return True
+
+    def set_stream_order(self, names, slots: int) -> None:
+        """Order of the streamed tensors (qwen_runtime.cu:1523-1593). Each name must be a tensor uploaded with
+        resident=False (ValueError otherwise, or when it repeats); those are in HBM here, so no ring is built."""
+        if isinstance(names, (str, bytes)) or not hasattr(names, "__iter__"):
+            raise TypeError("names must be a sequence of str")
+        order: list[str] = []
+        for n in names:
+            if not isinstance(n, str):
+                raise TypeError("names must be a sequence of str")
+            t = self.tensors.get(n)
+            if t is None or not t.streamed:
+                raise ValueError(f"{n} is not a loaded streamed tensor")
+            if n in order:
+                raise ValueError(f"{n} appears twice in the stream order")
+            order.append(n)
+        self._stream_order = order
+
+    def reserve_ring(self, slot_bytes: int, slots: int) -> None:
+        """Ring slots for streamed weights (qwen_runtime.cu:1595-1614): none are needed, nothing streams."""
+        if slot_bytes < 0 or slots < 0:
+            raise ValueError("reserve_ring sizes must be >= 0")
+
+    def vram_bytes(self) -> int:
+        """Device memory this runtime holds: arena, weight groups, tensors in their own allocations, buffers and
+        the matvec workspace (qwen_runtime.cu:1436-1446)."""
+        total = sum(g.data.numel() for g in self._groups)
+        total += self._arena.data.numel() if self._arena is not None else 0
+        total += sum(t.data.numel() for t in self.tensors.values() if t.home == "own")
+        return total + self.buffer_bytes() + self._ws.numel()
+
+    def buffer_bytes(self) -> int:
+        return sum(b.data.numel() * b.elem for b in self.buffers.values())
+
+    def staging_bytes(self) -> int:
+        return 0  # no staging buffers or ring slots
+
+    def pinned_bytes(self) -> int:
+        return 0  # no tensor lives in host memory
+
+    def streamed_bytes(self) -> int:
+        return 0  # nothing crosses PCIe on the matvec path
+
+    def map_range(self, name: str, offset: int, n: int) -> bool:
+        """Buffers are backed in full when allocated (alloc's virtual flag reserves nothing lazily), so every
+        in-bounds range is mapped (qwen_runtime.cu:1671-1680)."""
+        self._range_check(name, offset, n, "map_range")
+        return True
+
+    def unmap_range(self, name: str, offset: int, n: int) -> None:
+        self._range_check(name, offset, n, "unmap_range")
+
+    def map_cost(self, name: str, offset: int, n: int) -> int:
+        self._any_buffer(name)
+        return 0
+
+    def _range_check(self, name: str, offset: int, n: int, what: str) -> None:
+        b = self._any_buffer(name)
+        if offset < 0 or n < 0 or offset + n > b.data.numel():
+            raise ValueError(f"{what} out of bounds")
 
     def tensor_info(self, name: str) -> tuple[int, int, int, int, int, int, bool]:
         """(device_address, gguf_type, rows, cols, row_bytes, nbytes, resident) (qwen_runtime.cu:1460-1473)."""
@@ -771,66 +927,54 @@ def iq3s_grid_bytes() -> bytes:
 
 
 class HipWeightRuntime:
-    """Drop-in for CudaWeightRuntime (src/vinf/cuda/qwen_runtime.py:47-116) on the matvec path."""
+    """Drop-in for CudaWeightRuntime (src/vinf/cuda/qwen_runtime.py:47-116): the executor's `runtime=` object.
+
+    It owns a `Runtime` built with the IQ3_S codebook and adds the host-list conveniences the executor uses
+    (float lists in and out, GGUF uploads); every other attribute is the `Runtime` method of the same name.
+    """
 
     def __init__(self, device: int | None = None) -> None:
         self._rt = Runtime(iq3s_grid_bytes(), device)
 
-    def mem_info(self) -> tuple[int, int]:
-        return self._rt.mem_info()
-
-    def device_bytes(self) -> int:
-        return self._rt.device_bytes()
-
-    def has(self, name: str) -> bool:
-        return self._rt.has(name)
-
-    def free(self, name: str) -> None:
-        self._rt.free(name)
-
     def upload_gguf_tensor(self, gguf, name: str, *, device_name: str | None = None, resident: bool = True,
                            group: int = -1) -> int:
-        """Upload one tensor's raw blocks straight from the file's mapping (cuda/qwen_runtime.py:68-86): cols is
-        the innermost GGUF dimension, rows the product of the others; returns the tensor's byte size. Types
-        without a HIP matvec raise UnsupportedModelError. `gguf` is a GGUFFile (vinf_3080ti_amd.gguf)."""
+        """Upload one tensor's raw blocks from the file mapping (cuda/qwen_runtime.py:68-86) and return its
+        byte size. The innermost GGUF dimension is the row length; the outer ones multiply into the row count.
+        A type without a HIP matvec raises UnsupportedModelError before anything is mapped."""
         from .gguf import UnsupportedModelError
 
         info = gguf.tensors[name]
-        if int(info.tensor_type) not in HIP_MATVEC_TYPES:
-            raise UnsupportedModelError(f"{name}: no HIP matvec for {info.tensor_type.name}")
-        cols = info.dimensions[0]
-        rows = 1
-        for d in info.dimensions[1:]:
-            rows *= d
-        f, mm, view = gguf.mmap_tensor(name)
-        try:
-            self._rt.upload(device_name or name, view, int(info.tensor_type), cols, rows, resident, group)
-        finally:
-            view.release()
-            mm.close()
-            f.close()
+        kind = info.tensor_type
+        if int(kind) not in HIP_MATVEC_TYPES:
+            raise UnsupportedModelError(f"{name}: no HIP matvec for {kind.name}")
+        row_len, *outer = info.dimensions
+        with contextlib.ExitStack() as cleanup:
+            handle, mapping, view = gguf.mmap_tensor(name)
+            # Unwound last-in first-out: the view is released before its mapping and file are closed.
+            cleanup.callback(handle.close)
+            cleanup.callback(mapping.close)
+            cleanup.callback(view.release)
+            self._rt.upload(device_name or name, view, int(kind), row_len, math.prod(outer), resident, group)
         return info.nbytes
 
-    def upload_raw(self, name: str, data, tensor_type: GGUFTensorType, cols: int, rows: int, *, resident: bool = True) -> None:
+    def upload_raw(self, name: str, data, tensor_type: GGUFTensorType, cols: int, rows: int, *,
+                   resident: bool = True) -> None:
         if int(tensor_type) not in HIP_MATVEC_TYPES:
             raise ValueError(f"{name}: no HIP matvec for type {int(tensor_type)}")
         self._rt.upload(name, data, int(tensor_type), cols, rows, resident)
 
     def matvec(self, name: str, values: Sequence[float]) -> list[float]:
-        out = array("f")
-        out.frombytes(self._rt.matvec(name, array("f", values).tobytes()))
-        return out.tolist()
+        """Synchronous W @ values for one host vector, as a list of Python floats."""
+        packed = np.ascontiguousarray(values, dtype="<f4").tobytes()
+        return np.frombuffer(self._rt.matvec(name, packed), dtype="<f4").tolist()
 
     def read_floats(self, name: str, n: int = -1, offset: int = 0) -> list[float]:
-        data = self._rt.read(name, n, offset)
-        if self._rt.buffer_elem(name) == 2:
-            return list(struct.unpack(f"<{len(data) // 2}e", data))
-        out = array("f")
-        out.frombytes(data)
-        return out.tolist()
+        """A buffer's elements as Python floats; fp16 buffers (KV caches) are widened exactly."""
+        width = "<f2" if self._rt.buffer_elem(name) == 2 else "<f4"
+        return np.frombuffer(self._rt.read(name, n, offset), dtype=width).tolist()
 
     def write_floats(self, name: str, values, offset: int = 0) -> None:
-        self._rt.write(name, array("f", values).tobytes(), offset)
+        self._rt.write(name, np.ascontiguousarray(values, dtype="<f4").tobytes(), offset)
 
     def __getattr__(self, name: str):
         return getattr(self._rt, name)
