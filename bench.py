@@ -10,7 +10,7 @@ vq_lmhead_argmax for the LM head.
 
 Also reported: per-quant-type matvec throughput at 5120x17408 (configs[0..2] shapes, rotating over weight
 copies larger than the 256 MB MALL), the roofline of the dominant kernel (HIP events on its stream), and
-the reference CPU path timed on a bounded sample on this host.
+the reference CPU path (its bit-identical C restatement) timed on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ntok 1] [--no-graph] [--no-cpu]
 """
@@ -648,44 +648,55 @@ def host_cpu() -> dict:
 CPU_SHARE = 16  # host CPUs one GPU's share of the box may keep busy
 
 
-def cpu_child(threads: int) -> dict:
-    """Runs in a child process without torch (OMP_PROC_BIND is fixed when OpenMP starts): the reference's own
-    CPU path (oracle/_ref, compiled from qwen_cpu.c; the C restatement in oracle/ when it is absent) on
-    BASELINE.json configs 1-3 (median of 10 timed calls after one warm-up call each) and on a sample of the
-    27B sweep (each distinct matrix shape, median of 3 calls; the LM head on 1/16 of its rows, scaled)."""
-    import glob
-    import importlib.util
+def host_ram_bytes() -> int:
+    try:
+        return os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PHYS_PAGES")
+    except (ValueError, OSError):
+        return 0
+
+
+FULL_SWEEP_MIN_RAM = 32 << 30  # the full config-4 sweep holds 13.4 GiB of weights in host memory
+
+
+def fast_baseline_rows(ty, rows, cols, rng, base):
+    """synth.baseline_rows' distribution at memory speed for the 13.4 GiB CPU sweep: the block bytes are a
+    16 MiB random block XORed with a per-chunk constant (a bijection per byte, so each byte stays uniform and
+    every matrix occupies distinct memory), then every fp16 scale field is set to fp16(|N(0, 1e-3)|)."""
+    import numpy as np
+
+    from vinf_3080ti_amd.gguf_types import F16_FIELDS, GGUFTensorType, traits
+
+    bs, ts = traits(ty)
+    nblk = rows * cols // bs
+    n64 = -(-nblk * ts // 8)
+    out = np.empty(n64, np.uint64)
+    salt = int(rng.integers(1, 2**62))
+    for k in range(0, n64, base.size):
+        m = min(base.size, n64 - k)
+        np.bitwise_xor(base[:m], np.uint64((salt + k * 0x9E3779B97F4A7C15) % 2**64), out=out[k : k + m])
+    blocks = out.view(np.uint8)[: nblk * ts].reshape(nblk, ts)
+    for off in F16_FIELDS[GGUFTensorType(ty)]:
+        d = np.abs(rng.normal(0.0, 1e-3, nblk)).astype("<f2")
+        blocks[:, off : off + 2] = d.view(np.uint8).reshape(nblk, 2)
+    return blocks.reshape(-1)
+
+
+def cpu_child(threads: int, full_sweep: bool) -> dict:
+    """Runs in a child process without torch (OMP_PROC_BIND is fixed when OpenMP starts): the reference CPU
+    path as this repository's C restatement (oracle/vq_oracle.c: the reference's Cpu_qmv, qwen_cpu.c:581-641,
+    bit-identical to it, tests/test_oracle.py) on BASELINE.json configs 1-3 (median of 10 timed calls after one
+    warm-up call each) and on config 4: the full 27B sweep (every matrix of the step, 13.4 GiB of distinct
+    host memory, one warm-up pass and one timed pass) when full_sweep, else each distinct matrix shape (median
+    of 3 calls; the LM head on 1/16 of its rows, scaled) weighted by its per-step count."""
     import statistics
 
     import numpy as np
 
-    from vinf_3080ti_amd import synth, tables
+    from oracle import oracle
+    from vinf_3080ti_amd import synth
 
-    paths = glob.glob(str(ROOT / "oracle" / "_ref" / "_cpu_qwen*.so"))
-    if paths:
-        spec = importlib.util.spec_from_file_location("_cpu_qwen", paths[0])
-        mod = importlib.util.module_from_spec(spec)
-        spec.loader.exec_module(mod)
-        rt = mod.CpuRuntime(tables.table("iq3s_grid"), threads)
-        kind = "reference"
-
-        made = []
-
-        def prepare(ty, w, rows, cols, x, ntok):
-            k = len(made)
-            made.append(k)
-            rt.add_tensor(f"w{k}", w, ty, cols, rows)
-            rt.alloc(f"x{k}", cols * ntok)
-            rt.alloc(f"y{k}", rows * ntok)
-            rt.write(f"x{k}", x.tobytes())
-            return lambda: rt.qmv(f"w{k}", f"x{k}", f"y{k}", ntok)
-    else:
-        from oracle import oracle
-
-        kind = "port"
-
-        def prepare(ty, w, rows, cols, x, ntok):
-            return lambda: oracle.qmv(ty, w, rows, cols, x, ntok, threads=threads)
+    def prepare(ty, w, rows, cols, x, ntok):
+        return lambda: oracle.qmv(ty, w, rows, cols, x, ntok, threads=threads)
 
     def med(fns, reps):
         for f in fns:
@@ -713,54 +724,81 @@ def cpu_child(threads: int) -> dict:
         t = med(fns, 10)
         b = 2 * alg_bytes(Q3_K, F, H, n) + alg_bytes(Q6_K, H, F, n)
         res[f"config2_mlp_b{n}"] = {"ms": t * 1e3, "GBps": b / t / 1e9}
+    del wg, wu, wd
     for ty in (IQ4_XS, IQ3_S, IQ2_XXS):
         w3 = synth.baseline_rows(ty, H, F, rng)
         for n in (1, 8):
             x3 = rng.standard_normal(n * F).astype(np.float32)
             t = med([prepare(ty, w3, H, F, x3, n)], 10)
             res[f"config3_{TYPE_NAMES[ty]}_{H}x{F}_b{n}"] = {"ms": t * 1e3, "GBps": alg_bytes(ty, H, F, n) / t / 1e9}
-    counts = {}
-    for name, ty, rows, cols, _ in sweep_plan():
-        key = (ty, rows, cols)
-        counts[key] = counts.get(key, 0) + 1
-    total_s, total_b = 0.0, 0
-    for (ty, rows, cols), count in counts.items():
-        r = rows if rows < 100000 else rows // 16
-        w = synth.baseline_rows(ty, r, cols, rng)
-        x = rng.standard_normal(cols).astype(np.float32)
-        total_s += med([prepare(ty, w, r, cols, x, 1)], 3) * (rows / r) * count
-        total_b += alg_bytes(ty, rows, cols, 1) * count
-    res["config4_sweep_b1"] = {"ms": total_s * 1e3, "GBps": total_b / total_s / 1e9}
-    return {"kind": kind, "threads": threads, "configs": {k: {a: round(v, 3) for a, v in d.items()} for k, d in res.items()}}
+    plan = sweep_plan()
+    total_b = sum(alg_bytes(ty, rows, cols, 1) for _, ty, rows, cols, _ in plan)
+    if full_sweep:
+        base = rng.integers(0, 2**63, size=2 << 20, dtype=np.uint64)
+        t0 = time.perf_counter()
+        mats = [(ty, fast_baseline_rows(ty, rows, cols, rng, base), rows, cols) for _, ty, rows, cols, _ in plan]
+        gen_s = time.perf_counter() - t0
+        xs = {c: rng.standard_normal(c).astype(np.float32) for c in {m[3] for m in mats}}
+        passes = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            for ty, w, rows, cols in mats:
+                oracle.qmv(ty, w, rows, cols, xs[cols], 1, threads=threads)
+            passes.append(time.perf_counter() - t0)
+        del mats
+        res["config4_sweep_b1"] = {"ms": passes[1] * 1e3, "GBps": total_b / passes[1] / 1e9,
+                                   "warmup_pass_ms": passes[0] * 1e3, "weights_generated_s": gen_s, "full": 1}
+    else:
+        counts = {}
+        for _, ty, rows, cols, _ in plan:
+            counts[(ty, rows, cols)] = counts.get((ty, rows, cols), 0) + 1
+        total_s = 0.0
+        for (ty, rows, cols), count in counts.items():
+            r = rows if rows < 100000 else rows // 16
+            w = synth.baseline_rows(ty, r, cols, rng)
+            x = rng.standard_normal(cols).astype(np.float32)
+            total_s += med([prepare(ty, w, r, cols, x, 1)], 3) * (rows / r) * count
+        res["config4_sweep_b1"] = {"ms": total_s * 1e3, "GBps": total_b / total_s / 1e9, "full": 0}
+    return {"kind": "port", "threads": threads,
+            "configs": {k: {a: round(v, 3) for a, v in d.items()} for k, d in res.items()}}
 
 
 def cpu_baseline() -> dict:
-    """The reference CPU path at two thread settings, each in a child process (before this process touches the
-    GPU): the reference's default omp_get_num_procs() / 2 (qwen_cpu.c:438) and all physical cores bound close
-    (OMP_PROC_BIND=close, OMP_PLACES=cores), both capped at the GPU's host share of CPU_SHARE CPUs."""
+    """The reference CPU path (its bit-identical C restatement) on the GPU box's host, each setting in a child
+    process started before this process touches the GPU: one thread per physical core, bound close
+    (OMP_PROC_BIND=close, OMP_PLACES=cores), capped at the GPU's host share of CPU_SHARE CPUs -- the reported
+    figure, with the full 27B sweep when the host has FULL_SWEEP_MIN_RAM -- and the reference's default thread
+    count omp_get_num_procs() / 2 (qwen_cpu.c:438) on the sampled sweep, for comparison."""
     import subprocess
 
     host = host_cpu()
+    host["ram_bytes"] = host_ram_bytes()
     nprocs = host["cpus_in_affinity"]
     phys = min(host["physical_cores"] or nprocs, nprocs)
-    settings = {"ref_default": (max(1, min(CPU_SHARE, nprocs // 2)), {}),
-                "all_cores_close": (max(1, min(CPU_SHARE, phys)), {"OMP_PROC_BIND": "close", "OMP_PLACES": "cores"})}
+    full = host["ram_bytes"] >= FULL_SWEEP_MIN_RAM
+    settings = {"all_cores_close": (max(1, min(CPU_SHARE, phys)), {"OMP_PROC_BIND": "close", "OMP_PLACES": "cores"},
+                                    full),
+                "ref_default": (max(1, min(CPU_SHARE, nprocs // 2)), {}, False)}
     runs = {}
-    for label, (threads, extra) in settings.items():
+    for label, (threads, extra, sweep_full) in settings.items():
         env = dict(os.environ, **extra, OMP_NUM_THREADS=str(threads))
-        out = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--cpu-child", str(threads)], env=env,
-                             capture_output=True, text=True, timeout=600)
+        cmd = [sys.executable, str(ROOT / "bench.py"), "--cpu-child", str(threads)] + (["--cpu-full"] if sweep_full else [])
+        out = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=900)
         if out.returncode != 0:
             raise RuntimeError(f"cpu baseline child failed: {out.stderr[-2000:]}")
         runs[label] = json.loads(out.stdout.strip().splitlines()[-1])
-    main_run = runs["ref_default"]
+    main_run = runs["all_cores_close"]
     sweep = main_run["configs"]["config4_sweep_b1"]
+    if sweep.get("full"):
+        sample = ("the full 27B sweep at batch 1: every matrix of the step once (13.4 GiB of weights in host memory, "
+                  "one warm-up pass, then one timed pass)")
+    else:
+        sample = ("27B sweep at batch 1 estimated from each distinct matrix shape (median of 3 calls, LM head on "
+                  f"1/16 of its rows, scaled): host RAM below {FULL_SWEEP_MIN_RAM >> 30} GiB")
     return {"value": sweep["GBps"], "unit": "GB/s", "cores": main_run["threads"], "threads": main_run["threads"],
             "kind": main_run["kind"], "ms_per_step": sweep["ms"], "host": host,
-            "sample": "27B sweep at batch 1 estimated from each distinct matrix shape (median of 3 calls, LM head on "
-                      "1/16 of its rows, scaled) weighted by its per-step count; configs 1-3 timed whole, median "
-                      "of 10 calls after a warm-up call; threads capped at the GPU's host share "
-                      f"({CPU_SHARE})",
+            "sample": sample + "; configs 1-3 timed whole, median of 10 calls after a warm-up call; one thread per "
+                      f"physical core, capped at the GPU's host share ({CPU_SHARE})",
             "settings": {k: {"threads": v["threads"], "env": settings[k][1], "configs": v["configs"]}
                          for k, v in runs.items()}}
 
@@ -789,9 +827,10 @@ def main() -> None:
     ap.add_argument("--mlp-only", action="store_true",
                     help="only the SwiGLU MLP block at batch 1, 4, 8 (as vq_qmv routes) and 8 on the streaming kernel")
     ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-full", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_child:
-        print(json.dumps(cpu_child(args.cpu_child)), flush=True)
+        print(json.dumps(cpu_child(args.cpu_child, args.cpu_full)), flush=True)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the matvec would shard by weight "
@@ -801,7 +840,7 @@ def main() -> None:
     full = not (args.matvec or args.prefill_only or args.mlp_only or args.roofline_only or args.ops_only)
     cpu = None
     if full and not args.no_cpu:  # child processes, started before this process initialises the GPU
-        log("cpu baseline: reference CPU path, configs 1-3 and a sample of the sweep, two thread settings")
+        log("cpu baseline: reference CPU path (C restatement), configs 1-3 and the 27B sweep, two thread settings")
         cpu = cpu_baseline()
 
     import torch
