@@ -803,6 +803,75 @@ def cpu_baseline() -> dict:
                          for k, v in runs.items()}}
 
 
+def stamps_report(torch) -> dict:
+    """Per-workgroup timeline of the sweep's streaming launches from the timing build (vinf_3080ti_amd/_var/
+    libvq_stamps.so, `python -m vinf_3080ti_amd.build --stamps`): each workgroup's thread 0 stamps s_memrealtime
+    (100 MHz) at entry, after its activations are quantized, at the start-up barrier, when wave 0's first weight
+    stage has landed, after every wave's last stage and at the end; the last wave stamps its entry. Launches run one
+    at a time after a producer kernel writes x, rotating over 6 weight copies; medians over 10 launches."""
+    import ctypes
+
+    import numpy as np
+
+    from vinf_3080ti_amd.build import STAMPS_LIB
+
+    hip = Hip(torch, STAMPS_LIB)
+    raw = ctypes.CDLL(str(STAMPS_LIB))
+    n = 8192 * 8
+
+    def read(tu):
+        buf = np.zeros(n, np.uint64)
+        st = getattr(raw, "vq_stamps_read_" + tu)(buf.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(n * 8))
+        assert st == 0, st
+        return buf.reshape(-1, 8).astype(np.int64)
+
+    cases = [("Q3_K gate+up 2x17408x5120", "q3_k", [(Q3_K, 17408, 5120)] * 2, 5120),
+             ("Q4_K down 5120x17408", "q4_k", [(Q4_K, 5120, 17408)], 17408),
+             ("Q6_K out 5120x6144", "q6_k", [(Q6_K, 5120, 6144)], 6144),
+             ("Q4_K 4096x4096 (config 1)", "q4_k", [(Q4_K, 4096, 4096)], 4096)]
+    slots = {5: "last_wave_entry", 4: "thread0_activations_quantized", 1: "startup_barrier",
+             6: "wave0_first_stage_landed", 2: "all_waves_loop_done", 3: "end"}
+    out = {}
+    for name, tu, mats, cols in cases:
+        ws = [[make_weights(torch, t, r, c, 100 * k + i)[0] for i, (t, r, c) in enumerate(mats)] for k in range(6)]
+        x = torch.randn(1, cols, device="cuda")
+        ys = [torch.empty(1, r, device="cuda") for _, r, _ in mats]
+        rows = [r for _, r, _ in mats]
+        rel, skew, span = [], [], []
+        for it in range(14):
+            x.mul_(1.0)  # a producer kernel writes x just before, as in a forward pass
+            before = read(tu)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            hip.group_f32(mats[0][0], ws[it % 6], rows, ys, cols, x, 1)
+            e1.record()
+            torch.cuda.synchronize()
+            after = read(tu)
+            ch = np.nonzero(after[:, 0] != before[:, 0])[0]
+            if it < 4:
+                continue
+            a = after[ch]
+            rel.append((a - a[:, :1]) * 0.01)
+            t0 = a[:, 0] - a[:, 0].min()
+            b = np.arange(len(ch))
+            skew.append([float(t0[b % 8 == k].mean()) * 0.01 for k in range(8)])
+            span.append(((a[:, 3].max() - a[:, 0].min()) * 0.01, e0.elapsed_time(e1) * 1e3))
+        r = np.concatenate(rel)
+        out[name] = {
+            "per_workgroup_us_from_its_entry": {v: {"p10": round(float(np.percentile(r[:, k], 10)), 2),
+                                                    "median": round(float(np.median(r[:, k])), 2),
+                                                    "p90": round(float(np.percentile(r[:, k], 90)), 2)}
+                                                for k, v in slots.items()},
+            "mean_start_by_blockIdx_mod_8_us": [round(float(np.median([sk[k] for sk in skew])), 2) for k in range(8)],
+            "launch_span_first_entry_to_last_end_us": round(float(np.median([s_[0] for s_ in span])), 2),
+            "event_us_single_launch": round(float(np.median([s_[1] for s_ in span])), 2),
+        }
+        log(name, json.dumps(out[name]))
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -826,6 +895,9 @@ def main() -> None:
                     help="only the sequence ops (gated delta, conv update, attention) at the qwen35 shapes")
     ap.add_argument("--mlp-only", action="store_true",
                     help="only the SwiGLU MLP block at batch 1, 4, 8 (as vq_qmv routes) and 8 on the streaming kernel")
+    ap.add_argument("--stamps", action="store_true",
+                    help="only the per-workgroup timeline of the sweep's streaming launches (needs the timing build: "
+                         "python -m vinf_3080ti_amd.build --stamps)")
     ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--cpu-full", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -837,7 +909,8 @@ def main() -> None:
               "rows, one all-gather of y per layer). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    full = not (args.matvec or args.prefill_only or args.mlp_only or args.roofline_only or args.ops_only)
+    full = not (args.matvec or args.prefill_only or args.mlp_only or args.roofline_only or args.ops_only
+                or args.stamps)
     cpu = None
     if full and not args.no_cpu:  # child processes, started before this process initialises the GPU
         log("cpu baseline: reference CPU path (C restatement), configs 1-3 and the 27B sweep, two thread settings")
@@ -846,6 +919,9 @@ def main() -> None:
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.stamps:
+        print(json.dumps({"stamps": stamps_report(torch)}), flush=True)
+        return
     hip = Hip(torch)
 
     if args.matvec and args.libs:

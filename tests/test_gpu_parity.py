@@ -634,3 +634,34 @@ def test_iq3s_grid_setter_large_magnitudes(env, oracle_mod):
     finally:
         orig = (ctypes.c_uint8 * 2048).from_buffer_copy(grid.tobytes())
         assert lib.vq_set_iq3s_grid(ctypes.addressof(orig)) == 0
+
+
+@pytest.mark.parametrize("ty", [T.Q3_K, T.Q4_K, T.Q6_K, T.Q8_0, T.IQ2_XXS, T.IQ4_XS], ids=lambda t: t.name)
+@pytest.mark.parametrize("cols,ntok", [(256, 1), (5120, 1), (6144, 1), (17408, 1), (24576, 1), (5120, 3), (17408, 2),
+                                       (2048, 8), (6144, 5)])
+def test_in_kernel_quantizer_equals_packed_record(env, ty, cols, ntok):
+    """The streaming matvec quantizes fp32 activations itself (vq_qmv_group_f32); its outputs are bit-identical to
+    the same launch over the record vq_pack_x writes (vq_qmv_group), whose quantizer is bit-exact against the
+    reference CPU path (test_quantize_x_bit_exact). Includes a group of all-zero values and one of +-3e4."""
+    torch, lib = env
+    rng = np.random.default_rng(cols * 10 + ntok + int(ty))
+    rows = [96, 40]
+    ws = [synth.baseline_rows(ty, r, cols, rng) for r in rows]
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    x[0, 32:64] = 0.0
+    x[-1, 96:128] = np.where(np.arange(32) % 2, 3.0e4, -3.0e4)
+    wd = [wdev(torch, w) for w in ws]
+    wa = (ctypes.c_void_p * 2)(*[P(t) for t in wd])
+    ra = (ctypes.c_int * 2)(*rows)
+    outs = []
+    for f32 in (True, False):
+        ys = [torch.full((ntok, r), np.nan, dtype=torch.float32, device="cuda") for r in rows]
+        ya = (ctypes.c_void_p * 2)(*[P(t) for t in ys])
+        xin = dev(torch, x) if f32 else _pack(torch, lib, x, ntok, cols)
+        fn = lib.vq_qmv_group_f32 if f32 else lib.vq_qmv_group
+        assert fn(int(ty), 2, wa, ra, ya, cols, P(xin), ntok, None) == 0
+        torch.cuda.synchronize()
+        outs.append([y.cpu().numpy() for y in ys])
+    for a, b in zip(*outs):
+        assert not np.isnan(a).any()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

@@ -39,12 +39,15 @@ def hipcc() -> str:
     return str(Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "bin" / "hipcc")
 
 
-def _compile(src: Path, force: bool) -> Path:
-    obj = BUILD / (src.stem + ".o")
+STAMPS_LIB = PKG / "_var" / "libvq_stamps.so"  # timing build (-DVQ_STAMPS): per-workgroup timestamps
+
+
+def _compile(src: Path, force: bool, build_dir: Path = BUILD, extra: tuple[str, ...] = ()) -> Path:
+    obj = build_dir / (src.stem + ".o")
     newest = max(p.stat().st_mtime for p in headers() + [src])
     if force or not obj.exists() or obj.stat().st_mtime < newest:
         tmp = obj.with_suffix(".o.tmp")
-        res = subprocess.run([hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(tmp)], stdout=subprocess.PIPE,
+        res = subprocess.run([hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(tmp)], stdout=subprocess.PIPE,
                              stderr=subprocess.STDOUT, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}")
@@ -52,22 +55,27 @@ def _compile(src: Path, force: bool) -> Path:
     return obj
 
 
-def build(force: bool = True, jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile every translation unit and link LIB. force=False reuses objects newer than their inputs."""
-    BUILD.mkdir(exist_ok=True)
+def build(force: bool = True, jobs: int | None = None, verbose: bool = False, stamps: bool = False) -> Path:
+    """Compile every translation unit and link LIB. force=False reuses objects newer than their inputs.
+    stamps=True builds the timing variant STAMPS_LIB instead (the matvec writes per-workgroup s_memrealtime
+    stamps that vq_stamps_read_<type> returns; bench.py --stamps reads them); it never replaces LIB."""
+    build_dir = BUILD if not stamps else PKG / "_var" / "obj_stamps"
+    lib = LIB if not stamps else STAMPS_LIB
+    extra = ("-DVQ_STAMPS",) if stamps else ()
+    build_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     jobs = jobs or min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, force), srcs))
-    if force or not LIB.exists() or LIB.stat().st_mtime < max(o.stat().st_mtime for o in objs):
-        tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda s: _compile(s, force, build_dir, extra), srcs))
+    if force or not lib.exists() or lib.stat().st_mtime < max(o.stat().st_mtime for o in objs):
+        tmp = lib.with_suffix(".so.tmp")
         cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)
-        os.replace(tmp, LIB)
-    return LIB
+        os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    print(build(force="--force" in sys.argv, verbose=True))
+    print(build(force="--force" in sys.argv, verbose=True, stamps="--stamps" in sys.argv))

@@ -148,6 +148,24 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, long r) {
     return (static_cast<unsigned long long>(o) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(r));
 }
 
+// Timing builds only (-DVQ_STAMPS, never in the shipped library): per-workgroup s_memrealtime stamps.
+#ifdef VQ_STAMPS
+static __device__ unsigned long long g_stamps[8192 * 8];
+#define VQ_STAMP_IF(cond, slot)                                                                                \
+    do {                                                                                                       \
+        if (cond) g_stamps[blockIdx.x * 8 + (slot)] = __builtin_amdgcn_s_memrealtime();                        \
+    } while (0)
+#define VQ_STAMP(slot) VQ_STAMP_IF(threadIdx.x == 0, slot)
+#define VQ_STAMP_READER(NAME)                                                                                  \
+    extern "C" int NAME(void *dst, size_t bytes) {                                                             \
+        return static_cast<int>(hipMemcpyFromSymbol(dst, HIP_SYMBOL(vq::g_stamps), bytes, 0, hipMemcpyDeviceToHost)); \
+    }
+#else
+#define VQ_STAMP_IF(cond, slot)
+#define VQ_STAMP(slot)
+#define VQ_STAMP_READER(NAME)
+#endif
+
 // Quantized matvec: y[t][r] = W[r] . x[t] for t < NT.
 //
 // Workgroup b owns a contiguous range of rows of one job -- a contiguous byte range, since rows are back to
@@ -182,6 +200,8 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     __shared__ int s_next;                        // next stage to hand out
     __shared__ unsigned long long s_best[NT][NW];  // argmax reduction
 
+    VQ_STAMP(0);
+    VQ_STAMP_IF(threadIdx.x == blockDim.x - 64, 5);
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nu = (cols >> 5) / S::UG;
@@ -320,25 +340,52 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             }
             __syncthreads();  // the RMS sums' LDS is a stage buffer again from here
         } else {
-        for (int i = threadIdx.x; i < NT * xi.ng; i += blockDim.x) {
-            const int t = i / xi.ng, g = i - t * xi.ng;
-            const float4 *src = reinterpret_cast<const float4 *>(xf + static_cast<size_t>(t) * cols + 32 * g);
-            float v[32];
+        // Two lanes per (token, group), one 16-element half each: lane pairs read 128 contiguous bytes, so a load
+        // instruction touches half as many cache lines as with one lane per group, and the group's amax and the
+        // other half's sum come from the partner lane. The IEEE steps are quantize_group's (amax, d = amax/127,
+        // id = 1/d, q = rint(v * id)); integer sums do not depend on their order.
+        for (int i = threadIdx.x; i < 2 * NT * xi.ng; i += blockDim.x) {
+            const int h = i & 1, gi = i >> 1;
+            const int t = gi / xi.ng, g = gi - t * xi.ng;
+            const float4 *src = reinterpret_cast<const float4 *>(xf + static_cast<size_t>(t) * cols + 32 * g + 16 * h);
+            float v[16];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
+            for (int k = 0; k < 4; ++k) {
                 const float4 f = src[k];
                 v[4 * k] = f.x;
                 v[4 * k + 1] = f.y;
                 v[4 * k + 2] = f.z;
                 v[4 * k + 3] = f.w;
             }
-            const QGroup qg = quantize_group(v);
+            float amax = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) amax = fmaxf(amax, fabsf(v[k]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            const float d = amax / 127.0f;
+            const float id = d > 0.0f ? 1.0f / d : 0.0f;
+            uint32_t q[4];
+            int hs = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t p = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int c = static_cast<int>(__builtin_rintf(v[4 * k + b] * id));
+                    hs += c;
+                    p |= (static_cast<uint32_t>(c) & 0xFFu) << (8 * b);
+                }
+                q[k] = p;
+            }
+            const int hs_other = __shfl_xor(hs, 1, 64);
             uint8_t *img = s_dyn + t * xi.bytes;
-            *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 0)) = u32x4{qg.q[0], qg.q[1], qg.q[2], qg.q[3]};
-            *reinterpret_cast<u32x4 *>(img + xi.code_off(g, 1)) = u32x4{qg.q[4], qg.q[5], qg.q[6], qg.q[7]};
-            reinterpret_cast<float *>(img + xi.xq_bytes)[g] = qg.d;
-            reinterpret_cast<uint32_t *>(img + xi.xq_bytes + 4 * xi.ng)[g] = qg.half_sums();
+            *reinterpret_cast<u32x4 *>(img + xi.code_off(g, h)) = u32x4{q[0], q[1], q[2], q[3]};
+            if (h == 0) {
+                reinterpret_cast<float *>(img + xi.xq_bytes)[g] = d;
+                reinterpret_cast<uint32_t *>(img + xi.xq_bytes + 4 * xi.ng)[g] =
+                    (static_cast<uint32_t>(hs) & 0xFFFFu) | (static_cast<uint32_t>(hs_other) << 16);
+            }
         }
+        VQ_STAMP(4);
         }
     } else {
         for (int p = wv; p < xreg / 1024; p += NW) {
@@ -370,6 +417,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    VQ_STAMP(1);
 
     const int ul = lane / LPU;  // unit of this lane within a stage
     const int lj = lane % LPU;  // which of the unit's lanes
@@ -568,8 +616,15 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     // One lane takes the ticket (a wave-wide atomic would take one per lane); readfirstlane shares it.
     auto take = [&]() { return lane == 0 ? atomicAdd(&s_next, 1) : 0; };
     int ask = s >= 0 ? take() : nst;  // the stage after s (valid in lane 0)
+#ifdef VQ_STAMPS
+    bool first_stage = true;
+#endif
     while (s >= 0) {
         store_stage(RA);
+#ifdef VQ_STAMPS
+        VQ_STAMP_IF(first_stage && threadIdx.x == 0, 6);
+        first_stage = false;
+#endif
         const int sn = __builtin_amdgcn_readfirstlane(ask);
         if (sn < nst) {
             load_stage(sn, RA);
@@ -579,6 +634,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
         s = sn < nst ? sn : -1;
     }
     __syncthreads();
+    VQ_STAMP(2);
 
     // Each row's parts in a fixed order: the row's units are [r*nu - U0, (r+1)*nu - U0) of the range.
     unsigned long long best[NT];
@@ -634,6 +690,10 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             best[t] = key > best[t] ? key : best[t];
         }
     }
+#ifdef VQ_STAMPS
+    __syncthreads();
+    VQ_STAMP(3);
+#endif
     if (jobs.amax != nullptr) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {

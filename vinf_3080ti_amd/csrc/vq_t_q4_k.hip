@@ -3,3 +3,4 @@
 #include "vq_mfma_impl.h"
 
 VQ_INSTANTIATE(VQ_Q4_K)
+VQ_STAMP_READER(vq_stamps_read_q4_k)
