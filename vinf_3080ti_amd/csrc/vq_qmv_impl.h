@@ -360,7 +360,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             float amax = 0.0f;
 #pragma unroll
             for (int k = 0; k < 16; ++k) amax = fmaxf(amax, fabsf(v[k]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            amax = fmaxf(amax, dpp_f<0xB1>(amax));  // the partner lane (quad_perm [1,0,3,2])
             const float d = amax / 127.0f;
             const float id = d > 0.0f ? 1.0f / d : 0.0f;
             uint32_t q[4];
@@ -376,7 +376,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
                 }
                 q[k] = p;
             }
-            const int hs_other = __shfl_xor(hs, 1, 64);
+            const int hs_other = __builtin_amdgcn_update_dpp(0, hs, 0xB1, 0xF, 0xF, false);
             uint8_t *img = s_dyn + t * xi.bytes;
             *reinterpret_cast<u32x4 *>(img + xi.code_off(g, h)) = u32x4{q[0], q[1], q[2], q[3]};
             if (h == 0) {
@@ -641,7 +641,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
 #pragma unroll
     for (int t = 0; t < NT; ++t) best[t] = 0ull;
     if (per_lane) {
-        // Eight threads per row: thread k adds parts k, k+8, ... of the row's nu*LPU, then three xor steps.
+        // Eight threads per row: thread k adds parts k, k+8, ... of the row's nu*LPU, then three DPP steps.
         const int k = threadIdx.x & 7;
         for (int r0 = R0; r0 < R1; r0 += blockDim.x >> 3) {
             const int r = r0 + static_cast<int>(threadIdx.x >> 3);
@@ -656,9 +656,12 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                tot[t] += __shfl_xor(tot[t], 1, 64);
-                tot[t] += __shfl_xor(tot[t], 2, 64);
-                tot[t] += __shfl_xor(tot[t], 4, 64);
+                // The 8 threads' sums by DPP moves (no LDS round trips): pairs, quads, then the other quad of
+                // the half row (row_half_mirror: thread j takes thread 7 - j). Each thread ends with
+                // ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)) up to the order of commutative IEEE adds.
+                tot[t] += dpp_f<0xB1>(tot[t]);   // quad_perm [1,0,3,2]
+                tot[t] += dpp_f<0x4E>(tot[t]);   // quad_perm [2,3,0,1]
+                tot[t] += dpp_f<0x141>(tot[t]);  // row_half_mirror
             }
             if (ok && k == 0) {
 #pragma unroll
