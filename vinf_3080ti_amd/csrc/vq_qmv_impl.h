@@ -590,20 +590,30 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             return;
         }
         // Segmented inclusive scan over the lanes; segments are the stage's rows (q is non-decreasing in lane
-        // order). The last lane of each segment holds that row's part of the stage.
+        // order). The last lane of each segment holds that row's part of the stage. DPP moves, no LDS round trips:
+        // row_shr 1, 2, 4, 8 scan each 16-lane row, then row_bcast:15 (rows 1, 3 take the last lane of rows 0, 2)
+        // and row_bcast:31 (rows 2, 3 take lane 31), each step adding only where the source lane has the same key
+        // (a lane without a source reads key -1). Keys are non-decreasing, so a matching source lane carries the
+        // segment's whole part before it.
         const int key = valid ? q : 0x7FFFFFFF;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int kp = __shfl_up(key, d, 64);
-            const bool m = lane >= d && kp == key;
+        auto seg_step = [&](auto ctrl, auto rmask) {
+            constexpr int C = decltype(ctrl)::value, RM = decltype(rmask)::value;
+            const int kp = __builtin_amdgcn_update_dpp(-1, key, C, RM, 0xF, false);
+            const bool m = kp == key;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const float vp = __shfl_up(v[t], d, 64);
+                const float vp = dpp_f<C, RM>(v[t]);
                 v[t] += m ? vp : 0.0f;
             }
-        }
-        const int kn = __shfl_down(key, 1, 64);
-        if (valid && (lane == 63 || kn != key)) {
+        };
+        seg_step(std::integral_constant<int, 0x111>{}, std::integral_constant<int, 0xF>{});  // row_shr:1
+        seg_step(std::integral_constant<int, 0x112>{}, std::integral_constant<int, 0xF>{});  // row_shr:2
+        seg_step(std::integral_constant<int, 0x114>{}, std::integral_constant<int, 0xF>{});  // row_shr:4
+        seg_step(std::integral_constant<int, 0x118>{}, std::integral_constant<int, 0xF>{});  // row_shr:8
+        seg_step(std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xA>{});  // row_bcast:15
+        seg_step(std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xC>{});  // row_bcast:31
+        const int kn = __builtin_amdgcn_update_dpp(-2, key, 0x130, 0xF, 0xF, false);  // wave_shl:1, lane 63 reads -2
+        if (valid && kn != key) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) slots[(s * rs + q) * NT + t] = v[t];
         }
