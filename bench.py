@@ -83,6 +83,17 @@ def profiled_traffic():
     return None
 
 
+def profiled_trace_us():
+    """Average kernel-trace duration (µs) of the dominant launch in the committed rocprofv3 summary, or None."""
+    f = ROOT / "profiles" / "qmv_q3k_gateup_2x17408x5120_pmc.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("trace_avg_us:"):
+            return float(line.split(":")[1].strip())
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -166,10 +177,11 @@ def make_weights(torch, ty, rows, cols, seed, copies=1):
     return [torch_baseline_rows(ty, rows, cols, seed + 7919 * c, "cuda") for c in range(copies)]
 
 
-def time_kernel_loop(torch, fn, n_iter, graph=True):
+def time_kernel_loop(torch, fn, n_iter, graph=True, reps=1):
     """Average duration (ms) of fn(i) for i < n_iter, bracketed by HIP events on the stream the launches run
     on. With graph=True the n_iter launches are captured once in a hipGraph and replayed (back-to-back
-    kernels, as in a decode step, without the host's per-launch cost); else launched eagerly."""
+    kernels, as in a decode step, without the host's per-launch cost), the median of `reps` timed replays after
+    `reps` untimed ones (the clocks settle); else launched eagerly."""
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     if graph:
@@ -181,14 +193,18 @@ def time_kernel_loop(torch, fn, n_iter, graph=True):
                 for i in range(n_iter):
                     fn(i)
         torch.cuda.synchronize()
-        g.replay()  # warm
+        for _ in range(reps):  # warm
+            g.replay()
         torch.cuda.synchronize()
-        start.record()
-        g.replay()
-        stop.record()
-        torch.cuda.synchronize()
+        times = []
+        for _ in range(reps):
+            start.record()
+            g.replay()
+            stop.record()
+            torch.cuda.synchronize()
+            times.append(start.elapsed_time(stop) / n_iter)
         del g
-        return start.elapsed_time(stop) / n_iter
+        return sorted(times)[len(times) // 2]
     start.record()
     for i in range(n_iter):
         fn(i)
@@ -197,7 +213,7 @@ def time_kernel_loop(torch, fn, n_iter, graph=True):
     return start.elapsed_time(stop) / n_iter
 
 
-def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=640 << 20, group=1):
+def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=640 << 20, group=1, reps=1):
     """Per-launch µs and GB/s of the matvec kernel alone: `group` matrices of rows x cols (one
     vq_qmv_group_f32 launch, which quantizes the fp32 activations in-kernel, as in the sweep), rotating over
     weight copies larger than the MALL; launches captured in a hipGraph."""
@@ -217,7 +233,7 @@ def bench_matvec(torch, hip, ty, rows, cols, ntok, iters=60, min_rotation_bytes=
 
     for i in range(copies):  # warm-up
         launch(i)
-    ms = time_kernel_loop(torch, launch, iters)
+    ms = time_kernel_loop(torch, launch, iters, reps=reps)
     b = alg_bytes(ty, rows, cols, ntok) * group
     del ws
     torch.cuda.empty_cache()
@@ -974,8 +990,9 @@ def main() -> None:
 
     # Roofline of the dominant kernel: the FFN gate+up launch (2 x Q3_K 17408x5120, 64 launches per step).
     log("roofline: grouped Q3_K 2 x 17408x5120 matvec")
-    dom = bench_matvec(torch, hip, Q3_K, 17408, 5120, args.ntok, iters=100, group=2)
+    dom = bench_matvec(torch, hip, Q3_K, 17408, 5120, args.ntok, iters=100, group=2, reps=5)
     traffic = profiled_traffic()
+    trace_us = profiled_trace_us()
     roofline = {
         "bound": "hbm",
         "kernel": f"qmv_stream_kernel<Q3_K,{args.ntok}> gate+up group 2x17408x5120",
@@ -985,8 +1002,12 @@ def main() -> None:
         "frac": round(dom["frac"], 4),
         "avg_us": round(dom["us"], 3),
         "traffic": traffic,
-        # not counted in this run: the committed rocprofv3 PMC summary of the same launch and command
+        # not counted in this run: the committed rocprofv3 summaries of the same launch and command
         "traffic_source": "profiles/qmv_q3k_gateup_2x17408x5120_pmc.md (rocprofv3 FETCH_SIZE / WRITE_SIZE)",
+        "trace_avg_us": trace_us,
+        "trace_frac": round(dom["bytes"] / (trace_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4) if trace_us else None,
+        "trace_source": "profiles/qmv_q3k_gateup_2x17408x5120_pmc.md (rocprofv3 --kernel-trace of bench.py "
+                        "--roofline-only: the kernel's own duration, without the graph's launch gaps)",
     }
     if args.roofline_only:
         a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
