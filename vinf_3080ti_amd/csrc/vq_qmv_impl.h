@@ -398,7 +398,10 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     wait_vm<0>();
     __builtin_amdgcn_sched_barrier(0);
     if (s >= 0) load_stage(s, RA);  // waves without a stage load nothing
-    if (threadIdx.x == 0) s_next = NW;
+    // Stages 0 .. 2 NW - 1 are static: wave w takes w, then w + NW (no ticket round trip before the first
+    // decode); tickets hand out the rest.
+    const int s2 = wv + NW < nst ? wv + NW : -1;
+    if (threadIdx.x == 0) s_next = 2 * NW;
     Tabs tb{};
     if constexpr (SG) {
         tb.sg = reinterpret_cast<const uint32_t *>(s_grid);
@@ -625,7 +628,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     // asked for one stage ahead, so its LDS round trip hides behind a decode.
     // One lane takes the ticket (a wave-wide atomic would take one per lane); readfirstlane shares it.
     auto take = [&]() { return lane == 0 ? atomicAdd(&s_next, 1) : 0; };
-    int ask = s >= 0 ? take() : nst;  // the stage after s (valid in lane 0)
+    int ask = s2 >= 0 ? s2 : nst;  // the stage after s (valid in lane 0): the static second stage
 #ifdef VQ_STAMPS
     bool first_stage = true;
 #endif
