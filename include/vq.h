@@ -272,6 +272,20 @@ int vq_gated_delta_seg(const float *conv, const float *b, const float *a, const 
 int vq_qmv_staged(int type, const uint8_t *w, int rows, int cols, const float *x, const float *x2,
                   const float *norm_w, float eps, int flags, int ntok, float *y, void *stream);
 
+/* Workspace bytes with which vq_qmv_staged_ws runs 5-16 tokens (3-4 over inputs wider than the streaming kernel's
+ * activation image holds twice) of Q3_K..Q6_K and the IQ types but IQ4_NL on the f16-MFMA small-batch matvec: the
+ * per-token RMS scales (256 B) and the K ranges' partial sums. 0 for every other call (it then streams). */
+size_t vq_qmv_staged_workspace_bytes(int type, int rows, int cols, int ntok);
+
+/* vq_qmv_staged with a workspace: with >= vq_qmv_staged_workspace_bytes (16-byte aligned) the staging runs inside
+ * the f16-MFMA small-batch matvec, which stages each K range's activations before quantizing them (SILU_MUL;
+ * NORM with per-token scales rsqrt(mean(v^2) + eps) from one prepass launch) and adds y's previous value in its
+ * K-range sum (ADD); any cols multiple of 256. Otherwise it is vq_qmv_staged. Replaces: the megakernel's op_qmv
+ * staging at every batch size (qwen_megakernel.cu:468-551), for speculative-verify passes of 5-16 tokens. */
+int vq_qmv_staged_ws(int type, const uint8_t *w, int rows, int cols, const float *x, const float *x2,
+                     const float *norm_w, float eps, int flags, int ntok, float *y, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
 /* Same as vq_qmv with activations already packed by vq_pack_x (quantized types only), so several
  * matrices that share one input (gate/up, q/k/v) quantize it once. Replaces: dot_row_q's caller loop
  * (qwen_cpu.c:628-637). */

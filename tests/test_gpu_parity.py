@@ -665,3 +665,95 @@ def test_in_kernel_quantizer_equals_packed_record(env, ty, cols, ntok):
     for a, b in zip(*outs):
         assert not np.isnan(a).any()
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def _staged_ws_run(torch, lib, ty, w, rows, cols, x, x2, nw, y0, eps, flags, ntok):
+    nws = lib.vq_qmv_staged_workspace_bytes(int(ty), rows, cols, ntok)
+    ws = torch.empty(max(nws, 256), dtype=torch.uint8, device="cuda")
+    y = dev(torch, y0.copy())
+    st = lib.vq_qmv_staged_ws(int(ty), P(w), rows, cols, P(x), P(x2), P(nw), eps, flags, ntok, P(y), P(ws), nws,
+                              None)
+    assert st == 0, lib.vq_status_string(st)
+    torch.cuda.synchronize()
+    return y.cpu().numpy(), nws
+
+
+def _staged_bound_check(oracle_mod, ty, w, rows, cols, x, x2, nw, y0, eps, flags, got):
+    """The reference's int8-path bound for staged activations (test_phase31b_megakernel.py:184-199)."""
+    v = oracle_mod.stage_x(x, x2, nw, eps, flags)
+    wf = oracle_mod.dequant_rows(int(ty), w, rows, cols).astype(np.float64)
+    absw = np.abs(wf).reshape(rows, -1, 32).sum(2)
+    for t in range(x.shape[0]):
+        ref = wf @ v[t] + (y0[t].astype(np.float64) if flags & 1 else 0.0)
+        amax = np.abs(v[t].reshape(-1, 32)).max(1)
+        bound = (absw * amax / 254.0).sum(1)
+        assert np.all(np.abs(got[t] - ref) <= 1.05 * bound + 1e-4 * (1 + np.abs(ref))), (ty.name, flags, t)
+
+
+@pytest.mark.parametrize("ty", [T.Q3_K, T.Q4_K, T.Q5_K, T.Q6_K, T.IQ4_XS, T.IQ2_XXS], ids=lambda t: t.name)
+@pytest.mark.parametrize("flags", [0, 1, 2, 8, 10, 11])
+@pytest.mark.parametrize("ntok,rows,cols", [(5, 300, 2048), (8, 129, 512), (16, 200, 1536)])
+def test_qmv_staged_small_batch_f16(env, oracle_mod, ty, flags, ntok, rows, cols):
+    """vq_qmv_staged_ws on the f16-MFMA small-batch kernel (5-16 tokens): SILU_MUL / NORM staged per K range with
+    the RMS prepass, ADD in the K-range sum (or in the kernel with a single 512-column range), within the reference's
+    int8-path bound of the float64 staged matvec (qwen_megakernel.cu:468-551); bit-identical on a rerun; with no
+    flags bit-identical to vq_qmv with its workspace (the same kernel)."""
+    torch, lib = env
+    rng = np.random.default_rng(8800 + 10 * flags + ntok + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = (rng.standard_normal((ntok, cols)) * 2.0).astype(np.float32)
+    x2 = rng.standard_normal((ntok, cols)).astype(np.float32)
+    nw = rng.uniform(0.2, 1.5, cols).astype(np.float32)
+    y0 = rng.standard_normal((ntok, rows)).astype(np.float32)
+    eps = 1e-6
+    wd, xd, x2d, nwd = wdev(torch, w), dev(torch, x), dev(torch, x2), dev(torch, nw)
+    got, nws = _staged_ws_run(torch, lib, ty, wd, rows, cols, xd, x2d, nwd, y0, eps, flags, ntok)
+    assert nws > 0  # the f16 small-batch route
+    _staged_bound_check(oracle_mod, ty, w, rows, cols, x, x2, nw, y0, eps, flags, got)
+    again, _ = _staged_ws_run(torch, lib, ty, wd, rows, cols, xd, x2d, nwd, y0, eps, flags, ntok)
+    assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+    if flags == 0:
+        plain = gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok, fast=True)
+        assert np.array_equal(plain.view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.parametrize("ty,rows,cols,flags", [(T.Q3_K, 17408, 5120, 2), (T.Q6_K, 5120, 17408, 9)],
+                         ids=["Q3_K-gate-NORM", "Q6_K-down-SILU_MUL+ADD"])
+def test_qmv_staged_small_batch_f16_mlp_shapes(env, oracle_mod, ty, rows, cols, flags):
+    """The MLP block's staged projections at 8 tokens (speculative verify): RMSNorm into the Q3_K gate, SiLU * up
+    into the Q6_K down with the residual ADD, on the f16 small-batch path."""
+    torch, lib = env
+    ntok = 8
+    rng = np.random.default_rng(rows + flags)
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = (rng.standard_normal((ntok, cols)) * 2.0).astype(np.float32)
+    x2 = rng.standard_normal((ntok, cols)).astype(np.float32)
+    nw = rng.uniform(0.2, 1.5, cols).astype(np.float32)
+    y0 = rng.standard_normal((ntok, rows)).astype(np.float32)
+    got, nws = _staged_ws_run(torch, lib, ty, wdev(torch, w), rows, cols, dev(torch, x), dev(torch, x2),
+                              dev(torch, nw), y0, 1e-6, flags, ntok)
+    assert nws > 0
+    _staged_bound_check(oracle_mod, ty, w, rows, cols, x, x2, nw, y0, 1e-6, flags, got)
+
+
+def test_qmv_staged_ws_falls_back_to_streaming(env):
+    """Without the workspace (or for 1-4 tokens, Q8_0, ...) vq_qmv_staged_ws is vq_qmv_staged, bit for bit."""
+    torch, lib = env
+    rng = np.random.default_rng(91)
+    for ty, ntok, rows, cols in [(T.Q4_K, 8, 64, 1024), (T.Q4_K, 2, 64, 1024), (T.Q8_0, 8, 64, 1024)]:
+        w = wdev(torch, synth.baseline_rows(ty, rows, cols, rng))
+        x = dev(torch, rng.standard_normal((ntok, cols)).astype(np.float32))
+        x2 = dev(torch, rng.standard_normal((ntok, cols)).astype(np.float32))
+        nw = dev(torch, rng.uniform(0.5, 1.5, cols).astype(np.float32))
+        outs = []
+        for use_ws in (False, True):
+            y = torch.zeros(ntok, rows, dtype=torch.float32, device="cuda")
+            if use_ws:
+                st = lib.vq_qmv_staged_ws(int(ty), P(w), rows, cols, P(x), P(x2), P(nw), 1e-6, 10, ntok, P(y), None, 0,
+                                          None)
+            else:
+                st = lib.vq_qmv_staged(int(ty), P(w), rows, cols, P(x), P(x2), P(nw), 1e-6, 10, ntok, P(y), None)
+            assert st == 0, lib.vq_status_string(st)
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy())
+        assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), (ty.name, ntok)

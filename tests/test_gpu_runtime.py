@@ -233,11 +233,13 @@ def test_upload_gguf_tensor_from_a_file(rt, oracle_mod, tmp_path):
     rt.free("s")
 
 
-def test_qmv_staged_fuses_silu_mul_norm_and_add(rt, oracle_mod):
+@pytest.mark.parametrize("ntok", [2, 8])
+def test_qmv_staged_fuses_silu_mul_norm_and_add(rt, oracle_mod, ntok):
     """Runtime.qmv_staged: v = rmsnorm(silu(x) * x2) * norm, y += W v (the megakernel's QMV flags,
     qwen_megakernel.cu:468-551), against the float64 staged reference within the int8-path bound; the norm
-    weights as an uploaded F32 tensor and as a buffer give the same result."""
-    rows, cols, ntok = 24, 1024, 2
+    weights as an uploaded F32 tensor and as a buffer give the same result. 2 tokens stream, 8 take the f16
+    small-batch kernel with its RMS prepass."""
+    rows, cols = 24, 1024
     rng = np.random.default_rng(91)
     raw = synth.synthetic_rows(T.Q4_K, rows, cols, 91)
     x = rng.standard_normal((ntok, cols)).astype(np.float32)

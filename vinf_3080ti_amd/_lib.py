@@ -30,6 +30,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_qmv_workspace_bytes_for": (SZ, [I, I, I, I]),
     "vq_qmv_path": (I, [I, I, I, I, SZ]),
     "vq_qmv_staged": (I, [I, P, I, I, P, P, P, F, I, I, P, P]),
+    "vq_qmv_staged_workspace_bytes": (SZ, [I, I, I, I]),
+    "vq_qmv_staged_ws": (I, [I, P, I, I, P, P, P, F, I, I, P, P, SZ, P]),
     "vq_rmsnorm": (I, [P, P, P, P, I, I, F, P]),
     "vq_binary": (I, [I, P, P, P, ctypes.c_long, P]),
     "vq_split_gated_q": (I, [P, P, P, I, I, P]),
@@ -100,8 +102,14 @@ def load(path: Path | None = None) -> ctypes.CDLL:
         lib = ctypes.CDLL(str(p))
     except OSError as exc:
         raise LibraryUnavailableError(f"cannot load {p}: {exc}") from exc
+    variant = path is not None or "VQ_LIB_PATH" in os.environ
     for name, (res, args) in SIGNATURES.items():
-        fn = getattr(lib, name)
+        try:
+            fn = getattr(lib, name)
+        except AttributeError:
+            if variant:  # an older build compared against this one (bench.py --libs): it lacks newer entry points
+                continue
+            raise
         fn.restype = res
         fn.argtypes = args
     if path is None:

@@ -435,6 +435,9 @@ static bool small16_batch(int type, int cols, int ntok) {
 
 // The path vq_qmv takes (VQ_PATH_*), given whether a usable (non-NULL, 16-byte aligned) workspace of wsb
 // bytes comes with the call.
+// Head of the staged small-batch workspace: the per-token RMS scales (16 floats, padded).
+constexpr size_t kStagedRsBytes = 256;
+
 static int qmv_route(int type, int rows, int cols, int ntok, bool ws, size_t wsb) {
     if (type == VQ_F32 || type == VQ_F16) return VQ_PATH_STREAM;
     if (small16_batch(type, cols, ntok)) {
@@ -502,6 +505,39 @@ int vq_qmv_staged(int type, const uint8_t *w, int rows, int cols, const float *x
     hipStream_t s = static_cast<hipStream_t>(stream);
     return dispatch_quant(type, [&](auto tc) {
         return vq::launch_quant_staged<decltype(tc)::value>(w, rows, cols, rb, x, xs, ntok, y, s);
+    });
+}
+
+size_t vq_qmv_staged_workspace_bytes(int type, int rows, int cols, int ntok) {
+    if (check_matrix(type, rows, cols) || ntok < 1 || type == VQ_F32 || type == VQ_F16) return 0;
+    if (!small16_batch(type, cols, ntok)) return 0;
+    return kStagedRsBytes + vq::s16_part_bytes(rows, cols, ntok);
+}
+
+int vq_qmv_staged_ws(int type, const uint8_t *w, int rows, int cols, const float *x, const float *x2,
+                     const float *norm_w, float eps, int flags, int ntok, float *y, void *workspace,
+                     size_t workspace_bytes, void *stream) {
+    const int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (type == VQ_F32 || type == VQ_F16) return VQ_ERR_TYPE;
+    if (ntok < 1) return VQ_ERR_SHAPE;
+    if (flags & ~(VQ_QMV_ADD | VQ_QMV_NORM | VQ_QMV_SILU_MUL)) return VQ_ERR_ARG;
+    if (!w || !x || !y || misaligned16(w) || misaligned16(x)) return VQ_ERR_ARG;
+    if ((flags & VQ_QMV_SILU_MUL) && (!x2 || misaligned16(x2))) return VQ_ERR_ARG;
+    if ((flags & VQ_QMV_NORM) && (!norm_w || misaligned16(norm_w) || !(eps >= 0.0f))) return VQ_ERR_ARG;
+    const size_t need = vq_qmv_staged_workspace_bytes(type, rows, cols, ntok);
+    if (need == 0 || !workspace || misaligned16(workspace) || workspace_bytes < need)
+        return vq_qmv_staged(type, w, rows, cols, x, x2, norm_w, eps, flags, ntok, y, stream);
+    const vq::XStage xs{(flags & VQ_QMV_SILU_MUL) ? x2 : nullptr, (flags & VQ_QMV_NORM) ? norm_w : nullptr, eps,
+                        flags};
+    float *const rs = static_cast<float *>(workspace);
+    float *const part = vq::s16_part_bytes(rows, cols, ntok)
+                            ? reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + kStagedRsBytes)
+                            : nullptr;
+    const long rb = row_bytes_of(type, cols);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return dispatch_quant(type, [&](auto tc) {
+        return vq::launch_small16<decltype(tc)::value>(w, rows, cols, rb, x, ntok, y, part, s, xs, rs);
     });
 }
 

@@ -71,10 +71,11 @@ int launch_gemm16(const uint8_t *w, int rows, int cols, long row_bytes, const vo
 // activations; `part` holds s16_part_bytes(rows, cols, ntok) bytes (unused when that is 0).
 template <int T>
 int launch_small16_group(int n, const uint8_t *const *w, const int *rows, float *const *y, int cols, long row_bytes,
-                         const float *x, int ntok, float *part, hipStream_t s);
+                         const float *x, int ntok, float *part, hipStream_t s, const XStage &xs = XStage{},
+                         float *rs = nullptr);
 template <int T>
 int launch_small16(const uint8_t *w, int rows, int cols, long row_bytes, const float *x, int ntok, float *y,
-                   float *part, hipStream_t s);
+                   float *part, hipStream_t s, const XStage &xs = XStage{}, float *rs = nullptr);
 // Small-batch (2..16 tokens) matvec on int8 MFMA over fp32 activations (quantized in the kernel); `part` holds
 // mfma_part_bytes(rows, cols, ntok) bytes (unused when that is 0).
 template <int T>
@@ -107,9 +108,9 @@ int set_iq3s_grid(const uint8_t *grid);
     KW int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \
     KW int vq::launch_gemm16<T>(const uint8_t *, int, int, long, const void *, int, float *, int, hipStream_t, bool); \
     KW int vq::launch_small16_group<T>(int, const uint8_t *const *, const int *, float *const *, int, long,    \
-                                             const float *, int, float *, hipStream_t);                            \
+                                             const float *, int, float *, hipStream_t, const vq::XStage &, float *); \
     KW int vq::launch_small16<T>(const uint8_t *, int, int, long, const float *, int, float *, float *,          \
-                                       hipStream_t);                                                               \
+                                       hipStream_t, const vq::XStage &, float *);                                  \
     KW int vq::launch_mfma<T>(const uint8_t *, int, int, long, const float *, int, float *, float *,         \
                                     hipStream_t);                                                                \
     KW int vq::launch_partials<T>(const uint8_t *, int, int, long, const uint8_t *, int, int32_t *,          \

@@ -136,9 +136,49 @@ __device__ __forceinline__ void s16_frag(uint32_t c0, uint32_t c1, int isc, g16h
 
 __device__ __forceinline__ void s16_opaque(float &v) { asm volatile("" : "+v"(v)); }
 
-template <int T>
+// Staged activations (the megakernel's QMV flags, qwen_megakernel.cu:468-551): v = silu(x) * x2 with SILU_MUL, then
+// v * (rs[t] * nw[c]) with NORM, rs[t] = 1 / sqrt(mean(v^2) + eps) from s16_rms_kernel, before quantization; ADD
+// adds y's previous value to the result (in the K-range sum when there are several ranges). silu(z) = z / (1 +
+// e^-z) with the hardware exp2 and reciprocal, as the streaming kernel's staging.
+__device__ __forceinline__ float s16_silu(float z) {
+    return z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * 1.4426950408889634f));
+}
+
+// rs[t] = 1 / sqrt(sum_c v[t][c]^2 / cols + eps) of the staged (silu_mul-ed) values: one 256-thread workgroup per
+// token, float4 per thread and step, then a fixed-order tree; deterministic.
+__global__ __launch_bounds__(256) inline void s16_rms_kernel(const float *__restrict__ x, XStage xs, int cols,
+                                                             float *__restrict__ rs) {
+    __shared__ float red[256];
+    const int t = blockIdx.x;
+    const float4 *xr = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols);
+    const float4 *mr = reinterpret_cast<const float4 *>(xs.x2 + static_cast<size_t>(t) * cols);
+    const bool silu = (xs.flags & VQ_STAGE_SILU_MUL) != 0;
+    float acc = 0.0f;
+    for (int i = threadIdx.x; i < cols / 4; i += 256) {
+        float4 f = xr[i];
+        if (silu) {
+            const float4 m = mr[i];
+            f = float4{s16_silu(f.x) * m.x, s16_silu(f.y) * m.y, s16_silu(f.z) * m.z, s16_silu(f.w) * m.w};
+        }
+        acc = fmaf(f.x, f.x, acc);
+        acc = fmaf(f.y, f.y, acc);
+        acc = fmaf(f.z, f.z, acc);
+        acc = fmaf(f.w, f.w, acc);
+    }
+    red[threadIdx.x] = acc;
+    for (int h = 128; h > 0; h >>= 1) {
+        __syncthreads();
+        if (static_cast<int>(threadIdx.x) < h) red[threadIdx.x] += red[threadIdx.x + h];
+    }
+    if (threadIdx.x == 0) rs[t] = 1.0f / sqrtf(red[0] / static_cast<float>(cols) + xs.eps);
+}
+
+// STG: the staged instance (vq_qmv_staged_ws); the plain one compiles without the staging code (with it, the
+// plain batch-8 MLP block measured 95 -> 119 us: the compiler's load scheduling and registers change).
+template <int T, bool STG>
 __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S16Jobs J, int cols, long row_bytes,
-                                                              const float *__restrict__ x, int ntok) {
+                                                              const float *__restrict__ x, int ntok, const XStage xs,
+                                                              const float *__restrict__ rs) {
     using S = Sl<T>;
     constexpr int SPL = S::SPB / 4;  // slices per lane per super-block: a lane owns a quarter of it
     constexpr int NP = S::NP;
@@ -189,8 +229,11 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S1
     const bool has_group = tid < ntok * ngr;
     const int gt = has_group ? tid / ngr : 0, gg = has_group ? tid - gt * ngr : 0;
     float v[32];
+    const bool st_silu = STG && (xs.flags & VQ_STAGE_SILU_MUL) != 0, st_norm = STG && (xs.flags & VQ_STAGE_NORM) != 0;
+    float m2[32], nwv[32];  // staging inputs, loaded before the weights like x
     if (has_group) {
-        const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(gt) * cols + k0 + 32 * gg);
+        const size_t off = static_cast<size_t>(gt) * cols + k0 + 32 * gg;
+        const float4 *src = reinterpret_cast<const float4 *>(x + off);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const float4 f = src[q];
@@ -199,10 +242,41 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S1
             v[4 * q + 2] = f.z;
             v[4 * q + 3] = f.w;
         }
+        if (st_silu) {
+            const float4 *s2 = reinterpret_cast<const float4 *>(xs.x2 + off);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 f = s2[q];
+                m2[4 * q] = f.x;
+                m2[4 * q + 1] = f.y;
+                m2[4 * q + 2] = f.z;
+                m2[4 * q + 3] = f.w;
+            }
+        }
+        if (st_norm) {
+            const float4 *sn = reinterpret_cast<const float4 *>(xs.nw + k0 + 32 * gg);
+            const float r = rs[gt];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 f = sn[q];
+                nwv[4 * q] = r * f.x;
+                nwv[4 * q + 1] = r * f.y;
+                nwv[4 * q + 2] = r * f.z;
+                nwv[4 * q + 3] = r * f.w;
+            }
+        }
     }
     const int tile = blockIdx.x - J.tile0[jb];
     typename S::W wr[kS16NSB][SPL];
     load_tile(tile, wr);
+    if (has_group && st_silu) {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) v[k] = s16_silu(v[k]) * m2[k];
+    }
+    if (has_group && st_norm) {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) v[k] *= nwv[k];  // v * (rs * nw), as the streaming kernel's staging
+    }
 
     // 2. The activation slice: int8 codes per 32-group (the CPU path's quantize_group), then per token the
     // power of two 2^e with 127 max(xd) 2^e < 2^15, then b = xq * (xd 2^e) split into two f16.
@@ -321,10 +395,11 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S1
     // 4. Out: rows 16 wv + 4 lk + j of the tile for token lr, back from the token's 2^e (partials of K range kr
     // when the columns span several ranges).
     if (tok_ok) {
+        const bool add = STG && (xs.flags & VQ_STAGE_ADD) != 0 && kw == cols;  // one K range: o is y itself
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int r = tile * kS16Rows + 16 * wv + 4 * lk + j;
-            if (r < rows) o[r] = acc[j] * is;
+            if (r < rows) o[r] = add ? acc[j] * is + o[r] : acc[j] * is;
         }
     }
 }
@@ -354,12 +429,12 @@ __global__ __launch_bounds__(256) inline void s16_sum_kernel(const float *__rest
 
 // The same, one output per thread (any n).
 __global__ __launch_bounds__(256) inline void s16_sum1_kernel(const float *__restrict__ part, int nkr, long n,
-                                                             float *__restrict__ y) {
+                                                             float *__restrict__ y, bool add) {
     const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
     if (i >= n) return;
     float v = part[i];
     for (int k = 1; k < nkr; ++k) v += part[static_cast<size_t>(k) * n + i];
-    y[i] = v;
+    y[i] = add ? v + y[i] : v;
 }
 
 // The K-range sums of several jobs in one launch: job j's n[j] outputs (a multiple of 4) are the float4
@@ -371,7 +446,7 @@ struct S16Sum {
     long e0[kS16MaxJobs + 1];
     int jobs;
 };
-__global__ __launch_bounds__(256) inline void s16_sum_jobs_kernel(S16Sum P, int nkr) {
+__global__ __launch_bounds__(256) inline void s16_sum_jobs_kernel(S16Sum P, int nkr, bool add) {
     const long e = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
     if (e >= P.e0[P.jobs]) return;
     int jb = 0;
@@ -392,18 +467,25 @@ __global__ __launch_bounds__(256) inline void s16_sum_jobs_kernel(S16Sum P, int 
         const float4 a = p[k * st];
         v.x += a.x, v.y += a.y, v.z += a.z, v.w += a.w;
     }
-    *reinterpret_cast<float4 *>(P.y[jb] + i) = v;
+    float4 *const dst = reinterpret_cast<float4 *>(P.y[jb] + i);
+    if (add) {  // ADD staging flag: the sum of the ranges plus y's previous value
+        const float4 o = *dst;
+        v.x += o.x, v.y += o.y, v.z += o.z, v.w += o.w;
+    }
+    *dst = v;
 }
 
 // n <= kS16MaxJobs matrices of type T sharing cols and x: one qmv16 launch over all their row tiles, then one
 // launch of K-range sums (several K ranges: `part` holds the sum of s16_part_bytes(rows[j], cols, ntok)).
 template <int T>
 int launch_small16_group(int n, const uint8_t *const *w, const int *rows, float *const *y, int cols, long rb,
-                         const float *x, int ntok, float *part, hipStream_t s) {
+                         const float *x, int ntok, float *part, hipStream_t s, const XStage &xs, float *rs) {
     if constexpr (!kSmall16<T>) {
         (void)n, (void)w, (void)rows, (void)y, (void)cols, (void)rb, (void)x, (void)ntok, (void)part, (void)s;
+        (void)xs, (void)rs;
         return static_cast<int>(hipErrorInvalidValue);
     } else {
+        if ((xs.flags & VQ_STAGE_NORM) && rs == nullptr) return static_cast<int>(hipErrorInvalidValue);
         if (n < 1 || n > kS16MaxJobs || ntok < 1 || ntok > 16 || cols % 256 != 0)
             return static_cast<int>(hipErrorInvalidValue);
         const int nkr = s16_ranges(cols);
@@ -419,8 +501,17 @@ int launch_small16_group(int n, const uint8_t *const *w, const int *rows, float 
             if (nkr > 1) pp += s16_part_bytes(rows[k], cols, ntok);
             J.tile0[k + 1] = J.tile0[k] + (rows[k] + kS16Rows - 1) / kS16Rows;
         }
+        if (xs.flags & VQ_STAGE_NORM) {
+            s16_rms_kernel<<<dim3(ntok), dim3(256), 0, s>>>(x, xs, cols, rs);
+            const hipError_t e0 = hipGetLastError();
+            if (e0 != hipSuccess) return static_cast<int>(e0);
+        }
+        const bool add = (xs.flags & VQ_STAGE_ADD) != 0;
         const dim3 grid(J.tile0[n], nkr), block(64 * kS16Waves);
-        qmv16_kernel<T><<<grid, block, s16_lds(ntok), s>>>(J, cols, rb, x, ntok);
+        if (xs.flags != 0)
+            qmv16_kernel<T, true><<<grid, block, s16_lds(ntok), s>>>(J, cols, rb, x, ntok, xs, rs);
+        else
+            qmv16_kernel<T, false><<<grid, block, s16_lds(ntok), s>>>(J, cols, rb, x, ntok, xs, rs);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || nkr == 1) return static_cast<int>(e);
         bool vec = true;
@@ -437,11 +528,11 @@ int launch_small16_group(int n, const uint8_t *const *w, const int *rows, float 
                 P.n[k] = static_cast<long>(ntok) * rows[k];
                 P.e0[k + 1] = P.e0[k] + P.n[k] / 4;
             }
-            s16_sum_jobs_kernel<<<static_cast<unsigned>((P.e0[n] + 255) / 256), 256, 0, s>>>(P, nkr);
+            s16_sum_jobs_kernel<<<static_cast<unsigned>((P.e0[n] + 255) / 256), 256, 0, s>>>(P, nkr, add);
         } else {
             for (int k = 0; k < n; ++k) {
                 const long m = static_cast<long>(ntok) * rows[k];
-                s16_sum1_kernel<<<static_cast<unsigned>((m + 255) / 256), 256, 0, s>>>(J.out[k], nkr, m, y[k]);
+                s16_sum1_kernel<<<static_cast<unsigned>((m + 255) / 256), 256, 0, s>>>(J.out[k], nkr, m, y[k], add);
             }
         }
         e = hipGetLastError();
@@ -451,8 +542,8 @@ int launch_small16_group(int n, const uint8_t *const *w, const int *rows, float 
 
 template <int T>
 int launch_small16(const uint8_t *w, int rows, int cols, long rb, const float *x, int ntok, float *y, float *part,
-                   hipStream_t s) {
-    return launch_small16_group<T>(1, &w, &rows, &y, cols, rb, x, ntok, part, s);
+                   hipStream_t s, const XStage &xs, float *rs) {
+    return launch_small16_group<T>(1, &w, &rows, &y, cols, rb, x, ntok, part, s, xs, rs);
 }
 
 }  // namespace vq

@@ -420,8 +420,9 @@ class Runtime:
         """y[t] (+)= W v[t] with the activations staged inside the matvec, as the megakernel's QMV flags do
         (qwen_megakernel.cu:468-551; runtime/instructions.py:179-182): v = silu(x) * x2 when x2 is given, then
         rmsnorm(v) * norm when norm (an F32 tensor or fp32 buffer of cols values) is given; add=True
-        accumulates into y. Quantized weights, cols <= 24576. No counterpart in the per-op runtime, whose
-        callers run silu_mul, rmsnorm and add as passes of their own."""
+        accumulates into y. Quantized weights; cols <= 24576 except on the small-batch path (5-16 tokens of
+        Q3_K..Q6_K and the IQ types but IQ4_NL, any cols multiple of 256). No counterpart in the per-op runtime,
+        whose callers run silu_mul, rmsnorm and add as passes of their own."""
         if ntok < 1:
             raise ValueError("ntok must be positive")
         t = self._tensor(weight)
@@ -444,8 +445,13 @@ class Runtime:
                 nwp = nt.data.data_ptr()
             else:
                 nwp = self._f32_buffer(norm, t.cols).data_ptr()
-        st = self._lib.vq_qmv_staged(t.type, t.data.data_ptr(), t.rows, t.cols, xb.data_ptr(), x2p, nwp, float(eps),
-                                     flags, ntok, yb.data_ptr(), self._stream())
+        # 5-16 tokens of the f16 small-batch types stage inside that kernel (vq_qmv_staged_ws, with the RMS
+        # prepass and partial sums in the runtime's workspace); other calls stream (vq_qmv_staged).
+        nws = self._lib.vq_qmv_staged_workspace_bytes(t.type, t.rows, t.cols, ntok)
+        ws = self._workspace(nws) if nws else None
+        st = self._lib.vq_qmv_staged_ws(t.type, t.data.data_ptr(), t.rows, t.cols, xb.data_ptr(), x2p, nwp,
+                                        float(eps), flags, ntok, yb.data_ptr(), ws.data_ptr() if ws is not None else None,
+                                        nws, self._stream())
         _lib.check(st, "qmv_staged launch")
 
     # ---- ops around the matvec (the reference runtime's elementwise / norm ops) ------------------------------
