@@ -34,6 +34,27 @@ struct SegTable {
     Seg s[VQ_MAX_SEGMENTS];
 };
 
+// Cross-row lane exchanges of gfx950 without LDS: v_permlane16_swap (rows 0<->1, 2<->3) and v_permlane32_swap (lane
+// halves). Called with the same value twice, the pair holds each lane's value and its partner's (lane ^ 16 or
+// lane ^ 32) in an order that depends on the lane, so max and (commutative) sums come out bit-identical on both
+// partners, as with __shfl_xor.
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_add(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_add(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Global row index g (segments in table order) -> (segment, row within it).
 __device__ __forceinline__ const Seg &seg_of_row(const SegTable &T, int g, int &local) {
     int i = 0;
@@ -456,8 +477,8 @@ __device__ __forceinline__ void fa_keys(const C *__restrict__ kc, const C *__res
                 v[r] = p >= qs && p < qe && p < k_hi ? sc[r] : -INFINITY;
                 bm = fmaxf(bm, v[r]);
             }
-            bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+            bm = xor16_max(bm);
+            bm = xor32_max(bm);
             const float mn = fmaxf(m, bm);
             const float alpha = mn == -INFINITY ? 1.0f : expf(m - mn);  // 0 on the first visible block
             float pr[4], ps = 0.0f;
@@ -466,8 +487,8 @@ __device__ __forceinline__ void fa_keys(const C *__restrict__ kc, const C *__res
                 pr[r] = v[r] == -INFINITY ? 0.0f : expf(v[r] - mn);
                 ps += pr[r];
             }
-            ps += __shfl_xor(ps, 16, 64);
-            ps += __shfl_xor(ps, 32, 64);
+            ps = xor16_add(ps);
+            ps = xor32_add(ps);
             l = l * alpha + ps;
             m = mn;
             const float *vrow = tl.vt + col * kFaLdk + 16 * sub + 4 * grp;
@@ -650,8 +671,8 @@ __device__ __forceinline__ float fa16_q_split(const float4 (&qr)[HD / 16], float
     for (int i = 0; i < HD / 16; ++i)
         amax = fmaxf(fmaxf(amax, fmaxf(fabsf(qr[i].x), fabsf(qr[i].y))), fmaxf(fabsf(qr[i].z), fabsf(qr[i].w)));
     amax *= scale;
-    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    amax = xor16_max(amax);
+    amax = xor32_max(amax);
     int ex = 0;
     if (amax > 0.0f && amax <= 3.0e38f) frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
     const float up = ldexpf(1.0f, 14 - ex);
@@ -722,8 +743,8 @@ __device__ __forceinline__ void fa16_softmax_pv(const fa4 (&s)[2], int kb, int k
             v[4 * h + r] = p >= qs && p < qe && p < k_hi ? s[h][r] : -INFINITY;
             bm = fmaxf(bm, v[4 * h + r]);
         }
-    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    bm = xor16_max(bm);
+    bm = xor32_max(bm);
     const float mn = fmaxf(m, bm);
     const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
     fh8 ph, pl;
@@ -737,8 +758,8 @@ __device__ __forceinline__ void fa16_softmax_pv(const fa4 (&s)[2], int kb, int k
         ph[j] = hh;
         pl[j] = ll;
     }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
+    ps = xor16_add(ps);
+    ps = xor32_add(ps);
     l = l * alpha + ps;
     m = mn;
 #pragma unroll
@@ -1158,11 +1179,9 @@ __global__ __launch_bounds__(256) void conv_update_kernel(const float *__restric
 // once per pass (fp32, or fp16 widened to fp32 in registers and rounded once when written back).
 constexpr int kGdCols = 8, kGdGroups = 64 / kGdCols, kGdMaxKd = 256;
 
-__device__ __forceinline__ float gsum(float v) {  // sum over the 8 row groups of a column
-    v += __shfl_xor(v, 8, 64);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+__device__ __forceinline__ float gsum(float v) {  // sum over the 8 row groups of a column (lanes 8, 16, 32 apart)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+    return xor32_add(xor16_add(v));
 }
 __device__ __forceinline__ float ld_state(const float *p) { return *p; }
 __device__ __forceinline__ float ld_state(const _Float16 *p) { return static_cast<float>(*p); }
