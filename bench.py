@@ -831,8 +831,9 @@ def stamps_report(torch) -> dict:
 
     from vinf_3080ti_amd.build import STAMPS_LIB
 
-    hip = Hip(torch, STAMPS_LIB)
-    raw = ctypes.CDLL(str(STAMPS_LIB))
+    lib_path = Path(os.environ.get("VQ_STAMPS_LIB", STAMPS_LIB))  # another timing build, for comparisons
+    hip = Hip(torch, lib_path)
+    raw = ctypes.CDLL(str(lib_path))
     n = 8192 * 8
 
     def read(tu):
@@ -845,7 +846,7 @@ def stamps_report(torch) -> dict:
              ("Q4_K down 5120x17408", "q4_k", [(Q4_K, 5120, 17408)], 17408),
              ("Q6_K out 5120x6144", "q6_k", [(Q6_K, 5120, 6144)], 6144),
              ("Q4_K 4096x4096 (config 1)", "q4_k", [(Q4_K, 4096, 4096)], 4096)]
-    slots = {5: "last_wave_entry", 4: "thread0_activations_quantized", 1: "startup_barrier",
+    slots = {5: "last_wave_entry", 4: "thread0_activations_quantized", 1: "startup_barrier", 7: "slot7",
              6: "wave0_first_stage_landed", 2: "all_waves_loop_done", 3: "end"}
     out = {}
     for name, tu, mats, cols in cases:

@@ -148,14 +148,20 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, long r) {
     return (static_cast<unsigned long long>(o) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(r));
 }
 
-// Timing builds only (-DVQ_STAMPS, never in the shipped library): per-workgroup s_memrealtime stamps.
+// Timing builds only (-DVQ_STAMPS, never in the shipped library): per-workgroup s_memrealtime stamps, kept in LDS
+// until the end (global stores would add to the vmcnt waits the kernel makes) and written out by thread 0 then.
 #ifdef VQ_STAMPS
 static __device__ unsigned long long g_stamps[8192 * 8];
 #define VQ_STAMP_IF(cond, slot)                                                                                \
     do {                                                                                                       \
-        if (cond) g_stamps[blockIdx.x * 8 + (slot)] = __builtin_amdgcn_s_memrealtime();                        \
+        if (cond) s_stamp[slot] = __builtin_amdgcn_s_memrealtime();                                            \
     } while (0)
 #define VQ_STAMP(slot) VQ_STAMP_IF(threadIdx.x == 0, slot)
+#define VQ_STAMP_FLUSH()                                                                                       \
+    do {                                                                                                       \
+        __syncthreads();                                                                                       \
+        if (threadIdx.x < 8) g_stamps[blockIdx.x * 8 + threadIdx.x] = s_stamp[threadIdx.x];                    \
+    } while (0)
 #define VQ_STAMP_READER(NAME)                                                                                  \
     extern "C" int NAME(void *dst, size_t bytes) {                                                             \
         return static_cast<int>(hipMemcpyFromSymbol(dst, HIP_SYMBOL(vq::g_stamps), bytes, 0, hipMemcpyDeviceToHost)); \
@@ -163,6 +169,7 @@ static __device__ unsigned long long g_stamps[8192 * 8];
 #else
 #define VQ_STAMP_IF(cond, slot)
 #define VQ_STAMP(slot)
+#define VQ_STAMP_FLUSH()
 #define VQ_STAMP_READER(NAME)
 #endif
 
@@ -200,8 +207,10 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     __shared__ int s_next;                        // next stage to hand out
     __shared__ unsigned long long s_best[NT][NW];  // argmax reduction
 
+#ifdef VQ_STAMPS
+    __shared__ unsigned long long s_stamp[8];
+#endif
     VQ_STAMP(0);
-    VQ_STAMP_IF(threadIdx.x == blockDim.x - 64, 5);
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nu = (cols >> 5) / S::UG;
@@ -386,6 +395,8 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
             }
         }
         VQ_STAMP(4);
+        VQ_STAMP_IF(threadIdx.x == 128, 5);
+        VQ_STAMP_IF(threadIdx.x == 256, 7);
         }
     } else {
         for (int p = wv; p < xreg / 1024; p += NW) {
@@ -397,7 +408,17 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     }
     wait_vm<0>();
     __builtin_amdgcn_sched_barrier(0);
-    if (s >= 0) load_stage(s, RA);  // waves without a stage load nothing
+    // When a minority of the waves fetched activations or tables, those request their first stage only after the
+    // start-up barrier: by the time they are done, the other waves' first stages fill the CU's request queue, and
+    // issuing a load then stalls the wave until the queue drains (~1-2 us measured), holding every wave at the
+    // barrier. (When most waves fetch activations, e.g. a 17408-wide input, requesting late leaves the stream idle
+    // through the start-up instead: measured slower.)
+    int nact = 0;  // waves with start-up fetches: the first nact
+    if constexpr (XF32) nact = STG ? NW : (2 * NT * xi.ng + 63) / 64;
+    else nact = xreg / 1024;
+    if constexpr (TB > 0) nact = nact > TB / 1024 ? nact : TB / 1024;
+    const bool late = wv < nact && 2 * nact <= NW;
+    if (s >= 0 && !late) load_stage(s, RA);  // waves without a stage load nothing
     // Stages 0 .. 2 NW - 1 are static: wave w takes w, then w + NW (no ticket round trip before the first
     // decode); tickets hand out the rest.
     const int s2 = wv + NW < nst ? wv + NW : -1;
@@ -629,6 +650,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     // One lane takes the ticket (a wave-wide atomic would take one per lane); readfirstlane shares it.
     auto take = [&]() { return lane == 0 ? atomicAdd(&s_next, 1) : 0; };
     int ask = s2 >= 0 ? s2 : nst;  // the stage after s (valid in lane 0): the static second stage
+    if (s >= 0 && late) load_stage(s, RA);
 #ifdef VQ_STAMPS
     bool first_stage = true;
 #endif
@@ -709,6 +731,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
 #ifdef VQ_STAMPS
     __syncthreads();
     VQ_STAMP(3);
+    VQ_STAMP_FLUSH();
 #endif
     if (jobs.amax != nullptr) {
 #pragma unroll
