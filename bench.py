@@ -822,9 +822,10 @@ def cpu_baseline() -> dict:
 def stamps_report(torch) -> dict:
     """Per-workgroup timeline of the sweep's streaming launches from the timing build (vinf_3080ti_amd/_var/
     libvq_stamps.so, `python -m vinf_3080ti_amd.build --stamps`): each workgroup's thread 0 stamps s_memrealtime
-    (100 MHz) at entry, after its activations are quantized, at the start-up barrier, when wave 0's first weight
-    stage has landed, after every wave's last stage and at the end; the last wave stamps its entry. Launches run one
-    at a time after a producer kernel writes x, rotating over 6 weight copies; medians over 10 launches."""
+    (100 MHz, kept in LDS until the end) at entry, when waves 0, 2 and 4 have quantized their activations, at the
+    start-up barrier, when wave 0's first weight stage has landed, after every wave's last stage and at the end.
+    Launches run one at a time after a producer kernel writes x, rotating over 6 weight copies; medians over 10
+    launches."""
     import ctypes
 
     import numpy as np
@@ -846,7 +847,8 @@ def stamps_report(torch) -> dict:
              ("Q4_K down 5120x17408", "q4_k", [(Q4_K, 5120, 17408)], 17408),
              ("Q6_K out 5120x6144", "q6_k", [(Q6_K, 5120, 6144)], 6144),
              ("Q4_K 4096x4096 (config 1)", "q4_k", [(Q4_K, 4096, 4096)], 4096)]
-    slots = {5: "last_wave_entry", 4: "thread0_activations_quantized", 1: "startup_barrier", 7: "slot7",
+    slots = {4: "wave0_activations_quantized", 5: "wave2_activations_quantized", 7: "wave4_activations_quantized",
+             1: "startup_barrier",
              6: "wave0_first_stage_landed", 2: "all_waves_loop_done", 3: "end"}
     out = {}
     for name, tu, mats, cols in cases:
