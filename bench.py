@@ -983,6 +983,9 @@ def main() -> None:
         out = {}
         for rows, cols in ((17408, 5120), (5120, 17408)):
             out[f"Q4_K_{rows}x{cols}_M512"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512)
+        # The other types of a UD-Q3_K_XL prompt pass: FFN gate/up (Q3_K), attention/SSM projections (Q5_K, Q6_K).
+        for ty, rows, cols in ((Q3_K, 17408, 5120), (Q6_K, 5120, 17408), (Q5_K, 10240, 5120), (Q6_K, 5120, 6144)):
+            out[f"{TYPE_NAMES[ty]}_{rows}x{cols}_M512"] = bench_gemm(torch, hip, ty, rows, cols, 512)
         print(json.dumps({"prefill": out}), flush=True)
         return
     if args.mlp_only:
