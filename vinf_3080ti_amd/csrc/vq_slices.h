@@ -578,10 +578,13 @@ struct Sl<VQ_IQ2_XXS> {
     static constexpr int OFF = 0;
     static __device__ __forceinline__ void codes(const W &w, int, const Tabs &tb, uint32_t (&cc)[NP][4]) {
         const uint32_t a0 = w.a.word(0), a1 = w.a.word(1);
+        // The four grid reads first, so their LDS round trips overlap.
+        uint2 g[4];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) g[l] = tb.grid8[bfe(a0, 8 * l, 8)];
 #pragma unroll
         for (int l = 0; l < 4; ++l)
-            sign8(tb.grid8[bfe(a0, 8 * l, 8)], ksigns8(bfe(a1, 7 * l, 7)), cc[l >> 1][2 * (l & 1)],
-                  cc[l >> 1][2 * (l & 1) + 1]);
+            sign8(g[l], ksigns8(bfe(a1, 7 * l, 7)), cc[l >> 1][2 * (l & 1)], cc[l >> 1][2 * (l & 1) + 1]);
     }
     static __device__ __forceinline__ void scales(const W &w, int, float *sc, float *mn) {
         sc[0] = sc[1] = half_to_float(w.d.lo()) * (0.5f + static_cast<float>(w.a.word(1) >> 28)) * 0.25f;
@@ -615,11 +618,12 @@ struct Sl<VQ_IQ2_XS> {
     static constexpr int OFF = 0;
     static __device__ __forceinline__ void codes(const W &w, int, const Tabs &tb, uint32_t (&cc)[NP][4]) {
         const uint32_t a[2] = {w.a.word(0), w.a.word(1)};
+        uint2 g[4];  // the four grid reads first, so their LDS round trips overlap
 #pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            const uint32_t q = bfe(a[l >> 1], 16 * (l & 1), 16);
-            sign8(tb.grid8[q & 511u], ksigns8(q >> 9), cc[l >> 1][2 * (l & 1)], cc[l >> 1][2 * (l & 1) + 1]);
-        }
+        for (int l = 0; l < 4; ++l) g[l] = tb.grid8[bfe(a[l >> 1], 16 * (l & 1), 9)];
+#pragma unroll
+        for (int l = 0; l < 4; ++l)
+            sign8(g[l], ksigns8(bfe(a[l >> 1], 16 * (l & 1) + 9, 7)), cc[l >> 1][2 * (l & 1)], cc[l >> 1][2 * (l & 1) + 1]);
     }
     static __device__ __forceinline__ void scales(const W &w, int, float *sc, float *mn) {
         const float d = half_to_float(w.d.lo());
@@ -660,11 +664,12 @@ struct Sl<VQ_IQ2_S> {
     static constexpr int OFF = 0;
     static __device__ __forceinline__ void codes(const W &w, int, const Tabs &tb, uint32_t (&cc)[NP][4]) {
         const uint32_t qs = w.qs.word(0), sg = w.sg.word(0), qh = w.qh.lo();
+        uint2 g[4];  // the four grid reads first, so their LDS round trips overlap
 #pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            const uint32_t idx = bfe(qs, 8 * l, 8) | (bfe(qh, 2 * l, 2) << 8);
-            sign8(tb.grid8[idx], bfe(sg, 8 * l, 8), cc[l >> 1][2 * (l & 1)], cc[l >> 1][2 * (l & 1) + 1]);
-        }
+        for (int l = 0; l < 4; ++l) g[l] = tb.grid8[bfe(qs, 8 * l, 8) | (bfe(qh, 2 * l, 2) << 8)];
+#pragma unroll
+        for (int l = 0; l < 4; ++l)
+            sign8(g[l], bfe(sg, 8 * l, 8), cc[l >> 1][2 * (l & 1)], cc[l >> 1][2 * (l & 1) + 1]);
     }
     static __device__ __forceinline__ void scales(const W &w, int, float *sc, float *mn) {
         const float d = half_to_float(w.d.lo());
@@ -705,11 +710,13 @@ struct Sl<VQ_IQ3_XXS> {
     static __device__ __forceinline__ void codes(const W &w, int, const Tabs &tb, uint32_t (&cc)[NP][4]) {
         const uint32_t q[2] = {w.q.word(0), w.q.word(1)};
         const uint32_t aux = w.aux.word(0);
+        uint2 g[4];  // the eight grid reads first, so their LDS round trips overlap
 #pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            const uint2 g{tb.grid4[bfe(q[l >> 1], 16 * (l & 1), 8)], tb.grid4[bfe(q[l >> 1], 16 * (l & 1) + 8, 8)]};
-            sign8(g, ksigns8(bfe(aux, 7 * l, 7)), cc[l >> 1][2 * (l & 1)], cc[l >> 1][2 * (l & 1) + 1]);
-        }
+        for (int l = 0; l < 4; ++l)
+            g[l] = uint2{tb.grid4[bfe(q[l >> 1], 16 * (l & 1), 8)], tb.grid4[bfe(q[l >> 1], 16 * (l & 1) + 8, 8)]};
+#pragma unroll
+        for (int l = 0; l < 4; ++l)
+            sign8(g[l], ksigns8(bfe(aux, 7 * l, 7)), cc[l >> 1][2 * (l & 1)], cc[l >> 1][2 * (l & 1) + 1]);
     }
     static __device__ __forceinline__ void scales(const W &w, int, float *sc, float *mn) {
         sc[0] = sc[1] = half_to_float(w.d.lo()) * (0.5f + static_cast<float>(w.aux.word(0) >> 28)) * 0.5f;
@@ -746,18 +753,22 @@ struct Sl<VQ_IQ3_S> {
     static constexpr int OFF = 0;
     static __device__ __forceinline__ void codes(const W &w, int, const Tabs &tb, uint32_t (&cc)[NP][4]) {
         const uint32_t qh = w.qh.lo();
+        uint32_t g[2][8];  // the sixteen grid reads first, so their LDS round trips overlap
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
             const uint32_t q[2] = {w.qs.word(2 * gg), w.qs.word(2 * gg + 1)};
+#pragma unroll
+            for (int l = 0; l < 8; ++l) g[gg][l] = tb.grid4[bfe(q[l >> 2], 8 * (l & 3), 8) | (bfe(qh, 8 * gg + l, 1) << 8)];
+        }
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
             const uint32_t sg = w.sg.word(gg);
 #pragma unroll
             for (int m2 = 0; m2 < 4; ++m2) {  // entries 2*m2, 2*m2+1 of group gg share sign byte m2
                 const int l0 = 2 * m2, l1 = 2 * m2 + 1;
-                const uint32_t i0 = bfe(q[l0 >> 2], 8 * (l0 & 3), 8) | (bfe(qh, 8 * gg + l0, 1) << 8);
-                const uint32_t i1 = bfe(q[l1 >> 2], 8 * (l1 & 3), 8) | (bfe(qh, 8 * gg + l1, 1) << 8);
                 const uint32_t s8 = bfe(sg, 8 * m2, 8);
-                cc[2 * gg + (l0 >> 2)][l0 & 3] = sign4(tb.grid4[i0], s8 & 15u);
-                cc[2 * gg + (l1 >> 2)][l1 & 3] = sign4(tb.grid4[i1], s8 >> 4);
+                cc[2 * gg + (l0 >> 2)][l0 & 3] = sign4(g[gg][l0], s8 & 15u);
+                cc[2 * gg + (l1 >> 2)][l1 & 3] = sign4(g[gg][l1], s8 >> 4);
             }
         }
     }
