@@ -79,9 +79,11 @@ def test_host_side_argument_checks(lib):
     assert lib.vq_qmv_group(int(T.F32), 2, arr, rws, arr, 256, fake, 1, None) == _lib.VQ_ERR_TYPE
     assert lib.vq_qmv_group(int(T.Q4_K), 2, arr, rws, arr, 100, fake, 1, None) == _lib.VQ_ERR_SHAPE
     assert lib.vq_lmhead_argmax_workspace_bytes(int(T.F16), 4, 256, 1) == 0
-    # prefill: the f16-MFMA path (Q4_K/Q5_K) needs the split activations (2 x f16 per element) and more
-    assert lib.vq_qgemm_workspace_bytes(int(T.Q6_K), 17408, 5120, 512) == 0
-    assert lib.vq_qgemm_workspace_bytes(int(T.Q3_K), 17408, 5120, 512) == 0
+    # prefill: the f16-MFMA path (Q3_K-Q6_K) needs the split activations (2 x f16 per element) and more
+    assert lib.vq_qgemm_workspace_bytes(int(T.Q6_K), 17408, 5120, 512) >= 4 * 512 * 5120
+    assert lib.vq_qgemm_workspace_bytes(int(T.Q3_K), 17408, 5120, 512) >= 4 * 512 * 5120
+    assert lib.vq_qgemm_workspace_bytes(int(T.Q8_0), 17408, 5120, 512) == 0
+    assert lib.vq_qgemm_workspace_bytes(int(T.IQ4_XS), 17408, 5120, 512) == 0
     assert lib.vq_qgemm_workspace_bytes(int(T.Q4_K), 17408, 5120, 512) >= 4 * 512 * 5120
     assert lib.vq_qgemm_workspace_bytes(int(T.Q4_K), 17408, 5120, 0) == 0
     assert lib.vq_qgemm_ws(int(T.Q4_K), fake, 4, 256, fake, 1, fake, None, 0, None) == _lib.VQ_ERR_WORKSPACE

@@ -47,7 +47,7 @@ def _gemm(torch, lib, _lib, ty, wd, rows, cols, x, flags):
                          ids=lambda v: v.name if isinstance(v, T) else str(v))
 def test_qgemm_batch_invariant(env, oracle_mod, ty, rows, cols):
     """The same tokens alone, in a batch of 7 and at rows 131 .. of a 300-token batch (a third token tile):
-    bit-identical outputs under VQ_GEMM_BATCH_INVARIANT (the f16 path of Q4_K/Q5_K splits K by the matrix only;
+    bit-identical outputs under VQ_GEMM_BATCH_INVARIANT (the f16 path of Q3_K-Q6_K splits K by the matrix only;
     the int8 path of the other types takes the whole K range per tile), all within the bar."""
     torch, lib, _lib = env
     rng = np.random.default_rng(rows + cols + int(ty))
@@ -72,8 +72,7 @@ def test_qgemm_batch_invariant(env, oracle_mod, ty, rows, cols):
 
 def test_runtime_batch_invariant_mode(oracle_mod):
     """Runtime.set_batch_invariant: qmv of a token alone and inside batches of 4 and 12, qmv_group and
-    lmhead_argmax agree bit for bit; paged attention of one sequence alone and beside two others (one a prompt
-    segment) agrees bit for bit."""
+    lmhead_argmax agree bit for bit."""
     torch = pytest.importorskip("torch")
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
@@ -106,22 +105,41 @@ def test_runtime_batch_invariant_mode(oracle_mod):
         assert np.array_equal(g[3].view(np.uint32), outs[0].view(np.uint32))
         assert rt.lmhead_argmax("w", "x", 4) == [int(np.argmax(outs[0]))] * 4
 
-    heads, kvh, hd, page, pps, slots = 8, 2, 128, 16, 8, 3
+    rt.set_batch_invariant(False)
+    assert rt.gemm_min_rows == 0
+
+
+@pytest.mark.parametrize("elem,hd", [(4, 128), (2, 128), (2, 256)])
+def test_runtime_batch_invariant_attention(elem, hd):
+    """Batch-invariant paged attention, fp32 and fp16 page pools (fp16 takes the f16 prompt kernel): one
+    sequence's 3-token segment alone and beside a decode token and a 20-token prompt agrees bit for bit."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from vinf_3080ti_amd.runtime import HipWeightRuntime
+
+    rt = HipWeightRuntime()
+    rt.set_batch_invariant(True)
+    rng = np.random.default_rng(50 + elem + hd)
+    dt = np.float32 if elem == 4 else np.float16
+    heads, kvh, page, pps, slots = 8, 2, 16, 8, 3
     pt = rng.permutation(pps * slots).astype(np.int32)
     rt.alloc("pt", pt.size)
     rt.write("pt", pt.tobytes())
     rt.set_paging("pt", page, pps, slots)
-    pool = (rng.standard_normal((pps * slots, kvh, page, hd)) * 0.3).astype(np.float32)
+    pool = (rng.standard_normal((pps * slots, kvh, page, hd)) * 0.3).astype(dt)
     for name in ("pk", "pv"):
-        rt.alloc(name, pool.size)
+        rt.alloc(name, pool.size, elem)
         rt.write(name, pool.tobytes())
     q1 = rng.standard_normal((3, heads, hd)).astype(np.float32)
     rt.set_segments([(1, 40, 3)])
     rt.alloc("q", q1.size)
     rt.write("q", q1.tobytes())
     rt.alloc("o", q1.size)
+    print(f"invariant attention elem {elem} hd {hd}", flush=True)
     rt.attention_seg("q", "pk", "pv", "o", heads, kvh, hd)
     alone = np.array(rt.read_floats("o"), np.float32)
+    assert np.isfinite(alone).all()
     others = rng.standard_normal((1 + 20, heads, hd)).astype(np.float32)
     qa = np.concatenate([others[:1], q1, others[1:]])
     n = rt.set_segments([(0, 10, 1), (1, 40, 3), (2, 5, 20)])
@@ -132,5 +150,3 @@ def test_runtime_batch_invariant_mode(oracle_mod):
     rt.attention_seg("q", "pk", "pv", "o", heads, kvh, hd)
     beside = np.array(rt.read_floats("o"), np.float32).reshape(24, heads, hd)[1:4].reshape(-1)
     assert np.array_equal(alone.view(np.uint32), beside.view(np.uint32))
-    rt.set_batch_invariant(False)
-    assert rt.gemm_min_rows == 0

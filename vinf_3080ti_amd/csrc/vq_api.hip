@@ -316,9 +316,10 @@ __global__ __launch_bounds__(256) void gemm_xsplit_kernel(const uint8_t *__restr
     if (tid == 0) inv[t] = 1.0f / sc;
 }
 
-// The f16 path: Q4_K/Q5_K, with the activation split addressable by the kernel's 32-bit DMA offsets.
+// The f16 path: Q3_K, Q4_K, Q5_K, Q6_K, with the activation split addressable by the kernels' 32-bit DMA offsets.
 bool gemm16_ok(int type, int cols, int M) {
-    return (type == VQ_Q4_K || type == VQ_Q5_K) && static_cast<long>(M) * cols < (1L << 30);
+    return (type == VQ_Q3_K || type == VQ_Q4_K || type == VQ_Q5_K || type == VQ_Q6_K) &&
+           static_cast<long>(M) * cols < (1L << 30);
 }
 
 // Compute units of the current device (256 when there is none: workspace sizes stay computable).

@@ -1,6 +1,6 @@
 // vq_gemm16_impl.h -- prefill contraction Y[t][r] = W[r] . x[t] on CDNA4 f16 MFMA (v_mfma_f32_16x16x32_f16) for
-// the K-quants whose integer sub-block products are exact in f16 and whose blocks are 16-byte multiples
-// (Q4_K, Q5_K).
+// the K-quants with mins whose integer sub-block products are exact in f16 and whose blocks are 16-byte multiples
+// (Q4_K, Q5_K). Q3_K and Q6_K take qgemm16n_kernel (vq_gemm16n_impl.h) with the same plan and workspace.
 //
 // Numerics. The reference CPU path (Cpu_qmv, qwen_cpu.c:581-641) computes per 32-group
 //   y += d * sc * xd * S - dmin * m * xd * X,   S = sum(code * xq) exact, X = sum(xq)
@@ -396,10 +396,17 @@ __global__ __launch_bounds__(512) inline void g16_reduce_kernel(const float *__r
     }
 }
 
+// Q3_K and Q6_K: qgemm16n_kernel (vq_gemm16n_impl.h), same plan, workspace and reduction.
+template <int T>
+int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
+                   hipStream_t s, bool invariant);
+
 template <int T>
 int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
                   hipStream_t s, bool invariant) {
-    if constexpr (!kGemm16<T>) {
+    if constexpr (T == VQ_Q3_K || T == VQ_Q6_K) {
+        return launch_gemm16n<T>(w, rows, cols, rb, ws, M, y, cus, s, invariant);
+    } else if constexpr (!kGemm16<T>) {
         (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)y, (void)cus, (void)s, (void)invariant;
         return static_cast<int>(hipErrorInvalidValue);
     } else {

@@ -1,0 +1,296 @@
+// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q3_K and Q6_K: the K-quants without mins whose
+// blocks (110 and 210 bytes) are only 2-byte aligned inside a row.
+//
+// Numerics: those of the Q4_K/Q5_K contraction (vq_gemm16_impl.h) without the min term. Each weight element is
+// the integer a = code * sc: (q3) * (sc - 32), |a| <= 128, for Q3_K; Q6_K's (q - 32) * sc (|.| <= 4096) as the two
+// exact f16 terms 16 (q - 32) (sc >> 4) + (q - 32) (sc & 15). Each activation element is b = xq * xd * 2^e as the
+// f16 pair b_hi + b_lo, and each super-block's C = sum a * (b_hi + b_lo) (exact products, fp32 sums) is applied
+// once: acc += d * C (qwen_cpu.c:581-641 regrouped per super-block).
+//
+// Work split, tiles and reduction: those of qgemm16_kernel (G16Plan; 256-row x 128-token tiles, 8 waves of 64 x
+// 64). Differences:
+//  - K order. A step is 64 elements of one super-block, but not 64 consecutive ones: step j = 2n + p takes the
+//    elements 128 n + 32 k + 16 p + i (k = 0..3, i = 0..15). Both types store element 128 n + 32 k + l as a field
+//    of byte l of a 32-byte run (Q6_K: low/high nibble of ql[64 n + 32 (k & 1) + l] and bits 2k of qh[32 n + l];
+//    Q3_K: bits 2k of qs[32 n + l] and bit 4n + k of hmask[l]) and scales it by scale 8 n + 2 k + p, so a step
+//    needs one 16-byte piece of each run per row (Q6_K: 2 of ql, 1 of qh; Q3_K: 1 of qs, 1 of hmask) and every
+//    16-element run of it has one scale. MFMA lane (lr, lk) with chunk c holds k = 2c + (lk >> 1), i = 8 (lk & 1)
+//    .. +8; the activation tile of the step is DMA'd in that same permuted order.
+//  - Alignment. A piece starts m = (row offset of the block) mod 16 bytes past a 16-byte boundary (m even), so
+//    each piece is DMA'd as the 16-byte-aligned pair of chunks covering it (the second one only when m > 0;
+//    otherwise the first is fetched twice) and read from LDS as three dwords realigned by v_alignbyte. The scales
+//    and d of every row come the same way, once per super-block. No read goes past the 16 bytes of padding that
+//    follow the tensor.
+//  - Two step slots (one step of lead): with three, the chunk pairs and the activation tiles would not fit LDS.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vq_gemm16_impl.h"
+#include "vq_small16_impl.h"
+
+namespace vq {
+
+template <int T>
+struct G16N {
+    static constexpr bool Q6 = T == VQ_Q6_K;
+    static constexpr int UB = Q6 ? 210 : 110;
+    static constexpr int NPC = Q6 ? 3 : 2;         // 16-byte pieces per row and step
+    static constexpr int CPR = 2 * NPC;            // chunks DMA'd per row and step
+    static constexpr int SOFF = Q6 ? 192 : 96;     // scales; d follows them
+    static constexpr int SLEN = Q6 ? 18 : 14;      // scale bytes + d
+    static constexpr int CODE_BYTES = kG16BM * CPR * 16;
+    static constexpr int STEP_BYTES = CODE_BYTES + 2 * kG16BN * 128;
+    static constexpr int SB_BYTES = kG16BM * 32;   // per row: the chunk pair covering scales and d
+    static constexpr int CODE_DMA = CPR / 2;       // per wave and step: 32 rows x CPR chunks
+    static_assert(kG16BM * 2 == 64 * kG16Waves, "one super-block DMA per wave");
+    // Block offset of piece pc of step (n, p).
+    __device__ static int poff(int pc, int n, int p) {
+        if constexpr (Q6)
+            return pc == 2 ? 128 + 32 * n + 16 * p : 64 * n + 32 * pc + 16 * p;
+        else
+            return pc == 0 ? 32 + 32 * n + 16 * p : 16 * p;
+    }
+    // Super-block element of MFMA chunk q = 4 c + lk of step j.
+    __device__ static int bpos(int j, int q) {
+        return 128 * (j >> 1) + 32 * (2 * (q >> 2) + ((q & 3) >> 1)) + 16 * (j & 1) + 8 * (q & 1);
+    }
+};
+
+// Eight bytes at LDS byte offset `off` (even) of `base` (4-byte aligned): three dwords, realigned.
+__device__ __forceinline__ uint2 g16n_read8(const uint8_t *base, int off) {
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(base + (off & ~3));
+    const uint32_t d0 = q[0], d1 = q[1], d2 = q[2], sh = static_cast<uint32_t>(off & 3);
+    return uint2{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh)};
+}
+
+template <int T>
+__global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t *__restrict__ w, int rows, int cols,
+                                                                   long row_bytes, const _Float16 *__restrict__ bh,
+                                                                   const _Float16 *__restrict__ bl,
+                                                                   const float *__restrict__ inv, int M, G16Plan pl,
+                                                                   float *__restrict__ y, float *__restrict__ part) {
+    using G = G16N<T>;
+    __shared__ __attribute__((aligned(1024))) uint8_t s_step[2][G::STEP_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_sb[2][G::SB_BYTES];
+
+    const int b = blockIdx.x;
+    const int v = (b & 7) * pl.per_xcd + (b >> 3);  // XCD-aware share order, as qgemm16_kernel
+    if (v >= pl.W) return;
+    const int nsb = pl.nsb;
+    const long ue = pl.u0(v + 1);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int wr = 64 * (wv & 3), wt = 64 * (wv >> 2);
+    const int lr = lane & 15, lk = lane >> 4;
+    for (long u = pl.u0(v); u < ue;) {
+    const int tile = static_cast<int>(u / nsb);
+    const int sb0 = static_cast<int>(u - static_cast<long>(tile) * nsb);
+    const int sb1 = ue - u < nsb - sb0 ? sb0 + static_cast<int>(ue - u) : nsb;
+    const int rt = tile / pl.ntt, tt = tile - rt * pl.ntt;
+    const int r0 = rt * kG16BM, t0 = tt * kG16BN;
+    const int nsteps = (sb1 - sb0) * 4;
+    const uint8_t *const wbase = w + static_cast<size_t>(r0) * row_bytes;  // 16-byte aligned (r0 % 256 == 0)
+    // Misalignment of tile row R's block sb (the row clamped as the DMA clamps it).
+    auto mis = [&](int R, int sb) {
+        const int rc = min(r0 + R, rows - 1) - r0;
+        return static_cast<int>((static_cast<uint32_t>(rc * row_bytes) + static_cast<uint32_t>(sb * G::UB)) & 15u);
+    };
+
+    // DMA of step st into step slot st & 1 (and, on a super-block's first step, its scales into slot sb & 1).
+    auto issue = [&](int st) {
+        const int sb = sb0 + (st >> 2), j = st & 3, n = j >> 1, p = j & 1;
+        uint8_t *const slot = s_step[st & 1];
+#pragma unroll
+        for (int k = 0; k < G::CODE_DMA; ++k) {
+            const int ci = 64 * k + lane, rr = 32 * wv + ci / G::CPR, ch = ci % G::CPR;
+            const int row = min(r0 + rr, rows - 1) - r0;
+            const uint32_t a = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + G::poff(ch >> 1, n, p));
+            const uint32_t off = (a & ~15u) + ((ch & 1) && (a & 15u) ? 16u : 0u);
+            dma16(wbase, off, slot + 1024 * (G::CODE_DMA * wv + k));
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * wv + k, ii = i & 15;
+            const int row = 8 * ii + (lane >> 3);
+            const int tok = min(t0 + row, M - 1);
+            const int c = (lane & 7) ^ ((row >> 1) & 7);
+            const uint32_t off = static_cast<uint32_t>((static_cast<long>(tok) * cols + 256L * sb + G::bpos(j, c)) * 2);
+            dma16(i < 16 ? static_cast<const void *>(bh) : static_cast<const void *>(bl), off,
+                  slot + G::CODE_BYTES + (i < 16 ? 0 : kG16BN * 128) + 1024 * ii);
+        }
+        if (j != 0) return;
+        {
+            const int ci = 64 * wv + lane, rr = ci >> 1;
+            const int row = min(r0 + rr, rows - 1) - r0;
+            const uint32_t a = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + G::SOFF);
+            const uint32_t off = (a & ~15u) + ((ci & 1) && (a & 15u) + G::SLEN > 16u ? 16u : 0u);
+            dma16(wbase, off, s_sb[sb & 1] + 1024 * wv);
+        }
+    };
+
+    g16f4 acc[4][4], C[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[i][q] = C[i][q] = g16f4{0.f, 0.f, 0.f, 0.f};
+
+    if (nsteps > 0) issue(0);
+    uint32_t scw[4][2];  // [rb][c]: scales 8n + 4c .. +4 of row wr + 16 rb + lr (Q3_K: 6-bit, unpacked), one per byte
+    for (int st = 0; st < nsteps; ++st) {
+        wait_vm<0>();
+        __syncthreads();  // step st landed for every wave; step st - 1's slot is free
+        if (st + 1 < nsteps) issue(st + 1);
+        const int sb = sb0 + (st >> 2), j = st & 3, n = j >> 1, p = j & 1;
+        const uint8_t *const slot = s_step[st & 1];
+        const uint8_t *const sbs = s_sb[sb & 1];
+        const uint8_t *const sBh = slot + G::CODE_BYTES, *const sBl = sBh + kG16BN * 128;
+        if (p == 0) {  // the half's eight scales, on its first step
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int R = wr + 16 * rb + lr, o = R * 32 + mis(R, sb);
+                const uint32_t sh = static_cast<uint32_t>(o & 3);
+                if constexpr (G::Q6) {
+                    const uint32_t *q = reinterpret_cast<const uint32_t *>(sbs + (o & ~3) + 8 * n);
+                    const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
+                    scw[rb][0] = __builtin_amdgcn_alignbyte(d1, d0, sh);
+                    scw[rb][1] = __builtin_amdgcn_alignbyte(d2, d1, sh);
+                } else {  // 6-bit scales: low nibbles in bytes 0..7, high pairs in bytes 8..11 (the k3 packing)
+                    const uint32_t *q = reinterpret_cast<const uint32_t *>(sbs + (o & ~3));
+                    const uint32_t d0 = q[0], d1 = q[1], d2 = q[2], d3 = q[3];
+                    const uint32_t a0 = __builtin_amdgcn_alignbyte(d1, d0, sh), a1 = __builtin_amdgcn_alignbyte(d2, d1, sh),
+                                   a2 = __builtin_amdgcn_alignbyte(d3, d2, sh) >> (4 * n);
+                    scw[rb][0] = ((a0 >> (4 * n)) & 0x0F0F0F0Fu) | ((a2 & 0x03030303u) << 4);
+                    scw[rb][1] = ((a1 >> (4 * n)) & 0x0F0F0F0Fu) | (((a2 >> 2) & 0x03030303u) << 4);
+                }
+            }
+        }
+        // A fragments: row R = wr + 16 rb + lr, chunk c: k = 2c + (lk >> 1), elements 8 (lk & 1) .. +8 of the
+        // step's 16-element run of k.
+        const int hf = 8 * (lk & 1), kl = lk >> 1;
+        const uint32_t sbyte = 8u * static_cast<uint32_t>(p + 2 * kl);  // the run's scale: byte p + 2 kl of dword 2n + c
+        uint2 ra[4], rh[4];  // [rb]: Q6_K ql (run kl) and qh; Q3_K qs and hmask
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int R = wr + 16 * rb + lr;
+            const int base = R * G::CPR * 16 + mis(R, sb) + hf;
+            ra[rb] = g16n_read8(slot, base + (G::Q6 ? 32 * kl : 0));
+            rh[rb] = g16n_read8(slot, base + (G::Q6 ? 64 : 32));
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int k = 2 * c + kl;
+            g16h8 a1[4], a2[4];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const uint32_t sw = scw[rb][c];
+                uint32_t c0, c1;
+                int isc;
+                if constexpr (G::Q6) {
+                    c0 = ((ra[rb].x >> (4 * c)) & 0x0F0F0F0Fu) | (((rh[rb].x >> (2 * k)) & 0x03030303u) << 4);
+                    c1 = ((ra[rb].y >> (4 * c)) & 0x0F0F0F0Fu) | (((rh[rb].y >> (2 * k)) & 0x03030303u) << 4);
+                    isc = static_cast<int>(static_cast<int8_t>(sw >> sbyte));
+                } else {
+                    const uint32_t hs = static_cast<uint32_t>(4 * n + k);
+                    c0 = ((ra[rb].x >> (2 * k)) & 0x03030303u) | (((rh[rb].x >> hs) & 0x01010101u) << 2);
+                    c1 = ((ra[rb].y >> (2 * k)) & 0x03030303u) | (((rh[rb].y >> hs) & 0x01010101u) << 2);
+                    isc = static_cast<int>((sw >> sbyte) & 0xFFu) - 32;
+                }
+                s16_frag<T>(c0, c1, isc, a1[rb], a2[rb]);
+            }
+            g16h8 bhf[4], blf[4];
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                const int r = wt + 16 * tb + lr;
+                const int o = r * 128 + (((4 * c + lk) ^ ((r >> 1) & 7)) << 4);
+                bhf[tb] = *reinterpret_cast<const g16h8 *>(sBh + o);
+                blf[tb] = *reinterpret_cast<const g16h8 *>(sBl + o);
+            }
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+                    C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], bhf[tb], C[rb][tb], 0, 0, 0);
+                    C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], blf[tb], C[rb][tb], 0, 0, 0);
+                    if constexpr (G::Q6) {
+                        C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], bhf[tb], C[rb][tb], 0, 0, 0);
+                        C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], blf[tb], C[rb][tb], 0, 0, 0);
+                    }
+                }
+        }
+        if (j == 3) {
+            // Super-block end: acc += d C; C element q of a block is row 4 lk + q, token lr.
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                float dq[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int R = wr + 16 * rb + 4 * lk + q;
+                    dq[q] = half_to_float(*reinterpret_cast<const uint16_t *>(sbs + R * 32 + mis(R, sb) + G::SLEN - 2));
+                }
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[rb][tb][q] = fmaf(dq[q], C[rb][tb][q], acc[rb][tb][q]);
+                    C[rb][tb] = g16f4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+    }
+
+    // Output, as qgemm16_kernel: a whole tile to y, a part of one to its slot.
+    if (sb0 == 0 && sb1 == nsb) {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const int t = t0 + wt + 16 * tb + lr;
+            if (t >= M) continue;
+            const float is = inv[t];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int r = r0 + wr + 16 * rb + 4 * lk;
+                float *const dst = y + static_cast<size_t>(t) * rows + r;
+                if ((rows & 3) == 0 && r + 3 < rows) {
+                    *reinterpret_cast<float4 *>(dst) = float4{acc[rb][tb][0] * is, acc[rb][tb][1] * is, acc[rb][tb][2] * is, acc[rb][tb][3] * is};
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (r + q < rows) dst[q] = acc[rb][tb][q] * is;
+                }
+            }
+        }
+    } else {
+        const int k = v - pl.wg_of(static_cast<long>(tile) * nsb);
+        float *const slot = part + (static_cast<size_t>(tile) * pl.maxseg + k) * kG16TileFloats;
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const int t = min(t0 + wt + 16 * tb + lr, M - 1);
+            const float is = inv[t];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) slot[static_cast<size_t>((rb * 4 + tb) * 4 + q) * 512 + tid] = acc[rb][tb][q] * is;
+        }
+    }
+    __syncthreads();  // the slots are reused by the next segment's first DMAs
+    u += sb1 - sb0;
+    }
+}
+
+template <int T>
+int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
+                   hipStream_t s, bool invariant) {
+    const G16Plan pl = g16_plan(rows, cols, M, cus, invariant);
+    const G16Ws l = g16_layout(cols, M, pl);
+    uint8_t *base = static_cast<uint8_t *>(const_cast<void *>(ws));
+    float *const part = reinterpret_cast<float *>(base + l.part);
+    qgemm16n_kernel<T><<<dim3(8 * pl.per_xcd), dim3(64 * kG16Waves), 0, s>>>(
+        w, rows, cols, rb, reinterpret_cast<const _Float16 *>(base + l.bh), reinterpret_cast<const _Float16 *>(base + l.bl),
+        reinterpret_cast<const float *>(base + l.inv), M, pl, y, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return static_cast<int>(e);
+    g16_reduce_kernel<<<dim3(16 * pl.tiles), dim3(512), 0, s>>>(part, pl, rows, M, y);
+    e = hipGetLastError();
+    return e == hipSuccess ? 0 : static_cast<int>(e);
+}
+
+}  // namespace vq

@@ -22,6 +22,7 @@
 
 #include "vq_gemm_impl.h"
 #include "vq_gemm16_impl.h"
+#include "vq_gemm16n_impl.h"
 #include "vq_small16_impl.h"
 #include "vq_qmv.h"
 #include "vq_tables.h"

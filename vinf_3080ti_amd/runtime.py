@@ -132,6 +132,14 @@ class Runtime:
             self._ws = torch.empty(max(nbytes, 2 * self._ws.numel()), dtype=torch.uint8, device=self.device)
         return self._ws
 
+    def _logits_scratch(self, n: int) -> torch.Tensor:
+        """fp32 logits of the batch-invariant argmax when the caller keeps none: grown on demand and reused
+        (separate from the workspace, which the matvec itself may use)."""
+        buf = getattr(self, "_logits", None)
+        if buf is None or buf.numel() < n:
+            buf = self._logits = torch.empty(n, dtype=torch.float32, device=self.device)
+        return buf
+
     def _tensor(self, name: str) -> _Tensor:
         t = self.tensors.get(name)
         if t is None:
@@ -395,7 +403,7 @@ class Runtime:
     def _qmv_ptrs(self, t: _Tensor, x_ptr: int, y_ptr: int, ntok: int) -> None:
         if t.type not in (0, 1) and self.gemm_min_rows > 0 and ntok >= self.gemm_min_rows:
             # Prompt pass: the MFMA contraction (the prefill branch of Runtime_qmv, qwen_runtime.cu:1886-1902):
-            # packed activations, then the contraction's own workspace (f16 path of Q4_K/Q5_K; 0 bytes otherwise).
+            # packed activations, then the contraction's own workspace (f16 path of Q3_K-Q6_K; 0 bytes otherwise).
             flags = _lib.VQ_GEMM_BATCH_INVARIANT if self.batch_invariant else 0
             nx = (self._lib.vq_xpack_bytes(t.cols, ntok) + 255) // 256 * 256
             ng = self._lib.vq_qgemm_workspace_bytes_ex(t.type, t.rows, t.cols, ntok, flags)
@@ -845,7 +853,7 @@ class Runtime:
         xb = self._f32_buffer(x, t.cols * ntok)
         if self.batch_invariant:  # the matvec on the invariant path, then the row argmax
             yt = (self._f32_buffer(logits, t.rows * ntok) if logits is not None
-                  else torch.empty(t.rows * ntok, dtype=torch.float32, device=self.device))
+                  else self._logits_scratch(t.rows * ntok))
             self._qmv_ptrs(t, xb.data_ptr(), yt.data_ptr(), ntok)
             _lib.check(self._lib.vq_argmax_rows(yt.data_ptr(), t.rows, ntok, self._argmax_out.data_ptr(),
                                                 self._stream()), "argmax_rows")
