@@ -15,14 +15,15 @@
 //
 // Work split: a workgroup of 8 waves computes a 256-row x 128-token tile over a range of super-blocks (split
 // K when the tiles alone would leave CUs idle; partial tiles are added in a fixed order by the library's
-// reduction, so results are deterministic). Wave w owns rows 64 (w % 4) .. +64 and tokens 64 (w / 4) .. +64:
-// 4 x 4 blocks of 16 x 16. A K step is 64 elements (a quarter super-block). All global data reaches LDS by
+// reduction, so results are deterministic). Wave w owns rows 32 w .. +32 and all 128 tokens: 2 x 8 blocks of 16 x
+// 16, so every weight row is decoded by one wave (with 64 x 64 per wave, two waves decoded each row: 3-16 %
+// slower by type, at half the B-fragment reads). A K step is 64 elements (a quarter super-block). All global data reaches LDS by
 // global_load_lds_dwordx4, two steps ahead, into a ring of three step slots (the step's 32 code bytes of
 // every row; the tokens' b_hi/b_lo tile, 16-byte chunks XOR-swizzled by row against bank conflicts) and two
 // super-block slots (the first 16/48 bytes of every row's block -- d, dmin, scales, Q5_K's high bits -- and
 // the tokens' min terms). Every wave issues the same number of DMAs per step, so one vmcnt wait and one
 // barrier per step cover the ring. Each wave decodes its own A fragments (code * scale -> f16 via v_perm_b32
-// and v_pk_fma_f16) from the raw bytes while its MFMAs run: 2 x 16 x 2 v_mfma_f32_16x16x32_f16 per step. A
+// and v_pk_fma_f16) from the raw bytes: 2 x 16 x 2 v_mfma_f32_16x16x32_f16 per step. A
 // super-block's min term is one v_mfma_f32_16x16x16_f16 per block over [m_0..m_7, m_0..m_7] x
 // [XS_hi_0..7, XS_lo_0..7].
 #pragma once
@@ -38,6 +39,12 @@ template <int T>
 constexpr bool kGemm16 = T == VQ_Q4_K || T == VQ_Q5_K;
 
 constexpr int kG16BM = 256, kG16BN = 128, kG16KS = 64, kG16Waves = 8, kG16Ring = 3;
+// 16-row blocks per wave: 2 (a wave owns 32 rows x all 128 tokens of the tile, so each row is decoded by one
+// wave) or 4 (64 rows x 64 tokens: two waves decode every row, half the B-fragment reads).
+#ifndef VQ_G16_RB
+#define VQ_G16_RB 2
+#endif
+constexpr int kG16RB = VQ_G16_RB;
 
 typedef _Float16 g16h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 g16h4 __attribute__((ext_vector_type(4)));
@@ -163,7 +170,8 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     const long ue = pl.u0(v + 1);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int wr = 64 * (wv & 3), wt = 64 * (wv >> 2);
+    constexpr int RB = kG16RB, TB = 16 / RB;  // 16-row blocks x 16-token blocks of a wave
+    const int wr = 16 * RB * (wv % (16 / RB)), wt = 16 * TB * (wv / (16 / RB));
     const int lr = lane & 15, lk = lane >> 4;
     // The share's tile segments: tile t, super-blocks [sb0, sb1).
     for (long u = pl.u0(v); u < ue;) {
@@ -217,15 +225,15 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
         }
     };
 
-    g16f4 acc[4][4], C[4][4];
+    g16f4 acc[RB][TB], C[RB][TB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[i][q] = C[i][q] = g16f4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < TB; ++q) acc[i][q] = C[i][q] = g16f4{0.f, 0.f, 0.f, 0.f};
 
     if (nsteps > 0) issue(0);
     if (nsteps > 1) issue(1);
-    uint32_t scl[4] = {0u, 0u, 0u, 0u}, sch[4] = {0u, 0u, 0u, 0u};  // [rb]: 6-bit scales of groups 0..3 / 4..7 of
+    uint32_t scl[RB] = {}, sch[RB] = {};  // [rb]: 6-bit scales of groups 0..3 / 4..7 of
                                                                       // row wr + 16 rb + lr, one per byte
     const g16h2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
     for (int st = 0; st < nsteps; ++st) {
@@ -246,7 +254,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
             // The super-block's 6-bit scales, four per dword (the k4_scale_min packing, qwen_cpu.c:54-62):
             // groups 0..3 from scales[0..3], groups 4..7 from scales[8..11] plus the top bits of scales[0..3].
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 const uint4 h = *reinterpret_cast<const uint4 *>(sbs + (wr + 16 * rb + lr) * G::HB);
                 scl[rb] = h.y & 0x3F3F3F3Fu;
                 sch[rb] = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
@@ -254,9 +262,9 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
         }
         // A fragments: rows wr + 16 rb + lr, elements 8 lk .. +8 of groups 2j (c = 0) and 2j + 1 (c = 1).
         const uint32_t ssel = (j & 1) ? 0x04030402u : 0x04010400u;
-        g16h8 a[2][4];
+        g16h8 a[2][RB];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < RB; ++rb) {
             const int row = wr + 16 * rb + lr;
             const uint32_t sw = j < 2 ? scl[rb] : sch[rb];
             const g16h2 sc = g16_pair(sw, ssel) - k1024;
@@ -275,28 +283,32 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
         }
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            g16h8 bhf[4], blf[4];
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-                const int r = wt + 16 * tb + lr;
-                const int o = r * 128 + (((4 * c + lk) ^ ((r >> 1) & 7)) << 4);
-                bhf[tb] = *reinterpret_cast<const g16h8 *>(sBh + o);
-                blf[tb] = *reinterpret_cast<const g16h8 *>(sBl + o);
-            }
+            for (int h = 0; h < TB / 4; ++h) {  // token blocks four at a time (B fragments' registers)
+                g16h8 bhf[4], blf[4];
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
-                    C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][rb], bhf[tb], C[rb][tb], 0, 0, 0);
-                    C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][rb], blf[tb], C[rb][tb], 0, 0, 0);
+                for (int i = 0; i < 4; ++i) {
+                    const int r = wt + 16 * (4 * h + i) + lr;
+                    const int o = r * 128 + (((4 * c + lk) ^ ((r >> 1) & 7)) << 4);
+                    bhf[i] = *reinterpret_cast<const g16h8 *>(sBh + o);
+                    blf[i] = *reinterpret_cast<const g16h8 *>(sBl + o);
                 }
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        g16f4 &cc = C[rb][4 * h + i];
+                        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][rb], bhf[i], cc, 0, 0, 0);
+                        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][rb], blf[i], cc, 0, 0, 0);
+                    }
+            }
         }
         if (j == 3) {
             // Super-block end: acc += d C - 32 dmin (m . XS); C restarts at zero. C element q of a block is row
             // 4 lk + q, token lr.
             const uint8_t *const sxs = sbs + kG16BM * G::HB;
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 float dq[4], mq[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -310,7 +322,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
                 const g16h2 m01 = g16_pair(mw, 0x04010400u) - k1024, m23 = g16_pair(mw, 0x04030402u) - k1024;
                 const g16h4 amin = {m01[0], m01[1], m23[0], m23[1]};
 #pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
+                for (int tb = 0; tb < TB; ++tb) {
                     const g16h4 bm = *reinterpret_cast<const g16h4 *>(sxs + (wt + 16 * tb + lr) * 32 + 8 * lk);
                     const g16f4 cm = __builtin_amdgcn_mfma_f32_16x16x16f16(amin, bm, g16f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
@@ -326,12 +338,12 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     // part of a tile to its slot, in thread order (coalesced: value i of thread x at [i][x]).
     if (sb0 == 0 && sb1 == nsb) {
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
+        for (int tb = 0; tb < TB; ++tb) {
             const int t = t0 + wt + 16 * tb + lr;
             if (t >= M) continue;
             const float is = inv[t];
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 const int r = r0 + wr + 16 * rb + 4 * lk;
                 float *const dst = y + static_cast<size_t>(t) * rows + r;
                 if ((rows & 3) == 0 && r + 3 < rows) {
@@ -347,13 +359,13 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
         const int k = v - pl.wg_of(static_cast<long>(tile) * nsb);
         float *const slot = part + (static_cast<size_t>(tile) * pl.maxseg + k) * kG16TileFloats;
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
+        for (int tb = 0; tb < TB; ++tb) {
             const int t = min(t0 + wt + 16 * tb + lr, M - 1);
             const float is = inv[t];
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
+            for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) slot[static_cast<size_t>((rb * 4 + tb) * 4 + q) * 512 + tid] = acc[rb][tb][q] * is;
+                for (int q = 0; q < 4; ++q) slot[static_cast<size_t>((rb * TB + tb) * 4 + q) * 512 + tid] = acc[rb][tb][q] * is;
         }
     }
     __syncthreads();  // the ring is reused by the next segment's first DMAs
@@ -363,19 +375,22 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
 
 // Partial tiles: y = the sum of a tile's slots in slot order. Workgroup (tile, block pair (rb, tb)) of 512
 // threads, thread x summing the four values the GEMM's thread x held for that pair (independent loads, so the
-// slots stream); tiles that one workgroup covered are already in y.
-__global__ __launch_bounds__(512) inline void g16_reduce_kernel(const float *__restrict__ part, G16Plan pl, int rows,
-                                                                int M, float *__restrict__ y) {
+// slots stream); tiles that one workgroup covered are already in y. RB: the GEMM's 16-row blocks per wave (4: 64
+// rows x 64 tokens per wave; 2: 32 rows x 128 tokens).
+template <int RB = 4>
+__global__ __launch_bounds__(512) void g16_reduce_kernel(const float *__restrict__ part, G16Plan pl, int rows, int M,
+                                                         float *__restrict__ y) {
     const int tile = blockIdx.x >> 4, pair = blockIdx.x & 15;
     const int k0 = pl.wg_of(static_cast<long>(tile) * pl.nsb), k1 = pl.wg_of(static_cast<long>(tile) * pl.nsb + pl.nsb - 1);
     if (k1 == k0) return;
+    constexpr int TB = 16 / RB;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wr = 64 * (wv & 3), wt = 64 * (wv >> 2), lr = lane & 15, lk = lane >> 4;
-    const int rb = pair >> 2, tb = pair & 3;
+    const int wr = 16 * RB * (wv % (16 / RB)), wt = 16 * TB * (wv / (16 / RB)), lr = lane & 15, lk = lane >> 4;
+    const int rb = pair / TB, tb = pair % TB;
     const int rt = tile / pl.ntt, tt = tile - rt * pl.ntt;
     const int t = tt * kG16BN + wt + 16 * tb + lr, r = rt * kG16BM + wr + 16 * rb + 4 * lk;
     const float *const base = part + static_cast<size_t>(tile) * pl.maxseg * kG16TileFloats +
-                              static_cast<size_t>((rb * 4 + tb) * 4) * 512 + tid;
+                              static_cast<size_t>((rb * TB + tb) * 4) * 512 + tid;
     float v4[4] = {0.f, 0.f, 0.f, 0.f};
     for (int k = 0; k <= k1 - k0; ++k) {
         const float *const sk = base + static_cast<size_t>(k) * kG16TileFloats;
@@ -422,7 +437,7 @@ int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws,
         );
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return static_cast<int>(e);
-        g16_reduce_kernel<<<dim3(16 * pl.tiles), dim3(512), 0, s>>>(part, pl, rows, M, y);
+        g16_reduce_kernel<kG16RB><<<dim3(16 * pl.tiles), dim3(512), 0, s>>>(part, pl, rows, M, y);
         e = hipGetLastError();
         return e == hipSuccess ? 0 : static_cast<int>(e);
     }

@@ -7,8 +7,8 @@
 // f16 pair b_hi + b_lo, and each super-block's C = sum a * (b_hi + b_lo) (exact products, fp32 sums) is applied
 // once: acc += d * C (qwen_cpu.c:581-641 regrouped per super-block).
 //
-// Work split, tiles and reduction: those of qgemm16_kernel (G16Plan; 256-row x 128-token tiles, 8 waves of 64 x
-// 64). Differences:
+// Work split, tiles and reduction: those of qgemm16_kernel (G16Plan; 256-row x 128-token tiles, 8 waves of 32
+// rows x 128 tokens). Differences:
 //  - K order. A step is 64 elements of one super-block, but not 64 consecutive ones: step j = 2n + p takes the
 //    elements 128 n + 32 k + 16 p + i (k = 0..3, i = 0..15). Both types store element 128 n + 32 k + l as a field
 //    of byte l of a 32-byte run (Q6_K: low/high nibble of ql[64 n + 32 (k & 1) + l] and bits 2k of qh[32 n + l];
@@ -81,7 +81,8 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
     const long ue = pl.u0(v + 1);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int wr = 64 * (wv & 3), wt = 64 * (wv >> 2);
+    constexpr int RB = kG16RB, TB = 16 / RB;  // 16-row blocks x 16-token blocks of a wave
+    const int wr = 16 * RB * (wv % (16 / RB)), wt = 16 * TB * (wv / (16 / RB));
     const int lr = lane & 15, lk = lane >> 4;
     for (long u = pl.u0(v); u < ue;) {
     const int tile = static_cast<int>(u / nsb);
@@ -129,14 +130,14 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         }
     };
 
-    g16f4 acc[4][4], C[4][4];
+    g16f4 acc[RB][TB], C[RB][TB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[i][q] = C[i][q] = g16f4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < TB; ++q) acc[i][q] = C[i][q] = g16f4{0.f, 0.f, 0.f, 0.f};
 
     if (nsteps > 0) issue(0);
-    uint32_t scw[4][2];  // [rb][c]: scales 8n + 4c .. +4 of row wr + 16 rb + lr (Q3_K: 6-bit, unpacked), one per byte
+    uint32_t scw[RB][2];  // [rb][c]: scales 8n + 4c .. +4 of row wr + 16 rb + lr (Q3_K: 6-bit, unpacked), one per byte
     for (int st = 0; st < nsteps; ++st) {
         wait_vm<0>();
         __syncthreads();  // step st landed for every wave; step st - 1's slot is free
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         const uint8_t *const sBh = slot + G::CODE_BYTES, *const sBl = sBh + kG16BN * 128;
         if (p == 0) {  // the half's eight scales, on its first step
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 const int R = wr + 16 * rb + lr, o = R * 32 + mis(R, sb);
                 const uint32_t sh = static_cast<uint32_t>(o & 3);
                 if constexpr (G::Q6) {
@@ -169,9 +170,9 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         // step's 16-element run of k.
         const int hf = 8 * (lk & 1), kl = lk >> 1;
         const uint32_t sbyte = 8u * static_cast<uint32_t>(p + 2 * kl);  // the run's scale: byte p + 2 kl of dword 2n + c
-        uint2 ra[4], rh[4];  // [rb]: Q6_K ql (run kl) and qh; Q3_K qs and hmask
+        uint2 ra[RB], rh[RB];  // [rb]: Q6_K ql (run kl) and qh; Q3_K qs and hmask
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < RB; ++rb) {
             const int R = wr + 16 * rb + lr;
             const int base = R * G::CPR * 16 + mis(R, sb) + hf;
             ra[rb] = g16n_read8(slot, base + (G::Q6 ? 32 * kl : 0));
@@ -180,9 +181,9 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const int k = 2 * c + kl;
-            g16h8 a1[4], a2[4];
+            g16h8 a1[RB], a2[RB];
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 const uint32_t sw = scw[rb][c];
                 uint32_t c0, c1;
                 int isc;
@@ -198,30 +199,34 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                 }
                 s16_frag<T>(c0, c1, isc, a1[rb], a2[rb]);
             }
-            g16h8 bhf[4], blf[4];
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-                const int r = wt + 16 * tb + lr;
-                const int o = r * 128 + (((4 * c + lk) ^ ((r >> 1) & 7)) << 4);
-                bhf[tb] = *reinterpret_cast<const g16h8 *>(sBh + o);
-                blf[tb] = *reinterpret_cast<const g16h8 *>(sBl + o);
-            }
+            for (int h = 0; h < TB / 4; ++h) {  // token blocks four at a time (B fragments' registers)
+                g16h8 bhf[4], blf[4];
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
-                    C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], bhf[tb], C[rb][tb], 0, 0, 0);
-                    C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], blf[tb], C[rb][tb], 0, 0, 0);
-                    if constexpr (G::Q6) {
-                        C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], bhf[tb], C[rb][tb], 0, 0, 0);
-                        C[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], blf[tb], C[rb][tb], 0, 0, 0);
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    const int r = wt + 16 * (4 * h + i) + lr;
+                    const int o = r * 128 + (((4 * c + lk) ^ ((r >> 1) & 7)) << 4);
+                    bhf[i] = *reinterpret_cast<const g16h8 *>(sBh + o);
+                    blf[i] = *reinterpret_cast<const g16h8 *>(sBl + o);
                 }
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        g16f4 &cc = C[rb][4 * h + i];
+                        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], bhf[i], cc, 0, 0, 0);
+                        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], blf[i], cc, 0, 0, 0);
+                        if constexpr (G::Q6) {
+                            cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], bhf[i], cc, 0, 0, 0);
+                            cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], blf[i], cc, 0, 0, 0);
+                        }
+                    }
+            }
         }
         if (j == 3) {
             // Super-block end: acc += d C; C element q of a block is row 4 lk + q, token lr.
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 float dq[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -229,7 +234,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                     dq[q] = half_to_float(*reinterpret_cast<const uint16_t *>(sbs + R * 32 + mis(R, sb) + G::SLEN - 2));
                 }
 #pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
+                for (int tb = 0; tb < TB; ++tb) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) acc[rb][tb][q] = fmaf(dq[q], C[rb][tb][q], acc[rb][tb][q]);
                     C[rb][tb] = g16f4{0.f, 0.f, 0.f, 0.f};
@@ -241,12 +246,12 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
     // Output, as qgemm16_kernel: a whole tile to y, a part of one to its slot.
     if (sb0 == 0 && sb1 == nsb) {
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
+        for (int tb = 0; tb < TB; ++tb) {
             const int t = t0 + wt + 16 * tb + lr;
             if (t >= M) continue;
             const float is = inv[t];
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 const int r = r0 + wr + 16 * rb + 4 * lk;
                 float *const dst = y + static_cast<size_t>(t) * rows + r;
                 if ((rows & 3) == 0 && r + 3 < rows) {
@@ -262,13 +267,13 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         const int k = v - pl.wg_of(static_cast<long>(tile) * nsb);
         float *const slot = part + (static_cast<size_t>(tile) * pl.maxseg + k) * kG16TileFloats;
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
+        for (int tb = 0; tb < TB; ++tb) {
             const int t = min(t0 + wt + 16 * tb + lr, M - 1);
             const float is = inv[t];
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
+            for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) slot[static_cast<size_t>((rb * 4 + tb) * 4 + q) * 512 + tid] = acc[rb][tb][q] * is;
+                for (int q = 0; q < 4; ++q) slot[static_cast<size_t>((rb * TB + tb) * 4 + q) * 512 + tid] = acc[rb][tb][q] * is;
         }
     }
     __syncthreads();  // the slots are reused by the next segment's first DMAs
@@ -288,7 +293,7 @@ int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws
         reinterpret_cast<const float *>(base + l.inv), M, pl, y, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
-    g16_reduce_kernel<<<dim3(16 * pl.tiles), dim3(512), 0, s>>>(part, pl, rows, M, y);
+    g16_reduce_kernel<kG16RB><<<dim3(16 * pl.tiles), dim3(512), 0, s>>>(part, pl, rows, M, y);
     e = hipGetLastError();
     return e == hipSuccess ? 0 : static_cast<int>(e);
 }
