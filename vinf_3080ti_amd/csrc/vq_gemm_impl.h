@@ -60,8 +60,8 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(const uint8_t *_
     __shared__ float s_xd[kGemmBN][NG], s_xs[kGemmBN][NG * 2];
     __shared__ uint2 s8[TabSpec<T>::n8 > 0 ? TabSpec<T>::n8 : 1];
     __shared__ uint32_t s4[TabSpec<T>::n4 > 0 ? TabSpec<T>::n4 : 1];
-    __shared__ uint4 sks[TabSpec<T>::ks ? 128 : 1];
-    __shared__ uint4 ssm[TabSpec<T>::sm ? 256 : 1];
+    __shared__ uint2 sks[TabSpec<T>::ks ? 128 : 1];
+    __shared__ uint2 ssm[TabSpec<T>::sm ? 256 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r0 = blockIdx.y * kGemmBM, t0 = blockIdx.x * kGemmBN;

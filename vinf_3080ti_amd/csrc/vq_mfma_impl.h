@@ -65,8 +65,8 @@ __global__ __launch_bounds__(64 * kMfmaRowWaves) void qmv_mfma_kernel(const uint
     __shared__ float s_sc[kMfmaRowWaves][16][16], s_mn[kMfmaRowWaves][16][16];
     __shared__ uint2 s8[TabSpec<T>::n8 > 0 ? TabSpec<T>::n8 : 1];
     __shared__ uint32_t s4[TabSpec<T>::n4 > 0 ? TabSpec<T>::n4 : 1];
-    __shared__ uint4 sks[TabSpec<T>::ks ? 128 : 1];
-    __shared__ uint4 ssm[TabSpec<T>::sm ? 256 : 1];
+    __shared__ uint2 sks[TabSpec<T>::ks ? 128 : 1];
+    __shared__ uint2 ssm[TabSpec<T>::sm ? 256 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);

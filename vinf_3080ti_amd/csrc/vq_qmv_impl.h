@@ -202,8 +202,8 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     constexpr bool SG = use_signed_grid<T, NT>();
     extern __shared__ __attribute__((aligned(1024))) uint8_t s_dyn[];
     __shared__ __attribute__((aligned(1024))) uint8_t s_grid[TB > 0 ? TB : 16];
-    __shared__ uint4 sks[TabSpec<T>::ks ? 128 : 1];
-    __shared__ uint4 ssm[TabSpec<T>::sm ? 256 : 1];
+    __shared__ uint2 sks[TabSpec<T>::ks ? 128 : 1];
+    __shared__ uint2 ssm[TabSpec<T>::sm ? 256 : 1];
     __shared__ int s_next;                        // next stage to hand out
     __shared__ unsigned long long s_best[NT][NW];  // argmax reduction
 

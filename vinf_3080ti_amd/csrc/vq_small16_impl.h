@@ -195,12 +195,11 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S1
 
     __shared__ uint2 s8[TabSpec<T>::n8 > 0 ? TabSpec<T>::n8 : 1];  // IQ grids (staged before the first barrier)
     __shared__ uint32_t s4[TabSpec<T>::n4 > 0 ? TabSpec<T>::n4 : 1];
-    __shared__ uint4 sks[1], ssm[1];
+    __shared__ uint2 sks[TabSpec<T>::ks ? 128 : 1], ssm[TabSpec<T>::sm ? 256 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lr = lane & 15, lk = lane >> 4;
-    static_assert(!TabSpec<T>::ks && !TabSpec<T>::sm, "sign tables are not staged here");
     const Tabs tabs = stage_tabs<T>(s8, s4, sks, ssm);
     int jb = 0;
     while (jb + 1 < J.n && static_cast<int>(blockIdx.x) >= J.tile0[jb + 1]) ++jb;

@@ -91,26 +91,25 @@ __device__ __forceinline__ Grids global_grids() {
 }
 
 // ---- LDS tables ----------------------------------------------------------------------------------------
-// Sign-mask entry for 8 sign bits b: m = 0xFF in byte k where bit k is set (lo dword: bits 0-3, hi: 4-7),
-// e = m & 0x01010101; applying it to magnitudes g >= 1 as (g ^ m) + e negates exactly the flagged bytes.
-__device__ __forceinline__ uint4 sign_entry(uint32_t b) {
-    const uint32_t lo = ((b & 15u) * 0x00204081u) & 0x01010101u;
-    const uint32_t hi = (((b >> 4) & 15u) * 0x00204081u) & 0x01010101u;
-    return make_uint4(lo * 0xFFu, hi * 0xFFu, lo, hi);
-}
+// Sign entry for 8 sign bits b: the v_perm_b32 selectors of sign4 (vq_slices.h) for bits 0-3 (lo) and 4-7 (hi):
+// byte k selects byte k of -g (selector k + 4) where bit k is set, else byte k of g.
+__host__ __device__ constexpr uint32_t sign_sel4(uint32_t s4) { return ((s4 * 0x00810204u) & 0x04040404u) | 0x03020100u; }
+__device__ __forceinline__ uint2 sign_entry(uint32_t b) { return uint2{sign_sel4(b & 15u), sign_sel4((b >> 4) & 15u)}; }
 
 template <int T>
 struct TabSpec {
     static constexpr int n8 = T == VQ_IQ2_XXS ? 256 : T == VQ_IQ2_XS ? 512 : T == VQ_IQ2_S ? 1024 : 0;
     static constexpr int n4 = T == VQ_IQ3_XXS ? 256 : T == VQ_IQ3_S ? 512 : 0;
-    // Sign tables: no decoder reads them any more (signs are built in registers, sign4 in vq_slices.h).
-    static constexpr bool ks = false;
+    // Sign bits -> permute selectors, one 8-byte LDS read per 8 weights instead of ~8 VALU (the parity bit and
+    // the two selectors): the 7-bit ksigns of IQ2_XXS and IQ2_XS (-6 % and -1 to -3.5 % per launch). Measured
+    // slower and not taken: IQ3_XXS (ksigns; +4-6 %) and IQ2_S (raw 8 bits, 256 entries; +3.5 %).
+    static constexpr bool ks = T == VQ_IQ2_XXS || T == VQ_IQ2_XS;
     static constexpr bool sm = false;
 };
 
 // Workgroup-wide: fill the LDS tables type T needs (caller synchronises afterwards).
 template <int T>
-__device__ __forceinline__ Tabs stage_tabs(uint2 *s8, uint32_t *s4, uint4 *sks, uint4 *ssm) {
+__device__ __forceinline__ Tabs stage_tabs(uint2 *s8, uint32_t *s4, uint2 *sks, uint2 *ssm) {
     const Grids g = global_grids();
     Tabs tb{};
     if constexpr (TabSpec<T>::n8 > 0) {
@@ -136,27 +135,17 @@ __device__ __forceinline__ Tabs stage_tabs(uint2 *s8, uint32_t *s4, uint4 *sks, 
 
 // Global-memory copies of the sign tables for the (non-hot) hook kernels.
 struct SignTabs {
-    uint4 ks[128], sm[256];
+    uint2 ks[128], sm[256];
 };
 constexpr SignTabs make_sign_tabs() {
     SignTabs t{};
     for (uint32_t i = 0; i < 256; ++i) {
-        uint32_t lo = 0, hi = 0;
-        for (int k = 0; k < 4; ++k) {
-            lo |= ((i >> k) & 1u) << (8 * k);
-            hi |= ((i >> (k + 4)) & 1u) << (8 * k);
-        }
-        t.sm[i] = uint4{lo * 0xFFu, hi * 0xFFu, lo, hi};
+        t.sm[i] = uint2{sign_sel4(i & 15u), sign_sel4(i >> 4)};
         if (i < 128) {
-            uint32_t b = i, par = 0;
+            uint32_t par = 0;
             for (int k = 0; k < 7; ++k) par ^= (i >> k) & 1u;
-            b |= par << 7;
-            uint32_t l2 = 0, h2 = 0;
-            for (int k = 0; k < 4; ++k) {
-                l2 |= ((b >> k) & 1u) << (8 * k);
-                h2 |= ((b >> (k + 4)) & 1u) << (8 * k);
-            }
-            t.ks[i] = uint4{l2 * 0xFFu, h2 * 0xFFu, l2, h2};
+            const uint32_t b = i | (par << 7);
+            t.ks[i] = uint2{sign_sel4(b & 15u), sign_sel4(b >> 4)};
         }
     }
     return t;
