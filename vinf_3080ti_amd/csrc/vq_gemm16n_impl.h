@@ -51,6 +51,9 @@ struct G16N {
         else
             return pc == 0 ? 32 + 32 * n + 16 * p : 16 * p;
     }
+    // Q3_K's two pieces of row R sit in the step slot in swapped order when bit 2 of R is set: with its 64-byte
+    // row pitch, rows R and R + 4 would otherwise read the same banks.
+    __device__ static int pslot(int pc, int R) { return Q6 ? pc : pc ^ ((R >> 2) & 1); }
     // Super-block element of MFMA chunk q = 4 c + lk of step j.
     __device__ static int bpos(int j, int q) {
         return 128 * (j >> 1) + 32 * (2 * (q >> 2) + ((q & 3) >> 1)) + 16 * (j & 1) + 8 * (q & 1);
@@ -104,9 +107,10 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         uint8_t *const slot = s_step[st & 1];
 #pragma unroll
         for (int k = 0; k < G::CODE_DMA; ++k) {
-            const int ci = 64 * k + lane, rr = 32 * wv + ci / G::CPR, ch = ci % G::CPR;
+            const int ci = 64 * k + lane, rr = 32 * wv + ci / G::CPR, ch = ci % G::CPR;  // slot position of row rr
             const int row = min(r0 + rr, rows - 1) - r0;
-            const uint32_t a = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + G::poff(ch >> 1, n, p));
+            const int pc = G::pslot(ch >> 1, rr);  // the piece stored there (pslot is its own inverse)
+            const uint32_t a = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + G::poff(pc, n, p));
             const uint32_t off = (a & ~15u) + ((ch & 1) && (a & 15u) ? 16u : 0u);
             dma16(wbase, off, slot + 1024 * (G::CODE_DMA * wv + k));
         }
@@ -175,8 +179,8 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         for (int rb = 0; rb < RB; ++rb) {
             const int R = wr + 16 * rb + lr;
             const int base = R * G::CPR * 16 + mis(R, sb) + hf;
-            ra[rb] = g16n_read8(slot, base + (G::Q6 ? 32 * kl : 0));
-            rh[rb] = g16n_read8(slot, base + (G::Q6 ? 64 : 32));
+            ra[rb] = g16n_read8(slot, base + 32 * G::pslot(G::Q6 ? kl : 0, R));
+            rh[rb] = g16n_read8(slot, base + 32 * G::pslot(G::Q6 ? 2 : 1, R));
         }
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
