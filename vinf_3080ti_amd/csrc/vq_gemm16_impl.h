@@ -192,7 +192,11 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
         uint8_t *const slot = s_step[st % kG16Ring];
         {
             const int row = min(r0 + 32 * wv + (lane >> 1), rows - 1) - r0;
-            const uint32_t off = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + G::QOFF + 32 * j + 16 * (lane & 1));
+            // The row's two 16-byte halves in swapped order when bit 3 of its tile row is set (rows R and R + 8
+            // would read the same LDS banks at the 32-byte row pitch).
+            const int rr = 32 * wv + (lane >> 1);
+            const uint32_t off = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + G::QOFF + 32 * j +
+                                                       16 * ((lane & 1) ^ ((rr >> 3) & 1)));
             dma16(wbase, off, slot + 1024 * wv);
         }
 #pragma unroll
@@ -268,7 +272,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
             const int row = wr + 16 * rb + lr;
             const uint32_t sw = j < 2 ? scl[rb] : sch[rb];
             const g16h2 sc = g16_pair(sw, ssel) - k1024;
-            const uint2 q = *reinterpret_cast<const uint2 *>(slot + row * 32 + 8 * lk);
+            const uint2 q = *reinterpret_cast<const uint2 *>(slot + row * 32 + 16 * ((lk >> 1) ^ ((row >> 3) & 1)) + 8 * (lk & 1));
             uint32_t lo0 = q.x & 0x0F0F0F0Fu, lo1 = q.y & 0x0F0F0F0Fu;
             uint32_t hi0 = (q.x >> 4) & 0x0F0F0F0Fu, hi1 = (q.y >> 4) & 0x0F0F0F0Fu;
             if constexpr (T == VQ_Q5_K) {
