@@ -8,7 +8,7 @@ namespace vq {
 
 // Activation image geometry of the streaming kernel.
 constexpr int kXLdsMax = 64 * 1024;  // bytes of activation records one launch keeps in LDS
-constexpr int kXPad = 32;            // bytes of padding after each 256 codes of the image
+constexpr int kXPad = 16;            // bytes of padding after each 256 codes of the image (bank spread)
 // Bytes of one token's activation image (codes padded per 256, then 8 bytes of scales per 32-group).
 __host__ __device__ inline int x_image_bytes(int cols) {
     return (((cols / 32 + 7) / 8) * (256 + kXPad) + (cols / 32) * 8 + 15) / 16 * 16;
