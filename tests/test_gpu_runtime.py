@@ -180,11 +180,14 @@ def test_qmv_group_and_lmhead_argmax(rt, oracle_mod, cols):
         rt.free(n)
 
 
-def test_gemm_min_rows_routes_prompts_to_the_mfma_contraction(rt, oracle_mod):
-    rows, cols, ntok = 200, 2048, 70
-    raw = synth.baseline_rows(T.Q6_K, rows, cols, 12)
+@pytest.mark.parametrize("ty", [T.Q6_K, T.Q3_K, T.Q4_K], ids=lambda t: t.name)
+def test_gemm_min_rows_routes_prompts_to_the_mfma_contraction(rt, oracle_mod, ty):
+    """Runtime.qmv with ntok >= gemm_min_rows: packed activations and the f16-MFMA prefill contraction (its
+    workspace from the runtime), 201 rows (a ragged last row tile) x 70 tokens."""
+    rows, cols, ntok = 201, 2048, 70
+    raw = synth.baseline_rows(ty, rows, cols, 12)
     x = np.random.default_rng(12).standard_normal((ntok, cols)).astype(np.float32)
-    rt.upload_raw("pf", raw.tobytes(), T.Q6_K, cols, rows)
+    rt.upload_raw("pf", raw.tobytes(), ty, cols, rows)
     rt.alloc("pfx", cols * ntok)
     rt.alloc("pfy", rows * ntok)
     rt.write_floats("pfx", x.reshape(-1).tolist())
@@ -194,7 +197,7 @@ def test_gemm_min_rows_routes_prompts_to_the_mfma_contraction(rt, oracle_mod):
     finally:
         rt.set_gemm_min_rows(0)
     got = np.array(rt.read_floats("pfy"), np.float32).reshape(ntok, rows)
-    assert rel_l2(got, oracle_mod.qmv(int(T.Q6_K), raw, rows, cols, x, ntok)) <= 1e-5
+    assert rel_l2(got, oracle_mod.qmv(int(ty), raw, rows, cols, x, ntok)) <= 1e-5
     with pytest.raises(ValueError):
         rt.set_gemm_min_rows(-1)
     rt.free("pf")
