@@ -1027,9 +1027,9 @@ def main() -> None:
     if not args.no_per_type:
         for ty in PER_TYPE:
             log(f"per-type: {TYPE_NAMES[ty]} 5120x17408")
-            r = bench_matvec(torch, hip, ty, 5120, 17408, args.ntok)
+            r = bench_matvec(torch, hip, ty, 5120, 17408, args.ntok, reps=3)  # median of 3 graph replays
             per_type[TYPE_NAMES[ty]] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
-        r = bench_matvec(torch, hip, Q4_K, 4096, 4096, args.ntok)
+        r = bench_matvec(torch, hip, Q4_K, 4096, 4096, args.ntok, reps=3)
         per_type["Q4_K@4096x4096"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
         for ty in (IQ4_XS, IQ3_S, IQ2_XXS):  # config 3 at batch 8, routed as vq_qmv routes it
             log(f"per-type batch 8: {TYPE_NAMES[ty]} 5120x17408")
