@@ -62,8 +62,12 @@ typedef float g16f4 __attribute__((ext_vector_type(4)));
 //    batch it runs in (the reference's contract for its prompt kernels, qwen_runtime.cu:1883-1885), at 10-20 %
 //    more time at 512 tokens (more partial tiles to add).
 struct G16Plan {
-    int tiles, ntt, nsb, W, per_xcd, maxseg;
+    int tiles, ntt, nrt, nsb, W, per_xcd, maxseg;
     long U;
+    // Tile order: token-tile major (tile = tt * nrt + rt), so the workgroups of one XCD (consecutive shares) work
+    // on one token tile, whose activation tile then stays in that XCD's L2.
+    __host__ __device__ int tile_rt(int tile) const { return tile % nrt; }
+    __host__ __device__ int tile_tt(int tile) const { return tile / nrt; }
     __host__ __device__ int wg_of(long u) const { return static_cast<int>(((u + 1) * W - 1) / U); }  // owner of u
     __host__ __device__ long u0(int b) const { return static_cast<long>(b) * U / W; }
 };
@@ -71,6 +75,7 @@ inline G16Plan g16_plan(int rows, int cols, int M, int cus, bool invariant = fal
     G16Plan p{};
     p.ntt = (M + kG16BN - 1) / kG16BN;
     const int row_tiles = (rows + kG16BM - 1) / kG16BM;
+    p.nrt = row_tiles;
     p.tiles = row_tiles * p.ntt;
     p.nsb = cols >> 8;
     p.U = static_cast<long>(p.tiles) * p.nsb;
@@ -161,8 +166,8 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     __shared__ __attribute__((aligned(1024))) uint8_t s_sb[2][G::SB_BYTES];
 
     // Workgroup id -> share: consecutive ids go round-robin over the 8 XCDs; the ids one XCD receives own
-    // consecutive shares, i.e. a contiguous range of tiles (all token tiles of a row tile share its weights in
-    // that XCD's L2).
+    // consecutive shares, i.e. a contiguous range of tiles: row tiles of one token tile, which share its
+    // activations in that XCD's L2 (G16Plan's tile order).
     const int b = blockIdx.x;
     const int v = (b & 7) * pl.per_xcd + (b >> 3);
     if (v >= pl.W) return;
@@ -178,11 +183,43 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     const int tile = static_cast<int>(u / nsb);
     const int sb0 = static_cast<int>(u - static_cast<long>(tile) * nsb);
     const int sb1 = ue - u < nsb - sb0 ? sb0 + static_cast<int>(ue - u) : nsb;
-    const int rt = tile / pl.ntt, tt = tile - rt * pl.ntt;
+    const int rt = pl.tile_rt(tile), tt = pl.tile_tt(tile);
     const int r0 = rt * kG16BM, t0 = tt * kG16BN;
     const int nsteps = (sb1 - sb0) * 4;
     const uint8_t *const wbase = w + static_cast<size_t>(r0) * row_bytes;  // wave-uniform
 
+    // Lane offsets of the DMAs, fixed for the segment (the step moves only the wave-uniform base, so a copy costs
+    // no VALU): the wave's code row piece, its four activation chunks, and its super-block slot chunks.
+    uint32_t vo_code, vo_b[4], vo_sb[G::SB_DMA];
+    {
+        const int row = min(r0 + 32 * wv + (lane >> 1), rows - 1) - r0;
+        // The row's two 16-byte halves in swapped order when bit 3 of its tile row is set (rows R and R + 8
+        // would read the same LDS banks at the 32-byte row pitch).
+        const int rr = 32 * wv + (lane >> 1);
+        vo_code = static_cast<uint32_t>(row * row_bytes + G::QOFF + 16 * ((lane & 1) ^ ((rr >> 3) & 1)));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int ii = (4 * wv + k) & 15;
+            const int trow = 8 * ii + (lane >> 3);
+            const int tok = min(t0 + trow, M - 1);
+            const int c = (lane & 7) ^ ((trow >> 1) & 7);
+            vo_b[k] = static_cast<uint32_t>((static_cast<long>(tok) * cols + 8 * c) * 2);
+        }
+#pragma unroll
+        for (int k = 0; k < G::SB_DMA; ++k) {
+            const int i = G::SB_DMA * wv + k;
+            const int ci = 64 * i + lane;
+            constexpr int CH = G::HB / 16, NHC = kG16BM * G::HB / 16;
+            if (i * 64 < NHC) {
+                const int hrow = min(r0 + ci / CH, rows - 1) - r0;
+                vo_sb[k] = static_cast<uint32_t>(hrow * row_bytes + 16 * (ci % CH));
+            } else {
+                const int cj = ci - NHC;
+                const int tok = min(t0 + (cj >> 1), M - 1);
+                vo_sb[k] = static_cast<uint32_t>((static_cast<long>(tok) * nsb * 16 + 8 * (cj & 1)) * 2);
+            }
+        }
+    }
     // DMA of step st (j = st % 4 of super-block sb0 + st / 4) into ring slot st % 3 and super-block slot sb & 1.
     // Per wave: codes (rows 32 wv .. +32, two lanes per row), 4 of the 32 KB of b_hi/b_lo (8 tokens per 1 KB,
     // chunk position p of token row r holds chunk p ^ ((r >> 1) & 7): the 16 rows an MFMA fragment reads then
@@ -190,42 +227,24 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     auto issue = [&](int st) {
         const int sb = sb0 + (st >> 2), j = st & 3;
         uint8_t *const slot = s_step[st % kG16Ring];
-        {
-            const int row = min(r0 + 32 * wv + (lane >> 1), rows - 1) - r0;
-            // The row's two 16-byte halves in swapped order when bit 3 of its tile row is set (rows R and R + 8
-            // would read the same LDS banks at the 32-byte row pitch).
-            const int rr = 32 * wv + (lane >> 1);
-            const uint32_t off = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + G::QOFF + 32 * j +
-                                                       16 * ((lane & 1) ^ ((rr >> 3) & 1)));
-            dma16(wbase, off, slot + 1024 * wv);
-        }
+        dma16s(wbase + static_cast<long>(sb) * G::UB + 32 * j, vo_code, slot + 1024 * wv);
+        const long kb = (256L * sb + 64 * j) * 2;  // the step's byte offset in a token row of b_hi / b_lo
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int i = 4 * wv + k, ii = i & 15;
-            const int row = 8 * ii + (lane >> 3);
-            const int tok = min(t0 + row, M - 1);
-            const int c = (lane & 7) ^ ((row >> 1) & 7);
-            const uint32_t off = static_cast<uint32_t>((static_cast<long>(tok) * cols + 256L * sb + 64 * j + 8 * c) * 2);
-            dma16(i < 16 ? static_cast<const void *>(bh) : static_cast<const void *>(bl), off,
-                  slot + kG16BM * 32 + (i < 16 ? 0 : kG16BN * 128) + 1024 * ii);
+            dma16s(reinterpret_cast<const uint8_t *>(i < 16 ? bh : bl) + kb, vo_b[k],
+                   slot + kG16BM * 32 + (i < 16 ? 0 : kG16BN * 128) + 1024 * ii);
         }
         if (j != 0) return;  // the super-block slot: once, with the super-block's first step
         uint8_t *const sbs = s_sb[sb & 1];
 #pragma unroll
         for (int k = 0; k < G::SB_DMA; ++k) {
             const int i = G::SB_DMA * wv + k;
-            const int ci = 64 * i + lane;
-            constexpr int CH = G::HB / 16, NHC = kG16BM * G::HB / 16;
-            if (i * 64 < NHC) {
-                const int row = min(r0 + ci / CH, rows - 1) - r0;
-                const uint32_t off = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + 16 * (ci % CH));
-                dma16(wbase, off, sbs + 1024 * i);
-            } else {
-                const int cj = ci - NHC;
-                const int tok = min(t0 + (cj >> 1), M - 1);
-                const uint32_t off = static_cast<uint32_t>(((static_cast<long>(tok) * nsb + sb) * 16 + 8 * (cj & 1)) * 2);
-                dma16(xs, off, sbs + 1024 * i);
-            }
+            constexpr int NHC = kG16BM * G::HB / 16;
+            if (i * 64 < NHC)
+                dma16s(wbase + static_cast<long>(sb) * G::UB, vo_sb[k], sbs + 1024 * i);
+            else
+                dma16s(reinterpret_cast<const uint8_t *>(xs) + sb * 32, vo_sb[k], sbs + 1024 * i);
         }
     };
 
@@ -391,7 +410,7 @@ __global__ __launch_bounds__(512) void g16_reduce_kernel(const float *__restrict
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wr = 16 * RB * (wv % (16 / RB)), wt = 16 * TB * (wv / (16 / RB)), lr = lane & 15, lk = lane >> 4;
     const int rb = pair / TB, tb = pair % TB;
-    const int rt = tile / pl.ntt, tt = tile - rt * pl.ntt;
+    const int rt = pl.tile_rt(tile), tt = pl.tile_tt(tile);
     const int t = tt * kG16BN + wt + 16 * tb + lr, r = rt * kG16BM + wr + 16 * rb + 4 * lk;
     const float *const base = part + static_cast<size_t>(tile) * pl.maxseg * kG16TileFloats +
                               static_cast<size_t>((rb * TB + tb) * 4) * 512 + tid;

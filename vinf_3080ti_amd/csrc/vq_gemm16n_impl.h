@@ -91,7 +91,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
     const int tile = static_cast<int>(u / nsb);
     const int sb0 = static_cast<int>(u - static_cast<long>(tile) * nsb);
     const int sb1 = ue - u < nsb - sb0 ? sb0 + static_cast<int>(ue - u) : nsb;
-    const int rt = tile / pl.ntt, tt = tile - rt * pl.ntt;
+    const int rt = pl.tile_rt(tile), tt = pl.tile_tt(tile);
     const int r0 = rt * kG16BM, t0 = tt * kG16BN;
     const int nsteps = (sb1 - sb0) * 4;
     const uint8_t *const wbase = w + static_cast<size_t>(r0) * row_bytes;  // 16-byte aligned (r0 % 256 == 0)

@@ -25,6 +25,12 @@ __device__ __forceinline__ void dma16(const void *base, uint32_t voff, void *dst
                  "v"(dst)
                  : "memory", "m0");
 }
+// The same copy with base and dst in SGPRs (dst still a pointer operand of the asm, see dma16): no VALU per copy
+// when the caller's base and dst are already uniform values.
+__device__ __forceinline__ void dma16s(const void *base, uint32_t voff, void *dst) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, %0" ::"s"(base), "v"(voff), "s"(lds_addr(dst)), "s"(dst)
+                 : "memory", "m0");
+}
 template <int N>
 __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
