@@ -158,10 +158,8 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
                                                                   const _Float16 *__restrict__ bl,
                                                                   const _Float16 *__restrict__ xs,
                                                                   const float *__restrict__ inv, int M, G16Plan pl,
-                                                                  float *__restrict__ y, float *__restrict__ part,
-                                                                  unsigned long long *tm) {
+                                                                  float *__restrict__ y, float *__restrict__ part) {
     using G = G16Geo<T>;
-    (void)tm;
     __shared__ __attribute__((aligned(1024))) uint8_t s_step[kG16Ring][G::STEP_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t s_sb[2][G::SB_BYTES];
 
@@ -455,9 +453,7 @@ int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws,
         qgemm16_kernel<T><<<dim3(8 * pl.per_xcd), dim3(64 * kG16Waves), 0, s>>>(
             w, rows, cols, rb, reinterpret_cast<const _Float16 *>(base + l.bh),
             reinterpret_cast<const _Float16 *>(base + l.bl), reinterpret_cast<const _Float16 *>(base + l.xs),
-            reinterpret_cast<const float *>(base + l.inv), M, pl, y, part,
-            nullptr
-        );
+            reinterpret_cast<const float *>(base + l.inv), M, pl, y, part);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return static_cast<int>(e);
         g16_reduce_kernel<kG16RB><<<dim3(16 * pl.tiles), dim3(512), 0, s>>>(part, pl, rows, M, y);
