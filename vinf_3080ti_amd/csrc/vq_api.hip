@@ -279,7 +279,9 @@ __global__ __launch_bounds__(256) void gemm_xsplit_kernel(const uint8_t *__restr
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     int E = 0;
     (void)frexpf(127.0f * m, &E);  // 127 m < 2^E
-    const float sc = m > 0.0f ? ldexpf(1.0f, 15 - E) : 1.0f;
+    // 2^(15 - E) puts the token's largest |b| just below 2^15; capped at 2^126 so that it and 1/sc stay finite
+    // and normal for tokens whose activations are below ~1e-32 (the values then stay below 2^15 instead).
+    const float sc = m > 0.0f ? ldexpf(1.0f, min(15 - E, 126)) : 1.0f;
     const size_t base = static_cast<size_t>(t) * cols;
     for (int c = tid; c < cols / 8; c += 256) {
         const float ds = xd[c >> 2] * sc;

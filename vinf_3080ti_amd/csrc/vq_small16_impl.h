@@ -298,7 +298,7 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S1
         for (int g = 0; g < ngr; ++g) m = fmaxf(m, xdg[tid * (kS16KR / 32) + g]);
         int E = 0;
         (void)frexpf(127.0f * m, &E);
-        tsc[tid] = m > 0.0f ? ldexpf(1.0f, 15 - E) : 1.0f;
+        tsc[tid] = m > 0.0f ? ldexpf(1.0f, min(15 - E, 126)) : 1.0f;  // capped: finite for tiny tokens
     }
     __syncthreads();
     for (int i = tid; i < ntok * (kw / 4); i += blockDim.x) {
