@@ -378,14 +378,16 @@ def test_gated_delta_seg_snapshots_single_segment(rt, oracle_mod):
 @pytest.mark.parametrize("heads,kvh,hd", [(QW_HEADS, QW_KVH, QW_HD), (8, 2, 128), (6, 6, 64), (4, 1, 40)])
 @pytest.mark.parametrize("ntok,seq_len,bidirectional,window", [(37, 1, 0, 0), (16, 300, 0, 0), (9, 50, 1, 0),
                                                                (70, 20, 0, 33)])
-def test_prompt_attention_matches_oracle(rt, oracle_mod, elem, heads, kvh, hd, ntok, seq_len, bidirectional, window):
+@pytest.mark.parametrize("qmag", [1.0, 1e-36])
+def test_prompt_attention_matches_oracle(rt, oracle_mod, elem, heads, kvh, hd, ntok, seq_len, bidirectional, window,
+                                         qmag):
     """attention over more than 8 query rows (the MFMA kernel; the reference's tiled / tensor-core prompt kernels,
     qwen_runtime.cu:181-393): GQA groups of 6, 4, 1 and 4 heads (one workgroup holds 4), hd 256 / 128 / 64 and a
     ragged 40, causal from position 0, after a cached prefix, bidirectional and sliding window; fp32 operands
     and accumulation, so held to the decode kernel's bar."""
     rng = np.random.default_rng(ntok * 31 + hd + heads + elem + window)
     max_seq = seq_len + ntok + 3
-    q = rng.standard_normal((ntok, heads, hd)).astype(np.float32)
+    q = (rng.standard_normal((ntok, heads, hd)) * qmag).astype(np.float32)
     dt = np.float32 if elem == 4 else np.float16
     kc = (rng.standard_normal((kvh, max_seq, hd)) * 0.3).astype(dt)
     vc = rng.standard_normal((kvh, max_seq, hd)).astype(dt)
@@ -467,12 +469,14 @@ def test_decode_attention_split_and_per_row_kernels(oracle_mod, elem, ntok, seq_
 
 @pytest.mark.parametrize("heads,kvh,hd,ntok,seq_len,qmag", [(32, 2, 128, 8, 2000, 1.0), (8, 8, 64, 1, 5000, 1.0),
                                                             (24, 4, 256, 1, 33, 1e3), (24, 4, 256, 3, 300, 1e-3),
-                                                            (4, 1, 128, 7, 129, 1.0), (24, 4, 256, 8, 9000, 1.0)])
+                                                            (4, 1, 128, 7, 129, 1.0), (24, 4, 256, 8, 9000, 1.0),
+                                                            (24, 4, 256, 2, 300, 1e-36), (8, 2, 128, 1, 700, 0.0)])
 def test_decode_attention_fp16_cache_shapes(oracle_mod, heads, kvh, hd, ntok, seq_len, qmag):
     """The fp16-cache decode kernel (f16 MFMA on exact hi/lo splits of the query and the softmax weights) over
     head shapes 64/128/256, groups of 1 to 16 query heads per kv head (up to 8 query groups of 16 vectors), one
-    chunk (no merge) and many, and queries of magnitude 1e3 and 1e-3 (the per-vector power-of-two scaling):
-    within the fp32 bar of the float64 restatement, bit-identical on a rerun."""
+    chunk (no merge) and many, and queries of magnitude 1e3, 1e-3, 1e-36 and 0 (the per-vector power-of-two
+    scaling, capped so that tiny queries give near-uniform weights, not NaN): within the fp32 bar of the float64
+    restatement, bit-identical on a rerun."""
     torch = pytest.importorskip("torch")
     if not torch.cuda.is_available():
         pytest.skip("no GPU")

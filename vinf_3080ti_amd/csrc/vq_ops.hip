@@ -675,7 +675,10 @@ __device__ __forceinline__ float fa16_q_split(const float4 (&qr)[HD / 16], float
     amax = xor32_max(amax);
     int ex = 0;
     if (amax > 0.0f && amax <= 3.0e38f) frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
-    const float up = ldexpf(1.0f, 14 - ex);
+    // Capped at 2^126 so that the scale and its inverse stay finite for queries below ~1e-34 (their scores are
+    // then tiny, as they should be, instead of NaN).
+    const int e2 = 14 - ex < 126 ? 14 - ex : 126;
+    const float up = ldexpf(1.0f, e2);
 #pragma unroll
     for (int u = 0; u < HD / 32; ++u) {
         const float v[8] = {qr[2 * u].x, qr[2 * u].y, qr[2 * u].z, qr[2 * u].w,
@@ -688,7 +691,7 @@ __device__ __forceinline__ float fa16_q_split(const float4 (&qr)[HD / 16], float
             ql[u][j] = l;
         }
     }
-    return ldexpf(1.0f, ex - 14) * 1.44269504088896341f;  // S in base-2 units: the softmax uses exp2
+    return ldexpf(1.0f, -e2) * 1.44269504088896341f;  // S in base-2 units: the softmax uses exp2
 }
 
 // The raw K and V of one 32-key block in registers: K as S^T A operands, V as units of four keys x one
