@@ -214,30 +214,31 @@ def test_zero_and_extreme_activations(env, oracle_mod):
 EXTREME_TOKEN_SCALES = [1.0, 1e-35, 1e-33, 3e-31, 0.0, 1e30, 1e-3]
 
 
-@pytest.mark.parametrize("route", ["prefill_f16", "small_batch_f16", "stream"])
-@pytest.mark.parametrize("ty", [T.Q4_K, T.Q6_K, T.IQ4_XS], ids=lambda t: t.name)
+@pytest.mark.parametrize("route", ["prefill", "small_batch", "stream"])
+@pytest.mark.parametrize("ty", [T.Q4_K, T.Q6_K, T.IQ4_XS, T.Q8_0, T.Q2_K], ids=lambda t: t.name)
 def test_extreme_token_scales(env, oracle_mod, route, ty):
-    """Every token within the fp32 bar of the CPU path (the zero token exactly zero) on the f16 prefill contraction,
-    the f16 small-batch matvec and the streaming matvec."""
+    """Every token within the fp32 bar of the CPU path (the zero token exactly zero) on the prefill contraction and
+    the small-batch matvec (f16 MFMA; int8 MFMA for Q8_0, Q2_K and, for prefill, IQ4_XS) and on the streaming
+    matvec."""
     torch, lib = env
     rows, cols = 300, 2048
     n = len(EXTREME_TOKEN_SCALES)
     rng = np.random.default_rng(4242 + int(ty))
     w = synth.baseline_rows(ty, rows, cols, rng)
     x = (rng.standard_normal((n, cols)) * np.array(EXTREME_TOKEN_SCALES)[:, None]).astype(np.float32)
-    if route == "prefill_f16":
-        if not lib.vq_qgemm_workspace_bytes(int(ty), rows, cols, n):
-            pytest.skip("no f16 prefill path for this type")
+    if route == "prefill":
         y = torch.full((n, rows), np.nan, dtype=torch.float32, device="cuda")
         _qgemm_ws(torch, lib, ty, wdev(torch, w), rows, cols, _pack(torch, lib, x, n, cols), n, y)
         torch.cuda.synchronize()
         got = y.cpu().numpy()
     else:
-        fast = route == "small_batch_f16"
+        fast = route == "small_batch"
         if fast:
-            assert lib.vq_qmv_path(int(ty), rows, cols, n, lib.vq_qmv_workspace_bytes_for(int(ty), rows, cols, n)) == 2
-        got = np.concatenate([gpu_qmv(torch, lib, ty, w, rows, cols, x[i:i + 4], len(x[i:i + 4]))
-                              for i in range(0, n, 4)]) if not fast else gpu_qmv(torch, lib, ty, w, rows, cols, x, n, fast=True)
+            want = 1 if ty in (T.Q8_0, T.Q2_K) else 2  # VQ_PATH_MFMA_I8 / VQ_PATH_MFMA_F16
+            assert lib.vq_qmv_path(int(ty), rows, cols, n, lib.vq_qmv_workspace_bytes_for(int(ty), rows, cols, n)) == want
+        else:
+            assert lib.vq_qmv_path(int(ty), rows, cols, n, lib.vq_qmv_workspace_bytes(cols, n)) == 0
+        got = gpu_qmv(torch, lib, ty, w, rows, cols, x, n, fast=fast)
     ref = oracle_mod.qmv(int(ty), w, rows, cols, x, n)
     assert np.isfinite(got).all(), route
     for t, scale in enumerate(EXTREME_TOKEN_SCALES):
