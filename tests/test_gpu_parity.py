@@ -146,6 +146,23 @@ def test_qmv_matches_oracle(env, oracle_mod, ty, ntok):
         assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, ntok, t)
 
 
+@pytest.mark.parametrize("ty", [T.Q4_K, T.Q3_K, T.Q6_K, T.Q8_0, T.IQ2_XXS, T.F16], ids=lambda t: t.name)
+@pytest.mark.parametrize("ntok", [17, 40])
+@pytest.mark.parametrize("fast", [False, True], ids=["min_ws", "full_ws"])
+def test_qmv_more_tokens_than_a_pass(env, oracle_mod, ty, ntok, fast):
+    """vq_qmv beyond 16 tokens (more than one streaming pass or small-batch tile), with the minimal workspace and
+    with vq_qmv_workspace_bytes_for: every token within the fp32 bar of the CPU path."""
+    torch, lib = env
+    rows, cols = 70, 1024
+    rng = np.random.default_rng(31 * ntok + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    got = gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok, fast=fast)
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok)
+    for t in range(ntok):
+        assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, ntok, t)
+
+
 @pytest.mark.parametrize(
     "ty,rows,cols",
     [(T.Q4_K, 5120, 17408), (T.Q3_K, 5120, 17408), (T.Q6_K, 5120, 17408), (T.IQ4_XS, 5120, 17408),
