@@ -814,3 +814,44 @@ def test_qmv_staged_ws_falls_back_to_streaming(env):
             torch.cuda.synchronize()
             outs.append(y.cpu().numpy())
         assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), (ty.name, ntok)
+
+
+@pytest.mark.parametrize("ty", [T.Q4_K, T.Q6_K, T.Q3_K, T.IQ2_XXS, T.IQ4_XS, T.Q8_0], ids=lambda t: t.name)
+@pytest.mark.parametrize("rows,cols", [(1, 256), (5, 768)])
+def test_tiny_matrices_every_route(env, oracle_mod, ty, rows, cols):
+    """A one-row and a five-row matrix, one or three super-blocks wide, on every route: the streaming matvec (1
+    and 3 tokens), the small-batch matvec (8 and 16 tokens), the prefill contraction (2 and 20 tokens), a grouped
+    launch of two such matrices and the fused LM-head argmax. With one row a token's output is a single sum, whose
+    relative error under fp32 reordering grows with its cancellation (up to ~5e-5 in the CPU path itself here), so
+    the bar applies to each call's whole output."""
+    torch, lib = env
+    rng = np.random.default_rng(rows * 1000 + cols + int(ty))
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    wd = wdev(torch, w)
+    for ntok, fast in ((1, False), (3, False), (8, True), (16, True)):
+        x = rng.standard_normal((ntok, cols)).astype(np.float32)
+        got = gpu_qmv(torch, lib, ty, w, rows, cols, x, ntok, fast=fast)
+        ref = oracle_mod.qmv(int(ty), w, rows, cols, x, ntok)
+        assert rel_l2(got, ref) <= REL_L2_TOL, ("qmv", ntok)
+    for M in (2, 20):
+        x = rng.standard_normal((M, cols)).astype(np.float32)
+        y = torch.full((M, rows), np.nan, dtype=torch.float32, device="cuda")
+        _qgemm_ws(torch, lib, ty, wd, rows, cols, _pack(torch, lib, x, M, cols), M, y)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        ref = oracle_mod.qmv(int(ty), w, rows, cols, x, M)
+        assert rel_l2(got, ref) <= REL_L2_TOL, ("qgemm", M)
+    x = rng.standard_normal((2, cols)).astype(np.float32)
+    ys = [torch.full((2, rows), np.nan, dtype=torch.float32, device="cuda") for _ in range(2)]
+    wa = (ctypes.c_void_p * 2)(P(wd), P(wd))
+    ra = (ctypes.c_int * 2)(rows, rows)
+    ya = (ctypes.c_void_p * 2)(*[P(t) for t in ys])
+    assert lib.vq_qmv_group_f32(int(ty), 2, wa, ra, ya, cols, P(dev(torch, x)), 2, None) == 0
+    torch.cuda.synchronize()
+    ref = oracle_mod.qmv(int(ty), w, rows, cols, x, 2)
+    for y in ys:
+        assert rel_l2(y.cpu().numpy(), ref) <= REL_L2_TOL, "group"
+    idx, logits = _lmhead(torch, lib, ty, wd, rows, cols, x, 2)
+    assert rel_l2(logits, ref) <= REL_L2_TOL, "lmhead"
+    for t in range(2):
+        assert idx[t] == int(np.argmax(logits[t]))
