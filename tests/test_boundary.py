@@ -82,6 +82,7 @@ def test_host_side_argument_checks(lib):
     # prefill: the f16-MFMA path (Q3_K-Q6_K) needs the split activations (2 x f16 per element) and more
     assert lib.vq_qgemm_workspace_bytes(int(T.Q6_K), 17408, 5120, 512) >= 4 * 512 * 5120
     assert lib.vq_qgemm_workspace_bytes(int(T.Q3_K), 17408, 5120, 512) >= 4 * 512 * 5120
+    assert lib.vq_qgemm_workspace_bytes(int(T.Q2_K), 17408, 5120, 512) >= 4 * 512 * 5120
     assert lib.vq_qgemm_workspace_bytes(int(T.Q8_0), 17408, 5120, 512) == 0
     assert lib.vq_qgemm_workspace_bytes(int(T.IQ4_XS), 17408, 5120, 512) == 0
     assert lib.vq_qgemm_workspace_bytes(int(T.Q4_K), 17408, 5120, 512) >= 4 * 512 * 5120

@@ -264,7 +264,8 @@ __device__ __forceinline__ void opaque(float &v) { asm volatile("" : "+v"(v)); }
 // X_g xd_g 2^e / 32 (X_g = the group's code sum, |X_g| <= 32 * 127) likewise; inv = 2^-e.
 __global__ __launch_bounds__(256) void gemm_xsplit_kernel(const uint8_t *__restrict__ xpack, int cols,
                                                           _Float16 *__restrict__ bh, _Float16 *__restrict__ bl,
-                                                          _Float16 *__restrict__ xs, float *__restrict__ inv) {
+                                                          _Float16 *__restrict__ xs, float *__restrict__ inv,
+                                                          int halves) {
     const int t = blockIdx.x, tid = threadIdx.x, ng = cols >> 5;
     const uint8_t *rec = xpack + static_cast<size_t>(t) * vq_xpack_stride(cols);
     const float *xd = reinterpret_cast<const float *>(rec + cols);
@@ -299,6 +300,26 @@ __global__ __launch_bounds__(256) void gemm_xsplit_kernel(const uint8_t *__restr
         *reinterpret_cast<uint4 *>(bl + base + 8 * c) = __builtin_bit_cast(uint4, l);
     }
     const int nsb = cols >> 8;
+    if (halves) {  // Q2_K: the 16 halves' X_h xd 2^e / 32, 16 hi then 16 lo per super-block
+        for (int sb = tid; sb < nsb; sb += 256) {
+            _Float16 o[32];
+#pragma unroll
+            for (int hh = 0; hh < 16; ++hh) {
+                const int g = 8 * sb + (hh >> 1);
+                const uint32_t hx = xh[g];
+                const int X = static_cast<int>(static_cast<int16_t>((hh & 1) ? hx >> 16 : hx & 0xFFFFu));
+                float v = static_cast<float>(X) * (xd[g] * sc) * 0.03125f;
+                opaque(v);
+                o[hh] = static_cast<_Float16>(v);
+                o[16 + hh] = static_cast<_Float16>(v - static_cast<float>(o[hh]));
+            }
+            uint4 *dst = reinterpret_cast<uint4 *>(xs + (static_cast<size_t>(t) * nsb + sb) * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[i] = __builtin_bit_cast(uint4, *reinterpret_cast<const _Float16(*)[8]>(o + 8 * i));
+        }
+        if (tid == 0) inv[t] = 1.0f / sc;
+        return;
+    }
     for (int sb = tid; sb < nsb; sb += 256) {
         _Float16 o[16];
 #pragma unroll
@@ -318,9 +339,9 @@ __global__ __launch_bounds__(256) void gemm_xsplit_kernel(const uint8_t *__restr
     if (tid == 0) inv[t] = 1.0f / sc;
 }
 
-// The f16 path: Q3_K, Q4_K, Q5_K, Q6_K, with the activation split addressable by the kernels' 32-bit DMA offsets.
+// The f16 path: Q2_K..Q6_K, with the activation split addressable by the kernels' 32-bit DMA offsets.
 bool gemm16_ok(int type, int cols, int M) {
-    return (type == VQ_Q3_K || type == VQ_Q4_K || type == VQ_Q5_K || type == VQ_Q6_K) &&
+    return (type == VQ_Q2_K || type == VQ_Q3_K || type == VQ_Q4_K || type == VQ_Q5_K || type == VQ_Q6_K) &&
            static_cast<long>(M) * cols < (1L << 30);
 }
 
@@ -765,7 +786,8 @@ int vq_qgemm(int type, const uint8_t *w, int rows, int cols, const void *xpack, 
 size_t vq_qgemm_workspace_bytes_ex(int type, int rows, int cols, int M, int flags) {
     if (check_matrix(type, rows, cols) || M < 1 || !gemm16_ok(type, cols, M) || (flags & ~VQ_GEMM_BATCH_INVARIANT))
         return 0;
-    return vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, device_cus(), flags & VQ_GEMM_BATCH_INVARIANT)).total;
+    return vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, device_cus(), flags & VQ_GEMM_BATCH_INVARIANT),
+                          type == VQ_Q2_K).total;
 }
 
 size_t vq_qgemm_workspace_bytes(int type, int rows, int cols, int M) {
@@ -787,11 +809,11 @@ int vq_qgemm_ws_ex(int type, const uint8_t *w, int rows, int cols, const void *x
     const long rb = row_bytes_of(type, cols);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int cus = device_cus();
-    const vq::G16Ws l = vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, cus, inv));
+    const vq::G16Ws l = vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, cus, inv), type == VQ_Q2_K);
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     gemm_xsplit_kernel<<<M, 256, 0, s>>>(static_cast<const uint8_t *>(xpack), cols, reinterpret_cast<_Float16 *>(ws + l.bh),
                                          reinterpret_cast<_Float16 *>(ws + l.bl), reinterpret_cast<_Float16 *>(ws + l.xs),
-                                         reinterpret_cast<float *>(ws + l.inv));
+                                         reinterpret_cast<float *>(ws + l.inv), type == VQ_Q2_K ? 1 : 0);
     st = hip_status(hipGetLastError());
     if (st) return st;
     return dispatch_quant(type, [&](auto tc) {

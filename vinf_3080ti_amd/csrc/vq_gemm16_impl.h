@@ -1,6 +1,6 @@
 // vq_gemm16_impl.h -- prefill contraction Y[t][r] = W[r] . x[t] on CDNA4 f16 MFMA (v_mfma_f32_16x16x32_f16) for
 // the K-quants with mins whose integer sub-block products are exact in f16 and whose blocks are 16-byte multiples
-// (Q4_K, Q5_K). Q3_K and Q6_K take qgemm16n_kernel (vq_gemm16n_impl.h) with the same plan and workspace.
+// (Q4_K, Q5_K). Q2_K, Q3_K and Q6_K take qgemm16n_kernel (vq_gemm16n_impl.h) with the same plan and workspace.
 //
 // Numerics. The reference CPU path (Cpu_qmv, qwen_cpu.c:581-641) computes per 32-group
 //   y += d * sc * xd * S - dmin * m * xd * X,   S = sum(code * xq) exact, X = sum(xq)
@@ -102,20 +102,21 @@ inline G16Plan g16_plan(int rows, int cols, int M, int cus, bool invariant = fal
 }
 
 // Workspace layout of the f16 path for M tokens of `cols` columns: b_hi [M][cols] f16, b_lo [M][cols] f16,
-// xs [M][cols/256][16] f16 (per super-block: X_g xd_g 2^e / 32 as 8 hi then 8 lo), inv [M] fp32 (2^-e),
+// xs [M][cols/256][16] f16 (per super-block: X_g xd_g 2^e / 32 as 8 hi then 8 lo; for Q2_K, whose mins apply per
+// 16 elements, [M][cols/256][32]: the 16 halves' X_h xd 2^e / 32 as 16 hi then 16 lo), inv [M] fp32 (2^-e),
 // then the partial-tile slots [tiles][maxseg][64 values][512 threads] fp32.
 constexpr size_t kG16TileFloats = static_cast<size_t>(kG16BM) * kG16BN;
 struct G16Ws {
     size_t bh, bl, xs, inv, part, total;
 };
-inline G16Ws g16_layout(int cols, int M, const G16Plan &p) {
+inline G16Ws g16_layout(int cols, int M, const G16Plan &p, bool halves = false) {
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
     G16Ws l{};
     const size_t nb = static_cast<size_t>(M) * cols * 2;
     l.bh = 0;
     l.bl = al(nb);
     l.xs = l.bl + al(nb);
-    l.inv = l.xs + al(static_cast<size_t>(M) * (cols / 256) * 32);
+    l.inv = l.xs + al(static_cast<size_t>(M) * (cols / 256) * (halves ? 64 : 32));
     l.part = l.inv + al(static_cast<size_t>(M) * 4);
     l.total = l.part + al(static_cast<size_t>(p.tiles) * p.maxseg * kG16TileFloats * 4);
     return l;
@@ -432,7 +433,7 @@ __global__ __launch_bounds__(512) void g16_reduce_kernel(const float *__restrict
     }
 }
 
-// Q3_K and Q6_K: qgemm16n_kernel (vq_gemm16n_impl.h), same plan, workspace and reduction.
+// Q2_K, Q3_K and Q6_K: qgemm16n_kernel (vq_gemm16n_impl.h), same plan, workspace and reduction.
 template <int T>
 int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
                    hipStream_t s, bool invariant);
@@ -440,7 +441,7 @@ int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws
 template <int T>
 int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
                   hipStream_t s, bool invariant) {
-    if constexpr (T == VQ_Q3_K || T == VQ_Q6_K) {
+    if constexpr (T == VQ_Q2_K || T == VQ_Q3_K || T == VQ_Q6_K) {
         return launch_gemm16n<T>(w, rows, cols, rb, ws, M, y, cus, s, invariant);
     } else if constexpr (!kGemm16<T>) {
         (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)y, (void)cus, (void)s, (void)invariant;

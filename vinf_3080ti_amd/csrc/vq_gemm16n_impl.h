@@ -1,25 +1,29 @@
-// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q3_K and Q6_K: the K-quants without mins whose
-// blocks (110 and 210 bytes) are only 2-byte aligned inside a row.
+// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q2_K, Q3_K and Q6_K: the K-quants with 16-element
+// sub-blocks whose blocks (84, 110 and 210 bytes) are only 2- or 4-byte aligned inside a row.
 //
-// Numerics: those of the Q4_K/Q5_K contraction (vq_gemm16_impl.h) without the min term. Each weight element is
-// the integer a = code * sc: (q3) * (sc - 32), |a| <= 128, for Q3_K; Q6_K's (q - 32) * sc (|.| <= 4096) as the two
-// exact f16 terms 16 (q - 32) (sc >> 4) + (q - 32) (sc & 15). Each activation element is b = xq * xd * 2^e as the
-// f16 pair b_hi + b_lo, and each super-block's C = sum a * (b_hi + b_lo) (exact products, fp32 sums) is applied
-// once: acc += d * C (qwen_cpu.c:581-641 regrouped per super-block).
+// Numerics: those of the Q4_K/Q5_K contraction (vq_gemm16_impl.h). Each weight element is the integer
+// a = code * sc: (q3) * (sc - 32), |a| <= 128, for Q3_K; q2 * sc, |a| <= 45, for Q2_K; Q6_K's (q - 32) * sc
+// (|.| <= 4096) as the two exact f16 terms 16 (q - 32) (sc >> 4) + (q - 32) (sc & 15). Each activation element is
+// b = xq * xd * 2^e as the f16 pair b_hi + b_lo, and each super-block's C = sum a * (b_hi + b_lo) (exact products,
+// fp32 sums) is applied once: acc += d * C, for Q2_K minus 32 dmin (m . XS) with the 16 sub-blocks' mins m and
+// XS_h = X_h xd 2^e / 32 (X_h the code sum of 16-element half h; qwen_cpu.c:205-230) as one
+// v_mfma_f32_16x16x16_f16 per hi and lo part (qwen_cpu.c:581-641 regrouped per super-block).
 //
 // Work split, tiles and reduction: those of qgemm16_kernel (G16Plan; 256-row x 128-token tiles, 8 waves of 32
 // rows x 128 tokens). Differences:
 //  - K order. A step is 64 elements of one super-block, but not 64 consecutive ones: step j = 2n + p takes the
-//    elements 128 n + 32 k + 16 p + i (k = 0..3, i = 0..15). Both types store element 128 n + 32 k + l as a field
+//    elements 128 n + 32 k + 16 p + i (k = 0..3, i = 0..15). The types store element 128 n + 32 k + l as a field
 //    of byte l of a 32-byte run (Q6_K: low/high nibble of ql[64 n + 32 (k & 1) + l] and bits 2k of qh[32 n + l];
-//    Q3_K: bits 2k of qs[32 n + l] and bit 4n + k of hmask[l]) and scales it by scale 8 n + 2 k + p, so a step
-//    needs one 16-byte piece of each run per row (Q6_K: 2 of ql, 1 of qh; Q3_K: 1 of qs, 1 of hmask) and every
+//    Q3_K: bits 2k of qs[32 n + l] and bit 4n + k of hmask[l]; Q2_K: bits 2k of qs[32 n + l]) and scale it by scale
+//    8 n + 2 k + p, so a step needs one 16-byte piece of each run per row (Q6_K: 2 of ql, 1 of qh; Q3_K: 1 of qs,
+//    1 of hmask; Q2_K: 1 of qs) and every
 //    16-element run of it has one scale. MFMA lane (lr, lk) with chunk c holds k = 2c + (lk >> 1), i = 8 (lk & 1)
 //    .. +8; the activation tile of the step is DMA'd in that same permuted order.
 //  - Alignment. A piece starts m = (row offset of the block) mod 16 bytes past a 16-byte boundary (m even), so
 //    each piece is DMA'd as the 16-byte-aligned pair of chunks covering it (the second one only when m > 0;
 //    otherwise the first is fetched twice) and read from LDS as three dwords realigned by v_alignbyte. The scales
-//    and d of every row come the same way, once per super-block. No read goes past the 16 bytes of padding that
+//    and d of every row come the same way, once per super-block (Q2_K: two chunk pairs, its 16 scale bytes at the
+//    block's start and d, dmin at byte 80; with its XS tile). No read goes past the 16 bytes of padding that
 //    follow the tensor.
 //  - Two step slots (one step of lead): with three, the chunk pairs and the activation tiles would not fit LDS.
 #pragma once
@@ -33,27 +37,33 @@ namespace vq {
 
 template <int T>
 struct G16N {
-    static constexpr bool Q6 = T == VQ_Q6_K;
-    static constexpr int UB = Q6 ? 210 : 110;
-    static constexpr int NPC = Q6 ? 3 : 2;         // 16-byte pieces per row and step
-    static constexpr int CPR = 2 * NPC;            // chunks DMA'd per row and step
-    static constexpr int SOFF = Q6 ? 192 : 96;     // scales; d follows them
-    static constexpr int SLEN = Q6 ? 18 : 14;      // scale bytes + d
+    static constexpr bool Q6 = T == VQ_Q6_K, Q2 = T == VQ_Q2_K;
+    static constexpr int UB = Q6 ? 210 : Q2 ? 84 : 110;
+    static constexpr int NPC = Q6 ? 3 : Q2 ? 1 : 2;  // 16-byte pieces per row and step
+    static constexpr int CPR = 2 * NPC;              // chunks DMA'd per row and step
+    static constexpr int SOFF = Q6 ? 192 : Q2 ? 0 : 96;  // scales (and, but for Q2_K, d right after them)
+    static constexpr int SLEN = Q6 ? 18 : Q2 ? 16 : 14;  // bytes from SOFF
+    static constexpr int DOFF = Q6 ? 208 : Q2 ? 80 : 108;  // d (Q2_K: then dmin)
+    static constexpr int SBR = Q2 ? 64 : 32;         // super-block slot bytes per row: chunk pairs (scales, d)
     static constexpr int CODE_BYTES = kG16BM * CPR * 16;
     static constexpr int STEP_BYTES = CODE_BYTES + 2 * kG16BN * 128;
-    static constexpr int SB_BYTES = kG16BM * 32;   // per row: the chunk pair covering scales and d
-    static constexpr int CODE_DMA = CPR / 2;       // per wave and step: 32 rows x CPR chunks
-    static_assert(kG16BM * 2 == 64 * kG16Waves, "one super-block DMA per wave");
+    static constexpr int XS_BYTES = Q2 ? kG16BN * 64 : 0;  // the tokens' XS (16 hi, 16 lo f16 each)
+    static constexpr int SB_BYTES = kG16BM * SBR + XS_BYTES;
+    static constexpr int SB_DMA = SB_BYTES / (1024 * kG16Waves);  // per wave, first step of a super-block
+    static constexpr int CODE_DMA = CPR / 2;         // per wave and step: 32 rows x CPR chunks
+    static_assert(SB_BYTES % (1024 * kG16Waves) == 0, "super-block slot split");
     // Block offset of piece pc of step (n, p).
     __device__ static int poff(int pc, int n, int p) {
         if constexpr (Q6)
             return pc == 2 ? 128 + 32 * n + 16 * p : 64 * n + 32 * pc + 16 * p;
+        else if constexpr (Q2)
+            return 16 + 32 * n + 16 * p;
         else
             return pc == 0 ? 32 + 32 * n + 16 * p : 16 * p;
     }
     // Q3_K's two pieces of row R sit in the step slot in swapped order when bit 2 of R is set: with its 64-byte
     // row pitch, rows R and R + 4 would otherwise read the same banks.
-    __device__ static int pslot(int pc, int R) { return Q6 ? pc : pc ^ ((R >> 2) & 1); }
+    __device__ static int pslot(int pc, int R) { return Q6 || Q2 ? pc : pc ^ ((R >> 2) & 1); }
     // Super-block element of MFMA chunk q = 4 c + lk of step j.
     __device__ static int bpos(int j, int q) {
         return 128 * (j >> 1) + 32 * (2 * (q >> 2) + ((q & 3) >> 1)) + 16 * (j & 1) + 8 * (q & 1);
@@ -71,6 +81,7 @@ template <int T>
 __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t *__restrict__ w, int rows, int cols,
                                                                    long row_bytes, const _Float16 *__restrict__ bh,
                                                                    const _Float16 *__restrict__ bl,
+                                                                   const _Float16 *__restrict__ xs,
                                                                    const float *__restrict__ inv, int M, G16Plan pl,
                                                                    float *__restrict__ y, float *__restrict__ part) {
     using G = G16N<T>;
@@ -125,12 +136,24 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                   slot + G::CODE_BYTES + (i < 16 ? 0 : kG16BN * 128) + 1024 * ii);
         }
         if (j != 0) return;
-        {
-            const int ci = 64 * wv + lane, rr = ci >> 1;
-            const int row = min(r0 + rr, rows - 1) - r0;
-            const uint32_t a = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + G::SOFF);
-            const uint32_t off = (a & ~15u) + ((ci & 1) && (a & 15u) + G::SLEN > 16u ? 16u : 0u);
-            dma16(wbase, off, s_sb[sb & 1] + 1024 * wv);
+#pragma unroll
+        for (int k = 0; k < G::SB_DMA; ++k) {
+            const int ci = 64 * (G::SB_DMA * wv + k) + lane;  // 16-byte chunk of the super-block slot
+            uint8_t *const dst = s_sb[sb & 1] + 1024 * (G::SB_DMA * wv + k);
+            if (ci < kG16BM * G::SBR / 16) {
+                // Row rr's chunk pair(s): Q2_K's second pair holds d and dmin (byte 80, the same misalignment).
+                const int rr = ci / (G::SBR / 16), pr = (ci >> 1) & (G::SBR / 32 - 1);
+                const int row = min(r0 + rr, rows - 1) - r0;
+                const int so = pr ? G::DOFF : G::SOFF, sl = pr ? 4 : G::SLEN;
+                const uint32_t a = static_cast<uint32_t>(row * row_bytes + static_cast<long>(sb) * G::UB + so);
+                const uint32_t off = (a & ~15u) + ((ci & 1) && (a & 15u) + sl > 16u ? 16u : 0u);
+                dma16(wbase, off, dst);
+            } else {  // Q2_K: the tokens' XS, 64 bytes each
+                const int cj = ci - kG16BM * G::SBR / 16;
+                const int tok = min(t0 + (cj >> 2), M - 1);
+                const uint32_t off = static_cast<uint32_t>(((static_cast<long>(tok) * nsb + sb) * 32 + 8 * (cj & 3)) * 2);
+                dma16(xs, off, dst);
+            }
         }
     };
 
@@ -153,9 +176,14 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         if (p == 0) {  // the half's eight scales, on its first step
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
-                const int R = wr + 16 * rb + lr, o = R * 32 + mis(R, sb);
+                const int R = wr + 16 * rb + lr, o = R * G::SBR + mis(R, sb);
                 const uint32_t sh = static_cast<uint32_t>(o & 3);
-                if constexpr (G::Q6) {
+                if constexpr (G::Q2) {  // 4-bit scales in the low nibbles of bytes 8n .. 8n + 7
+                    const uint32_t *q = reinterpret_cast<const uint32_t *>(sbs + (o & ~3) + 8 * n);
+                    const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
+                    scw[rb][0] = __builtin_amdgcn_alignbyte(d1, d0, sh) & 0x0F0F0F0Fu;
+                    scw[rb][1] = __builtin_amdgcn_alignbyte(d2, d1, sh) & 0x0F0F0F0Fu;
+                } else if constexpr (G::Q6) {
                     const uint32_t *q = reinterpret_cast<const uint32_t *>(sbs + (o & ~3) + 8 * n);
                     const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
                     scw[rb][0] = __builtin_amdgcn_alignbyte(d1, d0, sh);
@@ -180,7 +208,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
             const int R = wr + 16 * rb + lr;
             const int base = R * G::CPR * 16 + mis(R, sb) + hf;
             ra[rb] = g16n_read8(slot, base + 32 * G::pslot(G::Q6 ? kl : 0, R));
-            rh[rb] = g16n_read8(slot, base + 32 * G::pslot(G::Q6 ? 2 : 1, R));
+            if constexpr (!G::Q2) rh[rb] = g16n_read8(slot, base + 32 * G::pslot(G::Q6 ? 2 : 1, R));
         }
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -191,7 +219,11 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                 const uint32_t sw = scw[rb][c];
                 uint32_t c0, c1;
                 int isc;
-                if constexpr (G::Q6) {
+                if constexpr (G::Q2) {
+                    c0 = (ra[rb].x >> (2 * k)) & 0x03030303u;
+                    c1 = (ra[rb].y >> (2 * k)) & 0x03030303u;
+                    isc = static_cast<int>((sw >> sbyte) & 0xFFu);
+                } else if constexpr (G::Q6) {
                     c0 = ((ra[rb].x >> (4 * c)) & 0x0F0F0F0Fu) | (((rh[rb].x >> (2 * k)) & 0x03030303u) << 4);
                     c1 = ((ra[rb].y >> (4 * c)) & 0x0F0F0F0Fu) | (((rh[rb].y >> (2 * k)) & 0x03030303u) << 4);
                     isc = static_cast<int>(static_cast<int8_t>(sw >> sbyte));
@@ -228,19 +260,44 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
             }
         }
         if (j == 3) {
-            // Super-block end: acc += d C; C element q of a block is row 4 lk + q, token lr.
+            // Super-block end: acc += d C (Q2_K: - 32 dmin (m . XS)); C element q of a block is row 4 lk + q,
+            // token lr.
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
-                float dq[4];
+                float dq[4], mq[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int R = wr + 16 * rb + 4 * lk + q;
-                    dq[q] = half_to_float(*reinterpret_cast<const uint16_t *>(sbs + R * 32 + mis(R, sb) + G::SLEN - 2));
+                    const int od = R * G::SBR + mis(R, sb) + (G::Q2 ? 32 : G::SLEN - 2);
+                    const uint32_t hd = *reinterpret_cast<const uint16_t *>(sbs + od) |
+                                        (G::Q2 ? static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(sbs + od + 2)) << 16 : 0u);
+                    dq[q] = half_to_float(hd);
+                    mq[q] = 32.0f * half_to_float(hd >> 16);
+                }
+                g16h4 amin = {};
+                if constexpr (G::Q2) {
+                    // A_min fragment: row wr + 16 rb + lr, k = 4 lk .. +4 -> the mins (high nibbles) of
+                    // sub-blocks 4 lk .. 4 lk + 3.
+                    const int R = wr + 16 * rb + lr;
+                    const uint32_t mw = (g16n_read8(sbs, R * G::SBR + mis(R, sb) + 4 * lk).x >> 4) & 0x0F0F0F0Fu;
+                    const g16h2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+                    const g16h2 m01 = g16_pair(mw, 0x04010400u) - k1024, m23 = g16_pair(mw, 0x04030402u) - k1024;
+                    amin = g16h4{m01[0], m01[1], m23[0], m23[1]};
                 }
 #pragma unroll
                 for (int tb = 0; tb < TB; ++tb) {
+                    if constexpr (G::Q2) {
+                        const uint8_t *const sx = sbs + kG16BM * G::SBR + (wt + 16 * tb + lr) * 64 + 8 * lk;
+                        const g16h4 bm_hi = *reinterpret_cast<const g16h4 *>(sx);
+                        const g16h4 bm_lo = *reinterpret_cast<const g16h4 *>(sx + 32);
+                        g16f4 cm = __builtin_amdgcn_mfma_f32_16x16x16f16(amin, bm_hi, g16f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        cm = __builtin_amdgcn_mfma_f32_16x16x16f16(amin, bm_lo, cm, 0, 0, 0);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[rb][tb][q] = fmaf(dq[q], C[rb][tb][q], acc[rb][tb][q]);
+                        for (int q = 0; q < 4; ++q) acc[rb][tb][q] = fmaf(dq[q], C[rb][tb][q], fmaf(-mq[q], cm[q], acc[rb][tb][q]));
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) acc[rb][tb][q] = fmaf(dq[q], C[rb][tb][q], acc[rb][tb][q]);
+                    }
                     C[rb][tb] = g16f4{0.f, 0.f, 0.f, 0.f};
                 }
             }
@@ -289,12 +346,12 @@ template <int T>
 int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
                    hipStream_t s, bool invariant) {
     const G16Plan pl = g16_plan(rows, cols, M, cus, invariant);
-    const G16Ws l = g16_layout(cols, M, pl);
+    const G16Ws l = g16_layout(cols, M, pl, T == VQ_Q2_K);
     uint8_t *base = static_cast<uint8_t *>(const_cast<void *>(ws));
     float *const part = reinterpret_cast<float *>(base + l.part);
     qgemm16n_kernel<T><<<dim3(8 * pl.per_xcd), dim3(64 * kG16Waves), 0, s>>>(
         w, rows, cols, rb, reinterpret_cast<const _Float16 *>(base + l.bh), reinterpret_cast<const _Float16 *>(base + l.bl),
-        reinterpret_cast<const float *>(base + l.inv), M, pl, y, part);
+        reinterpret_cast<const _Float16 *>(base + l.xs), reinterpret_cast<const float *>(base + l.inv), M, pl, y, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     g16_reduce_kernel<kG16RB><<<dim3(16 * pl.tiles), dim3(512), 0, s>>>(part, pl, rows, M, y);

@@ -76,7 +76,7 @@ __device__ __forceinline__ void s16_frag(uint32_t c0, uint32_t c1, int isc, g16h
     const g16h2 k = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
     g16h2 v[4] = {g16_pair(c0, 0x04010400u), g16_pair(c0, 0x04030402u), g16_pair(c1, 0x04010400u),
                   g16_pair(c1, 0x04030402u)};  // 1024 + code
-    if constexpr (T == VQ_Q4_K || T == VQ_Q5_K) {
+    if constexpr (T == VQ_Q4_K || T == VQ_Q5_K || T == VQ_Q2_K) {
         const _Float16 s = static_cast<_Float16>(isc);
         const g16h2 s2 = {s, s};
         const _Float16 nb = static_cast<_Float16>(-1024.0f) * s;  // exact: sc < 64
