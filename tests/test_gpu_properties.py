@@ -95,7 +95,7 @@ def test_grouped_gate_up_scaling_and_permutation(env, ntok):
 
 
 @pytest.mark.parametrize("ty,rows,cols", [(T.Q4_K, 17408, 5120), (T.Q6_K, 5120, 17408), (T.Q2_K, 17408, 5120),
-                                          (T.IQ3_S, 5120, 5120)],
+                                          (T.IQ2_XS, 5120, 17408), (T.IQ3_S, 5120, 5120)],
                          ids=lambda v: v.name if isinstance(v, T) else str(v))
 @pytest.mark.parametrize("flags", [0, 1], ids=["stream_k", "batch_invariant"])
 def test_prefill_scaling_and_permutation(env, ty, rows, cols, flags):

@@ -1,5 +1,5 @@
-// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q2_K, Q3_K and Q6_K: the K-quants with 16-element
-// sub-blocks whose blocks (84, 110 and 210 bytes) are only 2- or 4-byte aligned inside a row.
+// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q2_K, Q3_K, Q6_K and IQ2_XS: the types with
+// 16-element sub-blocks whose blocks (84, 110, 210 and 74 bytes) are only 2- or 4-byte aligned inside a row.
 //
 // Numerics: those of the Q4_K/Q5_K contraction (vq_gemm16_impl.h). Each weight element is the integer
 // a = code * sc: (q3) * (sc - 32), |a| <= 128, for Q3_K; q2 * sc, |a| <= 45, for Q2_K; Q6_K's (q - 32) * sc
@@ -38,13 +38,15 @@ namespace vq {
 template <int T>
 struct G16N {
     static constexpr bool Q6 = T == VQ_Q6_K, Q2 = T == VQ_Q2_K;
-    static constexpr int UB = Q6 ? 210 : Q2 ? 84 : 110;
-    static constexpr int NPC = Q6 ? 3 : Q2 ? 1 : 2;  // 16-byte pieces per row and step
+    static constexpr bool IQ = T == VQ_IQ2_XS;  // consecutive elements, grid codes (LDS tables), no mins
+    static constexpr int UB = Q6 ? 210 : Q2 ? 84 : IQ ? 74 : 110;
+    static constexpr int NPC = Q6 ? 3 : Q2 || IQ ? 1 : 2;  // 16-byte pieces per row and step
     static constexpr int CPR = 2 * NPC;              // chunks DMA'd per row and step
-    static constexpr int SOFF = Q6 ? 192 : Q2 ? 0 : 96;  // scales (and, but for Q2_K, d right after them)
-    static constexpr int SLEN = Q6 ? 18 : Q2 ? 16 : 14;  // bytes from SOFF
-    static constexpr int DOFF = Q6 ? 208 : Q2 ? 80 : 108;  // d (Q2_K: then dmin)
-    static constexpr int SBR = Q2 ? 64 : 32;         // super-block slot bytes per row: chunk pairs (scales, d)
+    static constexpr int SOFF = Q6 ? 192 : Q2 ? 0 : IQ ? 66 : 96;  // scales (Q3_K, Q6_K: d right after them)
+    static constexpr int SLEN = Q6 ? 18 : Q2 ? 16 : IQ ? 8 : 14;   // bytes from SOFF
+    static constexpr int DOFF = Q6 ? 208 : Q2 ? 80 : IQ ? 0 : 108;  // d (Q2_K: then dmin)
+    static constexpr int POFF0 = IQ ? 2 : 0;         // the code pieces' offset mod 16 in the block
+    static constexpr int SBR = Q2 || IQ ? 64 : 32;   // super-block slot bytes per row: chunk pairs (scales, d)
     static constexpr int CODE_BYTES = kG16BM * CPR * 16;
     static constexpr int STEP_BYTES = CODE_BYTES + 2 * kG16BN * 128;
     static constexpr int XS_BYTES = Q2 ? kG16BN * 64 : 0;  // the tokens' XS (16 hi, 16 lo f16 each)
@@ -58,14 +60,17 @@ struct G16N {
             return pc == 2 ? 128 + 32 * n + 16 * p : 64 * n + 32 * pc + 16 * p;
         else if constexpr (Q2)
             return 16 + 32 * n + 16 * p;
+        else if constexpr (IQ)
+            return 2 + 32 * n + 16 * p;  // qs entries 8 j .. 8 j + 7 of step j = 2 n + p
         else
             return pc == 0 ? 32 + 32 * n + 16 * p : 16 * p;
     }
     // Q3_K's two pieces of row R sit in the step slot in swapped order when bit 2 of R is set: with its 64-byte
     // row pitch, rows R and R + 4 would otherwise read the same banks.
-    __device__ static int pslot(int pc, int R) { return Q6 || Q2 ? pc : pc ^ ((R >> 2) & 1); }
-    // Super-block element of MFMA chunk q = 4 c + lk of step j.
+    __device__ static int pslot(int pc, int R) { return Q6 || Q2 || IQ ? pc : pc ^ ((R >> 2) & 1); }
+    // Super-block element of MFMA chunk q = 4 c + lk of step j (IQ2_XS: in order, 64 j + 8 q).
     __device__ static int bpos(int j, int q) {
+        if constexpr (IQ) return 64 * j + 8 * q;
         return 128 * (j >> 1) + 32 * (2 * (q >> 2) + ((q & 3) >> 1)) + 16 * (j & 1) + 8 * (q & 1);
     }
 };
@@ -87,6 +92,10 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
     using G = G16N<T>;
     __shared__ __attribute__((aligned(1024))) uint8_t s_step[2][G::STEP_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t s_sb[2][G::SB_BYTES];
+    // IQ2_XS: its grid and sign-selector tables in LDS (the first step's barrier orders them before any read).
+    __shared__ uint2 s8[TabSpec<T>::n8 > 0 ? TabSpec<T>::n8 : 1];
+    __shared__ uint2 sks[TabSpec<T>::ks ? 128 : 1];
+    const Tabs tb = stage_tabs<T>(s8, nullptr, sks, nullptr);
 
     const int b = blockIdx.x;
     const int v = (b & 7) * pl.per_xcd + (b >> 3);  // XCD-aware share order, as qgemm16_kernel
@@ -107,9 +116,9 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
     const int nsteps = (sb1 - sb0) * 4;
     const uint8_t *const wbase = w + static_cast<size_t>(r0) * row_bytes;  // 16-byte aligned (r0 % 256 == 0)
     // Misalignment of tile row R's block sb (the row clamped as the DMA clamps it).
-    auto mis = [&](int R, int sb) {
+    auto mis = [&](int R, int sb, int off = 0) {
         const int rc = min(r0 + R, rows - 1) - r0;
-        return static_cast<int>((static_cast<uint32_t>(rc * row_bytes) + static_cast<uint32_t>(sb * G::UB)) & 15u);
+        return static_cast<int>((static_cast<uint32_t>(rc * row_bytes) + static_cast<uint32_t>(sb * G::UB + off)) & 15u);
     };
 
     // DMA of step st into step slot st & 1 (and, on a super-block's first step, its scales into slot sb & 1).
@@ -173,12 +182,16 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         const uint8_t *const slot = s_step[st & 1];
         const uint8_t *const sbs = s_sb[sb & 1];
         const uint8_t *const sBh = slot + G::CODE_BYTES, *const sBl = sBh + kG16BN * 128;
-        if (p == 0) {  // the half's eight scales, on its first step
+        if (G::IQ ? j == 0 : p == 0) {  // the half's eight scales, on its first step (IQ2_XS: all eight at once)
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
-                const int R = wr + 16 * rb + lr, o = R * G::SBR + mis(R, sb);
+                const int R = wr + 16 * rb + lr, o = R * G::SBR + mis(R, sb, G::SOFF);
                 const uint32_t sh = static_cast<uint32_t>(o & 3);
-                if constexpr (G::Q2) {  // 4-bit scales in the low nibbles of bytes 8n .. 8n + 7
+                if constexpr (G::IQ) {  // scales[8]: byte g holds the two 16-element halves of group g
+                    const uint2 v = g16n_read8(sbs, o);
+                    scw[rb][0] = v.x;
+                    scw[rb][1] = v.y;
+                } else if constexpr (G::Q2) {  // 4-bit scales in the low nibbles of bytes 8n .. 8n + 7
                     const uint32_t *q = reinterpret_cast<const uint32_t *>(sbs + (o & ~3) + 8 * n);
                     const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
                     scw[rb][0] = __builtin_amdgcn_alignbyte(d1, d0, sh) & 0x0F0F0F0Fu;
@@ -206,9 +219,14 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const int R = wr + 16 * rb + lr;
-            const int base = R * G::CPR * 16 + mis(R, sb) + hf;
-            ra[rb] = g16n_read8(slot, base + 32 * G::pslot(G::Q6 ? kl : 0, R));
-            if constexpr (!G::Q2) rh[rb] = g16n_read8(slot, base + 32 * G::pslot(G::Q6 ? 2 : 1, R));
+            if constexpr (G::IQ) {  // entries lk (c = 0) and 4 + lk (c = 1) of the step's eight
+                const int pb = R * G::CPR * 16 + mis(R, sb, G::POFF0) + 2 * lk;
+                ra[rb] = uint2{g16n_read8(slot, pb).x & 0xFFFFu, g16n_read8(slot, pb + 8).x & 0xFFFFu};
+            } else {
+                const int base = R * G::CPR * 16 + mis(R, sb) + hf;
+                ra[rb] = g16n_read8(slot, base + 32 * G::pslot(G::Q6 ? kl : 0, R));
+                if constexpr (!G::Q2) rh[rb] = g16n_read8(slot, base + 32 * G::pslot(G::Q6 ? 2 : 1, R));
+            }
         }
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -219,7 +237,16 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                 const uint32_t sw = scw[rb][c];
                 uint32_t c0, c1;
                 int isc;
-                if constexpr (G::Q2) {
+                if constexpr (G::IQ) {
+                    // Entry e: grid index e & 511 (eight magnitudes), signs from the 7 stored bits e >> 9; the
+                    // half's scale 2 s + 1 (d / 8 applies at the super-block's end).
+                    const uint32_t e = c ? ra[rb].y : ra[rb].x;
+                    const uint2 g = tb.grid8[e & 511u], sel = tb.ks128[e >> 9];
+                    c0 = sign4_sel(g.x, sel.x);
+                    c1 = sign4_sel(g.y, sel.y);
+                    const int grp = 2 * j + c;
+                    isc = 2 * static_cast<int>((scw[rb][grp >> 2] >> (8 * (grp & 3) + 4 * kl)) & 15u) + 1;
+                } else if constexpr (G::Q2) {
                     c0 = (ra[rb].x >> (2 * k)) & 0x03030303u;
                     c1 = (ra[rb].y >> (2 * k)) & 0x03030303u;
                     isc = static_cast<int>((sw >> sbyte) & 0xFFu);
@@ -268,10 +295,10 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int R = wr + 16 * rb + 4 * lk + q;
-                    const int od = R * G::SBR + mis(R, sb) + (G::Q2 ? 32 : G::SLEN - 2);
+                    const int od = G::Q2 || G::IQ ? R * G::SBR + 32 + mis(R, sb, G::DOFF) : R * G::SBR + mis(R, sb) + G::SLEN - 2;
                     const uint32_t hd = *reinterpret_cast<const uint16_t *>(sbs + od) |
                                         (G::Q2 ? static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(sbs + od + 2)) << 16 : 0u);
-                    dq[q] = half_to_float(hd);
+                    dq[q] = half_to_float(hd) * (G::IQ ? 0.125f : 1.0f);
                     mq[q] = 32.0f * half_to_float(hd >> 16);
                 }
                 g16h4 amin = {};
