@@ -393,7 +393,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA, AMD-published (no sparsi
 
 def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 << 20):
     """Prefill contraction: M tokens x (rows x cols) weights through vq_qgemm_ws (f16
-    MFMA for Q2_K-Q6_K and IQ2_XS: exact code*scale weights, activations as two f16 -> two MFMAs per useful multiply-add,
+    MFMA for Q2_K-Q6_K, IQ2_XS and IQ2_XXS: exact code*scale weights, activations as two f16 -> two MFMAs per useful multiply-add,
     four for Q6_K's two-term weights; the int8-MFMA vq_qgemm for other types), activations packed beforehand. Reports us per launch (the
     activation split, the contraction and the reduction of split tiles), useful TFLOP/s (2*M*rows*cols) and
     its fraction of the path's dense MFMA peak; `mfma_issued_util` counts the hi/lo MFMAs actually issued."""
@@ -984,9 +984,9 @@ def main() -> None:
         for rows, cols in ((17408, 5120), (5120, 17408)):
             out[f"Q4_K_{rows}x{cols}_M512"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512)
         # The other types of a UD-Q3_K_XL prompt pass: FFN gate/up (Q3_K), attention/SSM projections (Q5_K, Q6_K);
-        # and the FFN gate/up of Q2_K- and IQ2_XS-based mixes.
+        # and the FFN gate/up of Q2_K-, IQ2_XS- and IQ2_XXS-based mixes.
         for ty, rows, cols in ((Q3_K, 17408, 5120), (Q6_K, 5120, 17408), (Q5_K, 10240, 5120), (Q6_K, 5120, 6144),
-                               (Q2_K, 17408, 5120), (IQ2_XS, 17408, 5120)):
+                               (Q2_K, 17408, 5120), (IQ2_XS, 17408, 5120), (IQ2_XXS, 17408, 5120)):
             out[f"{TYPE_NAMES[ty]}_{rows}x{cols}_M512"] = bench_gemm(torch, hip, ty, rows, cols, 512)
         print(json.dumps({"prefill": out}), flush=True)
         return

@@ -1,8 +1,9 @@
-// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q2_K, Q3_K, Q6_K and IQ2_XS: the types with
-// 16-element sub-blocks whose blocks (84, 110, 210 and 74 bytes) are only 2- or 4-byte aligned inside a row.
+// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q2_K, Q3_K, Q6_K, IQ2_XS and IQ2_XXS: blocks
+// (84, 110, 210, 74 and 66 bytes) only 2- or 4-byte aligned inside a row, most with 16-element sub-blocks.
 //
 // Numerics: those of the Q4_K/Q5_K contraction (vq_gemm16_impl.h). Each weight element is the integer
-// a = code * sc: (q3) * (sc - 32), |a| <= 128, for Q3_K; q2 * sc, |a| <= 45, for Q2_K; Q6_K's (q - 32) * sc
+// a = code * sc: (q3) * (sc - 32), |a| <= 128, for Q3_K; q2 * sc, |a| <= 45, for Q2_K; grid * sign * (2 s + 1),
+// |a| <= 43 * 31, for IQ2_XS and IQ2_XXS (d / 8 applied per super-block); Q6_K's (q - 32) * sc
 // (|.| <= 4096) as the two exact f16 terms 16 (q - 32) (sc >> 4) + (q - 32) (sc & 15). Each activation element is
 // b = xq * xd * 2^e as the f16 pair b_hi + b_lo, and each super-block's C = sum a * (b_hi + b_lo) (exact products,
 // fp32 sums) is applied once: acc += d * C, for Q2_K minus 32 dmin (m . XS) with the 16 sub-blocks' mins m and
@@ -38,15 +39,17 @@ namespace vq {
 template <int T>
 struct G16N {
     static constexpr bool Q6 = T == VQ_Q6_K, Q2 = T == VQ_Q2_K;
-    static constexpr bool IQ = T == VQ_IQ2_XS;  // consecutive elements, grid codes (LDS tables), no mins
-    static constexpr int UB = Q6 ? 210 : Q2 ? 84 : IQ ? 74 : 110;
+    static constexpr bool IQX = T == VQ_IQ2_XXS;     // scales inside the code pieces
+    static constexpr bool IQ = T == VQ_IQ2_XS || IQX;  // consecutive elements, grid codes (LDS tables), no mins
+    static constexpr int UB = Q6 ? 210 : Q2 ? 84 : IQX ? 66 : IQ ? 74 : 110;
     static constexpr int NPC = Q6 ? 3 : Q2 || IQ ? 1 : 2;  // 16-byte pieces per row and step
     static constexpr int CPR = 2 * NPC;              // chunks DMA'd per row and step
-    static constexpr int SOFF = Q6 ? 192 : Q2 ? 0 : IQ ? 66 : 96;  // scales (Q3_K, Q6_K: d right after them)
-    static constexpr int SLEN = Q6 ? 18 : Q2 ? 16 : IQ ? 8 : 14;   // bytes from SOFF
+    static constexpr int SOFF = Q6 ? 192 : Q2 || IQX ? 0 : IQ ? 66 : 96;  // scales (Q3_K, Q6_K: d right after
+                                                                          // them; IQ2_XXS: d alone)
+    static constexpr int SLEN = Q6 ? 18 : Q2 ? 16 : IQX ? 2 : IQ ? 8 : 14;   // bytes from SOFF
     static constexpr int DOFF = Q6 ? 208 : Q2 ? 80 : IQ ? 0 : 108;  // d (Q2_K: then dmin)
     static constexpr int POFF0 = IQ ? 2 : 0;         // the code pieces' offset mod 16 in the block
-    static constexpr int SBR = Q2 || IQ ? 64 : 32;   // super-block slot bytes per row: chunk pairs (scales, d)
+    static constexpr int SBR = Q2 || (IQ && !IQX) ? 64 : 32;  // super-block slot bytes per row: chunk pairs
     static constexpr int CODE_BYTES = kG16BM * CPR * 16;
     static constexpr int STEP_BYTES = CODE_BYTES + 2 * kG16BN * 128;
     static constexpr int XS_BYTES = Q2 ? kG16BN * 64 : 0;  // the tokens' XS (16 hi, 16 lo f16 each)
@@ -182,7 +185,8 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         const uint8_t *const slot = s_step[st & 1];
         const uint8_t *const sbs = s_sb[sb & 1];
         const uint8_t *const sBh = slot + G::CODE_BYTES, *const sBl = sBh + kG16BN * 128;
-        if (G::IQ ? j == 0 : p == 0) {  // the half's eight scales, on its first step (IQ2_XS: all eight at once)
+        if (G::IQX ? false : G::IQ ? j == 0 : p == 0) {  // the half's eight scales, on its first step (IQ2_XS: all
+                                                           // eight at once; IQ2_XXS: in the code pieces)
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
                 const int R = wr + 16 * rb + lr, o = R * G::SBR + mis(R, sb, G::SOFF);
@@ -219,7 +223,11 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const int R = wr + 16 * rb + lr;
-            if constexpr (G::IQ) {  // entries lk (c = 0) and 4 + lk (c = 1) of the step's eight
+            if constexpr (G::IQX) {  // the two groups' (aux0, aux1): grid bytes, then 4 x 7 sign bits and the scale
+                const int pb = R * G::CPR * 16 + mis(R, sb, G::POFF0);
+                ra[rb] = g16n_read8(slot, pb);
+                rh[rb] = g16n_read8(slot, pb + 8);
+            } else if constexpr (G::IQ) {  // entries lk (c = 0) and 4 + lk (c = 1) of the step's eight
                 const int pb = R * G::CPR * 16 + mis(R, sb, G::POFF0) + 2 * lk;
                 ra[rb] = uint2{g16n_read8(slot, pb).x & 0xFFFFu, g16n_read8(slot, pb + 8).x & 0xFFFFu};
             } else {
@@ -237,7 +245,14 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                 const uint32_t sw = scw[rb][c];
                 uint32_t c0, c1;
                 int isc;
-                if constexpr (G::IQ) {
+                if constexpr (G::IQX) {
+                    // Group 2 j + c: grid index = byte lk of aux0, signs = 7 bits lk of aux1, scale 2 (aux1 >> 28) + 1.
+                    const uint2 ax = c ? rh[rb] : ra[rb];
+                    const uint2 g = tb.grid8[(ax.x >> (8 * lk)) & 255u], sel = tb.ks128[(ax.y >> (7 * lk)) & 127u];
+                    c0 = sign4_sel(g.x, sel.x);
+                    c1 = sign4_sel(g.y, sel.y);
+                    isc = 2 * static_cast<int>(ax.y >> 28) + 1;
+                } else if constexpr (G::IQ) {
                     // Entry e: grid index e & 511 (eight magnitudes), signs from the 7 stored bits e >> 9; the
                     // half's scale 2 s + 1 (d / 8 applies at the super-block's end).
                     const uint32_t e = c ? ra[rb].y : ra[rb].x;
@@ -295,7 +310,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int R = wr + 16 * rb + 4 * lk + q;
-                    const int od = G::Q2 || G::IQ ? R * G::SBR + 32 + mis(R, sb, G::DOFF) : R * G::SBR + mis(R, sb) + G::SLEN - 2;
+                    const int od = G::SBR == 64 ? R * G::SBR + 32 + mis(R, sb, G::DOFF) : R * G::SBR + mis(R, sb, G::SOFF) + G::SLEN - 2;
                     const uint32_t hd = *reinterpret_cast<const uint16_t *>(sbs + od) |
                                         (G::Q2 ? static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(sbs + od + 2)) << 16 : 0u);
                     dq[q] = half_to_float(hd) * (G::IQ ? 0.125f : 1.0f);
