@@ -1,9 +1,10 @@
-// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q2_K, Q3_K, Q6_K, IQ2_XS and IQ2_XXS: blocks
-// (84, 110, 210, 74 and 66 bytes) only 2- or 4-byte aligned inside a row, most with 16-element sub-blocks.
+// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q2_K, Q3_K, Q6_K, IQ2_XS, IQ2_XXS and IQ2_S:
+// blocks (84, 110, 210, 74, 66 and 82 bytes) only 2- or 4-byte aligned inside a row, most with 16-element
+// sub-blocks.
 //
 // Numerics: those of the Q4_K/Q5_K contraction (vq_gemm16_impl.h). Each weight element is the integer
 // a = code * sc: (q3) * (sc - 32), |a| <= 128, for Q3_K; q2 * sc, |a| <= 45, for Q2_K; grid * sign * (2 s + 1),
-// |a| <= 43 * 31, for IQ2_XS and IQ2_XXS (d / 8 applied per super-block); Q6_K's (q - 32) * sc
+// |a| <= 43 * 31, for IQ2_XS, IQ2_XXS and IQ2_S (d / 8 applied per super-block); Q6_K's (q - 32) * sc
 // (|.| <= 4096) as the two exact f16 terms 16 (q - 32) (sc >> 4) + (q - 32) (sc & 15). Each activation element is
 // b = xq * xd * 2^e as the f16 pair b_hi + b_lo, and each super-block's C = sum a * (b_hi + b_lo) (exact products,
 // fp32 sums) is applied once: acc += d * C, for Q2_K minus 32 dmin (m . XS) with the 16 sub-blocks' mins m and
@@ -40,11 +41,12 @@ template <int T>
 struct G16N {
     static constexpr bool Q6 = T == VQ_Q6_K, Q2 = T == VQ_Q2_K;
     static constexpr bool IQX = T == VQ_IQ2_XXS;     // scales inside the code pieces
-    static constexpr bool IQ = T == VQ_IQ2_XS || IQX;  // consecutive elements, grid codes (LDS tables), no mins
-    static constexpr int UB = Q6 ? 210 : Q2 ? 84 : IQX ? 66 : IQ ? 74 : 110;
-    static constexpr int NPC = Q6 ? 3 : Q2 || IQ ? 1 : 2;  // 16-byte pieces per row and step
+    static constexpr bool IQS = T == VQ_IQ2_S;       // three pieces: grid index bytes, sign bytes, high index bits
+    static constexpr bool IQ = T == VQ_IQ2_XS || IQX || IQS;  // consecutive elements, grid codes (LDS), no mins
+    static constexpr int UB = Q6 ? 210 : Q2 ? 84 : IQX ? 66 : IQS ? 82 : IQ ? 74 : 110;
+    static constexpr int NPC = Q6 || IQS ? 3 : Q2 || IQ ? 1 : 2;  // 16-byte pieces per row and step
     static constexpr int CPR = 2 * NPC;              // chunks DMA'd per row and step
-    static constexpr int SOFF = Q6 ? 192 : Q2 || IQX ? 0 : IQ ? 66 : 96;  // scales (Q3_K, Q6_K: d right after
+    static constexpr int SOFF = Q6 ? 192 : Q2 || IQX ? 0 : IQS ? 74 : IQ ? 66 : 96;  // scales (Q3_K, Q6_K: d after
                                                                           // them; IQ2_XXS: d alone)
     static constexpr int SLEN = Q6 ? 18 : Q2 ? 16 : IQX ? 2 : IQ ? 8 : 14;   // bytes from SOFF
     static constexpr int DOFF = Q6 ? 208 : Q2 ? 80 : IQ ? 0 : 108;  // d (Q2_K: then dmin)
@@ -63,6 +65,8 @@ struct G16N {
             return pc == 2 ? 128 + 32 * n + 16 * p : 64 * n + 32 * pc + 16 * p;
         else if constexpr (Q2)
             return 16 + 32 * n + 16 * p;
+        else if constexpr (IQS)  // step j = 2 n + p: qs[8 j .. +8], signs[8 j .. +8], qh[2 j .. +2]
+            return pc == 0 ? 2 + 8 * (2 * n + p) : pc == 1 ? 34 + 8 * (2 * n + p) : 66 + 2 * (2 * n + p);
         else if constexpr (IQ)
             return 2 + 32 * n + 16 * p;  // qs entries 8 j .. 8 j + 7 of step j = 2 n + p
         else
@@ -219,11 +223,17 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         // step's 16-element run of k.
         const int hf = 8 * (lk & 1), kl = lk >> 1;
         const uint32_t sbyte = 8u * static_cast<uint32_t>(p + 2 * kl);  // the run's scale: byte p + 2 kl of dword 2n + c
-        uint2 ra[RB], rh[RB];  // [rb]: Q6_K ql (run kl) and qh; Q3_K qs and hmask
+        uint2 ra[RB], rh[RB];  // [rb]: Q6_K ql (run kl) and qh; Q3_K qs and hmask; IQ2_S index and sign bytes
+        uint32_t rq2[RB];      // [rb]: IQ2_S high index bits
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const int R = wr + 16 * rb + lr;
-            if constexpr (G::IQX) {  // the two groups' (aux0, aux1): grid bytes, then 4 x 7 sign bits and the scale
+            if constexpr (G::IQS) {  // the step's 8 index bytes, 8 sign bytes and 2 high-bit bytes
+                const int rb0 = R * G::CPR * 16;
+                ra[rb] = g16n_read8(slot, rb0 + mis(R, sb, G::poff(0, n, p)));
+                rh[rb] = g16n_read8(slot, rb0 + 32 + mis(R, sb, G::poff(1, n, p)));
+                rq2[rb] = g16n_read8(slot, rb0 + 64 + mis(R, sb, G::poff(2, n, p))).x;
+            } else if constexpr (G::IQX) {  // the two groups' (aux0, aux1): grid bytes, then 4 x 7 sign bits and the scale
                 const int pb = R * G::CPR * 16 + mis(R, sb, G::POFF0);
                 ra[rb] = g16n_read8(slot, pb);
                 rh[rb] = g16n_read8(slot, pb + 8);
@@ -245,7 +255,17 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                 const uint32_t sw = scw[rb][c];
                 uint32_t c0, c1;
                 int isc;
-                if constexpr (G::IQX) {
+                if constexpr (G::IQS) {
+                    // Entry lk of group 2 j + c: grid index = its qs byte | 2 bits of the group's qh byte << 8, its
+                    // 8 sign bits from the signs byte; the half's scale 2 s + 1.
+                    const uint32_t e = 4 * c + lk;
+                    const uint32_t idx = ((e < 4 ? ra[rb].x : ra[rb].y) >> (8 * (e & 3)) & 255u) |
+                                         (((rq2[rb] >> (8 * c + 2 * lk)) & 3u) << 8);
+                    const uint32_t s8 = (e < 4 ? rh[rb].x : rh[rb].y) >> (8 * (e & 3)) & 255u;
+                    sign8(tb.grid8[idx], s8, c0, c1);
+                    const int grp = 2 * j + c;
+                    isc = 2 * static_cast<int>((scw[rb][grp >> 2] >> (8 * (grp & 3) + 4 * kl)) & 15u) + 1;
+                } else if constexpr (G::IQX) {
                     // Group 2 j + c: grid index = byte lk of aux0, signs = 7 bits lk of aux1, scale 2 (aux1 >> 28) + 1.
                     const uint2 ax = c ? rh[rb] : ra[rb];
                     const uint2 g = tb.grid8[(ax.x >> (8 * lk)) & 255u], sel = tb.ks128[(ax.y >> (7 * lk)) & 127u];
