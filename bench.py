@@ -31,7 +31,7 @@ METRIC = "achieved HBM GB/s (% of MI355X peak) per quant type; ms per 27B decode
 
 # Per-layer matrices (name, type, rows, cols, input group); shapes from qwen_tensors.py:98-118 via the
 # survey's config 4. Full attention at layers 3, 7, ..., 63 (test_phase29_qwen_ops.py:207-209).
-Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, IQ4_XS, IQ3_S, IQ2_XXS, IQ2_XS, IQ2_S = 10, 11, 12, 13, 14, 8, 23, 21, 16, 17, 22
+Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, IQ4_XS, IQ3_S, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS = 10, 11, 12, 13, 14, 8, 23, 21, 16, 17, 22, 18
 SSM_LAYER = [
     ("ssm.qkv", Q5_K, 10240, 5120, "in"),
     ("ssm.gate", Q5_K, 6144, 5120, "in"),
@@ -65,7 +65,7 @@ def sweep_plan():
     return plan
 
 
-TYPE_NAMES = {Q2_K: "Q2_K", IQ2_XS: "IQ2_XS", IQ2_S: "IQ2_S", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_0: "Q8_0", IQ4_XS: "IQ4_XS",
+TYPE_NAMES = {Q2_K: "Q2_K", IQ2_XS: "IQ2_XS", IQ2_S: "IQ2_S", IQ3_XXS: "IQ3_XXS", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_0: "Q8_0", IQ4_XS: "IQ4_XS",
               IQ3_S: "IQ3_S", IQ2_XXS: "IQ2_XXS"}
 FUSED_QUANT_MAX_COLS = 24576  # narrower inputs are quantized inside the matvec (vq_qmv_group_f32)
 PER_TYPE = [Q4_K, Q3_K, IQ4_XS, IQ3_S, IQ2_XXS, Q6_K]
@@ -393,7 +393,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA, AMD-published (no sparsi
 
 def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 << 20):
     """Prefill contraction: M tokens x (rows x cols) weights through vq_qgemm_ws (f16
-    MFMA for Q2_K-Q6_K and IQ2_XXS/XS/S: exact code*scale weights, activations as two f16 -> two MFMAs per useful multiply-add,
+    MFMA for Q2_K-Q6_K, IQ2_XXS/XS/S and IQ3_XXS: exact code*scale weights, activations as two f16 -> two MFMAs per useful multiply-add,
     four for Q6_K's two-term weights; the int8-MFMA vq_qgemm for other types), activations packed beforehand. Reports us per launch (the
     activation split, the contraction and the reduction of split tiles), useful TFLOP/s (2*M*rows*cols) and
     its fraction of the path's dense MFMA peak; `mfma_issued_util` counts the hi/lo MFMAs actually issued."""
@@ -984,10 +984,10 @@ def main() -> None:
         for rows, cols in ((17408, 5120), (5120, 17408)):
             out[f"Q4_K_{rows}x{cols}_M512"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512)
         # The other types of a UD-Q3_K_XL prompt pass: FFN gate/up (Q3_K), attention/SSM projections (Q5_K, Q6_K);
-        # and the FFN gate/up of Q2_K- and IQ2-based mixes.
+        # and the FFN gate/up of Q2_K-, IQ2- and IQ3_XXS-based mixes.
         for ty, rows, cols in ((Q3_K, 17408, 5120), (Q6_K, 5120, 17408), (Q5_K, 10240, 5120), (Q6_K, 5120, 6144),
                                (Q2_K, 17408, 5120), (IQ2_XS, 17408, 5120), (IQ2_XXS, 17408, 5120),
-                               (IQ2_S, 17408, 5120)):
+                               (IQ2_S, 17408, 5120), (IQ3_XXS, 17408, 5120)):
             out[f"{TYPE_NAMES[ty]}_{rows}x{cols}_M512"] = bench_gemm(torch, hip, ty, rows, cols, 512)
         print(json.dumps({"prefill": out}), flush=True)
         return

@@ -331,13 +331,13 @@ int vq_qmv_group_mixed_f32(int n, const int *types, const uint8_t *const *w, con
  * x to fp16 instead of using the CPU path's int8 activations. */
 int vq_qgemm(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *stream);
 
-/* Workspace bytes of vq_qgemm_ws for this matrix and M tokens: non-zero for Q2_K..Q6_K and IQ2_XXS/XS/S (the
- * f16-MFMA path, M * cols < 2^30), 0 otherwise (vq_qgemm_ws then runs vq_qgemm and ignores the workspace). */
+/* Workspace bytes of vq_qgemm_ws for this matrix and M tokens: non-zero for Q2_K..Q6_K, IQ2_XXS/XS/S and IQ3_XXS
+ * (the f16-MFMA path, M * cols < 2^30), 0 otherwise (vq_qgemm_ws then runs vq_qgemm and ignores the workspace). */
 size_t vq_qgemm_workspace_bytes(int type, int rows, int cols, int M);
 
-/* vq_qgemm with a workspace: for Q2_K..Q6_K and IQ2_XXS/XS/S the contraction runs on f16 MFMA
- * (v_mfma_f32_16x16x32_f16) with each weight element as the exact f16 integer code * sub-block scale (IQ2: grid
- * magnitude * sign * (2s + 1); Q6_K: two exact f16 terms) and each
+/* vq_qgemm with a workspace: for Q2_K..Q6_K, IQ2_XXS/XS/S and IQ3_XXS the contraction runs on f16 MFMA
+ * (v_mfma_f32_16x16x32_f16) with each weight element as the exact f16 integer code * sub-block scale (IQ2 and
+ * IQ3_XXS: grid magnitude * sign * (2s + 1); Q6_K: two exact f16 terms) and each
  * activation element as xq * xd split into two f16 (22 significant bits); d and dmin apply once per super-block. Same bar against
  * the reference CPU path (rel-L2 <= 1e-5), deterministic (split-K partials add in a fixed order). Workspace
  * below vq_qgemm_workspace_bytes -> VQ_ERR_WORKSPACE. Replaces: as vq_qgemm (qwen_runtime.cu:1886-1902). */

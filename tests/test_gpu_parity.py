@@ -409,7 +409,7 @@ def _qgemm_ws(torch, lib, ty, w_dev, rows, cols, xp, M, y):
     return need
 
 
-@pytest.mark.parametrize("ty", [T.Q4_K, T.Q5_K, T.Q3_K, T.Q6_K, T.Q2_K, T.IQ2_XS, T.IQ2_XXS, T.IQ2_S],
+@pytest.mark.parametrize("ty", [T.Q4_K, T.Q5_K, T.Q3_K, T.Q6_K, T.Q2_K, T.IQ2_XS, T.IQ2_XXS, T.IQ2_S, T.IQ3_XXS],
                          ids=lambda t: t.name)
 @pytest.mark.parametrize("rows,cols,M", [(300, 2048, 50), (256, 256, 130), (520, 1024, 129), (17, 512, 1),
                                          (64, 2560, 300)])
@@ -439,7 +439,8 @@ def test_qgemm_f16_matches_oracle(env, oracle_mod, ty, rows, cols, M):
 
 @pytest.mark.parametrize("ty,rows,cols", [(T.Q4_K, 17408, 5120), (T.Q4_K, 5120, 17408), (T.Q5_K, 4096, 5120),
                                           (T.Q3_K, 17408, 5120), (T.Q6_K, 5120, 17408), (T.Q2_K, 17408, 5120),
-                                          (T.IQ2_XS, 5120, 17408), (T.IQ2_XXS, 17408, 5120), (T.IQ2_S, 5120, 17408)],
+                                          (T.IQ2_XS, 5120, 17408), (T.IQ2_XXS, 17408, 5120), (T.IQ2_S, 5120, 17408),
+                                          (T.IQ3_XXS, 17408, 5120)],
                          ids=lambda v: v.name if isinstance(v, T) else str(v))
 def test_qgemm_f16_prefill_shapes(env, oracle_mod, ty, rows, cols):
     """The benchmark's prefill shapes at 512 tokens (several K splits on the narrow one), all 512 tokens compared."""
@@ -458,7 +459,7 @@ def test_qgemm_f16_prefill_shapes(env, oracle_mod, ty, rows, cols):
         assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, t)
 
 
-@pytest.mark.parametrize("ty", [T.Q8_0, T.IQ3_XXS, T.IQ4_XS], ids=lambda t: t.name)
+@pytest.mark.parametrize("ty", [T.Q8_0, T.IQ3_S, T.IQ4_XS], ids=lambda t: t.name)
 def test_qgemm_ws_other_types_run_the_int8_path(env, oracle_mod, ty):
     torch, lib = env
     rows, cols, M = 70, 512, 20

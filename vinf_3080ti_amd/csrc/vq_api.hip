@@ -339,10 +339,10 @@ __global__ __launch_bounds__(256) void gemm_xsplit_kernel(const uint8_t *__restr
     if (tid == 0) inv[t] = 1.0f / sc;
 }
 
-// The f16 path: Q2_K..Q6_K and IQ2_XXS/XS/S, with the activation split addressable by the kernels' 32-bit DMA offsets.
+// The f16 path: Q2_K..Q6_K, IQ2_XXS/XS/S and IQ3_XXS, with the activation split addressable by the kernels' 32-bit DMA offsets.
 bool gemm16_ok(int type, int cols, int M) {
     return (type == VQ_Q2_K || type == VQ_Q3_K || type == VQ_Q4_K || type == VQ_Q5_K || type == VQ_Q6_K ||
-            type == VQ_IQ2_XS || type == VQ_IQ2_XXS || type == VQ_IQ2_S) &&
+            type == VQ_IQ2_XS || type == VQ_IQ2_XXS || type == VQ_IQ2_S || type == VQ_IQ3_XXS) &&
            static_cast<long>(M) * cols < (1L << 30);
 }
 

@@ -433,7 +433,7 @@ __global__ __launch_bounds__(512) void g16_reduce_kernel(const float *__restrict
     }
 }
 
-// Q2_K, Q3_K, Q6_K and IQ2_XXS/XS/S: qgemm16n_kernel (vq_gemm16n_impl.h), same plan, workspace and reduction.
+// Q2_K, Q3_K, Q6_K, IQ2_XXS/XS/S and IQ3_XXS: qgemm16n_kernel (vq_gemm16n_impl.h), same plan, workspace and reduction.
 template <int T>
 int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
                    hipStream_t s, bool invariant);
@@ -442,7 +442,7 @@ template <int T>
 int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
                   hipStream_t s, bool invariant) {
     if constexpr (T == VQ_Q2_K || T == VQ_Q3_K || T == VQ_Q6_K || T == VQ_IQ2_XS || T == VQ_IQ2_XXS ||
-                  T == VQ_IQ2_S) {
+                  T == VQ_IQ2_S || T == VQ_IQ3_XXS) {
         return launch_gemm16n<T>(w, rows, cols, rb, ws, M, y, cus, s, invariant);
     } else if constexpr (!kGemm16<T>) {
         (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)y, (void)cus, (void)s, (void)invariant;

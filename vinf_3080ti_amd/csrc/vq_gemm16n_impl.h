@@ -1,11 +1,11 @@
-// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q2_K, Q3_K, Q6_K, IQ2_XS, IQ2_XXS and IQ2_S:
-// blocks (84, 110, 210, 74, 66 and 82 bytes) only 2- or 4-byte aligned inside a row, most with 16-element
-// sub-blocks.
+// vq_gemm16n_impl.h -- prefill contraction on CDNA4 f16 MFMA for Q2_K, Q3_K, Q6_K, IQ2_XXS/XS/S and IQ3_XXS: blocks
+// (84, 110, 210, 66, 74, 82 and 98 bytes) only 2- or 4-byte aligned inside a row.
 //
 // Numerics: those of the Q4_K/Q5_K contraction (vq_gemm16_impl.h). Each weight element is the integer
 // a = code * sc: (q3) * (sc - 32), |a| <= 128, for Q3_K; q2 * sc, |a| <= 45, for Q2_K; grid * sign * (2 s + 1),
-// |a| <= 43 * 31, for IQ2_XS, IQ2_XXS and IQ2_S (d / 8 applied per super-block); Q6_K's (q - 32) * sc
-// (|.| <= 4096) as the two exact f16 terms 16 (q - 32) (sc >> 4) + (q - 32) (sc & 15). Each activation element is
+// |a| <= 43 * 31, for the IQ2 types (d / 8 applied per super-block) and <= 62 * 31 for IQ3_XXS (d / 4); Q6_K's
+// (q - 32) * sc (|.| <= 4096) as the two exact f16 terms 16 (q - 32) (sc >> 4) + (q - 32) (sc & 15). Each
+// activation element is
 // b = xq * xd * 2^e as the f16 pair b_hi + b_lo, and each super-block's C = sum a * (b_hi + b_lo) (exact products,
 // fp32 sums) is applied once: acc += d * C, for Q2_K minus 32 dmin (m . XS) with the 16 sub-blocks' mins m and
 // XS_h = X_h xd 2^e / 32 (X_h the code sum of 16-element half h; qwen_cpu.c:205-230) as one
@@ -42,16 +42,18 @@ struct G16N {
     static constexpr bool Q6 = T == VQ_Q6_K, Q2 = T == VQ_Q2_K;
     static constexpr bool IQX = T == VQ_IQ2_XXS;     // scales inside the code pieces
     static constexpr bool IQS = T == VQ_IQ2_S;       // three pieces: grid index bytes, sign bytes, high index bits
-    static constexpr bool IQ = T == VQ_IQ2_XS || IQX || IQS;  // consecutive elements, grid codes (LDS), no mins
-    static constexpr int UB = Q6 ? 210 : Q2 ? 84 : IQX ? 66 : IQS ? 82 : IQ ? 74 : 110;
-    static constexpr int NPC = Q6 || IQS ? 3 : Q2 || IQ ? 1 : 2;  // 16-byte pieces per row and step
+    static constexpr bool IQ3X = T == VQ_IQ3_XXS;    // two pieces: grid index bytes, (signs, scale) words
+    static constexpr bool IQ = T == VQ_IQ2_XS || IQX || IQS || IQ3X;  // consecutive elements, grid codes, no mins
+    static constexpr bool DONLY = IQX || IQ3X;       // scales in the code pieces: the super-block slot holds d only
+    static constexpr int UB = Q6 ? 210 : Q2 ? 84 : IQX ? 66 : IQS ? 82 : IQ3X ? 98 : IQ ? 74 : 110;
+    static constexpr int NPC = Q6 || IQS ? 3 : Q2 || IQX || T == VQ_IQ2_XS ? 1 : 2;  // 16-byte pieces per row and step
     static constexpr int CPR = 2 * NPC;              // chunks DMA'd per row and step
-    static constexpr int SOFF = Q6 ? 192 : Q2 || IQX ? 0 : IQS ? 74 : IQ ? 66 : 96;  // scales (Q3_K, Q6_K: d after
-                                                                          // them; IQ2_XXS: d alone)
-    static constexpr int SLEN = Q6 ? 18 : Q2 ? 16 : IQX ? 2 : IQ ? 8 : 14;   // bytes from SOFF
+    static constexpr int SOFF = Q6 ? 192 : Q2 || DONLY ? 0 : IQS ? 74 : IQ ? 66 : 96;  // scales (Q3_K, Q6_K: d
+                                                                                         // after them; DONLY: d)
+    static constexpr int SLEN = Q6 ? 18 : Q2 ? 16 : DONLY ? 2 : IQ ? 8 : 14;   // bytes from SOFF
     static constexpr int DOFF = Q6 ? 208 : Q2 ? 80 : IQ ? 0 : 108;  // d (Q2_K: then dmin)
     static constexpr int POFF0 = IQ ? 2 : 0;         // the code pieces' offset mod 16 in the block
-    static constexpr int SBR = Q2 || (IQ && !IQX) ? 64 : 32;  // super-block slot bytes per row: chunk pairs
+    static constexpr int SBR = Q2 || (IQ && !DONLY) ? 64 : 32;  // super-block slot bytes per row: chunk pairs
     static constexpr int CODE_BYTES = kG16BM * CPR * 16;
     static constexpr int STEP_BYTES = CODE_BYTES + 2 * kG16BN * 128;
     static constexpr int XS_BYTES = Q2 ? kG16BN * 64 : 0;  // the tokens' XS (16 hi, 16 lo f16 each)
@@ -65,6 +67,8 @@ struct G16N {
             return pc == 2 ? 128 + 32 * n + 16 * p : 64 * n + 32 * pc + 16 * p;
         else if constexpr (Q2)
             return 16 + 32 * n + 16 * p;
+        else if constexpr (IQ3X)  // step j = 2 n + p: qs[16 j .. +16], aux[2 j .. +2]
+            return pc == 0 ? 2 + 16 * (2 * n + p) : 66 + 8 * (2 * n + p);
         else if constexpr (IQS)  // step j = 2 n + p: qs[8 j .. +8], signs[8 j .. +8], qh[2 j .. +2]
             return pc == 0 ? 2 + 8 * (2 * n + p) : pc == 1 ? 34 + 8 * (2 * n + p) : 66 + 2 * (2 * n + p);
         else if constexpr (IQ)
@@ -101,8 +105,13 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
     __shared__ __attribute__((aligned(1024))) uint8_t s_sb[2][G::SB_BYTES];
     // IQ2_XS: its grid and sign-selector tables in LDS (the first step's barrier orders them before any read).
     __shared__ uint2 s8[TabSpec<T>::n8 > 0 ? TabSpec<T>::n8 : 1];
-    __shared__ uint2 sks[TabSpec<T>::ks ? 128 : 1];
-    const Tabs tb = stage_tabs<T>(s8, nullptr, sks, nullptr);
+    __shared__ uint32_t s4[TabSpec<T>::n4 > 0 ? TabSpec<T>::n4 : 1];
+    __shared__ uint2 sks[TabSpec<T>::ks || G::IQ3X ? 128 : 1];
+    Tabs tb = stage_tabs<T>(s8, s4, sks, nullptr);
+    if constexpr (G::IQ3X) {  // the sign selectors (the streaming kernel decodes IQ3_XXS signs in registers)
+        for (int i = threadIdx.x; i < 128; i += blockDim.x) sks[i] = sign_entry(ksigns(i));
+        tb.ks128 = sks;
+    }
 
     const int b = blockIdx.x;
     const int v = (b & 7) * pl.per_xcd + (b >> 3);  // XCD-aware share order, as qgemm16_kernel
@@ -189,7 +198,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         const uint8_t *const slot = s_step[st & 1];
         const uint8_t *const sbs = s_sb[sb & 1];
         const uint8_t *const sBh = slot + G::CODE_BYTES, *const sBl = sBh + kG16BN * 128;
-        if (G::IQX ? false : G::IQ ? j == 0 : p == 0) {  // the half's eight scales, on its first step (IQ2_XS: all
+        if (G::DONLY ? false : G::IQ ? j == 0 : p == 0) {  // the half's eight scales, on its first step (IQ2_XS: all
                                                            // eight at once; IQ2_XXS: in the code pieces)
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
@@ -228,7 +237,11 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const int R = wr + 16 * rb + lr;
-            if constexpr (G::IQS) {  // the step's 8 index bytes, 8 sign bytes and 2 high-bit bytes
+            if constexpr (G::IQ3X) {  // index bytes 2 lk, 2 lk + 1 of each group; the groups' aux words
+                const int rb0 = R * G::CPR * 16, pb = rb0 + mis(R, sb, G::poff(0, n, p)) + 2 * lk;
+                ra[rb] = uint2{g16n_read8(slot, pb).x & 0xFFFFu, g16n_read8(slot, pb + 8).x & 0xFFFFu};
+                rh[rb] = g16n_read8(slot, rb0 + 32 + mis(R, sb, G::poff(1, n, p)));
+            } else if constexpr (G::IQS) {  // the step's 8 index bytes, 8 sign bytes and 2 high-bit bytes
                 const int rb0 = R * G::CPR * 16;
                 ra[rb] = g16n_read8(slot, rb0 + mis(R, sb, G::poff(0, n, p)));
                 rh[rb] = g16n_read8(slot, rb0 + 32 + mis(R, sb, G::poff(1, n, p)));
@@ -255,7 +268,15 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                 const uint32_t sw = scw[rb][c];
                 uint32_t c0, c1;
                 int isc;
-                if constexpr (G::IQS) {
+                if constexpr (G::IQ3X) {
+                    // Lane lk of group 2 j + c: two 4-magnitude grid entries, 7 sign bits lk of the aux word (with
+                    // their parity bit), scale 2 (aux >> 28) + 1 (d / 4 applies at the super-block's end).
+                    const uint32_t e = c ? ra[rb].y : ra[rb].x, ax = c ? rh[rb].y : rh[rb].x;
+                    const uint2 sel = tb.ks128[(ax >> (7 * lk)) & 127u];
+                    c0 = sign4_sel(tb.grid4[e & 255u], sel.x);
+                    c1 = sign4_sel(tb.grid4[e >> 8], sel.y);
+                    isc = 2 * static_cast<int>(ax >> 28) + 1;
+                } else if constexpr (G::IQS) {
                     // Entry lk of group 2 j + c: grid index = its qs byte | 2 bits of the group's qh byte << 8, its
                     // 8 sign bits from the signs byte; the half's scale 2 s + 1.
                     const uint32_t e = 4 * c + lk;
@@ -333,7 +354,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                     const int od = G::SBR == 64 ? R * G::SBR + 32 + mis(R, sb, G::DOFF) : R * G::SBR + mis(R, sb, G::SOFF) + G::SLEN - 2;
                     const uint32_t hd = *reinterpret_cast<const uint16_t *>(sbs + od) |
                                         (G::Q2 ? static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(sbs + od + 2)) << 16 : 0u);
-                    dq[q] = half_to_float(hd) * (G::IQ ? 0.125f : 1.0f);
+                    dq[q] = half_to_float(hd) * (G::IQ3X ? 0.25f : G::IQ ? 0.125f : 1.0f);
                     mq[q] = 32.0f * half_to_float(hd >> 16);
                 }
                 g16h4 amin = {};

@@ -60,7 +60,7 @@ int launch_mixed2(int n, const int *types, const uint8_t *const *w, const int *r
 template <int T>
 int launch_gemm(const uint8_t *w, int rows, int cols, long row_bytes, const uint8_t *xpack, int M, float *y,
                 hipStream_t s);
-// Prefill contraction on f16 MFMA (Q2_K..Q6_K, IQ2_XXS/XS/S; other types return hipErrorInvalidValue): `ws` holds the split
+// Prefill contraction on f16 MFMA (Q2_K..Q6_K, IQ2_XXS/XS/S, IQ3_XXS; other types return hipErrorInvalidValue): `ws` holds the split
 // activations written by the library's pre-pass and the partial-tile slots (layout g16_layout for
 // g16_plan(rows, cols, M, cus, invariant)) and the reduction of split tiles; invariant: the K split depends on the
 // matrix only (batch-invariant results).

@@ -403,7 +403,8 @@ class Runtime:
     def _qmv_ptrs(self, t: _Tensor, x_ptr: int, y_ptr: int, ntok: int) -> None:
         if t.type not in (0, 1) and self.gemm_min_rows > 0 and ntok >= self.gemm_min_rows:
             # Prompt pass: the MFMA contraction (the prefill branch of Runtime_qmv, qwen_runtime.cu:1886-1902):
-            # packed activations, then the contraction's own workspace (f16 path of Q2_K-Q6_K and IQ2_XXS/XS/S; 0 bytes otherwise).
+            # packed activations, then the contraction's own workspace (f16 path of Q2_K-Q6_K, IQ2_XXS/XS/S and
+            # IQ3_XXS; 0 bytes otherwise).
             flags = _lib.VQ_GEMM_BATCH_INVARIANT if self.batch_invariant else 0
             nx = (self._lib.vq_xpack_bytes(t.cols, ntok) + 255) // 256 * 256
             ng = self._lib.vq_qgemm_workspace_bytes_ex(t.type, t.rows, t.cols, ntok, flags)
