@@ -394,7 +394,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA, AMD-published (no sparsi
 def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 << 20):
     """Prefill contraction: M tokens x (rows x cols) weights through vq_qgemm_ws (f16
     MFMA for Q2_K-Q6_K, IQ2_XXS/XS/S and IQ3_XXS: exact code*scale weights, activations as two f16 -> two MFMAs per useful multiply-add,
-    four for Q6_K's two-term weights; the int8-MFMA vq_qgemm for other types), activations packed beforehand. Reports us per launch (the
+    three for Q6_K (its weight as an f16 rounding plus a remainder); the int8-MFMA vq_qgemm for other types), activations packed beforehand. Reports us per launch (the
     activation split, the contraction and the reduction of split tiles), useful TFLOP/s (2*M*rows*cols) and
     its fraction of the path's dense MFMA peak; `mfma_issued_util` counts the hi/lo MFMAs actually issued."""
     from vinf_3080ti_amd import row_bytes
@@ -424,8 +424,8 @@ def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 <
     peak = MFMA_F16_PEAK_TFLOPS if f16 else MFMA_INT8_PEAK_TOPS
     out = {"us": round(ms * 1e3, 3), "path": "f16-mfma" if f16 else "int8-mfma", "tflops": round(tops, 2),
            "mfma_util": round(tops / peak, 4), "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
-    if f16:  # hi/lo activation MFMAs per useful product; Q6_K's weights are two exact terms as well
-        out["mfma_issued_util"] = round((4 if ty == Q6_K else 2) * tops / peak, 4)
+    if f16:  # hi/lo activation MFMAs per useful product; Q6_K adds its remainder's b_hi product
+        out["mfma_issued_util"] = round((3 if ty == Q6_K else 2) * tops / peak, 4)
     return out
 
 
