@@ -1,6 +1,7 @@
 // vq_gemm16_impl.h -- prefill contraction Y[t][r] = W[r] . x[t] on CDNA4 f16 MFMA (v_mfma_f32_16x16x32_f16) for
 // the K-quants with mins whose integer sub-block products are exact in f16 and whose blocks are 16-byte multiples
-// (Q4_K, Q5_K). Q2_K, Q3_K and Q6_K take qgemm16n_kernel (vq_gemm16n_impl.h) with the same plan and workspace.
+// (Q4_K, Q5_K). Q2_K, Q3_K, Q6_K, IQ2_XXS/XS/S and IQ3_XXS take qgemm16n_kernel (vq_gemm16n_impl.h) with the
+// same plan and workspace.
 //
 // Numerics. The reference CPU path (Cpu_qmv, qwen_cpu.c:581-641) computes per 32-group
 //   y += d * sc * xd * S - dmin * m * xd * X,   S = sum(code * xq) exact, X = sum(xq)
