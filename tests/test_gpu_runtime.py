@@ -180,7 +180,7 @@ def test_qmv_group_and_lmhead_argmax(rt, oracle_mod, cols):
         rt.free(n)
 
 
-@pytest.mark.parametrize("ty", [T.Q6_K, T.Q3_K, T.Q4_K], ids=lambda t: t.name)
+@pytest.mark.parametrize("ty", [T.Q6_K, T.Q3_K, T.Q4_K, T.Q2_K, T.IQ2_XS, T.IQ3_XXS], ids=lambda t: t.name)
 def test_gemm_min_rows_routes_prompts_to_the_mfma_contraction(rt, oracle_mod, ty):
     """Runtime.qmv with ntok >= gemm_min_rows: packed activations and the f16-MFMA prefill contraction (its
     workspace from the runtime), 201 rows (a ragged last row tile) x 70 tokens."""
