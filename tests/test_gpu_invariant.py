@@ -43,7 +43,8 @@ def _gemm(torch, lib, _lib, ty, wd, rows, cols, x, flags):
 
 
 @pytest.mark.parametrize("ty,rows,cols", [(T.Q4_K, 1024, 5120), (T.Q5_K, 300, 4096), (T.Q6_K, 1000, 2048),
-                                          (T.IQ4_XS, 640, 2048), (T.Q3_K, 512, 3072)],
+                                          (T.IQ4_XS, 640, 2048), (T.Q3_K, 512, 3072), (T.Q2_K, 700, 2048),
+                                          (T.IQ2_S, 300, 4096), (T.IQ3_XXS, 512, 2048)],
                          ids=lambda v: v.name if isinstance(v, T) else str(v))
 def test_qgemm_batch_invariant(env, oracle_mod, ty, rows, cols):
     """The same tokens alone, in a batch of 7 and at rows 131 .. of a 300-token batch (a third token tile):
