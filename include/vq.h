@@ -337,7 +337,8 @@ size_t vq_qgemm_workspace_bytes(int type, int rows, int cols, int M);
 
 /* vq_qgemm with a workspace: for Q2_K..Q6_K, IQ2_XXS/XS/S and IQ3_XXS the contraction runs on f16 MFMA
  * (v_mfma_f32_16x16x32_f16) with each weight element as the exact f16 integer code * sub-block scale (IQ2 and
- * IQ3_XXS: grid magnitude * sign * (2s + 1); Q6_K: two exact f16 terms) and each
+ * IQ3_XXS: grid magnitude * sign * (2s + 1); Q6_K: its f16 rounding plus the exact remainder, whose b_lo product,
+ * under ~1e-7 of it, is left out) and each
  * activation element as xq * xd split into two f16 (22 significant bits); d and dmin apply once per super-block. Same bar against
  * the reference CPU path (rel-L2 <= 1e-5), deterministic (split-K partials add in a fixed order). Workspace
  * below vq_qgemm_workspace_bytes -> VQ_ERR_WORKSPACE. Replaces: as vq_qgemm (qwen_runtime.cu:1886-1902). */

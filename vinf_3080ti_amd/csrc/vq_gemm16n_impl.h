@@ -4,7 +4,8 @@
 // Numerics: those of the Q4_K/Q5_K contraction (vq_gemm16_impl.h). Each weight element is the integer
 // a = code * sc: (q3) * (sc - 32), |a| <= 128, for Q3_K; q2 * sc, |a| <= 45, for Q2_K; grid * sign * (2 s + 1),
 // |a| <= 43 * 31, for the IQ2 types (d / 8 applied per super-block) and <= 62 * 31 for IQ3_XXS (d / 4); Q6_K's
-// (q - 32) * sc (|.| <= 4096) as the two exact f16 terms 16 (q - 32) (sc >> 4) + (q - 32) (sc & 15). Each
+// (q - 32) * sc (|.| <= 4096, past f16's exact integers) as its f16 rounding p and the exact remainder a - p in
+// {-1, 0, 1} (s16_frag), three MFMAs per product: p b_hi + p b_lo + r b_hi (r b_lo, under ~1e-7 of it, left out). Each
 // activation element is
 // b = xq * xd * 2^e as the f16 pair b_hi + b_lo, and each super-block's C = sum a * (b_hi + b_lo) (exact products,
 // fp32 sums) is applied once: acc += d * C, for Q2_K minus 32 dmin (m . XS) with the 16 sub-blocks' mins m and
@@ -85,30 +86,6 @@ struct G16N {
         return 128 * (j >> 1) + 32 * (2 * (q >> 2) + ((q & 3) >> 1)) + 16 * (j & 1) + 8 * (q & 1);
     }
 };
-
-#ifndef VQ_G16N_Q6R
-#define VQ_G16N_Q6R 1
-#endif
-// Q6_K's weight a = (q - 32) sc (|a| <= 4096) as its f16 rounding p = f16(a) (the product of the two exact f16
-// factors, one rounding) and the remainder r = a - p in {-1, 0, 1} (one fused multiply-add, exact): three MFMAs
-// per product, p b_hi + p b_lo + r b_hi, instead of the four of two exact terms. The r b_lo term left out is
-// below 2^-11 of r b, i.e. under ~1e-7 of the products it belongs to.
-__device__ __forceinline__ void q6_round_split(uint32_t c0, uint32_t c1, int isc, g16h8 &a1, g16h8 &a2) {
-    const g16h2 off = {static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
-    const _Float16 sc = static_cast<_Float16>(isc);
-    const g16h2 s2 = {sc, sc};
-    const g16h2 v[4] = {g16_pair(c0, 0x04010400u), g16_pair(c0, 0x04030402u), g16_pair(c1, 0x04010400u),
-                        g16_pair(c1, 0x04030402u)};  // 1024 + code
-    g16h2 w1[4], w2[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const g16h2 q = v[i] - off;                       // q - 32, exact
-        w1[i] = q * s2;                                   // f16(a)
-        w2[i] = __builtin_elementwise_fma(q, s2, -w1[i]);  // a - f16(a), exact
-    }
-    a1 = g16h8{w1[0][0], w1[0][1], w1[1][0], w1[1][1], w1[2][0], w1[2][1], w1[3][0], w1[3][1]};
-    a2 = g16h8{w2[0][0], w2[0][1], w2[1][0], w2[1][1], w2[2][0], w2[2][1], w2[3][0], w2[3][1]};
-}
 
 // Eight bytes at LDS byte offset `off` (even) of `base` (4-byte aligned): three dwords, realigned.
 __device__ __forceinline__ uint2 g16n_read8(const uint8_t *base, int off) {
@@ -340,10 +317,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                     c1 = ((ra[rb].y >> (2 * k)) & 0x03030303u) | (((rh[rb].y >> hs) & 0x01010101u) << 2);
                     isc = static_cast<int>((sw >> sbyte) & 0xFFu) - 32;
                 }
-                if constexpr (G::Q6 && VQ_G16N_Q6R)
-                    q6_round_split(c0, c1, isc, a1[rb], a2[rb]);
-                else
-                    s16_frag<T>(c0, c1, isc, a1[rb], a2[rb]);
+                s16_frag<T>(c0, c1, isc, a1[rb], a2[rb]);
             }
 #pragma unroll
             for (int h = 0; h < TB / 4; ++h) {  // token blocks four at a time (B fragments' registers)
@@ -364,7 +338,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                         cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], blf[i], cc, 0, 0, 0);
                         if constexpr (G::Q6) {
                             cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], bhf[i], cc, 0, 0, 0);
-                            if constexpr (!VQ_G16N_Q6R) cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], blf[i], cc, 0, 0, 0);
+                            if constexpr (!VQ_S16_RSPLIT) cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], blf[i], cc, 0, 0, 0);
                         }
                     }
             }

@@ -1,10 +1,11 @@
 // vq_small16_impl.h -- matvec for a few tokens (1..16: speculative verify, small batches) on f16 MFMA, for the K-quants
-// whose sub-block products fit f16 exactly (Q3_K, Q4_K, Q5_K; Q6_K as two exact terms) and the IQ types with signed
-// codes (IQ2_XXS/XS/S, IQ3_XXS; IQ3_S and IQ4_XS as two exact terms).
+// whose sub-block products fit f16 exactly (Q3_K, Q4_K, Q5_K; Q6_K as an f16 rounding plus remainder) and the IQ
+// types with signed codes (IQ2_XXS/XS/S, IQ3_XXS; IQ3_S and IQ4_XS as an f16 rounding plus remainder).
 //
 // Numerics: those of the prefill path (vq_gemm16_impl.h). Each weight element is the integer a = code * sc
-// (exact in f16: |a| <= 128 for Q3_K, 945 for Q4_K, 1953 for Q5_K; Q6_K's |(q - 32) * sc| <= 4096 is split into
-// 16 * ((q - 32) * (sc >> 4)) + (q - 32) * (sc & 15), both exact), each activation element b = xq * xd * 2^e
+// (exact in f16: |a| <= 128 for Q3_K, 945 for Q4_K, 1953 for Q5_K; Q6_K's |(q - 32) * sc| <= 4096 goes in as
+// its f16 rounding plus the exact remainder in {-1, 0, 1}, the remainder's b_lo product -- under ~1e-7 of the
+// product -- left out), each activation element b = xq * xd * 2^e
 // (the CPU path's int8 codes and group scale, one fp32 rounding, 2^e per token and K range) is two f16
 // (b_hi + b_lo), and each super-block's C = sum a * (b_hi + b_lo) comes from v_mfma_f32_16x16x32_f16 (exact
 // products, fp32 sums) before acc += d * C - 32 * dmin * (m . XS) once per super-block (qwen_cpu.c:581-641
@@ -41,6 +42,11 @@ constexpr bool kSmall16 = T == VQ_Q3_K || T == VQ_Q4_K || T == VQ_Q5_K || T == V
 // any magnitude up to 127, scale up to 31). The fixed IQ2 and IQ3_XXS grids stay below 64 (x 31 <= 1953).
 template <int T>
 constexpr bool kS16TwoTerm = T == VQ_Q6_K || T == VQ_IQ4_XS || T == VQ_IQ3_S;
+// Those types' weight as its f16 rounding plus the remainder a - f16(a) in {-1, 0, 1} (three MFMAs per product,
+// the remainder's b_lo product, under ~1e-7 of the product, left out), or as two exact terms (four MFMAs).
+#ifndef VQ_S16_RSPLIT
+#define VQ_S16_RSPLIT 1
+#endif
 
 constexpr int kS16Occ = 2;  // waves per SIMD the register budget is set for
 constexpr int kS16Waves = 8, kS16Rows = 16 * kS16Waves, kS16KR = 512, kS16NSB = kS16KR / 256;
@@ -100,14 +106,24 @@ __device__ __forceinline__ void s16_frag(uint32_t c0, uint32_t c1, int isc, g16h
 #pragma unroll
         for (int i = 0; i < 4; ++i) q[i] = q[i] - off;
         if constexpr (kS16TwoTerm<T>) {
+            g16h2 w1[4], w2[4];
+#if VQ_S16_RSPLIT
+            const _Float16 sc = static_cast<_Float16>(isc);
+            const g16h2 s2 = {sc, sc};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                w1[i] = q[i] * s2;                                   // f16(c * sc)
+                w2[i] = __builtin_elementwise_fma(q[i], s2, -w1[i]);  // c * sc - f16(c * sc) in {-1, 0, 1}: exact
+            }
+#else
             const _Float16 sh = static_cast<_Float16>(16 * (isc >> 4)), sl = static_cast<_Float16>(isc & 15);
             const g16h2 h2 = {sh, sh}, l2 = {sl, sl};
-            g16h2 w1[4], w2[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 w1[i] = q[i] * h2;  // multiple of 16, |.| <= 4096: exact
                 w2[i] = q[i] * l2;  // |.| <= 1920: exact
             }
+#endif
             a1 = g16h8{w1[0][0], w1[0][1], w1[1][0], w1[1][1], w1[2][0], w1[2][1], w1[3][0], w1[3][1]};
             a2 = g16h8{w2[0][0], w2[0][1], w2[1][0], w2[1][1], w2[2][0], w2[2][1], w2[3][0], w2[3][1]};
         } else {
@@ -117,17 +133,28 @@ __device__ __forceinline__ void s16_frag(uint32_t c0, uint32_t c1, int isc, g16h
             for (int i = 0; i < 4; ++i) q[i] = q[i] * s2;  // |.| <= 63 * 31: exact
             a1 = g16h8{q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
         }
-    } else {  // Q6_K: (q - 32) * sc = (q - 32) * 16 (sc >> 4) + (q - 32) * (sc & 15)
+    } else {  // Q6_K: (q - 32) * sc as f16(a) + (a - f16(a)), or as (q - 32) * 16 (sc >> 4) + (q - 32) * (sc & 15)
         const g16h2 off = {static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
+        g16h2 w1[4], w2[4];
+#if VQ_S16_RSPLIT
+        const _Float16 sc = static_cast<_Float16>(isc);
+        const g16h2 s2 = {sc, sc};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const g16h2 q = v[i] - off;                       // q - 32, exact
+            w1[i] = q * s2;                                   // f16(a)
+            w2[i] = __builtin_elementwise_fma(q, s2, -w1[i]);  // a - f16(a), exact
+        }
+#else
         const _Float16 sh = static_cast<_Float16>(16 * (isc >> 4)), sl = static_cast<_Float16>(isc & 15);
         const g16h2 h2 = {sh, sh}, l2 = {sl, sl};
-        g16h2 w1[4], w2[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const g16h2 q = v[i] - off;  // q - 32, exact
             w1[i] = q * h2;              // multiple of 16, |.| <= 4096: exact
             w2[i] = q * l2;              // |.| <= 480: exact
         }
+#endif
         a1 = g16h8{w1[0][0], w1[0][1], w1[1][0], w1[1][1], w1[2][0], w1[2][1], w1[3][0], w1[3][1]};
         a2 = g16h8{w2[0][0], w2[0][1], w2[1][0], w2[1][1], w2[2][0], w2[2][1], w2[3][0], w2[3][1]};
     }
@@ -363,7 +390,7 @@ __global__ __launch_bounds__(64 * kS16Waves, kS16Occ) void qmv16_kernel(const S1
                     C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bl, C, 0, 0, 0);
                     if constexpr (kS16TwoTerm<T>) {
                         C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bh, C, 0, 0, 0);
-                        C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bl, C, 0, 0, 0);
+                        if constexpr (!VQ_S16_RSPLIT) C = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bl, C, 0, 0, 0);
                     }
                 }
             }
