@@ -89,10 +89,13 @@ inline G16Plan g16_plan(int rows, int cols, int M, int cus, bool invariant = fal
         return p;
     }
     // Fewer tiles than CUs: an equal whole number of workgroups per tile (each tile splits at super-block
-    // boundaries into that many segments, no workgroup straddles two tiles); else one workgroup per CU.
+    // boundaries into that many segments, no workgroup straddles two tiles), unless that leaves more than a
+    // tenth of the CUs idle (160 tiles: one workgroup each, 62 % of 256 CUs); then, as for many tiles, one
+    // workgroup per CU with stream-K shares, as long as every CU still gets at least one super-block of work.
     if (p.tiles <= cus) {
         const int per = cus / p.tiles < p.nsb ? cus / p.tiles : p.nsb;
         p.W = p.tiles * per;
+        if (p.W * 10 < cus * 9 && p.U >= cus) p.W = cus;
     } else {
         p.W = cus;
     }
