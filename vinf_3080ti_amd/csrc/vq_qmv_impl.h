@@ -23,6 +23,19 @@ template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ float dpp_f(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
 }
+// x in the lanes whose bit of the wave-uniform mask m is set, 0 elsewhere: one v_cndmask on the SGPR pair. Inline
+// asm on purpose: written as a select, hipcc turns it into an exec-masked branch around the DPP move that produces
+// x, and a DPP move under a partial exec reads 0 from the disabled source lanes.
+// The same with bound_ctrl: lanes without a source read 0 (no zeroed old operand needed).
+template <int CTRL>
+__device__ __forceinline__ float dpp_fz(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float keep_lanes(float x, uint64_t m) {
+    float r;
+    asm("v_cndmask_b32_e64 %0, 0, %1, %2" : "=v"(r) : "v"(x), "s"(m));
+    return r;
+}
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f<0xB1>(v);        // quad_perm [1,0,3,2]
     v += dpp_f<0x4E>(v);        // quad_perm [2,3,0,1]
@@ -448,6 +461,9 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
     const int ul = lane / LPU;  // unit of this lane within a stage
     const int lj = lane % LPU;  // which of the unit's lanes
     const float inv_nu = 1.0f / static_cast<float>(nu);
+    // Lanes 0, LPU nu, 2 LPU nu, ...: shifted by a stage's first row start, the lanes that begin a row.
+    uint64_t row_pat = 0;
+    for (int p = 0; p < 64; p += LPU * nu) row_pat |= 1ull << p;
 
     // Decode stage s from the stage buffer; each row's part goes to its slot.
     auto run_stage = [&](int s) {
@@ -618,26 +634,36 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
         // Segmented inclusive scan over the lanes; segments are the stage's rows (q is non-decreasing in lane
         // order). The last lane of each segment holds that row's part of the stage. DPP moves, no LDS round trips:
         // row_shr 1, 2, 4, 8 scan each 16-lane row, then row_bcast:15 (rows 1, 3 take the last lane of rows 0, 2)
-        // and row_bcast:31 (rows 2, 3 take lane 31), each step adding only where the source lane has the same key
-        // (a lane without a source reads key -1). Keys are non-decreasing, so a matching source lane carries the
-        // segment's whole part before it.
+        // and row_bcast:31 (rows 2, 3 take lane 31). A lane adds its source only if no row starts after the
+        // source lane and at or before it. Row starts are the same for every lane (lane LPU (nu - col) and every
+        // LPU nu lanes after it), so each step's mask of lanes that add is built once in scalar registers:
+        // ~(starts smeared over the step's distance). Lanes past the stage's units add garbage among themselves
+        // only: sources always lie below a lane.
         const int key = valid ? q : 0x7FFFFFFF;
-        auto seg_step = [&](auto ctrl, auto rmask) {
-            constexpr int C = decltype(ctrl)::value, RM = decltype(rmask)::value;
-            const int kp = __builtin_amdgcn_update_dpp(-1, key, C, RM, 0xF, false);
-            const bool m = kp == key;
+        {
+            const int p1 = LPU * (nu - col);
+            const uint64_t b = p1 < 64 ? row_pat << p1 : 0ull;
+            const uint64_t s2 = b | (b << 1), s4 = s2 | (s2 << 2), s8 = s4 | (s4 << 4);
+            uint64_t w = b;  // a row starts in [16 (lane / 16), lane]
+            w |= (w << 1) & 0xFFFEFFFEFFFEFFFEull;
+            w |= (w << 2) & 0xFFFCFFFCFFFCFFFCull;
+            w |= (w << 4) & 0xFFF0FFF0FFF0FFF0ull;
+            w |= (w << 8) & 0xFF00FF00FF00FF00ull;
+            const uint32_t bh = static_cast<uint32_t>(b >> 32);  // a row starts in [32, lane]
+            const uint64_t vh = bh ? ~0ull << (32 + __builtin_ctz(bh)) : 0ull;
+            const uint64_t m1 = ~b, m2 = ~s2, m4 = ~s4, m8 = ~s8, m15 = ~w, m31 = ~vh;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const float vp = dpp_f<C, RM>(v[t]);
-                v[t] += m ? vp : 0.0f;
+                float x = v[t];
+                x += keep_lanes(dpp_fz<0x111>(x), m1);        // row_shr:1
+                x += keep_lanes(dpp_fz<0x112>(x), m2);        // row_shr:2
+                x += keep_lanes(dpp_fz<0x114>(x), m4);        // row_shr:4
+                x += keep_lanes(dpp_fz<0x118>(x), m8);        // row_shr:8
+                x += keep_lanes(dpp_f<0x142, 0xA>(x), m15);  // row_bcast:15
+                x += keep_lanes(dpp_f<0x143, 0xC>(x), m31);  // row_bcast:31
+                v[t] = x;
             }
-        };
-        seg_step(std::integral_constant<int, 0x111>{}, std::integral_constant<int, 0xF>{});  // row_shr:1
-        seg_step(std::integral_constant<int, 0x112>{}, std::integral_constant<int, 0xF>{});  // row_shr:2
-        seg_step(std::integral_constant<int, 0x114>{}, std::integral_constant<int, 0xF>{});  // row_shr:4
-        seg_step(std::integral_constant<int, 0x118>{}, std::integral_constant<int, 0xF>{});  // row_shr:8
-        seg_step(std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xA>{});  // row_bcast:15
-        seg_step(std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xC>{});  // row_bcast:31
+        }
         const int kn = __builtin_amdgcn_update_dpp(-2, key, 0x130, 0xF, 0xF, false);  // wave_shl:1, lane 63 reads -2
         if (valid && kn != key) {
 #pragma unroll
