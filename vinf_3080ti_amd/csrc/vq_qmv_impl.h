@@ -67,7 +67,7 @@ struct XImage {
     __host__ __device__ explicit XImage(int cols)
         : ng(cols / 32), nblk((cols / 32 + 7) / 8), xq_bytes(((cols / 32 + 7) / 8) * (256 + kXPad)),
           bytes(x_image_bytes(cols)) {}
-    __device__ int code_off(int G, int h) const { return (G >> 3) * (256 + kXPad) + (G & 7) * 32 + 16 * h; }
+    __device__ int code_off(int G, int h) const { return __mul24(G >> 3, 256 + kXPad) + (G & 7) * 32 + 16 * h; }
     // Byte of the packed record (vq_xpack_h_offset layout) that LDS image byte o (16-byte aligned) holds,
     // or -1 for padding.
     __device__ int src_of(int o, int cols) const {
@@ -460,7 +460,7 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
 
     const int ul = lane / LPU;  // unit of this lane within a stage
     const int lj = lane % LPU;  // which of the unit's lanes
-    const float inv_nu = 1.0f / static_cast<float>(nu);
+    const int ul_bytes = ul * UB;  // this lane's unit within a stage, in bytes past the stage's first unit
     // Lanes 0, LPU nu, 2 LPU nu, ...: shifted by a stage's first row start, the lanes that begin a row.
     uint64_t row_pat = 0;
     for (int p = 0; p < 64; p += LPU * nu) row_pat |= 1ull << p;
@@ -472,13 +472,17 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
         const int rf = ua / nu;                          // row of the stage's first unit
         const int col = ua - rf * nu;                    // its unit index within that row
         const bool valid = ul < nval;
-        const uint8_t *up = sbuf + ((static_cast<long>(ua) + (valid ? ul : 0)) * UB - ((static_cast<long>(ua) * UB >> 4) << 4));
-        // Row and column unit of this lane's unit: c = col + ul = q*nu + cu. c < nu + 64 and nu < 2^13, so
-        // (c + 1/2) / nu lies at least 1/(2nu) from an integer, far beyond the fp32 error of (c + 1/2) * inv_nu:
-        // the truncation is the exact quotient.
+        // The stage buffer starts at the 16-byte boundary at or below the stage's first unit.
+        const uint8_t *up = sbuf + ((static_cast<unsigned>(ua) * UB) & 15u) + (valid ? ul_bytes : 0);
+        // Lanes that start a row (after the stage's first): lane LPU (nu - col) and every LPU nu lanes after it.
+        const int p1 = LPU * (nu - col);
+        const uint64_t b = p1 < 64 ? row_pat << p1 : 0ull;
+        // Row and column unit of this lane's unit: c = col + ul = q*nu + cu, q = the row starts at or below this
+        // lane (lane 0 never starts one, so: the bits of b >> 1 below this lane).
         const int c = col + ul;
-        const int q = static_cast<int>((static_cast<float>(c) + 0.5f) * inv_nu);
-        const int cu = __mul24(-q, nu) + c;
+        const int q = static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(b >> 33),
+                                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b >> 1), 0)));
+        const int cu = c - __mul24(q, nu);
         const int G0 = cu * S::UG;
 
         float v[NT];
@@ -641,8 +645,6 @@ __device__ __forceinline__ void stream_wg(const QJobs &jobs, const int jb, const
         // only: sources always lie below a lane.
         const int key = valid ? q : 0x7FFFFFFF;
         {
-            const int p1 = LPU * (nu - col);
-            const uint64_t b = p1 < 64 ? row_pat << p1 : 0ull;
             const uint64_t s2 = b | (b << 1), s4 = s2 | (s2 << 2), s8 = s4 | (s4 << 4);
             uint64_t w = b;  // a row starts in [16 (lane / 16), lane]
             w |= (w << 1) & 0xFFFEFFFEFFFEFFFEull;
