@@ -391,12 +391,14 @@ MFMA_INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, AMD-published (no sparsi
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA, AMD-published (no sparsity)
 
 
-def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 << 20):
+def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 << 20, f16x=False):
     """Prefill contraction: M tokens x (rows x cols) weights through vq_qgemm_ws (f16
     MFMA for Q2_K-Q6_K, IQ2_XXS/XS/S and IQ3_XXS: exact code*scale weights, activations as two f16 -> two MFMAs per useful multiply-add,
     three for Q6_K (its weight as an f16 rounding plus a remainder); the int8-MFMA vq_qgemm for other types), activations packed beforehand. Reports us per launch (the
     activation split, the contraction and the reduction of split tiles), useful TFLOP/s (2*M*rows*cols) and
-    its fraction of the path's dense MFMA peak; `mfma_issued_util` counts the hi/lo MFMAs actually issued."""
+    its fraction of the path's dense MFMA peak; `mfma_issued_util` counts the hi/lo MFMAs actually issued.
+    f16x: vq_qgemm_f16x_ws instead (fp32 activations rounded to f16 in the timed pre-pass, the reference's
+    tensor-core numerics: one MFMA per product)."""
     from vinf_3080ti_amd import row_bytes
 
     nbytes = rows * row_bytes(ty, cols)
@@ -410,8 +412,12 @@ def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 <
     wk = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
 
     def launch(i):
-        st = hip.lib.vq_qgemm_ws(ty, ws[i % copies].data_ptr(), rows, cols, xp.data_ptr(), M, y.data_ptr(),
-                                 wk.data_ptr() if need else None, need, hip.s())
+        if f16x:
+            st = hip.lib.vq_qgemm_f16x_ws(ty, ws[i % copies].data_ptr(), rows, cols, x.data_ptr(), M, y.data_ptr(),
+                                          wk.data_ptr(), need, 0, hip.s())
+        else:
+            st = hip.lib.vq_qgemm_ws(ty, ws[i % copies].data_ptr(), rows, cols, xp.data_ptr(), M, y.data_ptr(),
+                                     wk.data_ptr() if need else None, need, hip.s())
         assert st == 0, st
 
     for i in range(copies):
@@ -424,7 +430,9 @@ def bench_gemm(torch, hip, ty, rows, cols, M, iters=20, min_rotation_bytes=640 <
     peak = MFMA_F16_PEAK_TFLOPS if f16 else MFMA_INT8_PEAK_TOPS
     out = {"us": round(ms * 1e3, 3), "path": "f16-mfma" if f16 else "int8-mfma", "tflops": round(tops, 2),
            "mfma_util": round(tops / peak, 4), "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
-    if f16:  # hi/lo activation MFMAs per useful product; Q6_K adds its remainder's b_hi product
+    if f16x:
+        out["path"] = "f16-mfma, f16 activations"
+    elif f16:  # hi/lo activation MFMAs per useful product; Q6_K adds its remainder's b_hi product
         out["mfma_issued_util"] = round((3 if ty == Q6_K else 2) * tops / peak, 4)
     return out
 
@@ -989,6 +997,9 @@ def main() -> None:
                                (Q2_K, 17408, 5120), (IQ2_XS, 17408, 5120), (IQ2_XXS, 17408, 5120),
                                (IQ2_S, 17408, 5120), (IQ3_XXS, 17408, 5120)):
             out[f"{TYPE_NAMES[ty]}_{rows}x{cols}_M512"] = bench_gemm(torch, hip, ty, rows, cols, 512)
+        # The reference's own numerics (activations rounded to f16): vq_qgemm_f16x_ws.
+        for ty, rows, cols in ((Q4_K, 17408, 5120), (Q4_K, 5120, 17408), (Q5_K, 10240, 5120)):
+            out[f"{TYPE_NAMES[ty]}_{rows}x{cols}_M512_f16x"] = bench_gemm(torch, hip, ty, rows, cols, 512, f16x=True)
         print(json.dumps({"prefill": out}), flush=True)
         return
     if args.mlp_only:

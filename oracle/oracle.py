@@ -6,6 +6,8 @@ Functions mirror the reference CPU path (/root/reference/engine/csrc/cpu/qwen_cp
   dequant_rows   dequant.py:121-500 / qwen_quant.cuh deq8 (:151-279)
   int_partials   exact int32 sum of code*xq per (token, row, group, 16-half)
   decode_codes   integer codes + per-16 scales/mins with dequant == scale*code - min
+  qgemm_f16x     prompt GEMM with fp16 activations (f32_to_f16_rows_kernel + vinf_qgemm_kernel,
+                 qwen_runtime.cu:657-739), exact weights, float64 numpy
   argmax_rows    argmax_kernel (qwen_runtime.cu:850-876), ties to the lowest index
   stage_x        the megakernel's QMV activation staging (qwen_megakernel.cu:485-551), float64 numpy
   rope_neox      NeoX partial RoPE (rope_neox_kernel, qwen_runtime.cu:81-92), float64 numpy
@@ -123,6 +125,27 @@ def qmv(type_id: int, raw, rows: int, cols: int, x: np.ndarray, ntok: int, threa
     if lib().vqo_qmv(type_id, _p(w), rows, cols, _p(x), ntok, _p(y), threads):
         raise ValueError("qmv: bad type/shape")
     return y
+
+
+def f16x_scales(x: np.ndarray) -> np.ndarray:
+    """Per token 2^min(15 - E, 126) with max|x| < 2^E (frexp), 1 for an all-zero token: the largest scaled |x| lies
+    in [2^14, 2^15), far inside fp16's range."""
+    m = np.abs(x).max(axis=1).astype(np.float64)
+    e = np.frexp(m)[1]
+    return np.where(m > 0, np.ldexp(1.0, np.minimum(15 - e, 126)), 1.0)
+
+
+def qgemm_f16x(type_id: int, raw, rows: int, cols: int, x: np.ndarray, ntok: int) -> np.ndarray:
+    """y[t] = W f16(x[t] s_t) / s_t in float64: W the exact dequantized weights (dequant_rows), f16 the IEEE
+    round-to-nearest-even conversion the reference applies to every activation before its fp16 MMA
+    (f32_to_f16_rows_kernel, qwen_runtime.cu:657-661; vinf_qgemm_kernel :663-739 accumulates the products in fp32),
+    s_t = f16x_scales. Scaling by a power of two commutes with the rounding wherever x s_t and x are both normal
+    fp16 numbers, so for such tokens this is W f16(x) exactly."""
+    w = dequant_rows(type_id, raw, rows, cols).astype(np.float64)
+    x = np.ascontiguousarray(x, np.float32).reshape(ntok, cols)
+    s = f16x_scales(x)
+    xb = (x * s[:, None].astype(np.float32)).astype(np.float16).astype(np.float64)
+    return (xb @ w.T) / s[:, None]
 
 
 def argmax_rows(x: np.ndarray, n: int, ntok: int) -> list[int]:

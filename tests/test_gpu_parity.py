@@ -858,3 +858,49 @@ def test_tiny_matrices_every_route(env, oracle_mod, ty, rows, cols):
     assert rel_l2(logits, ref) <= REL_L2_TOL, "lmhead"
     for t in range(2):
         assert idx[t] == int(np.argmax(logits[t]))
+
+
+@pytest.mark.parametrize("ty,rows,cols,M,flags", [
+    (T.Q4_K, 17408, 5120, 512, 0), (T.Q4_K, 5120, 17408, 512, 0), (T.Q5_K, 10240, 5120, 512, 0),
+    (T.Q4_K, 70, 512, 37, 0), (T.Q5_K, 300, 1024, 129, 1), (T.Q4_K, 1000, 5120, 1, 0), (T.Q5_K, 2048, 2048, 300, 1)],
+    ids=lambda v: v.name if isinstance(v, T) else str(v))
+def test_qgemm_f16x_matches_oracle(env, oracle_mod, ty, rows, cols, M, flags):
+    """vq_qgemm_f16x_ws against f16(x)-times-exact-weights in float64, every token; tokens 0 and 1 scaled to 1e-30
+    and 1e25 (their 2^e cap and a range plain fp16 cannot hold)."""
+    torch, lib = env
+    rng = np.random.default_rng(rows * 7 + cols + M)
+    w = synth.baseline_rows(ty, rows, cols, rng)
+    x = rng.standard_normal((M, cols)).astype(np.float32)
+    if M > 2:
+        x[0] *= np.float32(1e-30)
+        x[1] *= np.float32(1e25)
+    need = lib.vq_qgemm_workspace_bytes_ex(int(ty), rows, cols, M, flags)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    y = torch.full((M, rows), float("nan"), dtype=torch.float32, device="cuda")
+    xd = torch.from_numpy(x).cuda()
+    assert lib.vq_qgemm_f16x_ws(int(ty), P(wdev(torch, w)), rows, cols, P(xd), M, P(y), P(ws), need, flags, None) == 0
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    ref = oracle_mod.qgemm_f16x(int(ty), w, rows, cols, x, M)
+    for t in range(M):
+        assert rel_l2(got[t], ref[t]) <= REL_L2_TOL, (ty.name, t)
+
+
+def test_qgemm_f16x_errors(env):
+    from vinf_3080ti_amd._lib import VQ_ERR_ARG, VQ_ERR_TYPE, VQ_ERR_WORKSPACE
+
+    torch, lib = env
+    rows, cols, M = 64, 512, 8
+    w = torch.zeros(rows * cols, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(M, cols, dtype=torch.float32, device="cuda")
+    y = torch.empty(M, rows, dtype=torch.float32, device="cuda")
+    need = lib.vq_qgemm_workspace_bytes_ex(int(T.Q4_K), rows, cols, M, 0)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    args = (P(w), rows, cols, P(x), M, P(y))
+    assert lib.vq_qgemm_f16x_ws(int(T.Q6_K), *args, P(ws), need, 0, None) == VQ_ERR_TYPE
+    assert lib.vq_qgemm_f16x_ws(int(T.Q4_K), *args, P(ws), need - 256, 0, None) == VQ_ERR_WORKSPACE
+    assert lib.vq_qgemm_f16x_ws(int(T.Q4_K), *args, P(ws), need, 2, None) == VQ_ERR_ARG
+    assert lib.vq_qgemm_f16x_ws(int(T.Q4_K), *args, P(ws), need, 0, None) == 0
+    torch.cuda.synchronize()
+    assert not y.cpu().numpy().any()

@@ -389,3 +389,34 @@ def test_paged_rows_round_trip():
         for p, r in zip(range(length), rows):
             assert r // (kvh * page) == pt[p // page] and r % page == p % page and (r // page) % kvh == h
     assert np.array_equal(oracle.gather_paged(pool, pt, page, kvh, length), cont)
+
+
+def test_qgemm_f16x_is_pinned_by_brute_force_and_plain_f16(oracle_mod):
+    """The fp16-activation prompt GEMM restatement: (1) pure-Python brute force on a tiny case, rounding each
+    activation with struct's IEEE half packing (independent of numpy's float16); (2) for tokens whose values are
+    normal fp16 numbers, bit-identical to W f16(x) with no scaling, i.e. the reference's f32_to_f16_rows_kernel
+    (qwen_runtime.cu:657-661); (3) a token far outside fp16's range still gives 2^k times the in-range result."""
+    rng = np.random.default_rng(3)
+    rows, cols, ntok = 3, 256, 2
+    for ty in (T.Q4_K, T.Q5_K):
+        w = synth.baseline_rows(ty, rows, cols, rng)
+        x = rng.standard_normal((ntok, cols)).astype(np.float32)
+        got = oracle_mod.qgemm_f16x(int(ty), w, rows, cols, x, ntok)
+        wd = oracle_mod.dequant_rows(int(ty), w, rows, cols).astype(np.float64)
+        for t in range(ntok):
+            m = max(abs(float(v)) for v in x[t])
+            e = 0
+            while 2.0 ** e <= m:
+                e += 1
+            while 2.0 ** (e - 1) > m:
+                e -= 1
+            s = 2.0 ** min(15 - e, 126)
+            xb = [struct.unpack("<e", struct.pack("<e", float(v) * s))[0] for v in x[t]]
+            for r in range(rows):
+                want = sum(float(wd[r][k]) * xb[k] for k in range(cols)) / s
+                assert abs(got[t][r] - want) <= 1e-12 * max(1.0, abs(want)), (ty, t, r)
+        xn = np.where(np.abs(x) < 1e-3, np.float32(1e-3), x)  # every value a normal fp16 number
+        plain = (xn.astype(np.float16).astype(np.float64) @ wd.T)
+        assert np.array_equal(oracle_mod.qgemm_f16x(int(ty), w, rows, cols, xn, ntok), plain)
+        big = (xn * np.float32(2.0 ** 40)).astype(np.float32)  # far above fp16's 65504
+        assert np.array_equal(oracle_mod.qgemm_f16x(int(ty), w, rows, cols, big, ntok), plain * 2.0 ** 40)

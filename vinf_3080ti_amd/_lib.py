@@ -69,6 +69,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vq_qgemm_ws": (I, [I, P, I, I, P, I, P, P, SZ, P]),
     "vq_qgemm_workspace_bytes_ex": (SZ, [I, I, I, I, I]),
     "vq_qgemm_ws_ex": (I, [I, P, I, I, P, I, P, P, SZ, I, P]),
+    "vq_qgemm_f16x_ws": (I, [I, P, I, I, P, I, P, P, SZ, I, P]),
     "vq_lmhead_argmax_workspace_bytes": (SZ, [I, I, I, I]),
     "vq_lmhead_argmax": (I, [I, P, I, I, P, I, P, P, P, SZ, P]),
     "vq_dequant_rows": (I, [I, P, I, I, P, P]),

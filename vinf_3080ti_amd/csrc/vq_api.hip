@@ -822,6 +822,84 @@ int vq_qgemm_ws_ex(int type, const uint8_t *w, int rows, int cols, const void *x
     });
 }
 
+// Activations of the f16x contraction, one workgroup per token: b_hi = f16(x 2^e) rounded to nearest even, with
+// the token's 2^e putting its largest |x| just below 2^15 (capped at 2^126, as for the split above); b_lo is not
+// written. xs: per 32-group the fp32 sum of the rounded values (eight per thread in order, then the four threads
+// of the group pairwise: a fixed order) times 2^-5, as f16 hi then lo, 8 groups per super-block.
+__global__ __launch_bounds__(256) void gemm_f16x_split_kernel(const float *__restrict__ x, int cols,
+                                                              _Float16 *__restrict__ bh, _Float16 *__restrict__ xs,
+                                                              float *__restrict__ inv) {
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float4 *xr = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols);
+    __shared__ float red[4];
+    float m = 0.0f;
+    for (int i = tid; i < cols / 4; i += 256) {
+        const float4 v = xr[i];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int E = 0;
+    (void)frexpf(m, &E);  // m < 2^E
+    const float sc = m > 0.0f ? ldexpf(1.0f, min(15 - E, 126)) : 1.0f;
+    const size_t base = static_cast<size_t>(t) * cols;
+    const int nsb = cols >> 8;
+    // cols / 8 is a multiple of 32: the four threads of a group are active together.
+    for (int c = tid; c < cols / 8; c += 256) {
+        const float4 v0 = xr[2 * c], v1 = xr[2 * c + 1];
+        const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        _Float16 h[8];
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            h[i] = static_cast<_Float16>(f[i] * sc);
+            sum += static_cast<float>(h[i]);
+        }
+        *reinterpret_cast<uint4 *>(bh + base + 8 * c) = __builtin_bit_cast(uint4, h);
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if ((c & 3) == 0) {
+            const int g = c >> 2;
+            float v = sum * 0.03125f;
+            opaque(v);
+            const _Float16 hi = static_cast<_Float16>(v);
+            _Float16 *const dst = xs + (static_cast<size_t>(t) * nsb + (g >> 3)) * 16 + (g & 7);
+            dst[0] = hi;
+            dst[8] = static_cast<_Float16>(v - static_cast<float>(hi));
+        }
+    }
+    if (tid == 0) inv[t] = 1.0f / sc;
+}
+
+int vq_qgemm_f16x_ws(int type, const uint8_t *w, int rows, int cols, const float *x, int M, float *y, void *workspace,
+                     size_t workspace_bytes, int flags, void *stream) {
+    int st = check_matrix(type, rows, cols);
+    if (st) return st;
+    if (type != VQ_Q4_K && type != VQ_Q5_K) return VQ_ERR_TYPE;
+    if (flags & ~VQ_GEMM_BATCH_INVARIANT) return VQ_ERR_ARG;
+    if (!w || !x || !y || misaligned16(w) || misaligned16(x)) return VQ_ERR_ARG;
+    if (M < 1) return VQ_ERR_SHAPE;
+    const size_t need = vq_qgemm_workspace_bytes_ex(type, rows, cols, M, flags);
+    if (need == 0) return VQ_ERR_SHAPE;
+    if (!workspace || workspace_bytes < need || misaligned16(workspace)) return VQ_ERR_WORKSPACE;
+    const long rb = row_bytes_of(type, cols);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool invariant = (flags & VQ_GEMM_BATCH_INVARIANT) != 0;
+    const vq::G16Ws l = vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, device_cus(), invariant));
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    gemm_f16x_split_kernel<<<M, 256, 0, s>>>(x, cols, reinterpret_cast<_Float16 *>(ws + l.bh),
+                                             reinterpret_cast<_Float16 *>(ws + l.xs), reinterpret_cast<float *>(ws + l.inv));
+    st = hip_status(hipGetLastError());
+    if (st) return st;
+    const int cus = device_cus();
+    return dispatch_quant(type, [&](auto tc) {
+        return vq::launch_gemm16<decltype(tc)::value>(w, rows, cols, rb, ws, M, y, cus, s, invariant, true);
+    });
+}
+
 int vq_qgemm_ws(int type, const uint8_t *w, int rows, int cols, const void *xpack, int M, float *y, void *workspace,
                 size_t workspace_bytes, void *stream) {
     return vq_qgemm_ws_ex(type, w, rows, cols, xpack, M, y, workspace, workspace_bytes, 0, stream);

@@ -143,28 +143,31 @@ __device__ __forceinline__ g16h8 g16_frag(uint32_t c0, uint32_t c1, _Float16 sc)
     return g16h8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
-template <int T>
+// LO: activations as b_hi + b_lo (the int8 path's values, exact); without it b_hi alone (activations rounded to
+// f16 under the token's 2^e, the reference's tensor-core numerics): half the activation DMA, LDS and MFMAs.
+template <int T, bool LO = true>
 struct G16Geo {
     static constexpr int UB = Sl<T>::UB;
     static constexpr int HB = T == VQ_Q5_K ? 48 : 16;          // leading block bytes kept per super-block
     static constexpr int QOFF = T == VQ_Q5_K ? 48 : 16;        // offset of qs in the block
     static constexpr int SB_CHUNKS = kG16BM * HB / 16 + kG16BN * 2;  // 16-byte chunks of a super-block slot
     static constexpr int SB_DMA = SB_CHUNKS / (64 * kG16Waves);      // per wave, first step of a super-block
-    static constexpr int NDMA = 1 + 4;                               // per wave, every step
+    static constexpr int NB = LO ? 4 : 2;                            // activation DMAs per wave and step
+    static constexpr int NDMA = 1 + NB;                              // per wave, every step
     static constexpr int NDMA_SB = NDMA + SB_DMA;                    // per wave, first step of a super-block
-    static constexpr int STEP_BYTES = kG16BM * 32 + 2 * kG16BN * 128;  // codes + b_hi + b_lo
+    static constexpr int STEP_BYTES = kG16BM * 32 + (LO ? 2 : 1) * kG16BN * 128;  // codes + b_hi (+ b_lo)
     static constexpr int SB_BYTES = SB_CHUNKS * 16;
     static_assert(SB_CHUNKS % (64 * kG16Waves) == 0, "super-block slot split");
 };
 
-template <int T>
+template <int T, bool LO>
 __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *__restrict__ w, int rows, int cols,
                                                                   long row_bytes, const _Float16 *__restrict__ bh,
                                                                   const _Float16 *__restrict__ bl,
                                                                   const _Float16 *__restrict__ xs,
                                                                   const float *__restrict__ inv, int M, G16Plan pl,
                                                                   float *__restrict__ y, float *__restrict__ part) {
-    using G = G16Geo<T>;
+    using G = G16Geo<T, LO>;
     __shared__ __attribute__((aligned(1024))) uint8_t s_step[kG16Ring][G::STEP_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t s_sb[2][G::SB_BYTES];
 
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
 
     // Lane offsets of the DMAs, fixed for the segment (the step moves only the wave-uniform base, so a copy costs
     // no VALU): the wave's code row piece, its four activation chunks, and its super-block slot chunks.
-    uint32_t vo_code, vo_b[4], vo_sb[G::SB_DMA];
+    uint32_t vo_code, vo_b[G::NB], vo_sb[G::SB_DMA];
     {
         const int row = min(r0 + 32 * wv + (lane >> 1), rows - 1) - r0;
         // The row's two 16-byte halves in swapped order when bit 3 of its tile row is set (rows R and R + 8
@@ -201,8 +204,8 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
         const int rr = 32 * wv + (lane >> 1);
         vo_code = static_cast<uint32_t>(row * row_bytes + G::QOFF + 16 * ((lane & 1) ^ ((rr >> 3) & 1)));
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int ii = (4 * wv + k) & 15;
+        for (int k = 0; k < G::NB; ++k) {
+            const int ii = (G::NB * wv + k) & 15;
             const int trow = 8 * ii + (lane >> 3);
             const int tok = min(t0 + trow, M - 1);
             const int c = (lane & 7) ^ ((trow >> 1) & 7);
@@ -233,8 +236,8 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
         dma16s(wbase + static_cast<long>(sb) * G::UB + 32 * j, vo_code, slot + 1024 * wv);
         const long kb = (256L * sb + 64 * j) * 2;  // the step's byte offset in a token row of b_hi / b_lo
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = 4 * wv + k, ii = i & 15;
+        for (int k = 0; k < G::NB; ++k) {
+            const int i = G::NB * wv + k, ii = i & 15;
             dma16s(reinterpret_cast<const uint8_t *>(i < 16 ? bh : bl) + kb, vo_b[k],
                    slot + kG16BM * 32 + (i < 16 ? 0 : kG16BN * 128) + 1024 * ii);
         }
@@ -317,7 +320,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
                     const int r = wt + 16 * (4 * h + i) + lr;
                     const int o = r * 128 + (((4 * c + lk) ^ ((r >> 1) & 7)) << 4);
                     bhf[i] = *reinterpret_cast<const g16h8 *>(sBh + o);
-                    blf[i] = *reinterpret_cast<const g16h8 *>(sBl + o);
+                    if constexpr (LO) blf[i] = *reinterpret_cast<const g16h8 *>(sBl + o);
                 }
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb)
@@ -325,7 +328,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
                     for (int i = 0; i < 4; ++i) {
                         g16f4 &cc = C[rb][4 * h + i];
                         cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][rb], bhf[i], cc, 0, 0, 0);
-                        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][rb], blf[i], cc, 0, 0, 0);
+                        if constexpr (LO) cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][rb], blf[i], cc, 0, 0, 0);
                     }
             }
         }
@@ -442,21 +445,25 @@ template <int T>
 int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
                    hipStream_t s, bool invariant);
 
+// f16x: b_hi alone holds the activations (rounded to f16); only qgemm16_kernel's types take it.
 template <int T>
 int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
-                  hipStream_t s, bool invariant) {
+                  hipStream_t s, bool invariant, bool f16x) {
     if constexpr (T == VQ_Q2_K || T == VQ_Q3_K || T == VQ_Q6_K || T == VQ_IQ2_XS || T == VQ_IQ2_XXS ||
                   T == VQ_IQ2_S || T == VQ_IQ3_XXS) {
+        if (f16x) return static_cast<int>(hipErrorInvalidValue);
         return launch_gemm16n<T>(w, rows, cols, rb, ws, M, y, cus, s, invariant);
     } else if constexpr (!kGemm16<T>) {
-        (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)y, (void)cus, (void)s, (void)invariant;
+        (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)y, (void)cus, (void)s, (void)invariant,
+            (void)f16x;
         return static_cast<int>(hipErrorInvalidValue);
     } else {
         const G16Plan pl = g16_plan(rows, cols, M, cus, invariant);
         const G16Ws l = g16_layout(cols, M, pl);
         uint8_t *base = static_cast<uint8_t *>(const_cast<void *>(ws));
         float *const part = reinterpret_cast<float *>(base + l.part);
-        qgemm16_kernel<T><<<dim3(8 * pl.per_xcd), dim3(64 * kG16Waves), 0, s>>>(
+        auto *const kern = f16x ? qgemm16_kernel<T, false> : qgemm16_kernel<T, true>;
+        kern<<<dim3(8 * pl.per_xcd), dim3(64 * kG16Waves), 0, s>>>(
             w, rows, cols, rb, reinterpret_cast<const _Float16 *>(base + l.bh),
             reinterpret_cast<const _Float16 *>(base + l.bl), reinterpret_cast<const _Float16 *>(base + l.xs),
             reinterpret_cast<const float *>(base + l.inv), M, pl, y, part);

@@ -63,10 +63,10 @@ int launch_gemm(const uint8_t *w, int rows, int cols, long row_bytes, const uint
 // Prefill contraction on f16 MFMA (Q2_K..Q6_K, IQ2_XXS/XS/S, IQ3_XXS; other types return hipErrorInvalidValue): `ws` holds the split
 // activations written by the library's pre-pass and the partial-tile slots (layout g16_layout for
 // g16_plan(rows, cols, M, cus, invariant)) and the reduction of split tiles; invariant: the K split depends on the
-// matrix only (batch-invariant results).
+// matrix only (batch-invariant results); f16x: the activations are b_hi alone, rounded to f16 (Q4_K and Q5_K).
 template <int T>
 int launch_gemm16(const uint8_t *w, int rows, int cols, long row_bytes, const void *ws, int M, float *y, int cus,
-                  hipStream_t s, bool invariant);
+                  hipStream_t s, bool invariant, bool f16x = false);
 // Matvec of 1..16 tokens on f16 MFMA (Q3_K, Q4_K, Q5_K, Q6_K; other types return hipErrorInvalidValue), fp32
 // activations; `part` holds s16_part_bytes(rows, cols, ntok) bytes (unused when that is 0).
 template <int T>
@@ -106,7 +106,7 @@ int set_iq3s_grid(const uint8_t *grid);
     KW int vq::launch_mixed_q8<T>(int, const int *, const uint8_t *const *, const int *, float *const *, int, \
                                         const float *, int, hipStream_t);                                          \
     KW int vq::launch_gemm<T>(const uint8_t *, int, int, long, const uint8_t *, int, float *, hipStream_t);    \
-    KW int vq::launch_gemm16<T>(const uint8_t *, int, int, long, const void *, int, float *, int, hipStream_t, bool); \
+    KW int vq::launch_gemm16<T>(const uint8_t *, int, int, long, const void *, int, float *, int, hipStream_t, bool, bool); \
     KW int vq::launch_small16_group<T>(int, const uint8_t *const *, const int *, float *const *, int, long,    \
                                              const float *, int, float *, hipStream_t, const vq::XStage &, float *); \
     KW int vq::launch_small16<T>(const uint8_t *, int, int, long, const float *, int, float *, float *,          \
