@@ -998,7 +998,9 @@ def main() -> None:
                                (IQ2_S, 17408, 5120), (IQ3_XXS, 17408, 5120)):
             out[f"{TYPE_NAMES[ty]}_{rows}x{cols}_M512"] = bench_gemm(torch, hip, ty, rows, cols, 512)
         # The reference's own numerics (activations rounded to f16): vq_qgemm_f16x_ws.
-        for ty, rows, cols in ((Q4_K, 17408, 5120), (Q4_K, 5120, 17408), (Q5_K, 10240, 5120)):
+        for ty, rows, cols in ((Q4_K, 17408, 5120), (Q4_K, 5120, 17408), (Q3_K, 17408, 5120), (Q6_K, 5120, 17408),
+                               (Q5_K, 10240, 5120), (Q6_K, 5120, 6144), (Q2_K, 17408, 5120), (IQ2_XS, 17408, 5120),
+                               (IQ2_XXS, 17408, 5120), (IQ2_S, 17408, 5120), (IQ3_XXS, 17408, 5120)):
             out[f"{TYPE_NAMES[ty]}_{rows}x{cols}_M512_f16x"] = bench_gemm(torch, hip, ty, rows, cols, 512, f16x=True)
         print(json.dumps({"prefill": out}), flush=True)
         return

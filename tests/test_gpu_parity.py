@@ -862,7 +862,10 @@ def test_tiny_matrices_every_route(env, oracle_mod, ty, rows, cols):
 
 @pytest.mark.parametrize("ty,rows,cols,M,flags", [
     (T.Q4_K, 17408, 5120, 512, 0), (T.Q4_K, 5120, 17408, 512, 0), (T.Q5_K, 10240, 5120, 512, 0),
-    (T.Q4_K, 70, 512, 37, 0), (T.Q5_K, 300, 1024, 129, 1), (T.Q4_K, 1000, 5120, 1, 0), (T.Q5_K, 2048, 2048, 300, 1)],
+    (T.Q4_K, 70, 512, 37, 0), (T.Q5_K, 300, 1024, 129, 1), (T.Q4_K, 1000, 5120, 1, 0), (T.Q5_K, 2048, 2048, 300, 1),
+    (T.Q6_K, 5120, 17408, 512, 0), (T.Q3_K, 17408, 5120, 512, 0), (T.Q6_K, 300, 1024, 129, 1), (T.Q3_K, 70, 512, 37, 0),
+    (T.Q2_K, 1000, 5120, 200, 0), (T.Q2_K, 300, 1024, 129, 1), (T.IQ2_XS, 1000, 5120, 200, 0),
+    (T.IQ2_XXS, 1000, 5120, 200, 1), (T.IQ2_S, 1000, 5120, 200, 0), (T.IQ3_XXS, 1000, 5120, 200, 0)],
     ids=lambda v: v.name if isinstance(v, T) else str(v))
 def test_qgemm_f16x_matches_oracle(env, oracle_mod, ty, rows, cols, M, flags):
     """vq_qgemm_f16x_ws against f16(x)-times-exact-weights in float64, every token; tokens 0 and 1 scaled to 1e-30
@@ -898,7 +901,8 @@ def test_qgemm_f16x_errors(env):
     need = lib.vq_qgemm_workspace_bytes_ex(int(T.Q4_K), rows, cols, M, 0)
     ws = torch.empty(need, dtype=torch.uint8, device="cuda")
     args = (P(w), rows, cols, P(x), M, P(y))
-    assert lib.vq_qgemm_f16x_ws(int(T.Q6_K), *args, P(ws), need, 0, None) == VQ_ERR_TYPE
+    assert lib.vq_qgemm_f16x_ws(int(T.Q8_0), *args, P(ws), need, 0, None) == VQ_ERR_TYPE
+    assert lib.vq_qgemm_f16x_ws(int(T.IQ3_S), *args, P(ws), need, 0, None) == VQ_ERR_TYPE
     assert lib.vq_qgemm_f16x_ws(int(T.Q4_K), *args, P(ws), need - 256, 0, None) == VQ_ERR_WORKSPACE
     assert lib.vq_qgemm_f16x_ws(int(T.Q4_K), *args, P(ws), need, 2, None) == VQ_ERR_ARG
     assert lib.vq_qgemm_f16x_ws(int(T.Q4_K), *args, P(ws), need, 0, None) == 0

@@ -825,10 +825,11 @@ int vq_qgemm_ws_ex(int type, const uint8_t *w, int rows, int cols, const void *x
 // Activations of the f16x contraction, one workgroup per token: b_hi = f16(x 2^e) rounded to nearest even, with
 // the token's 2^e putting its largest |x| just below 2^15 (capped at 2^126, as for the split above); b_lo is not
 // written. xs: per 32-group the fp32 sum of the rounded values (eight per thread in order, then the four threads
-// of the group pairwise: a fixed order) times 2^-5, as f16 hi then lo, 8 groups per super-block.
+// of the group pairwise: a fixed order) times 2^-5, as f16 hi then lo, 8 groups per super-block; halves (Q2_K):
+// per 16-element half (two threads), 16 hi then 16 lo per super-block.
 __global__ __launch_bounds__(256) void gemm_f16x_split_kernel(const float *__restrict__ x, int cols,
                                                               _Float16 *__restrict__ bh, _Float16 *__restrict__ xs,
-                                                              float *__restrict__ inv) {
+                                                              float *__restrict__ inv, int halves) {
     const int t = blockIdx.x, tid = threadIdx.x;
     const float4 *xr = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols);
     __shared__ float red[4];
@@ -860,6 +861,17 @@ __global__ __launch_bounds__(256) void gemm_f16x_split_kernel(const float *__res
         }
         *reinterpret_cast<uint4 *>(bh + base + 8 * c) = __builtin_bit_cast(uint4, h);
         sum += __shfl_xor(sum, 1, 64);
+        if (halves) {
+            if ((c & 1) == 0) {
+                float v = sum * 0.03125f;
+                opaque(v);
+                const _Float16 hi = static_cast<_Float16>(v);
+                _Float16 *const dst = xs + (static_cast<size_t>(t) * nsb + (c >> 5)) * 32 + ((c >> 1) & 15);
+                dst[0] = hi;
+                dst[16] = static_cast<_Float16>(v - static_cast<float>(hi));
+            }
+            continue;
+        }
         sum += __shfl_xor(sum, 2, 64);
         if ((c & 3) == 0) {
             const int g = c >> 2;
@@ -878,7 +890,7 @@ int vq_qgemm_f16x_ws(int type, const uint8_t *w, int rows, int cols, const float
                      size_t workspace_bytes, int flags, void *stream) {
     int st = check_matrix(type, rows, cols);
     if (st) return st;
-    if (type != VQ_Q4_K && type != VQ_Q5_K) return VQ_ERR_TYPE;
+    if (type == VQ_F32 || type == VQ_F16 || !gemm16_ok(type, cols, 1)) return VQ_ERR_TYPE;
     if (flags & ~VQ_GEMM_BATCH_INVARIANT) return VQ_ERR_ARG;
     if (!w || !x || !y || misaligned16(w) || misaligned16(x)) return VQ_ERR_ARG;
     if (M < 1) return VQ_ERR_SHAPE;
@@ -888,10 +900,12 @@ int vq_qgemm_f16x_ws(int type, const uint8_t *w, int rows, int cols, const float
     const long rb = row_bytes_of(type, cols);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool invariant = (flags & VQ_GEMM_BATCH_INVARIANT) != 0;
-    const vq::G16Ws l = vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, device_cus(), invariant));
+    const bool halves = type == VQ_Q2_K;
+    const vq::G16Ws l = vq::g16_layout(cols, M, vq::g16_plan(rows, cols, M, device_cus(), invariant), halves);
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     gemm_f16x_split_kernel<<<M, 256, 0, s>>>(x, cols, reinterpret_cast<_Float16 *>(ws + l.bh),
-                                             reinterpret_cast<_Float16 *>(ws + l.xs), reinterpret_cast<float *>(ws + l.inv));
+                                             reinterpret_cast<_Float16 *>(ws + l.xs), reinterpret_cast<float *>(ws + l.inv),
+                                             halves ? 1 : 0);
     st = hip_status(hipGetLastError());
     if (st) return st;
     const int cus = device_cus();

@@ -443,16 +443,15 @@ __global__ __launch_bounds__(512) void g16_reduce_kernel(const float *__restrict
 // Q2_K, Q3_K, Q6_K, IQ2_XXS/XS/S and IQ3_XXS: qgemm16n_kernel (vq_gemm16n_impl.h), same plan, workspace and reduction.
 template <int T>
 int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
-                   hipStream_t s, bool invariant);
+                   hipStream_t s, bool invariant, bool f16x);
 
-// f16x: b_hi alone holds the activations (rounded to f16); only qgemm16_kernel's types take it.
+// f16x: b_hi alone holds the activations (rounded to f16).
 template <int T>
 int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
                   hipStream_t s, bool invariant, bool f16x) {
     if constexpr (T == VQ_Q2_K || T == VQ_Q3_K || T == VQ_Q6_K || T == VQ_IQ2_XS || T == VQ_IQ2_XXS ||
                   T == VQ_IQ2_S || T == VQ_IQ3_XXS) {
-        if (f16x) return static_cast<int>(hipErrorInvalidValue);
-        return launch_gemm16n<T>(w, rows, cols, rb, ws, M, y, cus, s, invariant);
+        return launch_gemm16n<T>(w, rows, cols, rb, ws, M, y, cus, s, invariant, f16x);
     } else if constexpr (!kGemm16<T>) {
         (void)w, (void)rows, (void)cols, (void)rb, (void)ws, (void)M, (void)y, (void)cus, (void)s, (void)invariant,
             (void)f16x;

@@ -38,7 +38,8 @@
 
 namespace vq {
 
-template <int T>
+// LO as for qgemm16_kernel: activations as b_hi + b_lo, or b_hi alone (rounded to f16).
+template <int T, bool LO = true>
 struct G16N {
     static constexpr bool Q6 = T == VQ_Q6_K, Q2 = T == VQ_Q2_K;
     static constexpr bool IQX = T == VQ_IQ2_XXS;     // scales inside the code pieces
@@ -56,7 +57,8 @@ struct G16N {
     static constexpr int POFF0 = IQ ? 2 : 0;         // the code pieces' offset mod 16 in the block
     static constexpr int SBR = Q2 || (IQ && !DONLY) ? 64 : 32;  // super-block slot bytes per row: chunk pairs
     static constexpr int CODE_BYTES = kG16BM * CPR * 16;
-    static constexpr int STEP_BYTES = CODE_BYTES + 2 * kG16BN * 128;
+    static constexpr int NB = LO ? 4 : 2;  // activation DMAs per wave and step
+    static constexpr int STEP_BYTES = CODE_BYTES + (LO ? 2 : 1) * kG16BN * 128;
     static constexpr int XS_BYTES = Q2 ? kG16BN * 64 : 0;  // the tokens' XS (16 hi, 16 lo f16 each)
     static constexpr int SB_BYTES = kG16BM * SBR + XS_BYTES;
     static constexpr int SB_DMA = SB_BYTES / (1024 * kG16Waves);  // per wave, first step of a super-block
@@ -94,14 +96,14 @@ __device__ __forceinline__ uint2 g16n_read8(const uint8_t *base, int off) {
     return uint2{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh)};
 }
 
-template <int T>
+template <int T, bool LO>
 __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t *__restrict__ w, int rows, int cols,
                                                                    long row_bytes, const _Float16 *__restrict__ bh,
                                                                    const _Float16 *__restrict__ bl,
                                                                    const _Float16 *__restrict__ xs,
                                                                    const float *__restrict__ inv, int M, G16Plan pl,
                                                                    float *__restrict__ y, float *__restrict__ part) {
-    using G = G16N<T>;
+    using G = G16N<T, LO>;
     __shared__ __attribute__((aligned(1024))) uint8_t s_step[2][G::STEP_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t s_sb[2][G::SB_BYTES];
     // IQ2_XS: its grid and sign-selector tables in LDS (the first step's barrier orders them before any read).
@@ -152,8 +154,8 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
             dma16(wbase, off, slot + 1024 * (G::CODE_DMA * wv + k));
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = 4 * wv + k, ii = i & 15;
+        for (int k = 0; k < G::NB; ++k) {
+            const int i = G::NB * wv + k, ii = i & 15;
             const int row = 8 * ii + (lane >> 3);
             const int tok = min(t0 + row, M - 1);
             const int c = (lane & 7) ^ ((row >> 1) & 7);
@@ -327,7 +329,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                     const int r = wt + 16 * (4 * h + i) + lr;
                     const int o = r * 128 + (((4 * c + lk) ^ ((r >> 1) & 7)) << 4);
                     bhf[i] = *reinterpret_cast<const g16h8 *>(sBh + o);
-                    blf[i] = *reinterpret_cast<const g16h8 *>(sBl + o);
+                    if constexpr (LO) blf[i] = *reinterpret_cast<const g16h8 *>(sBl + o);
                 }
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb)
@@ -335,10 +337,11 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                     for (int i = 0; i < 4; ++i) {
                         g16f4 &cc = C[rb][4 * h + i];
                         cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], bhf[i], cc, 0, 0, 0);
-                        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], blf[i], cc, 0, 0, 0);
+                        if constexpr (LO) cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], blf[i], cc, 0, 0, 0);
                         if constexpr (G::Q6) {
                             cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], bhf[i], cc, 0, 0, 0);
-                            if constexpr (!VQ_S16_RSPLIT) cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], blf[i], cc, 0, 0, 0);
+                            if constexpr (LO && !VQ_S16_RSPLIT)
+                                cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], blf[i], cc, 0, 0, 0);
                         }
                     }
             }
@@ -428,12 +431,13 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
 
 template <int T>
 int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws, int M, float *y, int cus,
-                   hipStream_t s, bool invariant) {
+                   hipStream_t s, bool invariant, bool f16x) {
     const G16Plan pl = g16_plan(rows, cols, M, cus, invariant);
     const G16Ws l = g16_layout(cols, M, pl, T == VQ_Q2_K);
     uint8_t *base = static_cast<uint8_t *>(const_cast<void *>(ws));
     float *const part = reinterpret_cast<float *>(base + l.part);
-    qgemm16n_kernel<T><<<dim3(8 * pl.per_xcd), dim3(64 * kG16Waves), 0, s>>>(
+    auto *const kern = f16x ? qgemm16n_kernel<T, false> : qgemm16n_kernel<T, true>;
+    kern<<<dim3(8 * pl.per_xcd), dim3(64 * kG16Waves), 0, s>>>(
         w, rows, cols, rb, reinterpret_cast<const _Float16 *>(base + l.bh), reinterpret_cast<const _Float16 *>(base + l.bl),
         reinterpret_cast<const _Float16 *>(base + l.xs), reinterpret_cast<const float *>(base + l.inv), M, pl, y, part);
     hipError_t e = hipGetLastError();
