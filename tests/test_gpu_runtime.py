@@ -203,6 +203,35 @@ def test_gemm_min_rows_routes_prompts_to_the_mfma_contraction(rt, oracle_mod, ty
     rt.free("pf")
 
 
+@pytest.mark.parametrize("ty", [T.Q4_K, T.Q6_K, T.IQ2_XXS, T.Q8_0], ids=lambda t: t.name)
+def test_gemm_f16_activations_route(rt, oracle_mod, ty):
+    """set_gemm_f16_activations: prompt passes of the f16 path's types through vq_qgemm_f16x_ws (against f16(x)
+    times the exact weights); Q8_0 keeps the int8 contraction (against the CPU path)."""
+    rows, cols, ntok = 201, 2048, 70
+    raw = synth.baseline_rows(ty, rows, cols, 14)
+    x = np.random.default_rng(14).standard_normal((ntok, cols)).astype(np.float32)
+    rt.upload_raw("pf16", raw.tobytes(), ty, cols, rows)
+    rt.alloc("pf16x", cols * ntok)
+    rt.alloc("pf16y", rows * ntok)
+    rt.write_floats("pf16x", x.reshape(-1).tolist())
+    rt.set_gemm_min_rows(64)
+    rt.set_gemm_f16_activations(True)
+    try:
+        rt.qmv("pf16", "pf16x", "pf16y", ntok)
+    finally:
+        rt.set_gemm_min_rows(0)
+        rt.set_gemm_f16_activations(False)
+    got = np.array(rt.read_floats("pf16y"), np.float32).reshape(ntok, rows)
+    if ty == T.Q8_0:
+        ref = oracle_mod.qmv(int(ty), raw, rows, cols, x, ntok)
+    else:
+        ref = oracle_mod.qgemm_f16x(int(ty), raw, rows, cols, x, ntok)
+        # and it is the f16 rounding, not the int8 codes: far from the CPU path at this tolerance
+        assert rel_l2(got, oracle_mod.qmv(int(ty), raw, rows, cols, x, ntok)) > 1e-5
+    assert rel_l2(got, ref) <= 1e-5
+    rt.free("pf16")
+
+
 def test_upload_gguf_tensor_from_a_file(rt, oracle_mod, tmp_path):
     """upload_gguf_tensor (cuda/qwen_runtime.py:68-86): raw blocks straight from the file's mapping, cols =
     innermost dimension, rows = product of the others, the byte size returned; types without a matvec
