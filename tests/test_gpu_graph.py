@@ -2,7 +2,7 @@
 
 One graph holds every kind of launch sequence the benchmark captures: grouped and mixed streaming matvecs, the
 small-batch f16 and int8 paths with their K-range sums, the no-allocation matvec, the prefill contraction (split,
-GEMM, reduction of split tiles), the fused LM-head argmax and the split decode attention with its merge. It is
+GEMM, reduction of split tiles; also with f16 activations), the fused LM-head argmax and the split decode attention with its merge. It is
 replayed three times; before each replay its outputs are overwritten with NaN and the same calls run eagerly on
 other buffers, and every replay must reproduce the eager outputs bit for bit (the kernels are deterministic).
 """
@@ -73,13 +73,14 @@ def test_graph_replays_match_eager_calls(env):
     assert lib.vq_qmv_path(int(T.Q6_K), 700, cols, 8, ws6.numel()) == 2
     assert lib.vq_qmv_path(int(T.Q8_0), 300, cols, 8, ws8.numel()) == 1
     wsg = ws(lib.vq_qgemm_workspace_bytes(int(T.Q4_K), 300, cols, M))
+    wsf = ws(lib.vq_qgemm_workspace_bytes(int(T.Q4_K), 300, cols, M))
     wsh = ws(lib.vq_lmhead_argmax_workspace_bytes(int(T.Q6_K), 4099, 1024, 2))
     wsa = ws(lib.vq_attention_workspace_bytes(heads, kvh, hd, seq, 1, 0))
 
     def outputs():
         f = lambda *s: torch.empty(*s, dtype=torch.float32, device="cuda")
         return {"group": [f(1, 300), f(1, 300)], "mixed": [f(1, r) for r in mix_r], "small16": f(8, 700),
-                "int8": f(8, 300), "noalloc": f(8, 300), "gemm": f(M, 300), "logits": f(2, 4099),
+                "int8": f(8, 300), "noalloc": f(8, 300), "gemm": f(M, 300), "gemm_f16x": f(M, 300), "logits": f(2, 4099),
                 "idx": torch.empty(2, dtype=torch.int32, device="cuda"), "attn": f(1, heads, hd)}
 
     def run(o, stream):
@@ -95,6 +96,8 @@ def test_graph_replays_match_eager_calls(env):
         assert lib.vq_qmv(int(T.Q8_0), P(w8), 300, cols, P(x8), 8, P(o["int8"]), P(ws8), ws8.numel(), s) == 0
         assert lib.vq_qmv_noalloc(int(T.Q4_K), P(w4), 300, cols, P(x8), 8, P(o["noalloc"]), s) == 0
         assert lib.vq_qgemm_ws(int(T.Q4_K), P(w4), 300, cols, P(xp), M, P(o["gemm"]), P(wsg), wsg.numel(), s) == 0
+        assert lib.vq_qgemm_f16x_ws(int(T.Q4_K), P(w4), 300, cols, P(xm), M, P(o["gemm_f16x"]), P(wsf), wsf.numel(), 0,
+                                    s) == 0
         assert lib.vq_lmhead_argmax(int(T.Q6_K), P(head), 4099, 1024, P(xh), 2, P(o["idx"]), P(o["logits"]),
                                     P(wsh), wsh.numel(), s) == 0
         assert lib.vq_attention_ws(P(q), P(kc), P(vc), P(o["attn"]), 2, heads, kvh, hd, seq + 4, seq, 1, 0, 0,

@@ -119,6 +119,26 @@ def test_prefill_scaling_and_permutation(env, ty, rows, cols, flags):
     _check(torch, run, torch.randn(M, cols, device="cuda"), permute=flags == 1)
 
 
+@pytest.mark.parametrize("ty,rows,cols", [(T.Q4_K, 17408, 5120), (T.Q6_K, 5120, 17408), (T.Q2_K, 17408, 5120)],
+                         ids=lambda v: v.name if isinstance(v, T) else str(v))
+@pytest.mark.parametrize("flags", [0, 1], ids=["stream_k", "batch_invariant"])
+def test_prefill_f16x_scaling_and_permutation(env, ty, rows, cols, flags):
+    """vq_qgemm_f16x_ws at 512 tokens: a power of two on a token moves its 2^e, so its f16 operands keep their bits."""
+    torch, lib = env
+    M = 512
+    w = torch_baseline_rows(ty, rows, cols, 31 + int(ty), "cuda")
+    need = lib.vq_qgemm_workspace_bytes_ex(int(ty), rows, cols, M, flags)
+    wk = torch.empty(need, dtype=torch.uint8, device="cuda")
+
+    def run(x):
+        y = torch.full((M, rows), float("nan"), dtype=torch.float32, device="cuda")
+        assert lib.vq_qgemm_f16x_ws(int(ty), P(w), rows, cols, P(x), M, P(y), P(wk), need, flags, None) == 0
+        torch.cuda.synchronize()
+        return y.cpu().numpy()
+
+    _check(torch, run, torch.randn(M, cols, device="cuda"), permute=flags == 1)
+
+
 def test_lm_head_scaling_and_permutation(env):
     """The fused LM-head argmax over the full 248320-row Q6_K head: logits scale exactly, indices do not move."""
     torch, lib = env
