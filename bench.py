@@ -1060,6 +1060,8 @@ def main() -> None:
         for rows, cols in ((17408, 5120), (5120, 17408)):
             log(f"prefill: 512 tokens x Q4_K {rows}x{cols}")
             prefill[f"Q4_K_{rows}x{cols}_M512"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512)
+            # the reference's numerics for this config (fp16 activations, one MFMA per product)
+            prefill[f"Q4_K_{rows}x{cols}_M512_f16x"] = bench_gemm(torch, hip, Q4_K, rows, cols, 512, f16x=True)
         log("sequence ops (gated delta, conv update, attention)")
         ops = bench_ops(torch, hip)
 
