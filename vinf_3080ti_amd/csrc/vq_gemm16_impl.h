@@ -56,21 +56,29 @@ typedef float g16f4 __attribute__((ext_vector_type(4)));
 // tile-major order (unit u = tile * nsb + sb; workgroup b owns [b U / W, (b+1) U / W)). A workgroup that covers a
 // whole tile writes y; the parts of a tile split between workgroups go to slots [tile][k] (k = the workgroup's
 // order among the tile's) that vq_gemm16_reduce adds in slot order (deterministic). Two plans:
-//  - default: with more tiles than CUs, W = CUs (stream-K: no CU idles through a partial last round); else W is
-//    the largest multiple of the tile count that fits the CUs (plain split-K). The split depends on M.
+//  - default: with more tiles than CUs, W = CUs: each workgroup first takes `rounds` = tiles / CUs whole tiles
+//    (units [b rounds nsb, (b+1) rounds nsb), written straight to y), then an equal contiguous share of the
+//    remaining tiles' units (stream-K over the last tiles % CUs tiles: only those have parts to add; when they
+//    hold fewer units than CUs, stream-K over every unit instead). Else W is the largest multiple of the tile
+//    count that fits the CUs (plain split-K). The split depends on M.
 //  - batch-invariant: every tile's super-blocks are cut at the same P - 1 boundaries (P = CUs / row tiles,
 //    rounded, at most nsb), W = tiles x P. P depends only on the matrix, so a token's result is the same whatever
 //    batch it runs in (the reference's contract for its prompt kernels, qwen_runtime.cu:1883-1885), at 10-20 %
 //    more time at 512 tokens (more partial tiles to add).
 struct G16Plan {
     int tiles, ntt, nrt, nsb, W, per_xcd, maxseg;
-    long U;
+    int rounds, t0;  // whole tiles per workgroup; t0 = W rounds tiles taken whole (0: all units shared)
+    long U, D;       // units; D = t0 nsb units of the whole tiles
     // Tile order: token-tile major (tile = tt * nrt + rt), so the workgroups of one XCD (consecutive shares) work
     // on one token tile, whose activation tile then stays in that XCD's L2.
     __host__ __device__ int tile_rt(int tile) const { return tile % nrt; }
     __host__ __device__ int tile_tt(int tile) const { return tile / nrt; }
-    __host__ __device__ int wg_of(long u) const { return static_cast<int>(((u + 1) * W - 1) / U); }  // owner of u
-    __host__ __device__ long u0(int b) const { return static_cast<long>(b) * U / W; }
+    __host__ __device__ int wg_of(long u) const {  // owner of unit u
+        return u < D ? static_cast<int>(u / nsb / rounds) : static_cast<int>(((u - D + 1) * W - 1) / (U - D));
+    }
+    __host__ __device__ long u0(int b) const { return D + static_cast<long>(b) * (U - D) / W; }  // shared units
+    __host__ __device__ long dp0(int b) const { return static_cast<long>(b) * rounds * nsb; }  // whole tiles
+    __host__ __device__ long dp1(int b) const { return D ? dp0(b + 1) : 0; }
 };
 inline G16Plan g16_plan(int rows, int cols, int M, int cus, bool invariant = false) {
     G16Plan p{};
@@ -80,6 +88,7 @@ inline G16Plan g16_plan(int rows, int cols, int M, int cus, bool invariant = fal
     p.tiles = row_tiles * p.ntt;
     p.nsb = cols >> 8;
     p.U = static_cast<long>(p.tiles) * p.nsb;
+    p.rounds = 1;
     if (invariant) {
         int P = (cus + row_tiles / 2) / row_tiles;
         P = P < 1 ? 1 : P > p.nsb ? p.nsb : P;
@@ -98,17 +107,23 @@ inline G16Plan g16_plan(int rows, int cols, int M, int cus, bool invariant = fal
         if (p.W * 10 < cus * 9 && p.U >= cus) p.W = cus;
     } else {
         p.W = cus;
+        const int rem = p.tiles % cus;
+        if (rem == 0 || static_cast<long>(rem) * p.nsb >= cus) {
+            p.rounds = p.tiles / cus;
+            p.t0 = p.rounds * cus;
+            p.D = static_cast<long>(p.t0) * p.nsb;
+        }
     }
     p.per_xcd = (p.W + 7) / 8;
-    const long share = p.U / p.W;  // >= 1
-    p.maxseg = static_cast<int>((p.nsb + share - 1) / share + 1);
+    const long share = (p.U - p.D) / p.W;  // >= 1 unless every tile is whole
+    p.maxseg = share ? static_cast<int>((p.nsb + share - 1) / share + 1) : 1;
     return p;
 }
 
 // Workspace layout of the f16 path for M tokens of `cols` columns: b_hi [M][cols] f16, b_lo [M][cols] f16,
 // xs [M][cols/256][16] f16 (per super-block: X_g xd_g 2^e / 32 as 8 hi then 8 lo; for Q2_K, whose mins apply per
 // 16 elements, [M][cols/256][32]: the 16 halves' X_h xd 2^e / 32 as 16 hi then 16 lo), inv [M] fp32 (2^-e),
-// then the partial-tile slots [tiles][maxseg][64 values][512 threads] fp32.
+// then the partial-tile slots [tiles - t0][maxseg][64 values][512 threads] fp32.
 constexpr size_t kG16TileFloats = static_cast<size_t>(kG16BM) * kG16BN;
 struct G16Ws {
     size_t bh, bl, xs, inv, part, total;
@@ -122,7 +137,7 @@ inline G16Ws g16_layout(int cols, int M, const G16Plan &p, bool halves = false) 
     l.xs = l.bl + al(nb);
     l.inv = l.xs + al(static_cast<size_t>(M) * (cols / 256) * (halves ? 64 : 32));
     l.part = l.inv + al(static_cast<size_t>(M) * 4);
-    l.total = l.part + al(static_cast<size_t>(p.tiles) * p.maxseg * kG16TileFloats * 4);
+    l.total = l.part + al(static_cast<size_t>(p.tiles - p.t0) * p.maxseg * kG16TileFloats * 4);
     return l;
 }
 
@@ -178,14 +193,17 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     const int v = (b & 7) * pl.per_xcd + (b >> 3);
     if (v >= pl.W) return;
     const int nsb = pl.nsb;
-    const long ue = pl.u0(v + 1);
+    // The workgroup's whole tiles, then its share of the others.
+    long ue = pl.dp1(v), u = pl.dp0(v);
+    bool whole = u < ue;
+    if (!whole) u = pl.u0(v), ue = pl.u0(v + 1);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     constexpr int RB = kG16RB, TB = 16 / RB;  // 16-row blocks x 16-token blocks of a wave
     const int wr = 16 * RB * (wv % (16 / RB)), wt = 16 * TB * (wv / (16 / RB));
     const int lr = lane & 15, lk = lane >> 4;
     // The share's tile segments: tile t, super-blocks [sb0, sb1).
-    for (long u = pl.u0(v); u < ue;) {
+    while (u < ue) {
     const int tile = static_cast<int>(u / nsb);
     const int sb0 = static_cast<int>(u - static_cast<long>(tile) * nsb);
     const int sb1 = ue - u < nsb - sb0 ? sb0 + static_cast<int>(ue - u) : nsb;
@@ -386,7 +404,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
         }
     } else {
         const int k = v - pl.wg_of(static_cast<long>(tile) * nsb);
-        float *const slot = part + (static_cast<size_t>(tile) * pl.maxseg + k) * kG16TileFloats;
+        float *const slot = part + (static_cast<size_t>(tile - pl.t0) * pl.maxseg + k) * kG16TileFloats;
 #pragma unroll
         for (int tb = 0; tb < TB; ++tb) {
             const int t = min(t0 + wt + 16 * tb + lr, M - 1);
@@ -399,6 +417,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
     }
     __syncthreads();  // the ring is reused by the next segment's first DMAs
     u += sb1 - sb0;
+    if (whole && u >= ue) whole = false, u = pl.u0(v), ue = pl.u0(v + 1);
     }
 }
 
@@ -409,7 +428,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16_kernel(const uint8_t *
 template <int RB = 4>
 __global__ __launch_bounds__(512) void g16_reduce_kernel(const float *__restrict__ part, G16Plan pl, int rows, int M,
                                                          float *__restrict__ y) {
-    const int tile = blockIdx.x >> 4, pair = blockIdx.x & 15;
+    const int tile = pl.t0 + (blockIdx.x >> 4), pair = blockIdx.x & 15;
     const int k0 = pl.wg_of(static_cast<long>(tile) * pl.nsb), k1 = pl.wg_of(static_cast<long>(tile) * pl.nsb + pl.nsb - 1);
     if (k1 == k0) return;
     constexpr int TB = 16 / RB;
@@ -418,7 +437,7 @@ __global__ __launch_bounds__(512) void g16_reduce_kernel(const float *__restrict
     const int rb = pair / TB, tb = pair % TB;
     const int rt = pl.tile_rt(tile), tt = pl.tile_tt(tile);
     const int t = tt * kG16BN + wt + 16 * tb + lr, r = rt * kG16BM + wr + 16 * rb + 4 * lk;
-    const float *const base = part + static_cast<size_t>(tile) * pl.maxseg * kG16TileFloats +
+    const float *const base = part + static_cast<size_t>(tile - pl.t0) * pl.maxseg * kG16TileFloats +
                               static_cast<size_t>((rb * TB + tb) * 4) * 512 + tid;
     float v4[4] = {0.f, 0.f, 0.f, 0.f};
     for (int k = 0; k <= k1 - k0; ++k) {
@@ -468,7 +487,7 @@ int launch_gemm16(const uint8_t *w, int rows, int cols, long rb, const void *ws,
             reinterpret_cast<const float *>(base + l.inv), M, pl, y, part);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return static_cast<int>(e);
-        g16_reduce_kernel<kG16RB><<<dim3(16 * pl.tiles), dim3(512), 0, s>>>(part, pl, rows, M, y);
+        if (pl.tiles > pl.t0) g16_reduce_kernel<kG16RB><<<dim3(16 * (pl.tiles - pl.t0)), dim3(512), 0, s>>>(part, pl, rows, M, y);
         e = hipGetLastError();
         return e == hipSuccess ? 0 : static_cast<int>(e);
     }

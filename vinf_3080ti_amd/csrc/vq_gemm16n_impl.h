@@ -120,13 +120,16 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
     const int v = (b & 7) * pl.per_xcd + (b >> 3);  // XCD-aware share order, as qgemm16_kernel
     if (v >= pl.W) return;
     const int nsb = pl.nsb;
-    const long ue = pl.u0(v + 1);
+    // The workgroup's whole tiles, then its share of the others.
+    long ue = pl.dp1(v), u = pl.dp0(v);
+    bool whole = u < ue;
+    if (!whole) u = pl.u0(v), ue = pl.u0(v + 1);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     constexpr int RB = kG16RB, TB = 16 / RB;  // 16-row blocks x 16-token blocks of a wave
     const int wr = 16 * RB * (wv % (16 / RB)), wt = 16 * TB * (wv / (16 / RB));
     const int lr = lane & 15, lk = lane >> 4;
-    for (long u = pl.u0(v); u < ue;) {
+    while (u < ue) {
     const int tile = static_cast<int>(u / nsb);
     const int sb0 = static_cast<int>(u - static_cast<long>(tile) * nsb);
     const int sb1 = ue - u < nsb - sb0 ? sb0 + static_cast<int>(ue - u) : nsb;
@@ -413,7 +416,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
         }
     } else {
         const int k = v - pl.wg_of(static_cast<long>(tile) * nsb);
-        float *const slot = part + (static_cast<size_t>(tile) * pl.maxseg + k) * kG16TileFloats;
+        float *const slot = part + (static_cast<size_t>(tile - pl.t0) * pl.maxseg + k) * kG16TileFloats;
 #pragma unroll
         for (int tb = 0; tb < TB; ++tb) {
             const int t = min(t0 + wt + 16 * tb + lr, M - 1);
@@ -426,6 +429,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
     }
     __syncthreads();  // the slots are reused by the next segment's first DMAs
     u += sb1 - sb0;
+    if (whole && u >= ue) whole = false, u = pl.u0(v), ue = pl.u0(v + 1);
     }
 }
 
@@ -442,7 +446,7 @@ int launch_gemm16n(const uint8_t *w, int rows, int cols, long rb, const void *ws
         reinterpret_cast<const _Float16 *>(base + l.xs), reinterpret_cast<const float *>(base + l.inv), M, pl, y, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
-    g16_reduce_kernel<kG16RB><<<dim3(16 * pl.tiles), dim3(512), 0, s>>>(part, pl, rows, M, y);
+    if (pl.tiles > pl.t0) g16_reduce_kernel<kG16RB><<<dim3(16 * (pl.tiles - pl.t0)), dim3(512), 0, s>>>(part, pl, rows, M, y);
     e = hipGetLastError();
     return e == hipSuccess ? 0 : static_cast<int>(e);
 }
