@@ -865,7 +865,8 @@ def test_tiny_matrices_every_route(env, oracle_mod, ty, rows, cols):
     (T.Q4_K, 70, 512, 37, 0), (T.Q5_K, 300, 1024, 129, 1), (T.Q4_K, 1000, 5120, 1, 0), (T.Q5_K, 2048, 2048, 300, 1),
     (T.Q6_K, 5120, 17408, 512, 0), (T.Q3_K, 17408, 5120, 512, 0), (T.Q6_K, 300, 1024, 129, 1), (T.Q3_K, 70, 512, 37, 0),
     (T.Q2_K, 1000, 5120, 200, 0), (T.Q2_K, 300, 1024, 129, 1), (T.IQ2_XS, 1000, 5120, 200, 0),
-    (T.IQ2_XXS, 1000, 5120, 200, 1), (T.IQ2_S, 1000, 5120, 200, 0), (T.IQ3_XXS, 1000, 5120, 200, 0)],
+    (T.IQ2_XXS, 1000, 5120, 200, 1), (T.IQ2_S, 1000, 5120, 200, 0), (T.IQ3_XXS, 1000, 5120, 200, 0),
+    (T.Q4_K, 300, 20480, 37, 0), (T.Q2_K, 300, 20480, 37, 0)],  # rows past the split's register-held part
     ids=lambda v: v.name if isinstance(v, T) else str(v))
 def test_qgemm_f16x_matches_oracle(env, oracle_mod, ty, rows, cols, M, flags):
     """vq_qgemm_f16x_ws against f16(x)-times-exact-weights in float64, every token; tokens 0 and 1 scaled to 1e-30

@@ -830,14 +830,25 @@ int vq_qgemm_ws_ex(int type, const uint8_t *w, int rows, int cols, const void *x
 __global__ __launch_bounds__(256) void gemm_f16x_split_kernel(const float *__restrict__ x, int cols,
                                                               _Float16 *__restrict__ bh, _Float16 *__restrict__ xs,
                                                               float *__restrict__ inv, int halves) {
-    const int t = blockIdx.x, tid = threadIdx.x;
+    // Rows of up to 256 x KR chunks of 8 values (18432 columns) are read once, into registers; longer rows are
+    // read again past that for the conversion.
+    constexpr int KR = 9;
+    const int t = blockIdx.x, tid = threadIdx.x, nch = cols / 8;
     const float4 *xr = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * cols);
     __shared__ float red[4];
+    auto amax = [](float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
+    float4 r[KR][2];
     float m = 0.0f;
-    for (int i = tid; i < cols / 4; i += 256) {
-        const float4 v = xr[i];
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+        const int c = tid + 256 * k;
+        if (c < nch) {
+            r[k][0] = xr[2 * c];
+            r[k][1] = xr[2 * c + 1];
+            m = fmaxf(m, fmaxf(amax(r[k][0]), amax(r[k][1])));
+        }
     }
+    for (int c = tid + 256 * KR; c < nch; c += 256) m = fmaxf(m, fmaxf(amax(xr[2 * c]), amax(xr[2 * c + 1])));
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     if ((tid & 63) == 0) red[tid >> 6] = m;
@@ -848,9 +859,9 @@ __global__ __launch_bounds__(256) void gemm_f16x_split_kernel(const float *__res
     const float sc = m > 0.0f ? ldexpf(1.0f, min(15 - E, 126)) : 1.0f;
     const size_t base = static_cast<size_t>(t) * cols;
     const int nsb = cols >> 8;
-    // cols / 8 is a multiple of 32: the four threads of a group are active together.
-    for (int c = tid; c < cols / 8; c += 256) {
-        const float4 v0 = xr[2 * c], v1 = xr[2 * c + 1];
+    // Chunk c (8 values): b_hi, then its group's (or half's) sum. nch is a multiple of 32, so the four threads of a
+    // group (consecutive c) are active together.
+    auto convert = [&](int c, float4 v0, float4 v1) {
         const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         _Float16 h[8];
         float sum = 0.0f;
@@ -870,7 +881,7 @@ __global__ __launch_bounds__(256) void gemm_f16x_split_kernel(const float *__res
                 dst[0] = hi;
                 dst[16] = static_cast<_Float16>(v - static_cast<float>(hi));
             }
-            continue;
+            return;
         }
         sum += __shfl_xor(sum, 2, 64);
         if ((c & 3) == 0) {
@@ -882,7 +893,13 @@ __global__ __launch_bounds__(256) void gemm_f16x_split_kernel(const float *__res
             dst[0] = hi;
             dst[8] = static_cast<_Float16>(v - static_cast<float>(hi));
         }
+    };
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+        const int c = tid + 256 * k;
+        if (c < nch) convert(c, r[k][0], r[k][1]);
     }
+    for (int c = tid + 256 * KR; c < nch; c += 256) convert(c, xr[2 * c], xr[2 * c + 1]);
     if (tid == 0) inv[t] = 1.0f / sc;
 }
 
