@@ -358,11 +358,12 @@ int vq_qgemm_ws_ex(int type, const uint8_t *w, int rows, int cols, const void *x
 /* The prefill contraction with the reference's tensor-core numerics: fp32 activations x [M][cols] rounded to f16
  * (each token first scaled by a power of two that puts its largest |x| just below 2^15, undone on the outputs, so
  * no token overflows or flushes to zero where the reference's plain conversion would), weights exact, fp32
- * accumulation: y = sum_k deq(w) f16(x). One MFMA per product instead of the b_hi/b_lo pair of vq_qgemm_ws (Q6_K:
- * two, its weight's f16 rounding and remainder), for the types of vq_qgemm_ws's f16 path (Q2_K-Q6_K, IQ2_XXS/XS/S,
- * IQ3_XXS; other types -> VQ_ERR_TYPE). Workspace and flags as vq_qgemm_ws_ex (same byte count).
+ * accumulation: y = sum_k deq(w) f16(x). One MFMA per product instead of the b_hi/b_lo pair of vq_qgemm_ws, for the
+ * types of vq_qgemm_ws's f16 path (Q2_K-Q6_K, IQ2_XXS/XS/S, IQ3_XXS; other types -> VQ_ERR_TYPE). Weights are exact
+ * but for Q6_K, whose integer product (q - 32) sc is rounded to f16 once (within 2^-11, as the reference rounds
+ * every dequantized weight to fp16). Workspace and flags as vq_qgemm_ws_ex (same byte count).
  * Against the int8 activations of vq_qgemm_ws the outputs move by the f16 rounding of x (rel-L2 ~1e-4); against
- * f16(x) evaluated exactly, rel-L2 <= 1e-5. Replaces: f32_to_f16_rows_kernel + vinf_qgemm_kernel
+ * those operands evaluated exactly, rel-L2 <= 1e-5. Replaces: f32_to_f16_rows_kernel + vinf_qgemm_kernel
  * (qwen_runtime.cu:657-661,663-739, launched :1898). */
 int vq_qgemm_f16x_ws(int type, const uint8_t *w, int rows, int cols, const float *x, int M, float *y, void *workspace,
                      size_t workspace_bytes, int flags, void *stream);

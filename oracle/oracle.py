@@ -135,13 +135,31 @@ def f16x_scales(x: np.ndarray) -> np.ndarray:
     return np.where(m > 0, np.ldexp(1.0, np.minimum(15 - e, 126)), 1.0)
 
 
+def f16x_weights(type_id: int, raw, rows: int, cols: int) -> np.ndarray:
+    """The weights of the f16-activation contraction, float64: exact (dequant_rows) for every type but Q6_K, whose
+    integer product (q - 32) sc (up to 32 x 128, past fp16's exact integers) is rounded to fp16 once before d
+    applies: d f16((q - 32) sc), within 2^-11 of the exact weight, as the reference rounds every dequantized weight
+    to fp16 (vinf_qgemm_kernel's a_tile, qwen_runtime.cu:700-702). Q6_K block: ql[128] qh[64] scales[16] int8
+    d f16 (210 bytes); scale j covers elements 16 j .. 16 j + 15."""
+    exact = dequant_rows(type_id, raw, rows, cols).astype(np.float64)
+    if type_id != 14:
+        return exact
+    codes, _, _ = decode_codes(type_id, raw, rows, cols)
+    blk = _u8(raw)[: rows * (cols // 256) * 210].reshape(rows, cols // 256, 210)
+    sc = blk[:, :, 192:208].copy().view(np.int8).astype(np.float64).reshape(rows, cols // 16)
+    d = blk[:, :, 208:210].copy().view(np.float16).astype(np.float64).reshape(rows, cols // 256)
+    prod = codes.astype(np.float64).reshape(rows, cols // 16, 16) * sc[:, :, None]
+    w = prod.astype(np.float16).astype(np.float64).reshape(rows, cols // 256, 256) * d[:, :, None]
+    return w.reshape(rows, cols)
+
+
 def qgemm_f16x(type_id: int, raw, rows: int, cols: int, x: np.ndarray, ntok: int) -> np.ndarray:
-    """y[t] = W f16(x[t] s_t) / s_t in float64: W the exact dequantized weights (dequant_rows), f16 the IEEE
+    """y[t] = W f16(x[t] s_t) / s_t in float64: W = f16x_weights (exact, Q6_K rounded once), f16 the IEEE
     round-to-nearest-even conversion the reference applies to every activation before its fp16 MMA
     (f32_to_f16_rows_kernel, qwen_runtime.cu:657-661; vinf_qgemm_kernel :663-739 accumulates the products in fp32),
     s_t = f16x_scales. Scaling by a power of two commutes with the rounding wherever x s_t and x are both normal
     fp16 numbers, so for such tokens this is W f16(x) exactly."""
-    w = dequant_rows(type_id, raw, rows, cols).astype(np.float64)
+    w = f16x_weights(type_id, raw, rows, cols)
     x = np.ascontiguousarray(x, np.float32).reshape(ntok, cols)
     s = f16x_scales(x)
     xb = (x * s[:, None].astype(np.float32)).astype(np.float16).astype(np.float64)

@@ -420,3 +420,31 @@ def test_qgemm_f16x_is_pinned_by_brute_force_and_plain_f16(oracle_mod):
         assert np.array_equal(oracle_mod.qgemm_f16x(int(ty), w, rows, cols, xn, ntok), plain)
         big = (xn * np.float32(2.0 ** 40)).astype(np.float32)  # far above fp16's 65504
         assert np.array_equal(oracle_mod.qgemm_f16x(int(ty), w, rows, cols, big, ntok), plain * 2.0 ** 40)
+
+
+def test_f16x_weights_round_q6k_once(oracle_mod):
+    """f16x_weights: Q6_K's weight d f16((q - 32) sc) lies within 2^-11 of the exact dequantized weight (a wrong
+    scale or element mapping would be off by far more), equals it wherever |(q - 32) sc| <= 2048 (exact in fp16),
+    and matches a per-element struct-rounded restatement; every other type is exact."""
+    rng = np.random.default_rng(9)
+    rows, cols = 5, 512
+    raw = synth.baseline_rows(T.Q6_K, rows, cols, rng)
+    ex = oracle_mod.dequant_rows(int(T.Q6_K), raw, rows, cols).astype(np.float64)
+    w = oracle_mod.f16x_weights(int(T.Q6_K), raw, rows, cols)
+    assert np.all(np.abs(w - ex) <= 2.0 ** -11 * np.abs(ex))
+    codes, _, _ = oracle_mod.decode_codes(int(T.Q6_K), raw, rows, cols)
+    blk = np.frombuffer(bytes(raw), np.uint8)[: rows * (cols // 256) * 210].reshape(rows, cols // 256, 210)
+    for r in range(rows):
+        for e in range(cols):
+            b, j = divmod(e, 256)
+            sc = int(np.int8(blk[r, b, 192 + j // 16]))
+            d = struct.unpack("<e", bytes(blk[r, b, 208:210]))[0]
+            prod = int(codes[r, e]) * sc
+            want = struct.unpack("<e", struct.pack("<e", float(prod)))[0] * d
+            assert w[r, e] == want, (r, e)
+            if abs(prod) <= 2048:
+                assert w[r, e] == ex[r, e]
+    assert (w != ex).any()  # the shape exercises the rounding
+    raw4 = synth.baseline_rows(T.Q4_K, rows, cols, rng)
+    assert np.array_equal(oracle_mod.f16x_weights(int(T.Q4_K), raw4, rows, cols),
+                          oracle_mod.dequant_rows(int(T.Q4_K), raw4, rows, cols).astype(np.float64))

@@ -341,7 +341,7 @@ __global__ __launch_bounds__(64 * kG16Waves) void qgemm16n_kernel(const uint8_t 
                         g16f4 &cc = C[rb][4 * h + i];
                         cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], bhf[i], cc, 0, 0, 0);
                         if constexpr (LO) cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[rb], blf[i], cc, 0, 0, 0);
-                        if constexpr (G::Q6) {
+                        if constexpr (G::Q6 && LO) {  // b_hi alone: the weight as its f16 rounding p only
                             cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], bhf[i], cc, 0, 0, 0);
                             if constexpr (LO && !VQ_S16_RSPLIT)
                                 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2[rb], blf[i], cc, 0, 0, 0);
